@@ -1,0 +1,163 @@
+/*
+ * ntlowbit.h: C-ABI of the MI355X (gfx950) low-bit linear hot path.
+ *
+ * One shared library, libntlowbit.so, built from nano-train_amd/csrc/.  The
+ * signatures hold only plain pointers, integers and an opaque stream handle
+ * (a hipStream_t passed as void*, NULL = the null stream), so any FFI can
+ * bind them.  All device pointers are caller-allocated; no entry point
+ * allocates, frees or synchronizes.  Every launch is asynchronous on `stream`.
+ *
+ * Each entry point replaces one torch-op sequence of nano-train's emulated
+ * backend; the reference function it stands in for is cited as
+ * path:line into lastweek/nano-train.
+ *
+ * Return values: NTLB_OK (0) on success, a negative NTLB_E* status otherwise;
+ * ntlb_last_error() then describes the failure (thread-local string).
+ *
+ * Conventions
+ *   dtype   : NTLB_F32, NTLB_BF16, NTLB_F16 for float tensors.
+ *   grid    : NTLB_GRID_INT  - int8 codes of the reference's symmetric integer
+ *                              grid, |q| <= qmax = 2^(bits-1)-1, scale =
+ *                              amax/qmax (te_backend.py:98-106); a NaN element
+ *                              is stored as code -128;
+ *             NTLB_GRID_E4M3 - OCP e4m3fn codes, scale = amax/448 (the
+ *                              DeepSeek-V3 recipe).
+ *   rounding: NTLB_ROUND_NEAREST (torch.round, half to even) or
+ *             NTLB_ROUND_STOCHASTIC: element e uses r = word e%4 of
+ *             Philox4x32-10(counter {lo(e/4), hi(e/4), lo(offset), hi(offset)},
+ *             key {lo(seed), hi(seed)}), u = (r >> 8) * 2^-24, and rounds
+ *             floor(v+u) for v >= 0, ceil(v-u) for v < 0 (te_backend.py:61-65).
+ *             e is the row-major index of the element in the source matrix.
+ *   codes   : uint8 [rows, ldc], ldc >= ceil(K/128)*128 where tiles pad K;
+ *             padding columns are written as 0.
+ *   scales  : fp32; element (i, t) lives at scales[i*s_row + t*s_col], so
+ *             either layout (row-major or tile-major) can be requested.
+ */
+#ifndef NTLOWBIT_H
+#define NTLOWBIT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NTLB_ABI_VERSION 1
+
+#define NTLB_OK 0
+#define NTLB_EINVAL (-1)       /* bad shape, stride, alignment or enum */
+#define NTLB_ELAUNCH (-2)      /* the HIP runtime refused a launch */
+#define NTLB_EUNSUPPORTED (-3) /* valid request this build does not cover */
+
+#define NTLB_F32 0
+#define NTLB_BF16 1
+#define NTLB_F16 2
+
+#define NTLB_GRID_INT 0
+#define NTLB_GRID_E4M3 1
+
+#define NTLB_ROUND_NEAREST 0
+#define NTLB_ROUND_STOCHASTIC 1
+
+/* scale rules: te_backend.py:74-79 (safe(amax/qmax)) and moe.py:94-98
+ * (amax checked before the division) */
+#define NTLB_SCALE_AFTER_DIVIDE 0
+#define NTLB_SCALE_BEFORE_DIVIDE 1
+
+int ntlb_abi_version(void);
+const char* ntlb_last_error(void);
+
+/*
+ * 1x128 tile quantizer.  Replaces _tile_quant_dequant (te_backend.py:82-110)
+ * and the tile_1x128 branch of _quantize_dequantize_with_granularity
+ * (te_backend.py:187-193).
+ *   x      [R, K] with row stride ldx (elements), last dim contiguous.
+ *   codes  [R, ldc] uint8, ldc >= ceil(K/128)*128, multiple of 8.
+ *   scales [R, T] (T = ceil(K/128)) addressed with (s_row, s_col).
+ *   dq     optional [R, K] (row stride lddq) = q*scale cast to dq_dtype
+ *          (the tensor the reference returns); NULL to skip.
+ *   nan_rows optional int32 [R]: rows holding a NaN get 1 OR-ed in; the
+ *          caller zeroes it.  NULL to skip.
+ */
+int ntlb_quant_tile_1x128(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int grid, int qmax,
+                          int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes,
+                          int64_t ldc, float* scales, int64_t s_row, int64_t s_col, void* dq, int dq_dtype,
+                          int64_t lddq, int32_t* nan_rows, void* stream);
+
+/*
+ * 128x128 block quantizer for a 2-D weight.  Replaces _block_quant_dequant
+ * (te_backend.py:113-149).
+ *   w [N, K] (row stride ldw); codes [N, ldc]; scales [ceil(N/128), T] via
+ *   (s_row, s_col); optional transposed codes codes_t [K, ldct] (ldct >=
+ *   ceil(N/128)*128) for GEMMs that contract over N; optional dq and
+ *   nan_rows as for the tile quantizer.
+ */
+int ntlb_quant_block_128x128(const void* w, int w_dtype, int64_t N, int64_t K, int64_t ldw, int grid, int qmax,
+                             int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes,
+                             int64_t ldc, uint8_t* codes_t, int64_t ldct, float* scales, int64_t s_row,
+                             int64_t s_col, void* dq, int dq_dtype, int64_t lddq, int32_t* nan_rows, void* stream);
+
+/*
+ * Grouped amax: amax_bits[(i/gr)*n_gc + k/gc] = max |x[i,k]| as fp32 bits
+ * (NaN-propagating).  The caller zeroes amax_bits.  Together with
+ * ntlb_quant_grouped this covers the granularities whose groups span many
+ * rows: tensor (gr=R, gc=K; te_backend.py:165-173), channel along the last
+ * axis (gr=R, gc=1) or axis 0 (gr=1, gc=K) (te_backend.py:175-185), and the
+ * comm-quant strip (gr=R, gc=128; moe.py:123-140).
+ */
+int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr, int64_t gc,
+                      uint32_t* amax_bits, void* stream);
+
+/*
+ * Quantize with precomputed group amaxes (from ntlb_amax_grouped).  Writes
+ * scales[(i/gr)*n_gc + k/gc] (fp32, computed from the amax with scale_rule),
+ * codes [R, ldc] (ldc >= K), optional dq and nan_rows.
+ */
+int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr, int64_t gc,
+                       const uint32_t* amax_bits, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                       uint64_t offset, uint8_t* codes, int64_t ldc, float* scales, void* dq, int dq_dtype,
+                       int64_t lddq, int32_t* nan_rows, void* stream);
+
+/*
+ * 128x1 tile quantizer with transposed codes: groups of 128 consecutive rows
+ * of one column share a scale, and the codes are written transposed,
+ * codes_t [K, ldct] (ldct >= ceil(R/128)*128, a multiple of 16).  These are
+ * the contraction-over-tokens operands X^T and dY^T of the DeepSeek-V3 wgrad
+ * recipe; there is no reference function (te_backend.py:250-260 leaves dY
+ * unquantized).  It is _tile_quant_dequant (te_backend.py:82-110) applied to
+ * x^T.  scales(k, mb) = scales[k*s_row + mb*s_col].  SR bits are keyed by the
+ * source index r*K + k.  Optional dq [R, K] and nan_rows [R] as above.
+ */
+int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int grid, int qmax,
+                            int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes_t,
+                            int64_t ldct, float* scales, int64_t s_row, int64_t s_col, void* dq, int dq_dtype,
+                            int64_t lddq, int32_t* nan_rows, void* stream);
+
+/*
+ * Blockwise-scaled GEMM  Y[M,N] = sum_kb sa(m,kb) * sb(n,kb) * (A_kb[m,:] . B_kb[n,:])  (+ bias[n]).
+ * The math of F.linear(X_dq, W_dq, bias) in te_backend.py:253-259 with the
+ * operands kept as codes plus scales: every 128-wide K block is multiplied
+ * on the matrix cores (int8 MFMA for NTLB_GRID_INT, fp8 e4m3 MFMA for
+ * NTLB_GRID_E4M3) and promoted into an fp32 accumulator with its scales.
+ *   a  [M, Kp] codes, row stride lda;  b [N, Kp] codes, row stride ldb;
+ *      Kp a multiple of 128, lda/ldb multiples of 16, 16-byte aligned.
+ *   sa(m, kb) = sa[(m >> a_shift) * sa_row + kb * sa_col]
+ *   sb(n, kb) = sb[(n >> b_shift) * sb_row + kb * sb_col]
+ *      shift 0: per row (1x128 tiles, or channel with *_col = 0);
+ *      shift 7: per 128-row block (128x128 blocks);  row = col = 0: tensor.
+ *   bias optional [N] (bias_dtype); y [M, N] with row stride ldy, y_dtype.
+ *   nan_a / nan_b optional int32 [M] / [N] row flags from the quantizers:
+ *      a flagged row of A (or of B) makes its output row (column) NaN, as
+ *      the NaN would in the reference's fp32 GEMM.
+ */
+int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row, int64_t sa_col,
+                          int a_shift, const uint8_t* b, int64_t ldb, const float* sb, int64_t sb_row,
+                          int64_t sb_col, int b_shift, int64_t M, int64_t N, int64_t Kp, const void* bias,
+                          int bias_dtype, void* y, int y_dtype, int64_t ldy, const int32_t* nan_a,
+                          const int32_t* nan_b, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NTLOWBIT_H */

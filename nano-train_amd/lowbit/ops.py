@@ -1,0 +1,287 @@
+"""Tensor-level wrappers of the gfx950 low-bit kernels.
+
+Every function here takes and returns torch tensors on a ROCm device, allocates
+outputs with torch's caching allocator, and launches on torch's current HIP
+stream through the C-ABI in ``include/ntlowbit.h``.  Nothing here computes on
+the CPU: a CPU tensor is an error.
+
+Quantized operands are carried as :class:`QTensor` (codes + scales + how the
+scales are indexed), which is exactly what the blockwise GEMM consumes.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_DTYPE_CODE = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError as exc:
+        raise TypeError(f"unsupported dtype {dt}; expected float32, bfloat16 or float16") from exc
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*ts: Optional[torch.Tensor]) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "the MI355X low-bit kernels need tensors on a ROCm device "
+                f"(got {t.device}); there is no CPU path"
+            )
+
+
+def _as_2d(x: torch.Tensor) -> torch.Tensor:
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() != 2 else x
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2
+
+
+def cdiv(a: int, b: int) -> int:
+    return -(-a // b)
+
+
+def grid_code(fmt: str) -> int:
+    if fmt in ("int", "int_grid", "grid"):
+        return _lib.GRID_INT
+    if fmt == "e4m3":
+        return _lib.GRID_E4M3
+    raise ValueError(f"unknown code format {fmt!r}; expected 'int_grid' or 'e4m3'")
+
+
+def rounding_code(mode: str) -> int:
+    if mode == "nearest":
+        return _lib.ROUND_NEAREST
+    if mode == "stochastic":
+        return _lib.ROUND_STOCHASTIC
+    raise ValueError(f"unknown rounding mode {mode!r}")
+
+
+@dataclass
+class QTensor:
+    """Codes plus scales of a quantized [rows, K] matrix.
+
+    scale(i, kb) = scales.flatten()[(i >> shift) * s_row + kb * s_col]
+    (kb = 128-column block; shift 7 = one scale per 128 rows).
+    """
+
+    codes: torch.Tensor  # uint8 [rows, ldc]
+    scales: torch.Tensor  # fp32, flat indexing through s_row / s_col
+    s_row: int
+    s_col: int
+    shift: int
+    grid: int
+    rows: int
+    K: int
+    nan_rows: Optional[torch.Tensor] = None
+    dq: Optional[torch.Tensor] = None
+
+    @property
+    def Kp(self) -> int:
+        return cdiv(self.K, 128) * 128
+
+
+def quant_tile_1x128(
+    x: torch.Tensor,
+    *,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    tile_major_scales: bool = True,
+    want_dq: bool = False,
+    dq_dtype: Optional[torch.dtype] = None,
+    want_nan_rows: bool = False,
+) -> QTensor:
+    """te_backend.py:82-110 on x viewed as [R, K] (leading dims flattened)."""
+    _require_device(x)
+    x2 = _as_2d(x)
+    R, K = x2.shape
+    T = cdiv(K, 128)
+    ldc = T * 128
+    dev = x.device
+    codes = torch.empty((R, ldc), dtype=torch.uint8, device=dev)
+    if tile_major_scales:
+        rp = cdiv(max(R, 1), 4) * 4
+        scales = torch.empty((T, rp), dtype=torch.float32, device=dev)
+        s_row, s_col = 1, rp
+    else:
+        scales = torch.empty((R, T), dtype=torch.float32, device=dev)
+        s_row, s_col = T, 1
+    dq = None
+    if want_dq:
+        dq = torch.empty((R, K), dtype=dq_dtype or x.dtype, device=dev)
+    nan_rows = torch.zeros(R, dtype=torch.int32, device=dev) if want_nan_rows else None
+    call(
+        "ntlb_quant_tile_1x128", x2.data_ptr(), _dtype_code(x2.dtype), R, K, x2.stride(0), grid_code(fmt),
+        (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset, codes.data_ptr(), ldc,
+        scales.data_ptr(), s_row, s_col, _ptr(dq), _dtype_code(dq.dtype) if dq is not None else 0,
+        dq.stride(0) if dq is not None else 0, _ptr(nan_rows), _stream(),
+    )
+    return QTensor(codes, scales, s_row, s_col, 0, grid_code(fmt), R, K, nan_rows, dq)
+
+
+def quant_block_128x128(
+    w: torch.Tensor,
+    *,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    want_transposed: bool = False,
+    want_dq: bool = False,
+    dq_dtype: Optional[torch.dtype] = None,
+    want_nan_rows: bool = False,
+):
+    """te_backend.py:113-149 for a 2-D weight [N, K].
+
+    Returns (QTensor, QTensor-of-W^T or None).  The transposed operand shares
+    the scale tensor (block (nb, kb) of W is block (kb, nb) of W^T)."""
+    _require_device(w)
+    if w.dim() != 2:
+        raise ValueError("block_128x128 needs a 2-D weight")
+    w2 = w if w.stride(-1) == 1 else w.contiguous()
+    N, K = w2.shape
+    T, NB = cdiv(K, 128), cdiv(N, 128)
+    ldc = T * 128
+    dev = w.device
+    codes = torch.empty((N, ldc), dtype=torch.uint8, device=dev)
+    scales = torch.empty((NB, T), dtype=torch.float32, device=dev)
+    codes_t = torch.empty((K, NB * 128), dtype=torch.uint8, device=dev) if want_transposed else None
+    dq = torch.empty((N, K), dtype=dq_dtype or w.dtype, device=dev) if want_dq else None
+    nan_rows = torch.zeros(N, dtype=torch.int32, device=dev) if want_nan_rows else None
+    call(
+        "ntlb_quant_block_128x128", w2.data_ptr(), _dtype_code(w2.dtype), N, K, w2.stride(0), grid_code(fmt),
+        (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset, codes.data_ptr(), ldc,
+        _ptr(codes_t), NB * 128 if codes_t is not None else 0, scales.data_ptr(), T, 1, _ptr(dq),
+        _dtype_code(dq.dtype) if dq is not None else 0, dq.stride(0) if dq is not None else 0, _ptr(nan_rows),
+        _stream(),
+    )
+    q = QTensor(codes, scales, T, 1, 7, grid_code(fmt), N, K, nan_rows, dq)
+    qt = None
+    if codes_t is not None:
+        qt = QTensor(codes_t, scales, 1, T, 7, grid_code(fmt), K, N, None, None)
+    return q, qt
+
+
+def quant_tile_128x1_t(
+    x: torch.Tensor,
+    *,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    want_dq: bool = False,
+    dq_dtype: Optional[torch.dtype] = None,
+) -> QTensor:
+    """128x1 tiles of x [R, K] with transposed codes: a QTensor of x^T [K, R]."""
+    _require_device(x)
+    x2 = _as_2d(x)
+    R, K = x2.shape
+    MB = cdiv(R, 128)
+    ldct = MB * 128
+    dev = x.device
+    codes_t = torch.empty((K, ldct), dtype=torch.uint8, device=dev)
+    kp = cdiv(max(K, 1), 4) * 4
+    scales = torch.empty((MB, kp), dtype=torch.float32, device=dev)  # tile-major for the GEMM
+    dq = torch.empty((R, K), dtype=dq_dtype or x.dtype, device=dev) if want_dq else None
+    call(
+        "ntlb_quant_tile_128x1_t", x2.data_ptr(), _dtype_code(x2.dtype), R, K, x2.stride(0), grid_code(fmt),
+        (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset, codes_t.data_ptr(), ldct,
+        scales.data_ptr(), 1, kp, _ptr(dq), _dtype_code(dq.dtype) if dq is not None else 0,
+        dq.stride(0) if dq is not None else 0, None, _stream(),
+    )
+    return QTensor(codes_t, scales, 1, kp, 0, grid_code(fmt), K, R, None, dq)
+
+
+def quant_grouped(
+    x: torch.Tensor,
+    gr: int,
+    gc: int,
+    *,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    ldc: Optional[int] = None,
+    want_dq: bool = False,
+    dq_dtype: Optional[torch.dtype] = None,
+    want_nan_rows: bool = False,
+):
+    """One scale per (gr x gc) group of x viewed as [R, K].
+
+    Returns (codes [R, ldc], scales [ceil(R/gr), ceil(K/gc)], dq, nan_rows)."""
+    _require_device(x)
+    x2 = _as_2d(x)
+    R, K = x2.shape
+    gr = max(1, min(gr, max(R, 1)))
+    gc = max(1, min(gc, max(K, 1)))
+    ldc = K if ldc is None else ldc
+    dev = x.device
+    ngr, ngc = cdiv(R, gr), cdiv(K, gc)
+    amax = torch.zeros((ngr, ngc), dtype=torch.int32, device=dev)
+    codes = torch.zeros((R, ldc), dtype=torch.uint8, device=dev)
+    scales = torch.empty((ngr, ngc), dtype=torch.float32, device=dev)
+    dq = torch.empty((R, K), dtype=dq_dtype or x.dtype, device=dev) if want_dq else None
+    nan_rows = torch.zeros(R, dtype=torch.int32, device=dev) if want_nan_rows else None
+    xc = _dtype_code(x2.dtype)
+    call("ntlb_amax_grouped", x2.data_ptr(), xc, R, K, x2.stride(0), gr, gc, amax.data_ptr(), _stream())
+    call(
+        "ntlb_quant_grouped", x2.data_ptr(), xc, R, K, x2.stride(0), gr, gc, amax.data_ptr(), grid_code(fmt),
+        (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset, codes.data_ptr(), ldc,
+        scales.data_ptr(), _ptr(dq), _dtype_code(dq.dtype) if dq is not None else 0,
+        dq.stride(0) if dq is not None else 0, _ptr(nan_rows), _stream(),
+    )
+    return codes, scales, dq, nan_rows
+
+
+def gemm_blockscaled(
+    a: QTensor,
+    b: QTensor,
+    *,
+    bias: Optional[torch.Tensor] = None,
+    out_dtype: torch.dtype = torch.bfloat16,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Y[M, N] = dequant(a) @ dequant(b)^T (+ bias), fp32 accumulation."""
+    _require_device(a.codes, b.codes, bias)
+    if a.grid != b.grid:
+        raise ValueError("operands must share a code format")
+    if a.K != b.K:
+        raise ValueError(f"contraction mismatch: {a.K} vs {b.K}")
+    M, N, Kp = a.rows, b.rows, a.Kp
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.codes.device)
+    if bias is not None and bias.stride(-1) != 1:
+        bias = bias.contiguous()
+    call(
+        "ntlb_gemm_blockscaled", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
+        a.s_col, a.shift, b.codes.data_ptr(), b.codes.stride(0), b.scales.data_ptr(), b.s_row, b.s_col, b.shift,
+        M, N, Kp, _ptr(bias), _dtype_code(bias.dtype) if bias is not None else 0, out.data_ptr(),
+        _dtype_code(out.dtype), out.stride(0), _ptr(a.nan_rows), _ptr(b.nan_rows), _stream(),
+    )
+    return out

@@ -1,0 +1,155 @@
+"""GPU parity of the quantizers against the CPU oracle: codes, scales, dq and
+NaN row flags must be bit-exact on identical seeded inputs."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import assert_bits_equal, scales_row_major, seeded, to_np32
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GRIDS = [("int_grid", O.GRID_INT), ("e4m3", O.GRID_E4M3)]
+ROUNDS = [("nearest", O.ROUND_NEAREST), ("stochastic", O.ROUND_STOCHASTIC)]
+SHAPES = [(3, 257), (64, 1024), (130, 300), (512, 1024), (1, 8), (5, 4)]
+
+
+def _check_tile(x, fmt, grid, rname, rcode, bits=8, seed=0, offset=0):
+    from lowbit import ops
+
+    R, K = x.reshape(-1, x.shape[-1]).shape
+    q = ops.quant_tile_1x128(x, fmt=fmt, bits=bits, rounding=rname, seed=seed, offset=offset, want_dq=True,
+                             want_nan_rows=True)
+    torch.cuda.synchronize()
+    xn = to_np32(x).reshape(R, K)
+    codes, scales, qv, dq = O.quant_tile_1x128(xn, grid=grid, bits=bits, rounding=rcode, seed=seed, offset=offset)
+    assert_bits_equal(q.codes.cpu().numpy(), codes, "codes")
+    assert_bits_equal(scales_row_major(q, R, scales.shape[1]), scales, "scales")
+    dq_ref = torch.from_numpy(dq).to(x.dtype).float().numpy()
+    assert_bits_equal(to_np32(q.dq), dq_ref, "dq")
+    nan_ref = np.isnan(qv).any(axis=1).astype(np.int32)
+    assert np.array_equal(q.nan_rows.cpu().numpy(), nan_ref)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_tile_1x128_parity(gpu_device, shape, fmt, grid, rname, rcode, dtype):
+    x = seeded(shape, seed=20260101, dtype=dtype, outliers=0.01).to(gpu_device)
+    _check_tile(x, fmt, grid, rname, rcode, seed=1234, offset=7)
+
+
+def test_tile_1x128_fp4_mode_and_3d(gpu_device):
+    # bits=4 (the fp4 emulated mode, qmax 7) on a 3-D activation
+    x = seeded((2, 3, 257), seed=20260102, dtype=torch.bfloat16).to(gpu_device)
+    _check_tile(x, "int_grid", O.GRID_INT, "nearest", O.ROUND_NEAREST, bits=4)
+
+
+def test_tile_1x128_special_values(gpu_device):
+    x = torch.zeros(6, 256)
+    x[1, :3] = torch.tensor([float("inf"), 2.6, -300.0])
+    x[2, :3] = torch.tensor([float("nan"), 2.6, -300.0])
+    x[3, :2] = torch.tensor([1e-45, -1e-45])
+    x[4, 130] = -0.0
+    x[5] = torch.linspace(-3, 3, 256)
+    for dtype in (torch.float32, torch.bfloat16):
+        for fmt, grid in GRIDS:
+            for rname, rcode in ROUNDS:
+                _check_tile(x.to(dtype).to(gpu_device), fmt, grid, rname, rcode, seed=5)
+
+
+@pytest.mark.parametrize("shape", [(300, 260), (128, 128), (1024, 1024), (129, 520)])
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+def test_block_128x128_parity(gpu_device, shape, fmt, grid, rname, rcode):
+    from lowbit import ops
+
+    w = seeded(shape, seed=20260103, std=0.02).to(gpu_device)
+    q, qt = ops.quant_block_128x128(w, fmt=fmt, rounding=rname, seed=99, offset=3, want_transposed=True,
+                                    want_dq=True)
+    torch.cuda.synchronize()
+    N, K = shape
+    codes, scales, qv, dq = O.quant_block_128x128(to_np32(w), grid=grid, rounding=rcode, seed=99, offset=3)
+    assert_bits_equal(q.codes.cpu().numpy(), codes, "codes")
+    assert_bits_equal(q.scales.cpu().numpy(), scales, "scales")
+    assert_bits_equal(to_np32(q.dq), torch.from_numpy(dq).to(w.dtype).float().numpy(), "dq")
+    NB = -(-N // 128)
+    ct = np.zeros((K, NB * 128), dtype=np.uint8)
+    ct[:, :N] = codes[:, :K].T
+    assert_bits_equal(qt.codes.cpu().numpy(), ct, "codes_t")
+
+
+@pytest.mark.parametrize("shape", [(300, 70), (256, 1024), (130, 257)])
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+def test_tile_128x1_transposed_parity(gpu_device, shape, fmt, grid, rname, rcode):
+    from lowbit import ops
+
+    x = seeded(shape, seed=20260104, std=1e-3).to(gpu_device)
+    q = ops.quant_tile_128x1_t(x, fmt=fmt, rounding=rname, seed=17, offset=11, want_dq=True)
+    torch.cuda.synchronize()
+    R, K = shape
+    ct, st, qv, dq = O.quant_tile_128x1_t(to_np32(x), grid=grid, rounding=rcode, seed=17, offset=11)
+    assert_bits_equal(q.codes.cpu().numpy(), ct, "codes_t")
+    assert_bits_equal(scales_row_major(q, K, st.shape[1]), st, "scales")
+    assert_bits_equal(to_np32(q.dq), torch.from_numpy(dq).to(x.dtype).float().numpy(), "dq")
+
+
+@pytest.mark.parametrize("kind", ["tensor", "channel_last", "channel_rows", "strip"])
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+def test_grouped_parity(gpu_device, kind, fmt, grid, rname, rcode):
+    from lowbit import ops
+
+    R, K = 300, 520
+    x = seeded((R, K), seed=20260105, outliers=0.01).to(gpu_device)
+    gr, gc, rule = {
+        "tensor": (R, K, O.SCALE_AFTER_DIVIDE),
+        "channel_last": (R, 1, O.SCALE_AFTER_DIVIDE),
+        "channel_rows": (1, K, O.SCALE_AFTER_DIVIDE),
+        "strip": (R, 128, O.SCALE_BEFORE_DIVIDE),
+    }[kind]
+    codes, scales, dq, nan_rows = ops.quant_grouped(x, gr, gc, fmt=fmt, rounding=rname, seed=3, offset=1,
+                                                    scale_rule=rule, want_dq=True, want_nan_rows=True)
+    torch.cuda.synchronize()
+    c2, s2, q2, d2 = O.quant_grouped(to_np32(x), gr, gc, grid=grid, rounding=rcode, seed=3, offset=1, scale_rule=rule)
+    assert_bits_equal(codes.cpu().numpy(), c2, "codes")
+    assert_bits_equal(scales.cpu().numpy(), s2, "scales")
+    assert_bits_equal(to_np32(dq), torch.from_numpy(d2).to(x.dtype).float().numpy(), "dq")
+
+
+def test_strip_subnormal_amax_rule(gpu_device):
+    from lowbit import ops
+
+    x = torch.zeros(4, 128)
+    x[0, :2] = torch.tensor([1e-45, -1e-45])
+    x = x.to(gpu_device)
+    codes, scales, dq, _ = ops.quant_grouped(x, 4, 128, scale_rule=O.SCALE_BEFORE_DIVIDE, want_dq=True)
+    c2, s2, q2, d2 = O.quant_grouped(to_np32(x), 4, 128, scale_rule=O.SCALE_BEFORE_DIVIDE)
+    assert_bits_equal(codes.cpu().numpy(), c2, "codes")
+    assert_bits_equal(scales.cpu().numpy(), s2, "scales")
+    assert_bits_equal(to_np32(dq), d2, "dq")
+
+
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+def test_full_size_c2_activation_and_weight(gpu_device, fmt, grid):
+    """Bit-exact at the DeepSeek-V3 MLP shapes of BASELINE config 2."""
+    from lowbit import ops
+
+    x = seeded((8192, 7168), seed=20260201, heavy_channels=True).to(gpu_device)
+    q = ops.quant_tile_1x128(x, fmt=fmt, tile_major_scales=False)
+    torch.cuda.synchronize()
+    codes, scales, _, _ = O.quant_tile_1x128(to_np32(x), grid=grid)
+    assert_bits_equal(q.codes.cpu().numpy(), codes, "X codes")
+    assert_bits_equal(q.scales.cpu().numpy(), scales, "X scales")
+    del q, x
+    w = seeded((18432, 7168), seed=20260202, std=0.006).to(gpu_device)
+    qw, _ = ops.quant_block_128x128(w, fmt=fmt)
+    torch.cuda.synchronize()
+    codes, scales, _, _ = O.quant_block_128x128(to_np32(w), grid=grid)
+    assert_bits_equal(qw.codes.cpu().numpy(), codes, "W codes")
+    assert_bits_equal(qw.scales.cpu().numpy(), scales, "W scales")

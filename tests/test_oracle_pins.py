@@ -1,0 +1,386 @@
+"""Pins for the CPU oracle (oracle/lowbit_oracle.c + oracle/oracle.py).
+
+The reference holds no numeric fixtures for this path, so each oracle function
+is pinned here by an independent source: published known-answer vectors
+(Philox), a library routine (torch's float8_e4m3fn cast, numpy argmin, Python's
+round-half-even), closed forms built into the inputs (per-tile amax values
+that fix every scale exactly), or the format's specification table (OCP e2m1).
+Each pin is chosen so that a plausible mistake (a dropped /qmax, a transposed
+block index, a wrong tie rule, swapped nibbles) fails it.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+# ---------------------------------------------------------------------------
+# Philox4x32-10: known-answer vectors of Random123 (Salmon et al., SC'11)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize(
+    "ctr,key,expect",
+    [
+        ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
+        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
+        (
+            [0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344],
+            [0xA4093822, 0x299F31D0],
+            [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1],
+        ),
+    ],
+)
+def test_philox_known_answers(ctr, key, expect):
+    assert list(O.philox4x32_10(ctr, key)) == expect
+
+
+def test_sr_bits_contract_layout():
+    seed, offset = 0x1234_5678_9ABC_DEF0, 0x0000_0002_0000_0007
+    bits = O.sr_bits(seed, offset, 40, 8)
+    for j in range(8):
+        e = 40 + j
+        g = e // 4
+        ctr = [g & 0xFFFFFFFF, g >> 32, offset & 0xFFFFFFFF, offset >> 32]
+        key = [seed & 0xFFFFFFFF, seed >> 32]
+        assert bits[j] == O.philox4x32_10(ctr, key)[e % 4]
+
+
+def test_sr_uniform_statistics():
+    bits = O.sr_bits(7, 3, 0, 1 << 16)
+    u = (bits >> 8).astype(np.float64) * 2.0**-24
+    assert abs(u.mean() - 0.5) < 0.01
+    assert abs(u.var() - 1 / 12) < 0.005
+
+
+# ---------------------------------------------------------------------------
+# e4m3: torch's float8_e4m3fn cast is the library oracle
+# ---------------------------------------------------------------------------
+def test_e4m3_encode_matches_torch_on_all_bf16():
+    f = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    mine = O.e4m3_encode(f)
+    ref = torch.from_numpy(f.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(mine, ref)
+
+
+def test_e4m3_encode_matches_torch_on_random_fp32():
+    rng = np.random.default_rng(1)
+    f = rng.integers(0, 2**32, size=2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    # concentrate on the e4m3 range and its rounding boundaries as well
+    g = (rng.standard_normal(1_000_000) * 100).astype(np.float32)
+    for arr in (f, g):
+        mine = O.e4m3_encode(arr)
+        ref = torch.from_numpy(arr.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(mine, ref)
+
+
+def test_e4m3_decode_matches_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    mine = O.decode_codes(codes, O.GRID_E4M3)
+    ref = torch.from_numpy(codes.copy()).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(np.isnan(mine), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(mine[ok].view(np.uint32), ref[ok].view(np.uint32))
+
+
+# ---------------------------------------------------------------------------
+# int grid, round to nearest: te_backend.py:82-110
+# ---------------------------------------------------------------------------
+def test_round_half_even_textbook():
+    # amax = 127 makes the scale exactly 1.0, so q = round-half-even(x)
+    vals = [0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -125.5, 3.4999998, 0.49999997, 127.0]
+    x = np.zeros((1, 128), dtype=np.float32)
+    x[0, : len(vals)] = vals
+    codes, scales, q, dq = O.quant_tile_1x128(x)
+    assert scales[0, 0] == np.float32(1.0)
+    expect = [round(v) for v in vals]  # Python rounds half to even
+    assert list(q[0, : len(vals)]) == expect
+    assert list(codes[0, : len(vals)].view(np.int8)) == expect
+    assert np.array_equal(dq, q)
+
+
+def test_tile_scales_follow_tile_index():
+    # tile (r, t) holds amax a_rt = 10*(r+1) + t at a known column; every other
+    # element is smaller.  A transposed tile index or a dropped /qmax fails.
+    R, K = 3, 300
+    rng = np.random.default_rng(2)
+    x = (rng.uniform(-1, 1, size=(R, K))).astype(np.float32)
+    T = 3
+    for r in range(R):
+        for t in range(T):
+            col = t * 128 + (17 * r + 5 * t) % min(128, K - t * 128)
+            x[r, col] = -(10.0 * (r + 1) + t) if (r + t) % 2 else 10.0 * (r + 1) + t
+    codes, scales, q, dq = O.quant_tile_1x128(x)
+    assert codes.shape == (R, 384)
+    for r in range(R):
+        for t in range(T):
+            assert scales[r, t] == np.float32(10.0 * (r + 1) + t) / np.float32(127.0)
+    # padding columns are zero codes; the amax element lands on +-127
+    assert not codes[:, 300:].any()
+    assert np.abs(q).max() == 127
+
+
+def test_block_scales_follow_block_index():
+    N, K = 300, 260  # 3 x 3 blocks, partial last row and column blocks
+    rng = np.random.default_rng(3)
+    w = rng.uniform(-0.5, 0.5, size=(N, K)).astype(np.float32)
+    for nb in range(3):
+        for kb in range(3):
+            r = nb * 128 + (31 * kb + 7 * nb) % min(128, N - nb * 128)
+            c = kb * 128 + (13 * nb + 3 * kb) % min(128, K - kb * 128)
+            w[r, c] = 1.0 + 7 * nb + kb
+    codes, scales, q, dq = O.quant_block_128x128(w)
+    for nb in range(3):
+        for kb in range(3):
+            assert scales[nb, kb] == np.float32(1.0 + 7 * nb + kb) / np.float32(127.0)
+    assert codes.shape == (N, 384) and not codes[:, 260:].any()
+
+
+def test_rn_reconstruction_invariants():
+    rng = np.random.default_rng(4)
+    x = (rng.standard_normal((64, 512)) * np.exp(rng.uniform(-3, 3, size=(64, 1)))).astype(np.float32)
+    codes, scales, q, dq = O.quant_tile_1x128(x)
+    s = np.repeat(scales, 128, axis=1)
+    assert np.all(np.abs(x - dq) <= s * 0.5000001)
+    assert np.all(np.abs(q).reshape(64, 4, 128).max(axis=2) == 127)
+
+
+def test_special_values():
+    x = np.zeros((4, 128), dtype=np.float32)
+    x[1, :3] = [np.inf, 2.6, -300.0]
+    x[2, :3] = [np.nan, 2.6, -300.0]
+    x[3, :2] = [1e-45, -1e-45]  # subnormal amax
+    codes, scales, q, dq = O.quant_tile_1x128(x)
+    # zero tile: scale 1 (te_backend.py:74-79 applied after the division)
+    assert scales[0, 0] == 1.0 and not codes[0].any()
+    # inf: amax/127 = inf -> scale 1, inf clamps to 127, the rest round(x) clamped
+    assert scales[1, 0] == 1.0 and list(q[1, :3]) == [127.0, 3.0, -127.0]
+    # NaN: amax NaN -> scale 1, NaN code -128, dq NaN
+    assert scales[2, 0] == 1.0 and codes[2, 0] == 0x80 and np.isnan(dq[2, 0])
+    assert list(q[2, 1:3]) == [3.0, -127.0]
+    # subnormal amax: amax/127 underflows to 0 -> scale 1 under the te_backend rule
+    assert scales[3, 0] == 1.0 and list(q[3, :2]) == [0.0, -0.0]
+    # the moe.py:94-98 rule checks amax > 0 first: scale = amax/127 = 0 -> x/0
+    _, s2, q2, _ = O.quant_grouped(x[3:4], 1, 128, scale_rule=O.SCALE_BEFORE_DIVIDE)
+    assert s2[0, 0] == 0.0 and q2[0, 0] == 127.0 and q2[0, 1] == -127.0 and np.isnan(q2[0, 2])
+
+
+def test_negative_zero_kept_in_q():
+    x = np.zeros((1, 128), dtype=np.float32)
+    x[0, 0] = 127.0
+    x[0, 1] = -0.3
+    _, _, q, dq = O.quant_tile_1x128(x)
+    assert np.signbit(q[0, 1]) and np.signbit(dq[0, 1])
+
+
+# ---------------------------------------------------------------------------
+# stochastic rounding
+# ---------------------------------------------------------------------------
+def test_sr_int_grid_brackets_and_is_unbiased():
+    x = np.zeros((1, 128), dtype=np.float32)
+    x[0, 0] = 127.0  # scale 1
+    x[0, 1:6] = [2.25, -2.25, 5.0, -7.0, 0.75]
+    acc = np.zeros(6)
+    draws = 4000
+    for s in range(draws):
+        _, _, q, _ = O.quant_tile_1x128(x, rounding=O.ROUND_STOCHASTIC, seed=s, offset=9)
+        v = x[0, 1:6]
+        assert np.all((q[0, 1:6] == np.floor(v)) | (q[0, 1:6] == np.ceil(v)))
+        assert q[0, 3] == 5.0 and q[0, 4] == -7.0  # integers are exact
+        acc[:5] += q[0, 1:6]
+    mean = acc[:5] / draws
+    assert abs(mean[0] - 2.25) < 0.03 and abs(mean[1] + 2.25) < 0.03 and abs(mean[4] - 0.75) < 0.03
+
+
+def test_sr_uses_contract_bits():
+    # floor(v + u) with u from the Philox contract, element index r*K + k
+    x = np.full((2, 131), 0.5, dtype=np.float32)
+    x[:, 0] = 127.0  # both tiles get scale 1
+    x[:, 128] = 127.0
+    _, _, q, _ = O.quant_tile_1x128(x, rounding=O.ROUND_STOCHASTIC, seed=11, offset=5)
+    bits = O.sr_bits(11, 5, 0, 2 * 131).reshape(2, 131)
+    u = (bits >> 8).astype(np.float32) * np.float32(2.0**-24)
+    expect = np.floor(np.float32(0.5) + u)
+    cols = [c for c in range(131) if c not in (0, 128)]
+    assert np.array_equal(q[:, cols], expect[:, cols])
+    assert 0 < q[:, cols].mean() < 1
+
+
+def test_sr_e4m3_brackets_and_is_unbiased():
+    v = np.array([1.1, -3.3, 0.004, 300.0, -0.017], dtype=np.float32)
+    n = 20000
+    bits = O.sr_bits(3, 1, 0, n * v.size).reshape(n, v.size)
+    codes = O.e4m3_sr_encode(np.broadcast_to(v, (n, v.size)), bits)
+    vals = O.decode_codes(codes, O.GRID_E4M3)
+    lo = O.decode_codes(O.e4m3_encode(v), O.GRID_E4M3)
+    for j in range(v.size):
+        uniq = np.unique(vals[:, j])
+        assert len(uniq) <= 2
+        assert lo[j] in uniq or len(uniq) == 1
+        assert abs(vals[:, j].mean() - v[j]) < abs(v[j]) * 0.01 + 2e-4
+
+
+def test_e4m3_grid_scale_and_range():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((8, 256)) * 3).astype(np.float32)
+    codes, scales, q, dq = O.quant_tile_1x128(x, grid=O.GRID_E4M3)
+    amax = np.abs(x).reshape(8, 2, 128).max(axis=2)
+    assert np.array_equal(scales, amax / np.float32(448.0))
+    assert np.abs(q).max() == 448.0
+    ref = torch.from_numpy((x / np.repeat(scales, 128, axis=1)).clip(-448, 448)).to(torch.float8_e4m3fn)
+    assert np.array_equal(codes, ref.view(torch.uint8).numpy())
+
+
+# ---------------------------------------------------------------------------
+# grouped granularities: tensor / channel / strip (te_backend.py:165-185, moe.py:123-140)
+# ---------------------------------------------------------------------------
+def test_grouped_scales_follow_groups():
+    R, K = 5, 260
+    rng = np.random.default_rng(6)
+    x = rng.uniform(-1, 1, size=(R, K)).astype(np.float32)
+    x[3, 200] = 9.0
+    # tensor
+    _, s, _, _ = O.quant_grouped(x, R, K)
+    assert s.shape == (1, 1) and s[0, 0] == np.float32(9.0) / np.float32(127)
+    # channel along the last axis: one scale per column over all rows
+    _, s, _, _ = O.quant_grouped(x, R, 1)
+    assert s.shape == (1, K)
+    assert np.array_equal(s[0], np.abs(x).max(axis=0) / np.float32(127))
+    # channel along axis 0: one scale per row
+    _, s, _, _ = O.quant_grouped(x, 1, K)
+    assert np.array_equal(s[:, 0], np.abs(x).max(axis=1) / np.float32(127))
+    # comm strip: one scale per 128 columns over all rows
+    _, s, _, _ = O.quant_grouped(x, R, 128, scale_rule=O.SCALE_BEFORE_DIVIDE)
+    expect = [np.abs(x[:, i : i + 128]).max() / np.float32(127) for i in (0, 128, 256)]
+    assert list(s[0]) == expect
+
+
+def test_tile_128x1_is_tile_of_transpose():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((300, 70)).astype(np.float32)
+    ct, st, q, dq = O.quant_tile_128x1_t(x)
+    c2, s2, q2, dq2 = O.quant_tile_1x128(np.ascontiguousarray(x.T))
+    assert np.array_equal(ct, c2) and np.array_equal(st, s2)
+    assert np.array_equal(dq, dq2.T)
+
+
+# ---------------------------------------------------------------------------
+# GEMM oracle: exact integer arithmetic when the scales are powers of two
+# ---------------------------------------------------------------------------
+def test_gemm_oracle_exact_on_power_of_two_scales():
+    rng = np.random.default_rng(8)
+    M, N, K = 37, 45, 256
+    qa = rng.integers(-127, 128, size=(M, K))
+    qb = rng.integers(-127, 128, size=(N, K))
+    sa = 2.0 ** rng.integers(-6, 6, size=(M, 2))
+    sb = 2.0 ** rng.integers(-6, 6, size=(1, 2))
+    a_dq = O.dequant_grouped(qa.astype(np.int8).view(np.uint8), sa.astype(np.float32), K, 1, 128, O.GRID_INT)
+    b_dq = O.dequant_grouped(qb.astype(np.int8).view(np.uint8), sb.astype(np.float32), K, 128, 128, O.GRID_INT)
+    y = O.gemm_ref(a_dq, b_dq)
+    exact = np.zeros((M, N))
+    for kb in range(2):
+        part = qa[:, kb * 128 : (kb + 1) * 128] @ qb[:, kb * 128 : (kb + 1) * 128].T
+        exact += part * sa[:, kb : kb + 1] * sb[0, kb]
+    assert np.array_equal(y, exact)
+
+
+def test_bf16_rounding_helper_matches_torch():
+    rng = np.random.default_rng(9)
+    f = rng.integers(0, 2**32, size=200_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    mine = O.to_bf16_bits(f)
+    ref = torch.from_numpy(f.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    ok = ~np.isnan(f)
+    assert np.array_equal(mine[ok], ref[ok])
+
+
+# ---------------------------------------------------------------------------
+# NF4 (layers.py:60-184): numpy argmin (first minimum) is the library oracle
+# ---------------------------------------------------------------------------
+def test_nf4_indices_match_numpy_argmin():
+    rng = np.random.default_rng(10)
+    w = (rng.standard_normal(4096) * 0.02).astype(np.float32)
+    w[5] = np.nan
+    for block in (64, 4096):
+        packed, scales = O.nf4_quant(w, block)
+        idx = np.empty(w.size, dtype=np.int64)
+        idx[0::2] = packed & 15
+        idx[1::2] = packed >> 4
+        s = np.repeat(scales, block)[: w.size]
+        c = np.clip(w / s, -1.0, 1.0).astype(np.float32)
+        d = np.abs(c[:, None] - O.NF4_CODEBOOK[None, :])
+        expect = np.where(np.isnan(c), 0, np.nanargmin(np.where(np.isnan(d), np.inf, d), axis=1))
+        assert np.array_equal(idx, expect)
+
+
+def test_nf4_ties_pick_lower_index_and_pack_low_nibble_first():
+    cb = O.NF4_CODEBOOK
+    mids = [(cb[i] + cb[i + 1]) / np.float32(2) for i in range(15)]
+    w = np.array([1.0] + mids, dtype=np.float32)  # amax 1 -> scale 1, normalized = w
+    packed, scales = O.nf4_quant(w, w.size)
+    assert scales[0] == 1.0
+    idx = np.empty(16, dtype=np.int64)
+    idx[0::2] = packed & 15
+    idx[1::2] = packed >> 4
+    assert idx[0] == 15
+    for i in range(15):
+        m = np.float32(mids[i])
+        dl, dh = abs(m - cb[i]), abs(m - cb[i + 1])
+        assert idx[i + 1] == (i if dl <= dh else i + 1)
+    # nibble order on a hand-built example
+    w2 = np.array([-1.0, 1.0, 0.0], dtype=np.float32)
+    p2, _ = O.nf4_quant(w2, 3)
+    assert list(p2) == [0x0 | (0xF << 4), 0x7]
+
+
+def test_nf4_dequant_round_trip_error_bound():
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal(64 * 100) * 0.02).astype(np.float32)
+    packed, scales = O.nf4_quant(w, 64)
+    d = O.nf4_dequant(packed, scales, w.size, 64)
+    gap = np.max(np.diff(O.NF4_CODEBOOK))
+    assert np.all(np.abs(d - w) <= np.repeat(scales, 64) * gap / 2 + 1e-7)
+
+
+# ---------------------------------------------------------------------------
+# MXFP4 (OCP MX v1.0): e2m1 table and the shared-exponent rule
+# ---------------------------------------------------------------------------
+def test_e2m1_table():
+    vals = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], dtype=np.float32)
+    codes = np.arange(16, dtype=np.uint8)
+    dec = np.array([O.decode_codes(np.array([0]), 0)[0]])  # warm the lib
+    del dec
+    enc = O.e2m1_encode(np.concatenate([vals, -vals]))
+    assert list(enc) == list(range(8)) + [8 | i for i in range(8)]
+    # midpoints round to the even code; above 6 saturates
+    mids = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0, 7.9, 100.0], dtype=np.float32)
+    assert list(O.e2m1_encode(mids)) == [0, 2, 2, 4, 4, 6, 6, 7, 7]
+    assert codes.size == 16
+
+
+def test_mxfp4_shared_exponent():
+    w = np.zeros(64, dtype=np.float32)
+    w[0] = 6.0  # floor(log2 6) = 2 -> X = 2^0
+    w[32] = 1.0  # floor(log2 1) = 0 -> X = 2^-2, 1.0 -> e2m1 4.0
+    w[33] = 0.3  # 0.3 / 0.25 = 1.2 -> 1.0
+    packed, scales = O.mxfp4_quant(w)
+    assert list(scales) == [127, 125]
+    d = O.mxfp4_dequant(packed, scales, 64)
+    assert d[0] == 6.0 and d[32] == 1.0 and d[33] == 0.25
+    w2 = np.full(32, np.nan, dtype=np.float32)
+    p2, s2 = O.mxfp4_quant(w2)
+    assert s2[0] == 0xFF and np.isnan(O.mxfp4_dequant(p2, s2, 32)).all()
+
+
+def test_fp8_persistent_matches_torch_formula():
+    # layers.py:104-117 evaluated with torch ops is the library oracle here
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((16, 64)) * 0.02).astype(np.float32)
+    codes, scales = O.fp8_persistent_quant(w, 64)
+    t = torch.from_numpy(w)
+    s = t.abs().amax(dim=1, keepdim=True)
+    ref = (t / s).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy().reshape(-1)
+    assert np.array_equal(codes, ref) and np.array_equal(scales, s.numpy().reshape(-1))
