@@ -1,0 +1,220 @@
+"""Benchmark of the low-bit linear hot path on one MI355X.
+
+One step = one emulated-FP8 Linear forward of BASELINE config 2 (the
+DeepSeek-V3 dense MLP up-projection): quantize X [8192, 7168] per 1x128 tile,
+quantize W [18432, 7168] per 128x128 block (e4m3, amax/448 scales, round to
+nearest), and the blockwise-scaled FP8 GEMM Y = X_dq W_dq^T (fp32 accumulate,
+bf16 out).  Inputs are resident in HBM before the timed region; three input
+sets rotate so that no step reads its inputs from the 256 MB Infinity Cache.
+
+`value` = GEMM FLOPs per step / step time (quantizers included).  The
+`roofline` object is the GEMM kernel alone, timed with HIP events on the
+stream the kernels run on.  `cpu_baseline` times the CPU oracle (oracle/,
+numpy + C) on a 1024-row sample of the same workload.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--format e4m3|int_grid]
+                  [--rounding nearest|stochastic] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "nano-train_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0  # dense fp8 (and int8 TOP/s) of MI355X
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--format", default="e4m3", choices=["e4m3", "int_grid"])
+    p.add_argument("--rounding", default="nearest", choices=["nearest", "stochastic"])
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-sample-rows", type=int, default=1024)
+    p.add_argument("--calib-copy", action="store_true",
+                   help="also launch a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
+    return p.parse_args()
+
+
+def cpu_baseline(fmt: str, rounding: str, rows: int):
+    """The CPU oracle's emulated linear (te_backend.py:229-260 restated) on a row sample."""
+    import numpy as np
+    import torch
+
+    from lowbit import workloads
+    from oracle import oracle as O
+
+    x, w = workloads.c2_inputs(device="cpu", rows=rows)
+    xn = x.float().numpy()
+    wn = w.float().numpy()
+    grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    O.lib()
+    t0 = time.perf_counter()
+    y = O.emulated_linear_forward(xn, wn, grid=grid, rounding=rc)
+    dt = time.perf_counter() - t0
+    flops = 2.0 * rows * wn.shape[0] * wn.shape[1]
+    threads = None
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:
+        threads = os.cpu_count()
+    del y
+    return {
+        "value": round(flops / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": int(threads or 1),
+        "kind": "port",
+        "sample": (f"oracle emulated linear (1x128 X quant + 128x128 W quant in C on 1 thread, "
+                   f"fp32 dequant, numpy fp32 matmul on {threads} BLAS threads) over X rows [0, {rows}) "
+                   f"of config 2 with the full W [18432, 7168]; {dt:.2f} s; CPU {_cpu_model()}"),
+    }
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build covers one GPU only; run with --gpus 1 "
+                                   "(the sharding design is described in DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+
+    from lowbit import ops, workloads
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    shp = workloads.SHAPES[2]
+    M, N, K = shp["M"], shp["N"], shp["K"]
+
+    # input set 0 from the seeded CPU generators (identical to the parity tests),
+    # sets 1 and 2 are device-side permutations of it at other addresses
+    x0, w0 = workloads.c2_inputs(device="cpu")
+    x0, w0 = x0.to(dev), w0.to(dev)
+    sets = [(x0, w0), (-x0, w0.flip(0).contiguous()), (x0.flip(0).contiguous(), -w0)]
+    torch.cuda.synchronize()
+
+    rounding = args.rounding
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev=None):
+        x, w = sets[i % len(sets)]
+        if ev is not None:
+            ev[0].record(stream)
+        qx = ops.quant_tile_1x128(x, fmt=args.format, rounding=rounding, seed=1, offset=2 * i)
+        if ev is not None:
+            ev[1].record(stream)
+        qw, _ = ops.quant_block_128x128(w, fmt=args.format, rounding=rounding, seed=1, offset=2 * i + 1)
+        if ev is not None:
+            ev[2].record(stream)
+        y = ops.gemm_blockscaled(qx, qw, out_dtype=torch.bfloat16)
+        if ev is not None:
+            ev[3].record(stream)
+        return y
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        y = step(args.warmup + i, events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    del y
+
+    qx_ms = [e[0].elapsed_time(e[1]) for e in events]
+    qw_ms = [e[1].elapsed_time(e[2]) for e in events]
+    gm_ms = [e[2].elapsed_time(e[3]) for e in events]
+    step_ms = [e[0].elapsed_time(e[3]) for e in events]
+    avg = lambda v: sum(v) / len(v)
+    flops = 2.0 * M * N * K
+    ms_per_step = wall * 1e3 / args.steps
+    value = flops / (ms_per_step * 1e-3) / 1e12
+
+    # algorithmic bytes of the quantizers: bf16 in + 1-byte code + fp32 scale per tile/block
+    qx_bytes = M * K * 2 + M * K + M * (K // 128) * 4
+    qw_bytes = N * K * 2 + N * K + (N // 128) * (K // 128) * 4
+    gemm_tflops = flops / (avg(gm_ms) * 1e-3) / 1e12
+    # the GEMM's own minimum HBM traffic: both code matrices, their scales, bf16 out
+    gemm_min_bytes = M * K + N * K + M * (K // 128) * 4 + (N // 128) * (K // 128) * 4 + M * N * 2
+
+    if args.calib_copy:
+        a = torch.empty(1 << 29, dtype=torch.int16, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+
+    result = {
+        "metric": "FP8 blockwise GEMM TFLOP/s (% fp8 MFMA peak); quantizer GB/s (% HBM peak)",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3" if args.format == "e4m3" else "int8",
+        "data": "synthetic (seeded, BASELINE config 2 distributions); 3 rotating input sets",
+        "config": {
+            "workload": "c2 DeepSeek-V3 dense MLP up-projection forward: quant X 1x128 + quant W 128x128 + "
+                        "blockwise-scaled GEMM",
+            "M": M, "N": N, "K": K, "code_format": args.format, "rounding": rounding,
+            "out_dtype": "bf16", "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "gemm_blockscaled_kernel",
+            "achieved": round(gemm_tflops, 2),
+            "peak": FP8_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
+            "traffic": None,
+            "avg_ms": round(avg(gm_ms), 4),
+            "min_hbm_bytes": gemm_min_bytes,
+        },
+        "quantizers": {
+            "x_tile_1x128": {"avg_us": round(avg(qx_ms) * 1e3, 2), "bytes": qx_bytes,
+                             "GB/s": round(qx_bytes / (avg(qx_ms) * 1e-3) / 1e9, 1),
+                             "frac_hbm": round(qx_bytes / (avg(qx_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "w_block_128x128": {"avg_us": round(avg(qw_ms) * 1e3, 2), "bytes": qw_bytes,
+                                "GB/s": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9, 1),
+                                "frac_hbm": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        },
+        "event_ms_per_step": round(avg(step_ms), 4),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.format, rounding, args.cpu_sample_rows)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -6,13 +6,19 @@
 //   int-grid codes: 2x v_mfma_i32_16x16x64_i8, exact int32 partials
 //     (|partial| <= 128*127^2 < 2^24, so the int32 -> fp32 conversion is exact)
 // and the partial tile is promoted into the fp32 accumulator with
-// sa(m,kb)*sb(n,kb) in VALU.
+// sa(m,kb)*sb(n,kb) in VALU, one FMA per accumulator per K block.
 //
-// Block tile 128x128, K step 128 (= one scale block), 256 threads as 2x2 waves
-// of 64x64.  A and B tiles go global -> registers -> LDS (double buffered,
-// 16-byte chunks XOR-swizzled by row so the MFMA fragment reads are
-// bank-conflict free); the next K block's loads are in flight while the current
-// one is multiplied.
+// Tiling: 256x256 output tile per workgroup, K step 128 (= one scale block),
+// 512 threads = 8 waves as 2 (M) x 4 (N), each wave 128x64.  The MFMA is fed
+// with the B tile as its first operand and the A tile as its second, so each
+// lane's four results are four consecutive output columns of one row: one
+// A-scale per lane per 16-row group, and 8-byte packed writes in the epilogue.
+//
+// Operand tiles move global -> LDS with global_load_lds_dwordx4 (no register
+// staging), double buffered; the next K block streams in while the current
+// one is multiplied.  16-byte chunks are XOR-swizzled by row so the fragment
+// reads are bank-conflict free.  The epilogue stages each wave's tile through
+// LDS and writes full 128-byte row segments.
 #include <hip/hip_runtime.h>
 
 #include "ntlb_device.h"
@@ -43,16 +49,26 @@ struct GemmArgs {
   int64_t ldy;
   const int32_t* nan_a;
   const int32_t* nan_b;
+  int vec_out;  // y 16-byte aligned with 16-byte row pitch
 };
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int TILE_BYTES = BM * BK;  // 16 KiB per operand tile
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int NTHREADS = 512;
+constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // 32 KiB each
+constexpr int STAGE = TILE_A + TILE_B;
+constexpr int EPI_PITCH_F32 = 64 * 4 + 16;  // bytes per staged row (fp32)
+constexpr int EPI_WAVE = 64 * EPI_PITCH_F32;
+constexpr int SMEM_MAIN = 2 * STAGE + 2 * (BM + BN) * 4;
+constexpr int SMEM_EPI = 8 * EPI_WAVE;
+constexpr int SMEM_BYTES = SMEM_MAIN > SMEM_EPI ? SMEM_MAIN : SMEM_EPI;
 
-// byte offset of 16-byte chunk c of row r inside a swizzled 128x128 tile
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// byte offset of 16-byte chunk c of row r inside a swizzled [rows][128] tile
 __device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ (r & 7)) << 4); }
 
-// MFMA fragment for a 16-row group: row = lane%16, 32 K bytes from group lane/16.
-// A and B use the same (lane group, byte) -> K mapping, so the products pair up.
+// MFMA fragment of 16 rows: row = lane%16, 32 K bytes of group lane/16.
+// Both operands use the same (lane group, byte) -> K mapping, so the products pair up.
 __device__ __forceinline__ v8i load_frag(const uint8_t* tile, int row0, int lane) {
   const int r = row0 + (lane & 15);
   const int g = lane >> 4;
@@ -64,35 +80,59 @@ __device__ __forceinline__ v8i load_frag(const uint8_t* tile, int row0, int lane
   return f;
 }
 
+// D[i][j] = sum_k P[i][k] Q[j][k] for a 16x16 tile; lane l holds D[4*(l/16)+r][l%16]
 template <int GRID>
-__device__ __forceinline__ v4f mma_block(const v8i& a, const v8i& b) {
+__device__ __forceinline__ v4f mma_block(const v8i& p, const v8i& q) {
   if constexpr (GRID == GRID_E4M3) {
     v4f z = {0.f, 0.f, 0.f, 0.f};
     // fmt 0 = e4m3 for both operands; e8m0 scale 127 = 2^0
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 0, 0, 0, 127, 0, 127);
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(p, q, z, 0, 0, 0, 127, 0, 127);
   } else {
     v4i z = {0, 0, 0, 0};
-    v4i a0 = {a[0], a[1], a[2], a[3]}, a1 = {a[4], a[5], a[6], a[7]};
-    v4i b0 = {b[0], b[1], b[2], b[3]}, b1 = {b[4], b[5], b[6], b[7]};
-    v4i p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, z, 0, 0, 0);
-    p = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, p, 0, 0, 0);
-    v4f f = {(float)p[0], (float)p[1], (float)p[2], (float)p[3]};
+    v4i p0 = {p[0], p[1], p[2], p[3]}, p1 = {p[4], p[5], p[6], p[7]};
+    v4i q0 = {q[0], q[1], q[2], q[3]}, q1 = {q[4], q[5], q[6], q[7]};
+    v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(p0, q0, z, 0, 0, 0);
+    s = __builtin_amdgcn_mfma_i32_16x16x64_i8(p1, q1, s, 0, 0, 0);
+    v4f f = {(float)s[0], (float)s[1], (float)s[2], (float)s[3]};
     return f;
   }
 }
 
+// Direct-to-LDS copies of one K block through buffer resources: each wave
+// moves 4 groups of 8 rows (1 KiB) of A and of B.  Lane i lands at byte 16*i
+// of its group (row i/8, physical chunk i%8) and fetches logical chunk
+// (i%8) ^ (row & 7); its 32-bit row offset is fixed for the whole K loop and
+// the group / K offsets ride in the scalar offset.  Rows past M (or N) lie
+// beyond the resource's num_records and read as zero.
+struct StageSrc {
+  __amdgpu_buffer_rsrc_t ra, rb;
+  uint32_t a_off, b_off;   // per-lane byte offset of row (wave*32 + lane/8), chunk c
+  uint32_t a_grp, b_grp;   // 8 rows of A / B in bytes
+};
+
+__device__ __forceinline__ void issue_stage(const StageSrc& s, uint8_t* stage, int kt, int wave) {
+  const uint32_t koff = (uint32_t)kt * BK;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r0 = (wave * 4 + j) * 8;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.ra, (lds_ptr_t)(stage + r0 * BK), 16, s.a_off, koff + j * s.a_grp,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rb, (lds_ptr_t)(stage + TILE_A + r0 * BK), 16, s.b_off,
+                                             koff + j * s.b_grp, 0, 0);
+  }
+}
+
 template <int GRID, bool B_UNIFORM>
-__global__ void __launch_bounds__(256, 2) gemm_blockscaled_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][TILE_BYTES];
-  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][TILE_BYTES];
-  __shared__ __attribute__((aligned(16))) float lds_sa[2][BM];
-  __shared__ __attribute__((aligned(16))) float lds_sb[2][BN];
+__global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
+  float* lds_sa = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM]
+  float* lds_sb = lds_sa + 2 * BM;                              // [2][BN]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
 
-  // workgroup -> output tile: undo the round-robin XCD dispatch so that each
-  // XCD walks a contiguous range, then a grouped (8 row-tiles) raster order.
+  // workgroup -> output tile: undo the round-robin XCD dispatch so each XCD
+  // walks a contiguous range, then a grouped raster (GROUP_M row-tiles)
   const int num_m = (int)((g.M + BM - 1) / BM), num_n = (int)((g.N + BN - 1) / BN);
   const int nwg = num_m * num_n;
   int pid = blockIdx.x;
@@ -101,122 +141,175 @@ __global__ void __launch_bounds__(256, 2) gemm_blockscaled_kernel(GemmArgs g) {
     const int per = nwg >> 3, extra = nwg & 7;
     pid = xcd * per + min(xcd, extra) + local;
   }
-  constexpr int GROUP_M = 8;
+  constexpr int GROUP_M = 4;
   const int group = pid / (GROUP_M * num_n);
   const int first_m = group * GROUP_M;
   const int gsize = min(num_m - first_m, GROUP_M);
   const int in_group = pid - group * GROUP_M * num_n;
-  const int tile_m = first_m + in_group % gsize;
-  const int tile_n = in_group / gsize;
-  const int64_t m0 = (int64_t)tile_m * BM, n0 = (int64_t)tile_n * BN;
+  const int64_t m0 = (int64_t)(first_m + in_group % gsize) * BM;
+  const int64_t n0 = (int64_t)(in_group / gsize) * BN;
 
-  // global -> LDS copy assignment: chunk c of rows (tid>>3) + 32*i
-  const int cc = tid & 7, cr = tid >> 3;
-  const uint8_t* a_src[4];
-  const uint8_t* b_src[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    int64_t ra = min<int64_t>(m0 + cr + 32 * i, g.M - 1);
-    int64_t rb = min<int64_t>(n0 + cr + 32 * i, g.N - 1);
-    a_src[i] = g.a + ra * g.lda + cc * 16;
-    b_src[i] = g.b + rb * g.ldb + cc * 16;
-  }
-  // scale copy: threads 0..127 fetch sa for rows m0+tid, 128..255 fetch sb
-  const int64_t srow = (tid < BM) ? min<int64_t>(m0 + tid, g.M - 1) : min<int64_t>(n0 + tid - BM, g.N - 1);
-  const float* s_src = (tid < BM) ? g.sa + (srow >> g.a_shift) * g.sa_row : g.sb + (srow >> g.b_shift) * g.sb_row;
-  const int64_t s_step = (tid < BM) ? g.sa_col : g.sb_col;
-  const float* sb_uniform = g.sb + (n0 >> g.b_shift) * g.sb_row;
+  // scale fetch: threads 0..255 own sa of row m0+tid, 256..511 sb of row n0+tid-256
+  const bool own_a = tid < BM;
+  const int64_t srow = own_a ? min<int64_t>(m0 + tid, g.M - 1) : min<int64_t>(n0 + tid - BM, g.N - 1);
+  const float* s_src = own_a ? g.sa + (srow >> g.a_shift) * g.sa_row : g.sb + (srow >> g.b_shift) * g.sb_row;
+  const int64_t s_step = own_a ? g.sa_col : g.sb_col;
+  float* s_dst = own_a ? lds_sa + tid : lds_sb + (tid - BM);
+  const float* sb_wave = g.sb + ((n0 + wn * 64) >> g.b_shift) * g.sb_row;
 
   const int nk = (int)(g.Kp / BK);
-  uint4 ra[4], rb[4];
-  float rs;
 
-  auto gload = [&](int kt) {
-    const int64_t koff = (int64_t)kt * BK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ra[i] = *reinterpret_cast<const uint4*>(a_src[i] + koff);
-      rb[i] = *reinterpret_cast<const uint4*>(b_src[i] + koff);
-    }
-    rs = s_src[kt * s_step];
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = cr + 32 * i;
-      *reinterpret_cast<uint4*>(&lds_a[buf][swz(r, cc)]) = ra[i];
-      *reinterpret_cast<uint4*>(&lds_b[buf][swz(r, cc)]) = rb[i];
-    }
-    if (tid < BM)
-      lds_sa[buf][tid] = rs;
-    else
-      lds_sb[buf][tid - BM] = rs;
-  };
+  StageSrc src;
+  {
+    const int r = wave * 32 + (lane >> 3);
+    const int c = (lane & 7) ^ (r & 7);
+    src.ra = __builtin_amdgcn_make_buffer_rsrc((void*)g.a, (short)0, (int)(g.M * g.lda), 0x00020000);
+    src.rb = __builtin_amdgcn_make_buffer_rsrc((void*)g.b, (short)0, (int)(g.N * g.ldb), 0x00020000);
+    src.a_off = (uint32_t)((m0 + r) * g.lda + c * 16);
+    src.b_off = (uint32_t)((n0 + r) * g.ldb + c * 16);
+    src.a_grp = (uint32_t)(8 * g.lda);
+    src.b_grp = (uint32_t)(8 * g.ldb);
+  }
 
-  v4f acc[4][4];
+  v4f acc[8][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
-  lstore(0);
+  issue_stage(src, smem, 0, wave);
+  float s_next = s_src[0];
+  s_dst[0] = s_next;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);
+    if (kt + 1 < nk) {
+      issue_stage(src, smem + (buf ^ 1) * STAGE, kt + 1, wave);
+      s_next = s_src[(int64_t)(kt + 1) * s_step];
+    }
+    const uint8_t* ta = smem + buf * STAGE;
+    const uint8_t* tb = ta + TILE_A;
+    const float* sa_buf = lds_sa + buf * BM;
 
-    const uint8_t* ta = lds_a[buf];
-    const uint8_t* tb = lds_b[buf];
     v8i bf[4];
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) bf[tn] = load_frag(tb, wn * 64 + tn * 16, lane);
-    float sbv[4];
+
+    float sbu = 0.f;
+    v4f sbv[4];
     if constexpr (B_UNIFORM) {
-      const float s = sb_uniform[(int64_t)kt * g.sb_col];
-#pragma unroll
-      for (int tn = 0; tn < 4; ++tn) sbv[tn] = s;
+      sbu = sb_wave[(int64_t)kt * g.sb_col];
     } else {
+      const float* sb_buf = lds_sb + buf * BN;
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) sbv[tn] = lds_sb[buf][wn * 64 + tn * 16 + (lane & 15)];
+      for (int tn = 0; tn < 4; ++tn)
+        sbv[tn] = *reinterpret_cast<const v4f*>(sb_buf + wn * 64 + tn * 16 + (lane >> 4) * 4);
     }
+    // A fragments are double buffered by hand: the next 16-row group is read
+    // from LDS while the current one is on the matrix cores.  The scheduling
+    // fence keeps the compiler from hoisting all eight groups (64 VGPRs) at once.
+    float sam_all[8];
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
-      const v8i af = load_frag(ta, wm * 64 + tm * 16, lane);
-      const float4 sa4 = *reinterpret_cast<const float4*>(&lds_sa[buf][wm * 64 + tm * 16 + (lane >> 4) * 4]);
+    for (int tm = 0; tm < 8; ++tm) sam_all[tm] = sa_buf[wm * 128 + tm * 16 + (lane & 15)];
+    v8i af = load_frag(ta, wm * 128, lane);
+#pragma unroll
+    for (int tm = 0; tm < 8; ++tm) {
+      v8i af_next;
+      if (tm + 1 < 8) af_next = load_frag(ta, wm * 128 + (tm + 1) * 16, lane);
+      const float sam = sam_all[tm];
+      v4f d[4];
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
-        const v4f d = mma_block<GRID>(af, bf[tn]);
-        acc[tm][tn][0] += d[0] * (sa4.x * sbv[tn]);
-        acc[tm][tn][1] += d[1] * (sa4.y * sbv[tn]);
-        acc[tm][tn][2] += d[2] * (sa4.z * sbv[tn]);
-        acc[tm][tn][3] += d[3] * (sa4.w * sbv[tn]);
+        if constexpr (B_UNIFORM) {
+          const float s = sam * sbu;
+          acc[tm][tn] += d[tn] * s;
+        } else {
+          acc[tm][tn] += (d[tn] * sbv[tn]) * sam;
+        }
       }
+      // this group's accumulators are final here, and no later LDS read
+      // moves above this point
+      asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
+      if (tm + 1 < 8) af = af_next;
     }
-    if (kt + 1 < nk) lstore(buf ^ 1);
+    if (kt + 1 < nk) s_dst[(buf ^ 1) * (own_a ? BM : BN)] = s_next;
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 
-  // epilogue: NaN flags, bias, cast, store (16 lanes cover 16 consecutive columns)
+  // ---------------------------------------------------------------- epilogue
+  // lane holds rows m = m0 + wm*128 + tm*16 + lane%16 and columns
+  // n = n0 + wn*64 + tn*16 + 4*(lane/16) + r
+  uint8_t* stage_w = smem + wave * EPI_WAVE;
+  const bool out_f32 = g.y_dtype == DT_F32;
+  const int pitch = out_f32 ? EPI_PITCH_F32 : (64 * 2 + 16);
+  float bias[4][4];
+  bool nan_col[4][4];
 #pragma unroll
-  for (int tn = 0; tn < 4; ++tn) {
-    const int64_t col = n0 + wn * 64 + tn * 16 + (lane & 15);
-    if (col >= g.N) continue;
-    float bias = 0.f;
-    if (g.bias) bias = load_elem(g.bias, g.bias_dtype, col);
-    const bool nan_col = g.nan_b && g.nan_b[col];
+  for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
-    for (int tm = 0; tm < 4; ++tm) {
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + wn * 64 + tn * 16 + (lane >> 4) * 4 + r;
+      const bool in = n < g.N;
+      bias[tn][r] = (g.bias && in) ? load_elem(g.bias, g.bias_dtype, n) : 0.f;
+      nan_col[tn][r] = g.nan_b && in && g.nan_b[n];
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t row = m0 + wm * 64 + tm * 16 + (lane >> 4) * 4 + i;
-        if (row >= g.M) continue;
-        float v = acc[tm][tn][i] + bias;
-        if (nan_col || (g.nan_a && g.nan_a[row])) v = __uint_as_float(0x7FC00000u);
-        store_elem(g.y, g.y_dtype, row * g.ldy + col, v);
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int tm = half * 4 + t;
+      const int rloc = t * 16 + (lane & 15);
+      const int64_t m = m0 + wm * 128 + tm * 16 + (lane & 15);
+      const bool nan_row = g.nan_a && m < g.M && g.nan_a[m];
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          v[r] = acc[tm][tn][r] + bias[tn][r];
+          if (nan_row || nan_col[tn][r]) v[r] = __uint_as_float(0x7FC00000u);
+        }
+        const int cbyte = (tn * 16 + (lane >> 4) * 4) * (out_f32 ? 4 : 2);
+        uint8_t* dst = stage_w + rloc * pitch + cbyte;
+        if (out_f32) {
+          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else if (g.y_dtype == DT_BF16) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(
+              (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
+              (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
+        } else {
+          __half h[4] = {__float2half(v[0]), __float2half(v[1]), __float2half(v[2]), __float2half(v[3])};
+          *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(h);
+        }
       }
     }
+    __syncthreads();
+    // 64 rows x (128 or 256) bytes; 16-byte chunks, row-contiguous across lanes
+    const int chunks_per_row = out_f32 ? 16 : 8;
+    const int esz = out_f32 ? 4 : 2;
+    const int epc = 16 / esz;  // elements per chunk
+#pragma unroll
+    for (int j = 0; j < (out_f32 ? 16 : 8); ++j) {
+      const int q = lane + 64 * j;
+      const int row = q / chunks_per_row, c = q % chunks_per_row;
+      const int64_t m = m0 + wm * 128 + half * 64 + row;
+      const int64_t n = n0 + wn * 64 + c * epc;
+      if (m >= g.M || n >= g.N) continue;
+      const uint8_t* src = stage_w + row * pitch + c * 16;
+      uint8_t* ydst = reinterpret_cast<uint8_t*>(g.y) + (m * g.ldy + n) * esz;
+      if (g.vec_out && n + epc <= g.N) {
+        *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+      } else {
+        for (int e = 0; e < epc && n + e < g.N; ++e)
+          for (int bidx = 0; bidx < esz; ++bidx) ydst[e * esz + bidx] = src[e * esz + bidx];
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -244,6 +337,9 @@ extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, co
   if (Kp == 0) return fail(NTLB_EUNSUPPORTED, "%s: K == 0", fn);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  // buffer resources address each operand with 32-bit byte offsets
+  if ((M + BM) * lda >= (int64_t)0x7FFFFFFF || (N + BN) * ldb >= (int64_t)0x7FFFFFFF)
+    return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
   GemmArgs g;
   g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
   g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = b_shift;
@@ -251,10 +347,11 @@ extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, co
   g.bias = bias; g.bias_dtype = bias_dtype;
   g.y = y; g.y_dtype = y_dtype; g.ldy = ldy;
   g.nan_a = nan_a; g.nan_b = nan_b;
-  // B's scale is uniform over a 128-column tile for 128x128 blocks and tensor scales
+  g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
+  // B's scale is uniform over each wave's 64 columns for 128x128 blocks and tensor scales
   const bool b_uniform = (b_shift == 7) || (sb_row == 0);
   hipStream_t st = as_stream(stream);
-  dim3 grd((unsigned)tiles), blk(256);
+  dim3 grd((unsigned)tiles), blk(NTHREADS);
   if (grid == NTLB_GRID_E4M3) {
     if (b_uniform)
       gemm_blockscaled_kernel<GRID_E4M3, true><<<grd, blk, 0, st>>>(g);

@@ -16,6 +16,9 @@
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 
+// every fp32 operation rounds on its own, as the reference's torch ops do
+#pragma clang fp contract(off)
+
 namespace ntlb {
 
 struct QuantArgs {
