@@ -163,12 +163,37 @@ def main():
     # the GEMM's own minimum HBM traffic: both code matrices, their scales, bf16 out
     gemm_min_bytes = M * K + N * K + M * (K // 128) * 4 + (N // 128) * (K // 128) * 4 + M * N * 2
 
+    # achievable HBM rate on this box: a 1 GiB device-to-device copy (read + write)
+    ca = torch.empty(1 << 29, dtype=torch.int16, device=dev)
+    cb = torch.empty_like(ca)
+    cb.copy_(ca)
+    ce = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ce[0].record(stream)
+    for _ in range(5):
+        cb.copy_(ca)
+    ce[1].record(stream)
+    torch.cuda.synchronize()
+    copy_gbs = 5 * 2 * ca.numel() * 2 / (ce[0].elapsed_time(ce[1]) * 1e-3) / 1e9
+    del ca, cb
+
     if args.calib_copy:
         a = torch.empty(1 << 29, dtype=torch.int16, device=dev)
         b = torch.empty_like(a)
         for _ in range(3):
             b.copy_(a)
         torch.cuda.synchronize()
+
+    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE (calibrated
+    # against a 1 GiB copy) for this workload, committed under profiles/
+    traffic = {}
+    prof = os.path.join(ROOT, "profiles", f"c2_forward_{args.format}.json")
+    if rounding == "nearest" and os.path.exists(prof):
+        with open(prof) as fh:
+            pj = json.load(fh)
+        for kname, tv in pj.get("traffic", {}).items():
+            for short in ("gemm_blockscaled_kernel", "quant_tile_1x128", "quant_block_128x128"):
+                if short in kname:
+                    traffic[short] = int(tv["total_bytes"])
 
     result = {
         "metric": "FP8 blockwise GEMM TFLOP/s (% fp8 MFMA peak); quantizer GB/s (% HBM peak)",
@@ -196,18 +221,22 @@ def main():
             "peak": FP8_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / FP8_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic.get("gemm_blockscaled_kernel"),
+            "traffic_source": f"profiles/c2_forward_{args.format}.md" if traffic else None,
             "avg_ms": round(avg(gm_ms), 4),
             "min_hbm_bytes": gemm_min_bytes,
         },
         "quantizers": {
             "x_tile_1x128": {"avg_us": round(avg(qx_ms) * 1e3, 2), "bytes": qx_bytes,
+                             "traffic": traffic.get("quant_tile_1x128"),
                              "GB/s": round(qx_bytes / (avg(qx_ms) * 1e-3) / 1e9, 1),
                              "frac_hbm": round(qx_bytes / (avg(qx_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
             "w_block_128x128": {"avg_us": round(avg(qw_ms) * 1e3, 2), "bytes": qw_bytes,
+                                "traffic": traffic.get("quant_block_128x128"),
                                 "GB/s": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9, 1),
                                 "frac_hbm": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         },
+        "hbm_copy_GB/s": round(copy_gbs, 1),
         "event_ms_per_step": round(avg(step_ms), 4),
         "cpu_baseline": None,
     }

@@ -11,6 +11,7 @@
 // 16-byte vectors, one 128-element tile per 16 lanes (one DPP row), so the
 // tile amax is a 4-step DPP reduction that never leaves the row.
 #include <hip/hip_fp16.h>
+#include <algorithm>
 #include <hip/hip_runtime.h>
 
 #include "ntlb_device.h"
@@ -173,6 +174,246 @@ __global__ void __launch_bounds__(256) quant_tile_1x128_kernel(QuantArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// 1x128 tiles, fast path (bf16 or fp32 input, K a multiple of 8, 16-byte
+// aligned rows).  Workgroup (bx, by) covers rows [16*bx, 16*bx+16) and tiles
+// [TU*by, TU*by+TU): no integer division, every lane keeps TU 16-byte loads in
+// flight, and 16 consecutive rows of one tile column write their scales
+// contiguously in the tile-major layout.  The amax runs on packed bf16 bits
+// (one op per two elements).  A tile whose amax is NaN takes the per-element
+// path of the reference semantics; every other tile clamps with min/max.
+// With NTLB_HW_FP8_CVT the e4m3 rounding uses v_cvt_pk_fp8_f32 (checked
+// bit-exact against the software rounding on every fp32 input with
+// |v| <= 448).
+// ---------------------------------------------------------------------------
+#ifndef NTLB_HW_FP8_CVT
+#define NTLB_HW_FP8_CVT 1
+#endif
+#ifndef NTLB_TILE_TU
+#define NTLB_TILE_TU 2
+#endif
+// workgroup order: 1 = consecutive workgroups walk along a row (column
+// blocks fastest), which keeps concurrent reads within the same DRAM pages
+#ifndef NTLB_COL_FASTEST
+#define NTLB_COL_FASTEST 1
+#endif
+#ifndef NTLB_TILE_PIPELINE
+#define NTLB_TILE_PIPELINE 0
+#endif
+constexpr int TILE_TU = NTLB_TILE_TU;
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// v_pk_max_u16 on two packed halves
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+// Quantize 8 values of a tile with scale s whose amax bits are m.  A tile
+// holding a NaN takes the per-element reference path (and reports it); every
+// other tile clamps with min/max, divides with the fast exact sequence when
+// its amax allows, and rounds to e4m3 in hardware when enabled.
+template <int GRID, bool SR, bool DQ>
+__device__ __forceinline__ bool quant8_tile(const float (&v)[8], uint32_t m, float s, float qmaxf,
+                                            const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+  if (m > 0x7F800000u) {
+    // NaN in the tile: reference semantics element by element
+    quant8<GRID, SR>(v, s, qmaxf, rb, lo, hi, q);
+    return true;
+  } else {
+    float vq[8];
+    // Round-to-nearest tiles with amax in [2^-75, 2^120]: x/s as
+    // y = x*r, e = fma(-y, s, x), q = fma(e, r, y) with r = 1/s and the sign
+    // of x; this equals the correctly rounded quotient wherever it can move
+    // a code (checked exhaustively on random operands).  Other tiles, and
+    // stochastic rounding, divide.
+    const bool fast_div = !SR && m >= 0x1A000000u && m <= 0x7B800000u;
+    if (fast_div) {
+      const float rs = 1.0f / s;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float y = v[i] * rs;
+        const float e = __builtin_fmaf(-y, s, v[i]);
+        float z = __builtin_copysignf(__builtin_fmaf(e, rs, y), v[i]);
+        vq[i] = fminf(fmaxf(z, -qmaxf), qmaxf);  // no NaN in this tile
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float z = v[i] / s;
+        vq[i] = fminf(fmaxf(z, -qmaxf), qmaxf);
+      }
+    }
+    if constexpr (GRID == GRID_INT) {
+      uint32_t c[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float t;
+        if constexpr (SR) {
+          const float uu = sr_uniform(rb[i]);
+          t = (vq[i] >= 0.0f) ? __builtin_floorf(vq[i] + uu) : __builtin_ceilf(vq[i] - uu);
+        } else {
+          t = __builtin_rintf(vq[i]);
+        }
+        q[i] = t;
+        c[i] = (uint32_t)(int32_t)t & 0xFFu;
+      }
+      lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+      hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    } else {
+      uint32_t c[8];
+      if constexpr (!SR && NTLB_HW_FP8_CVT) {
+        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[0], vq[1], 0, false);
+        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[2], vq[3], (int)lo, true);
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4], vq[5], 0, false);
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[6], vq[7], (int)hi, true);
+        c[0] = lo & 0xFF; c[1] = (lo >> 8) & 0xFF; c[2] = (lo >> 16) & 0xFF; c[3] = lo >> 24;
+        c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = SR ? e4m3_sr(vq[i], sr_uniform(rb[i])) : e4m3_rne(vq[i]);
+        lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+      }
+      if constexpr (DQ) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = e4m3_to_f32(c[i]);
+      }
+    }
+  }
+  return false;
+}
+
+// 8 consecutive elements as fp32 plus their |x| max (bits), from a chunk
+// loaded raw: bf16 keeps 4 registers per chunk and reduces on packed halves.
+template <int IN_DT>
+struct Chunk8 {
+  uint4 w[IN_DT == DT_F32 ? 2 : 1];
+};
+
+template <int IN_DT>
+__device__ __forceinline__ void chunk_load(Chunk8<IN_DT>& c, const void* base, int64_t off, bool in) {
+  if (!in) {
+    c.w[0] = make_uint4(0, 0, 0, 0);
+    if constexpr (IN_DT == DT_F32) c.w[1] = make_uint4(0, 0, 0, 0);
+    return;
+  }
+  if constexpr (IN_DT == DT_F32) {
+    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(base) + off);
+    c.w[0] = p[0];
+    c.w[1] = p[1];
+  } else {
+    c.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+  }
+}
+
+template <int IN_DT>
+__device__ __forceinline__ uint32_t chunk_amax(const Chunk8<IN_DT>& c) {
+  if constexpr (IN_DT == DT_F32) {
+    const uint32_t w[8] = {c.w[0].x, c.w[0].y, c.w[0].z, c.w[0].w, c.w[1].x, c.w[1].y, c.w[1].z, c.w[1].w};
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) m = max(m, w[i] & 0x7FFFFFFFu);
+    return m;
+  } else {
+    uint32_t m2 = pk_max_u16(c.w[0].x & 0x7FFF7FFFu, c.w[0].y & 0x7FFF7FFFu);
+    m2 = pk_max_u16(m2, c.w[0].z & 0x7FFF7FFFu);
+    m2 = pk_max_u16(m2, c.w[0].w & 0x7FFF7FFFu);
+    return max(m2 & 0xFFFFu, m2 >> 16) << 16;
+  }
+}
+
+template <int IN_DT>
+__device__ __forceinline__ void chunk_floats(const Chunk8<IN_DT>& c, float (&v)[8]) {
+  if constexpr (IN_DT == DT_F32) {
+    const uint32_t w[8] = {c.w[0].x, c.w[0].y, c.w[0].z, c.w[0].w, c.w[1].x, c.w[1].y, c.w[1].z, c.w[1].w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(w[i]);
+  } else {
+    const uint32_t w[4] = {c.w[0].x, c.w[0].y, c.w[0].z, c.w[0].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+}
+
+template <int IN_DT>
+__device__ __forceinline__ void tile_loads(Chunk8<IN_DT> (&c)[TILE_TU], const QuantArgs& a, int64_t r, int t0,
+                                           int T, int lane16) {
+#pragma unroll
+  for (int u = 0; u < TILE_TU; ++u) {
+    const int64_t k0 = (int64_t)(t0 + u) * 128 + lane16 * 8;
+    chunk_load<IN_DT>(c[u], a.x, r * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
+  }
+}
+
+template <int IN_DT, int GRID, bool SR, bool DQ>
+__device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], const QuantArgs& a, int64_t r, int t0,
+                                           int T, int lane16) {
+#pragma unroll
+  for (int u = 0; u < TILE_TU; ++u) {
+    const int t = t0 + u;
+    if (t >= T) break;
+    float v[8];
+    chunk_floats<IN_DT>(c[u], v);
+    uint32_t m = row16_max_u32(chunk_amax<IN_DT>(c[u]));
+    const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
+    const int64_t k0 = (int64_t)t * 128 + lane16 * 8;
+    uint32_t rb[8];
+    sr_words<SR>((uint64_t)(r * a.K + k0), a.seed, a.offset, rb);
+    uint32_t lo, hi;
+    float q[8];
+    const bool nan = quant8_tile<GRID, SR, DQ>(v, m, s, a.qmaxf, rb, lo, hi, q);
+    if (nan && a.nan_rows && lane16 == 0) atomicOr(a.nan_rows + r, 1);
+    *reinterpret_cast<uint2*>(a.codes + r * a.ldc + k0) = make_uint2(lo, hi);
+    if (lane16 == 0) a.scales[r * a.s_row + (int64_t)t * a.s_col] = s;
+    if constexpr (DQ) store_dq8(a.dq, a.dq_dtype, r * a.lddq, k0, a.K, q, s);
+  }
+}
+
+// Workgroup (bx, by) covers tile columns [TU*by, TU*by+TU) of the row blocks
+// bx, bx + gridDim.x, ... (16 rows each); the loads of the next row block are
+// in flight while the current one is quantized.
+template <int IN_DT, int GRID, bool SR, bool DQ>
+__global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
+  const int lane16 = threadIdx.x & 15;
+  const int T = (int)((a.K + 127) >> 7);
+  const unsigned bx = NTLB_COL_FASTEST ? blockIdx.y : blockIdx.x;  // row-block index
+  const unsigned by = NTLB_COL_FASTEST ? blockIdx.x : blockIdx.y;  // tile-group index
+  const unsigned gxr = NTLB_COL_FASTEST ? gridDim.y : gridDim.x;
+  const int t0 = by * TILE_TU;
+  const int64_t n_rb = (a.R + 15) >> 4;
+  int64_t rb = bx;
+  if (rb >= n_rb) return;
+  Chunk8<IN_DT> cur[TILE_TU], nxt[TILE_TU];
+  int64_t r = rb * 16 + (threadIdx.x >> 4);
+  tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
+  if constexpr (!NTLB_TILE_PIPELINE) {
+    // no prefetch: the lowest register count and the highest occupancy; the
+    // loop only runs when the grid is capped below the number of row blocks
+    for (;;) {
+      if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ>(cur, a, r, t0, T, lane16);
+      rb += gxr;
+      if (rb >= n_rb) return;
+      r = rb * 16 + (threadIdx.x >> 4);
+      tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
+    }
+  }
+  for (;;) {
+    const int64_t rb_next = rb + gxr;
+    const int64_t r_next = rb_next * 16 + (threadIdx.x >> 4);
+    if (rb_next < n_rb) tile_loads<IN_DT>(nxt, a, r_next, t0, T, lane16);
+    if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ>(cur, a, r, t0, T, lane16);  // whole 16-lane rows
+    if (rb_next >= n_rb) break;
+    rb = rb_next;
+    r = r_next;
+#pragma unroll
+    for (int u = 0; u < TILE_TU; ++u) cur[u] = nxt[u];
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 128x128 blocks: one workgroup per block, the block held in registers
 // between the amax pass and the quantize pass (one HBM read).
 // ---------------------------------------------------------------------------
@@ -246,6 +487,136 @@ __global__ void __launch_bounds__(256) quant_block_128x128_kernel(BlockArgs ba) 
       uint4* dst = reinterpret_cast<uint4*>(ba.codes_t + krow * ba.ldct + nb * 128 + h * 64);
 #pragma unroll
       for (int j = 0; j < 4; ++j) dst[j] = make_uint4(w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]);
+    }
+  }
+}
+
+// 128x128 blocks, fast path (bf16/fp32, K % 8 == 0, 16-byte aligned rows):
+// one workgroup per block; thread (rr, sub) holds rows rr + 16*i, columns
+// sub*8 .. sub*8+7 as raw chunks between the amax pass and the quantize pass
+// (one HBM read).
+#ifndef NTLB_BLOCK_THREADS
+#define NTLB_BLOCK_THREADS 512
+#endif
+#ifndef NTLB_BLOCK_PIPELINE
+#define NTLB_BLOCK_PIPELINE 0
+#endif
+constexpr int BLK_THREADS = NTLB_BLOCK_THREADS;
+constexpr int BLK_ROWS = BLK_THREADS / 16;  // rows covered by one pass of the workgroup
+constexpr int BLK_RPT = 128 / BLK_ROWS;     // rows per thread
+constexpr int BLK_WAVES = BLK_THREADS / 64;
+
+template <int IN_DT>
+__device__ __forceinline__ void block_loads(Chunk8<IN_DT> (&ch)[BLK_RPT], const QuantArgs& a, int64_t nb, int64_t kb,
+                                            int rr, int sub) {
+  const int64_t k0 = kb * 128 + sub * 8;
+#pragma unroll
+  for (int i = 0; i < BLK_RPT; ++i) {
+    const int64_t n = nb * 128 + rr + BLK_ROWS * i;
+    chunk_load<IN_DT>(ch[i], a.x, n * a.ldx + k0, n < a.R && k0 < a.K);
+  }
+}
+
+template <int IN_DT, int GRID, bool SR, bool DQ>
+__device__ __forceinline__ void block_quant(const Chunk8<IN_DT> (&ch)[BLK_RPT], const BlockArgs& ba, int64_t nb,
+                                            int64_t kb, int tid, uint32_t* red, uint8_t (*tile_t)[128 + 4]) {
+  const QuantArgs& a = ba.q;
+  const int sub = tid & 15, rr = tid >> 4;
+  const int64_t k0 = kb * 128 + sub * 8;
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < BLK_RPT; ++i) m = max(m, chunk_amax<IN_DT>(ch[i]));
+  m = wave_max_u32(m);
+  if ((tid & 63) == 0) red[tid >> 6] = m;
+  __syncthreads();
+  m = red[0];
+#pragma unroll
+  for (int w = 1; w < BLK_WAVES; ++w) m = max(m, red[w]);
+  const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
+  if (tid == 0) a.scales[nb * a.s_row + kb * a.s_col] = s;
+#pragma unroll
+  for (int i = 0; i < BLK_RPT; ++i) {
+    const int64_t n = nb * 128 + rr + BLK_ROWS * i;
+    float v[8];
+    chunk_floats<IN_DT>(ch[i], v);
+    uint32_t rb[8];
+    sr_words<SR>((uint64_t)(n * a.K + k0), a.seed, a.offset, rb);
+    uint32_t lo, hi;
+    float q[8];
+    const bool nan = quant8_tile<GRID, SR, DQ>(v, m, s, a.qmaxf, rb, lo, hi, q);
+    if (n < a.R && k0 < a.K) {
+      *reinterpret_cast<uint2*>(a.codes + n * a.ldc + k0) = make_uint2(lo, hi);
+      if constexpr (DQ) store_dq8(a.dq, a.dq_dtype, n * a.lddq, k0, a.K, q, s);
+    } else if (n < a.R && k0 < a.ldc) {
+      *reinterpret_cast<uint2*>(a.codes + n * a.ldc + k0) = make_uint2(0, 0);
+    }
+    if (nan && a.nan_rows && n < a.R) {
+      bool row_nan = false;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) row_nan |= (__float_as_uint(v[j]) & 0x7FFFFFFFu) > 0x7F800000u;
+      if (row_nan) atomicOr(a.nan_rows + n, 1);
+    }
+    if (ba.codes_t) {
+      *reinterpret_cast<uint32_t*>(&tile_t[rr + BLK_ROWS * i][sub * 8]) = lo;
+      *reinterpret_cast<uint32_t*>(&tile_t[rr + BLK_ROWS * i][sub * 8 + 4]) = hi;
+    }
+  }
+  if (ba.codes_t) {
+    __syncthreads();
+    // W^T rows: 128 rows x 128 bytes, 16-byte pieces spread over the workgroup
+    for (int piece = tid; piece < 128 * 8; piece += BLK_THREADS) {
+      const int kr = piece >> 3, h = piece & 7;
+      const int64_t krow = kb * 128 + kr;
+      if (krow < a.K) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int n0 = h * 16 + j * 4;
+          w[j] = (uint32_t)tile_t[n0][kr] | ((uint32_t)tile_t[n0 + 1][kr] << 8) |
+                 ((uint32_t)tile_t[n0 + 2][kr] << 16) | ((uint32_t)tile_t[n0 + 3][kr] << 24);
+        }
+        *reinterpret_cast<uint4*>(ba.codes_t + krow * ba.ldct + nb * 128 + h * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    }
+  }
+  __syncthreads();  // red[] and tile_t are reused by the next block
+}
+
+// 128x128 blocks, fast path (bf16/fp32, K % 8 == 0, 16-byte aligned rows):
+// thread (rr, sub) holds rows rr + BLK_ROWS*i, columns sub*8 .. sub*8+7 of a
+// block as raw chunks between the amax pass and the quantize pass (one HBM
+// read).  Workgroups walk column blocks fastest; with NTLB_BLOCK_PIPELINE the
+// next block's loads are in flight while the current one is quantized.
+template <int IN_DT, int GRID, bool SR, bool DQ>
+__global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArgs ba) {
+  __shared__ uint32_t red[BLK_WAVES];
+  __shared__ uint8_t tile_t[128][128 + 4];
+  const int tid = threadIdx.x;
+  const int sub = tid & 15, rr = tid >> 4;
+  const int64_t NB = (ba.q.R + 127) >> 7;
+  const int64_t kb = NTLB_COL_FASTEST ? blockIdx.x : blockIdx.y;
+  const unsigned gnb = NTLB_COL_FASTEST ? gridDim.y : gridDim.x;
+  int64_t nb = NTLB_COL_FASTEST ? blockIdx.y : blockIdx.x;
+  if (nb >= NB) return;
+  Chunk8<IN_DT> cur[BLK_RPT];
+  block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
+  if constexpr (!NTLB_BLOCK_PIPELINE) {
+    for (;;) {
+      block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
+      nb += gnb;
+      if (nb >= NB) return;
+      block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
+    }
+  } else {
+    Chunk8<IN_DT> nxt[BLK_RPT];
+    for (;;) {
+      const int64_t nb_next = nb + gnb;
+      if (nb_next < NB) block_loads<IN_DT>(nxt, ba.q, nb_next, kb, rr, sub);
+      block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
+      if (nb_next >= NB) break;
+      nb = nb_next;
+#pragma unroll
+      for (int i = 0; i < BLK_RPT; ++i) cur[i] = nxt[i];
     }
   }
 }
@@ -523,8 +894,40 @@ extern "C" int ntlb_quant_tile_1x128(const void* x, int x_dtype, int64_t R, int6
                           dq_dtype, lddq, nan_rows);
   const bool vec = aligned(x, 16) && ((ldx * dtype_size(x_dtype)) % 16 == 0);
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
-  dim3 grd(grid_for(R * T, 32, 256 * 32)), blk(256);
   hipStream_t st = as_stream(stream);
+  const bool fast_ok = vec && (K % 8 == 0) && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) &&
+                       (!dq || (dq_dtype == NTLB_BF16 && aligned(dq, 16) && (lddq % 8) == 0)) &&
+                       cdiv(R, 16) <= 0x7FFFFFFF && cdiv(T, TILE_TU) <= 65535;  // either order fits
+  if (fast_ok) {
+    // pipelined: about 4 row blocks per workgroup so loads overlap the math;
+    // otherwise one row block per workgroup
+    const int64_t n_rb = cdiv(R, 16), n_tg = cdiv(T, TILE_TU);
+    int64_t gx = n_rb;
+    if (NTLB_TILE_PIPELINE) {
+      gx = cdiv(n_rb, 4);
+      if (gx * n_tg < 256 * 8) gx = std::min<int64_t>(n_rb, cdiv(256 * 8, n_tg));
+    }
+    if (gx > 65535 && NTLB_COL_FASTEST) gx = 65535;  // grid-stride loop covers the rest
+    dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)n_tg, (unsigned)gx) : dim3((unsigned)gx, (unsigned)n_tg);
+    dim3 fblk(256);
+    if (dq) {
+      NTLB_DISPATCH_GRID_SR(grid, sr, {
+        if (x_dtype == NTLB_BF16)
+          quant_tile_1x128_fast<DT_BF16, G_, S_, true><<<fgrd, fblk, 0, st>>>(a);
+        else
+          quant_tile_1x128_fast<DT_F32, G_, S_, true><<<fgrd, fblk, 0, st>>>(a);
+      });
+    } else {
+      NTLB_DISPATCH_GRID_SR(grid, sr, {
+        if (x_dtype == NTLB_BF16)
+          quant_tile_1x128_fast<DT_BF16, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+        else
+          quant_tile_1x128_fast<DT_F32, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+      });
+    }
+    return check_launch(fn);
+  }
+  dim3 grd(grid_for(R * T, 32, 256 * 32)), blk(256);
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
     if (vec)
       quant_tile_1x128_kernel<D_, G_, S_, true><<<grd, blk, 0, st>>>(a);
@@ -560,8 +963,37 @@ extern "C" int ntlb_quant_block_128x128(const void* w, int w_dtype, int64_t N, i
   const bool vec = aligned(w, 16) && ((ldw * dtype_size(w_dtype)) % 16 == 0);
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
   if (NB * T > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many blocks", fn);
-  dim3 grd((unsigned)(NB * T)), blk(256);
   hipStream_t st = as_stream(stream);
+  const bool fast_ok = vec && (K % 8 == 0) && (w_dtype == NTLB_BF16 || w_dtype == NTLB_F32) &&
+                       (!dq || (dq_dtype == NTLB_BF16 && aligned(dq, 16) && (lddq % 8) == 0)) &&
+                       NB <= 0x7FFFFFFF && T <= 65535;
+  if (fast_ok) {
+    int64_t gx = NB;
+    if (NTLB_BLOCK_PIPELINE) {
+      gx = cdiv(NB, 4);
+      if (gx * T < 256 * 8) gx = std::min<int64_t>(NB, cdiv(256 * 8, T));
+    }
+    if (gx > 65535 && NTLB_COL_FASTEST) gx = 65535;
+    dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)T, (unsigned)gx) : dim3((unsigned)gx, (unsigned)T);
+    dim3 fblk(BLK_THREADS);
+    if (dq) {
+      NTLB_DISPATCH_GRID_SR(grid, sr, {
+        if (w_dtype == NTLB_BF16)
+          quant_block_128x128_fast<DT_BF16, G_, S_, true><<<fgrd, fblk, 0, st>>>(ba);
+        else
+          quant_block_128x128_fast<DT_F32, G_, S_, true><<<fgrd, fblk, 0, st>>>(ba);
+      });
+    } else {
+      NTLB_DISPATCH_GRID_SR(grid, sr, {
+        if (w_dtype == NTLB_BF16)
+          quant_block_128x128_fast<DT_BF16, G_, S_, false><<<fgrd, fblk, 0, st>>>(ba);
+        else
+          quant_block_128x128_fast<DT_F32, G_, S_, false><<<fgrd, fblk, 0, st>>>(ba);
+      });
+    }
+    return check_launch(fn);
+  }
+  dim3 grd((unsigned)(NB * T)), blk(256);
   NTLB_DISPATCH_DT(w_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
     if (vec)
       quant_block_128x128_kernel<D_, G_, S_, true><<<grd, blk, 0, st>>>(ba);

@@ -12,7 +12,8 @@ import os
 import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libntlowbit.so")
+# NTLB_LIB_PATH points at another build of the same ABI (a tuned or debug build)
+LIB_PATH = os.environ.get("NTLB_LIB_PATH") or os.path.join(_HERE, "libntlowbit.so")
 ABI_VERSION = 1
 
 NTLB_OK = 0

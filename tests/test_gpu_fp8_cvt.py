@@ -1,0 +1,33 @@
+"""The hardware fp8 pack-convert agrees with the software e4m3 rounding.
+
+The quantizers round to e4m3 with v_cvt_pk_fp8_f32 on tiles without NaN.  The
+test program tests/hip/fp8_cvt_probe (built by __graft_entry__.build()) runs
+both conversions on every fp32 bit pattern with |v| <= 448 and every NaN; the
+only allowed differences are NaN inputs (the hardware writes 0xFF for +NaN),
+which the quantizers route to the software path."""
+
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+pytestmark = pytest.mark.gpu
+
+PROBE = os.path.join(ROOT, "tests", "hip", "fp8_cvt_probe")
+
+
+def test_hw_fp8_convert_matches_software_rounding(gpu_device):
+    if not os.path.exists(PROBE):
+        pytest.fail("tests/hip/fp8_cvt_probe is not built; run __graft_entry__.build()")
+    res = subprocess.run([PROBE], capture_output=True, text=True, timeout=120)
+    line = res.stdout.splitlines()[0]
+    assert line.startswith("status=no error"), res.stdout
+    fields = dict(re.findall(r"(\w+)=(\d+)", line))
+    assert int(fields["checked"]) > 2_000_000_000
+    assert int(fields["non_nan_mismatches"]) == 0, res.stdout
+    assert res.returncode == 0
