@@ -134,6 +134,17 @@ int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, int64_t K, in
                             int64_t lddq, int32_t* nan_rows, void* stream);
 
 /*
+ * Dequantize codes back to a float tensor: out[i, k] = q(code) * scale(i, k)
+ * with scale(i, k) = scales[(i >> r_shift) * s_row + (k >> c_shift) * s_col]
+ * (shifts 0 or 7; a zero stride broadcasts), cast to out_dtype.  The receive
+ * side of the comm-quant wire format (the receiver's .to(tokens.dtype) of
+ * moe.py:822-823, :998-999) and the dq of any quantizer above.
+ */
+int ntlb_dequant(int grid, const uint8_t* codes, int64_t ldc, const float* scales, int64_t s_row, int64_t s_col,
+                 int r_shift, int c_shift, int64_t R, int64_t K, void* out, int out_dtype, int64_t ldo,
+                 void* stream);
+
+/*
  * Blockwise-scaled GEMM  Y[M,N] = sum_kb sa(m,kb) * sb(n,kb) * (A_kb[m,:] . B_kb[n,:])  (+ bias[n]).
  * The math of F.linear(X_dq, W_dq, bias) in te_backend.py:253-259 with the
  * operands kept as codes plus scales: every 128-wide K block is multiplied
@@ -155,6 +166,77 @@ int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* 
                           int64_t sb_col, int b_shift, int64_t M, int64_t N, int64_t Kp, const void* bias,
                           int bias_dtype, void* y, int y_dtype, int64_t ldy, const int32_t* nan_a,
                           const int32_t* nan_b, void* stream);
+
+/*
+ * Grouped (per-expert) blockwise-scaled GEMM over a token-offset table.
+ * Replaces the per-expert loop of _run_local_experts (moe.py:888-962) /
+ * _forward_single_rank (moe.py:1062-1097) in which every expert's Linear runs
+ * the emulated backend on its selected rows.  Rows of A are sorted by expert:
+ * expert e owns rows [offsets[e], offsets[e+1]) (int32 [E+1], device memory,
+ * offsets[E] == M_total) and multiplies weight codes b + e*b_estride
+ * ([N, Kp] each, row stride ldb) with scales sb + e*sb_estride.  Scale
+ * indexing as ntlb_gemm_blockscaled, with A rows indexed globally.  Output
+ * y [M_total, N].  nan_b, when given, is [E, N].  No host synchronization.
+ */
+int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                  int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, int64_t b_estride,
+                                  const float* sb, int64_t sb_row, int64_t sb_col, int b_shift, int64_t sb_estride,
+                                  const int32_t* offsets, int n_experts, int64_t M_total, int64_t N, int64_t Kp,
+                                  void* y, int y_dtype, int64_t ldy, const int32_t* nan_a, const int32_t* nan_b,
+                                  void* stream);
+
+/*
+ * NF4 refresh of a persistent weight (the flat tensor of n elements):
+ * _quantize_nf4_persistent + _pack_nibbles (layers.py:130-139, :156-169).
+ * One scale per run of `block` consecutive elements (K for per_channel on an
+ * [N, K] weight, n for per_tensor, 64 for the 64-element recipe): scale = amax
+ * if finite and > 0 else 1 (layers.py:86-101).  code = argmin over the NF4
+ * codebook (layers.py:60-83) of |clamp(w/s, -1, 1) - cb|, first minimum wins.
+ * packed [ceil(n/2)]: element 2i in the low nibble of byte i.  amax_ws is a
+ * caller-zeroed uint32 workspace of ceil(n/block) words; scales [ceil(n/block)].
+ */
+int ntlb_nf4_quant(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws, uint8_t* packed,
+                   float* scales, void* stream);
+
+/* cb[code] * scale cast to out_dtype: _unpack_nibbles + _dequantize_nf4_persistent
+ * (layers.py:142-153, :172-184). */
+int ntlb_nf4_dequant(const uint8_t* packed, const float* scales, int64_t n, int64_t block, void* out,
+                     int out_dtype, void* stream);
+
+/*
+ * MXFP4 (OCP MX v1.0) refresh: 32-element blocks, e8m0 scale
+ * X = 2^(floor(log2 amax) - 2) (exponent clamped to [-127, 127]; 0xFF when the
+ * block holds a NaN or inf), e2m1 codes rounded to nearest even with
+ * saturation, packed as NF4.  No reference function.
+ */
+int ntlb_mxfp4_quant(const void* w, int w_dtype, int64_t n, uint8_t* packed, uint8_t* scales, void* stream);
+int ntlb_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t n, void* out, int out_dtype,
+                       void* stream);
+
+/*
+ * Persistent FP8 (layers.py:104-127): scale = amax per block (K for
+ * per_channel, n for per_tensor; finite and > 0 else 1), codes =
+ * e4m3fn(clamp(w/s, -448, 448)); dequant = e4m3 value * scale cast to out_dtype.
+ * amax_ws: caller-zeroed uint32 [ceil(n/block)].
+ */
+int ntlb_fp8_persistent_quant(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws,
+                              uint8_t* codes, float* scales, void* stream);
+int ntlb_fp8_persistent_dequant(const uint8_t* codes, const float* scales, int64_t n, int64_t block, void* out,
+                                int out_dtype, void* stream);
+
+/*
+ * Dequant-fused GEMMs: Y[M, N] = X[M, K] (bf16) . deq(W)[N, K]^T with fp32
+ * accumulation on bf16 MFMA, W dequantized in the B-tile prologue exactly as
+ * ntlb_nf4_dequant / ntlb_mxfp4_dequant would (bf16 of value * scale).  The
+ * persistent-weight forward of _persistent_weight_ste + F.linear
+ * (layers.py:409-436, :595-632) without materializing the bf16 weight.
+ * K % 64 == 0; NF4 block divides K and is a multiple of 32, or 0 for a
+ * single tensor scale; ldx % 8 == 0; y bf16 or fp32.
+ */
+int ntlb_gemm_nf4(const void* x, int64_t ldx, const uint8_t* w_packed, const float* w_scales, int64_t block,
+                  int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
+int ntlb_gemm_mxfp4(const void* x, int64_t ldx, const uint8_t* w_packed, const uint8_t* w_scales, int64_t M,
+                    int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,12 @@ struct GemmArgs {
   const int32_t* nan_a;
   const int32_t* nan_b;
   int vec_out;  // y 16-byte aligned with 16-byte row pitch
+  // grouped (per-expert) mode: rows of A sorted by expert, expert e owns rows
+  // [offsets[e], offsets[e+1]) and multiplies B + e*b_estride (codes) with
+  // scales sb + e*sb_estride
+  const int32_t* offsets;
+  int n_experts;
+  int64_t b_estride, sb_estride;
 };
 
 constexpr int BM = 256, BN = 256, BK = 128;
@@ -122,7 +128,7 @@ __device__ __forceinline__ void issue_stage(const StageSrc& s, uint8_t* stage, i
   }
 }
 
-template <int GRID, bool B_UNIFORM>
+template <int GRID, bool B_UNIFORM, bool GROUPED>
 __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
   float* lds_sa = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM]
@@ -133,21 +139,45 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
 
   // workgroup -> output tile: undo the round-robin XCD dispatch so each XCD
   // walks a contiguous range, then a grouped raster (GROUP_M row-tiles)
-  const int num_m = (int)((g.M + BM - 1) / BM), num_n = (int)((g.N + BN - 1) / BN);
-  const int nwg = num_m * num_n;
+  const int num_n = (int)((g.N + BN - 1) / BN);
+  const int nwg = (int)gridDim.x;
   int pid = blockIdx.x;
   {
     const int xcd = pid & 7, local = pid >> 3;
     const int per = nwg >> 3, extra = nwg & 7;
     pid = xcd * per + min(xcd, extra) + local;
   }
-  constexpr int GROUP_M = 4;
-  const int group = pid / (GROUP_M * num_n);
-  const int first_m = group * GROUP_M;
-  const int gsize = min(num_m - first_m, GROUP_M);
-  const int in_group = pid - group * GROUP_M * num_n;
-  const int64_t m0 = (int64_t)(first_m + in_group % gsize) * BM;
-  const int64_t n0 = (int64_t)(in_group / gsize) * BN;
+  int64_t m0, n0;
+  if constexpr (GROUPED) {
+    // row tile mt of the concatenated per-expert tilings; n fastest so that
+    // consecutive workgroups share the A rows and sweep one expert's B
+    const int mt = pid / num_n;
+    n0 = (int64_t)(pid - mt * num_n) * BN;
+    int e = 0, before = 0;
+    int64_t lo = 0, hi = 0;
+    for (; e < g.n_experts; ++e) {
+      lo = g.offsets[e];
+      hi = g.offsets[e + 1];
+      const int tiles = (int)((hi - lo + BM - 1) / BM);
+      if (mt < before + tiles) break;
+      before += tiles;
+    }
+    if (e >= g.n_experts) return;  // beyond the last expert's tiles: the grid is an upper bound
+    m0 = lo + (int64_t)(mt - before) * BM;
+    g.M = hi;  // rows at or past the expert's end are not stored
+    g.b += (int64_t)e * g.b_estride;
+    g.sb += (int64_t)e * g.sb_estride;
+    if (g.nan_b) g.nan_b += (int64_t)e * g.N;
+  } else {
+    const int num_m = (int)((g.M + BM - 1) / BM);
+    constexpr int GROUP_M = 4;
+    const int group = pid / (GROUP_M * num_n);
+    const int first_m = group * GROUP_M;
+    const int gsize = min(num_m - first_m, GROUP_M);
+    const int in_group = pid - group * GROUP_M * num_n;
+    m0 = (int64_t)(first_m + in_group % gsize) * BM;
+    n0 = (int64_t)(in_group / gsize) * BN;
+  }
 
   // scale fetch: threads 0..255 own sa of row m0+tid, 256..511 sb of row n0+tid-256
   const bool own_a = tid < BM;
@@ -348,20 +378,71 @@ extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, co
   g.y = y; g.y_dtype = y_dtype; g.ldy = ldy;
   g.nan_a = nan_a; g.nan_b = nan_b;
   g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
+  g.offsets = nullptr; g.n_experts = 0; g.b_estride = 0; g.sb_estride = 0;
   // B's scale is uniform over each wave's 64 columns for 128x128 blocks and tensor scales
   const bool b_uniform = (b_shift == 7) || (sb_row == 0);
   hipStream_t st = as_stream(stream);
   dim3 grd((unsigned)tiles), blk(NTHREADS);
   if (grid == NTLB_GRID_E4M3) {
     if (b_uniform)
-      gemm_blockscaled_kernel<GRID_E4M3, true><<<grd, blk, 0, st>>>(g);
+      gemm_blockscaled_kernel<GRID_E4M3, true, false><<<grd, blk, 0, st>>>(g);
     else
-      gemm_blockscaled_kernel<GRID_E4M3, false><<<grd, blk, 0, st>>>(g);
+      gemm_blockscaled_kernel<GRID_E4M3, false, false><<<grd, blk, 0, st>>>(g);
   } else {
     if (b_uniform)
-      gemm_blockscaled_kernel<GRID_INT, true><<<grd, blk, 0, st>>>(g);
+      gemm_blockscaled_kernel<GRID_INT, true, false><<<grd, blk, 0, st>>>(g);
     else
-      gemm_blockscaled_kernel<GRID_INT, false><<<grd, blk, 0, st>>>(g);
+      gemm_blockscaled_kernel<GRID_INT, false, false><<<grd, blk, 0, st>>>(g);
+  }
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                             int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb,
+                                             int64_t b_estride, const float* sb, int64_t sb_row, int64_t sb_col,
+                                             int b_shift, int64_t sb_estride, const int32_t* offsets, int n_experts,
+                                             int64_t M_total, int64_t N, int64_t Kp, void* y, int y_dtype,
+                                             int64_t ldy, const int32_t* nan_a, const int32_t* nan_b, void* stream) {
+  const char* fn = "ntlb_gemm_grouped_blockscaled";
+  if (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3) return fail(NTLB_EINVAL, "%s: bad grid %d", fn, grid);
+  if (M_total < 0 || N < 0 || Kp < 0 || n_experts < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (Kp % 128) return fail(NTLB_EINVAL, "%s: Kp %lld is not a multiple of 128", fn, (long long)Kp);
+  if (M_total == 0 || N == 0 || n_experts == 0) return NTLB_OK;
+  if (!a || !b || !sa || !sb || !y || !offsets) return fail(NTLB_EINVAL, "%s: NULL operand", fn);
+  if (lda < Kp || ldb < Kp || (lda % 16) || (ldb % 16) || !aligned(a, 16) || !aligned(b, 16) ||
+      (b_estride % 16) || b_estride < N * ldb)
+    return fail(NTLB_EINVAL, "%s: code matrices need ld >= Kp, ld %% 16 == 0, 16-byte alignment and "
+                "b_estride >= N*ldb", fn);
+  if (!(a_shift == 0 || a_shift == 7) || !(b_shift == 0 || b_shift == 7))
+    return fail(NTLB_EINVAL, "%s: scale shifts must be 0 or 7", fn);
+  if (!valid_dtype(y_dtype) || ldy < N) return fail(NTLB_EINVAL, "%s: bad output dtype or ldy", fn);
+  if (Kp == 0) return fail(NTLB_EUNSUPPORTED, "%s: K == 0", fn);
+  if ((M_total + BM) * lda >= (int64_t)0x7FFFFFFF || (N + BN) * ldb >= (int64_t)0x7FFFFFFF)
+    return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
+  const int64_t tiles = ((M_total + BM - 1) / BM + n_experts) * ((N + BN - 1) / BN);
+  if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  GemmArgs g;
+  g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
+  g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = b_shift;
+  g.M = M_total; g.N = N; g.Kp = Kp;
+  g.bias = nullptr; g.bias_dtype = 0;
+  g.y = y; g.y_dtype = y_dtype; g.ldy = ldy;
+  g.nan_a = nan_a; g.nan_b = nan_b;
+  g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
+  g.offsets = offsets; g.n_experts = n_experts; g.b_estride = b_estride; g.sb_estride = sb_estride;
+  const bool b_uniform = (b_shift == 7) || (sb_row == 0);
+  hipStream_t st = as_stream(stream);
+  dim3 grd((unsigned)tiles), blk(NTHREADS);
+  if (grid == NTLB_GRID_E4M3) {
+    if (b_uniform)
+      gemm_blockscaled_kernel<GRID_E4M3, true, true><<<grd, blk, 0, st>>>(g);
+    else
+      gemm_blockscaled_kernel<GRID_E4M3, false, true><<<grd, blk, 0, st>>>(g);
+  } else {
+    if (b_uniform)
+      gemm_blockscaled_kernel<GRID_INT, true, true><<<grd, blk, 0, st>>>(g);
+    else
+      gemm_blockscaled_kernel<GRID_INT, false, true><<<grd, blk, 0, st>>>(g);
   }
   return check_launch(fn);
 }

@@ -1,0 +1,596 @@
+// Persistent low-bit weights for gfx950: NF4 (src/layers.py:60-184) and
+// MXFP4 (OCP MX v1.0 e2m1 + e8m0; no reference function), their refresh
+// (quantize) and dequantize kernels, and the GEMM with the dequantization
+// fused into the B-tile prologue on bf16 MFMA.
+//
+// NF4: one fp32 scale per run of `block` consecutive elements of the flat
+// weight (block = K per output row for per_channel, numel for per_tensor, 64
+// for the 64-element recipe): scale = amax, non-finite or <= 0 -> 1
+// (layers.py:86-101); code = argmin_i |clamp(w/s, -1, 1) - cb_i| with the
+// first minimum winning (layers.py:165-166); two codes per byte, the even
+// element in the low nibble (layers.py:130-139).  Dequantized value:
+// bf16/fp32 of cb[code] * scale (layers.py:172-184).
+//
+// MXFP4: 32-element blocks, shared scale X = 2^(floor(log2 amax) - 2) stored
+// as e8m0 (exponent clamped to [-127, 127]; 0xFF = NaN when the block holds a
+// NaN or inf), elements rounded to nearest even onto e2m1 with saturation.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "ntlb_device.h"
+#include "ntlb_host.h"
+
+#pragma clang fp contract(off)
+
+namespace ntlb {
+
+__constant__ float kNF4[16] = {-1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
+                               -0.09105004f, 0.0f,         0.0795803f,   0.1609302f,  0.2461123f,   0.33791524f,
+                               0.44070983f,  0.562617f,    0.72295684f,  1.0f};
+__constant__ float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+
+enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1 };
+
+// ---------------------------------------------------------------------------
+// element codes
+// ---------------------------------------------------------------------------
+// NF4 index of c = clamp(w/s): the pair of codebook entries bracketing c
+// decides (every other entry is farther by at least the codebook gap); ties
+// go to the lower index; NaN gives 0 as torch.argmin does on an all-NaN row.
+__device__ __forceinline__ uint32_t nf4_index(float c) {
+  int below = 0;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) below += (kNF4[i] <= c) ? 1 : 0;
+  if (!(c == c)) return 0;
+  if (below >= 15) return 15;
+  const float d0 = fabsf(c - kNF4[below]);
+  const float d1 = fabsf(c - kNF4[below + 1]);
+  return (d1 < d0) ? (uint32_t)(below + 1) : (uint32_t)below;
+}
+
+// e2m1 round to nearest even with saturation; the sign of v is kept
+__device__ __forceinline__ uint32_t e2m1_code(float v) {
+  const float a = fabsf(v);
+  uint32_t c = (a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) + (a > 5.0f);
+  if (!(a == a)) c = 0;
+  return c | ((__float_as_uint(v) >> 28) & 8u);
+}
+
+__device__ __forceinline__ float e2m1_value(uint32_t c) {
+  const float v = kE2M1[c & 7u];
+  return (c & 8u) ? -v : v;
+}
+
+// e8m0 shared exponent of a 32-element block from its amax bits
+__device__ __forceinline__ uint32_t mx_scale_byte(uint32_t amax_bits) {
+  if (amax_bits >= 0x7F800000u) return 0xFFu;  // NaN or inf in the block
+  if (amax_bits == 0u) return 0u;               // 2^-127
+  int e;
+  const uint32_t ef = amax_bits >> 23;
+  if (ef != 0) {
+    e = (int)ef - 127;
+  } else {  // subnormal amax: position of the top set mantissa bit
+    e = -127 - (__builtin_clz(amax_bits) - 9);
+  }
+  e -= 2;
+  e = e < -127 ? -127 : (e > 127 ? 127 : e);
+  return (uint32_t)(e + 127);
+}
+
+// ---------------------------------------------------------------------------
+// NF4 refresh: block amax (atomics on |w| bits), scales, codes
+// ---------------------------------------------------------------------------
+template <int IN_DT>
+__global__ void __launch_bounds__(256) flat_block_amax_kernel(const void* w, int64_t n, int64_t block,
+                                                              uint32_t* amax_bits) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  uint32_t m[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) m[i] = (e0 + i < n) ? abs_bits(load_elem(w, IN_DT, e0 + i)) : 0u;
+  if (block % 512 == 0) {
+    // a wave covers 512 consecutive elements inside one block
+    uint32_t mm = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mm = max(mm, m[i]);
+    mm = wave_max_u32(mm);
+    if ((threadIdx.x & 63) == 0 && e0 < n && mm) atomicMax(amax_bits + e0 / block, mm);
+  } else if (block % 8 == 0) {
+    uint32_t mm = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mm = max(mm, m[i]);
+    if (e0 < n && mm) atomicMax(amax_bits + e0 / block, mm);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (e0 + i < n && m[i]) atomicMax(amax_bits + (e0 + i) / block, m[i]);
+  }
+}
+
+// scale = amax when finite and > 0, else 1 (layers.py:98-100)
+__global__ void amax_to_scale_kernel(const uint32_t* amax_bits, int64_t nb, float* scales) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nb) {
+    const uint32_t b = amax_bits[i];
+    const float a = __uint_as_float(b);
+    scales[i] = (b < 0x7F800000u && a > 0.0f) ? a : 1.0f;
+  }
+}
+
+template <int IN_DT>
+__global__ void __launch_bounds__(256) nf4_quant_kernel(const void* w, int64_t n, int64_t block, const float* scales,
+                                                        uint8_t* packed) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= n) return;
+  uint32_t idx[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t e = e0 + i;
+    if (e < n) {
+      float c = load_elem(w, IN_DT, e) / scales[e / block];
+      c = (c < -1.0f) ? -1.0f : c;
+      c = (c > 1.0f) ? 1.0f : c;
+      idx[i] = nf4_index(c);
+    } else {
+      idx[i] = 0;
+    }
+  }
+  const int64_t nbytes = (n + 1) / 2;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t bidx = e0 / 2 + j;
+    if (bidx < nbytes) packed[bidx] = (uint8_t)(idx[2 * j] | (idx[2 * j + 1] << 4));
+  }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(256) lowbit_dequant_kernel(const uint8_t* packed, const void* scales, int64_t n,
+                                                             int64_t block, void* out, int out_dtype) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= n) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t e = e0 + i;
+    if (e >= n) break;
+    const uint32_t byte = packed[e >> 1];
+    const uint32_t c = (e & 1) ? (byte >> 4) : (byte & 15u);
+    float v;
+    if constexpr (FMT == FMT_NF4) {
+      v = kNF4[c] * reinterpret_cast<const float*>(scales)[e / block];
+    } else {
+      const uint32_t sb = reinterpret_cast<const uint8_t*>(scales)[e >> 5];
+      v = (sb == 0xFFu) ? __uint_as_float(0x7FC00000u) : ldexpf(e2m1_value(c), (int)sb - 127);
+    }
+    store_elem(out, out_dtype, e, v);
+  }
+}
+
+// MXFP4 refresh: 4 lanes (a DPP quad) per 32-element block
+template <int IN_DT>
+__global__ void __launch_bounds__(256) mxfp4_quant_kernel(const void* w, int64_t n, uint8_t* packed,
+                                                          uint8_t* scales) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  float v[8];
+  uint32_t m = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[i] = (e0 + i < n) ? load_elem(w, IN_DT, e0 + i) : 0.0f;
+    m = max(m, abs_bits(v[i]));
+  }
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0xB1, 0xF, 0xF, false));
+  m = max(m, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)m, 0x4E, 0xF, 0xF, false));
+  if (e0 >= n) return;
+  const uint32_t sb = mx_scale_byte(m);
+  if ((threadIdx.x & 3) == 0) scales[e0 >> 5] = (uint8_t)sb;
+  uint32_t c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c[i] = (sb == 0xFFu) ? 0u : e2m1_code(ldexpf(v[i], 127 - (int)sb));
+  const int64_t nbytes = (n + 1) / 2;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t bidx = e0 / 2 + j;
+    if (bidx < nbytes) packed[bidx] = (uint8_t)(c[2 * j] | (c[2 * j + 1] << 4));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent FP8 (layers.py:104-127): scale = amax per block (a row for
+// per_channel, everything for per_tensor), code = e4m3(clamp(w/s, +-448)),
+// dequantized value = e4m3 value * scale.
+// ---------------------------------------------------------------------------
+template <int IN_DT>
+__global__ void __launch_bounds__(256) fp8p_quant_kernel(const void* w, int64_t n, int64_t block, const float* scales,
+                                                         uint8_t* codes) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= n) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t e = e0 + i;
+    if (e >= n) break;
+    float v = load_elem(w, IN_DT, e) / scales[e / block];
+    v = (v < -448.0f) ? -448.0f : v;
+    v = (v > 448.0f) ? 448.0f : v;
+    codes[e] = (uint8_t)e4m3_rne(v);
+  }
+}
+
+__global__ void __launch_bounds__(256) fp8p_dequant_kernel(const uint8_t* codes, const float* scales, int64_t n,
+                                                           int64_t block, void* out, int out_dtype) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= n) return;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t e = e0 + i;
+    if (e >= n) break;
+    store_elem(out, out_dtype, e, e4m3_to_f32(codes[e]) * scales[e / block]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Dequant-fused GEMM  Y[M,N] = X[M,K] (bf16) . deq(W)[N,K]^T, fp32 accumulate.
+// 256x256 output tile, 8 waves of 128x64, K step 64 bf16 (128-byte rows, the
+// same swizzled tile layout as the fp8 kernel).  X tiles move global -> LDS
+// directly; each thread dequantizes 32 weights (16 packed bytes) of one B row
+// per K step into bf16 in LDS, with the next step's packed bytes already in
+// registers.  MFMA: v_mfma_f32_16x16x32_bf16, B tile as the first operand so
+// each lane holds four consecutive output columns.
+// ---------------------------------------------------------------------------
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+constexpr int FBM = 256, FBN = 256, FBK = 64;  // FBK in bf16 elements: 128 bytes per row
+constexpr int FROW = 128;                       // bytes per tile row
+constexpr int FT = 256 * FROW;                  // 32 KiB per operand tile
+constexpr int FSTAGE = 2 * FT;
+constexpr int F_EPI_PITCH = 64 * 4 + 16;
+constexpr int F_SMEM = (2 * FSTAGE > 8 * 64 * F_EPI_PITCH) ? 2 * FSTAGE : 8 * 64 * F_EPI_PITCH;
+
+__device__ __forceinline__ int fswz(int r, int c) { return r * FROW + ((c ^ (r & 7)) << 4); }
+
+__device__ __forceinline__ v8i frag32(const uint8_t* tile, int row0, int lane) {
+  const int r = row0 + (lane & 15);
+  const int g = lane >> 4;
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + fswz(r, 2 * g));
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + fswz(r, 2 * g + 1));
+  v8i f;
+  f[0] = (int)lo.x; f[1] = (int)lo.y; f[2] = (int)lo.z; f[3] = (int)lo.w;
+  f[4] = (int)hi.x; f[5] = (int)hi.y; f[6] = (int)hi.z; f[7] = (int)hi.w;
+  return f;
+}
+
+// two K=32 bf16 MFMAs over a 32-byte-per-lane fragment pair (64 K values)
+__device__ __forceinline__ v4f mma_bf16_64(const v8i& p, const v8i& q, v4f acc) {
+  typedef int v4i_t __attribute__((ext_vector_type(4)));
+  const v4i_t pl = {p[0], p[1], p[2], p[3]}, ph = {p[4], p[5], p[6], p[7]};
+  const v4i_t ql = {q[0], q[1], q[2], q[3]}, qh = {q[4], q[5], q[6], q[7]};
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, pl), __builtin_bit_cast(v8bf, ql), acc, 0, 0,
+                                                0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, ph), __builtin_bit_cast(v8bf, qh), acc, 0, 0,
+                                                0);
+  return acc;
+}
+
+struct FusedArgs {
+  const uint16_t* x;  // bf16 [M, K], row stride ldx
+  int64_t ldx;
+  const uint8_t* w;   // packed codes of the flat [N, K] weight
+  const void* scales;  // NF4: fp32 per block; MXFP4: e8m0 per 32
+  int64_t block;       // NF4 block (divides K, multiple of 32) or 0 for one tensor scale
+  int64_t M, N, K;
+  void* y;
+  int y_dtype;
+  int64_t ldy;
+  int vec_out;
+};
+
+template <int FMT>
+__device__ __forceinline__ void dequant32_to_lds(const uint4 raw, const FusedArgs& g, int64_t n, int64_t k0,
+                                                 uint8_t* tile, int r, int h) {
+  // scale of the 32 elements [k0, k0+32) of row n
+  float s = 1.0f;
+  uint32_t sb = 127;
+  if constexpr (FMT == FMT_NF4) {
+    const float* sc = reinterpret_cast<const float*>(g.scales);
+    s = (g.block == 0) ? sc[0] : sc[n * (g.K / g.block) + k0 / g.block];
+  } else {
+    sb = reinterpret_cast<const uint8_t*>(g.scales)[n * (g.K >> 5) + (k0 >> 5)];
+  }
+  const uint32_t bytes[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // 8 elements (4 bytes) per 16-byte LDS chunk
+    uint32_t out[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (bytes[j] >> (8 * b)) & 0xFFu;
+      float v0, v1;
+      if constexpr (FMT == FMT_NF4) {
+        v0 = kNF4[byte & 15u] * s;
+        v1 = kNF4[byte >> 4] * s;
+      } else if (sb == 0xFFu) {
+        v0 = v1 = __uint_as_float(0x7FC00000u);
+      } else {
+        v0 = ldexpf(e2m1_value(byte & 15u), (int)sb - 127);
+        v1 = ldexpf(e2m1_value(byte >> 4), (int)sb - 127);
+      }
+      out[b] = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
+    }
+    *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
+  }
+}
+
+template <int FMT>
+__global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[F_SMEM];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+  const int num_n = (int)((g.N + FBN - 1) / FBN);
+  const int num_m = (int)((g.M + FBM - 1) / FBM);
+  const int nwg = num_m * num_n;
+  int pid = blockIdx.x;
+  {
+    const int xcd = pid & 7, local = pid >> 3;
+    const int per = nwg >> 3, extra = nwg & 7;
+    pid = xcd * per + min(xcd, extra) + local;
+  }
+  constexpr int GROUP_M = 4;
+  const int group = pid / (GROUP_M * num_n);
+  const int first_m = group * GROUP_M;
+  const int gsize = min(num_m - first_m, GROUP_M);
+  const int in_group = pid - group * GROUP_M * num_n;
+  const int64_t m0 = (int64_t)(first_m + in_group % gsize) * FBM;
+  const int64_t n0 = (int64_t)(in_group / gsize) * FBN;
+
+  // X tile: direct-to-LDS, 4 groups of 8 rows per wave; rows past M read zero
+  __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)g.x, (short)0, (int)(g.M * g.ldx * 2), 0x00020000);
+  const int xr = wave * 32 + (lane >> 3);
+  const uint32_t x_off = (uint32_t)(((m0 + xr) * g.ldx) * 2 + (((lane & 7) ^ (xr & 7)) * 16));
+  const uint32_t x_grp = (uint32_t)(8 * g.ldx * 2);
+  // W: thread t dequantizes row t/2, half t%2 (32 weights = 16 packed bytes)
+  const int br = tid >> 1, bh = tid & 1;
+  const int64_t bn = min<int64_t>(n0 + br, g.N - 1);
+  const uint8_t* wrow = g.w + bn * (g.K >> 1) + bh * 16;
+
+  const int nk = (int)(g.K / FBK);
+  v4f acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  auto issue_x = [&](uint8_t* stage, int kt) {
+    const uint32_t koff = (uint32_t)kt * FROW;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(stage + (wave * 4 + j) * 8 * FROW), 16, x_off,
+                                               koff + j * x_grp, 0, 0);
+  };
+
+  uint4 wraw = *reinterpret_cast<const uint4*>(wrow);
+  issue_x(smem, 0);
+  dequant32_to_lds<FMT>(wraw, g, bn, bh * 32, smem + FT, br, bh);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    uint8_t* st = smem + buf * FSTAGE;
+    if (kt + 1 < nk) {
+      issue_x(smem + (buf ^ 1) * FSTAGE, kt + 1);
+      wraw = *reinterpret_cast<const uint4*>(wrow + (int64_t)(kt + 1) * (FBK / 2));
+    }
+    const uint8_t* ta = st;
+    const uint8_t* tb = st + FT;
+    v8i bf[4];
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) bf[tn] = frag32(tb, wn * 64 + tn * 16, lane);
+    v8i af = frag32(ta, wm * 128, lane);
+#pragma unroll
+    for (int tm = 0; tm < 8; ++tm) {
+      v8i af_next;
+      if (tm + 1 < 8) af_next = frag32(ta, wm * 128 + (tm + 1) * 16, lane);
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) acc[tm][tn] = mma_bf16_64(bf[tn], af, acc[tm][tn]);
+      asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
+      if (tm + 1 < 8) af = af_next;
+    }
+    if (kt + 1 < nk) dequant32_to_lds<FMT>(wraw, g, bn, (int64_t)(kt + 1) * FBK + bh * 32, smem + (buf ^ 1) * FSTAGE + FT,
+                                           br, bh);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // epilogue: stage each wave's 128x64 through LDS, 16-byte row-contiguous stores
+  uint8_t* stage_w = smem + wave * 64 * F_EPI_PITCH;
+  const bool out_f32 = g.y_dtype == DT_F32;
+  const int pitch = out_f32 ? F_EPI_PITCH : (64 * 2 + 16);
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int tm = half * 4 + t;
+      const int rloc = t * 16 + (lane & 15);
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        const v4f v = acc[tm][tn];
+        uint8_t* dst = stage_w + rloc * pitch + (tn * 16 + (lane >> 4) * 4) * (out_f32 ? 4 : 2);
+        if (out_f32) {
+          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2((uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
+                         (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
+        }
+      }
+    }
+    __syncthreads();
+    const int cpr = out_f32 ? 16 : 8;
+    const int esz = out_f32 ? 4 : 2;
+    const int epc = 16 / esz;
+    for (int j = 0; j < cpr; ++j) {
+      const int q = lane + 64 * j;
+      const int row = q / cpr, c = q % cpr;
+      const int64_t m = m0 + wm * 128 + half * 64 + row;
+      const int64_t n = n0 + wn * 64 + c * epc;
+      if (m >= g.M || n >= g.N) continue;
+      const uint8_t* src = stage_w + row * pitch + c * 16;
+      uint8_t* ydst = reinterpret_cast<uint8_t*>(g.y) + (m * g.ldy + n) * esz;
+      if (g.vec_out && n + epc <= g.N) {
+        *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+      } else {
+        for (int e = 0; e < epc && n + e < g.N; ++e)
+          for (int bi = 0; bi < esz; ++bi) ydst[e * esz + bi] = src[e * esz + bi];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace ntlb
+
+using namespace ntlb;
+
+extern "C" int ntlb_nf4_quant(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws,
+                              uint8_t* packed, float* scales, void* stream) {
+  const char* fn = "ntlb_nf4_quant";
+  if (!valid_dtype(w_dtype)) return fail(NTLB_EINVAL, "%s: bad dtype", fn);
+  if (n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad size or block", fn);
+  if (n == 0) return NTLB_OK;
+  if (!w || !amax_ws || !packed || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  const int64_t nb = cdiv(n, block);
+  const int64_t threads = cdiv(n, 8);
+  if (cdiv(threads, 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
+  hipStream_t st = as_stream(stream);
+  dim3 grd((unsigned)cdiv(threads, 256)), blk(256);
+  if (w_dtype == NTLB_BF16)
+    flat_block_amax_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
+  else if (w_dtype == NTLB_F32)
+    flat_block_amax_kernel<DT_F32><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
+  else
+    flat_block_amax_kernel<DT_F16><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
+  amax_to_scale_kernel<<<(unsigned)cdiv(nb, 256), 256, 0, st>>>(amax_ws, nb, scales);
+  if (w_dtype == NTLB_BF16)
+    nf4_quant_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, block, scales, packed);
+  else if (w_dtype == NTLB_F32)
+    nf4_quant_kernel<DT_F32><<<grd, blk, 0, st>>>(w, n, block, scales, packed);
+  else
+    nf4_quant_kernel<DT_F16><<<grd, blk, 0, st>>>(w, n, block, scales, packed);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_nf4_dequant(const uint8_t* packed, const float* scales, int64_t n, int64_t block, void* out,
+                                int out_dtype, void* stream) {
+  const char* fn = "ntlb_nf4_dequant";
+  if (!valid_dtype(out_dtype) || n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  if (n == 0) return NTLB_OK;
+  if (!packed || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  lowbit_dequant_kernel<FMT_NF4><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(packed, scales, n,
+                                                                                                 block, out, out_dtype);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_mxfp4_quant(const void* w, int w_dtype, int64_t n, uint8_t* packed, uint8_t* scales,
+                                void* stream) {
+  const char* fn = "ntlb_mxfp4_quant";
+  if (!valid_dtype(w_dtype) || n < 0) return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  if (n == 0) return NTLB_OK;
+  if (!w || !packed || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  dim3 grd((unsigned)cdiv(cdiv(n, 8), 256)), blk(256);
+  hipStream_t st = as_stream(stream);
+  if (w_dtype == NTLB_BF16)
+    mxfp4_quant_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, packed, scales);
+  else if (w_dtype == NTLB_F32)
+    mxfp4_quant_kernel<DT_F32><<<grd, blk, 0, st>>>(w, n, packed, scales);
+  else
+    mxfp4_quant_kernel<DT_F16><<<grd, blk, 0, st>>>(w, n, packed, scales);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t n, void* out, int out_dtype,
+                                  void* stream) {
+  const char* fn = "ntlb_mxfp4_dequant";
+  if (!valid_dtype(out_dtype) || n < 0) return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  if (n == 0) return NTLB_OK;
+  if (!packed || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  lowbit_dequant_kernel<FMT_MXFP4><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(
+      packed, scales, n, 32, out, out_dtype);
+  return check_launch(fn);
+}
+
+static int fused_launch(int fmt, const char* fn, const void* x, int64_t ldx, const uint8_t* w, const void* scales,
+                        int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
+                        void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (M == 0 || N == 0) return NTLB_OK;
+  if (!x || !w || !scales || !y) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (K % FBK) return fail(NTLB_EUNSUPPORTED, "%s: K must be a multiple of %d", fn, FBK);
+  if (ldx < K || (ldx % 8) || !aligned(x, 16) || !aligned(w, 16))
+    return fail(NTLB_EINVAL, "%s: x needs ldx >= K, ldx %% 8 == 0, 16-byte alignment; w 16-byte alignment", fn);
+  if (!(y_dtype == NTLB_BF16 || y_dtype == NTLB_F32) || ldy < N)
+    return fail(NTLB_EINVAL, "%s: output must be bf16 or fp32 with ldy >= N", fn);
+  if (fmt == FMT_NF4 && block != 0 && (K % block || block % 32))
+    return fail(NTLB_EUNSUPPORTED, "%s: NF4 block must divide K and be a multiple of 32 (or 0 = tensor)", fn);
+  if ((M + FBM) * ldx * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: X exceeds 2 GiB", fn);
+  const int64_t tiles = ((M + FBM - 1) / FBM) * ((N + FBN - 1) / FBN);
+  FusedArgs g;
+  g.x = reinterpret_cast<const uint16_t*>(x); g.ldx = ldx; g.w = w; g.scales = scales; g.block = block;
+  g.M = M; g.N = N; g.K = K; g.y = y; g.y_dtype = y_dtype; g.ldy = ldy;
+  g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
+  dim3 grd((unsigned)tiles), blk(512);
+  if (fmt == FMT_NF4)
+    gemm_lowbit_fused_kernel<FMT_NF4><<<grd, blk, 0, as_stream(stream)>>>(g);
+  else
+    gemm_lowbit_fused_kernel<FMT_MXFP4><<<grd, blk, 0, as_stream(stream)>>>(g);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_nf4(const void* x, int64_t ldx, const uint8_t* w_packed, const float* w_scales,
+                             int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
+                             void* stream) {
+  return fused_launch(FMT_NF4, "ntlb_gemm_nf4", x, ldx, w_packed, w_scales, block, M, N, K, y, y_dtype, ldy,
+                      stream);
+}
+
+extern "C" int ntlb_gemm_mxfp4(const void* x, int64_t ldx, const uint8_t* w_packed, const uint8_t* w_scales,
+                               int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream) {
+  if (K % 32) return fail(NTLB_EUNSUPPORTED, "ntlb_gemm_mxfp4: K must be a multiple of 32");
+  return fused_launch(FMT_MXFP4, "ntlb_gemm_mxfp4", x, ldx, w_packed, w_scales, 32, M, N, K, y, y_dtype, ldy,
+                      stream);
+}
+
+extern "C" int ntlb_fp8_persistent_quant(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws,
+                                         uint8_t* codes, float* scales, void* stream) {
+  const char* fn = "ntlb_fp8_persistent_quant";
+  if (!valid_dtype(w_dtype) || n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  if (n == 0) return NTLB_OK;
+  if (!w || !amax_ws || !codes || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  const int64_t nb = cdiv(n, block);
+  dim3 grd((unsigned)cdiv(cdiv(n, 8), 256)), blk(256);
+  hipStream_t st = as_stream(stream);
+  if (w_dtype == NTLB_BF16)
+    flat_block_amax_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
+  else if (w_dtype == NTLB_F32)
+    flat_block_amax_kernel<DT_F32><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
+  else
+    flat_block_amax_kernel<DT_F16><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
+  amax_to_scale_kernel<<<(unsigned)cdiv(nb, 256), 256, 0, st>>>(amax_ws, nb, scales);
+  if (w_dtype == NTLB_BF16)
+    fp8p_quant_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, block, scales, codes);
+  else if (w_dtype == NTLB_F32)
+    fp8p_quant_kernel<DT_F32><<<grd, blk, 0, st>>>(w, n, block, scales, codes);
+  else
+    fp8p_quant_kernel<DT_F16><<<grd, blk, 0, st>>>(w, n, block, scales, codes);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_fp8_persistent_dequant(const uint8_t* codes, const float* scales, int64_t n, int64_t block,
+                                           void* out, int out_dtype, void* stream) {
+  const char* fn = "ntlb_fp8_persistent_dequant";
+  if (!valid_dtype(out_dtype) || n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  if (n == 0) return NTLB_OK;
+  if (!codes || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  fp8p_dequant_kernel<<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(codes, scales, n, block, out,
+                                                                                     out_dtype);
+  return check_launch(fn);
+}

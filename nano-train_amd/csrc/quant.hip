@@ -787,6 +787,38 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// dequantize: out[i, k] = value(code[i, k]) * scale(i, k), cast to out dtype.
+// scale(i, k) = scales[(i >> r_shift) * s_row + (k >> c_shift) * s_col]
+// (r_shift/c_shift 0 or 7 cover rows, 128-blocks, tiles and strips; a zero
+// stride broadcasts).  The receive side of the comm-quant wire format.
+// ---------------------------------------------------------------------------
+template <int GRID>
+__global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* codes, int64_t ldc, const float* scales,
+                                                      int64_t s_row, int64_t s_col, int r_shift, int c_shift,
+                                                      int64_t R, int64_t K, void* out, int out_dtype, int64_t ldo) {
+  const int64_t chunks_per_row = (K + 7) >> 3;
+  const int64_t total = R * chunks_per_row;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+    const int64_t r = c / chunks_per_row;
+    const int64_t k0 = (c - r * chunks_per_row) * 8;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t k = k0 + i;
+      if (k < K) {
+        const uint32_t cd = codes[r * ldc + k];
+        const float q = (GRID == GRID_E4M3) ? e4m3_to_f32(cd)
+                                            : (cd == 0x80u ? __uint_as_float(0x7FC00000u) : (float)(int8_t)cd);
+        v[i] = q * scales[(r >> r_shift) * s_row + (k >> c_shift) * s_col];
+      } else {
+        v[i] = 0.0f;
+      }
+    }
+    store_dq8(out, out_dtype, r * ldo, k0, K, v, 1.0f);
+  }
+}
 // ---------------------------------------------------------------------------
 // dispatch helpers
 // ---------------------------------------------------------------------------
@@ -1076,5 +1108,27 @@ extern "C" int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, in
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
     quant_tile_128x1_t_kernel<D_, G_, S_><<<grd, blk, 0, st>>>(a);
   }));
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_dequant(int grid, const uint8_t* codes, int64_t ldc, const float* scales, int64_t s_row,
+                            int64_t s_col, int r_shift, int c_shift, int64_t R, int64_t K, void* out, int out_dtype,
+                            int64_t ldo, void* stream) {
+  const char* fn = "ntlb_dequant";
+  if (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3) return fail(NTLB_EINVAL, "%s: bad grid %d", fn, grid);
+  if (R < 0 || K < 0 || ldc < K || ldo < K) return fail(NTLB_EINVAL, "%s: bad shape", fn);
+  if (!(r_shift == 0 || r_shift == 7) || !(c_shift == 0 || c_shift == 7))
+    return fail(NTLB_EINVAL, "%s: shifts must be 0 or 7", fn);
+  if (!valid_dtype(out_dtype)) return fail(NTLB_EINVAL, "%s: bad output dtype", fn);
+  if (R * K == 0) return NTLB_OK;
+  if (!codes || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  hipStream_t st = as_stream(stream);
+  dim3 grd(grid_for(R * cdiv(K, 8), 256, 256 * 16)), blk(256);
+  if (grid == NTLB_GRID_E4M3)
+    dequant_kernel<GRID_E4M3><<<grd, blk, 0, st>>>(codes, ldc, scales, s_row, s_col, r_shift, c_shift, R, K, out,
+                                                   out_dtype, ldo);
+  else
+    dequant_kernel<GRID_INT><<<grd, blk, 0, st>>>(codes, ldc, scales, s_row, s_col, r_shift, c_shift, R, K, out,
+                                                  out_dtype, ldo);
   return check_launch(fn);
 }

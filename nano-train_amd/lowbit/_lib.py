@@ -44,8 +44,19 @@ SIGNATURES = {
                            _P, _P, _I32, _I64, _P, _P],
     "ntlb_quant_tile_128x1_t": [_P, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _U64, _U64, _P, _I64, _P, _I64,
                                 _I64, _P, _I32, _I64, _P, _P],
+    "ntlb_dequant": [_I32, _P, _I64, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_blockscaled": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64,
                               _I64, _P, _I32, _P, _I32, _I64, _P, _P, _P],
+    "ntlb_gemm_grouped_blockscaled": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I32,
+                                      _I64, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P],
+    "ntlb_nf4_quant": [_P, _I32, _I64, _I64, _P, _P, _P, _P],
+    "ntlb_nf4_dequant": [_P, _P, _I64, _I64, _P, _I32, _P],
+    "ntlb_mxfp4_quant": [_P, _I32, _I64, _P, _P, _P],
+    "ntlb_mxfp4_dequant": [_P, _P, _I64, _P, _I32, _P],
+    "ntlb_fp8_persistent_quant": [_P, _I32, _I64, _I64, _P, _P, _P, _P],
+    "ntlb_fp8_persistent_dequant": [_P, _P, _I64, _I64, _P, _I32, _P],
+    "ntlb_gemm_nf4": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
 }
 
 _lib = None

@@ -1,0 +1,163 @@
+"""MoE side of the low-bit path: comm-quant of the dispatch payload and the
+grouped per-expert GEMM, mirroring src/models/moe.py of nano-train.
+
+comm_quant_dequant() is the drop-in for _comm_quant_dequant (moe.py:79-143):
+same arguments, same granularities (one scale per tensor; per column;
+per 128-column strip over all rows for both 'tile_1x128' and
+'block_128x128'), the same before-division scale rule (moe.py:94-98), the int
+grid with qmax = 2^(bits-1)-1, and the same straight-through estimator
+`tensor + (dq - tensor).detach()` (moe.py:107-143).  Stochastic rounding draws
+its bits from the Philox contract of the C-ABI instead of torch.rand_like
+(moe.py:72-76).
+
+comm_quant() / comm_dequant() are the wire format a real expert-parallel
+all-to-all would carry (codes plus per-row 1x128 scales, e4m3 or int grid);
+the reference has no counterpart (it all-to-alls the dequantized bf16 tensor,
+moe.py:787-793).
+
+sort_by_expert() builds the token-offset table and grouped_linear() runs one
+Linear per expert over the rows sorted by expert (moe.py:888-962 loops over
+experts in Python instead).
+"""
+
+from __future__ import annotations
+
+import itertools
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from . import ops
+from .ops import QTensor
+
+_comm_calls = itertools.count()
+
+
+def _comm_seed_offset(seed: Optional[int], offset: Optional[int]):
+    if seed is None:
+        seed = torch.initial_seed() & 0xFFFFFFFFFFFFFFFF
+    if offset is None:
+        offset = (1 << 40) + next(_comm_calls)  # a stream of its own, apart from the Linear backends
+    return seed, offset
+
+
+def comm_quant_dequant(
+    tensor: torch.Tensor,
+    *,
+    granularity: str,
+    rounding_mode: str,
+    bits: int = 8,
+    seed: Optional[int] = None,
+    offset: Optional[int] = None,
+) -> torch.Tensor:
+    """Fake quant-dequant of a comm payload preserving autograd (moe.py:79-143)."""
+    if tensor.numel() == 0:
+        return tensor
+    if tensor.device.type != "cuda":
+        raise RuntimeError("comm_quant_dequant runs on a ROCm device only; there is no CPU path")
+    seed, offset = _comm_seed_offset(seed, offset)
+    x2 = tensor.reshape(-1, tensor.shape[-1]) if tensor.dim() >= 2 else tensor.reshape(1, -1)
+    R, K = x2.shape
+    if granularity in ("tile_1x128", "block_128x128") and tensor.dim() >= 1:
+        gr, gc = R, 128  # one scale per 128-column strip over all rows (moe.py:123-140)
+    elif granularity == "channel" and tensor.dim() >= 2:
+        gr, gc = R, 1  # one scale per column (moe.py:112-121)
+    else:
+        gr, gc = R, K  # tensor, 1-D channel, or anything else (moe.py:107-110, :141-143)
+    rounding = "stochastic" if rounding_mode == "stochastic" else "nearest"
+    _, _, dq, _ = ops.quant_grouped(
+        x2.detach(), gr, gc, fmt="int_grid", bits=bits, rounding=rounding, seed=seed, offset=offset,
+        scale_rule=_lib.SCALE_BEFORE_DIVIDE, want_dq=True, dq_dtype=tensor.dtype)
+    dq = dq.reshape(tensor.shape)
+    return tensor + (dq - tensor).detach()
+
+
+@dataclass
+class CommPayload:
+    """Quantized dispatch payload: codes [rows, Kp] plus 1x128 scales."""
+
+    q: QTensor
+    shape: tuple
+    dtype: torch.dtype
+
+    @property
+    def nbytes(self) -> int:
+        return self.q.codes.numel() + self.q.scales.numel() * 4
+
+
+def comm_quant(
+    tensor: torch.Tensor,
+    *,
+    fmt: str = "e4m3",
+    rounding_mode: str = "nearest",
+    bits: int = 8,
+    seed: Optional[int] = None,
+    offset: Optional[int] = None,
+) -> CommPayload:
+    """Quantize a payload [..., H] per 1x128 tile of each row (the DeepSeek-V3 wire format)."""
+    seed, offset = _comm_seed_offset(seed, offset)
+    rounding = "stochastic" if rounding_mode == "stochastic" else "nearest"
+    q = ops.quant_tile_1x128(tensor, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
+                             tile_major_scales=False)
+    return CommPayload(q, tuple(tensor.shape), tensor.dtype)
+
+
+def comm_dequant(payload: CommPayload, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """The receiver's dequantize back to the token dtype."""
+    out = ops.dequant(payload.q, out_dtype=dtype or payload.dtype, r_shift=0, c_shift=7)
+    return out.reshape(payload.shape)
+
+
+def sort_by_expert(expert_ids: torch.Tensor, n_experts: int):
+    """Token-offset table for top-k routing.
+
+    expert_ids [T, k] int -> (order [T*k] int64 indices into the flattened
+    (token, slot) pairs sorted by expert, stable; token_index [T*k] the source
+    token of each sorted row; offsets int32 [E+1])."""
+    flat = expert_ids.reshape(-1).to(torch.int64)
+    order = torch.sort(flat, stable=True).indices
+    counts = torch.bincount(flat, minlength=n_experts)
+    offsets = torch.zeros(n_experts + 1, dtype=torch.int32, device=expert_ids.device)
+    offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
+    token_index = order // expert_ids.shape[1]
+    return order, token_index, offsets
+
+
+def quantize_expert_weights(w: torch.Tensor, *, fmt: str = "e4m3", bits: int = 8, rounding: str = "nearest",
+                            seed: int = 0, offset: int = 0):
+    """128x128 block codes of stacked expert weights [E, N, K] (N % 128 == 0,
+    so no block straddles two experts): codes [E, N, Kp], scales [E, N/128, Kp/128]."""
+    E, N, K = w.shape
+    if N % 128:
+        raise ValueError("expert weights need N % 128 == 0 for per-expert 128x128 blocks")
+    q, _ = ops.quant_block_128x128(w.reshape(E * N, K), fmt=fmt, bits=bits, rounding=rounding, seed=seed,
+                                   offset=offset, want_nan_rows=True)
+    codes = q.codes.reshape(E, N, -1)
+    scales = q.scales.reshape(E, N // 128, -1)
+    return codes, scales, q.nan_rows.reshape(E, N)
+
+
+def grouped_linear(
+    x_sorted: torch.Tensor,
+    offsets: torch.Tensor,
+    w_codes: torch.Tensor,
+    w_scales: torch.Tensor,
+    *,
+    fmt: str = "e4m3",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    out_dtype: Optional[torch.dtype] = None,
+    w_nan_rows: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Y[rows of expert e] = X_dq[rows] @ W_dq[e]^T for rows sorted by expert.
+
+    X is quantized per 1x128 tile over all rows at once; the experts' codes
+    come from quantize_expert_weights()."""
+    qx = ops.quant_tile_1x128(x_sorted, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
+                              want_nan_rows=True)
+    return ops.gemm_grouped_blockscaled(qx, w_codes, w_scales, offsets, N=w_codes.shape[1],
+                                        out_dtype=out_dtype or x_sorted.dtype, b_nan_rows=w_nan_rows)

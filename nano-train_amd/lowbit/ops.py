@@ -285,3 +285,65 @@ def gemm_blockscaled(
         _dtype_code(out.dtype), out.stride(0), _ptr(a.nan_rows), _ptr(b.nan_rows), _stream(),
     )
     return out
+
+
+def dequant(q: QTensor, *, out_dtype: torch.dtype = torch.bfloat16, r_shift: Optional[int] = None,
+            c_shift: int = 7) -> torch.Tensor:
+    """value(code) * scale for a QTensor (codes [rows, >=K]) -> [rows, K]."""
+    _require_device(q.codes)
+    rows, K = q.rows, q.K
+    out = torch.empty((rows, K), dtype=out_dtype, device=q.codes.device)
+    call("ntlb_dequant", q.grid, q.codes.data_ptr(), q.codes.stride(0), q.scales.data_ptr(), q.s_row, q.s_col,
+         q.shift if r_shift is None else r_shift, c_shift, rows, K, out.data_ptr(), _dtype_code(out_dtype),
+         out.stride(0), _stream())
+    return out
+
+
+def dequant_raw(grid: int, codes: torch.Tensor, scales: torch.Tensor, *, K: int, s_row: int, s_col: int,
+                r_shift: int, c_shift: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """ntlb_dequant over explicit scale indexing (strips, channels, tensors)."""
+    _require_device(codes, scales)
+    rows = codes.shape[0]
+    out = torch.empty((rows, K), dtype=out_dtype, device=codes.device)
+    call("ntlb_dequant", grid, codes.data_ptr(), codes.stride(0), scales.data_ptr(), s_row, s_col, r_shift, c_shift,
+         rows, K, out.data_ptr(), _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def gemm_grouped_blockscaled(
+    a: QTensor,
+    b_codes: torch.Tensor,
+    b_scales: torch.Tensor,
+    offsets: torch.Tensor,
+    *,
+    N: int,
+    out_dtype: torch.dtype = torch.bfloat16,
+    b_nan_rows: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Per-expert GEMM over rows sorted by expert.
+
+    a        QTensor of the sorted rows [M_total, K] (1x128 tiles)
+    b_codes  [E, N, Kp] uint8 weight codes (128x128 blocks)
+    b_scales [E, ceil(N/128), Kp/128] fp32
+    offsets  int32 [E+1] on the device, offsets[E] == M_total
+    """
+    _require_device(a.codes, b_codes, b_scales, offsets)
+    if offsets.dtype != torch.int32:
+        raise TypeError("offsets must be int32")
+    E = b_codes.shape[0]
+    if offsets.numel() != E + 1:
+        raise ValueError(f"offsets has {offsets.numel()} entries for {E} experts")
+    if b_codes.shape[1] != N or b_codes.shape[2] < a.Kp:
+        raise ValueError(f"expert codes {tuple(b_codes.shape)} do not match N={N}, Kp={a.Kp}")
+    b_codes = b_codes.contiguous()
+    b_scales = b_scales.contiguous()
+    M = a.rows
+    out = torch.empty((M, N), dtype=out_dtype, device=a.codes.device)
+    nb, tb = b_scales.shape[1], b_scales.shape[2]
+    call(
+        "ntlb_gemm_grouped_blockscaled", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
+        a.s_col, a.shift, b_codes.data_ptr(), b_codes.stride(1), b_codes.stride(0), b_scales.data_ptr(), tb, 1, 7,
+        nb * tb, offsets.data_ptr(), E, M, N, a.Kp, out.data_ptr(), _dtype_code(out_dtype), out.stride(0),
+        _ptr(a.nan_rows), _ptr(b_nan_rows), _stream(),
+    )
+    return out

@@ -1,0 +1,177 @@
+"""Persistent low-bit weights on the MI355X kernels.
+
+Drop-ins for the persistent-parameter helpers of nano-train's src/layers.py,
+with the same signatures, buffer dtypes and scale shapes (so checkpoints keep
+the `_persistent_fp4_codes` uint8 packed nibbles, `_persistent_fp8_weight`
+float8_e4m3fn values and `_persistent_scale` fp32 layout, layers.py:235-246):
+
+  nf4_codebook                  layers.py:60-83
+  quantize_nf4_persistent       layers.py:156-169 (+ _pack_nibbles :130-139)
+  dequantize_nf4_persistent     layers.py:172-184 (+ _unpack_nibbles :142-153)
+  quantize_fp8_persistent       layers.py:104-117
+  dequantize_fp8_persistent     layers.py:120-127
+
+plus the BASELINE config 5 formats that have no reference function: NF4 with
+one scale per 64 elements, MXFP4 (e2m1 + e8m0 per 32), and the GEMMs with the
+dequantization fused into the weight-tile prologue (linear_nf4, linear_mxfp4).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import ops
+from ._lib import call
+
+NF4_CODEBOOK = (
+    -1.0, -0.6961928, -0.52507305, -0.3949175, -0.28444138, -0.18477343, -0.09105004, 0.0,
+    0.0795803, 0.1609302, 0.2461123, 0.33791524, 0.44070983, 0.562617, 0.72295684, 1.0,
+)
+
+
+def nf4_codebook(device: torch.device) -> torch.Tensor:
+    return torch.tensor(NF4_CODEBOOK, dtype=torch.float32, device=device)
+
+
+def _block_and_scale_shape(tensor: torch.Tensor, granularity: str):
+    """Scale grouping of layers.py:86-101: per_channel reduces over dims 1..,
+    per_tensor over everything (and so does per_channel on a 1-D tensor)."""
+    if granularity == "per_channel" and tensor.dim() > 1:
+        block = tensor.numel() // tensor.shape[0]
+        shape = (tensor.shape[0],) + (1,) * (tensor.dim() - 1)
+    else:
+        block = tensor.numel()
+        shape = ()
+    return max(block, 1), shape
+
+
+def _flat(t: torch.Tensor) -> torch.Tensor:
+    ops._require_device(t)
+    return t.detach().reshape(-1) if t.is_contiguous() else t.detach().contiguous().reshape(-1)
+
+
+def quantize_nf4_blocks(tensor: torch.Tensor, block: int):
+    """NF4 codes with one scale per `block` consecutive elements: (packed, scales[ceil(n/block)])."""
+    flat = _flat(tensor)
+    n = flat.numel()
+    nb = ops.cdiv(n, block) if n else 0
+    packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device=flat.device)
+    scales = torch.empty(nb, dtype=torch.float32, device=flat.device)
+    ws = torch.zeros(max(nb, 1), dtype=torch.int32, device=flat.device)
+    call("ntlb_nf4_quant", flat.data_ptr(), ops._dtype_code(flat.dtype), n, block, ws.data_ptr(), packed.data_ptr(),
+         scales.data_ptr(), ops._stream())
+    return packed, scales
+
+
+def quantize_nf4_persistent(tensor: torch.Tensor, *, granularity: str):
+    """(packed codes, scale) exactly as _quantize_nf4_persistent (layers.py:156-169)."""
+    block, shape = _block_and_scale_shape(tensor, granularity)
+    packed, scales = quantize_nf4_blocks(tensor, block)
+    return packed, scales.reshape(shape)
+
+
+def dequantize_nf4_blocks(packed: torch.Tensor, scales: torch.Tensor, *, num_values: int, block: int,
+                          target_dtype: torch.dtype) -> torch.Tensor:
+    ops._require_device(packed, scales)
+    out = torch.empty(num_values, dtype=target_dtype, device=packed.device)
+    sc = scales.reshape(-1).contiguous().float()
+    call("ntlb_nf4_dequant", packed.data_ptr(), sc.data_ptr(), num_values, block, out.data_ptr(),
+         ops._dtype_code(target_dtype), ops._stream())
+    return out
+
+
+def dequantize_nf4_persistent(packed_codes: torch.Tensor, scale: torch.Tensor, *, num_values: int,
+                              target_shape: torch.Size, target_dtype: torch.dtype) -> torch.Tensor:
+    """_dequantize_nf4_persistent (layers.py:172-184)."""
+    nscale = max(scale.numel(), 1)
+    block = max(num_values // nscale, 1) if num_values else 1
+    out = dequantize_nf4_blocks(packed_codes, scale, num_values=num_values, block=block, target_dtype=target_dtype)
+    return out.reshape(target_shape)
+
+
+def quantize_fp8_persistent(tensor: torch.Tensor, *, granularity: str):
+    """(float8_e4m3fn values, scale) exactly as _quantize_fp8_persistent (layers.py:104-117)."""
+    block, shape = _block_and_scale_shape(tensor, granularity)
+    flat = _flat(tensor)
+    n = flat.numel()
+    nb = ops.cdiv(n, block) if n else 0
+    codes = torch.empty(n, dtype=torch.uint8, device=flat.device)
+    scales = torch.empty(nb, dtype=torch.float32, device=flat.device)
+    ws = torch.zeros(max(nb, 1), dtype=torch.int32, device=flat.device)
+    call("ntlb_fp8_persistent_quant", flat.data_ptr(), ops._dtype_code(flat.dtype), n, block, ws.data_ptr(),
+         codes.data_ptr(), scales.data_ptr(), ops._stream())
+    return codes.view(torch.float8_e4m3fn).reshape(tensor.shape), scales.reshape(shape)
+
+
+def dequantize_fp8_persistent(fp8_values: torch.Tensor, scale: torch.Tensor, *,
+                              target_dtype: torch.dtype) -> torch.Tensor:
+    """_dequantize_fp8_persistent (layers.py:120-127)."""
+    ops._require_device(fp8_values, scale)
+    codes = fp8_values.contiguous().view(torch.uint8).reshape(-1)
+    n = codes.numel()
+    nscale = max(scale.numel(), 1)
+    block = max(n // nscale, 1) if n else 1
+    out = torch.empty(n, dtype=target_dtype, device=codes.device)
+    sc = scale.reshape(-1).contiguous().float()
+    call("ntlb_fp8_persistent_dequant", codes.data_ptr(), sc.data_ptr(), n, block, out.data_ptr(),
+         ops._dtype_code(target_dtype), ops._stream())
+    return out.reshape(fp8_values.shape)
+
+
+def quantize_mxfp4(tensor: torch.Tensor):
+    """MXFP4 codes: (packed [ceil(n/2)] uint8, e8m0 scales [ceil(n/32)] uint8)."""
+    flat = _flat(tensor)
+    n = flat.numel()
+    packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device=flat.device)
+    scales = torch.empty(ops.cdiv(n, 32), dtype=torch.uint8, device=flat.device)
+    call("ntlb_mxfp4_quant", flat.data_ptr(), ops._dtype_code(flat.dtype), n, packed.data_ptr(), scales.data_ptr(),
+         ops._stream())
+    return packed, scales
+
+
+def dequantize_mxfp4(packed: torch.Tensor, scales: torch.Tensor, *, num_values: int,
+                     target_dtype: torch.dtype) -> torch.Tensor:
+    ops._require_device(packed, scales)
+    out = torch.empty(num_values, dtype=target_dtype, device=packed.device)
+    call("ntlb_mxfp4_dequant", packed.data_ptr(), scales.data_ptr(), num_values, out.data_ptr(),
+         ops._dtype_code(target_dtype), ops._stream())
+    return out
+
+
+def _x2(x: torch.Tensor, K: int) -> torch.Tensor:
+    ops._require_device(x)
+    if x.dtype != torch.bfloat16:
+        raise TypeError("the fused low-bit GEMMs take bf16 activations")
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
+def linear_nf4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, out_features: int, block: int,
+               out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Y = x @ deq(W)^T with W [out_features, K] in NF4, dequantized inside the GEMM.
+
+    block: elements per scale (K for per_channel, 0 or numel for per_tensor, 64...)."""
+    K = x.shape[-1]
+    x2 = _x2(x, K)
+    M, N = x2.shape[0], out_features
+    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x.device)
+    blk = 0 if block >= N * K else block
+    call("ntlb_gemm_nf4", x2.data_ptr(), x2.stride(0), packed.data_ptr(), scales.reshape(-1).contiguous().data_ptr(),
+         blk, M, N, K, y.data_ptr(), ops._dtype_code(y.dtype), y.stride(0), ops._stream())
+    return y.reshape(*x.shape[:-1], N)
+
+
+def linear_mxfp4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, out_features: int,
+                 out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Y = x @ deq(W)^T with W [out_features, K] in MXFP4, dequantized inside the GEMM."""
+    K = x.shape[-1]
+    x2 = _x2(x, K)
+    M, N = x2.shape[0], out_features
+    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x.device)
+    call("ntlb_gemm_mxfp4", x2.data_ptr(), x2.stride(0), packed.data_ptr(), scales.data_ptr(), M, N, K, y.data_ptr(),
+         ops._dtype_code(y.dtype), y.stride(0), ops._stream())
+    return y.reshape(*x.shape[:-1], N)

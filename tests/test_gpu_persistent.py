@@ -1,0 +1,133 @@
+"""GPU parity of the persistent low-bit weights: NF4 (layers.py:60-184),
+persistent FP8 (layers.py:104-127), MXFP4, and the dequant-fused GEMMs.
+Codes and scales bit-exact against the oracle; GEMMs within 1e-3 relative
+Frobenius of the float64 matmul over the bf16-rounded dequantized weight."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import assert_bits_equal, rel_fro_bf16, seeded, to_np32
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape", [(64, 128), (129, 257), (7,), (33, 64)])
+@pytest.mark.parametrize("granularity", ["per_channel", "per_tensor"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_nf4_persistent_parity(gpu_device, shape, granularity, dtype):
+    from lowbit import persistent as P
+
+    w = seeded(shape, seed=20260501, std=0.02, dtype=dtype).to(gpu_device)
+    packed, scale = P.quantize_nf4_persistent(w, granularity=granularity)
+    torch.cuda.synchronize()
+    block = (w.numel() // shape[0]) if (granularity == "per_channel" and len(shape) > 1) else w.numel()
+    p_ref, s_ref = O.nf4_quant(to_np32(w), block)
+    assert packed.dtype == torch.uint8 and packed.numel() == (w.numel() + 1) // 2
+    assert_bits_equal(packed.cpu().numpy(), p_ref, "nf4 packed")
+    assert_bits_equal(scale.reshape(-1).cpu().numpy(), s_ref, "nf4 scale")
+    expect_shape = (shape[0],) + (1,) * (len(shape) - 1) if (granularity == "per_channel" and len(shape) > 1) else ()
+    assert tuple(scale.shape) == expect_shape
+    deq = P.dequantize_nf4_persistent(packed, scale, num_values=w.numel(), target_shape=w.shape, target_dtype=dtype)
+    d_ref = O.nf4_dequant(p_ref, s_ref, w.numel(), block)
+    assert_bits_equal(to_np32(deq).reshape(-1), torch.from_numpy(d_ref).to(dtype).float().numpy(), "nf4 dequant")
+
+
+def test_nf4_special_values_and_ties(gpu_device):
+    from lowbit import persistent as P
+
+    cb = O.NF4_CODEBOOK
+    mids = [(cb[i] + cb[i + 1]) / np.float32(2) for i in range(15)]
+    w = torch.tensor([1.0] + mids + [float("nan"), 0.0, -0.0, 1e-40], dtype=torch.float32).to(gpu_device)
+    packed, scale = P.quantize_nf4_persistent(w, granularity="per_tensor")
+    p_ref, s_ref = O.nf4_quant(to_np32(w), w.numel())
+    assert_bits_equal(packed.cpu().numpy(), p_ref, "nf4 packed")
+    assert_bits_equal(scale.reshape(-1).cpu().numpy(), s_ref, "nf4 scale")
+
+
+@pytest.mark.parametrize("shape", [(64, 128), (129, 256), (8, 96)])
+@pytest.mark.parametrize("granularity", ["per_channel", "per_tensor"])
+def test_fp8_persistent_parity(gpu_device, shape, granularity):
+    from lowbit import persistent as P
+
+    w = seeded(shape, seed=20260502, std=0.02, dtype=torch.bfloat16).to(gpu_device)
+    w[0, 0] = float("inf") if shape[0] > 8 else w[0, 0]
+    vals, scale = P.quantize_fp8_persistent(w, granularity=granularity)
+    torch.cuda.synchronize()
+    block = shape[1] if granularity == "per_channel" else w.numel()
+    c_ref, s_ref = O.fp8_persistent_quant(to_np32(w), block)
+    assert vals.dtype == torch.float8_e4m3fn
+    assert_bits_equal(vals.view(torch.uint8).reshape(-1).cpu().numpy(), c_ref, "fp8 codes")
+    assert_bits_equal(scale.reshape(-1).cpu().numpy(), s_ref, "fp8 scale")
+    deq = P.dequantize_fp8_persistent(vals, scale, target_dtype=torch.bfloat16)
+    ref = (torch.from_numpy(c_ref).view(torch.float8_e4m3fn).float() * torch.from_numpy(np.repeat(s_ref, block))
+           ).to(torch.bfloat16)
+    assert_bits_equal(to_np32(deq).reshape(-1), ref.float().numpy(), "fp8 dequant")
+
+
+@pytest.mark.parametrize("n", [64, 1000, 32 * 7 + 3])
+def test_mxfp4_parity(gpu_device, n):
+    from lowbit import persistent as P
+
+    w = seeded((n,), seed=20260503, std=0.02, dtype=torch.float32).to(gpu_device)
+    w[5] = 0.0
+    if n > 100:
+        w[40:72] = 0.0  # an all-zero block
+        w[80] = float("nan")
+    packed, scales = P.quantize_mxfp4(w)
+    p_ref, s_ref = O.mxfp4_quant(to_np32(w))
+    assert_bits_equal(scales.cpu().numpy(), s_ref, "e8m0 scales")
+    assert_bits_equal(packed.cpu().numpy(), p_ref, "e2m1 codes")
+    d = P.dequantize_mxfp4(packed, scales, num_values=n, target_dtype=torch.float32)
+    assert_bits_equal(to_np32(d), O.mxfp4_dequant(p_ref, s_ref, n), "mxfp4 dequant")
+
+
+@pytest.mark.parametrize("M,N,K,block", [(256, 256, 256, 64), (100, 300, 512, 64), (512, 384, 1024, 1024),
+                                         (64, 128, 128, 0)])
+def test_nf4_fused_gemm(gpu_device, M, N, K, block):
+    from lowbit import persistent as P
+
+    x = seeded((M, K), seed=20260504).to(gpu_device)
+    w = seeded((N, K), seed=20260505, std=0.02).to(gpu_device)
+    qb = block if block else N * K
+    packed, scales = P.quantize_nf4_blocks(w, qb)
+    y = P.linear_nf4(x, packed, scales, out_features=N, block=qb)
+    torch.cuda.synchronize()
+    p_ref, s_ref = O.nf4_quant(to_np32(w), qb)
+    wdq = O.round_bf16(O.nf4_dequant(p_ref, s_ref, N * K, qb)).reshape(N, K)  # weight dtype bf16 (layers.py:184)
+    assert rel_fro_bf16(y, O.gemm_ref(to_np32(x), wdq)) <= 1e-3
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (130, 200, 320), (512, 512, 2048)])
+def test_mxfp4_fused_gemm(gpu_device, M, N, K):
+    from lowbit import persistent as P
+
+    x = seeded((M, K), seed=20260506).to(gpu_device)
+    w = seeded((N, K), seed=20260507, std=0.02).to(gpu_device)
+    packed, scales = P.quantize_mxfp4(w)
+    y = P.linear_mxfp4(x, packed, scales, out_features=N)
+    torch.cuda.synchronize()
+    p_ref, s_ref = O.mxfp4_quant(to_np32(w))
+    wdq = O.round_bf16(O.mxfp4_dequant(p_ref, s_ref, N * K)).reshape(N, K)
+    assert rel_fro_bf16(y, O.gemm_ref(to_np32(x), wdq)) <= 1e-3
+
+
+def test_c5_nf4_fused_gemm_full_size_sampled(gpu_device):
+    """W [14336, 4096] NF4 (64-element blocks), X [4096, 4096]."""
+    from lowbit import persistent as P, workloads
+
+    x, w = workloads.c5_inputs(device="cpu")
+    xg, wg = x.to(gpu_device), w.to(gpu_device)
+    packed, scales = P.quantize_nf4_blocks(wg, 64)
+    y = P.linear_nf4(xg, packed, scales, out_features=14336, block=64)
+    torch.cuda.synchronize()
+    p_ref, s_ref = O.nf4_quant(w.float().numpy(), 64)
+    assert_bits_equal(packed.cpu().numpy(), p_ref, "c5 nf4 codes")
+    rows = np.random.default_rng(0).choice(4096, 32, replace=False)
+    cols = np.random.default_rng(1).choice(14336, 256, replace=False)
+    wdq = O.round_bf16(O.nf4_dequant(p_ref, s_ref, 14336 * 4096, 64)).reshape(14336, 4096)
+    ref = O.gemm_ref(x.float().numpy()[rows], wdq[cols])
+    assert rel_fro_bf16(y[rows][:, cols], ref) <= 1e-3
