@@ -43,7 +43,114 @@ def parse_args():
     p.add_argument("--cpu-sample-rows", type=int, default=1024)
     p.add_argument("--calib-copy", action="store_true",
                    help="also launch a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
+    p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                   help="c2 (default) is the headline; c1/c3/c4/c5 measure the other BASELINE configurations")
     return p.parse_args()
+
+
+def _time_ms(fn, n: int, warmup: int, stream) -> float:
+    import torch
+
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev[0].record(stream)
+    for i in range(n):
+        fn(warmup + i)
+    ev[1].record(stream)
+    torch.cuda.synchronize()
+    return ev[0].elapsed_time(ev[1]) / n
+
+
+def other_config(args) -> dict:
+    """One line for BASELINE configs 1, 3, 4, 5 (kernel times by HIP events)."""
+    import torch
+
+    from lowbit import moe, ops, persistent, workloads
+
+    dev = torch.device("cuda", 0)
+    st = torch.cuda.current_stream()
+    fmt = args.format
+    res = {"metric": f"{args.config} throughput", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "data": "synthetic (seeded)",
+           "cpu_baseline": None}
+    if args.config == "c1":
+        x, w = workloads.c1_inputs(device="cpu")
+        x, w = x.to(dev), w.to(dev)
+        step = lambda i: ops.gemm_blockscaled(ops.quant_tile_1x128(x, fmt=fmt), ops.quant_block_128x128(w, fmt=fmt)[0])
+        ms = _time_ms(step, args.steps, args.warmup, st)
+        res.update(value=round(2 * 512 * 1024 * 1024 / (ms * 1e-3) / 1e12, 3), unit="TFLOP/s",
+                   ms_per_step=round(ms, 4), dtype="fp8_e4m3" if fmt == "e4m3" else "int8",
+                   config={"workload": "c1 small emulated-FP8 Linear forward (latency-bound)", "M": 512, "N": 1024,
+                           "K": 1024})
+        return res
+    if args.config == "c3":
+        x, w = workloads.c2_inputs(device="cpu")
+        dy = workloads.c3_grad(device="cpu")
+        x, w, dy = x.to(dev), w.to(dev), dy.to(dev)
+        M, K = x.shape
+        N = w.shape[0]
+        qx_t = ops.quant_tile_128x1_t(x, fmt=fmt)
+        _, qw_t = ops.quant_block_128x128(w, fmt=fmt, want_transposed=True)
+        t = {}
+        t["dy_1x128_us"] = _time_ms(lambda i: ops.quant_tile_1x128(dy, fmt=fmt), args.steps, args.warmup, st) * 1e3
+        t["dy_128x1_us"] = _time_ms(lambda i: ops.quant_tile_128x1_t(dy, fmt=fmt), args.steps, args.warmup, st) * 1e3
+        qdy = ops.quant_tile_1x128(dy, fmt=fmt)
+        qdy_t = ops.quant_tile_128x1_t(dy, fmt=fmt)
+        dg = _time_ms(lambda i: ops.gemm_blockscaled(qdy, qw_t), args.steps, args.warmup, st)
+        wg = _time_ms(lambda i: ops.gemm_blockscaled(qdy_t, qx_t), args.steps, args.warmup, st)
+        fl = 2.0 * M * N * K
+        res.update(value=round(2 * fl / ((dg + wg) * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(dg + wg, 4),
+                   dtype="fp8_e4m3" if fmt == "e4m3" else "int8",
+                   config={"workload": "c3 backward GEMMs (dgrad + wgrad) of the c2 layer, fp8 recipe", "M": M,
+                           "N": N, "K": K},
+                   dgrad_tflops=round(fl / (dg * 1e-3) / 1e12, 2), wgrad_tflops=round(fl / (wg * 1e-3) / 1e12, 2),
+                   quantizers={k: round(v, 2) for k, v in t.items()},
+                   dy_1x128_GBs=round((M * N * 3 + M * (N // 128) * 4) / t["dy_1x128_us"] / 1e3, 1),
+                   dy_128x1_GBs=round((M * N * 3 + N * (M // 128) * 4) / t["dy_128x1_us"] / 1e3, 1))
+        return res
+    if args.config == "c4":
+        tokens, routing, w_up, w_down = workloads.c4_inputs(device="cpu")
+        tokens, routing = tokens.to(dev), routing.to(dev)
+        w_up, w_down = w_up.to(dev), w_down.to(dev)
+        order, tok_idx, offsets = moe.sort_by_expert(routing, 32)
+        xs = tokens[tok_idx].contiguous()
+        R, H = xs.shape
+        uc, us_, _ = moe.quantize_expert_weights(w_up, fmt=fmt)
+        dc, ds_, _ = moe.quantize_expert_weights(w_down, fmt=fmt)
+        comm_us = _time_ms(lambda i: moe.comm_quant(xs, fmt=fmt), args.steps, args.warmup, st) * 1e3
+        h = moe.grouped_linear(xs, offsets, uc, us_, fmt=fmt)
+        up = _time_ms(lambda i: moe.grouped_linear(xs, offsets, uc, us_, fmt=fmt), args.steps, args.warmup, st)
+        down = _time_ms(lambda i: moe.grouped_linear(h, offsets, dc, ds_, fmt=fmt), args.steps, args.warmup, st)
+        fl = 2.0 * R * H * 2048
+        comm_bytes = R * H * 3 + R * (H // 128) * 4
+        res.update(value=round(2 * fl / ((up + down) * 1e-3) / 1e12, 2), unit="TFLOP/s",
+                   ms_per_step=round(up + down, 4), dtype="fp8_e4m3" if fmt == "e4m3" else "int8",
+                   config={"workload": "c4 MoE local experts: 1x128 payload comm-quant + grouped up and down GEMMs",
+                           "rows": R, "hidden": H, "inter": 2048, "experts": 32, "top_k": 8},
+                   up_tflops=round(fl / (up * 1e-3) / 1e12, 2), down_tflops=round(fl / (down * 1e-3) / 1e12, 2),
+                   comm_quant_us=round(comm_us, 2), comm_quant_GBs=round(comm_bytes / comm_us / 1e3, 1),
+                   note="up and down include the 1x128 quantization of their input rows")
+        return res
+    # c5
+    x, w = workloads.c5_inputs(device="cpu")
+    x, w = x.to(dev), w.to(dev)
+    M, K = x.shape
+    N = w.shape[0]
+    pk, sc = persistent.quantize_nf4_blocks(w, 64)
+    mp, ms8 = persistent.quantize_mxfp4(w)
+    nf4 = _time_ms(lambda i: persistent.linear_nf4(x, pk, sc, out_features=N, block=64), args.steps, args.warmup, st)
+    mx = _time_ms(lambda i: persistent.linear_mxfp4(x, mp, ms8, out_features=N), args.steps, args.warmup, st)
+    bf = _time_ms(lambda i: torch.matmul(x, w.t()), args.steps, args.warmup, st)
+    fl = 2.0 * M * N * K
+    res.update(value=round(fl / (nf4 * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(nf4, 4), dtype="bf16",
+               config={"workload": "c5 NF4 (64-element blocks) dequant-fused GEMM", "M": M, "N": N, "K": K},
+               roofline={"bound": "mfma", "achieved": round(fl / (nf4 * 1e-3) / 1e12, 2), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(fl / (nf4 * 1e-3) / 1e12 / 2500.0, 4), "traffic": None},
+               mxfp4_tflops=round(fl / (mx * 1e-3) / 1e12, 2),
+               torch_bf16_matmul_tflops=round(fl / (bf * 1e-3) / 1e12, 2))
+    return res
 
 
 def cpu_baseline(fmt: str, rounding: str, rows: int):
@@ -106,6 +213,9 @@ def main():
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.config != "c2":
+        print(json.dumps(other_config(args)))
+        return
     shp = workloads.SHAPES[2]
     M, N, K = shp["M"], shp["N"], shp["K"]
 

@@ -1,0 +1,323 @@
+"""Low-bit-capable Linear layers on the MI355X kernels.
+
+Mirrors the Linear family of nano-train's src/layers.py (Linear :465-632,
+ColumnParallelLinear :1235-1360, RowParallelLinear :1363-1496) and the
+_LowBitPrecisionLinearMixin (:216-458): the same constructor arguments, the
+same `_persistent_*` state_dict buffers with the same dtypes, the same
+forward order (persistent-weight straight-through estimator -> low-bit
+backend -> per-module compute dtype -> F.linear), the same error messages,
+and tolerance of legacy checkpoints that lack the persistent buffers.
+
+Persistent NF4/FP8 weights are refreshed and dequantized by the HIP kernels of
+lowbit.persistent.  When a module stores NF4 weights, has no low-bit compute
+backend, and both activation and master weight are bf16, the forward runs the
+dequant-fused GEMM instead of materializing the bf16 weight; its backward is
+the reference's straight-through rule (dX = dY . W_deq, dW = dY^T . X).
+
+One GPU: the tensor-parallel classes accept tp_size == 1 only.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import persistent as P
+from .contracts import LowBitKernelSpec
+from .precision import dtype_alias_to_torch
+
+_PERSISTENT_SUFFIXES = ("_persistent_fp8_weight", "_persistent_fp4_codes", "_persistent_scale", "_persistent_numel")
+
+
+class _NF4FusedLinear(torch.autograd.Function):
+    """Forward: fused NF4 GEMM.  Backward: straight-through to the master weight."""
+
+    @staticmethod
+    def forward(ctx, x, weight, codes, scale, block):
+        N, K = weight.shape
+        y = P.linear_nf4(x, codes, scale, out_features=N, block=block)
+        ctx.save_for_backward(x, codes, scale)
+        ctx.meta = (N, K, block, weight.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, codes, scale = ctx.saved_tensors
+        N, K, block, wdt = ctx.meta
+        dx = dw = None
+        dy2 = dy.reshape(-1, N)
+        with torch.autocast(device_type="cuda", enabled=False):
+            if ctx.needs_input_grad[0]:
+                w_deq = P.dequantize_nf4_blocks(codes, scale, num_values=N * K, block=block,
+                                                target_dtype=wdt).reshape(N, K)
+                dx = torch.matmul(dy2, w_deq.to(dy2.dtype)).reshape(x.shape)
+            if ctx.needs_input_grad[1]:
+                dw = torch.matmul(dy2.t(), x.reshape(-1, K).to(dy2.dtype)).to(wdt)
+        return dx, dw, None, None, None
+
+
+class LowBitLinearMixin:
+    """Per-module low-bit compute and persistent-parameter hooks (layers.py:216-458)."""
+
+    def _init_lowbit_precision_state(self, *, module_path: str, module_type: str, precision_resolver,
+                                     lowbit_capable_type: str, kernel_spec: LowBitKernelSpec) -> None:
+        self._module_precision_state = precision_resolver.resolve_module_init_state(
+            module_path=module_path, module_type=module_type, lowbit_capable_type=lowbit_capable_type,
+            kernel_spec=kernel_spec)
+        dev = self.weight.device
+        self.register_buffer("_persistent_fp8_weight", torch.empty(0, device=dev), persistent=True)
+        self.register_buffer("_persistent_fp4_codes", torch.empty(0, dtype=torch.uint8, device=dev), persistent=True)
+        self.register_buffer("_persistent_scale", torch.empty(0, device=dev), persistent=True)
+        self.register_buffer("_persistent_numel", torch.zeros((), dtype=torch.int64, device=dev), persistent=True)
+        bind = getattr(self._module_precision_state.lowbit_backend, "bind_parameters", None)
+        if callable(bind):
+            bind(self.weight, self.bias)
+
+    # --- assignment views ---------------------------------------------------
+    @property
+    def module_precision_assignment(self):
+        return self._module_precision_state.assignment
+
+    @property
+    def module_path(self) -> str:
+        return str(self._module_precision_state.assignment.module_name)
+
+    @property
+    def master_ownership_mode(self) -> str:
+        return str(getattr(self._module_precision_state, "master_ownership_mode", "module"))
+
+    def _persistent_mode(self) -> str:
+        return str(getattr(self.module_precision_assignment, "persistent_lowbit_mode", "off"))
+
+    def _persistent_granularity(self) -> str:
+        return str(getattr(self.module_precision_assignment, "persistent_scale_granularity", "per_channel"))
+
+    def _compute_lowbit_mode(self) -> Optional[str]:
+        mode = getattr(self.module_precision_assignment, "compute_lowbit_mode", None)
+        return str(mode) if mode is not None and str(mode) in ("fp8", "fp4") else None
+
+    def _compute_dtype_override(self) -> Optional[torch.dtype]:
+        alias = getattr(self.module_precision_assignment, "compute_dtype_override", None)
+        return None if alias is None else dtype_alias_to_torch(str(alias))
+
+    # --- master weight binding (layers.py:269-278) ----------------------------
+    def bind_optimizer_master_weight(self, master_weight: nn.Parameter) -> None:
+        if not isinstance(master_weight, nn.Parameter):
+            raise TypeError("master_weight must be nn.Parameter")
+        if master_weight.shape != self.weight.shape:
+            raise ValueError("optimizer master weight shape mismatch: "
+                             f"expected={tuple(self.weight.shape)} got={tuple(master_weight.shape)}")
+        with torch.no_grad():
+            master_weight.copy_(self.weight.detach().to(device=master_weight.device))
+        self.weight = master_weight
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys, unexpected_keys,
+                              error_msgs) -> None:
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,  # type: ignore
+                                      unexpected_keys, error_msgs)
+        optional = {prefix + s for s in _PERSISTENT_SUFFIXES}
+        missing_keys[:] = [k for k in missing_keys if k not in optional]
+
+    # --- persistent buffers (layers.py:347-407) -------------------------------
+    def _clear_persistent_lowbit_buffers(self) -> None:
+        dev = self.weight.device
+        self._persistent_fp8_weight = torch.empty(0, device=dev)
+        self._persistent_fp4_codes = torch.empty(0, dtype=torch.uint8, device=dev)
+        self._persistent_scale = torch.empty(0, device=dev)
+        self._persistent_numel = torch.zeros((), dtype=torch.int64, device=dev)
+
+    @torch.no_grad()
+    def refresh_persistent_lowbit_params(self) -> None:
+        mode = self._persistent_mode()
+        if mode == "off":
+            self._clear_persistent_lowbit_buffers()
+            return
+        granularity = self._persistent_granularity()
+        if granularity not in ("per_tensor", "per_channel"):
+            raise ValueError(f"Unsupported persistent_scale_granularity={granularity!r} for low-bit persistent params")
+        dev = self.weight.device
+        numel = torch.tensor(int(self.weight.numel()), dtype=torch.int64, device=dev)
+        if mode == "fp8":
+            values, scale = P.quantize_fp8_persistent(self.weight.detach(), granularity=granularity)
+            self._persistent_fp8_weight = values
+            self._persistent_fp4_codes = torch.empty(0, dtype=torch.uint8, device=dev)
+            self._persistent_scale = scale
+            self._persistent_numel = numel
+            return
+        if mode == "fp4":
+            fmt = str(getattr(self.module_precision_assignment, "fp4_persistent_format", "nf4"))
+            if fmt != "nf4":
+                raise ValueError("Only nf4 is supported for FP4 persistent params")
+            packed, scale = P.quantize_nf4_persistent(self.weight.detach(), granularity=granularity)
+            self._persistent_fp4_codes = packed
+            self._persistent_fp8_weight = torch.empty(0, device=dev)
+            self._persistent_scale = scale
+            self._persistent_numel = numel
+            return
+        raise ValueError(f"Unsupported persistent low-bit mode: {mode}")
+
+    def _persistent_weight_ste(self) -> torch.Tensor:
+        """Weight used in forward, with a straight-through bridge to the master (layers.py:409-436)."""
+        mode = self._persistent_mode()
+        if mode == "off":
+            return self.weight
+        if mode == "fp8":
+            if self._persistent_fp8_weight.numel() != self.weight.numel():
+                self.refresh_persistent_lowbit_params()
+            deq = P.dequantize_fp8_persistent(self._persistent_fp8_weight, self._persistent_scale,
+                                              target_dtype=self.weight.dtype)
+        elif mode == "fp4":
+            if int(self._persistent_numel.item()) != int(self.weight.numel()):
+                self.refresh_persistent_lowbit_params()
+            deq = P.dequantize_nf4_persistent(self._persistent_fp4_codes, self._persistent_scale,
+                                              num_values=int(self.weight.numel()), target_shape=self.weight.shape,
+                                              target_dtype=self.weight.dtype)
+        else:
+            raise ValueError(f"Unsupported persistent low-bit mode: {mode}")
+        return self.weight + (deq - self.weight).detach()
+
+    def _fused_nf4_forward(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+        """NF4 persistent weight, no low-bit backend, bf16 everywhere: dequant inside the GEMM."""
+        if (self._persistent_mode() != "fp4" or self._compute_lowbit_mode() is not None
+                or self._compute_dtype_override() is not None or x.dtype != torch.bfloat16
+                or self.weight.dtype != torch.bfloat16 or x.device.type != "cuda" or self.weight.dim() != 2
+                or self.weight.shape[1] % 64):
+            return None
+        if int(self._persistent_numel.item()) != int(self.weight.numel()):
+            self.refresh_persistent_lowbit_params()
+        N, K = self.weight.shape
+        scale = self._persistent_scale
+        block = (N * K) if scale.numel() <= 1 else K
+        return _NF4FusedLinear.apply(x, self.weight, self._persistent_fp4_codes, scale.float(), block)
+
+    def _dispatch_lowbit_linear(self, *, x: torch.Tensor, weight: torch.Tensor,
+                                bias: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
+        mode = self._compute_lowbit_mode()
+        if mode is None:
+            return None
+        backend = self._module_precision_state.lowbit_backend
+        if backend is None:
+            name = self._module_precision_state.assignment.module_name
+            raise RuntimeError(f"Module {self.__class__.__name__} ({name}) requested compute mode {mode} "
+                               "without a bound low-bit backend")
+        return backend.linear(x, weight, bias)
+
+    def _linear_with_dtype_override(self, *, x, weight, bias) -> Optional[torch.Tensor]:
+        dt = self._compute_dtype_override()
+        if dt is None:
+            return None
+        return F.linear(x.to(dt), weight.to(dt), None if bias is None else bias.to(dt))
+
+    def _lowbit_forward(self, x: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+        if bias is None:
+            fused = self._fused_nf4_forward(x)
+            if fused is not None:
+                return fused
+        weight = self._persistent_weight_ste()
+        out = self._dispatch_lowbit_linear(x=x, weight=weight, bias=bias)
+        if out is not None:
+            return out
+        out = self._linear_with_dtype_override(x=x, weight=weight, bias=bias)
+        if out is not None:
+            return out
+        return F.linear(x, weight, bias)
+
+
+class Linear(LowBitLinearMixin, nn.Module):
+    """y = x W^T + b with the low-bit hooks (layers.py:465-632)."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, *, param_dtype: torch.dtype,
+                 param_device: Optional[torch.device], module_path: str, precision_resolver) -> None:
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, dtype=param_dtype, device=param_device))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, dtype=param_dtype, device=param_device))
+        else:
+            self.register_parameter("bias", None)
+        nn.init.normal_(self.weight, std=0.02)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+        self._init_lowbit_precision_state(
+            module_path=module_path, module_type=type(self).__name__, precision_resolver=precision_resolver,
+            lowbit_capable_type="linear",
+            kernel_spec=LowBitKernelSpec(module_type="linear", in_features=in_features, out_features=out_features,
+                                         has_bias=self.bias is not None))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._lowbit_forward(x, self.bias)
+
+
+def _check_tp(tp_size: int) -> None:
+    if tp_size != 1:
+        raise NotImplementedError("this MI355X build runs on one GPU: tensor-parallel layers need tp_size == 1")
+
+
+class ColumnParallelLinear(LowBitLinearMixin, nn.Module):
+    """Output-sharded linear (layers.py:1235-1360); one GPU, so one shard."""
+
+    def __init__(self, in_features: int, out_features: int, tp_rank: int, tp_size: int, bias: bool = True,
+                 tp_group=None, *, param_dtype: torch.dtype, param_device: Optional[torch.device], module_path: str,
+                 precision_resolver) -> None:
+        super().__init__()
+        _check_tp(tp_size)
+        if out_features % tp_size:
+            raise ValueError(f"out_features {out_features} must be divisible by tp_size {tp_size}")
+        self.in_features, self.out_features = in_features, out_features
+        self.tp_rank, self.tp_size, self.tp_group = tp_rank, tp_size, tp_group
+        self.shard_size = out_features // tp_size
+        self.weight = nn.Parameter(torch.empty(self.shard_size, in_features, dtype=param_dtype, device=param_device))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(self.shard_size, dtype=param_dtype, device=param_device))
+        else:
+            self.register_parameter("bias", None)
+        nn.init.normal_(self.weight, std=0.02)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+        self._init_lowbit_precision_state(
+            module_path=module_path, module_type=type(self).__name__, precision_resolver=precision_resolver,
+            lowbit_capable_type="column_parallel_linear",
+            kernel_spec=LowBitKernelSpec(module_type="column_parallel_linear", in_features=in_features,
+                                         out_features=self.shard_size, has_bias=self.bias is not None))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._lowbit_forward(x, self.bias)
+
+
+class RowParallelLinear(LowBitLinearMixin, nn.Module):
+    """Input-sharded linear (layers.py:1363-1496): the backend sees bias=None and
+    the bias is added after the (here trivial) reduction."""
+
+    def __init__(self, in_features: int, out_features: int, tp_rank: int, tp_size: int, bias: bool = True,
+                 tp_group=None, *, param_dtype: torch.dtype, param_device: Optional[torch.device], module_path: str,
+                 precision_resolver) -> None:
+        super().__init__()
+        _check_tp(tp_size)
+        if in_features % tp_size:
+            raise ValueError(f"in_features {in_features} must be divisible by tp_size {tp_size}")
+        self.in_features, self.out_features = in_features, out_features
+        self.tp_rank, self.tp_size, self.tp_group = tp_rank, tp_size, tp_group
+        self.shard_size = in_features // tp_size
+        self.weight = nn.Parameter(torch.empty(out_features, self.shard_size, dtype=param_dtype, device=param_device))
+        if bias:
+            self.bias = nn.Parameter(torch.empty(out_features, dtype=param_dtype, device=param_device))
+        else:
+            self.register_parameter("bias", None)
+        nn.init.normal_(self.weight, std=0.02)
+        if self.bias is not None:
+            nn.init.zeros_(self.bias)
+        self._init_lowbit_precision_state(
+            module_path=module_path, module_type=type(self).__name__, precision_resolver=precision_resolver,
+            lowbit_capable_type="row_parallel_linear",
+            kernel_spec=LowBitKernelSpec(module_type="row_parallel_linear", in_features=self.shard_size,
+                                         out_features=out_features, has_bias=self.bias is not None))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        out = self._lowbit_forward(x, None)
+        if self.bias is not None:
+            out = out + self.bias
+        return out

@@ -1,0 +1,249 @@
+"""GPU tests of the Linear layers and the HipLowBitBackend, mirroring nano-train's
+tests/test_fp8_granularity_semantics.py:100-109, test_lowbit_linear_backends.py:70-120,
+test_persistent_fp8_params.py, test_persistent_fp4_nf4_params.py and
+test_persistent_lowbit_trainability.py, plus numeric parity against the oracle
+(forward: fp32-dequantize-then-matmul; STE backward: dY @ bf16(W_dq),
+dY^T @ bf16(X_dq); fp8 backward recipe: quantized dgrad / wgrad)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _args import precision_args
+from _gpu_util import rel_fro_bf16, seeded, to_np32
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _resolver(**kw):
+    from lowbit.precision import build_module_precision_resolver, resolve_precision_config
+
+    config = resolve_precision_config(precision_args(**kw), torch.device("cuda", 0))
+    return config, build_module_precision_resolver(config)
+
+
+def _linear(res, i, o, *, bias=True, dtype=torch.bfloat16, path="decoder.blocks.0.mlp.fc1"):
+    from lowbit.layers import Linear
+
+    return Linear(i, o, bias, param_dtype=dtype, param_device=torch.device("cuda", 0), module_path=path,
+                  precision_resolver=res)
+
+
+def test_deepseek_recipe_runs_with_padding_shapes(gpu_device):
+    _, res = _resolver(precision_recipe="deepseek_v3", fp8_backend="hip")
+    layer = _linear(res, 257, 129, dtype=torch.float32)
+    x = torch.randn(3, 257, device=gpu_device, requires_grad=True)
+    y = layer(x)
+    assert y.shape == (3, 129) and torch.isfinite(y).all()
+    y.sum().backward()
+    assert x.grad is not None and layer.weight.grad is not None and layer.bias.grad is not None
+
+
+def test_backend_called_once_per_linear(gpu_device):
+    _, res = _resolver(fp8=True, fp8_backend="hip")
+    layer = _linear(res, 128, 64)
+    backend = layer._module_precision_state.lowbit_backend
+    calls = []
+    orig = backend.linear
+
+    def counting(x, w, b):
+        calls.append(1)
+        return orig(x, w, b)
+
+    backend.linear = counting
+    x = torch.randn(4, 128, device=gpu_device, dtype=torch.bfloat16, requires_grad=True)
+    layer(x).float().sum().backward()
+    assert len(calls) == 1 and x.grad is not None and layer.weight.grad is not None
+
+
+def _oracle_operand(t: np.ndarray, granularity: str, *, is_weight: bool, grid: int, bits: int, dim: int):
+    R, K = t.shape
+    if granularity == "tile_1x128" or (granularity == "block_128x128" and dim != 2):
+        return O.quant_tile_1x128(t, grid=grid, bits=bits)[3]
+    if granularity == "block_128x128":
+        return O.quant_block_128x128(t, grid=grid, bits=bits)[3]
+    if granularity == "tensor":
+        return O.quant_grouped(t, R, K, grid=grid, bits=bits)[3]
+    if granularity == "channel":
+        return O.quant_grouped(t, 1, K, grid=grid, bits=bits)[3] if is_weight else \
+            O.quant_grouped(t, R, 1, grid=grid, bits=bits)[3]
+    raise AssertionError(granularity)
+
+
+GRANS = ["tensor", "channel", "tile_1x128", "block_128x128"]
+
+
+@pytest.mark.parametrize("act", GRANS)
+@pytest.mark.parametrize("wgt", GRANS)
+@pytest.mark.parametrize("fmt", ["int_grid", "e4m3"])
+def test_backend_forward_parity_all_granularities(gpu_device, act, wgt, fmt):
+    from lowbit.backend import HipLowBitBackend
+    from lowbit.contracts import LowBitKernelSpec
+
+    spec = LowBitKernelSpec("linear", 384, 200, True, act, wgt, "nearest")
+    be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format=fmt)
+    x = seeded((2, 70, 384), seed=20260601, outliers=0.01).to(gpu_device)
+    w = seeded((200, 384), seed=20260602, std=0.02).to(gpu_device)
+    b = seeded((200,), seed=20260603).to(gpu_device)
+    y = be.linear(x, w, b)
+    grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
+    xd = _oracle_operand(to_np32(x).reshape(-1, 384), act, is_weight=False, grid=grid, bits=8, dim=3)
+    wd = _oracle_operand(to_np32(w), wgt, is_weight=True, grid=grid, bits=8, dim=2)
+    ref = O.gemm_ref(xd, wd, to_np32(b))
+    assert y.shape == (2, 70, 200) and y.dtype == torch.bfloat16
+    assert rel_fro_bf16(y.reshape(-1, 200), ref) <= 1e-3
+
+
+def test_backend_fp4_mode_and_fp32_tensors(gpu_device):
+    from lowbit.backend import HipLowBitBackend
+    from lowbit.contracts import LowBitKernelSpec
+
+    spec = LowBitKernelSpec("linear", 256, 96, False, "tile_1x128", "block_128x128", "nearest")
+    be = HipLowBitBackend(mode="fp4", kernel_spec=spec)
+    x = seeded((50, 256), seed=11, dtype=torch.float32).to(gpu_device)
+    w = seeded((96, 256), seed=12, dtype=torch.float32, std=0.05).to(gpu_device)
+    y = be.linear(x, w, None)
+    xd = O.quant_tile_1x128(to_np32(x), bits=4)[3]
+    wd = O.quant_block_128x128(to_np32(w), bits=4)[3]
+    assert y.dtype == torch.float32
+    assert O.rel_frobenius(y.cpu().numpy(), O.gemm_ref(xd, wd)) <= 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["int_grid", "e4m3"])
+def test_ste_backward_matches_reference_math(gpu_device, fmt):
+    from lowbit.backend import HipLowBitBackend
+    from lowbit.contracts import LowBitKernelSpec
+
+    spec = LowBitKernelSpec("linear", 512, 384, True, "tile_1x128", "block_128x128", "nearest")
+    be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format=fmt)
+    x = seeded((256, 512), seed=21).to(gpu_device).requires_grad_(True)
+    w = seeded((384, 512), seed=22, std=0.02).to(gpu_device).requires_grad_(True)
+    b = torch.zeros(384, device=gpu_device, dtype=torch.bfloat16, requires_grad=True)
+    dy = seeded((256, 384), seed=23, std=1e-3).to(gpu_device)
+    y = be.linear(x, w, b)
+    y.backward(dy)
+    grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
+    # the reference casts dq to the input dtype before its fp32 GEMMs (te_backend.py:173-202, :250-259)
+    xdq = O.round_bf16(O.quant_tile_1x128(to_np32(x), grid=grid)[3])
+    wdq = O.round_bf16(O.quant_block_128x128(to_np32(w), grid=grid)[3])
+    dyn = to_np32(dy)
+    assert rel_fro_bf16(x.grad, dyn.astype(np.float64) @ wdq.astype(np.float64)) <= 1e-3
+    assert rel_fro_bf16(w.grad, dyn.T.astype(np.float64) @ xdq.astype(np.float64)) <= 1e-3
+    torch.testing.assert_close(b.grad.float(), dy.float().sum(0).to(torch.bfloat16).float())
+
+
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_fp8_recipe_backward(gpu_device, rounding):
+    """BASELINE config 3 recipe: dY 1x128 for dgrad; dY^T, X^T per 128x1 for wgrad."""
+    from lowbit.backend import HipLowBitBackend
+    from lowbit.contracts import LowBitKernelSpec
+
+    spec = LowBitKernelSpec("linear", 384, 256, False, "tile_1x128", "block_128x128", rounding)
+    be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format="e4m3", backward="fp8", seed=77)
+    x = seeded((300, 384), seed=31).to(gpu_device).requires_grad_(True)
+    w = seeded((256, 384), seed=32, std=0.02).to(gpu_device).requires_grad_(True)
+    dy = seeded((300, 256), seed=33, std=1e-3).to(gpu_device)
+    y = be.linear(x, w, None)
+    y.backward(dy)
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    base = 0  # first call of this backend instance
+    dyd = O.quant_tile_1x128(to_np32(dy), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 2)[3]
+    wd = O.quant_block_128x128(to_np32(w), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 1)[3]
+    dx_ref = dyd.astype(np.float64) @ wd.astype(np.float64)
+    assert rel_fro_bf16(x.grad, dx_ref) <= 1e-3
+    dytd = O.quant_tile_128x1_t(to_np32(dy), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 3)[3]
+    xtd = O.quant_tile_128x1_t(to_np32(x), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 4)[3]
+    dw_ref = dytd.T.astype(np.float64) @ xtd.astype(np.float64)
+    assert rel_fro_bf16(w.grad, dw_ref) <= 1e-3
+
+
+def test_empty_input(gpu_device):
+    _, res = _resolver(fp8=True, fp8_backend="hip")
+    layer = _linear(res, 128, 32)
+    x = torch.zeros(0, 128, device=gpu_device, dtype=torch.bfloat16, requires_grad=True)
+    y = layer(x)
+    assert y.shape == (0, 32)
+    y.sum().backward()
+
+
+@pytest.mark.parametrize("gran", ["per_channel", "per_tensor"])
+def test_persistent_fp8_layer_refresh_forward_backward(gpu_device, gran):
+    from lowbit.precision import refresh_persistent_lowbit_params
+
+    _, res = _resolver(bf16=True, fp8_param=True, persistent_scale_granularity=gran,
+                       persistent_lowbit_include=["fc"], compute_lowbit_mode=None)
+    layer = _linear(res, 256, 64, path="fc")
+    model = torch.nn.Sequential(layer)
+    assert refresh_persistent_lowbit_params(model) == 1
+    assert layer._persistent_fp8_weight.dtype == torch.float8_e4m3fn
+    assert layer._persistent_numel.item() == 256 * 64
+    x = seeded((8, 256), seed=41).to(gpu_device).requires_grad_(True)
+    y = layer(x)
+    block = 256 if gran == "per_channel" else 256 * 64
+    c, s = O.fp8_persistent_quant(to_np32(layer.weight), block)
+    wdq = O.round_bf16((O.decode_codes(c, O.GRID_E4M3) * np.repeat(s, block)).reshape(64, 256))
+    ref = O.gemm_ref(to_np32(x), wdq, to_np32(layer.bias))
+    assert rel_fro_bf16(y, ref) <= 1e-3
+    y.float().sum().backward()
+    assert layer.weight.grad is not None and torch.isfinite(layer.weight.grad).all()
+
+
+def test_persistent_nf4_fused_matches_materialized_and_trains(gpu_device):
+    from lowbit import persistent as P
+    from lowbit.precision import refresh_persistent_lowbit_params
+
+    _, res = _resolver(bf16=True, fp4_param=True, persistent_lowbit_include=["fc"])
+    layer = _linear(res, 512, 256, bias=False, path="fc")
+    refresh_persistent_lowbit_params(torch.nn.Sequential(layer))
+    assert layer._persistent_fp4_codes.dtype == torch.uint8
+    assert tuple(layer._persistent_scale.shape) == (256, 1)
+    x = seeded((64, 512), seed=51).to(gpu_device).requires_grad_(True)
+    y = layer(x)  # fused NF4 GEMM
+    w_deq = P.dequantize_nf4_persistent(layer._persistent_fp4_codes, layer._persistent_scale, num_values=256 * 512,
+                                        target_shape=(256, 512), target_dtype=torch.bfloat16)
+    y_mat = torch.nn.functional.linear(x.detach(), w_deq)
+    assert rel_fro_bf16(y, y_mat.float().cpu().numpy().astype(np.float64)) <= 2e-3
+    p_ref, s_ref = O.nf4_quant(to_np32(layer.weight), 512)
+    wdq = O.round_bf16(O.nf4_dequant(p_ref, s_ref, 256 * 512, 512)).reshape(256, 512)
+    assert rel_fro_bf16(y, O.gemm_ref(to_np32(x), wdq)) <= 1e-3
+    # one SGD step through the straight-through estimator moves the master weight
+    before = layer.weight.detach().clone()
+    y.float().pow(2).mean().backward()
+    assert x.grad is not None and layer.weight.grad is not None
+    with torch.no_grad():
+        layer.weight -= 1e-1 * layer.weight.grad
+    assert not torch.equal(before, layer.weight.detach())
+    refresh_persistent_lowbit_params(torch.nn.Sequential(layer))
+    assert int(layer._persistent_numel.item()) == 256 * 512
+
+
+def test_c3_backward_full_size_sampled(gpu_device):
+    """BASELINE config 3 at full size with the fp8 backward recipe; dgrad and
+    wgrad checked on sampled rows/columns against the oracle."""
+    from lowbit import workloads
+    from lowbit.backend import HipLowBitBackend
+    from lowbit.contracts import LowBitKernelSpec
+
+    x, w = workloads.c2_inputs(device="cpu")
+    dy = workloads.c3_grad(device="cpu")
+    spec = LowBitKernelSpec("linear", 7168, 18432, False, "tile_1x128", "block_128x128", "nearest")
+    be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format="e4m3", backward="fp8", seed=5)
+    xg = x.to(gpu_device).requires_grad_(True)
+    wg = w.to(gpu_device).requires_grad_(True)
+    y = be.linear(xg, wg, None)
+    y.backward(dy.to(gpu_device))
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(0).choice(8192, 16, replace=False)
+    kcols = np.random.default_rng(1).choice(7168, 128, replace=False)
+    dyd = O.quant_tile_1x128(dy.float().numpy()[rows], grid=O.GRID_E4M3)[3]
+    wd = O.quant_block_128x128(w.float().numpy(), grid=O.GRID_E4M3)[3]
+    dx_ref = dyd.astype(np.float64) @ wd[:, kcols].astype(np.float64)
+    assert rel_fro_bf16(xg.grad[rows][:, kcols], dx_ref) <= 1e-3
+    ncols = np.random.default_rng(2).choice(18432, 16, replace=False)
+    dytd = O.quant_tile_128x1_t(np.ascontiguousarray(dy.float().numpy()[:, ncols]), grid=O.GRID_E4M3)[3]
+    xtd = O.quant_tile_128x1_t(np.ascontiguousarray(x.float().numpy()[:, kcols]), grid=O.GRID_E4M3)[3]
+    dw_ref = dytd.T.astype(np.float64) @ xtd.astype(np.float64)
+    assert rel_fro_bf16(wg.grad[ncols][:, kcols], dw_ref) <= 1e-3
