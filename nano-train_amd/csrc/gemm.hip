@@ -21,6 +21,8 @@
 // LDS and writes full 128-byte row segments.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 
@@ -61,12 +63,12 @@ struct GemmArgs {
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int NTHREADS = 512;
 constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // 32 KiB each
-constexpr int STAGE = TILE_A + TILE_B;
+// epilogue: each wave stages 32 rows of its 128x64 tile at a time inside a
+// 16 KiB slice of the (then idle) operand buffers
+constexpr int EPI_ROWS = 32;
 constexpr int EPI_PITCH_F32 = 64 * 4 + 16;  // bytes per staged row (fp32)
-constexpr int EPI_WAVE = 64 * EPI_PITCH_F32;
-constexpr int SMEM_MAIN = 2 * STAGE + 2 * (BM + BN) * 4;
-constexpr int SMEM_EPI = 8 * EPI_WAVE;
-constexpr int SMEM_BYTES = SMEM_MAIN > SMEM_EPI ? SMEM_MAIN : SMEM_EPI;
+constexpr int EPI_PITCH_16 = 64 * 2 + 16;   // bytes per staged row (bf16 / fp16)
+static_assert(EPI_ROWS * EPI_PITCH_F32 <= TILE_A / 2, "epilogue slice exceeds half an operand buffer");
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -116,23 +118,32 @@ struct StageSrc {
   uint32_t a_grp, b_grp;   // 8 rows of A / B in bytes
 };
 
-__device__ __forceinline__ void issue_stage(const StageSrc& s, uint8_t* stage, int kt, int wave) {
+__device__ __forceinline__ void issue_stage(const StageSrc& s, uint8_t* lds_a, uint8_t* lds_b, int kt, int wave) {
   const uint32_t koff = (uint32_t)kt * BK;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int r0 = (wave * 4 + j) * 8;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.ra, (lds_ptr_t)(stage + r0 * BK), 16, s.a_off, koff + j * s.a_grp,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.ra, (lds_ptr_t)(lds_a + r0 * BK), 16, s.a_off, koff + j * s.a_grp,
                                              0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rb, (lds_ptr_t)(stage + TILE_A + r0 * BK), 16, s.b_off,
-                                             koff + j * s.b_grp, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rb, (lds_ptr_t)(lds_b + r0 * BK), 16, s.b_off, koff + j * s.b_grp,
+                                             0, 0);
   }
 }
 
+// The two pipeline stages live in distinct LDS objects and the K loop is
+// unrolled by two, so every fragment read names one object and every
+// direct-to-LDS copy another: the compiler can then see that the copies in
+// flight for the next K block do not alias the reads of the current one, and
+// keeps them in flight across the whole MFMA phase instead of waiting on them
+// before the first read.
 template <int GRID, bool B_UNIFORM, bool GROUPED>
 __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[SMEM_BYTES];
-  float* lds_sa = reinterpret_cast<float*>(smem + 2 * STAGE);  // [2][BM]
-  float* lds_sb = lds_sa + 2 * BM;                              // [2][BN]
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a0[TILE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b0[TILE_B];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a1[TILE_A];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b1[TILE_B];
+  __shared__ __attribute__((aligned(16))) float lds_s0[BM + BN];  // A row scales, then B row scales
+  __shared__ __attribute__((aligned(16))) float lds_s1[BM + BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
@@ -179,13 +190,11 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     n0 = (int64_t)(in_group / gsize) * BN;
   }
 
-  // scale fetch: threads 0..255 own sa of row m0+tid, 256..511 sb of row n0+tid-256
+  // scale fetch: thread t < 256 owns sa of row m0+t, t >= 256 sb of row n0+t-256
   const bool own_a = tid < BM;
   const int64_t srow = own_a ? min<int64_t>(m0 + tid, g.M - 1) : min<int64_t>(n0 + tid - BM, g.N - 1);
   const float* s_src = own_a ? g.sa + (srow >> g.a_shift) * g.sa_row : g.sb + (srow >> g.b_shift) * g.sb_row;
   const int64_t s_step = own_a ? g.sa_col : g.sb_col;
-  float* s_dst = own_a ? lds_sa + tid : lds_sb + (tid - BM);
-  const float* sb_wave = g.sb + ((n0 + wn * 64) >> g.b_shift) * g.sb_row;
 
   const int nk = (int)(g.Kp / BK);
 
@@ -207,21 +216,22 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  issue_stage(src, smem, 0, wave);
-  float s_next = s_src[0];
-  s_dst[0] = s_next;
+  issue_stage(src, lds_a0, lds_b0, 0, wave);
+  lds_s0[tid] = s_src[0];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
+  // one K block from stage BUF while stage BUF^1 fills with block kt + 1
+  auto step = [&](auto bufc, int kt) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint8_t* ta = BUF ? lds_a1 : lds_a0;
+    const uint8_t* tb = BUF ? lds_b1 : lds_b0;
+    const float* s_cur = BUF ? lds_s1 : lds_s0;
+    float s_next = 0.f;
     if (kt + 1 < nk) {
-      issue_stage(src, smem + (buf ^ 1) * STAGE, kt + 1, wave);
+      issue_stage(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kt + 1, wave);
       s_next = s_src[(int64_t)(kt + 1) * s_step];
     }
-    const uint8_t* ta = smem + buf * STAGE;
-    const uint8_t* tb = ta + TILE_A;
-    const float* sa_buf = lds_sa + buf * BM;
 
     v8i bf[4];
 #pragma unroll
@@ -230,19 +240,18 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     float sbu = 0.f;
     v4f sbv[4];
     if constexpr (B_UNIFORM) {
-      sbu = sb_wave[(int64_t)kt * g.sb_col];
+      sbu = s_cur[BM + wn * 64];
     } else {
-      const float* sb_buf = lds_sb + buf * BN;
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn)
-        sbv[tn] = *reinterpret_cast<const v4f*>(sb_buf + wn * 64 + tn * 16 + (lane >> 4) * 4);
+        sbv[tn] = *reinterpret_cast<const v4f*>(s_cur + BM + wn * 64 + tn * 16 + (lane >> 4) * 4);
     }
     // A fragments are double buffered by hand: the next 16-row group is read
     // from LDS while the current one is on the matrix cores.  The scheduling
     // fence keeps the compiler from hoisting all eight groups (64 VGPRs) at once.
     float sam_all[8];
 #pragma unroll
-    for (int tm = 0; tm < 8; ++tm) sam_all[tm] = sa_buf[wm * 128 + tm * 16 + (lane & 15)];
+    for (int tm = 0; tm < 8; ++tm) sam_all[tm] = s_cur[wm * 128 + tm * 16 + (lane & 15)];
     v8i af = load_frag(ta, wm * 128, lane);
 #pragma unroll
     for (int tm = 0; tm < 8; ++tm) {
@@ -266,17 +275,23 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
       if (tm + 1 < 8) af = af_next;
     }
-    if (kt + 1 < nk) s_dst[(buf ^ 1) * (own_a ? BM : BN)] = s_next;
+    if (kt + 1 < nk) (BUF ? lds_s0 : lds_s1)[tid] = s_next;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+  };
+
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(std::integral_constant<int, 0>(), kt);
+    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   }
 
   // ---------------------------------------------------------------- epilogue
   // lane holds rows m = m0 + wm*128 + tm*16 + lane%16 and columns
   // n = n0 + wn*64 + tn*16 + 4*(lane/16) + r
-  uint8_t* stage_w = smem + wave * EPI_WAVE;
+  const int slab = wave >> 1;
+  uint8_t* stage_w = (slab == 0 ? lds_a0 : slab == 1 ? lds_b0 : slab == 2 ? lds_a1 : lds_b1) + (wave & 1) * (TILE_A / 2);
   const bool out_f32 = g.y_dtype == DT_F32;
-  const int pitch = out_f32 ? EPI_PITCH_F32 : (64 * 2 + 16);
+  const int pitch = out_f32 ? EPI_PITCH_F32 : EPI_PITCH_16;
   float bias[4][4];
   bool nan_col[4][4];
 #pragma unroll
@@ -289,10 +304,10 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       nan_col[tn][r] = g.nan_b && in && g.nan_b[n];
     }
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int part = 0; part < 4; ++part) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int tm = half * 4 + t;
+    for (int t = 0; t < 2; ++t) {
+      const int tm = part * 2 + t;
       const int rloc = t * 16 + (lane & 15);
       const int64_t m = m0 + wm * 128 + tm * 16 + (lane & 15);
       const bool nan_row = g.nan_a && m < g.M && g.nan_a[m];
@@ -319,15 +334,15 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       }
     }
     __syncthreads();
-    // 64 rows x (128 or 256) bytes; 16-byte chunks, row-contiguous across lanes
+    // 32 rows x (128 or 256) bytes; 16-byte chunks, row-contiguous across lanes
     const int chunks_per_row = out_f32 ? 16 : 8;
     const int esz = out_f32 ? 4 : 2;
     const int epc = 16 / esz;  // elements per chunk
 #pragma unroll
-    for (int j = 0; j < (out_f32 ? 16 : 8); ++j) {
+    for (int j = 0; j < (out_f32 ? 8 : 4); ++j) {
       const int q = lane + 64 * j;
       const int row = q / chunks_per_row, c = q % chunks_per_row;
-      const int64_t m = m0 + wm * 128 + half * 64 + row;
+      const int64_t m = m0 + wm * 128 + part * EPI_ROWS + row;
       const int64_t n = n0 + wn * 64 + c * epc;
       if (m >= g.M || n >= g.N) continue;
       const uint8_t* src = stage_w + row * pitch + c * 16;
