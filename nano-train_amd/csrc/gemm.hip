@@ -72,8 +72,14 @@ static_assert(EPI_ROWS * EPI_PITCH_F32 <= TILE_A / 2, "epilogue slice exceeds ha
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// byte offset of 16-byte chunk c of row r inside a swizzled [rows][128] tile
-__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ (r & 7)) << 4); }
+// Byte offset of 16-byte chunk c of row r inside a swizzled [rows][128] tile.
+// A fragment read has 16 lanes read 16 consecutive rows at one logical chunk;
+// the permutation f(r) = (r & 7) ^ bit3(r) gives rows 0-7 eight distinct
+// chunks (conflict-free in 8-lane phases over 128 bytes of banks) and gives
+// every 16-row window distinct (row parity, chunk) pairs (conflict-free in
+// 16-lane phases over 256 bytes of banks).
+__device__ __forceinline__ int swz_perm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ swz_perm(r)) << 4); }
 
 // MFMA fragment of 16 rows: row = lane%16, 32 K bytes of group lane/16.
 // Both operands use the same (lane group, byte) -> K mapping, so the products pair up.
@@ -106,28 +112,29 @@ __device__ __forceinline__ v4f mma_block(const v8i& p, const v8i& q) {
   }
 }
 
-// Direct-to-LDS copies of one K block through buffer resources: each wave
-// moves 4 groups of 8 rows (1 KiB) of A and of B.  Lane i lands at byte 16*i
-// of its group (row i/8, physical chunk i%8) and fetches logical chunk
-// (i%8) ^ (row & 7); its 32-bit row offset is fixed for the whole K loop and
-// the group / K offsets ride in the scalar offset.  Rows past M (or N) lie
-// beyond the resource's num_records and read as zero.
+// Direct-to-LDS copies of one K block through buffer resources: wave w moves
+// the 8-row groups w, w+8, w+16, w+24 (1 KiB each) of A and of B, so bit 3 of
+// every row it writes equals w & 1.  Lane i lands at byte 16*i of its group
+// (row i/8, physical chunk i%8) and fetches logical chunk (i%8) ^ swz_perm(row),
+// which is therefore the same for all four groups: its 32-bit row offset is
+// fixed for the whole K loop and the group / K offsets ride in the scalar
+// offset.  Rows past M (or N) lie beyond the resource's num_records and read
+// as zero.
 struct StageSrc {
   __amdgpu_buffer_rsrc_t ra, rb;
-  uint32_t a_off, b_off;   // per-lane byte offset of row (wave*32 + lane/8), chunk c
-  uint32_t a_grp, b_grp;   // 8 rows of A / B in bytes
+  uint32_t a_off, b_off;   // per-lane byte offset of row (wave*8 + lane/8), chunk c
+  uint32_t a_grp, b_grp;   // 64 rows of A / B in bytes
 };
 
-__device__ __forceinline__ void issue_stage(const StageSrc& s, uint8_t* lds_a, uint8_t* lds_b, int kt, int wave) {
+// group j (0..3) of this wave's share of K block kt, for A and for B
+__device__ __forceinline__ void issue_group(const StageSrc& s, uint8_t* lds_a, uint8_t* lds_b, int kt, int wave,
+                                            int j) {
   const uint32_t koff = (uint32_t)kt * BK;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r0 = (wave * 4 + j) * 8;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.ra, (lds_ptr_t)(lds_a + r0 * BK), 16, s.a_off, koff + j * s.a_grp,
-                                             0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rb, (lds_ptr_t)(lds_b + r0 * BK), 16, s.b_off, koff + j * s.b_grp,
-                                             0, 0);
-  }
+  const int r0 = (wave + 8 * j) * 8;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(s.ra, (lds_ptr_t)(lds_a + r0 * BK), 16, s.a_off, koff + j * s.a_grp, 0,
+                                           0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(s.rb, (lds_ptr_t)(lds_b + r0 * BK), 16, s.b_off, koff + j * s.b_grp, 0,
+                                           0);
 }
 
 // The two pipeline stages live in distinct LDS objects and the K loop is
@@ -200,14 +207,14 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
 
   StageSrc src;
   {
-    const int r = wave * 32 + (lane >> 3);
-    const int c = (lane & 7) ^ (r & 7);
+    const int r = wave * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ swz_perm(r);
     src.ra = __builtin_amdgcn_make_buffer_rsrc((void*)g.a, (short)0, (int)(g.M * g.lda), 0x00020000);
     src.rb = __builtin_amdgcn_make_buffer_rsrc((void*)g.b, (short)0, (int)(g.N * g.ldb), 0x00020000);
     src.a_off = (uint32_t)((m0 + r) * g.lda + c * 16);
     src.b_off = (uint32_t)((n0 + r) * g.ldb + c * 16);
-    src.a_grp = (uint32_t)(8 * g.lda);
-    src.b_grp = (uint32_t)(8 * g.ldb);
+    src.a_grp = (uint32_t)(64 * g.lda);
+    src.b_grp = (uint32_t)(64 * g.ldb);
   }
 
   v4f acc[8][4];
@@ -216,7 +223,8 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  issue_stage(src, lds_a0, lds_b0, 0, wave);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) issue_group(src, lds_a0, lds_b0, 0, wave, j);
   lds_s0[tid] = s_src[0];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -227,11 +235,9 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     const uint8_t* ta = BUF ? lds_a1 : lds_a0;
     const uint8_t* tb = BUF ? lds_b1 : lds_b0;
     const float* s_cur = BUF ? lds_s1 : lds_s0;
+    const bool more = kt + 1 < nk;
     float s_next = 0.f;
-    if (kt + 1 < nk) {
-      issue_stage(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kt + 1, wave);
-      s_next = s_src[(int64_t)(kt + 1) * s_step];
-    }
+    if (more) s_next = s_src[(int64_t)(kt + 1) * s_step];
 
     v8i bf[4];
 #pragma unroll
@@ -258,6 +264,9 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       v8i af_next;
       if (tm + 1 < 8) af_next = load_frag(ta, wm * 128 + (tm + 1) * 16, lane);
       const float sam = sam_all[tm];
+      // the next block's copies go out one group per 16-row step, spread
+      // over the first half of the MFMA phase
+      if (tm < 4 && more) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kt + 1, wave, tm);
       v4f d[4];
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
@@ -275,7 +284,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
       if (tm + 1 < 8) af = af_next;
     }
-    if (kt + 1 < nk) (BUF ? lds_s0 : lds_s1)[tid] = s_next;
+    if (more) (BUF ? lds_s0 : lds_s1)[tid] = s_next;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
