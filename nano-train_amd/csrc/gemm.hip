@@ -235,9 +235,11 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     const uint8_t* ta = BUF ? lds_a1 : lds_a0;
     const uint8_t* tb = BUF ? lds_b1 : lds_b0;
     const float* s_cur = BUF ? lds_s1 : lds_s0;
-    const bool more = kt + 1 < nk;
-    float s_next = 0.f;
-    if (more) s_next = s_src[(int64_t)(kt + 1) * s_step];
+    // The copies into the idle stage are unconditional so the step is one
+    // basic block: on the last K block they reload block kt (in bounds) into
+    // the stage nobody reads again before the epilogue's barrier.
+    const int kn = min(kt + 1, nk - 1);
+    const float s_next = s_src[(int64_t)kn * s_step];
 
     v8i bf[4];
 #pragma unroll
@@ -266,7 +268,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       const float sam = sam_all[tm];
       // the next block's copies go out one group per 16-row step, spread
       // over the first half of the MFMA phase
-      if (tm < 4 && more) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kt + 1, wave, tm);
+      if (tm < 4) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kn, wave, tm);
       v4f d[4];
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
@@ -284,7 +286,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
       if (tm + 1 < 8) af = af_next;
     }
-    if (more) (BUF ? lds_s0 : lds_s1)[tid] = s_next;
+    (BUF ? lds_s0 : lds_s1)[tid] = s_next;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   };
