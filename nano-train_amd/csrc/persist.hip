@@ -17,6 +17,8 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 
@@ -230,23 +232,33 @@ __global__ void __launch_bounds__(256) fp8p_dequant_kernel(const uint8_t* codes,
 // 256x256 output tile, 8 waves of 128x64, K step 64 bf16 (128-byte rows, the
 // same swizzled tile layout as the fp8 kernel).  X tiles move global -> LDS
 // directly; each thread dequantizes 32 weights (16 packed bytes) of one B row
-// per K step into bf16 in LDS, with the next step's packed bytes already in
-// registers.  MFMA: v_mfma_f32_16x16x32_bf16, B tile as the first operand so
-// each lane holds four consecutive output columns.
+// per K step into bf16 in LDS.  The packed bytes and the block scale of step
+// kt+1 are fetched into registers at the start of step kt and dequantized
+// into the idle stage in the middle of it, so the VALU work overlaps the
+// matrix cores.  The codebook sits in LDS.  The two stages are distinct LDS
+// objects and the K loop is unrolled by two (see the fp8 kernel): the copies
+// in flight never alias the fragment reads, so no read waits for them.
+// MFMA: v_mfma_f32_16x16x32_bf16, B tile as the first operand so each lane
+// holds four consecutive output columns.  bf16 rounding is the hardware RNE
+// pack-convert (v_cvt_pk_bf16_f32), the same rounding as f32_to_bf16_bits.
 // ---------------------------------------------------------------------------
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int FBM = 256, FBN = 256, FBK = 64;  // FBK in bf16 elements: 128 bytes per row
 constexpr int FROW = 128;                       // bytes per tile row
 constexpr int FT = 256 * FROW;                  // 32 KiB per operand tile
-constexpr int FSTAGE = 2 * FT;
+constexpr int F_EPI_ROWS = 32;
 constexpr int F_EPI_PITCH = 64 * 4 + 16;
-constexpr int F_SMEM = (2 * FSTAGE > 8 * 64 * F_EPI_PITCH) ? 2 * FSTAGE : 8 * 64 * F_EPI_PITCH;
+static_assert(F_EPI_ROWS * F_EPI_PITCH <= FT / 2, "epilogue slice exceeds half an operand tile");
 
-__device__ __forceinline__ int fswz(int r, int c) { return r * FROW + ((c ^ (r & 7)) << 4); }
+// 16-lane fragment reads are bank-conflict free for 8- and 16-lane phases
+// (the permutation of the fp8 GEMM)
+__device__ __forceinline__ int fswz_perm(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int fswz(int r, int c) { return r * FROW + ((c ^ fswz_perm(r)) << 4); }
 
 __device__ __forceinline__ v8i frag32(const uint8_t* tile, int row0, int lane) {
   const int r = row0 + (lane & 15);
@@ -284,19 +296,43 @@ struct FusedArgs {
   int vec_out;
 };
 
+// Scales of one weight row: the scale of the 32 weights [k0, k0+32) is
+// row[k0 / blk] (NF4 fp32 multiplier) or the e8m0 byte row[k0 / 32] (MXFP4,
+// carried in the float's bits).  A tensor-wide NF4 scale is a row of one
+// entry with blk past any K.  K < 2^31 keeps the division in 32 bits.
+struct RowScales {
+  const void* row;
+  uint32_t blk;
+};
+
 template <int FMT>
-__device__ __forceinline__ void dequant32_to_lds(const uint4 raw, const FusedArgs& g, int64_t n, int64_t k0,
-                                                 uint8_t* tile, int r, int h) {
-  // scale of the 32 elements [k0, k0+32) of row n
-  float s = 1.0f;
-  uint32_t sb = 127;
+__device__ __forceinline__ RowScales fused_row_scales(const FusedArgs& g, int64_t n) {
+  RowScales r;
   if constexpr (FMT == FMT_NF4) {
     const float* sc = reinterpret_cast<const float*>(g.scales);
-    s = (g.block == 0) ? sc[0] : sc[n * (g.K / g.block) + k0 / g.block];
+    r.row = g.block ? sc + n * (g.K / g.block) : sc;
+    r.blk = g.block ? (uint32_t)g.block : 0x40000000u;
   } else {
-    sb = reinterpret_cast<const uint8_t*>(g.scales)[n * (g.K >> 5) + (k0 >> 5)];
+    r.row = reinterpret_cast<const uint8_t*>(g.scales) + n * (g.K >> 5);
+    r.blk = 32;
   }
+  return r;
+}
+
+template <int FMT>
+__device__ __forceinline__ float fused_scale(const RowScales& r, uint32_t k0) {
+  if constexpr (FMT == FMT_NF4)
+    return reinterpret_cast<const float*>(r.row)[k0 / r.blk];
+  else
+    return __uint_as_float((uint32_t)reinterpret_cast<const uint8_t*>(r.row)[k0 >> 5]);
+}
+
+// 32 weights (16 packed bytes, low nibble first) of tile row r, half h
+template <int FMT>
+__device__ __forceinline__ void dequant32_to_lds(const uint4 raw, float s, const float* lut, uint8_t* tile, int r,
+                                                 int h) {
   const uint32_t bytes[4] = {raw.x, raw.y, raw.z, raw.w};
+  const uint32_t sb = __float_as_uint(s);  // MXFP4: e8m0 byte
 #pragma unroll
   for (int j = 0; j < 4; ++j) {  // 8 elements (4 bytes) per 16-byte LDS chunk
     uint32_t out[4];
@@ -305,15 +341,17 @@ __device__ __forceinline__ void dequant32_to_lds(const uint4 raw, const FusedArg
       const uint32_t byte = (bytes[j] >> (8 * b)) & 0xFFu;
       float v0, v1;
       if constexpr (FMT == FMT_NF4) {
-        v0 = kNF4[byte & 15u] * s;
-        v1 = kNF4[byte >> 4] * s;
-      } else if (sb == 0xFFu) {
-        v0 = v1 = __uint_as_float(0x7FC00000u);
+        v0 = lut[byte & 15u] * s;  // layers.py:172-184: codebook value times scale in fp32
+        v1 = lut[byte >> 4] * s;
       } else {
-        v0 = ldexpf(e2m1_value(byte & 15u), (int)sb - 127);
-        v1 = ldexpf(e2m1_value(byte >> 4), (int)sb - 127);
+        // e2m1 value (sign in bit 3) times 2^(e - 127); e = 0xFF marks a NaN block
+        const float a0 = ldexpf(lut[byte & 15u], (int)sb - 127);
+        const float a1 = ldexpf(lut[byte >> 4], (int)sb - 127);
+        v0 = (sb == 0xFFu) ? __uint_as_float(0x7FC00000u) : a0;
+        v1 = (sb == 0xFFu) ? __uint_as_float(0x7FC00000u) : a1;
       }
-      out[b] = (uint32_t)f32_to_bf16_bits(v0) | ((uint32_t)f32_to_bf16_bits(v1) << 16);
+      const v2bf p = {(__bf16)v0, (__bf16)v1};
+      out[b] = __builtin_bit_cast(uint32_t, p);
     }
     *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
   }
@@ -321,7 +359,11 @@ __device__ __forceinline__ void dequant32_to_lds(const uint4 raw, const FusedArg
 
 template <int FMT>
 __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[F_SMEM];
+  __shared__ __attribute__((aligned(16))) uint8_t fx0[FT];
+  __shared__ __attribute__((aligned(16))) uint8_t fw0[FT];
+  __shared__ __attribute__((aligned(16))) uint8_t fx1[FT];
+  __shared__ __attribute__((aligned(16))) uint8_t fw1[FT];
+  __shared__ float lut[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
   const int num_n = (int)((g.N + FBN - 1) / FBN);
@@ -341,16 +383,25 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   const int64_t m0 = (int64_t)(first_m + in_group % gsize) * FBM;
   const int64_t n0 = (int64_t)(in_group / gsize) * FBN;
 
-  // X tile: direct-to-LDS, 4 groups of 8 rows per wave; rows past M read zero
+  if (tid < 16) lut[tid] = (FMT == FMT_NF4) ? kNF4[tid] : e2m1_value((uint32_t)tid);
+
+  // X tile: direct-to-LDS; wave w moves the 8-row groups w, w+8, w+16, w+24
+  // (bit 3 of its rows is w & 1, so its lanes' swizzled chunks are the same
+  // for all four groups); rows past M read zero
   __amdgpu_buffer_rsrc_t rx =
       __builtin_amdgcn_make_buffer_rsrc((void*)g.x, (short)0, (int)(g.M * g.ldx * 2), 0x00020000);
-  const int xr = wave * 32 + (lane >> 3);
-  const uint32_t x_off = (uint32_t)(((m0 + xr) * g.ldx) * 2 + (((lane & 7) ^ (xr & 7)) * 16));
-  const uint32_t x_grp = (uint32_t)(8 * g.ldx * 2);
+  const int xr = wave * 8 + (lane >> 3);
+  const uint32_t x_off = (uint32_t)(((m0 + xr) * g.ldx) * 2 + (((lane & 7) ^ fswz_perm(xr)) * 16));
+  const uint32_t x_grp = (uint32_t)(64 * g.ldx * 2);
+  auto issue_x = [&](uint8_t* stage, int kt, int j) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(stage + (wave + 8 * j) * 8 * FROW), 16, x_off,
+                                             (uint32_t)kt * FROW + j * x_grp, 0, 0);
+  };
   // W: thread t dequantizes row t/2, half t%2 (32 weights = 16 packed bytes)
   const int br = tid >> 1, bh = tid & 1;
   const int64_t bn = min<int64_t>(n0 + br, g.N - 1);
   const uint8_t* wrow = g.w + bn * (g.K >> 1) + bh * 16;
+  const RowScales wsc = fused_row_scales<FMT>(g, bn);
 
   const int nk = (int)(g.K / FBK);
   v4f acc[8][4];
@@ -359,29 +410,40 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  auto issue_x = [&](uint8_t* stage, int kt) {
-    const uint32_t koff = (uint32_t)kt * FROW;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(stage + (wave * 4 + j) * 8 * FROW), 16, x_off,
-                                               koff + j * x_grp, 0, 0);
+  for (int j = 0; j < 4; ++j) issue_x(fx0, 0, j);
+  // packed weight bytes and scale of block kt+1 travel in registers during
+  // step kt-1 and step kt: they are loaded at the middle of step kt-1, after
+  // that step's X copies, and may stay in flight across its closing barrier.
+  // Register set kt & 1 holds block kt+2 (written by step kt, read by step
+  // kt+1), so with the K loop unrolled by two no set is copied.
+  auto w_load = [&](int kb, uint4& raw, float& sc) {
+    raw = *reinterpret_cast<const uint4*>(wrow + (int64_t)kb * (FBK / 2));
+    sc = fused_scale<FMT>(wsc, (uint32_t)(kb * FBK + bh * 32));
   };
-
-  uint4 wraw = *reinterpret_cast<const uint4*>(wrow);
-  issue_x(smem, 0);
-  dequant32_to_lds<FMT>(wraw, g, bn, bh * 32, smem + FT, br, bh);
+  uint4 raw_pf0, raw_pf1;
+  float sc_pf0, sc_pf1;
+  {
+    uint4 raw0;
+    float s0;
+    w_load(0, raw0, s0);
+    __syncthreads();  // lut
+    dequant32_to_lds<FMT>(raw0, s0, lut, fw0, br, bh);
+  }
+  w_load(min(1, nk - 1), raw_pf1, sc_pf1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    uint8_t* st = smem + buf * FSTAGE;
-    if (kt + 1 < nk) {
-      issue_x(smem + (buf ^ 1) * FSTAGE, kt + 1);
-      wraw = *reinterpret_cast<const uint4*>(wrow + (int64_t)(kt + 1) * (FBK / 2));
-    }
-    const uint8_t* ta = st;
-    const uint8_t* tb = st + FT;
+  auto step = [&](auto bufc, int kt) {
+    constexpr int BUF = decltype(bufc)::value;
+    const uint8_t* ta = BUF ? fx1 : fx0;
+    const uint8_t* tb = BUF ? fw1 : fw0;
+    uint8_t* xa_next = BUF ? fx0 : fx1;
+    uint8_t* wb_next = BUF ? fw0 : fw1;
+    // unconditional copies of block kn (the last step reloads itself into
+    // the idle stage) keep the step one basic block
+    const int kn = min(kt + 1, nk - 1);
+
     v8i bf[4];
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) bf[tn] = frag32(tb, wn * 64 + tn * 16, lane);
@@ -390,26 +452,46 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     for (int tm = 0; tm < 8; ++tm) {
       v8i af_next;
       if (tm + 1 < 8) af_next = frag32(ta, wm * 128 + (tm + 1) * 16, lane);
+      if (tm < 4) issue_x(xa_next, kn, tm);
+      if (tm == 4) {
+        // block kn's bytes become visible to the compiler only here, so none
+        // of the dequant work (or a wait for the loads) moves up into the
+        // first half of the MFMA phase; then block kn+1's loads go out, the
+        // last vector-memory operations of the step
+        uint4& r = BUF ? raw_pf0 : raw_pf1;
+        float& s = BUF ? sc_pf0 : sc_pf1;
+        asm volatile("" : "+v"(r.x), "+v"(r.y), "+v"(r.z), "+v"(r.w), "+v"(s));
+        w_load(min(kt + 2, nk - 1), BUF ? raw_pf1 : raw_pf0, BUF ? sc_pf1 : sc_pf0);
+        dequant32_to_lds<FMT>(r, s, lut, wb_next, br, bh);
+      }
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) acc[tm][tn] = mma_bf16_64(bf[tn], af, acc[tm][tn]);
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
       if (tm + 1 < 8) af = af_next;
     }
-    if (kt + 1 < nk) dequant32_to_lds<FMT>(wraw, g, bn, (int64_t)(kt + 1) * FBK + bh * 32, smem + (buf ^ 1) * FSTAGE + FT,
-                                           br, bh);
-    __builtin_amdgcn_s_waitcnt(0);
+    // vmcnt(1) lgkmcnt(0): vector loads complete in issue order, so every X
+    // copy of this step has landed while the last weight load may still be
+    // in flight; the dequant's LDS writes are done
+    __builtin_amdgcn_s_waitcnt(0x0071);
     __syncthreads();
+  };
+
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(std::integral_constant<int, 0>(), kt);
+    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   }
 
-  // epilogue: stage each wave's 128x64 through LDS, 16-byte row-contiguous stores
-  uint8_t* stage_w = smem + wave * 64 * F_EPI_PITCH;
+  // epilogue: each wave stages 32 rows of its 128x64 tile at a time in a
+  // 16 KiB slice of the idle operand tiles; 16-byte row-contiguous stores
+  const int slab = wave >> 1;
+  uint8_t* stage_w = (slab == 0 ? fx0 : slab == 1 ? fw0 : slab == 2 ? fx1 : fw1) + (wave & 1) * (FT / 2);
   const bool out_f32 = g.y_dtype == DT_F32;
   const int pitch = out_f32 ? F_EPI_PITCH : (64 * 2 + 16);
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
+  for (int part = 0; part < 4; ++part) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int tm = half * 4 + t;
+    for (int t = 0; t < 2; ++t) {
+      const int tm = part * 2 + t;
       const int rloc = t * 16 + (lane & 15);
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) {
@@ -428,10 +510,10 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     const int cpr = out_f32 ? 16 : 8;
     const int esz = out_f32 ? 4 : 2;
     const int epc = 16 / esz;
-    for (int j = 0; j < cpr; ++j) {
+    for (int j = 0; j < cpr / 2; ++j) {
       const int q = lane + 64 * j;
       const int row = q / cpr, c = q % cpr;
-      const int64_t m = m0 + wm * 128 + half * 64 + row;
+      const int64_t m = m0 + wm * 128 + part * F_EPI_ROWS + row;
       const int64_t n = n0 + wn * 64 + c * epc;
       if (m >= g.M || n >= g.N) continue;
       const uint8_t* src = stage_w + row * pitch + c * 16;

@@ -31,3 +31,22 @@ def test_hw_fp8_convert_matches_software_rounding(gpu_device):
     assert int(fields["checked"]) > 2_000_000_000
     assert int(fields["non_nan_mismatches"]) == 0, res.stdout
     assert res.returncode == 0
+
+
+BF16_PROBE = os.path.join(ROOT, "tests", "hip", "bf16_cvt_probe")
+
+
+def test_hw_bf16_convert_matches_software_rounding(gpu_device):
+    """The dequant-fused GEMMs round weights to bf16 with v_cvt_pk_bf16_f32;
+    every non-NaN fp32 input must round exactly as f32_to_bf16_bits (RNE) and
+    every NaN must stay a NaN."""
+    if not os.path.exists(BF16_PROBE):
+        pytest.fail("tests/hip/bf16_cvt_probe is not built; run __graft_entry__.build()")
+    res = subprocess.run([BF16_PROBE], capture_output=True, text=True, timeout=120)
+    line = res.stdout.splitlines()[0]
+    assert line.startswith("status=no error"), res.stdout
+    fields = dict(re.findall(r"(\w+)=(\d+)", line))
+    assert int(fields["checked"]) == 1 << 32
+    assert int(fields["non_nan_mismatches"]) == 0, res.stdout
+    assert int(fields["nan_not_nan"]) == 0, res.stdout
+    assert res.returncode == 0
