@@ -126,7 +126,8 @@ int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t
  * recipe; there is no reference function (te_backend.py:250-260 leaves dY
  * unquantized).  It is _tile_quant_dequant (te_backend.py:82-110) applied to
  * x^T.  scales(k, mb) = scales[k*s_row + mb*s_col].  SR bits are keyed by the
- * source index r*K + k.  Optional dq [R, K] and nan_rows [R] as above.
+ * source index r*K + k.  Optional dq [R, K] as above; optional nan_rows [K] has
+ * one flag per transposed row (source column k), set when a NaN reached it.
  */
 int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int grid, int qmax,
                             int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes_t,

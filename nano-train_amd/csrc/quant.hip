@@ -771,7 +771,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
       tr[c8 * 8 + j][slice * 4 + i] = (uint8_t)c;
       if (r < a.R && col < a.K) {
         if (a.dq) store_elem(a.dq, a.dq_dtype, r * a.lddq + col, q * s);
-        if (a.nan_rows && ((__float_as_uint(q) & 0x7FFFFFFFu) > 0x7F800000u)) atomicOr(a.nan_rows + r, 1);
+        if (a.nan_rows && ((__float_as_uint(q) & 0x7FFFFFFFu) > 0x7F800000u)) atomicOr(a.nan_rows + col, 1);
       }
     }
   }
@@ -784,6 +784,115 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
     uint4* dst = reinterpret_cast<uint4*>(a.codes + col * a.ldc + mb * 128 + part * 32);
     dst[0] = make_uint4(src[0], src[1], src[2], src[3]);
     dst[1] = make_uint4(src[4], src[5], src[6], src[7]);
+  }
+}
+
+
+// 128x1 tiles with transposed codes, for 8-aligned K and 16-byte aligned rows.
+// A workgroup covers 128 rows x 128 columns; thread t owns columns
+// cb*128 + 8*(t & 15) + [0, 8) of rows mb*128 + 8*(t >> 4) + [0, 8), read as
+// eight 16-byte row chunks (a wave reads four full 256-byte row segments per
+// load).  Column amax: packed per thread, shuffles across the four row groups
+// of a wave, LDS across the four waves.  Each of the thread's columns then
+// quantizes its 8 consecutive rows as one quant8_tile group (fast division and
+// the hardware e4m3 convert where they apply), whose 8 codes are 8
+// consecutive bytes of the transposed row: one 8-byte store.  Workgroups walk
+// column blocks fastest.  nan_rows, when given, is indexed by transposed row
+// (source column).
+template <int IN_DT, int GRID, bool SR, bool DQ>
+__global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
+  __shared__ uint32_t wmax[4][128];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cc = tid & 15, rg = tid >> 4;
+  const int64_t n_cb = (a.K + 127) / 128;
+  const int64_t mb = blockIdx.x / n_cb, cb = blockIdx.x - mb * n_cb;
+  const int64_t col0 = cb * 128 + cc * 8;
+  const int64_t row0 = mb * 128 + rg * 8;
+  const bool col_in = col0 < a.K;  // K % 8 == 0: a chunk is wholly in or out
+
+  Chunk8<IN_DT> c[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) chunk_load<IN_DT>(c[i], a.x, (row0 + i) * a.ldx + col0, col_in && row0 + i < a.R);
+
+  // column |x| maxima as fp32 bit patterns (NaN above every finite value)
+  uint32_t m[8];
+  if constexpr (IN_DT == DT_F32) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t mm = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint4 w = c[i].w[j >> 2];
+        const uint32_t b = (j & 3) == 0 ? w.x : (j & 3) == 1 ? w.y : (j & 3) == 2 ? w.z : w.w;
+        mm = max(mm, b & 0x7FFFFFFFu);
+      }
+      mm = max(mm, (uint32_t)__shfl_xor((int)mm, 16));
+      mm = max(mm, (uint32_t)__shfl_xor((int)mm, 32));
+      m[j] = mm;
+    }
+  } else {
+    uint32_t m2[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      m2[0] = pk_max_u16(m2[0], c[i].w[0].x & 0x7FFF7FFFu);
+      m2[1] = pk_max_u16(m2[1], c[i].w[0].y & 0x7FFF7FFFu);
+      m2[2] = pk_max_u16(m2[2], c[i].w[0].z & 0x7FFF7FFFu);
+      m2[3] = pk_max_u16(m2[3], c[i].w[0].w & 0x7FFF7FFFu);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 16));
+      m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 32));
+      m[2 * k] = m2[k] << 16;
+      m[2 * k + 1] = m2[k] & 0xFFFF0000u;
+    }
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) wmax[wave][cc * 8 + j] = m[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    m[j] = max(max(wmax[0][cc * 8 + j], wmax[1][cc * 8 + j]), max(wmax[2][cc * 8 + j], wmax[3][cc * 8 + j]));
+
+  uint32_t rb[8][8];  // [row i][column j]
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sr_words<SR>((uint64_t)((row0 + i) * a.K + col0), a.seed, a.offset, rb[i]);
+
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int64_t col = col0 + j;
+    const float s = scale_from_amax_bits(m[j], a.qmaxf, a.scale_rule);
+    float v[8];
+    uint32_t rbj[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (IN_DT == DT_F32) {
+        const uint4 w = c[i].w[j >> 2];
+        v[i] = __uint_as_float((j & 3) == 0 ? w.x : (j & 3) == 1 ? w.y : (j & 3) == 2 ? w.z : w.w);
+      } else {
+        const uint4 w = c[i].w[0];
+        const uint32_t b = (j >> 1) == 0 ? w.x : (j >> 1) == 1 ? w.y : (j >> 1) == 2 ? w.z : w.w;
+        v[i] = __uint_as_float((j & 1) ? (b & 0xFFFF0000u) : (b << 16));
+      }
+      rbj[i] = rb[i][j];
+    }
+    uint32_t lo, hi;
+    float q[8];
+    const bool nan = quant8_tile<GRID, SR, DQ>(v, m[j], s, a.qmaxf, rbj, lo, hi, q);
+    if (col_in) {
+      *reinterpret_cast<uint2*>(a.codes + col * a.ldc + row0) = make_uint2(lo, hi);
+      if (rg == 0) {
+        a.scales[col * a.s_row + mb * a.s_col] = s;
+        if (nan && a.nan_rows) atomicOr(a.nan_rows + col, 1);
+      }
+      if constexpr (DQ) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (row0 + i < a.R) store_elem(a.dq, a.dq_dtype, (row0 + i) * a.lddq + col, q[i] * s);
+      }
+    }
   }
 }
 
@@ -1103,8 +1212,24 @@ extern "C" int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, in
   QuantArgs a = make_args(x, R, K, ldx, grid, qmax, scale_rule, seed, offset, codes_t, ldct, scales, s_row, s_col,
                           dq, dq_dtype, lddq, nan_rows);
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
-  dim3 grd((unsigned)(MB * CB)), blk(256);
   hipStream_t st = as_stream(stream);
+  if (K % 8 == 0 && ldx % 8 == 0 && aligned(x, 16) && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) &&
+      cdiv(R, 128) * cdiv(K, 128) <= 0x7FFFFFFF) {
+    dim3 grd((unsigned)(cdiv(R, 128) * cdiv(K, 128))), blk(256);
+    if (x_dtype == NTLB_BF16) {
+      NTLB_DISPATCH_GRID_SR(grid, sr, {
+        if (dq) quant_tile_128x1_t_fast<DT_BF16, G_, S_, true><<<grd, blk, 0, st>>>(a);
+        else quant_tile_128x1_t_fast<DT_BF16, G_, S_, false><<<grd, blk, 0, st>>>(a);
+      });
+    } else {
+      NTLB_DISPATCH_GRID_SR(grid, sr, {
+        if (dq) quant_tile_128x1_t_fast<DT_F32, G_, S_, true><<<grd, blk, 0, st>>>(a);
+        else quant_tile_128x1_t_fast<DT_F32, G_, S_, false><<<grd, blk, 0, st>>>(a);
+      });
+    }
+    return check_launch(fn);
+  }
+  dim3 grd((unsigned)(MB * CB)), blk(256);
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
     quant_tile_128x1_t_kernel<D_, G_, S_><<<grd, blk, 0, st>>>(a);
   }));

@@ -186,13 +186,16 @@ def _fp8_recipe_backward(backend, dy2, x2, weight, base, needs):
     fmt, bits, rnd, seed = backend.code_format, backend.bits, backend._rounding_mode, backend.seed
     dx = dw = None
     if needs[0]:
-        qdy = ops.quant_tile_1x128(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 2)
+        qdy = ops.quant_tile_1x128(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 2,
+                                   want_nan_rows=True)
         _, qwt = ops.quant_block_128x128(weight, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 1,
                                          want_transposed=True)
         dx = ops.gemm_blockscaled(qdy, qwt, out_dtype=torch.float32 if dy2.dtype == torch.float32 else dy2.dtype)
     if needs[1]:
-        qdyt = ops.quant_tile_128x1_t(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 3)
-        qxt = ops.quant_tile_128x1_t(x2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 4)
+        qdyt = ops.quant_tile_128x1_t(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 3,
+                                      want_nan_rows=True)
+        qxt = ops.quant_tile_128x1_t(x2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 4,
+                                     want_nan_rows=True)
         dw = ops.gemm_blockscaled(qdyt, qxt, out_dtype=torch.float32 if dy2.dtype == torch.float32 else dy2.dtype)
     return dx, dw
 

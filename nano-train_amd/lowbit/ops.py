@@ -195,8 +195,11 @@ def quant_tile_128x1_t(
     scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
     want_dq: bool = False,
     dq_dtype: Optional[torch.dtype] = None,
+    want_nan_rows: bool = False,
 ) -> QTensor:
-    """128x1 tiles of x [R, K] with transposed codes: a QTensor of x^T [K, R]."""
+    """128x1 tiles of x [R, K] with transposed codes: a QTensor of x^T [K, R].
+
+    nan_rows, when requested, flags the rows of x^T (columns of x) that hold a NaN."""
     _require_device(x)
     x2 = _as_2d(x)
     R, K = x2.shape
@@ -207,13 +210,14 @@ def quant_tile_128x1_t(
     kp = cdiv(max(K, 1), 4) * 4
     scales = torch.empty((MB, kp), dtype=torch.float32, device=dev)  # tile-major for the GEMM
     dq = torch.empty((R, K), dtype=dq_dtype or x.dtype, device=dev) if want_dq else None
+    nan = torch.zeros((K,), dtype=torch.int32, device=dev) if want_nan_rows else None
     call(
         "ntlb_quant_tile_128x1_t", x2.data_ptr(), _dtype_code(x2.dtype), R, K, x2.stride(0), grid_code(fmt),
         (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset, codes_t.data_ptr(), ldct,
         scales.data_ptr(), 1, kp, _ptr(dq), _dtype_code(dq.dtype) if dq is not None else 0,
-        dq.stride(0) if dq is not None else 0, None, _stream(),
+        dq.stride(0) if dq is not None else 0, _ptr(nan), _stream(),
     )
-    return QTensor(codes_t, scales, 1, kp, 0, grid_code(fmt), K, R, None, dq)
+    return QTensor(codes_t, scales, 1, kp, 0, grid_code(fmt), K, R, nan, dq)
 
 
 def quant_grouped(

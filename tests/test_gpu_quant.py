@@ -99,6 +99,49 @@ def test_tile_128x1_transposed_parity(gpu_device, shape, fmt, grid, rname, rcode
     assert_bits_equal(to_np32(q.dq), torch.from_numpy(dq).to(x.dtype).float().numpy(), "dq")
 
 
+@pytest.mark.parametrize("shape", [(300, 136), (1000, 384), (128, 8), (2, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+@pytest.mark.parametrize("want_dq", [False, True])
+def test_tile_128x1_fast_path_special_columns(gpu_device, shape, dtype, fmt, grid, rname, rcode, want_dq):
+    """The 8-aligned path of the 128x1 quantizer: ragged R, both input dtypes,
+    columns holding a NaN, an inf, all zeros and subnormals; NaN flags land on
+    the transposed rows (source columns) that hold the NaN."""
+    from lowbit import ops
+
+    R, K = shape
+    x = seeded(shape, seed=20260110, std=1e-2, outliers=0.02).float()
+    if K >= 8:
+        x[R // 2, 1] = float("nan")
+        x[0, 3] = float("inf")
+        x[:, 5] = 0.0
+        x[:, 6] = 1e-39
+        x[R - 1, 7] = -float("inf")
+    x = x.to(dtype).to(gpu_device)
+    q = ops.quant_tile_128x1_t(x, fmt=fmt, rounding=rname, seed=5, offset=7, want_dq=want_dq, want_nan_rows=True)
+    torch.cuda.synchronize()
+    ct, st, qv, dq = O.quant_tile_128x1_t(to_np32(x), grid=grid, rounding=rcode, seed=5, offset=7)
+    assert_bits_equal(q.codes.cpu().numpy(), ct, "codes_t")
+    assert_bits_equal(scales_row_major(q, K, st.shape[1]), st, "scales")
+    if want_dq:
+        assert_bits_equal(to_np32(q.dq), torch.from_numpy(dq).to(x.dtype).float().numpy(), "dq")
+    nan_ref = np.isnan(to_np32(x)).any(axis=0).astype(np.int32)
+    assert np.array_equal(q.nan_rows.cpu().numpy(), nan_ref)
+
+
+def test_c3_dy_128x1_full_size(gpu_device):
+    """dY [8192, 18432] 128x1 tiles (the wgrad operand dY^T)."""
+    from lowbit import ops, workloads
+
+    dy = workloads.c3_grad(device="cpu")
+    q = ops.quant_tile_128x1_t(dy.to(gpu_device), fmt="e4m3")
+    torch.cuda.synchronize()
+    ct, st, _, _ = O.quant_tile_128x1_t(dy.float().numpy(), grid=O.GRID_E4M3)
+    assert_bits_equal(q.codes.cpu().numpy(), ct, "codes_t")
+    assert_bits_equal(scales_row_major(q, dy.shape[1], st.shape[1]), st, "scales")
+
+
 @pytest.mark.parametrize("kind", ["tensor", "channel_last", "channel_rows", "strip"])
 @pytest.mark.parametrize("fmt,grid", GRIDS)
 @pytest.mark.parametrize("rname,rcode", ROUNDS)
