@@ -96,6 +96,8 @@ def other_config(args) -> dict:
         t = {}
         t["dy_1x128_us"] = _time_ms(lambda i: ops.quant_tile_1x128(dy, fmt=fmt), args.steps, args.warmup, st) * 1e3
         t["dy_128x1_us"] = _time_ms(lambda i: ops.quant_tile_128x1_t(dy, fmt=fmt), args.steps, args.warmup, st) * 1e3
+        t["dy_dual_us"] = _time_ms(lambda i: ops.quant_dual_1x128_128x1(dy, fmt=fmt), args.steps, args.warmup,
+                                   st) * 1e3
         qdy = ops.quant_tile_1x128(dy, fmt=fmt)
         qdy_t = ops.quant_tile_128x1_t(dy, fmt=fmt)
         dg = _time_ms(lambda i: ops.gemm_blockscaled(qdy, qw_t), args.steps, args.warmup, st)
@@ -108,7 +110,9 @@ def other_config(args) -> dict:
                    dgrad_tflops=round(fl / (dg * 1e-3) / 1e12, 2), wgrad_tflops=round(fl / (wg * 1e-3) / 1e12, 2),
                    quantizers={k: round(v, 2) for k, v in t.items()},
                    dy_1x128_GBs=round((M * N * 3 + M * (N // 128) * 4) / t["dy_1x128_us"] / 1e3, 1),
-                   dy_128x1_GBs=round((M * N * 3 + N * (M // 128) * 4) / t["dy_128x1_us"] / 1e3, 1))
+                   dy_128x1_GBs=round((M * N * 3 + N * (M // 128) * 4) / t["dy_128x1_us"] / 1e3, 1),
+                   dy_dual_GBs=round((M * N * 4 + M * (N // 128) * 4 + N * (M // 128) * 4) / t["dy_dual_us"] / 1e3,
+                                     1))
         return res
     if args.config == "c4":
         tokens, routing, w_up, w_down = workloads.c4_inputs(device="cpu")

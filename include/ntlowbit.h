@@ -135,6 +135,25 @@ int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, int64_t K, in
                             int64_t lddq, int32_t* nan_rows, void* stream);
 
 /*
+ * Dual-output pass for a gradient dY: one read of x [R, K] writes both its
+ * 1x128 tiles (codes [R, ldc], scales addressed (s_row, s_col), nan_rows [R],
+ * SR offset offset_rows) -- exactly ntlb_quant_tile_1x128 -- and its 128x1
+ * tiles with transposed codes (codes_t [K, ldct], scales_t addressed
+ * (st_row, st_col), nan_cols [K], SR offset offset_cols) -- exactly
+ * ntlb_quant_tile_128x1_t.  These are the dgrad and wgrad operands of the
+ * DeepSeek-V3 recipe backward; there is no reference function (the reference
+ * backward, te_backend.py:250-260, leaves dY unquantized), and each output
+ * follows _tile_quant_dequant (te_backend.py:82-110) as its single-output
+ * entry point does.  Needs bf16 or fp32 x, K % 8 == 0, ldx % 8 == 0 and
+ * 16-byte aligned rows (NTLB_EUNSUPPORTED otherwise: use the two entry points).
+ */
+int ntlb_quant_dual_1x128_128x1(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int grid, int qmax,
+                                int rounding, int scale_rule, uint64_t seed, uint64_t offset_rows,
+                                uint64_t offset_cols, uint8_t* codes, int64_t ldc, float* scales, int64_t s_row,
+                                int64_t s_col, int32_t* nan_rows, uint8_t* codes_t, int64_t ldct, float* scales_t,
+                                int64_t st_row, int64_t st_col, int32_t* nan_cols, void* stream);
+
+/*
  * Dequantize codes back to a float tensor: out[i, k] = q(code) * scale(i, k)
  * with scale(i, k) = scales[(i >> r_shift) * s_row + (k >> c_shift) * s_col]
  * (shifts 0 or 7; a zero stride broadcasts), cast to out_dtype.  The receive

@@ -212,9 +212,18 @@ __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
 // holding a NaN takes the per-element reference path (and reports it); every
 // other tile clamps with min/max, divides with the fast exact sequence when
 // its amax allows, and rounds to e4m3 in hardware when enabled.
+// The fast division is taken for round-to-nearest tiles whose amax bits lie in
+// [0x1A000000, 0x7B800000] (no NaN, no inf).
+template <bool SR>
+__device__ __forceinline__ bool fast_div_ok(uint32_t m) {
+  return !SR && m >= 0x1A000000u && m <= 0x7B800000u;
+}
+
+// rs is 1/s (IEEE, correctly rounded) wherever fast_div_ok(m) holds; it is
+// not read otherwise.
 template <int GRID, bool SR, bool DQ>
-__device__ __forceinline__ bool quant8_tile(const float (&v)[8], uint32_t m, float s, float qmaxf,
-                                            const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+__device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, float s, float rs, float qmaxf,
+                                               const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
   if (m > 0x7F800000u) {
     // NaN in the tile: reference semantics element by element
     quant8<GRID, SR>(v, s, qmaxf, rb, lo, hi, q);
@@ -226,21 +235,21 @@ __device__ __forceinline__ bool quant8_tile(const float (&v)[8], uint32_t m, flo
     // of x; this equals the correctly rounded quotient wherever it can move
     // a code (checked exhaustively on random operands).  Other tiles, and
     // stochastic rounding, divide.
-    const bool fast_div = !SR && m >= 0x1A000000u && m <= 0x7B800000u;
-    if (fast_div) {
-      const float rs = 1.0f / s;
+    // no NaN reaches the clamp here (NaN tiles took the path above; x/s
+    // is finite or +-inf), so the single-instruction median is the clamp
+    if (fast_div_ok<SR>(m)) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float y = v[i] * rs;
         const float e = __builtin_fmaf(-y, s, v[i]);
         float z = __builtin_copysignf(__builtin_fmaf(e, rs, y), v[i]);
-        vq[i] = fminf(fmaxf(z, -qmaxf), qmaxf);  // no NaN in this tile
+        vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         float z = v[i] / s;
-        vq[i] = fminf(fmaxf(z, -qmaxf), qmaxf);
+        vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
       }
     }
     if constexpr (GRID == GRID_INT) {
@@ -281,6 +290,13 @@ __device__ __forceinline__ bool quant8_tile(const float (&v)[8], uint32_t m, flo
     }
   }
   return false;
+}
+
+template <int GRID, bool SR, bool DQ>
+__device__ __forceinline__ bool quant8_tile(const float (&v)[8], uint32_t m, float s, float qmaxf,
+                                            const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+  const float rs = fast_div_ok<SR>(m) ? 1.0f / s : 1.0f;
+  return quant8_tile_rs<GRID, SR, DQ>(v, m, s, rs, qmaxf, rb, lo, hi, q);
 }
 
 // 8 consecutive elements as fp32 plus their |x| max (bits), from a chunk
@@ -796,16 +812,48 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // of a wave, LDS across the four waves.  Each of the thread's columns then
 // quantizes its 8 consecutive rows as one quant8_tile group (fast division and
 // the hardware e4m3 convert where they apply), whose 8 codes are 8
-// consecutive bytes of the transposed row: one 8-byte store.  Workgroups walk
-// column blocks fastest.  nan_rows, when given, is indexed by transposed row
+// consecutive bytes of the transposed row.  They are staged in LDS (8-byte
+// slot rg ^ 2*(cc & 7) of a 144-byte row: 2-cycle writes, near-minimal
+// 16-byte reads) and leave as full 128-byte transposed rows, 16 bytes per
+// lane; direct 8-byte stores would scatter 32-byte pieces over 16 rows per
+// instruction.  Workgroups walk column blocks fastest.  nan_rows, when given, is indexed by transposed row
 // (source column).
-template <int IN_DT, int GRID, bool SR, bool DQ>
-__global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
+//
+// With DUAL the same pass also writes the 1x128 tiles of x, described by ar
+// (codes, ldc, scales, s_row, s_col, nan_rows and the SR offset): row i of a
+// thread's chunks is 8 columns of one 1x128 tile, whose other 120 columns are
+// held by the 15 lanes of the same row group, so a 16-lane max gives the tile
+// amax.  One read of dY feeds both the dgrad and the wgrad operands.
+// workgroup order of the 128x1 kernels: groups of T128_GM row blocks walk
+// one column block before the next (T128_GM consecutive workgroups write
+// adjacent 128-byte pieces of the same transposed rows)
+#ifndef NTLB_T128_GM
+#define NTLB_T128_GM 1
+#endif
+template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false>
+__global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, QuantArgs ar = QuantArgs()) {
+  constexpr int TP = 144;  // staged transposed row pitch (bytes)
   __shared__ uint32_t wmax[4][128];
+  __shared__ uint32_t rmax[128];
+  // per column (and, with DUAL, per row tile): amax bits, scale, 1/scale,
+  // computed once per workgroup by one thread each
+  __shared__ __attribute__((aligned(16))) uint32_t cm[128];
+  __shared__ __attribute__((aligned(16))) float cs[128], crs[128];
+  __shared__ __attribute__((aligned(16))) uint32_t rm[128];
+  __shared__ __attribute__((aligned(16))) float rs_[128], rrs[128];
+  __shared__ __attribute__((aligned(16))) uint8_t tcodes[128 * TP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cc = tid & 15, rg = tid >> 4;
-  const int64_t n_cb = (a.K + 127) / 128;
-  const int64_t mb = blockIdx.x / n_cb, cb = blockIdx.x - mb * n_cb;
+  const int64_t n_cb = (a.K + 127) / 128, n_mb = (a.R + 127) / 128;
+  int64_t mb, cb;
+  {
+    constexpr int GM = NTLB_T128_GM;
+    const int64_t pid = blockIdx.x;
+    const int64_t group = pid / (GM * n_cb), within = pid - group * GM * n_cb;
+    const int64_t gsize = min<int64_t>(GM, n_mb - group * GM);
+    mb = group * GM + within % gsize;
+    cb = within / gsize;
+  }
   const int64_t col0 = cb * 128 + cc * 8;
   const int64_t row0 = mb * 128 + rg * 8;
   const bool col_in = col0 < a.K;  // K % 8 == 0: a chunk is wholly in or out
@@ -814,8 +862,9 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) chunk_load<IN_DT>(c[i], a.x, (row0 + i) * a.ldx + col0, col_in && row0 + i < a.R);
 
-  // column |x| maxima as fp32 bit patterns (NaN above every finite value)
-  uint32_t m[8];
+  // column |x| maxima as fp32 bit patterns (NaN above every finite value):
+  // per thread, then across the four row groups of the wave, then (in LDS)
+  // across the four waves
   if constexpr (IN_DT == DT_F32) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -828,7 +877,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
       }
       mm = max(mm, (uint32_t)__shfl_xor((int)mm, 16));
       mm = max(mm, (uint32_t)__shfl_xor((int)mm, 32));
-      m[j] = mm;
+      if (lane < 16) wmax[wave][cc * 8 + j] = mm;
     }
   } else {
     uint32_t m2[4] = {0, 0, 0, 0};
@@ -843,18 +892,63 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
     for (int k = 0; k < 4; ++k) {
       m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 16));
       m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 32));
-      m[2 * k] = m2[k] << 16;
-      m[2 * k + 1] = m2[k] & 0xFFFF0000u;
+      if (lane < 16) {
+        wmax[wave][cc * 8 + 2 * k] = m2[k] << 16;
+        wmax[wave][cc * 8 + 2 * k + 1] = m2[k] & 0xFFFF0000u;
+      }
     }
   }
-  if (lane < 16) {
+  if constexpr (DUAL) {
+    // 1x128 tile amax of each of the 128 rows: the 16 lanes of a row group
+    // hold the tile's 128 columns
 #pragma unroll
-    for (int j = 0; j < 8; ++j) wmax[wave][cc * 8 + j] = m[j];
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t mr = row16_max_u32(chunk_amax<IN_DT>(c[i]));
+      if (cc == 0) rmax[rg * 8 + i] = mr;
+    }
   }
   __syncthreads();
+  if (tid < 128) {
+    const uint32_t mm = max(max(wmax[0][tid], wmax[1][tid]), max(wmax[2][tid], wmax[3][tid]));
+    const float sc = scale_from_amax_bits(mm, a.qmaxf, a.scale_rule);
+    cm[tid] = mm;
+    cs[tid] = sc;
+    crs[tid] = fast_div_ok<SR>(mm) ? 1.0f / sc : 1.0f;
+  } else if (DUAL) {
+    const int r = tid - 128;
+    const uint32_t mm = rmax[r];
+    const float sc = scale_from_amax_bits(mm, ar.qmaxf, ar.scale_rule);
+    rm[r] = mm;
+    rs_[r] = sc;
+    rrs[r] = fast_div_ok<SR>(mm) ? 1.0f / sc : 1.0f;
+  }
+  __syncthreads();
+
+  if constexpr (DUAL) {
+    // 1x128 tiles: tile cb of rows row0..row0+7; pad columns [K, ldc) get
+    // zero codes like every other 1x128 output
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    m[j] = max(max(wmax[0][cc * 8 + j], wmax[1][cc * 8 + j]), max(wmax[2][cc * 8 + j], wmax[3][cc * 8 + j]));
+    for (int i = 0; i < 8; ++i) {
+      const int64_t r = row0 + i;
+      const int rl = rg * 8 + i;
+      const uint32_t mr = rm[rl];
+      const float sr = rs_[rl];
+      float v[8];
+      chunk_floats<IN_DT>(c[i], v);
+      uint32_t rbr[8];
+      sr_words<SR>((uint64_t)(r * a.K + col0), ar.seed, ar.offset, rbr);
+      uint32_t lo, hi;
+      float q[8];
+      const bool nan = quant8_tile_rs<GRID, SR, false>(v, mr, sr, rrs[rl], ar.qmaxf, rbr, lo, hi, q);
+      if (r < a.R) {
+        *reinterpret_cast<uint2*>(ar.codes + r * ar.ldc + col0) = make_uint2(lo, hi);
+        if (cc == 0) {
+          ar.scales[r * ar.s_row + cb * ar.s_col] = sr;
+          if (nan && ar.nan_rows) atomicOr(ar.nan_rows + r, 1);
+        }
+      }
+    }
+  }
 
   uint32_t rb[8][8];  // [row i][column j]
 #pragma unroll
@@ -862,8 +956,10 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
 
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    const int cl = cc * 8 + j;
     const int64_t col = col0 + j;
-    const float s = scale_from_amax_bits(m[j], a.qmaxf, a.scale_rule);
+    const uint32_t mj = cm[cl];
+    const float s = cs[cl];
     float v[8];
     uint32_t rbj[8];
 #pragma unroll
@@ -880,9 +976,9 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
     }
     uint32_t lo, hi;
     float q[8];
-    const bool nan = quant8_tile<GRID, SR, DQ>(v, m[j], s, a.qmaxf, rbj, lo, hi, q);
+    const bool nan = quant8_tile_rs<GRID, SR, DQ>(v, mj, s, crs[cl], a.qmaxf, rbj, lo, hi, q);
+    *reinterpret_cast<uint2*>(tcodes + cl * TP + ((rg ^ (2 * (cc & 7))) * 8)) = make_uint2(lo, hi);
     if (col_in) {
-      *reinterpret_cast<uint2*>(a.codes + col * a.ldc + row0) = make_uint2(lo, hi);
       if (rg == 0) {
         a.scales[col * a.s_row + mb * a.s_col] = s;
         if (nan && a.nan_rows) atomicOr(a.nan_rows + col, 1);
@@ -892,6 +988,18 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a) {
         for (int i = 0; i < 8; ++i)
           if (row0 + i < a.R) store_elem(a.dq, a.dq_dtype, (row0 + i) * a.lddq + col, q[i] * s);
       }
+    }
+  }
+  __syncthreads();
+  // 128 transposed rows of 128 bytes (rows past R hold zero codes, inside ldct)
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int qi = p * 256 + tid;
+    const int cl = qi >> 3, k = qi & 7;
+    const int64_t col = cb * 128 + cl;
+    if (col < a.K) {
+      const uint4 v = *reinterpret_cast<const uint4*>(tcodes + cl * TP + (((2 * k) ^ (2 * ((cl >> 3) & 7))) * 8));
+      *reinterpret_cast<uint4*>(a.codes + col * a.ldc + mb * 128 + k * 16) = v;
     }
   }
 }
@@ -1233,6 +1341,44 @@ extern "C" int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, in
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
     quant_tile_128x1_t_kernel<D_, G_, S_><<<grd, blk, 0, st>>>(a);
   }));
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_quant_dual_1x128_128x1(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx,
+                                           int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                           uint64_t offset_rows, uint64_t offset_cols, uint8_t* codes, int64_t ldc,
+                                           float* scales, int64_t s_row, int64_t s_col, int32_t* nan_rows,
+                                           uint8_t* codes_t, int64_t ldct, float* scales_t, int64_t st_row,
+                                           int64_t st_col, int32_t* nan_cols, void* stream) {
+  const char* fn = "ntlb_quant_dual_1x128_128x1";
+  int rc = check_common(fn, x, x_dtype, R, K, ldx, grid, qmax, rounding, scale_rule, nullptr, NTLB_BF16, 0);
+  if (rc) return rc;
+  if (!(x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) || K % 8 || ldx % 8 || (x && !aligned(x, 16)))
+    return fail(NTLB_EUNSUPPORTED, "%s: needs bf16 or fp32 input, K %% 8 == 0, ldx %% 8 == 0, 16-byte rows", fn);
+  const int64_t T = cdiv(K, 128), MB = cdiv(R, 128);
+  if (ldc < T * 128 || ldc % 16 || (codes && !aligned(codes, 16)))
+    return fail(NTLB_EINVAL, "%s: ldc must be >= ceil(K/128)*128, a multiple of 16, 16-byte aligned", fn);
+  if (ldct < MB * 128 || ldct % 16 || (codes_t && !aligned(codes_t, 16)))
+    return fail(NTLB_EINVAL, "%s: ldct must be >= ceil(R/128)*128, a multiple of 16, 16-byte aligned", fn);
+  if (R * K == 0) return NTLB_OK;
+  if (!codes || !scales || !codes_t || !scales_t) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (MB * T > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many blocks", fn);
+  QuantArgs ac = make_args(x, R, K, ldx, grid, qmax, scale_rule, seed, offset_cols, codes_t, ldct, scales_t, st_row,
+                           st_col, nullptr, 0, 0, nan_cols);
+  QuantArgs ar = make_args(x, R, K, ldx, grid, qmax, scale_rule, seed, offset_rows, codes, ldc, scales, s_row, s_col,
+                           nullptr, 0, 0, nan_rows);
+  const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
+  hipStream_t st = as_stream(stream);
+  dim3 grd((unsigned)(MB * T)), blk(256);
+  if (x_dtype == NTLB_BF16) {
+    NTLB_DISPATCH_GRID_SR(grid, sr, {
+      quant_tile_128x1_t_fast<DT_BF16, G_, S_, false, true><<<grd, blk, 0, st>>>(ac, ar);
+    });
+  } else {
+    NTLB_DISPATCH_GRID_SR(grid, sr, {
+      quant_tile_128x1_t_fast<DT_F32, G_, S_, false, true><<<grd, blk, 0, st>>>(ac, ar);
+    });
+  }
   return check_launch(fn);
 }
 

@@ -185,15 +185,22 @@ def _fp8_recipe_backward(backend, dy2, x2, weight, base, needs):
     """DeepSeek-V3 recipe backward: quantized dgrad / wgrad."""
     fmt, bits, rnd, seed = backend.code_format, backend.bits, backend._rounding_mode, backend.seed
     dx = dw = None
+    qdy = qdyt = None
+    if needs[0] and needs[1]:
+        # one pass over dY for both operands
+        qdy, qdyt = ops.quant_dual_1x128_128x1(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed,
+                                               offset_rows=base + 2, offset_cols=base + 3, want_nan_rows=True)
     if needs[0]:
-        qdy = ops.quant_tile_1x128(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 2,
-                                   want_nan_rows=True)
+        if qdy is None:
+            qdy = ops.quant_tile_1x128(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 2,
+                                       want_nan_rows=True)
         _, qwt = ops.quant_block_128x128(weight, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 1,
                                          want_transposed=True)
         dx = ops.gemm_blockscaled(qdy, qwt, out_dtype=torch.float32 if dy2.dtype == torch.float32 else dy2.dtype)
     if needs[1]:
-        qdyt = ops.quant_tile_128x1_t(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 3,
-                                      want_nan_rows=True)
+        if qdyt is None:
+            qdyt = ops.quant_tile_128x1_t(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 3,
+                                          want_nan_rows=True)
         qxt = ops.quant_tile_128x1_t(x2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 4,
                                      want_nan_rows=True)
         dw = ops.gemm_blockscaled(qdyt, qxt, out_dtype=torch.float32 if dy2.dtype == torch.float32 else dy2.dtype)

@@ -220,6 +220,55 @@ def quant_tile_128x1_t(
     return QTensor(codes_t, scales, 1, kp, 0, grid_code(fmt), K, R, nan, dq)
 
 
+def quant_dual_1x128_128x1(
+    x: torch.Tensor,
+    *,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset_rows: int = 0,
+    offset_cols: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    want_nan_rows: bool = False,
+):
+    """One pass over x [R, K] giving (quant_tile_1x128(x), quant_tile_128x1_t(x)).
+
+    The two QTensors equal those of the two single-output calls with the same
+    arguments (SR offsets offset_rows and offset_cols).  Shapes the fused pass
+    does not take (K % 8 != 0, fp16 input, unaligned rows) run the two calls."""
+    _require_device(x)
+    x2 = _as_2d(x)
+    R, K = x2.shape
+    common = dict(fmt=fmt, bits=bits, rounding=rounding, seed=seed, scale_rule=scale_rule)
+    fused = (K % 8 == 0 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0
+             and x2.dtype in (torch.bfloat16, torch.float32))
+    if not fused or R * K == 0:
+        return (quant_tile_1x128(x2, offset=offset_rows, want_nan_rows=want_nan_rows, **common),
+                quant_tile_128x1_t(x2, offset=offset_cols, want_nan_rows=want_nan_rows, **common))
+    dev = x.device
+    T = cdiv(K, 128)
+    ldc = T * 128
+    rp = cdiv(R, 4) * 4
+    codes = torch.empty((R, ldc), dtype=torch.uint8, device=dev)
+    scales = torch.empty((T, rp), dtype=torch.float32, device=dev)
+    MB = cdiv(R, 128)
+    ldct = MB * 128
+    kp = cdiv(K, 4) * 4
+    codes_t = torch.empty((K, ldct), dtype=torch.uint8, device=dev)
+    scales_t = torch.empty((MB, kp), dtype=torch.float32, device=dev)
+    nan_r = torch.zeros(R, dtype=torch.int32, device=dev) if want_nan_rows else None
+    nan_c = torch.zeros(K, dtype=torch.int32, device=dev) if want_nan_rows else None
+    call(
+        "ntlb_quant_dual_1x128_128x1", x2.data_ptr(), _dtype_code(x2.dtype), R, K, x2.stride(0), grid_code(fmt),
+        (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset_rows, offset_cols,
+        codes.data_ptr(), ldc, scales.data_ptr(), 1, rp, _ptr(nan_r), codes_t.data_ptr(), ldct, scales_t.data_ptr(),
+        1, kp, _ptr(nan_c), _stream(),
+    )
+    return (QTensor(codes, scales, 1, rp, 0, grid_code(fmt), R, K, nan_r, None),
+            QTensor(codes_t, scales_t, 1, kp, 0, grid_code(fmt), K, R, nan_c, None))
+
+
 def quant_grouped(
     x: torch.Tensor,
     gr: int,

@@ -130,6 +130,40 @@ def test_tile_128x1_fast_path_special_columns(gpu_device, shape, dtype, fmt, gri
     assert np.array_equal(q.nan_rows.cpu().numpy(), nan_ref)
 
 
+@pytest.mark.parametrize("shape", [(300, 136), (1000, 384), (128, 8), (2, 264)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+def test_dual_1x128_128x1_parity(gpu_device, shape, dtype, fmt, grid, rname, rcode):
+    """The one-pass dY quantizer writes exactly the 1x128 and the 128x1
+    outputs of the oracle (and of the two single-output kernels)."""
+    from lowbit import ops
+
+    R, K = shape
+    x = seeded(shape, seed=20260111, std=1e-3, outliers=0.02).float()
+    x[R // 2, 1] = float("nan")
+    x[0, 3] = float("inf")
+    x[:, 5] = 0.0
+    x = x.to(dtype).to(gpu_device)
+    qr, qc = ops.quant_dual_1x128_128x1(x, fmt=fmt, rounding=rname, seed=9, offset_rows=2, offset_cols=3,
+                                        want_nan_rows=True)
+    torch.cuda.synchronize()
+    xn = to_np32(x)
+    codes, scales, qv, _ = O.quant_tile_1x128(xn, grid=grid, rounding=rcode, seed=9, offset=2)
+    assert_bits_equal(qr.codes.cpu().numpy(), codes, "1x128 codes")
+    assert_bits_equal(scales_row_major(qr, R, scales.shape[1]), scales, "1x128 scales")
+    assert np.array_equal(qr.nan_rows.cpu().numpy(), np.isnan(qv).any(axis=1).astype(np.int32))
+    ct, st, _, _ = O.quant_tile_128x1_t(xn, grid=grid, rounding=rcode, seed=9, offset=3)
+    assert_bits_equal(qc.codes.cpu().numpy(), ct, "128x1 codes_t")
+    assert_bits_equal(scales_row_major(qc, K, st.shape[1]), st, "128x1 scales")
+    assert np.array_equal(qc.nan_rows.cpu().numpy(), np.isnan(xn).any(axis=0).astype(np.int32))
+    q1 = ops.quant_tile_1x128(x, fmt=fmt, rounding=rname, seed=9, offset=2)
+    q2 = ops.quant_tile_128x1_t(x, fmt=fmt, rounding=rname, seed=9, offset=3)
+    assert torch.equal(q1.codes, qr.codes) and torch.equal(q2.codes, qc.codes)
+    # tile-major scale arrays pad rows to a multiple of 4; compare what is written
+    assert torch.equal(q1.scales[:, :R], qr.scales[:, :R]) and torch.equal(q2.scales[:, :K], qc.scales[:, :K])
+
+
 def test_c3_dy_128x1_full_size(gpu_device):
     """dY [8192, 18432] 128x1 tiles (the wgrad operand dY^T)."""
     from lowbit import ops, workloads
