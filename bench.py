@@ -63,6 +63,17 @@ def _time_ms(fn, n: int, warmup: int, stream) -> float:
     return ev[0].elapsed_time(ev[1]) / n
 
 
+def _calibration_copy(dev) -> None:
+    """A plain 1 GiB device copy: its FETCH_SIZE / WRITE_SIZE calibrate the HBM counters."""
+    import torch
+
+    a = torch.empty(1 << 29, dtype=torch.int16, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
 def other_config(args) -> dict:
     """One line for BASELINE configs 1, 3, 4, 5 (kernel times by HIP events)."""
     import torch
@@ -218,6 +229,8 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.config != "c2":
+        if args.calib_copy:
+            _calibration_copy(dev)
         print(json.dumps(other_config(args)))
         return
     shp = workloads.SHAPES[2]
@@ -291,11 +304,7 @@ def main():
     del ca, cb
 
     if args.calib_copy:
-        a = torch.empty(1 << 29, dtype=torch.int16, device=dev)
-        b = torch.empty_like(a)
-        for _ in range(3):
-            b.copy_(a)
-        torch.cuda.synchronize()
+        _calibration_copy(dev)
 
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE (calibrated
     # against a 1 GiB copy) for this workload, committed under profiles/
