@@ -158,35 +158,57 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   // workgroup -> output tile: undo the round-robin XCD dispatch so each XCD
   // walks a contiguous range, then a grouped raster (GROUP_M row-tiles)
   const int num_n = (int)((g.N + BN - 1) / BN);
-  const int nwg = (int)gridDim.x;
-  int pid = blockIdx.x;
-  {
-    const int xcd = pid & 7, local = pid >> 3;
+  // Workgroup pid runs on XCD pid % 8; xcd_local() renumbers the first nwg
+  // pids so each XCD walks a contiguous range of tiles (its own L2 then holds
+  // neighbouring tiles).  It is a bijection on [0, nwg).
+  auto xcd_local = [](int p, int nwg) {
+    const int xcd = p & 7, local = p >> 3;
     const int per = nwg >> 3, extra = nwg & 7;
-    pid = xcd * per + min(xcd, extra) + local;
-  }
+    return xcd * per + min(xcd, extra) + local;
+  };
+  int pid = blockIdx.x;
   int64_t m0, n0;
   if constexpr (GROUPED) {
-    // row tile mt of the concatenated per-expert tilings; n fastest so that
-    // consecutive workgroups share the A rows and sweep one expert's B
-    const int mt = pid / num_n;
-    n0 = (int64_t)(pid - mt * num_n) * BN;
-    int e = 0, before = 0;
+    // experts in order, each one's tiles in the grouped raster of the dense
+    // case (GROUP_M row tiles sweep all n tiles), so concurrent workgroups
+    // share both the expert's weight tiles and its activation rows in L2.
+    // The offset table is read once, in parallel, into LDS (the first stage
+    // buffer, free until the first copy) and searched there; a walk over
+    // global memory would be one dependent load per expert.
+    // The grid is an upper bound on the tile count, so the renumbering uses
+    // the real count: otherwise the idle tail of the grid would all land on
+    // the last XCDs.
+    int32_t* tab = reinterpret_cast<int32_t*>(lds_a0);
+    for (int i = tid; i <= g.n_experts; i += NTHREADS) tab[i] = g.offsets[i];
+    __syncthreads();
+    int total = 0;
+    for (int i = 0; i < g.n_experts; ++i) total += (int)((tab[i + 1] - tab[i] + BM - 1) / BM) * num_n;
+    if (pid < total) pid = xcd_local(pid, total);
+    int e = 0, before = 0, tiles_m = 0;
     int64_t lo = 0, hi = 0;
     for (; e < g.n_experts; ++e) {
-      lo = g.offsets[e];
-      hi = g.offsets[e + 1];
-      const int tiles = (int)((hi - lo + BM - 1) / BM);
-      if (mt < before + tiles) break;
-      before += tiles;
+      lo = tab[e];
+      hi = tab[e + 1];
+      tiles_m = (int)((hi - lo + BM - 1) / BM);
+      if (pid < before + tiles_m * num_n) break;
+      before += tiles_m * num_n;
     }
+    __syncthreads();  // the table's LDS is a copy target from here on
     if (e >= g.n_experts) return;  // beyond the last expert's tiles: the grid is an upper bound
-    m0 = lo + (int64_t)(mt - before) * BM;
+    constexpr int GROUP_M = 4;
+    const int l = pid - before;
+    const int group = l / (GROUP_M * num_n);
+    const int first_m = group * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in_group = l - group * GROUP_M * num_n;
+    m0 = lo + (int64_t)(first_m + in_group % gsize) * BM;
+    n0 = (int64_t)(in_group / gsize) * BN;
     g.M = hi;  // rows at or past the expert's end are not stored
     g.b += (int64_t)e * g.b_estride;
     g.sb += (int64_t)e * g.sb_estride;
     if (g.nan_b) g.nan_b += (int64_t)e * g.N;
   } else {
+    pid = xcd_local(pid, (int)gridDim.x);
     const int num_m = (int)((g.M + BM - 1) / BM);
     constexpr int GROUP_M = 4;
     const int group = pid / (GROUP_M * num_n);
@@ -445,6 +467,8 @@ extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t
   if (Kp == 0) return fail(NTLB_EUNSUPPORTED, "%s: K == 0", fn);
   if ((M_total + BM) * lda >= (int64_t)0x7FFFFFFF || (N + BN) * ldb >= (int64_t)0x7FFFFFFF)
     return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
+  if ((int64_t)(n_experts + 1) * 4 > TILE_A)
+    return fail(NTLB_EUNSUPPORTED, "%s: more than %d experts", fn, TILE_A / 4 - 1);
   const int64_t tiles = ((M_total + BM - 1) / BM + n_experts) * ((N + BN - 1) / BN);
   if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
   GemmArgs g;
