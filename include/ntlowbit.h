@@ -206,6 +206,45 @@ int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t lda, const
                                   void* stream);
 
 /*
+ * Gate and up projections of the SwiGLU expert MLP in one blockscaled GEMM,
+ * with h = silu(gate) * up and its 1x128 quantization in the epilogue.
+ * Replaces F.silu(self.gate_proj(x)) * self.up_proj(x) (moe.py:190-193) and
+ * the 1x128 quantization the down projection's backend applies to it
+ * (te_backend.py:82-110), so h never makes an HBM round trip in fp32 or bf16.
+ *   b, sb   interleaved weight: 128-row blocks gate block t, up block t, ...,
+ *           N = 2*I rows (I a multiple of 128), 128x128 block scales
+ *           (sb_row, sb_col) of the interleaved rows
+ *   h       optional bf16 [M, I] (row stride ldh): bf16(silu(g) * u) with
+ *           g, u the bf16-rounded projections and silu(x) = x / (1 + exp(-x))
+ *           in fp32 rounded to bf16, as F.silu on a bf16 tensor
+ *   hc, hs  h codes [M, ldhc] and scales hs[row*hs_row + tile*hs_col] with
+ *           the grid, qmax, rounding, scale rule and SR (seed, offset) of
+ *           ntlb_quant_tile_1x128 applied to h (SR keyed by row*I + column)
+ *   h_nan   optional per-row NaN flags of h
+ * nan_a / nan_b flag NaN rows of A and of the interleaved B as in
+ * ntlb_gemm_blockscaled.
+ */
+int ntlb_gemm_swiglu_quant(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row, int64_t sa_col,
+                           int a_shift, const uint8_t* b, int64_t ldb, const float* sb, int64_t sb_row,
+                           int64_t sb_col, int64_t M, int64_t N, int64_t Kp, const int32_t* nan_a,
+                           const int32_t* nan_b, uint16_t* h, int64_t ldh, uint8_t* hc, int64_t ldhc, float* hs,
+                           int64_t hs_row, int64_t hs_col, int32_t* h_nan, int qmax, int rounding, int scale_rule,
+                           uint64_t seed, uint64_t offset, void* stream);
+
+/*
+ * Per-expert form of ntlb_gemm_swiglu_quant over rows sorted by expert (the
+ * offsets table and expert strides of ntlb_gemm_grouped_blockscaled): the
+ * gate/up half of the expert loop of moe.py:888-962 for all local experts.
+ */
+int ntlb_gemm_grouped_swiglu_quant(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                   int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, int64_t b_estride,
+                                   const float* sb, int64_t sb_row, int64_t sb_col, int64_t sb_estride,
+                                   const int32_t* offsets, int n_experts, int64_t M_total, int64_t N, int64_t Kp,
+                                   const int32_t* nan_a, const int32_t* nan_b, uint16_t* h, int64_t ldh, uint8_t* hc,
+                                   int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col, int32_t* h_nan, int qmax,
+                                   int rounding, int scale_rule, uint64_t seed, uint64_t offset, void* stream);
+
+/*
  * NF4 refresh of a persistent weight (the flat tensor of n elements):
  * _quantize_nf4_persistent + _pack_nibbles (layers.py:130-139, :156-169).
  * One scale per run of `block` consecutive elements (K for per_channel on an

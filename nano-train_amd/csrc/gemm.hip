@@ -25,6 +25,7 @@
 
 #include "ntlb_device.h"
 #include "ntlb_host.h"
+#include "ntlb_quant8.h"
 
 namespace ntlb {
 
@@ -58,7 +59,24 @@ struct GemmArgs {
   const int32_t* offsets;
   int n_experts;
   int64_t b_estride, sb_estride;
+  // SwiGLU epilogue (EPI_SWIGLU): B's rows come in 128-row blocks alternating
+  // gate block t and up block t, so output tile columns [0,128) are gate and
+  // [128,256) up for h columns n0/2 + [0,128).  h = bf16(silu(bf16(gate)) *
+  // bf16(up)) is quantized per 1x128 tile (one tile per output tile row).
+  uint16_t* h;    // optional bf16 h [M, I], row stride ldh
+  int64_t ldh;
+  uint8_t* hc;    // h codes [M, ldhc]
+  int64_t ldhc;
+  float* hs;      // h scales: hs[row * hs_row + tile * hs_col]
+  int64_t hs_row, hs_col;
+  int32_t* h_nan;  // optional per-row NaN flags of h
+  float h_qmaxf;
+  int h_sr, h_scale_rule;
+  uint64_t h_seed, h_offset;
+  int64_t I;  // width of h = N / 2
 };
+
+constexpr int EPI_STORE = 0, EPI_SWIGLU = 1;
 
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int NTHREADS = 512;
@@ -143,7 +161,19 @@ __device__ __forceinline__ void issue_group(const StageSrc& s, uint8_t* lds_a, u
 // flight for the next K block do not alias the reads of the current one, and
 // keeps them in flight across the whole MFMA phase instead of waiting on them
 // before the first read.
-template <int GRID, bool B_UNIFORM, bool GROUPED>
+template <int GRID, bool SR>
+__device__ __forceinline__ void swiglu_quant_rows(const GemmArgs& g, const uint8_t* s0, const uint8_t* s1,
+                                                  const uint8_t* s2, const uint8_t* s3, int64_t m0, int64_t n0,
+                                                  int tid);
+
+// staged epilogue rows: slab k (one of the four 32 KiB stage buffers) holds
+// tile rows 64k .. 64k+63, 512 bytes each
+__device__ __forceinline__ uint8_t* slab_row(uint8_t* s0, uint8_t* s1, uint8_t* s2, uint8_t* s3, int r) {
+  const int k = r >> 6;
+  return (k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3) + (r & 63) * 512;
+}
+
+template <int GRID, bool B_UNIFORM, bool GROUPED, int EPI = EPI_STORE>
 __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[TILE_A];
   __shared__ __attribute__((aligned(16))) uint8_t lds_b0[TILE_B];
@@ -318,6 +348,39 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   }
 
+  if constexpr (EPI == EPI_SWIGLU) {
+    // Stage the whole 256x256 tile as bf16 (the reference's Linear outputs):
+    // slab k holds rows 64k..64k+63, 512 bytes per row, 16-byte units
+    // XOR-swizzled by row so 16 lanes on 16 rows hit distinct banks.
+#pragma unroll
+    for (int tm = 0; tm < 8; ++tm) {
+      const int r = wm * 128 + tm * 16 + (lane & 15);
+      const int64_t m = m0 + r;
+      const bool nan_row = g.nan_a && m < g.M && g.nan_a[m];
+      uint8_t* rowp = slab_row(lds_a0, lds_b0, lds_a1, lds_b1, r);
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn) {
+        const int c = wn * 64 + tn * 16 + (lane >> 4) * 4;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t n = n0 + c + q;
+          v[q] = acc[tm][tn][q];
+          if (nan_row || (g.nan_b && n < g.N && g.nan_b[n])) v[q] = __uint_as_float(0x7FC00000u);
+        }
+        *reinterpret_cast<uint2*>(rowp + (((c >> 3) ^ (r & 15)) << 4) + (c & 4) * 2) =
+            make_uint2((uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
+                       (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
+      }
+    }
+    __syncthreads();
+    if (g.h_sr)
+      swiglu_quant_rows<GRID, true>(g, lds_a0, lds_b0, lds_a1, lds_b1, m0, n0, tid);
+    else
+      swiglu_quant_rows<GRID, false>(g, lds_a0, lds_b0, lds_a1, lds_b1, m0, n0, tid);
+    return;
+  }
+
   // ---------------------------------------------------------------- epilogue
   // lane holds rows m = m0 + wm*128 + tm*16 + lane%16 and columns
   // n = n0 + wn*64 + tn*16 + 4*(lane/16) + r
@@ -388,6 +451,67 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       }
     }
     __syncthreads();
+  }
+}
+
+// Thread t finishes row t/2 of the staged tile, h columns 64*(t%2) + [0,64):
+// h = bf16(silu(gate) * up) with silu(x) = x / (1 + exp(-x)) in fp32 rounded
+// to bf16 (F.silu on a bf16 tensor), the 1x128 tile amax shared with the
+// partner lane t^1, then the tile's codes, scale, NaN flag and optional h.
+template <int GRID, bool SR>
+__device__ __forceinline__ void swiglu_quant_rows(const GemmArgs& g, const uint8_t* s0, const uint8_t* s1,
+                                                  const uint8_t* s2, const uint8_t* s3, int64_t m0, int64_t n0,
+                                                  int tid) {
+#pragma clang fp contract(off)
+  const int r = tid >> 1, hh = tid & 1;
+  const int64_t m = m0 + r;
+  const int64_t j0 = n0 / 2 + hh * 64;  // first h column of this thread
+  uint8_t* rowp = slab_row(const_cast<uint8_t*>(s0), const_cast<uint8_t*>(s1), const_cast<uint8_t*>(s2),
+                           const_cast<uint8_t*>(s3), r);
+  // pass 1: h in bf16, written back over this thread's own gate units (no
+  // other thread reads them), and the |h| maximum
+  uint32_t amax = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    uint8_t* gp = rowp + (((hh * 8 + k) ^ (r & 15)) << 4);
+    const uint4 gw = *reinterpret_cast<const uint4*>(gp);
+    const uint4 uw = *reinterpret_cast<const uint4*>(rowp + (((16 + hh * 8 + k) ^ (r & 15)) << 4));
+    const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w}, uu[4] = {uw.x, uw.y, uw.z, uw.w};
+    uint32_t hb[4];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const float gv = bf16_bits_to_f32((gg[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+      const float uv = bf16_bits_to_f32((uu[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+      const float sg = bf16_bits_to_f32(f32_to_bf16_bits(gv / (1.0f + expf(-gv))));
+      const uint32_t h = f32_to_bf16_bits(sg * uv);
+      amax = max(amax, (h & 0x7FFFu) << 16);
+      hb[q >> 1] = (q & 1) ? (hb[q >> 1] | (h << 16)) : h;
+    }
+    *reinterpret_cast<uint4*>(gp) = make_uint4(hb[0], hb[1], hb[2], hb[3]);
+  }
+  amax = max(amax, (uint32_t)__shfl_xor((int)amax, 1));
+  const float s = scale_from_amax_bits(amax, g.h_qmaxf, g.h_scale_rule);
+  const float rs = fast_div_ok<SR>(amax) ? 1.0f / s : 1.0f;
+  if (m >= g.M) return;
+  // pass 2: codes (and h) 8 columns at a time from the bf16 h in LDS
+  bool nan = false;
+  for (int k = 0; k < 8; ++k) {
+    const uint4 hw = *reinterpret_cast<const uint4*>(rowp + (((hh * 8 + k) ^ (r & 15)) << 4));
+    const uint32_t hh4[4] = {hw.x, hw.y, hw.z, hw.w};
+    float v[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = bf16_bits_to_f32((hh4[q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+    uint32_t rb[8];
+    sr_words<SR>((uint64_t)(m * g.I + j0 + k * 8), g.h_seed, g.h_offset, rb);
+    uint32_t lo, hi;
+    float q[8];
+    nan |= quant8_tile_rs<GRID, SR, false>(v, amax, s, rs, g.h_qmaxf, rb, lo, hi, q);
+    *reinterpret_cast<uint2*>(g.hc + m * g.ldhc + j0 + k * 8) = make_uint2(lo, hi);
+    if (g.h) *reinterpret_cast<uint4*>(g.h + m * g.ldh + j0 + k * 8) = hw;
+  }
+  if (hh == 0) {
+    g.hs[m * g.hs_row + (n0 / 256) * g.hs_col] = s;
+    if (nan && g.h_nan) atomicOr(g.h_nan + m, 1);
   }
 }
 
@@ -494,5 +618,117 @@ extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t
     else
       gemm_blockscaled_kernel<GRID_INT, false, true><<<grd, blk, 0, st>>>(g);
   }
+  return check_launch(fn);
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU + 1x128 quantization epilogue: the expert MLP's gate and up
+// projections (moe.py:190-193: F.silu(gate_proj(x)) * up_proj(x)) in one GEMM
+// over B rows interleaved in 128-row blocks (gate block t, then up block t),
+// writing h's 1x128 codes (the down projection's A operand) and optionally h.
+// ---------------------------------------------------------------------------
+static int swiglu_common(const char* fn, GemmArgs& g, int grid, int64_t N, uint16_t* h, int64_t ldh, uint8_t* hc,
+                         int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col, int32_t* h_nan, int qmax,
+                         int rounding, int scale_rule, uint64_t seed, uint64_t offset) {
+  if (N % 256) return fail(NTLB_EUNSUPPORTED, "%s: N = 2*I must be a multiple of 256 (I a multiple of 128)", fn);
+  const int64_t I = N / 2;
+  if (!hc || !hs) return fail(NTLB_EINVAL, "%s: NULL h codes or scales", fn);
+  if (ldhc < I || ldhc % 16 || !aligned(hc, 16))
+    return fail(NTLB_EINVAL, "%s: h codes need ldhc >= I, ldhc %% 16 == 0, 16-byte alignment", fn);
+  if (h && (ldh < I || ldh % 8 || !aligned(h, 16)))
+    return fail(NTLB_EINVAL, "%s: h needs ldh >= I, ldh %% 8 == 0, 16-byte alignment", fn);
+  if (grid == NTLB_GRID_INT && (qmax < 1 || qmax > 127)) return fail(NTLB_EINVAL, "%s: qmax outside [1, 127]", fn);
+  if (rounding != NTLB_ROUND_NEAREST && rounding != NTLB_ROUND_STOCHASTIC)
+    return fail(NTLB_EINVAL, "%s: bad rounding %d", fn, rounding);
+  if (scale_rule != NTLB_SCALE_AFTER_DIVIDE && scale_rule != NTLB_SCALE_BEFORE_DIVIDE)
+    return fail(NTLB_EINVAL, "%s: bad scale rule %d", fn, scale_rule);
+  g.h = h; g.ldh = ldh; g.hc = hc; g.ldhc = ldhc; g.hs = hs; g.hs_row = hs_row; g.hs_col = hs_col; g.h_nan = h_nan;
+  g.h_qmaxf = grid == NTLB_GRID_E4M3 ? 448.0f : (float)qmax;
+  g.h_sr = rounding == NTLB_ROUND_STOCHASTIC;
+  g.h_scale_rule = scale_rule;
+  g.h_seed = seed; g.h_offset = offset; g.I = I;
+  g.y = nullptr; g.y_dtype = NTLB_BF16; g.ldy = 0; g.vec_out = 0; g.bias = nullptr; g.bias_dtype = 0;
+  return NTLB_OK;
+}
+
+extern "C" int ntlb_gemm_swiglu_quant(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                      int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, const float* sb,
+                                      int64_t sb_row, int64_t sb_col, int64_t M, int64_t N, int64_t Kp,
+                                      const int32_t* nan_a, const int32_t* nan_b, uint16_t* h, int64_t ldh,
+                                      uint8_t* hc, int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col,
+                                      int32_t* h_nan, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                      uint64_t offset, void* stream) {
+  const char* fn = "ntlb_gemm_swiglu_quant";
+  if (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3) return fail(NTLB_EINVAL, "%s: bad grid %d", fn, grid);
+  if (M < 0 || N < 0 || Kp < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (Kp % 128 || Kp == 0) return fail(NTLB_EINVAL, "%s: Kp must be a positive multiple of 128", fn);
+  if (M == 0 || N == 0) return NTLB_OK;
+  if (!a || !b || !sa || !sb) return fail(NTLB_EINVAL, "%s: NULL operand", fn);
+  if (lda < Kp || ldb < Kp || (lda % 16) || (ldb % 16) || !aligned(a, 16) || !aligned(b, 16))
+    return fail(NTLB_EINVAL, "%s: code matrices need ld >= Kp, ld %% 16 == 0 and 16-byte alignment", fn);
+  if (!(a_shift == 0 || a_shift == 7)) return fail(NTLB_EINVAL, "%s: a_shift must be 0 or 7", fn);
+  if ((M + BM) * lda >= (int64_t)0x7FFFFFFF || (N + BN) * ldb >= (int64_t)0x7FFFFFFF)
+    return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  GemmArgs g;
+  g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
+  g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = 7;
+  g.M = M; g.N = N; g.Kp = Kp;
+  g.nan_a = nan_a; g.nan_b = nan_b;
+  g.offsets = nullptr; g.n_experts = 0; g.b_estride = 0; g.sb_estride = 0;
+  int rc = swiglu_common(fn, g, grid, N, h, ldh, hc, ldhc, hs, hs_row, hs_col, h_nan, qmax, rounding, scale_rule,
+                         seed, offset);
+  if (rc) return rc;
+  hipStream_t st = as_stream(stream);
+  dim3 grd((unsigned)tiles), blk(NTHREADS);
+  if (grid == NTLB_GRID_E4M3)
+    gemm_blockscaled_kernel<GRID_E4M3, true, false, EPI_SWIGLU><<<grd, blk, 0, st>>>(g);
+  else
+    gemm_blockscaled_kernel<GRID_INT, true, false, EPI_SWIGLU><<<grd, blk, 0, st>>>(g);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_grouped_swiglu_quant(int grid, const uint8_t* a, int64_t lda, const float* sa,
+                                              int64_t sa_row, int64_t sa_col, int a_shift, const uint8_t* b,
+                                              int64_t ldb, int64_t b_estride, const float* sb, int64_t sb_row,
+                                              int64_t sb_col, int64_t sb_estride, const int32_t* offsets,
+                                              int n_experts, int64_t M_total, int64_t N, int64_t Kp,
+                                              const int32_t* nan_a, const int32_t* nan_b, uint16_t* h, int64_t ldh,
+                                              uint8_t* hc, int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col,
+                                              int32_t* h_nan, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                              uint64_t offset, void* stream) {
+  const char* fn = "ntlb_gemm_grouped_swiglu_quant";
+  if (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3) return fail(NTLB_EINVAL, "%s: bad grid %d", fn, grid);
+  if (M_total < 0 || N < 0 || Kp < 0 || n_experts < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (Kp % 128 || Kp == 0) return fail(NTLB_EINVAL, "%s: Kp must be a positive multiple of 128", fn);
+  if (M_total == 0 || N == 0 || n_experts == 0) return NTLB_OK;
+  if (!a || !b || !sa || !sb || !offsets) return fail(NTLB_EINVAL, "%s: NULL operand", fn);
+  if (lda < Kp || ldb < Kp || (lda % 16) || (ldb % 16) || !aligned(a, 16) || !aligned(b, 16) ||
+      (b_estride % 16) || b_estride < N * ldb)
+    return fail(NTLB_EINVAL, "%s: code matrices need ld >= Kp, ld %% 16 == 0, 16-byte alignment and "
+                "b_estride >= N*ldb", fn);
+  if (!(a_shift == 0 || a_shift == 7)) return fail(NTLB_EINVAL, "%s: a_shift must be 0 or 7", fn);
+  if ((M_total + BM) * lda >= (int64_t)0x7FFFFFFF || (N + BN) * ldb >= (int64_t)0x7FFFFFFF)
+    return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
+  if ((int64_t)(n_experts + 1) * 4 > TILE_A)
+    return fail(NTLB_EUNSUPPORTED, "%s: more than %d experts", fn, TILE_A / 4 - 1);
+  const int64_t tiles = ((M_total + BM - 1) / BM + n_experts) * ((N + BN - 1) / BN);
+  if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  GemmArgs g;
+  g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
+  g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = 7;
+  g.M = M_total; g.N = N; g.Kp = Kp;
+  g.nan_a = nan_a; g.nan_b = nan_b;
+  g.offsets = offsets; g.n_experts = n_experts; g.b_estride = b_estride; g.sb_estride = sb_estride;
+  int rc = swiglu_common(fn, g, grid, N, h, ldh, hc, ldhc, hs, hs_row, hs_col, h_nan, qmax, rounding, scale_rule,
+                         seed, offset);
+  if (rc) return rc;
+  hipStream_t st = as_stream(stream);
+  dim3 grd((unsigned)tiles), blk(NTHREADS);
+  if (grid == NTLB_GRID_E4M3)
+    gemm_blockscaled_kernel<GRID_E4M3, true, true, EPI_SWIGLU><<<grd, blk, 0, st>>>(g);
+  else
+    gemm_blockscaled_kernel<GRID_INT, true, true, EPI_SWIGLU><<<grd, blk, 0, st>>>(g);
   return check_launch(fn);
 }

@@ -61,13 +61,17 @@ __device__ __forceinline__ Philox4 philox4x32_10(uint64_t group, uint64_t offset
   return o;
 }
 
-__device__ __forceinline__ float sr_uniform(uint32_t r) { return (float)(r >> 8) * 0x1p-24f; }
+__device__ __forceinline__ float sr_uniform(uint32_t r) {
+#pragma clang fp contract(off)
+  return (float)(r >> 8) * 0x1p-24f;
+}
 
 // ---------------------------------------------------------------------------
 // e4m3fn (OCP) encode / decode, bit-exact with torch's float8_e4m3fn cast on
 // the clamped range the quantizers use.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t e4m3_rne(float v) {
+#pragma clang fp contract(off)
   uint32_t bits = __float_as_uint(v);
   uint32_t sign = (bits >> 24) & 0x80u;
   uint32_t ab = bits & 0x7FFFFFFFu;
@@ -88,6 +92,7 @@ __device__ __forceinline__ uint32_t e4m3_rne(float v) {
 // floor(|v| + u) applied in units of the local e4m3 spacing, sign kept.
 // |v| <= 448 on entry (the callers clamp first).
 __device__ __forceinline__ uint32_t e4m3_sr(float v, float u) {
+#pragma clang fp contract(off)
   uint32_t bits = __float_as_uint(v);
   uint32_t sign = (bits >> 24) & 0x80u;
   uint32_t ab = bits & 0x7FFFFFFFu;
@@ -105,6 +110,7 @@ __device__ __forceinline__ uint32_t e4m3_sr(float v, float u) {
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
+#pragma clang fp contract(off)
   uint32_t ef = (c >> 3) & 0xFu, m = c & 7u;
   float v;
   if (ef == 0xFu && m == 7u) {
@@ -125,6 +131,7 @@ __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
 __device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
 
 __device__ __forceinline__ float scale_from_amax_bits(uint32_t amax_bits, float qmaxf, int rule) {
+#pragma clang fp contract(off)
   float amax = __uint_as_float(amax_bits);
   if (rule == SCALE_BEFORE_DIVIDE) {
     if (!(amax_bits < 0x7F800000u) || !(amax > 0.0f)) return 1.0f;
@@ -141,6 +148,7 @@ __device__ __forceinline__ float scale_from_amax_bits(uint32_t amax_bits, float 
 // ---------------------------------------------------------------------------
 template <int GRID, bool SR>
 __device__ __forceinline__ uint32_t quant_one(float x, float s, float qmaxf, uint32_t rbits, float& q) {
+#pragma clang fp contract(off)
   float v = x / s;
   if constexpr (GRID == GRID_INT) {
     float t;

@@ -1,0 +1,161 @@
+// Shared 8-element quantization helpers of the low-bit kernels: the Philox
+// stochastic-rounding words, the per-element reference path, and the fast
+// tile path (exact reciprocal division, hardware e4m3 convert).  Used by the
+// quantizers and by GEMM epilogues that quantize their output.  Every fp32
+// operation here rounds on its own (no contraction), as the reference's torch
+// ops do.
+#pragma once
+
+#include "ntlb_device.h"
+
+namespace ntlb {
+
+#ifndef NTLB_HW_FP8_CVT
+#define NTLB_HW_FP8_CVT 1
+#endif
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// v_pk_max_u16 on two packed halves
+__device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+
+// The 8 SR words for source elements e0 .. e0+7.
+template <bool SR>
+__device__ __forceinline__ void sr_words(uint64_t e0, uint64_t seed, uint64_t offset, uint32_t (&rb)[8]) {
+  if constexpr (SR) {
+    if ((e0 & 3u) == 0) {
+      Philox4 p0 = philox4x32_10(e0 >> 2, offset, seed);
+      Philox4 p1 = philox4x32_10((e0 >> 2) + 1, offset, seed);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rb[i] = p0.v[i];
+        rb[4 + i] = p1.v[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint64_t e = e0 + i;
+        Philox4 p = philox4x32_10(e >> 2, offset, seed);
+        uint32_t j = (uint32_t)(e & 3u);
+        rb[i] = j == 0 ? p.v[0] : (j == 1 ? p.v[1] : (j == 2 ? p.v[2] : p.v[3]));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rb[i] = 0;
+  }
+}
+
+// Quantize 8 values with one scale; returns the codes packed in two words
+// and whether any q was NaN.  Writes dq when requested.
+template <int GRID, bool SR>
+__device__ __forceinline__ bool quant8(const float (&v)[8], float s, float qmaxf, const uint32_t (&rb)[8],
+                                       uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+#pragma clang fp contract(off)
+  uint32_t c[8];
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    c[i] = quant_one<GRID, SR>(v[i], s, qmaxf, rb[i], q[i]);
+    nan |= (__float_as_uint(q[i]) & 0x7FFFFFFFu) > 0x7F800000u;
+  }
+  lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+  hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+  return nan;
+}
+
+// Quantize 8 values of a tile with scale s whose amax bits are m.  A tile
+// holding a NaN takes the per-element reference path (and reports it); every
+// other tile clamps with min/max, divides with the fast exact sequence when
+// its amax allows, and rounds to e4m3 in hardware when enabled.
+// The fast division is taken for round-to-nearest tiles whose amax bits lie in
+// [0x1A000000, 0x7B800000] (no NaN, no inf).
+template <bool SR>
+__device__ __forceinline__ bool fast_div_ok(uint32_t m) {
+  return !SR && m >= 0x1A000000u && m <= 0x7B800000u;
+}
+
+// rs is 1/s (IEEE, correctly rounded) wherever fast_div_ok(m) holds; it is
+// not read otherwise.
+template <int GRID, bool SR, bool DQ>
+__device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, float s, float rs, float qmaxf,
+                                               const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+#pragma clang fp contract(off)
+  if (m > 0x7F800000u) {
+    // NaN in the tile: reference semantics element by element
+    quant8<GRID, SR>(v, s, qmaxf, rb, lo, hi, q);
+    return true;
+  } else {
+    float vq[8];
+    // Round-to-nearest tiles with amax in [2^-75, 2^120]: x/s as
+    // y = x*r, e = fma(-y, s, x), q = fma(e, r, y) with r = 1/s and the sign
+    // of x; this equals the correctly rounded quotient wherever it can move
+    // a code (checked exhaustively on random operands).  Other tiles, and
+    // stochastic rounding, divide.
+    // no NaN reaches the clamp here (NaN tiles took the path above; x/s
+    // is finite or +-inf), so the single-instruction median is the clamp
+    if (fast_div_ok<SR>(m)) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float y = v[i] * rs;
+        const float e = __builtin_fmaf(-y, s, v[i]);
+        float z = __builtin_copysignf(__builtin_fmaf(e, rs, y), v[i]);
+        vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float z = v[i] / s;
+        vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
+      }
+    }
+    if constexpr (GRID == GRID_INT) {
+      uint32_t c[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float t;
+        if constexpr (SR) {
+          const float uu = sr_uniform(rb[i]);
+          t = (vq[i] >= 0.0f) ? __builtin_floorf(vq[i] + uu) : __builtin_ceilf(vq[i] - uu);
+        } else {
+          t = __builtin_rintf(vq[i]);
+        }
+        q[i] = t;
+        c[i] = (uint32_t)(int32_t)t & 0xFFu;
+      }
+      lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+      hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+    } else {
+      uint32_t c[8];
+      if constexpr (!SR && NTLB_HW_FP8_CVT) {
+        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[0], vq[1], 0, false);
+        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[2], vq[3], (int)lo, true);
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4], vq[5], 0, false);
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[6], vq[7], (int)hi, true);
+        c[0] = lo & 0xFF; c[1] = (lo >> 8) & 0xFF; c[2] = (lo >> 16) & 0xFF; c[3] = lo >> 24;
+        c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i] = SR ? e4m3_sr(vq[i], sr_uniform(rb[i])) : e4m3_rne(vq[i]);
+        lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+        hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+      }
+      if constexpr (DQ) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) q[i] = e4m3_to_f32(c[i]);
+      }
+    }
+  }
+  return false;
+}
+
+template <int GRID, bool SR, bool DQ>
+__device__ __forceinline__ bool quant8_tile(const float (&v)[8], uint32_t m, float s, float qmaxf,
+                                            const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+#pragma clang fp contract(off)
+  const float rs = fast_div_ok<SR>(m) ? 1.0f / s : 1.0f;
+  return quant8_tile_rs<GRID, SR, DQ>(v, m, s, rs, qmaxf, rb, lo, hi, q);
+}
+
+}  // namespace ntlb

@@ -51,6 +51,11 @@ SIGNATURES = {
                               _I64, _P, _I32, _P, _I32, _I64, _P, _P, _P],
     "ntlb_gemm_grouped_blockscaled": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I32,
                                       _I64, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P],
+    "ntlb_gemm_swiglu_quant": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
+                               _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _P, _I32, _I32, _I32, _U64, _U64, _P],
+    "ntlb_gemm_grouped_swiglu_quant": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I64,
+                                       _P, _I32, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _P,
+                                       _I32, _I32, _I32, _U64, _U64, _P],
     "ntlb_nf4_quant": [_P, _I32, _I64, _I64, _P, _P, _P, _P],
     "ntlb_nf4_dequant": [_P, _P, _I64, _I64, _P, _I32, _P],
     "ntlb_mxfp4_quant": [_P, _I32, _I64, _P, _P, _P],

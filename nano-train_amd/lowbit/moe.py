@@ -161,3 +161,67 @@ def grouped_linear(
                               want_nan_rows=True)
     return ops.gemm_grouped_blockscaled(qx, w_codes, w_scales, offsets, N=w_codes.shape[1],
                                         out_dtype=out_dtype or x_sorted.dtype, b_nan_rows=w_nan_rows)
+
+
+def interleave_gate_up(gate_codes: torch.Tensor, gate_scales: torch.Tensor, up_codes: torch.Tensor,
+                       up_scales: torch.Tensor, gate_nan: Optional[torch.Tensor] = None,
+                       up_nan: Optional[torch.Tensor] = None):
+    """Gate and up weight codes of the SwiGLU MLP (moe.py:160-177) interleaved in
+    128-row blocks, the B operand of ops.gemm_swiglu_quant.
+
+    Works on one expert ([I, Kp] codes, [I/128, Kp/128] scales) or a stack
+    ([E, I, Kp], [E, I/128, Kp/128]); 128x128 blocks move whole, so the block
+    scales stay valid.  Returns (codes, scales, nan_rows or None)."""
+    if gate_codes.shape != up_codes.shape or gate_scales.shape != up_scales.shape:
+        raise ValueError("gate and up weights must have the same shape")
+    I, Kp = gate_codes.shape[-2], gate_codes.shape[-1]
+    if I % 128:
+        raise ValueError(f"intermediate size {I} must be a multiple of 128")
+    lead = gate_codes.shape[:-2]
+    nb = I // 128
+    codes = torch.stack([gate_codes.reshape(*lead, nb, 128, Kp), up_codes.reshape(*lead, nb, 128, Kp)],
+                        dim=-3).reshape(*lead, 2 * I, Kp)
+    tb = gate_scales.shape[-1]
+    scales = torch.stack([gate_scales.reshape(*lead, nb, tb), up_scales.reshape(*lead, nb, tb)],
+                         dim=-2).reshape(*lead, 2 * nb, tb)
+    nan = None
+    if gate_nan is not None or up_nan is not None:
+        gn = gate_nan if gate_nan is not None else torch.zeros_like(up_nan)
+        un = up_nan if up_nan is not None else torch.zeros_like(gate_nan)
+        nan = torch.stack([gn.reshape(*lead, nb, 128), un.reshape(*lead, nb, 128)], dim=-2).reshape(*lead, 2 * I)
+    return codes.contiguous(), scales.contiguous(), nan
+
+
+def expert_mlp(
+    x_sorted: torch.Tensor,
+    offsets: torch.Tensor,
+    gate_up,
+    down,
+    *,
+    fmt: str = "e4m3",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    want_h: bool = False,
+):
+    """ExpertMLP.forward (moe.py:190-193) for all local experts at once.
+
+    x_sorted [T, H] rows sorted by expert, offsets int32 [E+1]; gate_up is
+    interleave_gate_up()'s (codes, scales, nan) of [E, 2I, Kp], down is
+    quantize_expert_weights()'s (codes, scales, nan) of [E, H, Ip].  Three
+    kernels: the 1x128 quantization of x, the gate/up GEMM with SwiGLU and the
+    1x128 quantization of h in its epilogue, the down GEMM.  Both projections
+    read one quantization of x (the reference quantizes x once per Linear;
+    with round to nearest the codes are the same).  Returns out [T, H] (and h
+    when want_h)."""
+    gu_codes, gu_scales, gu_nan = gate_up
+    d_codes, d_scales, d_nan = down
+    qx = ops.quant_tile_1x128(x_sorted, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
+                              want_nan_rows=True)
+    h, qh = ops.gemm_swiglu_quant(qx, gu_codes, gu_scales, offsets=offsets, fmt=fmt, bits=bits, rounding=rounding,
+                                  seed=seed, offset=offset + 1, want_h=want_h, want_nan_rows=True,
+                                  b_nan_rows=gu_nan)
+    out = ops.gemm_grouped_blockscaled(qh, d_codes, d_scales, offsets, N=d_codes.shape[1], out_dtype=x_sorted.dtype,
+                                       b_nan_rows=d_nan)
+    return (out, h) if want_h else out

@@ -400,3 +400,66 @@ def gemm_grouped_blockscaled(
         _ptr(a.nan_rows), _ptr(b_nan_rows), _stream(),
     )
     return out
+
+
+def gemm_swiglu_quant(
+    a: QTensor,
+    b_codes: torch.Tensor,
+    b_scales: torch.Tensor,
+    *,
+    offsets: Optional[torch.Tensor] = None,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    want_h: bool = True,
+    want_nan_rows: bool = False,
+    b_nan_rows: Optional[torch.Tensor] = None,
+):
+    """h = silu(X W_gate^T) * (X W_up^T) and its 1x128 quantization, in one GEMM.
+
+    b_codes / b_scales hold the gate and up weights interleaved in 128-row
+    blocks (moe.interleave_gate_up): [2I, Kp] and [2I/128, Kp/128], or per
+    expert [E, 2I, Kp] and [E, 2I/128, Kp/128] with rows of a sorted by expert
+    and offsets int32 [E+1].  Returns (h bf16 [M, I] or None, QTensor of h)."""
+    _require_device(a.codes, b_codes, b_scales)
+    grouped = offsets is not None
+    if grouped:
+        _require_device(offsets)
+        if offsets.dtype != torch.int32:
+            raise TypeError("offsets must be int32")
+        if b_codes.dim() != 3 or offsets.numel() != b_codes.shape[0] + 1:
+            raise ValueError("grouped weights must be [E, 2I, Kp] with offsets of E+1 entries")
+    elif b_codes.dim() != 2:
+        raise ValueError("dense weights must be [2I, Kp]")
+    N = b_codes.shape[-2]
+    if N % 256:
+        raise ValueError(f"2I = {N} must be a multiple of 256")
+    if b_codes.shape[-1] < a.Kp:
+        raise ValueError(f"weight codes {tuple(b_codes.shape)} are narrower than Kp={a.Kp}")
+    b_codes = b_codes.contiguous()
+    b_scales = b_scales.contiguous()
+    I = N // 2
+    M = a.rows
+    dev = a.codes.device
+    rp = cdiv(max(M, 1), 4) * 4
+    h = torch.empty((M, I), dtype=torch.bfloat16, device=dev) if want_h else None
+    hc = torch.empty((M, I), dtype=torch.uint8, device=dev)
+    hs = torch.empty((I // 128, rp), dtype=torch.float32, device=dev)
+    hn = torch.zeros(M, dtype=torch.int32, device=dev) if want_nan_rows else None
+    qmax = (1 << (bits - 1)) - 1
+    tail = (_ptr(a.nan_rows), _ptr(b_nan_rows), _ptr(h), I, hc.data_ptr(), I, hs.data_ptr(), 1, rp, _ptr(hn), qmax,
+            rounding_code(rounding), scale_rule, seed, offset, _stream())
+    if grouped:
+        E = b_codes.shape[0]
+        nb, tb = b_scales.shape[1], b_scales.shape[2]
+        call("ntlb_gemm_grouped_swiglu_quant", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(),
+             a.s_row, a.s_col, a.shift, b_codes.data_ptr(), b_codes.stride(1), b_codes.stride(0),
+             b_scales.data_ptr(), tb, 1, nb * tb, offsets.data_ptr(), E, M, N, a.Kp, *tail)
+    else:
+        tb = b_scales.shape[1]
+        call("ntlb_gemm_swiglu_quant", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
+             a.s_col, a.shift, b_codes.data_ptr(), b_codes.stride(0), b_scales.data_ptr(), tb, 1, M, N, a.Kp, *tail)
+    return h, QTensor(hc, hs, 1, rp, 0, a.grid, M, I, hn, None)

@@ -103,6 +103,12 @@ def c4_inputs(device="cpu", dtype=torch.bfloat16):
     return tokens, routing, w_up, w_down
 
 
+def c4_gate(device="cpu", dtype=torch.bfloat16):
+    """The SwiGLU gate weight of config 4's experts (same shape and law as W_up)."""
+    s = SHAPES[4]
+    return normal((s["experts"], s["inter"], s["hidden"]), std=0.006, seed=seed_for(4, 4), device=device, dtype=dtype)
+
+
 def c5_inputs(device="cpu", dtype=torch.bfloat16):
     s = SHAPES[5]
     w = normal((s["N"], s["K"]), std=0.02, seed=seed_for(5, 0), device=device, dtype=dtype)

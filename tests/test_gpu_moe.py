@@ -153,3 +153,99 @@ def test_c4_grouped_up_projection_full_size_sampled(gpu_device):
         _, _, _, xdq = O.quant_tile_1x128(to_np32(xs[rows]), grid=O.GRID_E4M3)
         _, _, _, wdq = O.quant_block_128x128(to_np32(w_up[e]), grid=O.GRID_E4M3)
         assert rel_fro_bf16(y[rows], O.gemm_ref(xdq, wdq)) <= 1e-3
+
+
+def _offsets(counts, device):
+    return torch.tensor(np.concatenate([[0], np.cumsum(counts)]), dtype=torch.int32, device=device)
+
+
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("fmt", ["e4m3", "int_grid"])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_swiglu_quant_matches_unfused(gpu_device, grouped, fmt, rounding):
+    """The gate/up GEMM with the SwiGLU + 1x128 epilogue equals, bit for bit,
+    two separate GEMMs, torch's F.silu(gate) * up on their bf16 outputs
+    (moe.py:191) and the 1x128 quantizer on that h: same accumulation order,
+    same exp and division, same roundings."""
+    import torch.nn.functional as F
+
+    from lowbit import moe, ops
+
+    H, I = 384, 256
+    counts = [300, 0, 17, 260, 129] if grouped else [300]
+    E, T = len(counts), sum(counts)
+    x = seeded((T, H), seed=20260601, outliers=0.01).to(gpu_device)
+    x[5, 7] = float("nan")
+    wg = seeded((E, I, H), seed=20260602, std=0.03).to(gpu_device)
+    wu = seeded((E, I, H), seed=20260603, std=0.03).to(gpu_device)
+    gc, gs, gn = moe.quantize_expert_weights(wg, fmt=fmt)
+    uc, us_, un = moe.quantize_expert_weights(wu, fmt=fmt)
+    codes, scales, nan = moe.interleave_gate_up(gc, gs, uc, us_, gn, un)
+    qx = ops.quant_tile_1x128(x, fmt=fmt, want_nan_rows=True)
+    kw = dict(fmt=fmt, rounding=rounding, seed=41, offset=9)
+    if grouped:
+        offs = _offsets(counts, gpu_device)
+        h, qh = ops.gemm_swiglu_quant(qx, codes, scales, offsets=offs, want_nan_rows=True, b_nan_rows=nan, **kw)
+        g_out = ops.gemm_grouped_blockscaled(qx, gc, gs, offs, N=I, b_nan_rows=gn)
+        u_out = ops.gemm_grouped_blockscaled(qx, uc, us_, offs, N=I, b_nan_rows=un)
+    else:
+        h, qh = ops.gemm_swiglu_quant(qx, codes[0], scales[0], want_nan_rows=True, b_nan_rows=nan[0], **kw)
+        qg = ops.QTensor(gc[0], gs[0].contiguous(), gs.shape[2], 1, 7, qx.grid, I, H, gn[0], None)
+        qu = ops.QTensor(uc[0], us_[0].contiguous(), us_.shape[2], 1, 7, qx.grid, I, H, un[0], None)
+        g_out = ops.gemm_blockscaled(qx, qg)
+        u_out = ops.gemm_blockscaled(qx, qu)
+    h_ref = F.silu(g_out) * u_out
+    q_ref = ops.quant_tile_1x128(h_ref, want_nan_rows=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(h.view(torch.int16), h_ref.view(torch.int16)), "h differs from the unfused path"
+    assert torch.equal(qh.codes, q_ref.codes)
+    assert torch.equal(qh.scales[:, :T], q_ref.scales[:, :T])
+    assert torch.equal(qh.nan_rows, q_ref.nan_rows)
+
+
+def test_expert_mlp_matches_oracle(gpu_device):
+    """ExpertMLP.forward (moe.py:190-193) for all experts, three kernels, against
+    the oracle pipeline (1x128 x, 128x128 weights, float64 GEMMs, bf16
+    projections, F.silu's formula, 1x128 h).  Checked in stages, each at the
+    1e-3 relative-Frobenius bar of one GEMM: h against the oracle's h, and the
+    output against the oracle's down projection of the GPU's h.  End to end
+    the bar is 5e-3: about 1% of the bf16 projections land one ulp away from
+    the float64 result (fp32 accumulation order), and re-quantizing h to 8-bit
+    codes turns a few of those into whole-code steps."""
+    from lowbit import moe
+
+    H, I = 512, 256
+    counts = [200, 64, 0, 311]
+    E, T = len(counts), sum(counts)
+    x = seeded((T, H), seed=20260611).to(gpu_device)
+    wg = seeded((E, I, H), seed=20260612, std=0.03).to(gpu_device)
+    wu = seeded((E, I, H), seed=20260613, std=0.03).to(gpu_device)
+    wd = seeded((E, H, I), seed=20260614, std=0.03).to(gpu_device)
+    gu = moe.interleave_gate_up(*moe.quantize_expert_weights(wg)[:2], *moe.quantize_expert_weights(wu)[:2])
+    dn = moe.quantize_expert_weights(wd)
+    offs = _offsets(counts, gpu_device)
+    out, h = moe.expert_mlp(x, offs, gu, dn, want_h=True)
+    torch.cuda.synchronize()
+
+    xn = to_np32(x)
+    hg = to_np32(h)
+    _, _, _, xdq = O.quant_tile_1x128(xn, grid=O.GRID_E4M3)
+    h_ref = np.zeros((T, I), dtype=np.float64)
+    out_from_gpu_h = np.zeros((T, H), dtype=np.float64)
+    out_ref = np.zeros((T, H), dtype=np.float64)
+    bounds = np.concatenate([[0], np.cumsum(counts)])
+    for e in range(E):
+        lo, hi = bounds[e], bounds[e + 1]
+        if hi == lo:
+            continue
+        dq = lambda w: O.quant_block_128x128(to_np32(w[e]), grid=O.GRID_E4M3)[3]  # noqa: E731
+        g = O.round_bf16(O.gemm_ref(xdq[lo:hi], dq(wg)).astype(np.float32))
+        u = O.round_bf16(O.gemm_ref(xdq[lo:hi], dq(wu)).astype(np.float32))
+        sg = O.round_bf16((g / (np.float32(1) + np.exp(-g))).astype(np.float32))
+        hh = O.round_bf16((sg * u).astype(np.float32))
+        h_ref[lo:hi] = hh
+        out_ref[lo:hi] = O.gemm_ref(O.quant_tile_1x128(hh, grid=O.GRID_E4M3)[3], dq(wd))
+        out_from_gpu_h[lo:hi] = O.gemm_ref(O.quant_tile_1x128(hg[lo:hi], grid=O.GRID_E4M3)[3], dq(wd))
+    assert rel_fro_bf16(h, h_ref) <= 1e-3
+    assert rel_fro_bf16(out, out_from_gpu_h) <= 1e-3
+    assert rel_fro_bf16(out, out_ref) <= 5e-3
