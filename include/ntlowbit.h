@@ -284,6 +284,30 @@ int ntlb_fp8_persistent_dequant(const uint8_t* codes, const float* scales, int64
                                 int out_dtype, void* stream);
 
 /*
+ * One AdamW step of DtypeConfiguredAdamW.step (optimizer_runtime.py:68-116)
+ * on fp32 main_param, exp_avg, exp_avg_sq [n] in place, with the gradient in
+ * grad_dtype, optionally writing the parameter copy in param_dtype
+ * (param.data.copy_(main_param_f.to(param.dtype))).  The float scalars are the
+ * reference's Python-double values cast to float32: beta1, 1-beta1, beta2,
+ * 1-beta2, eps, 1-lr*weight_decay, -lr/(1-beta1^step); inv_bc2_sqrt is
+ * (float)(1.0 / (1-beta2^step)^0.5), the reciprocal taken in double, since
+ * torch divides a tensor by a scalar as a multiplication by that reciprocal.
+ * The operations are those of the reference's torch ops on the GPU:
+ * add(alpha) = fma(alpha, b, a), addcmul = fma(value, t1*t2, self),
+ * addcdiv = fma(value, t1/t2, self), sqrt correctly rounded.
+ * refresh = 1 (NF4) or 2 (persistent FP8) also quantizes that parameter copy
+ * as refresh_persistent_lowbit_params does (layers.py:353-407), scale = amax
+ * of each block of `block` elements (a power of two in [8, 2048]), into the
+ * packed nibbles or e4m3 bytes `codes` and fp32 `scales`; refresh = 0 skips it.
+ * There is no reference function for the fusion (the reference refreshes in a
+ * second pass after the step).
+ */
+int ntlb_adamw_step_refresh(float* main_param, const void* grad, int grad_dtype, float* exp_avg, float* exp_avg_sq,
+                            void* param, int param_dtype, int64_t n, float beta1, float one_minus_beta1, float beta2,
+                            float one_minus_beta2, float inv_bc2_sqrt, float eps, float decay, float neg_step_size,
+                            int refresh, int64_t block, uint8_t* codes, float* scales, void* stream);
+
+/*
  * Dequant-fused GEMMs: Y[M, N] = X[M, K] (bf16) . deq(W)[N, K]^T with fp32
  * accumulation on bf16 MFMA, W dequantized in the B-tile prologue exactly as
  * ntlb_nf4_dequant / ntlb_mxfp4_dequant would (bf16 of value * scale).  The

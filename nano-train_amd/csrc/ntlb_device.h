@@ -203,6 +203,14 @@ __device__ __forceinline__ float load_elem(const void* p, int dtype, int64_t idx
   return ((const float*)p)[idx];
 }
 
+// v rounded to dtype (round to nearest even, as store_elem and torch's .to())
+// and widened back to fp32
+__device__ __forceinline__ float round_to_dtype(float v, int dtype) {
+  if (dtype == DT_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+  if (dtype == DT_F16) return __half2float(__float2half(v));
+  return v;
+}
+
 __device__ __forceinline__ void store_elem(void* p, int dtype, int64_t idx, float v) {
   if (dtype == DT_BF16) {
     ((uint16_t*)p)[idx] = f32_to_bf16_bits(v);

@@ -228,6 +228,115 @@ __global__ void __launch_bounds__(256) fp8p_dequant_kernel(const uint8_t* codes,
 }
 
 // ---------------------------------------------------------------------------
+// AdamW step fused with the persistent low-bit refresh.
+//
+// One pass over a parameter: the DtypeConfiguredAdamW update of
+// optimizer_runtime.py:68-116 on fp32 master, exp_avg and exp_avg_sq, the
+// parameter copy in its own dtype, and -- for scale blocks of at most 2048
+// elements -- the NF4 or persistent-FP8 codes and scales that
+// refresh_persistent_lowbit_params (layers.py:353-407) would compute from
+// that parameter copy.  The arithmetic is that of the reference's torch ops
+// on the GPU, operation for operation: add with alpha is fma(alpha, b, a),
+// addcmul is fma(value, t1*t2, self), addcdiv is fma(value, t1/t2, self), and
+// division by a scalar multiplies by its float reciprocal.  The host turns the
+// reference's Python-double scalars into the floats torch uses.
+// ---------------------------------------------------------------------------
+struct AdamArgs {
+  float* mp;  // fp32 master
+  const void* g;
+  int g_dtype;
+  float* m;
+  float* v;
+  void* p;  // optional parameter copy
+  int p_dtype;
+  int64_t n;
+  float b1, omb1, b2, omb2, inv_bc2_sqrt, eps, decay, neg_step;
+  int64_t block;  // power of two in [8, 2048]
+  uint8_t* codes;
+  float* scales;
+};
+
+enum RefreshFmt : int { REFRESH_NONE = 0, REFRESH_NF4 = 1, REFRESH_FP8 = 2 };
+
+template <int RF>
+__global__ void __launch_bounds__(256) adamw_refresh_kernel(AdamArgs a) {
+#pragma clang fp contract(off)
+  __shared__ uint32_t wave_amax[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + tid) * 8;
+  float w[8];  // the parameter in its dtype, as fp32
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t e = e0 + i;
+    w[i] = 0.0f;
+    if (e >= a.n) continue;
+    const float g = load_elem(a.g, a.g_dtype, e);
+    float m = a.m[e], v = a.v[e], p = a.mp[e];
+    m = m * a.b1;                               // exp_avg.mul_(beta1)
+    m = __builtin_fmaf(a.omb1, g, m);           // .add_(grad, alpha=1-beta1)
+    v = v * a.b2;                               // exp_avg_sq.mul_(beta2)
+    v = __builtin_fmaf(a.omb2, g * g, v);       // .addcmul_(grad, grad, value=1-beta2)
+    float d = __builtin_sqrtf(v);               // exp_avg_sq.sqrt()
+    d = d * a.inv_bc2_sqrt;                     // .div_(bias_correction2 ** 0.5)
+    d = d + a.eps;                              // .add_(eps)
+    p = p * a.decay;                            // main_param.mul_(1 - lr * weight_decay)
+    p = __builtin_fmaf(a.neg_step, m / d, p);   // .addcdiv_(exp_avg, denom, value=-step_size)
+    a.m[e] = m;
+    a.v[e] = v;
+    a.mp[e] = p;
+    if (a.p) store_elem(a.p, a.p_dtype, e, p);  // param.data.copy_(main_param_f.to(param.dtype))
+    const float pw = round_to_dtype(p, a.p_dtype);  // the tensor the refresh quantizes
+    w[i] = pw;
+    amax = max(amax, abs_bits(pw));  // NaN bits sort above every finite value
+  }
+  if constexpr (RF != REFRESH_NONE) {
+    // amax over the scale block: block/8 consecutive threads
+    const int gthreads = (int)(a.block >> 3);
+    for (int off = 1; off < gthreads && off < 64; off <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
+    if (gthreads > 64) {
+      if (lane == 0) wave_amax[wave] = amax;
+      __syncthreads();
+      const int wpg = gthreads >> 6;  // waves per group: 2 or 4
+      const int w0 = (wave / wpg) * wpg;
+      uint32_t mm = 0;
+      for (int i = 0; i < wpg; ++i) mm = max(mm, wave_amax[w0 + i]);
+      amax = mm;
+    }
+    if (e0 >= a.n) return;
+    // _safe_scale (layers.py:86-101): scale = amax; non-finite or 0 -> 1
+    const float amaxf = __uint_as_float(amax);
+    const float s = (amax < 0x7F800000u && amax != 0u) ? amaxf : 1.0f;
+    if ((tid & (gthreads - 1)) == 0) a.scales[e0 / a.block] = s;
+    if constexpr (RF == REFRESH_NF4) {
+      uint32_t idx[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float c = w[i] / s;
+        c = (c < -1.0f) ? -1.0f : c;
+        c = (c > 1.0f) ? 1.0f : c;
+        idx[i] = nf4_index(c);
+      }
+      const int64_t nbytes = (a.n + 1) / 2;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t bi = e0 / 2 + j;
+        if (bi < nbytes) a.codes[bi] = (uint8_t)(idx[2 * j] | (idx[2 * j + 1] << 4));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (e0 + i >= a.n) break;
+        float c = w[i] / s;
+        c = (c < -448.0f) ? -448.0f : c;
+        c = (c > 448.0f) ? 448.0f : c;
+        a.codes[e0 + i] = (uint8_t)e4m3_rne(c);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Dequant-fused GEMM  Y[M,N] = X[M,K] (bf16) . deq(W)[N,K]^T, fp32 accumulate.
 // 256x256 output tile, 8 waves of 128x64, K step 64 bf16 (128-byte rows, the
 // same swizzled tile layout as the fp8 kernel).  X tiles move global -> LDS
@@ -674,5 +783,42 @@ extern "C" int ntlb_fp8_persistent_dequant(const uint8_t* codes, const float* sc
   if (!codes || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
   fp8p_dequant_kernel<<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(codes, scales, n, block, out,
                                                                                      out_dtype);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_adamw_step_refresh(float* main_param, const void* grad, int grad_dtype, float* exp_avg,
+                                       float* exp_avg_sq, void* param, int param_dtype, int64_t n, float beta1,
+                                       float one_minus_beta1, float beta2, float one_minus_beta2, float inv_bc2_sqrt,
+                                       float eps, float decay, float neg_step_size, int refresh, int64_t block,
+                                       uint8_t* codes, float* scales, void* stream) {
+  const char* fn = "ntlb_adamw_step_refresh";
+  if (n < 0) return fail(NTLB_EINVAL, "%s: negative size", fn);
+  if (!valid_dtype(grad_dtype) || (param && !valid_dtype(param_dtype)))
+    return fail(NTLB_EINVAL, "%s: bad grad or param dtype", fn);
+  if (refresh != REFRESH_NONE && refresh != REFRESH_NF4 && refresh != REFRESH_FP8)
+    return fail(NTLB_EINVAL, "%s: bad refresh format %d", fn, refresh);
+  if (refresh != REFRESH_NONE) {
+    if (block < 8 || block > 2048 || (block & (block - 1)))
+      return fail(NTLB_EUNSUPPORTED, "%s: fused refresh needs a power-of-two block in [8, 2048]", fn);
+    if (!codes || !scales) return fail(NTLB_EINVAL, "%s: NULL codes or scales", fn);
+  }
+  if (n == 0) return NTLB_OK;
+  if (!main_param || !grad || !exp_avg || !exp_avg_sq) return fail(NTLB_EINVAL, "%s: NULL state", fn);
+  if (cdiv(cdiv(n, 8), 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
+  AdamArgs a;
+  a.mp = main_param; a.g = grad; a.g_dtype = grad_dtype; a.m = exp_avg; a.v = exp_avg_sq;
+  a.p = param; a.p_dtype = param ? param_dtype : NTLB_F32; a.n = n;
+  a.b1 = beta1; a.omb1 = one_minus_beta1; a.b2 = beta2; a.omb2 = one_minus_beta2; a.inv_bc2_sqrt = inv_bc2_sqrt;
+  a.eps = eps; a.decay = decay; a.neg_step = neg_step_size;
+  a.block = refresh != REFRESH_NONE ? block : 8;
+  a.codes = codes; a.scales = scales;
+  dim3 grd((unsigned)cdiv(cdiv(n, 8), 256)), blk(256);
+  hipStream_t st = as_stream(stream);
+  if (refresh == REFRESH_NF4)
+    adamw_refresh_kernel<REFRESH_NF4><<<grd, blk, 0, st>>>(a);
+  else if (refresh == REFRESH_FP8)
+    adamw_refresh_kernel<REFRESH_FP8><<<grd, blk, 0, st>>>(a);
+  else
+    adamw_refresh_kernel<REFRESH_NONE><<<grd, blk, 0, st>>>(a);
   return check_launch(fn);
 }

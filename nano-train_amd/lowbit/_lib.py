@@ -30,6 +30,7 @@ _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
 _U64 = ctypes.c_uint64
 _I32 = ctypes.c_int
+_F32 = ctypes.c_float
 
 # name -> argtypes, in the order of include/ntlowbit.h
 SIGNATURES = {
@@ -62,6 +63,8 @@ SIGNATURES = {
     "ntlb_mxfp4_dequant": [_P, _P, _I64, _P, _I32, _P],
     "ntlb_fp8_persistent_quant": [_P, _I32, _I64, _I64, _P, _P, _P, _P],
     "ntlb_fp8_persistent_dequant": [_P, _P, _I64, _I64, _P, _I32, _P],
+    "ntlb_adamw_step_refresh": [_P, _P, _I32, _P, _P, _P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F32, _F32,
+                                _F32, _I32, _I64, _P, _P, _P],
     "ntlb_gemm_nf4": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
 }

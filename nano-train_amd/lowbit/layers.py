@@ -159,6 +159,20 @@ class LowBitLinearMixin:
             return
         raise ValueError(f"Unsupported persistent low-bit mode: {mode}")
 
+    def _set_persistent_buffers(self, mode: str, codes: torch.Tensor, scales: torch.Tensor) -> None:
+        """Install codes and scales computed elsewhere (the fused optimizer step)
+        in the buffers and shapes refresh_persistent_lowbit_params writes."""
+        dev = self.weight.device
+        _, shape = P._block_and_scale_shape(self.weight, self._persistent_granularity())
+        self._persistent_scale = scales.reshape(shape)
+        self._persistent_numel = torch.tensor(int(self.weight.numel()), dtype=torch.int64, device=dev)
+        if mode == "fp8":
+            self._persistent_fp8_weight = codes.view(torch.float8_e4m3fn).reshape(self.weight.shape)
+            self._persistent_fp4_codes = torch.empty(0, dtype=torch.uint8, device=dev)
+        else:
+            self._persistent_fp4_codes = codes
+            self._persistent_fp8_weight = torch.empty(0, device=dev)
+
     def _persistent_weight_ste(self) -> torch.Tensor:
         """Weight used in forward, with a straight-through bridge to the master (layers.py:409-436)."""
         mode = self._persistent_mode()
