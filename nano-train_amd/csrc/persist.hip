@@ -39,15 +39,26 @@ enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1 };
 // NF4 index of c = clamp(w/s): the pair of codebook entries bracketing c
 // decides (every other entry is farther by at least the codebook gap); ties
 // go to the lower index; NaN gives 0 as torch.argmin does on an all-NaN row.
+// The codebook comes in as compile-time constants and the bracket is tracked
+// with selects, so the lookup never indexes memory.
 __device__ __forceinline__ uint32_t nf4_index(float c) {
-  int below = 0;
+  static constexpr float cb[16] = {-1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
+                                   -0.09105004f, 0.0f,         0.0795803f,   0.1609302f,  0.2461123f,   0.33791524f,
+                                   0.44070983f,  0.562617f,    0.72295684f,  1.0f};
+  uint32_t below = 0;
+  float lo = cb[0], hi = cb[1];
 #pragma unroll
-  for (int i = 1; i < 16; ++i) below += (kNF4[i] <= c) ? 1 : 0;
+  for (int i = 1; i < 16; ++i) {
+    const bool ge = cb[i] <= c;
+    below += ge ? 1u : 0u;
+    lo = ge ? cb[i] : lo;
+    hi = ge ? cb[i < 15 ? i + 1 : 15] : hi;
+  }
   if (!(c == c)) return 0;
   if (below >= 15) return 15;
-  const float d0 = fabsf(c - kNF4[below]);
-  const float d1 = fabsf(c - kNF4[below + 1]);
-  return (d1 < d0) ? (uint32_t)(below + 1) : (uint32_t)below;
+  const float d0 = fabsf(c - lo);
+  const float d1 = fabsf(c - hi);
+  return (d1 < d0) ? below + 1 : below;
 }
 
 // e2m1 round to nearest even with saturation; the sign of v is kept
@@ -258,83 +269,170 @@ struct AdamArgs {
 
 enum RefreshFmt : int { REFRESH_NONE = 0, REFRESH_NF4 = 1, REFRESH_FP8 = 2 };
 
+// Codes and scales of 8 consecutive values w[0..8) at e0 (thread tid of a
+// 256-thread workgroup covering 2048 consecutive elements), for power-of-two
+// scale blocks in [8, 2048]: the block amax is reduced over the block's
+// block/8 threads (shuffles, then LDS across waves), scale = amax with
+// _safe_scale (layers.py:86-101), then NF4 indices (layers.py:156-169) or
+// e4m3 of clamp(w/s, +-448) (layers.py:104-117).  Every thread of the
+// workgroup must call it (it may synchronize).
+template <int RF>
+__device__ __forceinline__ void refresh8(const float (&w)[8], uint32_t amax, int64_t e0, int64_t n, int64_t block,
+                                         uint8_t* codes, float* scales, uint32_t* wave_amax, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int gthreads = (int)(block >> 3);
+  for (int off = 1; off < gthreads && off < 64; off <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
+  if (gthreads > 64) {
+    if (lane == 0) wave_amax[wave] = amax;
+    __syncthreads();
+    const int wpg = gthreads >> 6;  // waves per block: 2 or 4
+    const int w0 = (wave / wpg) * wpg;
+    uint32_t mm = 0;
+    for (int i = 0; i < wpg; ++i) mm = max(mm, wave_amax[w0 + i]);
+    amax = mm;
+  }
+  if (e0 >= n) return;
+  const float s = (amax < 0x7F800000u && amax != 0u) ? __uint_as_float(amax) : 1.0f;
+  if ((tid & (gthreads - 1)) == 0) scales[e0 / block] = s;
+  const bool full = e0 + 8 <= n;
+  if constexpr (RF == REFRESH_NF4) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float c = w[i] / s;
+      c = (c < -1.0f) ? -1.0f : c;
+      c = (c > 1.0f) ? 1.0f : c;
+      word |= nf4_index(c) << (4 * i);
+    }
+    if (full) {
+      *reinterpret_cast<uint32_t*>(codes + e0 / 2) = word;
+    } else {
+      const int64_t nbytes = (n + 1) / 2;
+      for (int j = 0; j < 4; ++j)
+        if (e0 / 2 + j < nbytes) codes[e0 / 2 + j] = (uint8_t)(word >> (8 * j));
+    }
+  } else {
+    uint32_t c8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float c = w[i] / s;
+      c = (c < -448.0f) ? -448.0f : c;
+      c = (c > 448.0f) ? 448.0f : c;
+      c8[i] = e4m3_rne(c);
+    }
+    if (full) {
+      *reinterpret_cast<uint2*>(codes + e0) = make_uint2(c8[0] | (c8[1] << 8) | (c8[2] << 16) | (c8[3] << 24),
+                                                         c8[4] | (c8[5] << 8) | (c8[6] << 16) | (c8[7] << 24));
+    } else {
+      for (int i = 0; i < 8; ++i)
+        if (e0 + i < n) codes[e0 + i] = (uint8_t)c8[i];
+    }
+  }
+}
+
+// 8 consecutive values at e0 as fp32: one or two 16-byte loads when all 8 lie
+// inside [0, n) (e0 % 8 == 0 keeps them aligned), else element by element
+__device__ __forceinline__ void load8f(const void* p, int dtype, int64_t e0, int64_t n, float (&v)[8]) {
+  if (e0 + 8 <= n) {
+    if (dtype == DT_F32) {
+      const float4 a = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + e0)[0];
+      const float4 b = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + e0)[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+      return;
+    }
+    const uint4 r = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(p) + e0);
+    const uint32_t u[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (dtype == DT_BF16) {
+        v[2 * i] = bf16_bits_to_f32(u[i] & 0xFFFFu);
+        v[2 * i + 1] = bf16_bits_to_f32(u[i] >> 16);
+      } else {
+        v[2 * i] = __half2float(__ushort_as_half((unsigned short)(u[i] & 0xFFFFu)));
+        v[2 * i + 1] = __half2float(__ushort_as_half((unsigned short)(u[i] >> 16)));
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (e0 + i < n) ? load_elem(p, dtype, e0 + i) : 0.0f;
+}
+
+__device__ __forceinline__ void store8f(float* p, int64_t e0, int64_t n, const float (&v)[8]) {
+  if (e0 + 8 <= n) {
+    reinterpret_cast<float4*>(p + e0)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p + e0)[1] = make_float4(v[4], v[5], v[6], v[7]);
+    return;
+  }
+  for (int i = 0; i < 8; ++i)
+    if (e0 + i < n) p[e0 + i] = v[i];
+}
+
 template <int RF>
 __global__ void __launch_bounds__(256) adamw_refresh_kernel(AdamArgs a) {
 #pragma clang fp contract(off)
   __shared__ uint32_t wave_amax[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int64_t e0 = ((int64_t)blockIdx.x * 256 + tid) * 8;
-  float w[8];  // the parameter in its dtype, as fp32
+  float g[8], m[8], v[8], p[8], w[8];
+  load8f(a.g, a.g_dtype, e0, a.n, g);
+  load8f(a.m, DT_F32, e0, a.n, m);
+  load8f(a.v, DT_F32, e0, a.n, v);
+  load8f(a.mp, DT_F32, e0, a.n, p);
   uint32_t amax = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int64_t e = e0 + i;
-    w[i] = 0.0f;
-    if (e >= a.n) continue;
-    const float g = load_elem(a.g, a.g_dtype, e);
-    float m = a.m[e], v = a.v[e], p = a.mp[e];
-    m = m * a.b1;                               // exp_avg.mul_(beta1)
-    m = __builtin_fmaf(a.omb1, g, m);           // .add_(grad, alpha=1-beta1)
-    v = v * a.b2;                               // exp_avg_sq.mul_(beta2)
-    v = __builtin_fmaf(a.omb2, g * g, v);       // .addcmul_(grad, grad, value=1-beta2)
-    float d = __builtin_sqrtf(v);               // exp_avg_sq.sqrt()
-    d = d * a.inv_bc2_sqrt;                     // .div_(bias_correction2 ** 0.5)
-    d = d + a.eps;                              // .add_(eps)
-    p = p * a.decay;                            // main_param.mul_(1 - lr * weight_decay)
-    p = __builtin_fmaf(a.neg_step, m / d, p);   // .addcdiv_(exp_avg, denom, value=-step_size)
-    a.m[e] = m;
-    a.v[e] = v;
-    a.mp[e] = p;
-    if (a.p) store_elem(a.p, a.p_dtype, e, p);  // param.data.copy_(main_param_f.to(param.dtype))
-    const float pw = round_to_dtype(p, a.p_dtype);  // the tensor the refresh quantizes
-    w[i] = pw;
-    amax = max(amax, abs_bits(pw));  // NaN bits sort above every finite value
+    m[i] = m[i] * a.b1;                                  // exp_avg.mul_(beta1)
+    m[i] = __builtin_fmaf(a.omb1, g[i], m[i]);           // .add_(grad, alpha=1-beta1)
+    v[i] = v[i] * a.b2;                                  // exp_avg_sq.mul_(beta2)
+    v[i] = __builtin_fmaf(a.omb2, g[i] * g[i], v[i]);    // .addcmul_(grad, grad, value=1-beta2)
+    float d = __builtin_sqrtf(v[i]);                     // exp_avg_sq.sqrt()
+    d = d * a.inv_bc2_sqrt;                              // .div_(bias_correction2 ** 0.5)
+    d = d + a.eps;                                       // .add_(eps)
+    p[i] = p[i] * a.decay;                               // main_param.mul_(1 - lr * weight_decay)
+    p[i] = __builtin_fmaf(a.neg_step, m[i] / d, p[i]);   // .addcdiv_(exp_avg, denom, value=-step_size)
+    w[i] = round_to_dtype(p[i], a.p_dtype);              // the tensor the refresh quantizes
+    if (e0 + i < a.n) amax = max(amax, abs_bits(w[i]));  // NaN bits sort above every finite value
   }
-  if constexpr (RF != REFRESH_NONE) {
-    // amax over the scale block: block/8 consecutive threads
-    const int gthreads = (int)(a.block >> 3);
-    for (int off = 1; off < gthreads && off < 64; off <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
-    if (gthreads > 64) {
-      if (lane == 0) wave_amax[wave] = amax;
-      __syncthreads();
-      const int wpg = gthreads >> 6;  // waves per group: 2 or 4
-      const int w0 = (wave / wpg) * wpg;
-      uint32_t mm = 0;
-      for (int i = 0; i < wpg; ++i) mm = max(mm, wave_amax[w0 + i]);
-      amax = mm;
-    }
-    if (e0 >= a.n) return;
-    // _safe_scale (layers.py:86-101): scale = amax; non-finite or 0 -> 1
-    const float amaxf = __uint_as_float(amax);
-    const float s = (amax < 0x7F800000u && amax != 0u) ? amaxf : 1.0f;
-    if ((tid & (gthreads - 1)) == 0) a.scales[e0 / a.block] = s;
-    if constexpr (RF == REFRESH_NF4) {
-      uint32_t idx[8];
+  store8f(a.m, e0, a.n, m);
+  store8f(a.v, e0, a.n, v);
+  store8f(a.mp, e0, a.n, p);
+  if (a.p) {  // param.data.copy_(main_param_f.to(param.dtype))
+    if (a.p_dtype == DT_F32) {
+      store8f(reinterpret_cast<float*>(a.p), e0, a.n, p);
+    } else if (a.p_dtype == DT_BF16 && e0 + 8 <= a.n) {
+      uint32_t u[4];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float c = w[i] / s;
-        c = (c < -1.0f) ? -1.0f : c;
-        c = (c > 1.0f) ? 1.0f : c;
-        idx[i] = nf4_index(c);
-      }
-      const int64_t nbytes = (a.n + 1) / 2;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int64_t bi = e0 / 2 + j;
-        if (bi < nbytes) a.codes[bi] = (uint8_t)(idx[2 * j] | (idx[2 * j + 1] << 4));
-      }
+      for (int i = 0; i < 4; ++i)
+        u[i] = (uint32_t)f32_to_bf16_bits(p[2 * i]) | ((uint32_t)f32_to_bf16_bits(p[2 * i + 1]) << 16);
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.p) + e0) = make_uint4(u[0], u[1], u[2], u[3]);
     } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        if (e0 + i >= a.n) break;
-        float c = w[i] / s;
-        c = (c < -448.0f) ? -448.0f : c;
-        c = (c > 448.0f) ? 448.0f : c;
-        a.codes[e0 + i] = (uint8_t)e4m3_rne(c);
-      }
+      for (int i = 0; i < 8; ++i)
+        if (e0 + i < a.n) store_elem(a.p, a.p_dtype, e0 + i, p[i]);
     }
   }
+  if constexpr (RF != REFRESH_NONE) refresh8<RF>(w, amax, e0, a.n, a.block, a.codes, a.scales, wave_amax, tid);
 }
+
+// One-pass block quantizer of a flat tensor for power-of-two blocks in
+// [8, 2048]: the persistent NF4 / FP8 quantization without the separate amax
+// pass and its atomics.
+template <int RF>
+__global__ void __launch_bounds__(256) quant_blocks_onepass(const void* w_in, int w_dtype, int64_t n, int64_t block,
+                                                            uint8_t* codes, float* scales) {
+  __shared__ uint32_t wave_amax[4];
+  const int tid = threadIdx.x;
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + tid) * 8;
+  float w[8];
+  load8f(w_in, w_dtype, e0, n, w);
+  uint32_t amax = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    if (e0 + i < n) amax = max(amax, abs_bits(w[i]));
+  refresh8<RF>(w, amax, e0, n, block, codes, scales, wave_amax, tid);
+}
+
+static bool onepass_block(int64_t block) { return block >= 8 && block <= 2048 && (block & (block - 1)) == 0; }
 
 // ---------------------------------------------------------------------------
 // Dequant-fused GEMM  Y[M,N] = X[M,K] (bf16) . deq(W)[N,K]^T, fp32 accumulate.
@@ -649,6 +747,12 @@ extern "C" int ntlb_nf4_quant(const void* w, int w_dtype, int64_t n, int64_t blo
   if (n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad size or block", fn);
   if (n == 0) return NTLB_OK;
   if (!w || !amax_ws || !packed || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (onepass_block(block) && aligned(w, 16)) {
+    if (cdiv(cdiv(n, 8), 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
+    quant_blocks_onepass<REFRESH_NF4><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(
+        w, w_dtype, n, block, packed, scales);
+    return check_launch(fn);
+  }
   const int64_t nb = cdiv(n, block);
   const int64_t threads = cdiv(n, 8);
   if (cdiv(threads, 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
@@ -756,6 +860,12 @@ extern "C" int ntlb_fp8_persistent_quant(const void* w, int w_dtype, int64_t n, 
   if (!valid_dtype(w_dtype) || n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad argument", fn);
   if (n == 0) return NTLB_OK;
   if (!w || !amax_ws || !codes || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (onepass_block(block) && aligned(w, 16)) {
+    if (cdiv(cdiv(n, 8), 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
+    quant_blocks_onepass<REFRESH_FP8><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(
+        w, w_dtype, n, block, codes, scales);
+    return check_launch(fn);
+  }
   const int64_t nb = cdiv(n, block);
   dim3 grd((unsigned)cdiv(cdiv(n, 8), 256)), blk(256);
   hipStream_t st = as_stream(stream);
