@@ -188,6 +188,30 @@ int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* 
                           const int32_t* nan_b, void* stream);
 
 /*
+ * ntlb_gemm_blockscaled with a workspace for the tail of the tiling (the
+ * same product as te_backend.py:253-259).  256x256 output tiles run one per
+ * compute unit; when the tiles past the last whole wave would leave at least
+ * half the compute units idle, each of them is split into 2..8 K ranges whose
+ * fp32 partials meet in the workspace and are summed in a fixed order by the
+ * last range to finish (deterministic; no waiting on other workgroups).
+ *   workspace  256-byte aligned device memory of ws_bytes, ZEROED once before
+ *              its first use; every call leaves it ready for the next.  Calls
+ *              that may run concurrently need separate workspaces.
+ *   ws_bytes   at least ntlb_gemm_workspace_bytes(M, N, Kp), else (or with a
+ *              null workspace) the call runs unsplit like ntlb_gemm_blockscaled.
+ */
+int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                             int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, const float* sb,
+                             int64_t sb_row, int64_t sb_col, int b_shift, int64_t M, int64_t N, int64_t Kp,
+                             const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                             const int32_t* nan_a, const int32_t* nan_b, void* workspace, int64_t ws_bytes,
+                             void* stream);
+
+/* Workspace bytes ntlb_gemm_blockscaled_ws uses for this shape on the current
+ * device (0: the shape runs unsplit). */
+int64_t ntlb_gemm_workspace_bytes(int64_t M, int64_t N, int64_t Kp);
+
+/*
  * Grouped (per-expert) blockwise-scaled GEMM over a token-offset table.
  * Replaces the per-expert loop of _run_local_experts (moe.py:888-962) /
  * _forward_single_rank (moe.py:1062-1097) in which every expert's Linear runs

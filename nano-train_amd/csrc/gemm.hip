@@ -21,6 +21,7 @@
 // LDS and writes full 128-byte row segments.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "ntlb_device.h"
@@ -74,6 +75,13 @@ struct GemmArgs {
   int h_sr, h_scale_rule;
   uint64_t h_seed, h_offset;
   int64_t I;  // width of h = N / 2
+  // Split-K tail (dense, EPI_STORE): workgroups at or past split_base take K
+  // chunk (q % split_s) of tile split_base + q / split_s, q = pid - split_base;
+  // the chunks' fp32 partials meet in ws and the last one to finish sums them
+  // in chunk order and stores the tile.
+  int split_base, split_s;
+  float* ws;             // [tail tiles][split_s][NTHREADS * 128] fp32
+  uint32_t* ws_count;    // per tail tile; zero between calls (the kernel resets it)
 };
 
 constexpr int EPI_STORE = 0, EPI_SWIGLU = 1;
@@ -173,6 +181,33 @@ __device__ __forceinline__ uint8_t* slab_row(uint8_t* s0, uint8_t* s1, uint8_t* 
   return (k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3) + (r & 63) * 512;
 }
 
+// acc = sum over chunks c = 0..S-1, in that order, of the partial tiles at
+// part + c * NTHREADS * 32 (float4 units, this thread's slot 0).  Rounds of 32
+// loads are in flight at once; acc is rebuilt slot by slot, so only the slots
+// already summed stay live beside the loads.
+template <int S>
+__device__ __forceinline__ void sum_partials(v4f (&acc)[8][4], const float4* part) {
+  constexpr int SLOTS = 32 / S;
+#pragma unroll
+  for (int r = 0; r < 32; r += SLOTS) {
+    float4 v[S][SLOTS];
+#pragma unroll
+    for (int c = 0; c < S; ++c)
+#pragma unroll
+      for (int k = 0; k < SLOTS; ++k)
+        if (r + k < 32) v[c][k] = part[(int64_t)c * NTHREADS * 32 + (r + k) * NTHREADS];
+#pragma unroll
+    for (int k = 0; k < SLOTS; ++k) {
+      if (r + k < 32) {
+        v4f t = (v4f){v[0][k].x, v[0][k].y, v[0][k].z, v[0][k].w};
+#pragma unroll
+        for (int c = 1; c < S; ++c) t += (v4f){v[c][k].x, v[c][k].y, v[c][k].z, v[c][k].w};
+        acc[(r + k) >> 2][(r + k) & 3] = t;
+      }
+    }
+  }
+}
+
 template <int GRID, bool B_UNIFORM, bool GROUPED, int EPI = EPI_STORE>
 __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[TILE_A];
@@ -197,6 +232,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     return xcd * per + min(xcd, extra) + local;
   };
   int pid = blockIdx.x;
+  int split_tail = -1, split_chunk = 0;
   int64_t m0, n0;
   if constexpr (GROUPED) {
     // experts in order, each one's tiles in the grouped raster of the dense
@@ -238,7 +274,14 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     g.sb += (int64_t)e * g.sb_estride;
     if (g.nan_b) g.nan_b += (int64_t)e * g.N;
   } else {
-    pid = xcd_local(pid, (int)gridDim.x);
+    if (g.split_s > 1 && pid >= g.split_base) {
+      const int q = pid - g.split_base;
+      split_tail = q / g.split_s;
+      split_chunk = q - split_tail * g.split_s;
+      pid = g.split_base + split_tail;
+    } else {
+      pid = xcd_local(pid, g.split_s > 1 ? g.split_base : (int)gridDim.x);
+    }
     const int num_m = (int)((g.M + BM - 1) / BM);
     constexpr int GROUP_M = 4;
     const int group = pid / (GROUP_M * num_n);
@@ -256,6 +299,9 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   const int64_t s_step = own_a ? g.sa_col : g.sb_col;
 
   const int nk = (int)(g.Kp / BK);
+  // K blocks [kb0, kb1) of this workgroup: all of them, or one split chunk
+  const int kb0 = split_tail >= 0 ? (int)((int64_t)split_chunk * nk / g.split_s) : 0;
+  const int kb1 = split_tail >= 0 ? (int)((int64_t)(split_chunk + 1) * nk / g.split_s) : nk;
 
   StageSrc src;
   {
@@ -276,8 +322,8 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-  for (int j = 0; j < 4; ++j) issue_group(src, lds_a0, lds_b0, 0, wave, j);
-  lds_s0[tid] = s_src[0];
+  for (int j = 0; j < 4; ++j) issue_group(src, lds_a0, lds_b0, kb0, wave, j);
+  lds_s0[tid] = s_src[(int64_t)kb0 * s_step];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -290,7 +336,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     // The copies into the idle stage are unconditional so the step is one
     // basic block: on the last K block they reload block kt (in bounds) into
     // the stage nobody reads again before the epilogue's barrier.
-    const int kn = min(kt + 1, nk - 1);
+    const int kn = min(kt + 1, kb1 - 1);
     const float s_next = s_src[(int64_t)kn * s_step];
 
     v8i bf[4];
@@ -343,9 +389,45 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     __syncthreads();
   };
 
-  for (int kt = 0; kt < nk; kt += 2) {
+  for (int kt = kb0; kt < kb1; kt += 2) {
     step(std::integral_constant<int, 0>(), kt);
-    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+    if (kt + 1 < kb1) step(std::integral_constant<int, 1>(), kt + 1);
+  }
+
+  if constexpr (!GROUPED && EPI == EPI_STORE) {
+    if (split_tail >= 0) {
+      // publish this chunk's partial tile; the last chunk to arrive sums all
+      // of them in chunk order (the same order every call) and stores the tile
+      constexpr int PART4 = NTHREADS * 32;  // float4 per partial tile
+      float4* part = reinterpret_cast<float4*>(g.ws) + (int64_t)split_tail * g.split_s * PART4 + tid;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          part[(int64_t)split_chunk * PART4 + (i * 4 + j) * NTHREADS] =
+              make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      // every wave's stores are complete in this XCD's L2 after the barrier;
+      // one agent-scope release then writes them back before the count
+      __syncthreads();
+      __shared__ int last;
+      if (tid == 0)
+        last = __hip_atomic_fetch_add(g.ws_count + split_tail, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(g.split_s - 1);
+      __syncthreads();
+      if (!last) return;
+      if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __syncthreads();
+      switch (g.split_s) {
+        case 2: sum_partials<2>(acc, part); break;
+        case 3: sum_partials<3>(acc, part); break;
+        case 4: sum_partials<4>(acc, part); break;
+        case 5: sum_partials<5>(acc, part); break;
+        case 6: sum_partials<6>(acc, part); break;
+        case 7: sum_partials<7>(acc, part); break;
+        default: sum_partials<8>(acc, part); break;
+      }
+      if (tid == 0) atomicExch(g.ws_count + split_tail, 0u);  // ready for the next call
+    }
   }
 
   if constexpr (EPI == EPI_SWIGLU) {
@@ -519,11 +601,61 @@ __device__ __forceinline__ void swiglu_quant_rows(const GemmArgs& g, const uint8
 
 using namespace ntlb;
 
-extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
-                                     int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, const float* sb,
-                                     int64_t sb_row, int64_t sb_col, int b_shift, int64_t M, int64_t N, int64_t Kp,
-                                     const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
-                                     const int32_t* nan_a, const int32_t* nan_b, void* stream) {
+// Split plan of the tail of a dense tiling: tiles past the last whole wave
+// (one workgroup per CU) are cut into split_s K chunks when that fills the
+// idle CUs; split_s = 1 means no split.
+struct SplitPlan {
+  int base, s, tail;
+};
+
+static int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cus[dev] = c;
+  }
+  return cus[dev];
+}
+
+static SplitPlan split_plan(int64_t tiles, int nk) {
+  SplitPlan p{(int)tiles, 1, 0};
+  const int64_t cus = device_cus();
+  const int64_t full = (tiles / cus) * cus, rem = tiles - full;
+  if (rem == 0 || rem * 2 > cus) return p;
+  int s = (int)std::min<int64_t>(cus / rem, 8);
+  s = std::min(s, nk / 2);
+  if (s < 2) return p;
+  p.base = (int)full;
+  p.s = s;
+  p.tail = (int)rem;
+  return p;
+}
+
+// workspace layout: one uint32 counter per tail tile (padded to 256 bytes),
+// then the fp32 partials [tail][s][NTHREADS * 128]
+static int64_t split_count_bytes(const SplitPlan& p) { return ((int64_t)p.tail * 4 + 255) / 256 * 256; }
+
+static int64_t split_ws_bytes(const SplitPlan& p) {
+  if (p.s < 2) return 0;
+  return split_count_bytes(p) + (int64_t)p.tail * p.s * NTHREADS * 128 * 4;
+}
+
+extern "C" int64_t ntlb_gemm_workspace_bytes(int64_t M, int64_t N, int64_t Kp) {
+  if (M <= 0 || N <= 0 || Kp <= 0 || Kp % BK) return 0;
+  const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+  if (tiles > 0x7FFFFFFF) return 0;
+  return split_ws_bytes(split_plan(tiles, (int)(Kp / BK)));
+}
+
+extern "C" int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                        int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, const float* sb,
+                                        int64_t sb_row, int64_t sb_col, int b_shift, int64_t M, int64_t N,
+                                        int64_t Kp, const void* bias, int bias_dtype, void* y, int y_dtype,
+                                        int64_t ldy, const int32_t* nan_a, const int32_t* nan_b, void* workspace,
+                                        int64_t ws_bytes, void* stream) {
   const char* fn = "ntlb_gemm_blockscaled";
   if (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3) return fail(NTLB_EINVAL, "%s: bad grid %d", fn, grid);
   if (M < 0 || N < 0 || Kp < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
@@ -551,10 +683,22 @@ extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, co
   g.nan_a = nan_a; g.nan_b = nan_b;
   g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
   g.offsets = nullptr; g.n_experts = 0; g.b_estride = 0; g.sb_estride = 0;
+  g.split_base = (int)tiles; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
+  int64_t grid_wgs = tiles;
+  if (workspace) {
+    if (!aligned(workspace, 256)) return fail(NTLB_EINVAL, "%s: workspace must be 256-byte aligned", fn);
+    const SplitPlan plan = split_plan(tiles, (int)(Kp / BK));
+    if (plan.s > 1 && ws_bytes >= split_ws_bytes(plan)) {
+      g.split_base = plan.base; g.split_s = plan.s;
+      g.ws_count = reinterpret_cast<uint32_t*>(workspace);
+      g.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + split_count_bytes(plan));
+      grid_wgs = (int64_t)plan.base + (int64_t)plan.tail * plan.s;
+    }
+  }
   // B's scale is uniform over each wave's 64 columns for 128x128 blocks and tensor scales
   const bool b_uniform = (b_shift == 7) || (sb_row == 0);
   hipStream_t st = as_stream(stream);
-  dim3 grd((unsigned)tiles), blk(NTHREADS);
+  dim3 grd((unsigned)grid_wgs), blk(NTHREADS);
   if (grid == NTLB_GRID_E4M3) {
     if (b_uniform)
       gemm_blockscaled_kernel<GRID_E4M3, true, false><<<grd, blk, 0, st>>>(g);
@@ -567,6 +711,15 @@ extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, co
       gemm_blockscaled_kernel<GRID_INT, false, false><<<grd, blk, 0, st>>>(g);
   }
   return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                     int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, const float* sb,
+                                     int64_t sb_row, int64_t sb_col, int b_shift, int64_t M, int64_t N, int64_t Kp,
+                                     const void* bias, int bias_dtype, void* y, int y_dtype, int64_t ldy,
+                                     const int32_t* nan_a, const int32_t* nan_b, void* stream) {
+  return ntlb_gemm_blockscaled_ws(grid, a, lda, sa, sa_row, sa_col, a_shift, b, ldb, sb, sb_row, sb_col, b_shift, M,
+                                  N, Kp, bias, bias_dtype, y, y_dtype, ldy, nan_a, nan_b, nullptr, 0, stream);
 }
 
 extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
@@ -604,6 +757,7 @@ extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t
   g.nan_a = nan_a; g.nan_b = nan_b;
   g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
   g.offsets = offsets; g.n_experts = n_experts; g.b_estride = b_estride; g.sb_estride = sb_estride;
+  g.split_base = 0; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
   const bool b_uniform = (b_shift == 7) || (sb_row == 0);
   hipStream_t st = as_stream(stream);
   dim3 grd((unsigned)tiles), blk(NTHREADS);
@@ -677,6 +831,7 @@ extern "C" int ntlb_gemm_swiglu_quant(int grid, const uint8_t* a, int64_t lda, c
   g.M = M; g.N = N; g.Kp = Kp;
   g.nan_a = nan_a; g.nan_b = nan_b;
   g.offsets = nullptr; g.n_experts = 0; g.b_estride = 0; g.sb_estride = 0;
+  g.split_base = 0; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
   int rc = swiglu_common(fn, g, grid, N, h, ldh, hc, ldhc, hs, hs_row, hs_col, h_nan, qmax, rounding, scale_rule,
                          seed, offset);
   if (rc) return rc;
@@ -721,6 +876,7 @@ extern "C" int ntlb_gemm_grouped_swiglu_quant(int grid, const uint8_t* a, int64_
   g.M = M_total; g.N = N; g.Kp = Kp;
   g.nan_a = nan_a; g.nan_b = nan_b;
   g.offsets = offsets; g.n_experts = n_experts; g.b_estride = b_estride; g.sb_estride = sb_estride;
+  g.split_base = 0; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
   int rc = swiglu_common(fn, g, grid, N, h, ldh, hc, ldhc, hs, hs_row, hs_col, h_nan, qmax, rounding, scale_rule,
                          seed, offset);
   if (rc) return rc;

@@ -50,6 +50,8 @@ SIGNATURES = {
     "ntlb_dequant": [_I32, _P, _I64, _P, _I64, _I64, _I32, _I32, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_blockscaled": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64,
                               _I64, _P, _I32, _P, _I32, _I64, _P, _P, _P],
+    "ntlb_gemm_blockscaled_ws": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64,
+                                 _I64, _I64, _P, _I32, _P, _I32, _I64, _P, _P, _P, _I64, _P],
     "ntlb_gemm_grouped_blockscaled": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I32,
                                       _I64, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _P, _P],
     "ntlb_gemm_swiglu_quant": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64,
@@ -67,7 +69,11 @@ SIGNATURES = {
                                 _F32, _I32, _I64, _P, _P, _P],
     "ntlb_gemm_nf4": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_workspace_bytes": [_I64, _I64, _I64],
 }
+
+# entry points that return a value instead of a status
+RESTYPES = {"ntlb_gemm_workspace_bytes": _I64}
 
 _lib = None
 _lock = threading.Lock()
@@ -93,7 +99,7 @@ def lib() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         L.ntlb_last_error.restype = ctypes.c_char_p
         v = L.ntlb_abi_version()
         if v != ABI_VERSION:

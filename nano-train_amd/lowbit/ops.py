@@ -312,6 +312,25 @@ def quant_grouped(
     return codes, scales, dq, nan_rows
 
 
+_workspaces: dict = {}
+
+
+def gemm_workspace(M: int, N: int, Kp: int, device: torch.device) -> Optional[torch.Tensor]:
+    """The zeroed split-K workspace of the current stream on `device`, grown to
+    what an (M, N, Kp) product needs; None when that shape runs unsplit.  The
+    kernels leave it zeroed, and calls on one stream never overlap, so one
+    buffer per stream serves every GEMM issued there."""
+    need = int(_lib.lib().ntlb_gemm_workspace_bytes(M, N, Kp))
+    if need <= 0:
+        return None
+    key = (device.index, _stream())
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
 def gemm_blockscaled(
     a: QTensor,
     b: QTensor,
@@ -319,8 +338,13 @@ def gemm_blockscaled(
     bias: Optional[torch.Tensor] = None,
     out_dtype: torch.dtype = torch.bfloat16,
     out: Optional[torch.Tensor] = None,
+    split_tail: bool = True,
 ) -> torch.Tensor:
-    """Y[M, N] = dequant(a) @ dequant(b)^T (+ bias), fp32 accumulation."""
+    """Y[M, N] = dequant(a) @ dequant(b)^T (+ bias), fp32 accumulation.
+
+    split_tail lets the tiles past the last whole wave run as K-split
+    partials summed in a fixed order (results are deterministic, and equal
+    the unsplit ones up to fp32 summation order)."""
     _require_device(a.codes, b.codes, bias)
     if a.grid != b.grid:
         raise ValueError("operands must share a code format")
@@ -331,11 +355,13 @@ def gemm_blockscaled(
         out = torch.empty((M, N), dtype=out_dtype, device=a.codes.device)
     if bias is not None and bias.stride(-1) != 1:
         bias = bias.contiguous()
+    ws = gemm_workspace(M, N, Kp, a.codes.device) if split_tail else None
     call(
-        "ntlb_gemm_blockscaled", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
+        "ntlb_gemm_blockscaled_ws", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
         a.s_col, a.shift, b.codes.data_ptr(), b.codes.stride(0), b.scales.data_ptr(), b.s_row, b.s_col, b.shift,
         M, N, Kp, _ptr(bias), _dtype_code(bias.dtype) if bias is not None else 0, out.data_ptr(),
-        _dtype_code(out.dtype), out.stride(0), _ptr(a.nan_rows), _ptr(b.nan_rows), _stream(),
+        _dtype_code(out.dtype), out.stride(0), _ptr(a.nan_rows), _ptr(b.nan_rows), _ptr(ws),
+        ws.numel() if ws is not None else 0, _stream(),
     )
     return out
 

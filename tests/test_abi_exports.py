@@ -17,7 +17,7 @@ HEADER = os.path.join(ROOT, "include", "ntlowbit.h")
 def _declared():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    decls = re.findall(r"^(?:int|const char\*)\s+(ntlb_\w+)\s*\(([^;]*)\);", text, flags=re.M)
+    decls = re.findall(r"^(?:int64_t|int|const char\*)\s+(ntlb_\w+)\s*\(([^;]*)\);", text, flags=re.M)
     out = {}
     for name, args in decls:
         args = " ".join(args.split())
