@@ -167,26 +167,29 @@ def other_config(args) -> dict:
     M, K = x.shape
     N = w.shape[0]
     pk, sc = persistent.quantize_nf4_blocks(w, 64)
-    mp, ms8 = persistent.quantize_mxfp4(w)
+    mx_packed, mx_scales = persistent.quantize_mxfp4(w)
+    f8_vals, f8_scale = persistent.quantize_fp8_persistent(w, granularity="per_channel")
     # the optimizer side of the same weight: AdamW step + NF4 refresh, fused and as two passes
     from lowbit import optim
 
     n = N * K
-    mp = w.float().reshape(-1).contiguous()
-    mst, vst = torch.zeros_like(mp), torch.zeros_like(mp)
+    master = w.float().reshape(-1).contiguous()
+    mst, vst = torch.zeros_like(master), torch.zeros_like(master)
     grad = (torch.randn(n, device=dev, dtype=torch.bfloat16) * 1e-3)
     wp = w.reshape(-1).clone()
     codes = torch.empty(n // 2, dtype=torch.uint8, device=dev)
     scl = torch.empty(n // 64, dtype=torch.float32, device=dev)
     hp = dict(lr=1e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, step=1)
-    fused_ms = _time_ms(lambda i: optim.adamw_step_refresh(mp, grad, mst, vst, param=wp, refresh="nf4", block=64,
+    fused_ms = _time_ms(lambda i: optim.adamw_step_refresh(master, grad, mst, vst, param=wp, refresh="nf4", block=64,
                                                            codes=codes, scales=scl, **hp), args.steps, args.warmup, st)
-    two_ms = _time_ms(lambda i: (optim.adamw_step_refresh(mp, grad, mst, vst, param=wp, **hp),
+    two_ms = _time_ms(lambda i: (optim.adamw_step_refresh(master, grad, mst, vst, param=wp, **hp),
                                  persistent.quantize_nf4_blocks(wp, 64)), args.steps, args.warmup, st)
     # grad bf16 in, fp32 master/m/v in and out, bf16 param out, NF4 codes and 64-block scales out
     opt_bytes = n * (2 + 12 + 12 + 2) + n // 2 + (n // 64) * 4
     nf4 = _time_ms(lambda i: persistent.linear_nf4(x, pk, sc, out_features=N, block=64), args.steps, args.warmup, st)
-    mx = _time_ms(lambda i: persistent.linear_mxfp4(x, mp, ms8, out_features=N), args.steps, args.warmup, st)
+    mx = _time_ms(lambda i: persistent.linear_mxfp4(x, mx_packed, mx_scales, out_features=N), args.steps, args.warmup,
+                  st)
+    f8 = _time_ms(lambda i: persistent.linear_fp8p(x, f8_vals, f8_scale), args.steps, args.warmup, st)
     bf = _time_ms(lambda i: torch.matmul(x, w.t()), args.steps, args.warmup, st)
     fl = 2.0 * M * N * K
     res.update(value=round(fl / (nf4 * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(nf4, 4), dtype="bf16",
@@ -194,6 +197,7 @@ def other_config(args) -> dict:
                roofline={"bound": "mfma", "achieved": round(fl / (nf4 * 1e-3) / 1e12, 2), "peak": 2500.0,
                          "unit": "TFLOP/s", "frac": round(fl / (nf4 * 1e-3) / 1e12 / 2500.0, 4), "traffic": None},
                mxfp4_tflops=round(fl / (mx * 1e-3) / 1e12, 2),
+               fp8_persistent_tflops=round(fl / (f8 * 1e-3) / 1e12, 2),
                adamw_nf4_refresh={"fused_us": round(fused_ms * 1e3, 1), "two_pass_us": round(two_ms * 1e3, 1),
                                   "fused_GB/s": round(opt_bytes / (fused_ms * 1e-3) / 1e9, 1), "params": n},
                torch_bf16_matmul_tflops=round(fl / (bf * 1e-3) / 1e12, 2))

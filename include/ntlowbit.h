@@ -345,6 +345,17 @@ int ntlb_gemm_nf4(const void* x, int64_t ldx, const uint8_t* w_packed, const flo
 int ntlb_gemm_mxfp4(const void* x, int64_t ldx, const uint8_t* w_packed, const uint8_t* w_scales, int64_t M,
                     int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
 
+/*
+ * The same fused GEMM for the persistent FP8 weight: w_codes [N, K] e4m3
+ * bytes (the float8_e4m3fn `_persistent_fp8_weight`), dequantized as
+ * _dequantize_fp8_persistent (layers.py:120-127) would, bf16(value * scale),
+ * then multiplied as F.linear(x, weight) in the persistent forward
+ * (layers.py:409-436).  block = K for the per_channel scale [N] or 0 for
+ * per_tensor; K % 64 == 0.
+ */
+int ntlb_gemm_fp8p(const void* x, int64_t ldx, const uint8_t* w_codes, const float* w_scales, int64_t block,
+                   int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -31,7 +31,7 @@ __constant__ float kNF4[16] = {-1.0f,        -0.6961928f,  -0.52507305f, -0.3949
                                0.44070983f,  0.562617f,    0.72295684f,  1.0f};
 __constant__ float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
 
-enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1 };
+enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1, FMT_FP8P = 2 };
 
 // ---------------------------------------------------------------------------
 // element codes
@@ -453,6 +453,7 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
 typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int FBM = 256, FBN = 256, FBK = 64;  // FBK in bf16 elements: 128 bytes per row
@@ -493,9 +494,9 @@ __device__ __forceinline__ v4f mma_bf16_64(const v8i& p, const v8i& q, v4f acc) 
 struct FusedArgs {
   const uint16_t* x;  // bf16 [M, K], row stride ldx
   int64_t ldx;
-  const uint8_t* w;   // packed codes of the flat [N, K] weight
-  const void* scales;  // NF4: fp32 per block; MXFP4: e8m0 per 32
-  int64_t block;       // NF4 block (divides K, multiple of 32) or 0 for one tensor scale
+  const uint8_t* w;   // codes of the flat [N, K] weight: packed nibbles (NF4, MXFP4) or e4m3 bytes (FP8P)
+  const void* scales;  // NF4, FP8P: fp32 per block; MXFP4: e8m0 per 32
+  int64_t block;       // NF4/FP8P block (divides K, multiple of 32) or 0 for one tensor scale
   int64_t M, N, K;
   void* y;
   int y_dtype;
@@ -515,7 +516,7 @@ struct RowScales {
 template <int FMT>
 __device__ __forceinline__ RowScales fused_row_scales(const FusedArgs& g, int64_t n) {
   RowScales r;
-  if constexpr (FMT == FMT_NF4) {
+  if constexpr (FMT == FMT_NF4 || FMT == FMT_FP8P) {
     const float* sc = reinterpret_cast<const float*>(g.scales);
     r.row = g.block ? sc + n * (g.K / g.block) : sc;
     r.blk = g.block ? (uint32_t)g.block : 0x40000000u;
@@ -528,16 +529,48 @@ __device__ __forceinline__ RowScales fused_row_scales(const FusedArgs& g, int64_
 
 template <int FMT>
 __device__ __forceinline__ float fused_scale(const RowScales& r, uint32_t k0) {
-  if constexpr (FMT == FMT_NF4)
+  if constexpr (FMT == FMT_NF4 || FMT == FMT_FP8P)
     return reinterpret_cast<const float*>(r.row)[k0 / r.blk];
   else
     return __uint_as_float((uint32_t)reinterpret_cast<const uint8_t*>(r.row)[k0 >> 5]);
 }
 
+// The raw codes of 32 weights: 16 packed bytes (4-bit formats) or 32 e4m3
+// bytes (FP8P, second half in b)
+struct Raw32 {
+  uint4 a, b;
+};
+
+// 32 e4m3 weights of tile row r, half h: layers.py:121-127, the code's value
+// (hardware decode, exact for every code, NaN codes to NaN) times the scale
+// in fp32, rounded to bf16
+__device__ __forceinline__ void dequant32_fp8_to_lds(const Raw32& raw, float s, uint8_t* tile, int r, int h) {
+  const uint32_t words[8] = {raw.a.x, raw.a.y, raw.a.z, raw.a.w, raw.b.x, raw.b.y, raw.b.z, raw.b.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {  // 8 elements (8 bytes) per 16-byte LDS chunk
+    uint32_t out[4];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[2 * j + w], false);
+      const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[2 * j + w], true);
+      const v2bf p0 = {(__bf16)(lo[0] * s), (__bf16)(lo[1] * s)};
+      const v2bf p1 = {(__bf16)(hi[0] * s), (__bf16)(hi[1] * s)};
+      out[2 * w] = __builtin_bit_cast(uint32_t, p0);
+      out[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
+    }
+    *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
+  }
+}
+
 // 32 weights (16 packed bytes, low nibble first) of tile row r, half h
 template <int FMT>
-__device__ __forceinline__ void dequant32_to_lds(const uint4 raw, float s, const float* lut, uint8_t* tile, int r,
+__device__ __forceinline__ void dequant32_to_lds(const Raw32& rw, float s, const float* lut, uint8_t* tile, int r,
                                                  int h) {
+  if constexpr (FMT == FMT_FP8P) {
+    dequant32_fp8_to_lds(rw, s, tile, r, h);
+    return;
+  }
+  const uint4 raw = rw.a;
   const uint32_t bytes[4] = {raw.x, raw.y, raw.z, raw.w};
   const uint32_t sb = __float_as_uint(s);  // MXFP4: e8m0 byte
 #pragma unroll
@@ -590,7 +623,7 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   const int64_t m0 = (int64_t)(first_m + in_group % gsize) * FBM;
   const int64_t n0 = (int64_t)(in_group / gsize) * FBN;
 
-  if (tid < 16) lut[tid] = (FMT == FMT_NF4) ? kNF4[tid] : e2m1_value((uint32_t)tid);
+  if (tid < 16) lut[tid] = (FMT == FMT_NF4) ? kNF4[tid] : (FMT == FMT_MXFP4) ? e2m1_value((uint32_t)tid) : 0.f;
 
   // X tile: direct-to-LDS; wave w moves the 8-row groups w, w+8, w+16, w+24
   // (bit 3 of its rows is w & 1, so its lanes' swizzled chunks are the same
@@ -604,10 +637,12 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(stage + (wave + 8 * j) * 8 * FROW), 16, x_off,
                                              (uint32_t)kt * FROW + j * x_grp, 0, 0);
   };
-  // W: thread t dequantizes row t/2, half t%2 (32 weights = 16 packed bytes)
+  // W: thread t dequantizes row t/2, half t%2 (32 weights = 16 packed bytes,
+  // or 32 e4m3 bytes)
+  constexpr bool BYTE_CODES = FMT == FMT_FP8P;
   const int br = tid >> 1, bh = tid & 1;
   const int64_t bn = min<int64_t>(n0 + br, g.N - 1);
-  const uint8_t* wrow = g.w + bn * (g.K >> 1) + bh * 16;
+  const uint8_t* wrow = BYTE_CODES ? g.w + bn * g.K + bh * 32 : g.w + bn * (g.K >> 1) + bh * 16;
   const RowScales wsc = fused_row_scales<FMT>(g, bn);
 
   const int nk = (int)(g.K / FBK);
@@ -624,14 +659,19 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   // that step's X copies, and may stay in flight across its closing barrier.
   // Register set kt & 1 holds block kt+2 (written by step kt, read by step
   // kt+1), so with the K loop unrolled by two no set is copied.
-  auto w_load = [&](int kb, uint4& raw, float& sc) {
-    raw = *reinterpret_cast<const uint4*>(wrow + (int64_t)kb * (FBK / 2));
+  auto w_load = [&](int kb, Raw32& raw, float& sc) {
+    if constexpr (BYTE_CODES) {
+      raw.a = *reinterpret_cast<const uint4*>(wrow + (int64_t)kb * FBK);
+      raw.b = *reinterpret_cast<const uint4*>(wrow + (int64_t)kb * FBK + 16);
+    } else {
+      raw.a = *reinterpret_cast<const uint4*>(wrow + (int64_t)kb * (FBK / 2));
+    }
     sc = fused_scale<FMT>(wsc, (uint32_t)(kb * FBK + bh * 32));
   };
-  uint4 raw_pf0, raw_pf1;
+  Raw32 raw_pf0, raw_pf1;
   float sc_pf0, sc_pf1;
   {
-    uint4 raw0;
+    Raw32 raw0;
     float s0;
     w_load(0, raw0, s0);
     __syncthreads();  // lut
@@ -665,9 +705,10 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
         // of the dequant work (or a wait for the loads) moves up into the
         // first half of the MFMA phase; then block kn+1's loads go out, the
         // last vector-memory operations of the step
-        uint4& r = BUF ? raw_pf0 : raw_pf1;
+        Raw32& r = BUF ? raw_pf0 : raw_pf1;
         float& s = BUF ? sc_pf0 : sc_pf1;
-        asm volatile("" : "+v"(r.x), "+v"(r.y), "+v"(r.z), "+v"(r.w), "+v"(s));
+        asm volatile("" : "+v"(r.a.x), "+v"(r.a.y), "+v"(r.a.z), "+v"(r.a.w), "+v"(s));
+        if constexpr (BYTE_CODES) asm volatile("" : "+v"(r.b.x), "+v"(r.b.y), "+v"(r.b.z), "+v"(r.b.w));
         w_load(min(kt + 2, nk - 1), BUF ? raw_pf1 : raw_pf0, BUF ? sc_pf1 : sc_pf0);
         dequant32_to_lds<FMT>(r, s, lut, wb_next, br, bh);
       }
@@ -824,8 +865,8 @@ static int fused_launch(int fmt, const char* fn, const void* x, int64_t ldx, con
     return fail(NTLB_EINVAL, "%s: x needs ldx >= K, ldx %% 8 == 0, 16-byte alignment; w 16-byte alignment", fn);
   if (!(y_dtype == NTLB_BF16 || y_dtype == NTLB_F32) || ldy < N)
     return fail(NTLB_EINVAL, "%s: output must be bf16 or fp32 with ldy >= N", fn);
-  if (fmt == FMT_NF4 && block != 0 && (K % block || block % 32))
-    return fail(NTLB_EUNSUPPORTED, "%s: NF4 block must divide K and be a multiple of 32 (or 0 = tensor)", fn);
+  if (fmt != FMT_MXFP4 && block != 0 && (K % block || block % 32))
+    return fail(NTLB_EUNSUPPORTED, "%s: the scale block must divide K and be a multiple of 32 (or 0 = tensor)", fn);
   if ((M + FBM) * ldx * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: X exceeds 2 GiB", fn);
   const int64_t tiles = ((M + FBM - 1) / FBM) * ((N + FBN - 1) / FBN);
   FusedArgs g;
@@ -835,8 +876,10 @@ static int fused_launch(int fmt, const char* fn, const void* x, int64_t ldx, con
   dim3 grd((unsigned)tiles), blk(512);
   if (fmt == FMT_NF4)
     gemm_lowbit_fused_kernel<FMT_NF4><<<grd, blk, 0, as_stream(stream)>>>(g);
-  else
+  else if (fmt == FMT_MXFP4)
     gemm_lowbit_fused_kernel<FMT_MXFP4><<<grd, blk, 0, as_stream(stream)>>>(g);
+  else
+    gemm_lowbit_fused_kernel<FMT_FP8P><<<grd, blk, 0, as_stream(stream)>>>(g);
   return check_launch(fn);
 }
 
@@ -844,6 +887,13 @@ extern "C" int ntlb_gemm_nf4(const void* x, int64_t ldx, const uint8_t* w_packed
                              int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
                              void* stream) {
   return fused_launch(FMT_NF4, "ntlb_gemm_nf4", x, ldx, w_packed, w_scales, block, M, N, K, y, y_dtype, ldy,
+                      stream);
+}
+
+extern "C" int ntlb_gemm_fp8p(const void* x, int64_t ldx, const uint8_t* w_codes, const float* w_scales,
+                              int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
+                              void* stream) {
+  return fused_launch(FMT_FP8P, "ntlb_gemm_fp8p", x, ldx, w_codes, w_scales, block, M, N, K, y, y_dtype, ldy,
                       stream);
 }
 

@@ -69,6 +69,7 @@ SIGNATURES = {
                                 _F32, _I32, _I64, _P, _P, _P],
     "ntlb_gemm_nf4": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_fp8p": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_workspace_bytes": [_I64, _I64, _I64],
 }
 

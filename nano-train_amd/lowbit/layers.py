@@ -9,10 +9,11 @@ backend -> per-module compute dtype -> F.linear), the same error messages,
 and tolerance of legacy checkpoints that lack the persistent buffers.
 
 Persistent NF4/FP8 weights are refreshed and dequantized by the HIP kernels of
-lowbit.persistent.  When a module stores NF4 weights, has no low-bit compute
-backend, and both activation and master weight are bf16, the forward runs the
-dequant-fused GEMM instead of materializing the bf16 weight; its backward is
-the reference's straight-through rule (dX = dY . W_deq, dW = dY^T . X).
+lowbit.persistent.  When a module stores NF4 or FP8 weights, has no low-bit
+compute backend, and both activation and master weight are bf16, the forward
+runs the dequant-fused GEMM instead of materializing the bf16 weight; its
+backward is the reference's straight-through rule (dX = dY . W_deq,
+dW = dY^T . X).
 
 One GPU: the tensor-parallel classes accept tp_size == 1 only.
 """
@@ -32,31 +33,38 @@ from .precision import dtype_alias_to_torch
 _PERSISTENT_SUFFIXES = ("_persistent_fp8_weight", "_persistent_fp4_codes", "_persistent_scale", "_persistent_numel")
 
 
-class _NF4FusedLinear(torch.autograd.Function):
-    """Forward: fused NF4 GEMM.  Backward: straight-through to the master weight."""
+class _FusedPersistentLinear(torch.autograd.Function):
+    """Forward: dequant-fused GEMM over the persistent NF4 or FP8 weight.
+    Backward: straight-through to the master weight (layers.py:409-436)."""
 
     @staticmethod
-    def forward(ctx, x, weight, codes, scale, block):
+    def forward(ctx, x, weight, codes, scale, block, fmt):
         N, K = weight.shape
-        y = P.linear_nf4(x, codes, scale, out_features=N, block=block)
+        if fmt == "nf4":
+            y = P.linear_nf4(x, codes, scale, out_features=N, block=block)
+        else:
+            y = P.linear_fp8p(x, codes, scale)
         ctx.save_for_backward(x, codes, scale)
-        ctx.meta = (N, K, block, weight.dtype)
+        ctx.meta = (N, K, block, weight.dtype, fmt)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         x, codes, scale = ctx.saved_tensors
-        N, K, block, wdt = ctx.meta
+        N, K, block, wdt, fmt = ctx.meta
         dx = dw = None
         dy2 = dy.reshape(-1, N)
         with torch.autocast(device_type="cuda", enabled=False):
             if ctx.needs_input_grad[0]:
-                w_deq = P.dequantize_nf4_blocks(codes, scale, num_values=N * K, block=block,
-                                                target_dtype=wdt).reshape(N, K)
+                if fmt == "nf4":
+                    w_deq = P.dequantize_nf4_blocks(codes, scale, num_values=N * K, block=block,
+                                                    target_dtype=wdt).reshape(N, K)
+                else:
+                    w_deq = P.dequantize_fp8_persistent(codes, scale, target_dtype=wdt).reshape(N, K)
                 dx = torch.matmul(dy2, w_deq.to(dy2.dtype)).reshape(x.shape)
             if ctx.needs_input_grad[1]:
                 dw = torch.matmul(dy2.t(), x.reshape(-1, K).to(dy2.dtype)).to(wdt)
-        return dx, dw, None, None, None
+        return dx, dw, None, None, None, None
 
 
 class LowBitLinearMixin:
@@ -193,19 +201,28 @@ class LowBitLinearMixin:
             raise ValueError(f"Unsupported persistent low-bit mode: {mode}")
         return self.weight + (deq - self.weight).detach()
 
-    def _fused_nf4_forward(self, x: torch.Tensor) -> Optional[torch.Tensor]:
-        """NF4 persistent weight, no low-bit backend, bf16 everywhere: dequant inside the GEMM."""
-        if (self._persistent_mode() != "fp4" or self._compute_lowbit_mode() is not None
+    def _fused_persistent_forward(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+        """NF4 or FP8 persistent weight, no low-bit backend, bf16 everywhere:
+        dequant inside the GEMM instead of materializing the bf16 weight."""
+        mode = self._persistent_mode()
+        if (mode not in ("fp4", "fp8") or self._compute_lowbit_mode() is not None
                 or self._compute_dtype_override() is not None or x.dtype != torch.bfloat16
                 or self.weight.dtype != torch.bfloat16 or x.device.type != "cuda" or self.weight.dim() != 2
                 or self.weight.shape[1] % 64):
             return None
-        if int(self._persistent_numel.item()) != int(self.weight.numel()):
-            self.refresh_persistent_lowbit_params()
         N, K = self.weight.shape
+        if mode == "fp4":
+            if int(self._persistent_numel.item()) != int(self.weight.numel()):
+                self.refresh_persistent_lowbit_params()
+            scale = self._persistent_scale
+            block = (N * K) if scale.numel() <= 1 else K
+            return _FusedPersistentLinear.apply(x, self.weight, self._persistent_fp4_codes, scale.float(), block,
+                                                "nf4")
+        if self._persistent_fp8_weight.numel() != self.weight.numel():
+            self.refresh_persistent_lowbit_params()
         scale = self._persistent_scale
-        block = (N * K) if scale.numel() <= 1 else K
-        return _NF4FusedLinear.apply(x, self.weight, self._persistent_fp4_codes, scale.float(), block)
+        return _FusedPersistentLinear.apply(x, self.weight, self._persistent_fp8_weight, scale.float(),
+                                            0 if scale.numel() <= 1 else K, "fp8")
 
     def _dispatch_lowbit_linear(self, *, x: torch.Tensor, weight: torch.Tensor,
                                 bias: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
@@ -227,7 +244,7 @@ class LowBitLinearMixin:
 
     def _lowbit_forward(self, x: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
         if bias is None:
-            fused = self._fused_nf4_forward(x)
+            fused = self._fused_persistent_forward(x)
             if fused is not None:
                 return fused
         weight = self._persistent_weight_ste()

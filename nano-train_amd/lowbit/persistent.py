@@ -13,7 +13,8 @@ float8_e4m3fn values and `_persistent_scale` fp32 layout, layers.py:235-246):
 
 plus the BASELINE config 5 formats that have no reference function: NF4 with
 one scale per 64 elements, MXFP4 (e2m1 + e8m0 per 32), and the GEMMs with the
-dequantization fused into the weight-tile prologue (linear_nf4, linear_mxfp4).
+dequantization fused into the weight-tile prologue (linear_nf4, linear_mxfp4,
+and linear_fp8p for the persistent FP8 weight).
 """
 
 from __future__ import annotations
@@ -162,6 +163,26 @@ def linear_nf4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, o
     blk = 0 if block >= N * K else block
     call("ntlb_gemm_nf4", x2.data_ptr(), x2.stride(0), packed.data_ptr(), scales.reshape(-1).contiguous().data_ptr(),
          blk, M, N, K, y.data_ptr(), ops._dtype_code(y.dtype), y.stride(0), ops._stream())
+    return y.reshape(*x.shape[:-1], N)
+
+
+def linear_fp8p(x: torch.Tensor, fp8_values: torch.Tensor, scale: torch.Tensor, *,
+                out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Y = x @ deq(W)^T with W the persistent FP8 weight [N, K] (float8_e4m3fn
+    values and a per_channel [N, 1] or per_tensor scale), dequantized inside
+    the GEMM as _dequantize_fp8_persistent does (layers.py:120-127)."""
+    ops._require_device(fp8_values, scale)
+    N, K = fp8_values.shape
+    x2 = _x2(x, K)
+    M = x2.shape[0]
+    codes = fp8_values.contiguous().view(torch.uint8)
+    sc = scale.reshape(-1).contiguous().float()
+    block = 0 if sc.numel() <= 1 else K
+    if block and sc.numel() != N:
+        raise ValueError(f"scale must be per_tensor or one per row, got {tuple(scale.shape)}")
+    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x.device)
+    call("ntlb_gemm_fp8p", x2.data_ptr(), x2.stride(0), codes.data_ptr(), sc.data_ptr(), block, M, N, K,
+         y.data_ptr(), ops._dtype_code(y.dtype), y.stride(0), ops._stream())
     return y.reshape(*x.shape[:-1], N)
 
 

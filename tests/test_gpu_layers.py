@@ -191,6 +191,38 @@ def test_persistent_fp8_layer_refresh_forward_backward(gpu_device, gran):
     assert layer.weight.grad is not None and torch.isfinite(layer.weight.grad).all()
 
 
+@pytest.mark.parametrize("gran", ["per_channel", "per_tensor"])
+def test_persistent_fp8_fused_forward_and_ste_backward(gpu_device, gran):
+    """A bias-free persistent-FP8 layer runs the dequant-fused GEMM; forward
+    and the straight-through gradients match F.linear on the materialized
+    dequantized weight."""
+    from lowbit import persistent as P
+    from lowbit.precision import refresh_persistent_lowbit_params
+
+    _, res = _resolver(bf16=True, fp8_param=True, persistent_scale_granularity=gran,
+                       persistent_lowbit_include=["fc"], compute_lowbit_mode=None)
+    layer = _linear(res, 512, 320, bias=False, path="fc")
+    refresh_persistent_lowbit_params(torch.nn.Sequential(layer))
+    x = seeded((48, 512), seed=52).to(gpu_device).requires_grad_(True)
+    y = layer(x)
+    assert layer._fused_persistent_forward(x.detach()) is not None
+    w_deq = P.dequantize_fp8_persistent(layer._persistent_fp8_weight, layer._persistent_scale,
+                                        target_dtype=torch.bfloat16)
+    xr = x.detach().clone().requires_grad_(True)
+    wr = layer.weight.detach().clone().requires_grad_(True)
+    y_mat = torch.nn.functional.linear(xr, wr + (w_deq - wr).detach())
+    assert rel_fro_bf16(y, y_mat.float().detach().cpu().numpy().astype(np.float64)) <= 2e-3
+    block = 512 if gran == "per_channel" else 512 * 320
+    c, s = O.fp8_persistent_quant(to_np32(layer.weight), block)
+    wdq = O.round_bf16((O.decode_codes(c, O.GRID_E4M3) * np.repeat(s, block)).reshape(320, 512))
+    assert rel_fro_bf16(y, O.gemm_ref(to_np32(x), wdq)) <= 1e-3
+    dy = seeded((48, 320), seed=53).to(gpu_device)
+    y.backward(dy)
+    y_mat.backward(dy)
+    assert rel_fro_bf16(x.grad, xr.grad.float().cpu().numpy().astype(np.float64)) <= 2e-3
+    assert rel_fro_bf16(layer.weight.grad, wr.grad.float().cpu().numpy().astype(np.float64)) <= 2e-3
+
+
 def test_persistent_nf4_fused_matches_materialized_and_trains(gpu_device):
     from lowbit import persistent as P
     from lowbit.precision import refresh_persistent_lowbit_params

@@ -131,3 +131,80 @@ def test_c5_nf4_fused_gemm_full_size_sampled(gpu_device):
     wdq = O.round_bf16(O.nf4_dequant(p_ref, s_ref, 14336 * 4096, 64)).reshape(14336, 4096)
     ref = O.gemm_ref(x.float().numpy()[rows], wdq[cols])
     assert rel_fro_bf16(y[rows][:, cols], ref) <= 1e-3
+
+
+@pytest.mark.parametrize("per_tensor", [False, True])
+def test_fp8p_fused_gemm_dequant_exact_all_codes(gpu_device, per_tensor):
+    """X = I makes the fused GEMM return deq(W)^T exactly (one nonzero product
+    per output), so every e4m3 code's bf16(value * scale) is checked bit for
+    bit against the oracle decode; rows holding a NaN code (0x7F, 0xFF) turn
+    their output column NaN."""
+    from lowbit import persistent as P
+
+    K, N = 256, 96
+    rng = np.random.default_rng(20260601)
+    codes = np.stack([rng.permutation(256) for _ in range(N)]).astype(np.uint8)
+    nan_rows = [5, 70]
+    for r in range(N):
+        if r not in nan_rows:
+            codes[r][codes[r] == 0x7F] = 0x00
+            codes[r][codes[r] == 0xFF] = 0x80
+    scales = (np.exp(rng.uniform(np.log(1e-20), np.log(1e20), N))).astype(np.float32)
+    if per_tensor:
+        scales = scales[:1]
+    x = torch.eye(K, dtype=torch.bfloat16, device=gpu_device)
+    w = torch.from_numpy(codes).to(gpu_device).view(torch.float8_e4m3fn)
+    s = torch.from_numpy(scales).to(gpu_device).reshape(-1, 1) if not per_tensor else \
+        torch.from_numpy(scales).to(gpu_device).reshape(())
+    y = P.linear_fp8p(x, w, s, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().T  # [N, K]
+    vals = O.decode_codes(codes, O.GRID_E4M3)
+    want = O.round_bf16(vals * (scales[:, None] if not per_tensor else scales[0]))
+    for r in nan_rows:
+        assert np.isnan(got[r]).all()
+    keep = [r for r in range(N) if r not in nan_rows]
+    np.testing.assert_array_equal(got[keep], want[keep])
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (130, 200, 320), (512, 384, 2048), (1, 64, 64)])
+@pytest.mark.parametrize("granularity", ["per_channel", "per_tensor"])
+def test_fp8p_fused_gemm(gpu_device, M, N, K, granularity):
+    from lowbit import persistent as P
+
+    x = seeded((M, K), seed=20260602).to(gpu_device)
+    w = seeded((N, K), seed=20260603, std=0.02).to(gpu_device)
+    vals, scale = P.quantize_fp8_persistent(w, granularity=granularity)
+    y = P.linear_fp8p(x, vals, scale)
+    torch.cuda.synchronize()
+    block = K if granularity == "per_channel" else N * K
+    c_ref, s_ref = O.fp8_persistent_quant(to_np32(w), block)
+    wdq = O.round_bf16(O.decode_codes(c_ref, O.GRID_E4M3) * np.repeat(s_ref, block)).reshape(N, K)
+    assert rel_fro_bf16(y, O.gemm_ref(to_np32(x), wdq)) <= 1e-3
+
+
+def test_c5_fp8p_fused_gemm_full_size_sampled(gpu_device):
+    """The c5 shapes with the weight held as persistent FP8 (per_channel)."""
+    from lowbit import persistent as P, workloads
+
+    x, w = workloads.c5_inputs(device="cpu")
+    xg, wg = x.to(gpu_device), w.to(gpu_device)
+    vals, scale = P.quantize_fp8_persistent(wg, granularity="per_channel")
+    y = P.linear_fp8p(xg, vals, scale)
+    torch.cuda.synchronize()
+    c_ref, s_ref = O.fp8_persistent_quant(w.float().numpy(), 4096)
+    assert_bits_equal(vals.view(torch.uint8).reshape(-1).cpu().numpy(), c_ref, "c5 fp8 codes")
+    rows = np.random.default_rng(0).choice(4096, 32, replace=False)
+    cols = np.random.default_rng(1).choice(14336, 256, replace=False)
+    wdq = O.round_bf16(O.decode_codes(c_ref.reshape(14336, 4096)[cols], O.GRID_E4M3) * s_ref[cols, None])
+    ref = O.gemm_ref(x.float().numpy()[rows], wdq)
+    assert rel_fro_bf16(y[rows][:, cols], ref) <= 1e-3
+
+
+def test_fp8p_fused_gemm_rejects_bad_scale_shape(gpu_device):
+    from lowbit import persistent as P
+
+    x = torch.zeros(4, 64, dtype=torch.bfloat16, device=gpu_device)
+    w = torch.zeros(8, 64, dtype=torch.uint8, device=gpu_device).view(torch.float8_e4m3fn)
+    with pytest.raises(ValueError):
+        P.linear_fp8p(x, w, torch.ones(3, device=gpu_device))
