@@ -26,12 +26,18 @@
 
 namespace ntlb {
 
-__constant__ float kNF4[16] = {-1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
-                               -0.09105004f, 0.0f,         0.0795803f,   0.1609302f,  0.2461123f,   0.33791524f,
-                               0.44070983f,  0.562617f,    0.72295684f,  1.0f};
+// layers.py:60-83, as fp32
+#define NTLB_NF4_CODEBOOK                                                                                          \
+  {-1.0f,       -0.6961928f, -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f, -0.09105004f, 0.0f,         \
+   0.0795803f,  0.1609302f,  0.2461123f,   0.33791524f, 0.44070983f,  0.562617f,    0.72295684f,  1.0f}
+__constant__ float kNF4[16] = NTLB_NF4_CODEBOOK;
+// the same values as compile-time constants (folded into immediates)
+constexpr float kNF4c[16] = NTLB_NF4_CODEBOOK;
+constexpr float kE2M1c[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
 __constant__ float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
 
 enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1, FMT_FP8P = 2 };
+
 
 // ---------------------------------------------------------------------------
 // element codes
@@ -42,9 +48,7 @@ enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1, FMT_FP8P = 2 };
 // The codebook comes in as compile-time constants and the bracket is tracked
 // with selects, so the lookup never indexes memory.
 __device__ __forceinline__ uint32_t nf4_index(float c) {
-  static constexpr float cb[16] = {-1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f,
-                                   -0.09105004f, 0.0f,         0.0795803f,   0.1609302f,  0.2461123f,   0.33791524f,
-                                   0.44070983f,  0.562617f,    0.72295684f,  1.0f};
+  constexpr const float* cb = kNF4c;
   uint32_t below = 0;
   float lo = cb[0], hi = cb[1];
 #pragma unroll
@@ -438,13 +442,17 @@ static bool onepass_block(int64_t block) { return block >= 8 && block <= 2048 &&
 // Dequant-fused GEMM  Y[M,N] = X[M,K] (bf16) . deq(W)[N,K]^T, fp32 accumulate.
 // 256x256 output tile, 8 waves of 128x64, K step 64 bf16 (128-byte rows, the
 // same swizzled tile layout as the fp8 kernel).  X tiles move global -> LDS
-// directly; each thread dequantizes 32 weights (16 packed bytes) of one B row
-// per K step into bf16 in LDS.  The packed bytes and the block scale of step
-// kt+1 are fetched into registers at the start of step kt and dequantized
-// into the idle stage in the middle of it, so the VALU work overlaps the
-// matrix cores.  The codebook sits in LDS.  The two stages are distinct LDS
-// objects and the K loop is unrolled by two (see the fp8 kernel): the copies
-// in flight never alias the fragment reads, so no read waits for them.
+// directly; each thread dequantizes 32 weights (16 packed bytes, or 32 e4m3
+// bytes) of one B row per K step into bf16 in LDS.  The codes and the block
+// scale of block kt+1 are fetched into registers in the middle of step kt-1
+// and decoded into the idle stage during step kt, one 16-byte chunk per odd
+// 16-row group, so the VALU work interleaves with the matrix cores.  The
+// 4-bit formats decode through the 16 bf16 products value * scale, built once
+// per step in registers and looked up with byte permutes (a codebook in LDS
+// made the kernel LDS-bound); e4m3 decodes with the hardware convert.  The
+// two stages are distinct LDS objects and the K loop is unrolled by two (see
+// the fp8 kernel): the copies in flight never alias the fragment reads, so no
+// read waits for them.
 // MFMA: v_mfma_f32_16x16x32_bf16, B tile as the first operand so each lane
 // holds four consecutive output columns.  bf16 rounding is the hardware RNE
 // pack-convert (v_cvt_pk_bf16_f32), the same rounding as f32_to_bf16_bits.
@@ -541,59 +549,116 @@ struct Raw32 {
   uint4 a, b;
 };
 
-// 32 e4m3 weights of tile row r, half h: layers.py:121-127, the code's value
-// (hardware decode, exact for every code, NaN codes to NaN) times the scale
-// in fp32, rounded to bf16
-__device__ __forceinline__ void dequant32_fp8_to_lds(const Raw32& raw, float s, uint8_t* tile, int r, int h) {
+// e4m3 weights 8j..8j+7 of the 32 of tile row r, half h: layers.py:121-127,
+// the code's value (hardware decode, exact for every code, NaN codes to NaN)
+// times the scale in fp32, rounded to bf16
+__device__ __forceinline__ void dequant8_fp8_to_lds(const Raw32& raw, float s, int j, uint8_t* tile, int r, int h) {
   const uint32_t words[8] = {raw.a.x, raw.a.y, raw.a.z, raw.a.w, raw.b.x, raw.b.y, raw.b.z, raw.b.w};
+  uint32_t out[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {  // 8 elements (8 bytes) per 16-byte LDS chunk
-    uint32_t out[4];
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[2 * j + w], false);
-      const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[2 * j + w], true);
-      const v2bf p0 = {(__bf16)(lo[0] * s), (__bf16)(lo[1] * s)};
-      const v2bf p1 = {(__bf16)(hi[0] * s), (__bf16)(hi[1] * s)};
-      out[2 * w] = __builtin_bit_cast(uint32_t, p0);
-      out[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
-    }
-    *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
+  for (int w = 0; w < 2; ++w) {
+    const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[2 * j + w], false);
+    const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)words[2 * j + w], true);
+    const v2bf p0 = {(__bf16)(lo[0] * s), (__bf16)(lo[1] * s)};
+    const v2bf p1 = {(__bf16)(hi[0] * s), (__bf16)(hi[1] * s)};
+    out[2 * w] = __builtin_bit_cast(uint32_t, p0);
+    out[2 * w + 1] = __builtin_bit_cast(uint32_t, p1);
   }
+  *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-// 32 weights (16 packed bytes, low nibble first) of tile row r, half h
+// The 16 bf16 weight values a thread can meet in one K step (all 32 of its
+// weights share one scale): value(code) * scale rounded to bf16, held as two
+// byte tables -- lo[q] / hi[q] carry the low / high bytes of entries
+// 4q..4q+3 -- so a code is looked up with byte permutes instead of a memory
+// read per weight.
+struct Lut16 {
+  uint32_t lo[4], hi[4];
+};
+
 template <int FMT>
-__device__ __forceinline__ void dequant32_to_lds(const Raw32& rw, float s, const float* lut, uint8_t* tile, int r,
-                                                 int h) {
-  if constexpr (FMT == FMT_FP8P) {
-    dequant32_fp8_to_lds(rw, s, tile, r, h);
-    return;
-  }
-  const uint4 raw = rw.a;
-  const uint32_t bytes[4] = {raw.x, raw.y, raw.z, raw.w};
-  const uint32_t sb = __float_as_uint(s);  // MXFP4: e8m0 byte
+__device__ __forceinline__ Lut16 lut16_build(float s) {
+  uint32_t p[8];
+  if constexpr (FMT == FMT_NF4) {
+    // layers.py:172-184: codebook value times scale in fp32, then bf16
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {  // 8 elements (4 bytes) per 16-byte LDS chunk
-    uint32_t out[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint32_t byte = (bytes[j] >> (8 * b)) & 0xFFu;
-      float v0, v1;
-      if constexpr (FMT == FMT_NF4) {
-        v0 = lut[byte & 15u] * s;  // layers.py:172-184: codebook value times scale in fp32
-        v1 = lut[byte >> 4] * s;
-      } else {
-        // e2m1 value (sign in bit 3) times 2^(e - 127); e = 0xFF marks a NaN block
-        const float a0 = ldexpf(lut[byte & 15u], (int)sb - 127);
-        const float a1 = ldexpf(lut[byte >> 4], (int)sb - 127);
-        v0 = (sb == 0xFFu) ? __uint_as_float(0x7FC00000u) : a0;
-        v1 = (sb == 0xFFu) ? __uint_as_float(0x7FC00000u) : a1;
-      }
-      const v2bf p = {(__bf16)v0, (__bf16)v1};
-      out[b] = __builtin_bit_cast(uint32_t, p);
+    for (int k = 0; k < 8; ++k) {
+      const v2bf t = {(__bf16)(kNF4c[2 * k] * s), (__bf16)(kNF4c[2 * k + 1] * s)};
+      p[k] = __builtin_bit_cast(uint32_t, t);
     }
-    *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
+  } else {
+    // e2m1 value times 2^(e - 127) (s carries the e8m0 byte e); e = 0xFF
+    // marks a NaN block
+    const int e = (int)__float_as_uint(s) - 127;
+    const bool nan_block = __float_as_uint(s) == 0xFFu;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float v0 = ldexpf(k < 4 ? kE2M1c[2 * k] : -kE2M1c[2 * k - 8], e);
+      const float v1 = ldexpf(k < 4 ? kE2M1c[2 * k + 1] : -kE2M1c[2 * k - 7], e);
+      const v2bf t = {(__bf16)v0, (__bf16)v1};
+      p[k] = nan_block ? 0x7FC07FC0u : __builtin_bit_cast(uint32_t, t);
+    }
+  }
+  Lut16 t;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    t.lo[q] = __builtin_amdgcn_perm(p[2 * q + 1], p[2 * q], 0x06040200u);
+    t.hi[q] = __builtin_amdgcn_perm(p[2 * q + 1], p[2 * q], 0x07050301u);
+  }
+  return t;
+}
+
+// Low and high bytes of four entries: byte i of sel (0..7) indexes both
+// halves of the table, byte i of half (i or 4 + i) then takes the entry from
+// entries 0..7 or 8..15.
+__device__ __forceinline__ void lut16_lookup(const Lut16& t, uint32_t sel, uint32_t half, uint32_t& lo,
+                                             uint32_t& hi) {
+  const uint32_t l0 = __builtin_amdgcn_perm(t.lo[1], t.lo[0], sel);
+  const uint32_t l1 = __builtin_amdgcn_perm(t.lo[3], t.lo[2], sel);
+  const uint32_t h0 = __builtin_amdgcn_perm(t.hi[1], t.hi[0], sel);
+  const uint32_t h1 = __builtin_amdgcn_perm(t.hi[3], t.hi[2], sel);
+  lo = __builtin_amdgcn_perm(l1, l0, half);
+  hi = __builtin_amdgcn_perm(h1, h0, half);
+}
+
+// What a thread needs to decode its 32 weights of one K step: the byte
+// tables (4-bit formats) or the scale (FP8P)
+template <int FMT>
+struct StepDecode {
+  Lut16 t;
+  float s;
+};
+
+template <int FMT>
+__device__ __forceinline__ StepDecode<FMT> decode_begin(float s) {
+  StepDecode<FMT> d;
+  d.s = s;
+  if constexpr (FMT != FMT_FP8P) d.t = lut16_build<FMT>(s);
+  return d;
+}
+
+// weights 8j..8j+7 (4 packed bytes, low nibble first; or 8 e4m3 bytes) of
+// the 32 of tile row r, half h, as one 16-byte LDS chunk
+template <int FMT>
+__device__ __forceinline__ void decode_chunk(const StepDecode<FMT>& d, const Raw32& rw, int j, uint8_t* tile, int r,
+                                             int h) {
+  if constexpr (FMT == FMT_FP8P) {
+    dequant8_fp8_to_lds(rw, d.s, j, tile, r, h);
+  } else {
+    const uint32_t words[4] = {rw.a.x, rw.a.y, rw.a.z, rw.a.w};
+    const uint32_t w = words[j];
+    uint32_t le, he, lo_, ho;
+    // weights 0, 2, 4, 6 are the low nibbles, 1, 3, 5, 7 the high ones; bit 3
+    // of a nibble picks the table half
+    lut16_lookup(d.t, w & 0x07070707u, ((w >> 1) & 0x04040404u) | 0x03020100u, le, he);
+    lut16_lookup(d.t, (w >> 4) & 0x07070707u, ((w >> 5) & 0x04040404u) | 0x03020100u, lo_, ho);
+    const uint32_t l03 = __builtin_amdgcn_perm(lo_, le, 0x05010400u);  // low bytes of weights 0..3
+    const uint32_t h03 = __builtin_amdgcn_perm(ho, he, 0x05010400u);
+    const uint32_t l47 = __builtin_amdgcn_perm(lo_, le, 0x07030602u);
+    const uint32_t h47 = __builtin_amdgcn_perm(ho, he, 0x07030602u);
+    *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) =
+        make_uint4(__builtin_amdgcn_perm(h03, l03, 0x05010400u), __builtin_amdgcn_perm(h03, l03, 0x07030602u),
+                   __builtin_amdgcn_perm(h47, l47, 0x05010400u), __builtin_amdgcn_perm(h47, l47, 0x07030602u));
   }
 }
 
@@ -603,7 +668,6 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   __shared__ __attribute__((aligned(16))) uint8_t fw0[FT];
   __shared__ __attribute__((aligned(16))) uint8_t fx1[FT];
   __shared__ __attribute__((aligned(16))) uint8_t fw1[FT];
-  __shared__ float lut[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
   const int num_n = (int)((g.N + FBN - 1) / FBN);
@@ -623,7 +687,6 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   const int64_t m0 = (int64_t)(first_m + in_group % gsize) * FBM;
   const int64_t n0 = (int64_t)(in_group / gsize) * FBN;
 
-  if (tid < 16) lut[tid] = (FMT == FMT_NF4) ? kNF4[tid] : (FMT == FMT_MXFP4) ? e2m1_value((uint32_t)tid) : 0.f;
 
   // X tile: direct-to-LDS; wave w moves the 8-row groups w, w+8, w+16, w+24
   // (bit 3 of its rows is w & 1, so its lanes' swizzled chunks are the same
@@ -674,8 +737,9 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     Raw32 raw0;
     float s0;
     w_load(0, raw0, s0);
-    __syncthreads();  // lut
-    dequant32_to_lds<FMT>(raw0, s0, lut, fw0, br, bh);
+    const StepDecode<FMT> d0 = decode_begin<FMT>(s0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) decode_chunk<FMT>(d0, raw0, j, fw0, br, bh);
   }
   w_load(min(1, nk - 1), raw_pf1, sc_pf1);
   __builtin_amdgcn_s_waitcnt(0);
@@ -691,6 +755,7 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     // the idle stage) keep the step one basic block
     const int kn = min(kt + 1, nk - 1);
 
+    StepDecode<FMT> dec;
     v8i bf[4];
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) bf[tn] = frag32(tb, wn * 64 + tn * 16, lane);
@@ -700,18 +765,21 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
       v8i af_next;
       if (tm + 1 < 8) af_next = frag32(ta, wm * 128 + (tm + 1) * 16, lane);
       if (tm < 4) issue_x(xa_next, kn, tm);
-      if (tm == 4) {
-        // block kn's bytes become visible to the compiler only here, so none
-        // of the dequant work (or a wait for the loads) moves up into the
-        // first half of the MFMA phase; then block kn+1's loads go out, the
-        // last vector-memory operations of the step
-        Raw32& r = BUF ? raw_pf0 : raw_pf1;
-        float& s = BUF ? sc_pf0 : sc_pf1;
+      Raw32& r = BUF ? raw_pf0 : raw_pf1;
+      float& s = BUF ? sc_pf0 : sc_pf1;
+      // block kn's codes (loaded during the previous step) become visible to
+      // the compiler at tm == 0; their decode is spread over the step, one
+      // 16-byte chunk per odd tm, so it interleaves with the matrix-core work
+      // instead of stalling it in one burst
+      if (tm == 0) {
         asm volatile("" : "+v"(r.a.x), "+v"(r.a.y), "+v"(r.a.z), "+v"(r.a.w), "+v"(s));
         if constexpr (BYTE_CODES) asm volatile("" : "+v"(r.b.x), "+v"(r.b.y), "+v"(r.b.z), "+v"(r.b.w));
-        w_load(min(kt + 2, nk - 1), BUF ? raw_pf1 : raw_pf0, BUF ? sc_pf1 : sc_pf0);
-        dequant32_to_lds<FMT>(r, s, lut, wb_next, br, bh);
+        dec = decode_begin<FMT>(s);
       }
+      if (tm & 1) decode_chunk<FMT>(dec, r, tm >> 1, wb_next, br, bh);
+      // block kn+1's loads go out after this step's X copies, as the last
+      // vector-memory operations of the step
+      if (tm == 4) w_load(min(kt + 2, nk - 1), BUF ? raw_pf1 : raw_pf0, BUF ? sc_pf1 : sc_pf0);
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) acc[tm][tn] = mma_bf16_64(bf[tn], af, acc[tm][tn]);
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");

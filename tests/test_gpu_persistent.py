@@ -208,3 +208,50 @@ def test_fp8p_fused_gemm_rejects_bad_scale_shape(gpu_device):
     w = torch.zeros(8, 64, dtype=torch.uint8, device=gpu_device).view(torch.float8_e4m3fn)
     with pytest.raises(ValueError):
         P.linear_fp8p(x, w, torch.ones(3, device=gpu_device))
+
+
+@pytest.mark.parametrize("block", [64, 256, 0])
+def test_nf4_fused_gemm_dequant_exact_all_codes(gpu_device, block):
+    """X = I returns deq(W)^T exactly: every NF4 code at every nibble position,
+    under scales spanning many binades, against the oracle dequant (bit for
+    bit, after the bf16 rounding of the weight dtype)."""
+    from lowbit import persistent as P
+
+    K, N = 256, 80
+    rng = np.random.default_rng(20260604)
+    idx = np.stack([rng.permutation(np.tile(np.arange(16), K // 16)) for _ in range(N)]).astype(np.uint8)
+    flat = idx.reshape(-1)
+    packed = (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
+    nb = (N * K) // block if block else 1
+    scales = np.exp(rng.uniform(np.log(1e-30), np.log(1e30), nb)).astype(np.float32)
+    x = torch.eye(K, dtype=torch.bfloat16, device=gpu_device)
+    y = P.linear_nf4(x, torch.from_numpy(packed).to(gpu_device), torch.from_numpy(scales).to(gpu_device),
+                     out_features=N, block=block if block else N * K, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    want = O.round_bf16(O.nf4_dequant(packed, scales, N * K, block if block else N * K)).reshape(N, K)
+    np.testing.assert_array_equal(y.cpu().numpy().T, want)
+
+
+def test_mxfp4_fused_gemm_dequant_exact_all_codes(gpu_device):
+    """X = I returns deq(W)^T exactly for every e2m1 code under a range of
+    e8m0 scales; a block with scale byte 0xFF (NaN) turns its row's output
+    column NaN."""
+    from lowbit import persistent as P
+
+    K, N = 256, 64
+    rng = np.random.default_rng(20260605)
+    idx = np.stack([rng.permutation(np.tile(np.arange(16), K // 16)) for _ in range(N)]).astype(np.uint8)
+    flat = idx.reshape(-1)
+    packed = (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
+    sbytes = rng.integers(127 - 100, 127 + 100, (N * K) // 32).astype(np.uint8)
+    nan_row = 9
+    sbytes[nan_row * (K // 32) + 3] = 0xFF
+    x = torch.eye(K, dtype=torch.bfloat16, device=gpu_device)
+    y = P.linear_mxfp4(x, torch.from_numpy(packed).to(gpu_device), torch.from_numpy(sbytes).to(gpu_device),
+                       out_features=N, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().T
+    want = O.round_bf16(O.mxfp4_dequant(packed, sbytes, N * K)).reshape(N, K)
+    assert np.isnan(got[nan_row]).all()
+    keep = [r for r in range(N) if r != nan_row]
+    np.testing.assert_array_equal(got[keep], want[keep])
