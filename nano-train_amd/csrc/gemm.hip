@@ -33,6 +33,7 @@ namespace ntlb {
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 
 struct GemmArgs {
   const uint8_t* a;
@@ -84,7 +85,10 @@ struct GemmArgs {
   uint32_t* ws_count;    // per tail tile; zero between calls (the kernel resets it)
 };
 
-constexpr int EPI_STORE = 0, EPI_SWIGLU = 1;
+// Epilogues: store the tile as bf16 (EPI_STORE), fp32 or fp16, or the
+// SwiGLU + 1x128 quantization of the expert MLP.  The output dtype is part of
+// the kernel so that each kernel holds one straight-line store path.
+constexpr int EPI_STORE = 0, EPI_SWIGLU = 1, EPI_STORE_F32 = 2, EPI_STORE_F16 = 3;
 
 constexpr int BM = 256, BN = 256, BK = 128;
 constexpr int NTHREADS = 512;
@@ -181,31 +185,42 @@ __device__ __forceinline__ uint8_t* slab_row(uint8_t* s0, uint8_t* s1, uint8_t* 
   return (k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3) + (r & 63) * 512;
 }
 
-// acc = sum over chunks c = 0..S-1, in that order, of the partial tiles at
-// part + c * NTHREADS * 32 (float4 units, this thread's slot 0).  Rounds of 32
-// loads are in flight at once; acc is rebuilt slot by slot, so only the slots
-// already summed stay live beside the loads.
-template <int S>
-__device__ __forceinline__ void sum_partials(v4f (&acc)[8][4], const float4* part) {
-  constexpr int SLOTS = 32 / S;
+// acc = sum over chunks c = 0..s-1, in that order, of the partial tiles at
+// part + c * NTHREADS * 32 (float4 units, this thread's slot 0):
+// ((p0 + p1) + p2) + ...  Rounds of 16 loads (four slots of four chunks)
+// are in flight at once; one instance serves every s.
+__device__ __forceinline__ void sum_partials(v4f (&acc)[8][4], const float4* part, int s) {
+  for (int c0 = 0; c0 < s; c0 += 4) {
 #pragma unroll
-  for (int r = 0; r < 32; r += SLOTS) {
-    float4 v[S][SLOTS];
+    for (int r = 0; r < 32; r += 4) {
+      float4 v[4][4];
 #pragma unroll
-    for (int c = 0; c < S; ++c)
+      for (int c = 0; c < 4; ++c) {
+        const int cc = min(c0 + c, s - 1);  // in bounds; chunks past s are not added
 #pragma unroll
-      for (int k = 0; k < SLOTS; ++k)
-        if (r + k < 32) v[c][k] = part[(int64_t)c * NTHREADS * 32 + (r + k) * NTHREADS];
+        for (int k = 0; k < 4; ++k) v[c][k] = part[(int64_t)cc * NTHREADS * 32 + (r + k) * NTHREADS];
+      }
 #pragma unroll
-    for (int k = 0; k < SLOTS; ++k) {
-      if (r + k < 32) {
+      for (int k = 0; k < 4; ++k) {
+        v4f& a = acc[(r + k) >> 2][(r + k) & 3];
         v4f t = (v4f){v[0][k].x, v[0][k].y, v[0][k].z, v[0][k].w};
+        if (c0 > 0) t = a + t;
 #pragma unroll
-        for (int c = 1; c < S; ++c) t += (v4f){v[c][k].x, v[c][k].y, v[c][k].z, v[c][k].w};
-        acc[(r + k) >> 2][(r + k) & 3] = t;
+        for (int c = 1; c < 4; ++c)
+          if (c0 + c < s) t += (v4f){v[c][k].x, v[c][k].y, v[c][k].z, v[c][k].w};
+        a = t;
       }
     }
   }
+}
+
+// a 64-bit value that is the same in every lane, as a scalar
+template <typename T>
+__device__ __forceinline__ T uniform64(T v) {
+  const uint64_t u = (uint64_t)v;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+  return (T)(((uint64_t)hi << 32) | lo);
 }
 
 template <int GRID, bool B_UNIFORM, bool GROUPED, int EPI = EPI_STORE>
@@ -297,6 +312,23 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   const int64_t srow = own_a ? min<int64_t>(m0 + tid, g.M - 1) : min<int64_t>(n0 + tid - BM, g.N - 1);
   const float* s_src = own_a ? g.sa + (srow >> g.a_shift) * g.sa_row : g.sb + (srow >> g.b_shift) * g.sb_row;
   const int64_t s_step = own_a ? g.sa_col : g.sb_col;
+
+  // What the store epilogue reads of the arguments, loaded now and kept in
+  // scalar registers through the K loop: re-loading them after the loop
+  // costs a scalar-cache miss per use.
+  uintptr_t e_y = reinterpret_cast<uintptr_t>(g.y), e_bias = reinterpret_cast<uintptr_t>(g.bias);
+  uintptr_t e_nan_a = reinterpret_cast<uintptr_t>(g.nan_a), e_nan_b = reinterpret_cast<uintptr_t>(g.nan_b);
+  int64_t e_ldy = g.ldy, e_M = g.M, e_N = g.N;
+  int e_misc = (g.vec_out ? 1 : 0) | (g.bias_dtype << 1);
+  if constexpr (EPI != EPI_SWIGLU) {
+    // uniform by construction (the grouped mapping derives M and nan_b from
+    // the offset table in LDS, which the compiler treats as per-lane)
+    e_y = uniform64(e_y); e_bias = uniform64(e_bias); e_nan_a = uniform64(e_nan_a); e_nan_b = uniform64(e_nan_b);
+    e_ldy = uniform64(e_ldy); e_M = uniform64(e_M); e_N = uniform64(e_N);
+    e_misc = __builtin_amdgcn_readfirstlane(e_misc);
+    asm volatile("" : "+s"(e_y), "+s"(e_bias), "+s"(e_nan_a), "+s"(e_nan_b));
+    asm volatile("" : "+s"(e_ldy), "+s"(e_M), "+s"(e_N), "+s"(e_misc));
+  }
 
   const int nk = (int)(g.Kp / BK);
   // K blocks [kb0, kb1) of this workgroup: all of them, or one split chunk
@@ -394,7 +426,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     if (kt + 1 < kb1) step(std::integral_constant<int, 1>(), kt + 1);
   }
 
-  if constexpr (!GROUPED && EPI == EPI_STORE) {
+  if constexpr (!GROUPED && EPI != EPI_SWIGLU) {
     if (split_tail >= 0) {
       // publish this chunk's partial tile; the last chunk to arrive sums all
       // of them in chunk order (the same order every call) and stores the tile
@@ -417,15 +449,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       if (!last) return;
       if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       __syncthreads();
-      switch (g.split_s) {
-        case 2: sum_partials<2>(acc, part); break;
-        case 3: sum_partials<3>(acc, part); break;
-        case 4: sum_partials<4>(acc, part); break;
-        case 5: sum_partials<5>(acc, part); break;
-        case 6: sum_partials<6>(acc, part); break;
-        case 7: sum_partials<7>(acc, part); break;
-        default: sum_partials<8>(acc, part); break;
-      }
+      sum_partials(acc, part, g.split_s);
       if (tid == 0) atomicExch(g.ws_count + split_tail, 0u);  // ready for the next call
     }
   }
@@ -464,75 +488,134 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   }
 
   // ---------------------------------------------------------------- epilogue
-  // lane holds rows m = m0 + wm*128 + tm*16 + lane%16 and columns
-  // n = n0 + wn*64 + tn*16 + 4*(lane/16) + r
+  // The tile origin passes through an empty asm here so that no address
+  // arithmetic of the epilogue is hoisted above the K loop, where every
+  // register is taken (hoisted values would be spilled across the loop).
+  int lane_e = lane;
+  asm volatile("" : "+s"(m0), "+s"(n0), "+v"(lane_e));
+  // lane_e holds rows m = m0 + wm*128 + tm*16 + lane_e%16 and columns
+  // n = n0 + wn*64 + tn*16 + 4*(lane_e/16) + r
   const int slab = wave >> 1;
   uint8_t* stage_w = (slab == 0 ? lds_a0 : slab == 1 ? lds_b0 : slab == 2 ? lds_a1 : lds_b1) + (wave & 1) * (TILE_A / 2);
-  const bool out_f32 = g.y_dtype == DT_F32;
-  const int pitch = out_f32 ? EPI_PITCH_F32 : EPI_PITCH_16;
+  const int64_t M = e_M, N = e_N, ldy = e_ldy;
+  // bias and NaN flags: the indices are clamped into the matrix (values for
+  // columns or rows past it are never stored), so the loads are
+  // unconditional behind one uniform test per pointer; the flags are packed
+  // into bit masks
   float bias[4][4];
-  bool nan_col[4][4];
 #pragma unroll
   for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t n = n0 + wn * 64 + tn * 16 + (lane >> 4) * 4 + r;
-      const bool in = n < g.N;
-      bias[tn][r] = (g.bias && in) ? load_elem(g.bias, g.bias_dtype, n) : 0.f;
-      nan_col[tn][r] = g.nan_b && in && g.nan_b[n];
+    for (int r = 0; r < 4; ++r) bias[tn][r] = 0.f;
+  if (e_bias) {
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = min<int64_t>(n0 + wn * 64 + tn * 16 + (lane_e >> 4) * 4 + r, N - 1);
+        bias[tn][r] = load_elem(reinterpret_cast<const void*>(e_bias), e_misc >> 1, n);
+      }
+  }
+  uint32_t nan_cols = 0, nan_rows = 0;  // bit tn*4+r / bit tm
+  if (e_nan_b) {
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t n = min<int64_t>(n0 + wn * 64 + tn * 16 + (lane_e >> 4) * 4 + r, N - 1);
+        nan_cols |= (reinterpret_cast<const int32_t*>(e_nan_b)[n] != 0 ? 1u : 0u) << (tn * 4 + r);
+      }
+  }
+  if (e_nan_a) {
+#pragma unroll
+    for (int tm = 0; tm < 8; ++tm) {
+      const int64_t m = min<int64_t>(m0 + wm * 128 + tm * 16 + (lane_e & 15), M - 1);
+      nan_rows |= (reinterpret_cast<const int32_t*>(e_nan_a)[m] != 0 ? 1u : 0u) << tm;
     }
+  }
+  // Interior tiles (FULL) store without bounds checks; each wave stages and
+  // re-reads only its own slice, so the waits between the two halves of a
+  // pass are wave-local.
+  constexpr int ODT = EPI == EPI_STORE_F32 ? DT_F32 : EPI == EPI_STORE_F16 ? DT_F16 : DT_BF16;
+  auto store_tile = [&](auto fullc, auto flagsc) {
+    constexpr bool FULL = decltype(fullc)::value;
+    constexpr bool FLAGS = decltype(flagsc)::value;
+    constexpr int esz = ODT == DT_F32 ? 4 : 2;
+    constexpr int pitch = ODT == DT_F32 ? EPI_PITCH_F32 : EPI_PITCH_16;
 #pragma unroll
-  for (int part = 0; part < 4; ++part) {
+    for (int part = 0; part < 4; ++part) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int tm = part * 2 + t;
-      const int rloc = t * 16 + (lane & 15);
-      const int64_t m = m0 + wm * 128 + tm * 16 + (lane & 15);
-      const bool nan_row = g.nan_a && m < g.M && g.nan_a[m];
+      for (int t = 0; t < 2; ++t) {
+        const int tm = part * 2 + t;
+        const int rloc = t * 16 + (lane_e & 15);
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        float v[4];
+        for (int tn = 0; tn < 4; ++tn) {
+          float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          v[r] = acc[tm][tn][r] + bias[tn][r];
-          if (nan_row || nan_col[tn][r]) v[r] = __uint_as_float(0x7FC00000u);
+          for (int r = 0; r < 4; ++r) {
+            v[r] = acc[tm][tn][r] + bias[tn][r];
+            if constexpr (FLAGS) {
+              const bool nan = ((nan_rows >> tm) | (nan_cols >> (tn * 4 + r))) & 1u;
+              v[r] = nan ? __uint_as_float(0x7FC00000u) : v[r];
+            }
+          }
+          uint8_t* dst = stage_w + rloc * pitch + (tn * 16 + (lane_e >> 4) * 4) * esz;
+          if constexpr (ODT == DT_F32) {
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          } else if constexpr (ODT == DT_BF16) {
+            // hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32)
+            const v2bf p0 = {(__bf16)v[0], (__bf16)v[1]}, p1 = {(__bf16)v[2], (__bf16)v[3]};
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+          } else {
+            __half h[4] = {__float2half(v[0]), __float2half(v[1]), __float2half(v[2]), __float2half(v[3])};
+            *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(h);
+          }
         }
-        const int cbyte = (tn * 16 + (lane >> 4) * 4) * (out_f32 ? 4 : 2);
-        uint8_t* dst = stage_w + rloc * pitch + cbyte;
-        if (out_f32) {
-          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        } else if (g.y_dtype == DT_BF16) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(
-              (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
-              (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's staging writes are done
+      __builtin_amdgcn_wave_barrier();
+      // 32 rows x (128 or 256) bytes; 16-byte chunks, row-contiguous across lanes
+      constexpr int chunks_per_row = 64 * esz / 16;
+      constexpr int epc = 16 / esz;  // elements per chunk
+#pragma unroll
+      for (int j = 0; j < chunks_per_row / 2; ++j) {
+        const int q = lane_e + 64 * j;
+        const int row = q / chunks_per_row, c = q % chunks_per_row;
+        const int64_t m = m0 + wm * 128 + part * EPI_ROWS + row;
+        const int64_t n = n0 + wn * 64 + c * epc;
+        const uint8_t* src = stage_w + row * pitch + c * 16;
+        uint8_t* ydst = reinterpret_cast<uint8_t*>(e_y) + (m * ldy + n) * esz;
+        if constexpr (FULL) {
+          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+          continue;
+        }
+        if (m >= M || n >= N) continue;
+        if ((e_misc & 1) && n + epc <= N) {
+          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
         } else {
-          __half h[4] = {__float2half(v[0]), __float2half(v[1]), __float2half(v[2]), __float2half(v[3])};
-          *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(h);
+          // ragged edge or unaligned output: element by element
+          using E = std::conditional_t<esz == 4, uint32_t, uint16_t>;
+#pragma nounroll
+          for (int e = 0; e < epc && n + e < N; ++e)
+            reinterpret_cast<E*>(ydst)[e] = reinterpret_cast<const E*>(src)[e];
         }
       }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the re-reads are done before the next pass overwrites
+      __builtin_amdgcn_wave_barrier();
     }
-    __syncthreads();
-    // 32 rows x (128 or 256) bytes; 16-byte chunks, row-contiguous across lanes
-    const int chunks_per_row = out_f32 ? 16 : 8;
-    const int esz = out_f32 ? 4 : 2;
-    const int epc = 16 / esz;  // elements per chunk
-#pragma unroll
-    for (int j = 0; j < (out_f32 ? 8 : 4); ++j) {
-      const int q = lane + 64 * j;
-      const int row = q / chunks_per_row, c = q % chunks_per_row;
-      const int64_t m = m0 + wm * 128 + part * EPI_ROWS + row;
-      const int64_t n = n0 + wn * 64 + c * epc;
-      if (m >= g.M || n >= g.N) continue;
-      const uint8_t* src = stage_w + row * pitch + c * 16;
-      uint8_t* ydst = reinterpret_cast<uint8_t*>(g.y) + (m * g.ldy + n) * esz;
-      if (g.vec_out && n + epc <= g.N) {
-        *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
-      } else {
-        for (int e = 0; e < epc && n + e < g.N; ++e)
-          for (int bidx = 0; bidx < esz; ++bidx) ydst[e * esz + bidx] = src[e * esz + bidx];
-      }
-    }
-    __syncthreads();
+  };
+  const bool full = (e_misc & 1) && m0 + BM <= M && n0 + BN <= N;
+  if (e_nan_a || e_nan_b) {
+    if (full)
+      store_tile(std::true_type(), std::true_type());
+    else
+      store_tile(std::false_type(), std::true_type());
+  } else {
+    if (full)
+      store_tile(std::true_type(), std::false_type());
+    else
+      store_tile(std::false_type(), std::false_type());
   }
 }
 
@@ -601,6 +684,17 @@ __device__ __forceinline__ void swiglu_quant_rows(const GemmArgs& g, const uint8
 
 using namespace ntlb;
 
+// the store kernel for the output dtype
+template <int GRID, bool B_UNIFORM, bool GROUPED>
+static void launch_store(const GemmArgs& g, dim3 grd, dim3 blk, hipStream_t st) {
+  if (g.y_dtype == DT_F32)
+    gemm_blockscaled_kernel<GRID, B_UNIFORM, GROUPED, EPI_STORE_F32><<<grd, blk, 0, st>>>(g);
+  else if (g.y_dtype == DT_F16)
+    gemm_blockscaled_kernel<GRID, B_UNIFORM, GROUPED, EPI_STORE_F16><<<grd, blk, 0, st>>>(g);
+  else
+    gemm_blockscaled_kernel<GRID, B_UNIFORM, GROUPED, EPI_STORE><<<grd, blk, 0, st>>>(g);
+}
+
 // Split plan of the tail of a dense tiling: tiles past the last whole wave
 // (one workgroup per CU) are cut into split_s K chunks when that fills the
 // idle CUs; split_s = 1 means no split.
@@ -634,9 +728,12 @@ static SplitPlan split_plan(int64_t tiles, int nk) {
   return p;
 }
 
-// workspace layout: one uint32 counter per tail tile (padded to 256 bytes),
-// then the fp32 partials [tail][s][NTHREADS * 128]
-static int64_t split_count_bytes(const SplitPlan& p) { return ((int64_t)p.tail * 4 + 255) / 256 * 256; }
+// Workspace layout: the tile counters, then the fp32 partials
+// [tail][s][NTHREADS * 128].  The counter area is the same for every plan on
+// a device (one uint32 per possible tail tile: a plan's tail is at most half
+// the compute units), so calls of different shapes on one workspace find
+// their counters where the previous call left them, at zero.
+static int64_t split_count_bytes(const SplitPlan&) { return ((int64_t)device_cus() / 2 * 4 + 255) / 256 * 256; }
 
 static int64_t split_ws_bytes(const SplitPlan& p) {
   if (p.s < 2) return 0;
@@ -701,14 +798,14 @@ extern "C" int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda,
   dim3 grd((unsigned)grid_wgs), blk(NTHREADS);
   if (grid == NTLB_GRID_E4M3) {
     if (b_uniform)
-      gemm_blockscaled_kernel<GRID_E4M3, true, false><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_E4M3, true, false>(g, grd, blk, st);
     else
-      gemm_blockscaled_kernel<GRID_E4M3, false, false><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_E4M3, false, false>(g, grd, blk, st);
   } else {
     if (b_uniform)
-      gemm_blockscaled_kernel<GRID_INT, true, false><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_INT, true, false>(g, grd, blk, st);
     else
-      gemm_blockscaled_kernel<GRID_INT, false, false><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_INT, false, false>(g, grd, blk, st);
   }
   return check_launch(fn);
 }
@@ -763,14 +860,14 @@ extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t
   dim3 grd((unsigned)tiles), blk(NTHREADS);
   if (grid == NTLB_GRID_E4M3) {
     if (b_uniform)
-      gemm_blockscaled_kernel<GRID_E4M3, true, true><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_E4M3, true, true>(g, grd, blk, st);
     else
-      gemm_blockscaled_kernel<GRID_E4M3, false, true><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_E4M3, false, true>(g, grd, blk, st);
   } else {
     if (b_uniform)
-      gemm_blockscaled_kernel<GRID_INT, true, true><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_INT, true, true>(g, grd, blk, st);
     else
-      gemm_blockscaled_kernel<GRID_INT, false, true><<<grd, blk, 0, st>>>(g);
+      launch_store<GRID_INT, false, true>(g, grd, blk, st);
   }
   return check_launch(fn);
 }

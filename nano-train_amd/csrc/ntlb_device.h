@@ -21,10 +21,12 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_
 
 // fp32 -> bf16 round to nearest even; NaN stays NaN (quiet bit set).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  // a select, not an early return: inside unrolled loops a per-element branch
+  // turns into exec-mask control flow around every conversion
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rne = (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t qnan = (u >> 16) | 0x40u;
+  return (uint16_t)(((u & 0x7FFFFFFFu) > 0x7F800000u) ? qnan : rne);
 }
 
 // ---------------------------------------------------------------------------

@@ -137,3 +137,23 @@ def test_split_full_size_c3_dgrad(gpu_device):
     wdq = O.quant_block_128x128(to_np32(w), grid=O.GRID_E4M3)[3]
     err = rel_fro_bf16(yb[rows][:, cols], O.gemm_ref(xdq, wdq[cols]))
     assert err <= TOL, err
+
+
+def test_split_workspace_shared_across_plans(gpu_device):
+    """One workspace serves plans with different tail counts: a plan with 100
+    split tiles (counters past the first 256 bytes), then one with 8, then the
+    first again; every result matches the unsplit kernel."""
+    from lowbit import ops
+
+    big = _operands(2560, 2560, 1024, "e4m3", gpu_device, 20261109)[2:]
+    small = _operands(512, 1024, 1024, "e4m3", gpu_device, 20261110)[2:]
+    assert _splits(2560, 2560, 1024) and _splits(512, 1024, 1024)
+    stream = torch.cuda.Stream(device=gpu_device)  # its own workspace
+    stream.wait_stream(torch.cuda.current_stream())  # the operands were quantized there
+    with torch.cuda.stream(stream):
+        ref_big = ops.gemm_blockscaled(*big, out_dtype=torch.float32, split_tail=False)
+        ref_small = ops.gemm_blockscaled(*small, out_dtype=torch.float32, split_tail=False)
+        outs = [ops.gemm_blockscaled(*q, out_dtype=torch.float32) for q in (big, small, big, small, big)]
+    stream.synchronize()
+    for out, ref in zip(outs, (ref_big, ref_small, ref_big, ref_small, ref_big)):
+        assert O.rel_frobenius(out.cpu().numpy(), ref.cpu().numpy().astype(np.float64)) <= REASSOC
