@@ -458,27 +458,49 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     // Stage the whole 256x256 tile as bf16 (the reference's Linear outputs):
     // slab k holds rows 64k..64k+63, 512 bytes per row, 16-byte units
     // XOR-swizzled by row so 16 lanes on 16 rows hit distinct banks.
+    // NaN flags as bit masks (bit tm of the row flags, bit tn*4+q of the
+    // column flags), loaded from clamped indices behind one uniform test per
+    // pointer, so the staging below has no per-element branches
+    uint32_t nan_rows = 0, nan_cols = 0;
+    if (g.nan_a) {
 #pragma unroll
-    for (int tm = 0; tm < 8; ++tm) {
-      const int r = wm * 128 + tm * 16 + (lane & 15);
-      const int64_t m = m0 + r;
-      const bool nan_row = g.nan_a && m < g.M && g.nan_a[m];
-      uint8_t* rowp = slab_row(lds_a0, lds_b0, lds_a1, lds_b1, r);
-#pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        const int c = wn * 64 + tn * 16 + (lane >> 4) * 4;
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t n = n0 + c + q;
-          v[q] = acc[tm][tn][q];
-          if (nan_row || (g.nan_b && n < g.N && g.nan_b[n])) v[q] = __uint_as_float(0x7FC00000u);
-        }
-        *reinterpret_cast<uint2*>(rowp + (((c >> 3) ^ (r & 15)) << 4) + (c & 4) * 2) =
-            make_uint2((uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
-                       (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
-      }
+      for (int tm = 0; tm < 8; ++tm)
+        nan_rows |= (g.nan_a[min<int64_t>(m0 + wm * 128 + tm * 16 + (lane & 15), g.M - 1)] != 0 ? 1u : 0u) << tm;
     }
+    if (g.nan_b) {
+#pragma unroll
+      for (int tn = 0; tn < 4; ++tn)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          nan_cols |= (g.nan_b[min<int64_t>(n0 + wn * 64 + tn * 16 + (lane >> 4) * 4 + q, g.N - 1)] != 0 ? 1u : 0u)
+                      << (tn * 4 + q);
+    }
+    auto stage = [&](auto flagsc) {
+      constexpr bool FLAGS = decltype(flagsc)::value;
+#pragma unroll
+      for (int tm = 0; tm < 8; ++tm) {
+        const int r = wm * 128 + tm * 16 + (lane & 15);
+        uint8_t* rowp = slab_row(lds_a0, lds_b0, lds_a1, lds_b1, r);
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+          const int c = wn * 64 + tn * 16 + (lane >> 4) * 4;
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            v[q] = acc[tm][tn][q];
+            if constexpr (FLAGS)
+              v[q] = (((nan_rows >> tm) | (nan_cols >> (tn * 4 + q))) & 1u) ? __uint_as_float(0x7FC00000u) : v[q];
+          }
+          *reinterpret_cast<uint2*>(rowp + (((c >> 3) ^ (r & 15)) << 4) + (c & 4) * 2) =
+              make_uint2((uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
+                         (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
+        }
+      }
+    };
+    if (g.nan_a || g.nan_b)
+      stage(std::true_type());
+    else
+      stage(std::false_type());
     __syncthreads();
     if (g.h_sr)
       swiglu_quant_rows<GRID, true>(g, lds_a0, lds_b0, lds_a1, lds_b1, m0, n0, tid);
