@@ -214,15 +214,6 @@ __device__ __forceinline__ void sum_partials(v4f (&acc)[8][4], const float4* par
   }
 }
 
-// a 64-bit value that is the same in every lane, as a scalar
-template <typename T>
-__device__ __forceinline__ T uniform64(T v) {
-  const uint64_t u = (uint64_t)v;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
-  return (T)(((uint64_t)hi << 32) | lo);
-}
-
 template <int GRID, bool B_UNIFORM, bool GROUPED, int EPI = EPI_STORE>
 __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[TILE_A];

@@ -19,6 +19,16 @@ enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
+// a 64-bit value that is the same in every lane, as a scalar (lets values
+// the compiler cannot prove uniform be pinned in scalar registers)
+template <typename T>
+__device__ __forceinline__ T uniform64(T v) {
+  const uint64_t u = (uint64_t)v;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+  return (T)(((uint64_t)hi << 32) | lo);
+}
+
 // fp32 -> bf16 round to nearest even; NaN stays NaN (quiet bit set).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   // a select, not an early return: inside unrolled loops a per-element branch

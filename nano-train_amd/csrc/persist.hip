@@ -709,6 +709,13 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   const RowScales wsc = fused_row_scales<FMT>(g, bn);
 
   const int nk = (int)(g.K / FBK);
+  // the epilogue's arguments, kept in scalar registers through the K loop
+  uintptr_t e_y = reinterpret_cast<uintptr_t>(g.y);
+  int64_t e_ldy = g.ldy, e_M = g.M, e_N = g.N;
+  int e_f32 = g.y_dtype == DT_F32, e_vec = g.vec_out;
+  e_y = uniform64(e_y); e_ldy = uniform64(e_ldy); e_M = uniform64(e_M); e_N = uniform64(e_N);
+  e_f32 = __builtin_amdgcn_readfirstlane(e_f32); e_vec = __builtin_amdgcn_readfirstlane(e_vec);
+  asm volatile("" : "+s"(e_y), "+s"(e_ldy), "+s"(e_M), "+s"(e_N), "+s"(e_f32), "+s"(e_vec));
   v4f acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -797,51 +804,84 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
   }
 
+  // the tile origin and lane pass through an empty asm so that no epilogue
+  // address arithmetic is hoisted above the K loop, where every register is
+  // taken
+  int64_t m0e = uniform64(m0), n0e = uniform64(n0);
+  int lane_e = lane;
+  asm volatile("" : "+s"(m0e), "+s"(n0e), "+v"(lane_e));
   // epilogue: each wave stages 32 rows of its 128x64 tile at a time in a
-  // 16 KiB slice of the idle operand tiles; 16-byte row-contiguous stores
+  // 16 KiB slice of the idle operand tiles; 16-byte row-contiguous stores.
+  // One straight-line body per output dtype, interior tiles without bounds
+  // checks, and the arguments it needs held in scalar registers from before
+  // the K loop (re-loading them after it costs scalar-cache misses).
   const int slab = wave >> 1;
   uint8_t* stage_w = (slab == 0 ? fx0 : slab == 1 ? fw0 : slab == 2 ? fx1 : fw1) + (wave & 1) * (FT / 2);
-  const bool out_f32 = g.y_dtype == DT_F32;
-  const int pitch = out_f32 ? F_EPI_PITCH : (64 * 2 + 16);
+  auto store_tile = [&](auto f32c, auto fullc) {
+    constexpr bool OUT_F32 = decltype(f32c)::value;
+    constexpr bool FULL = decltype(fullc)::value;
+    constexpr int pitch = OUT_F32 ? F_EPI_PITCH : (64 * 2 + 16);
+    constexpr int esz = OUT_F32 ? 4 : 2;
+    constexpr int cpr = OUT_F32 ? 16 : 8;
+    constexpr int epc = 16 / esz;
 #pragma unroll
-  for (int part = 0; part < 4; ++part) {
+    for (int part = 0; part < 4; ++part) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int tm = part * 2 + t;
-      const int rloc = t * 16 + (lane & 15);
+      for (int t = 0; t < 2; ++t) {
+        const int tm = part * 2 + t;
+        const int rloc = t * 16 + (lane_e & 15);
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        const v4f v = acc[tm][tn];
-        uint8_t* dst = stage_w + rloc * pitch + (tn * 16 + (lane >> 4) * 4) * (out_f32 ? 4 : 2);
-        if (out_f32) {
-          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-          *reinterpret_cast<uint2*>(dst) =
-              make_uint2((uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16),
-                         (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
+        for (int tn = 0; tn < 4; ++tn) {
+          const v4f v = acc[tm][tn];
+          uint8_t* dst = stage_w + rloc * pitch + (tn * 16 + (lane_e >> 4) * 4) * esz;
+          if constexpr (OUT_F32) {
+            *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            const v2bf p0 = {(__bf16)v[0], (__bf16)v[1]}, p1 = {(__bf16)v[2], (__bf16)v[3]};
+            *reinterpret_cast<uint2*>(dst) =
+                make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
+          }
         }
       }
-    }
-    __syncthreads();
-    const int cpr = out_f32 ? 16 : 8;
-    const int esz = out_f32 ? 4 : 2;
-    const int epc = 16 / esz;
-    for (int j = 0; j < cpr / 2; ++j) {
-      const int q = lane + 64 * j;
-      const int row = q / cpr, c = q % cpr;
-      const int64_t m = m0 + wm * 128 + part * F_EPI_ROWS + row;
-      const int64_t n = n0 + wn * 64 + c * epc;
-      if (m >= g.M || n >= g.N) continue;
-      const uint8_t* src = stage_w + row * pitch + c * 16;
-      uint8_t* ydst = reinterpret_cast<uint8_t*>(g.y) + (m * g.ldy + n) * esz;
-      if (g.vec_out && n + epc <= g.N) {
-        *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
-      } else {
-        for (int e = 0; e < epc && n + e < g.N; ++e)
-          for (int bi = 0; bi < esz; ++bi) ydst[e * esz + bi] = src[e * esz + bi];
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's slice is written
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < cpr / 2; ++j) {
+        const int q = lane_e + 64 * j;
+        const int row = q / cpr, c = q % cpr;
+        const int64_t m = m0e + wm * 128 + part * F_EPI_ROWS + row;
+        const int64_t n = n0e + wn * 64 + c * epc;
+        const uint8_t* src = stage_w + row * pitch + c * 16;
+        uint8_t* ydst = reinterpret_cast<uint8_t*>(e_y) + (m * e_ldy + n) * esz;
+        if constexpr (FULL) {
+          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+          continue;
+        }
+        if (m >= e_M || n >= e_N) continue;
+        if (e_vec && n + epc <= e_N) {
+          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+        } else {
+          using E = std::conditional_t<esz == 4, uint32_t, uint16_t>;
+#pragma nounroll
+          for (int e = 0; e < epc && n + e < e_N; ++e)
+            reinterpret_cast<E*>(ydst)[e] = reinterpret_cast<const E*>(src)[e];
+        }
       }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the re-reads are done before the next part overwrites
+      __builtin_amdgcn_wave_barrier();
     }
-    __syncthreads();
+  };
+  const bool full = e_vec && m0e + FBM <= e_M && n0e + FBN <= e_N;
+  if (e_f32) {
+    if (full)
+      store_tile(std::true_type(), std::true_type());
+    else
+      store_tile(std::true_type(), std::false_type());
+  } else {
+    if (full)
+      store_tile(std::false_type(), std::true_type());
+    else
+      store_tile(std::false_type(), std::false_type());
   }
 }
 
