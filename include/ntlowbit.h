@@ -356,6 +356,69 @@ int ntlb_gemm_mxfp4(const void* x, int64_t ldx, const uint8_t* w_packed, const u
 int ntlb_gemm_fp8p(const void* x, int64_t ldx, const uint8_t* w_codes, const float* w_scales, int64_t block,
                    int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
 
+/*
+ * Expert-parallel dispatch wire format: one fixed-size record per routed
+ * (token, slot) assignment, so that a single byte all-to-all replaces the
+ * payload and four metadata all-to-alls of _dispatch_tokens
+ * (moe.py:795-863).  Record of a row of H values:
+ *   [0, S_OFF)      codes (1x128 tiles of the comm-quant, moe.py:808-814),
+ *                   S_OFF = 128*ceil(H/128), zero codes past column H
+ *   [S_OFF, ...)    ceil(H/128) fp32 tile scales
+ *   [M_OFF, +32)    int32 token index, int32 top-k slot, int32 local expert,
+ *                   int32 NaN flag, fp32 routing weight, 3 reserved int32,
+ *                   M_OFF = S_OFF + round_up(4*ceil(H/128), 16)
+ * ntlb_ep_record_bytes(H) = M_OFF + 32 (0 for H <= 0).
+ */
+int64_t ntlb_ep_record_bytes(int64_t H);
+
+/*
+ * Stable counting sort of n keys into buckets: bucket(i) = key(i) / divisor,
+ * key(i) the int32 (key_dtype 0) or int64 (1) at keys + i*key_stride bytes.
+ * pos[i] is i's place in bucket order (earlier keys first within a bucket),
+ * inv[pos[i]] = i; counts[b] (int64) and offsets[b] (int32, b <= buckets,
+ * exclusive prefix) are optional.  Sender: keys = topk_idx flattened,
+ * divisor = experts_per_rank, buckets = ep_size gives the destination order
+ * of _build_send_partitions (moe.py:670-717).  Receiver: keys = the records'
+ * local-expert field (key_stride = record bytes), divisor 1, buckets = local
+ * experts gives the grouping of _run_local_experts (moe.py:905-923) without
+ * capacity drop.  ws: int32 workspace of ceil(n/256)*buckets elements.
+ * buckets <= 4096.
+ */
+int ntlb_ep_partition(const void* keys, int key_dtype, int64_t key_stride, int64_t n, int64_t divisor, int buckets,
+                      int32_t* pos, int32_t* inv, int64_t* counts, int32_t* offsets, int32_t* ws, int64_t ws_elems,
+                      void* stream);
+
+/*
+ * Write the T*K send records: record p holds assignment a = inv[p] (inv from
+ * ntlb_ep_partition on topk_idx): token row a / K of tokens [T, H] (row
+ * stride ldt) quantized per 1x128 tile with the quantizer arguments of
+ * ntlb_quant_tile_1x128 (the SR element index is p*H + column, the row-major
+ * index in the send buffer), slot a % K, local expert topk_idx[a] %
+ * experts_per_rank, weight topk_w[a] (w_dtype) and the NaN flag.  topk_idx
+ * int32 (idx_dtype 0) or int64 (1), [T, K] contiguous.  tokens bf16 or fp32,
+ * H % 8 == 0, 16-byte aligned rows and records.
+ */
+int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt, const int32_t* inv,
+                         const void* topk_idx, int idx_dtype, const void* topk_w, int w_dtype, int64_t K,
+                         int64_t experts_per_rank, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                         uint64_t offset, uint8_t* records, void* stream);
+
+/*
+ * Receiver side: output row i is record inv[i] of the n received records
+ * (inv from ntlb_ep_partition on their local-expert field, or any order the
+ * caller chooses, e.g. after a capacity drop): codes (128*ceil(H/128)
+ * bytes with their zero padding, ldc at least that) to codes + i*ldc,
+ * scales to scales[i*s_row + t*s_col], and the optional NaN flag, token
+ * index, slot, routing weight and source rank (the s with recv_offsets[s] <=
+ * inv[i] < recv_offsets[s+1], int64 [ep_size + 1]) -- the tensors of
+ * _DispatchedTokens (moe.py:49-58) in expert order, with the payload kept as
+ * codes for the grouped GEMM.
+ */
+int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv,
+                           const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc, float* scales,
+                           int64_t s_row, int64_t s_col, int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,
+                           int32_t* src_rank, float* weight, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

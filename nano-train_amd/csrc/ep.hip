@@ -1,0 +1,215 @@
+// Expert-parallel dispatch wire format: the one-GPU share of the MoE payload
+// exchange of moe.py:670-863 (_build_send_partitions, _dispatch_tokens) and
+// of the receive-side grouping of _run_local_experts (moe.py:888-923).
+//
+// The reference sends five tensors per direction (comm-quantized tokens
+// dequantized to bf16, token index, slot index, local expert index, routing
+// weight), each with its own all-to-all after a count exchange.  Here every
+// routed (token, slot) assignment is one fixed-size record, so one byte
+// all-to-all carries everything:
+//
+//   bytes [0, S_OFF)         e4m3 / int-grid codes of the token row (1x128 tiles;
+//                            the columns past H hold zero codes)
+//   bytes [S_OFF, +4*ceil(H/128))  the row's fp32 tile scales
+//   bytes [M_OFF, +32)       int32 token index, int32 top-k slot, int32 local
+//                            expert, int32 NaN flag, fp32 routing weight, 3
+//                            reserved words (zero)
+//
+// with S_OFF = 128*ceil(H/128) (whole tiles, the GEMM's padded K), M_OFF =
+// S_OFF + round_up(4*ceil(H/128), 16) and the record size M_OFF + 32
+// (ntlb_ep_record_bytes).
+//
+// Sender: ntlb_ep_partition orders the T*K assignments by destination rank
+// (expert / experts_per_rank), stable in assignment order as the reference's
+// boolean masks are; ntlb_ep_pack_records (quant.hip) writes the records in
+// that order.  Receiver: ntlb_ep_partition on the records' local-expert field
+// groups them by local expert, stable in arrival order as the reference's
+// per-expert nonzero() is; ntlb_ep_unpack_records gathers codes, scales and
+// metadata in that order for the grouped GEMM.
+#include <hip/hip_runtime.h>
+
+#include "ntlb_device.h"
+#include "ntlb_host.h"
+
+namespace ntlb {
+
+constexpr int EP_BLOCK = 256;  // keys per partition block
+constexpr int EP_MAX_BUCKETS = 4096;
+
+__device__ __forceinline__ int64_t ep_key(const uint8_t* keys, int key_dt, int64_t stride, int64_t i) {
+  const uint8_t* p = keys + i * stride;
+  return key_dt == 1 ? *reinterpret_cast<const int64_t*>(p) : (int64_t) * reinterpret_cast<const int32_t*>(p);
+}
+
+// bucket of key i: key / divisor, clamped into [0, buckets) so that a bad key
+// can never index out of bounds (such input has no meaning to preserve)
+__device__ __forceinline__ int ep_bucket(const uint8_t* keys, int key_dt, int64_t stride, int64_t i, int64_t divisor,
+                                         int buckets) {
+  int64_t b = ep_key(keys, key_dt, stride, i) / divisor;
+  b = b < 0 ? 0 : (b >= buckets ? buckets - 1 : b);
+  return (int)b;
+}
+
+// pass 1: histogram of each block of EP_BLOCK keys, hist[block][bucket]
+__global__ void __launch_bounds__(EP_BLOCK) ep_hist_kernel(const uint8_t* keys, int key_dt, int64_t stride, int64_t n,
+                                                           int64_t divisor, int buckets, int32_t* hist) {
+  extern __shared__ int32_t h[];
+  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK) h[d] = 0;
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * EP_BLOCK + threadIdx.x;
+  if (i < n) atomicAdd(&h[ep_bucket(keys, key_dt, stride, i, divisor, buckets)], 1);
+  __syncthreads();
+  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK) hist[(int64_t)blockIdx.x * buckets + d] = h[d];
+}
+
+// pass 2 (one workgroup): hist becomes each block's first position per
+// bucket; counts[d] and offsets[d] (exclusive scan, offsets[buckets] = n)
+__global__ void __launch_bounds__(EP_BLOCK) ep_scan_kernel(int32_t* hist, int64_t nb, int buckets, int64_t* counts,
+                                                           int32_t* offsets) {
+  __shared__ int32_t base[EP_MAX_BUCKETS + 1];
+  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK) {
+    int32_t run = 0;
+    for (int64_t b = 0; b < nb; ++b) {
+      const int32_t c = hist[b * buckets + d];
+      hist[b * buckets + d] = run;  // position of the block's first key within bucket d
+      run += c;
+    }
+    base[d] = run;  // bucket total for now
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t acc = 0;
+    for (int d = 0; d < buckets; ++d) {
+      const int32_t c = base[d];
+      if (counts) counts[d] = c;
+      base[d] = acc;
+      acc += c;
+    }
+    base[buckets] = acc;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d <= buckets; d += EP_BLOCK)
+    if (offsets) offsets[d] = base[d];
+  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK)
+    for (int64_t b = 0; b < nb; ++b) hist[b * buckets + d] += base[d];
+}
+
+// pass 3: pos[i] = first position of (block, bucket) + number of earlier keys
+// of the block in the same bucket (stable); inv[pos[i]] = i
+__global__ void __launch_bounds__(EP_BLOCK) ep_place_kernel(const uint8_t* keys, int key_dt, int64_t stride,
+                                                            int64_t n, int64_t divisor, int buckets,
+                                                            const int32_t* start, int32_t* pos, int32_t* inv) {
+  __shared__ int32_t kb[EP_BLOCK];
+  const int64_t i = (int64_t)blockIdx.x * EP_BLOCK + threadIdx.x;
+  const int b = i < n ? ep_bucket(keys, key_dt, stride, i, divisor, buckets) : -1;
+  kb[threadIdx.x] = b;
+  __syncthreads();
+  if (i >= n) return;
+  int rank = 0;
+  for (int j = 0; j < (int)threadIdx.x; ++j) rank += kb[j] == b ? 1 : 0;
+  const int32_t p = start[(int64_t)blockIdx.x * buckets + b] + rank;
+  if (pos) pos[i] = p;
+  if (inv) inv[p] = (int32_t)i;
+}
+
+// receiver gather: output row i is record inv[i]; codes, scales (at
+// scales[i*s_row + t*s_col]), NaN flag and metadata, and the source rank of
+// the record (recv_offsets: [ep_size + 1] prefix of the received counts)
+template <bool VEC>
+__global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* rec, int64_t n, int64_t H, int64_t R,
+                                                        int64_t s_off, int64_t m_off, const int32_t* inv,
+                                                        const int64_t* recv_offsets, int ep_size, uint8_t* codes,
+                                                        int64_t ldc, float* scales, int64_t s_row, int64_t s_col,
+                                                        int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,
+                                                        int32_t* src_rank, float* weight) {
+  const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // four rows per workgroup, a wave each
+  const int lane = threadIdx.x & 63;
+  if (i >= n) return;
+  const int64_t src = min<int64_t>(max<int32_t>(inv[i], 0), n - 1);
+  const uint8_t* r = rec + src * R;
+  if constexpr (VEC) {
+    for (int64_t c = (int64_t)lane * 16; c < H; c += 64 * 16)
+      *reinterpret_cast<uint4*>(codes + i * ldc + c) = *reinterpret_cast<const uint4*>(r + c);
+  } else {
+    for (int64_t c = lane; c < H; c += 64) codes[i * ldc + c] = r[c];
+  }
+  const int64_t nt = (H + 127) >> 7;
+  const float* sc = reinterpret_cast<const float*>(r + s_off);
+  for (int64_t t = lane; t < nt; t += 64) scales[i * s_row + t * s_col] = sc[t];
+  if (lane == 0) {
+    const int32_t* m = reinterpret_cast<const int32_t*>(r + m_off);
+    if (token_idx) token_idx[i] = m[0];
+    if (slot_idx) slot_idx[i] = m[1];
+    if (nan_rows) nan_rows[i] = m[3];
+    if (weight) weight[i] = __int_as_float(m[4]);
+    if (src_rank) {
+      int s = 0;
+      while (s + 1 < ep_size && recv_offsets[s + 1] <= src) ++s;
+      src_rank[i] = s;
+    }
+  }
+}
+
+}  // namespace ntlb
+
+using namespace ntlb;
+
+extern "C" int64_t ntlb_ep_record_bytes(int64_t H) {
+  if (H <= 0) return 0;
+  const int64_t s_off = (H + 127) / 128 * 128;
+  const int64_t m_off = s_off + ((H + 127) / 128 * 4 + 15) / 16 * 16;
+  return m_off + 32;
+}
+
+extern "C" int ntlb_ep_partition(const void* keys, int key_dtype, int64_t key_stride, int64_t n, int64_t divisor,
+                                 int buckets, int32_t* pos, int32_t* inv, int64_t* counts, int32_t* offsets,
+                                 int32_t* ws, int64_t ws_elems, void* stream) {
+  const char* fn = "ntlb_ep_partition";
+  if (n < 0 || n > 0x7FFFFFFF || divisor < 1 || buckets < 1 || buckets > EP_MAX_BUCKETS)
+    return fail(NTLB_EINVAL, "%s: need 0 <= n < 2^31, divisor >= 1 and 1 <= buckets <= %d", fn, EP_MAX_BUCKETS);
+  if (key_dtype != 0 && key_dtype != 1) return fail(NTLB_EINVAL, "%s: key_dtype is 0 (int32) or 1 (int64)", fn);
+  const int64_t ksz = key_dtype ? 8 : 4;
+  if (key_stride < ksz || key_stride % ksz) return fail(NTLB_EINVAL, "%s: key_stride must be a multiple of the key size", fn);
+  if (n > 0 && (!keys || !aligned(keys, ksz))) return fail(NTLB_EINVAL, "%s: keys NULL or misaligned", fn);
+  const int64_t nb = cdiv(n, EP_BLOCK);
+  if (n > 0 && (!ws || ws_elems < nb * buckets)) return fail(NTLB_EINVAL, "%s: workspace needs %lld int32", fn,
+                                                             (long long)(nb * buckets));
+  hipStream_t st = as_stream(stream);
+  const uint8_t* k = reinterpret_cast<const uint8_t*>(keys);
+  if (n > 0)
+    ep_hist_kernel<<<(unsigned)nb, EP_BLOCK, buckets * sizeof(int32_t), st>>>(k, key_dtype, key_stride, n, divisor,
+                                                                             buckets, ws);
+  ep_scan_kernel<<<1, EP_BLOCK, 0, st>>>(ws, nb, buckets, counts, offsets);
+  if (n > 0)
+    ep_place_kernel<<<(unsigned)nb, EP_BLOCK, 0, st>>>(k, key_dtype, key_stride, n, divisor, buckets, ws, pos, inv);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv,
+                                      const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc,
+                                      float* scales, int64_t s_row, int64_t s_col, int32_t* nan_rows,
+                                      int32_t* token_idx, int32_t* slot_idx, int32_t* src_rank, float* weight,
+                                      void* stream) {
+  const char* fn = "ntlb_ep_unpack_records";
+  const int64_t Hp = (H + 127) / 128 * 128;  // codes with their zero padding
+  if (n < 0 || H <= 0 || ldc < Hp || ep_size < 1) return fail(NTLB_EINVAL, "%s: bad shape (ldc >= 128*ceil(H/128))", fn);
+  if (n == 0) return NTLB_OK;
+  if (!records || !inv || !codes || !scales || (src_rank && !recv_offsets))
+    return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (!aligned(records, 16)) return fail(NTLB_EINVAL, "%s: records must be 16-byte aligned", fn);
+  const int64_t R = ntlb_ep_record_bytes(H);
+  const int64_t s_off = Hp;
+  const int64_t m_off = R - 32;
+  const bool vec = aligned(codes, 16) && ldc % 16 == 0;
+  dim3 grd((unsigned)cdiv(n, 4)), blk(256);
+  hipStream_t st = as_stream(stream);
+  if (vec)
+    ep_gather_kernel<true><<<grd, blk, 0, st>>>(records, n, Hp, R, s_off, m_off, inv, recv_offsets, ep_size, codes,
+                                                 ldc, scales, s_row, s_col, nan_rows, token_idx, slot_idx, src_rank,
+                                                 weight);
+  else
+    ep_gather_kernel<false><<<grd, blk, 0, st>>>(records, n, Hp, R, s_off, m_off, inv, recv_offsets, ep_size, codes,
+                                                  ldc, scales, s_row, s_col, nan_rows, token_idx, slot_idx, src_rank,
+                                                  weight);
+  return check_launch(fn);
+}

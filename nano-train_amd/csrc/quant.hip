@@ -37,6 +37,12 @@ struct QuantArgs {
   int dq_dtype;
   int64_t lddq;
   int32_t* nan_rows;
+  // fast 1x128 path only: output row r quantizes input row row_map[r] /
+  // row_div (clamped below rows_in; the expert-parallel send records), and its
+  // NaN flag is nan_rows[r * nan_stride]
+  const int32_t* row_map;
+  int64_t row_div, rows_in;
+  int64_t nan_stride;
 };
 
 // Load 8 consecutive elements [k0, k0+8) of a row as fp32, zero past K.
@@ -216,7 +222,8 @@ __device__ __forceinline__ void tile_loads(Chunk8<IN_DT> (&c)[TILE_TU], const Qu
 #pragma unroll
   for (int u = 0; u < TILE_TU; ++u) {
     const int64_t k0 = (int64_t)(t0 + u) * 128 + lane16 * 8;
-    chunk_load<IN_DT>(c[u], a.x, r * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
+    const int64_t src = (a.row_map && r < a.R) ? min<int64_t>(max<int32_t>(a.row_map[r], 0) / a.row_div, a.rows_in - 1) : r;
+    chunk_load<IN_DT>(c[u], a.x, src * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
   }
 }
 
@@ -237,7 +244,7 @@ __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], co
     uint32_t lo, hi;
     float q[8];
     const bool nan = quant8_tile<GRID, SR, DQ>(v, m, s, a.qmaxf, rb, lo, hi, q);
-    if (nan && a.nan_rows && lane16 == 0) atomicOr(a.nan_rows + r, 1);
+    if (nan && a.nan_rows && lane16 == 0) atomicOr(a.nan_rows + r * a.nan_stride, 1);
     *reinterpret_cast<uint2*>(a.codes + r * a.ldc + k0) = make_uint2(lo, hi);
     if (lane16 == 0) a.scales[r * a.s_row + (int64_t)t * a.s_col] = s;
     if constexpr (DQ) store_dq8(a.dq, a.dq_dtype, r * a.lddq, k0, a.K, q, s);
@@ -973,6 +980,10 @@ static QuantArgs make_args(const void* x, int64_t R, int64_t K, int64_t ldx, int
   a.dq_dtype = dq_dtype;
   a.lddq = lddq;
   a.nan_rows = nan_rows;
+  a.row_map = nullptr;
+  a.row_div = 1;
+  a.rows_in = R;
+  a.nan_stride = 1;
   return a;
 }
 
@@ -1257,5 +1268,71 @@ extern "C" int ntlb_dequant(int grid, const uint8_t* codes, int64_t ldc, const f
   else
     dequant_kernel<GRID_INT><<<grd, blk, 0, st>>>(codes, ldc, scales, s_row, s_col, r_shift, c_shift, R, K, out,
                                                   out_dtype, ldo);
+  return check_launch(fn);
+}
+
+// Expert-parallel send records (the record layout is described in ep.hip):
+// metadata of record p from assignment a = inv[p] (token a / K, slot a % K,
+// local expert topk_idx[a] % experts_per_rank, routing weight topk_w[a]),
+// with the NaN flag cleared for the quantizer to set.
+__global__ void __launch_bounds__(256) ep_meta_kernel(uint8_t* rec, int64_t R, int64_t m_off, int64_t A,
+                                                      const int32_t* inv, const void* topk_idx, int idx_dt,
+                                                      const void* topk_w, int w_dt, int64_t K, int64_t epr) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= A) return;
+  const int64_t a = min<int64_t>(max<int32_t>(inv[p], 0), A - 1);
+  const int64_t e = idx_dt == 1 ? reinterpret_cast<const int64_t*>(topk_idx)[a]
+                                : (int64_t) reinterpret_cast<const int32_t*>(topk_idx)[a];
+  const float w = load_elem(topk_w, w_dt, a);
+  int32_t* m = reinterpret_cast<int32_t*>(rec + p * R + m_off);
+  *reinterpret_cast<int4*>(m) = make_int4((int32_t)(a / K), (int32_t)(a % K), (int32_t)(e % epr), 0);
+  *reinterpret_cast<int4*>(m + 4) = make_int4(__float_as_int(w), 0, 0, 0);
+}
+
+extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
+                                    const int32_t* inv, const void* topk_idx, int idx_dtype, const void* topk_w,
+                                    int w_dtype, int64_t K, int64_t experts_per_rank, int grid, int qmax,
+                                    int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
+                                    void* stream) {
+  const char* fn = "ntlb_ep_pack_records";
+  if (K < 1 || experts_per_rank < 1 || T < 0 || (idx_dtype != 0 && idx_dtype != 1) || !valid_dtype(w_dtype))
+    return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  const int64_t A = T * K;
+  if (A > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
+  int rc = check_common(fn, tokens, x_dtype, A, H, ldt, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (A == 0 || H == 0) return NTLB_OK;
+  if (!inv || !topk_idx || !topk_w || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  const int64_t R = ntlb_ep_record_bytes(H);
+  const int64_t s_off = (H + 127) / 128 * 128, m_off = R - 32;
+  const int64_t Tt = cdiv(H, 128);
+  const bool vec = aligned(tokens, 16) && ((ldt * dtype_size(x_dtype)) % 16 == 0);
+  if (!(vec && H % 8 == 0 && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) && aligned(records, 16) &&
+        cdiv(A, 16) <= 0x7FFFFFFF && cdiv(Tt, TILE_TU) <= 65535))
+    return fail(NTLB_EUNSUPPORTED, "%s: needs bf16/fp32 tokens, H %% 8 == 0, 16-byte aligned rows and records", fn);
+  hipStream_t st = as_stream(stream);
+  ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, m_off, A, inv, topk_idx, idx_dtype, topk_w,
+                                                          w_dtype, K, experts_per_rank);
+  QuantArgs a = make_args(tokens, A, H, ldt, grid, qmax, scale_rule, seed, offset, records, R,
+                          reinterpret_cast<float*>(records + s_off), R / 4, 1, nullptr, 0, 0,
+                          reinterpret_cast<int32_t*>(records + m_off + 12));
+  a.row_map = inv;
+  a.row_div = K;
+  a.rows_in = T;
+  a.nan_stride = R / 4;
+  const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
+  const int64_t n_rb = cdiv(A, 16), n_tg = cdiv(Tt, TILE_TU);
+  int64_t gx = n_rb;
+  if (NTLB_TILE_PIPELINE) {
+    gx = cdiv(n_rb, 4);
+    if (gx * n_tg < 256 * 8) gx = std::min<int64_t>(n_rb, cdiv(256 * 8, n_tg));
+  }
+  dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)n_tg, (unsigned)gx) : dim3((unsigned)gx, (unsigned)n_tg), fblk(256);
+  NTLB_DISPATCH_GRID_SR(grid, sr, {
+    if (x_dtype == NTLB_BF16)
+      quant_tile_1x128_fast<DT_BF16, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+    else
+      quant_tile_1x128_fast<DT_F32, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+  });
   return check_launch(fn);
 }

@@ -71,10 +71,15 @@ SIGNATURES = {
     "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_fp8p": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_workspace_bytes": [_I64, _I64, _I64],
+    "ntlb_ep_record_bytes": [_I64],
+    "ntlb_ep_partition": [_P, _I32, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P],
+    "ntlb_ep_pack_records": [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P, _I32, _I64, _I64, _I32, _I32, _I32,
+                             _I32, _U64, _U64, _P, _P],
+    "ntlb_ep_unpack_records": [_P, _I64, _I64, _P, _P, _I32, _P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P],
 }
 
 # entry points that return a value instead of a status
-RESTYPES = {"ntlb_gemm_workspace_bytes": _I64}
+RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64}
 
 _lib = None
 _lock = threading.Lock()

@@ -1,0 +1,183 @@
+"""Expert-parallel dispatch wire format on the MI355X kernels.
+
+nano-train's _dispatch_tokens (src/models/moe.py:795-863) sends, per
+destination rank, the comm-quantized token rows (dequantized to bf16 before
+the exchange), then token index, slot index, local expert index and routing
+weight, each with its own all_to_all after a count exchange
+(_build_send_partitions, moe.py:670-717).  Here every routed (token, slot)
+assignment becomes one fixed-size record holding the row's 1x128 codes and
+fp32 tile scales and its metadata (layout: include/ntlowbit.h,
+ntlb_ep_record_bytes), so the exchange is one count all_to_all plus one byte
+all_to_all, and the receiver hands the codes to the grouped GEMM without a
+dequantize/re-quantize round trip.
+
+  pack_dispatch     sender: destination order + records (kernels ntlb_ep_partition,
+                    ntlb_ep_pack_records)
+  exchange          the two all_to_alls (torch.distributed; one process per GPU)
+  unpack_dispatch   receiver: rows grouped by local expert in arrival order, as
+                    _run_local_experts selects them (moe.py:905-923), as a QTensor
+                    for ops.gemm_grouped_blockscaled plus the metadata of
+                    _DispatchedTokens (moe.py:49-58)
+
+Capacity dropping (moe.py:919-923) keeps the top-capacity rows of an expert by
+routing weight; unpack_dispatch takes an explicit row order for that case.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import ops
+from ._lib import call, lib
+from .ops import QTensor, cdiv
+
+KEY_INT32, KEY_INT64 = 0, 1
+
+
+def record_layout(H: int):
+    """(record bytes, scale offset, metadata offset) of a row of H values."""
+    R = int(lib().ntlb_ep_record_bytes(H))
+    s_off = cdiv(H, 128) * 128  # whole tiles of codes, zero past H
+    return R, s_off, R - 32
+
+
+def partition(keys: torch.Tensor, *, divisor: int, buckets: int):
+    """Stable counting sort of keys // divisor into buckets.
+
+    Returns (pos, inv, counts, offsets): pos[i] = place of i in bucket order,
+    inv[pos[i]] = i, counts int64 [buckets], offsets int32 [buckets + 1]."""
+    ops._require_device(keys)
+    if keys.dtype not in (torch.int32, torch.int64):
+        raise TypeError("keys must be int32 or int64")
+    keys = keys.contiguous().reshape(-1)
+    kd = KEY_INT64 if keys.dtype == torch.int64 else KEY_INT32
+    return _partition(keys.data_ptr(), kd, keys.element_size(), keys.numel(), divisor, buckets, keys.device)
+
+
+def _partition(ptr: int, key_dtype: int, key_stride: int, n: int, divisor: int, buckets: int, dev):
+    pos = torch.empty(n, dtype=torch.int32, device=dev)
+    inv = torch.empty(n, dtype=torch.int32, device=dev)
+    counts = torch.empty(buckets, dtype=torch.int64, device=dev)
+    offsets = torch.empty(buckets + 1, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(cdiv(n, 256) * buckets, 1), dtype=torch.int32, device=dev)
+    call("ntlb_ep_partition", ptr, key_dtype, key_stride, n, divisor, buckets, pos.data_ptr(), inv.data_ptr(),
+         counts.data_ptr(), offsets.data_ptr(), ws.data_ptr(), ws.numel(), ops._stream())
+    return pos, inv, counts, offsets
+
+
+@dataclass
+class SendBuffer:
+    records: torch.Tensor  # uint8 [T*K, R], destination-major
+    counts: torch.Tensor  # int64 [ep_size] (device)
+    H: int
+
+
+def pack_dispatch(tokens: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, *, experts_per_rank: int,
+                  ep_size: int, fmt: str = "e4m3", bits: int = 8, rounding: str = "nearest", seed: int = 0,
+                  offset: int = 0, scale_rule: int = 0) -> SendBuffer:
+    """The send side of _dispatch_tokens (moe.py:795-814) as records.
+
+    Assignment a = t*K + k goes to rank topk_idx[t, k] // experts_per_rank;
+    within a rank, assignments keep their order (the reference's boolean
+    masks).  Each record carries token t's row quantized per 1x128 tile with
+    the stochastic-rounding element index p*H + column of its send position
+    p, and (t, k, local expert, weight)."""
+    ops._require_device(tokens, topk_idx, topk_w)
+    if tokens.dim() != 2 or topk_idx.shape != topk_w.shape or topk_idx.dim() != 2 \
+            or topk_idx.shape[0] != tokens.shape[0]:
+        raise ValueError("tokens [T, H], topk_idx and topk_w [T, K]")
+    T, H = tokens.shape
+    K = topk_idx.shape[1]
+    idx = topk_idx.contiguous()
+    w = topk_w.contiguous()
+    if tokens.stride(-1) != 1 or tokens.stride(0) % 8 or tokens.data_ptr() % 16:
+        tokens = tokens.contiguous()
+    _, inv, counts, _ = partition(idx, divisor=experts_per_rank, buckets=ep_size)
+    R, _, _ = record_layout(H)
+    records = torch.empty((T * K, R), dtype=torch.uint8, device=tokens.device)
+    call("ntlb_ep_pack_records", tokens.data_ptr(), ops._dtype_code(tokens.dtype), T, H, tokens.stride(0),
+         inv.data_ptr(), idx.data_ptr(), KEY_INT64 if idx.dtype == torch.int64 else KEY_INT32, w.data_ptr(),
+         ops._dtype_code(w.dtype), K, experts_per_rank, ops.grid_code(fmt), (1 << (bits - 1)) - 1,
+         ops.rounding_code(rounding), scale_rule, seed, offset, records.data_ptr(), ops._stream())
+    return SendBuffer(records, counts, H)
+
+
+def exchange(send: SendBuffer, group=None):
+    """One count all_to_all and one byte all_to_all (replacing the 1 + 1 + 4
+    collectives of moe.py:720-863).  Returns (received records, counts per
+    source rank)."""
+    import torch.distributed as dist
+
+    R = send.records.shape[1]
+    recv_counts = torch.empty_like(send.counts)
+    dist.all_to_all_single(recv_counts, send.counts, group=group)
+    sc = [int(c) for c in send.counts.tolist()]
+    rc = [int(c) for c in recv_counts.tolist()]
+    recv = torch.empty((sum(rc), R), dtype=torch.uint8, device=send.records.device)
+    dist.all_to_all_single(recv.view(-1), send.records.view(-1), output_split_sizes=[c * R for c in rc],
+                           input_split_sizes=[c * R for c in sc], group=group)
+    return recv, rc
+
+
+@dataclass
+class ExpertRows:
+    """Received rows in expert order: the operand of the grouped GEMM and the
+    per-row metadata of _DispatchedTokens."""
+
+    q: QTensor  # codes [n, ldc] + tile-major 1x128 scales, nan_rows
+    offsets: torch.Tensor  # int32 [local_experts + 1]
+    counts: torch.Tensor  # int64 [local_experts]
+    token_idx: torch.Tensor  # int32 [n]
+    slot_idx: torch.Tensor  # int32 [n]
+    src_rank: torch.Tensor  # int32 [n]
+    weight: torch.Tensor  # fp32 [n]
+    order: torch.Tensor  # int32 [n]: received record of each row
+
+
+def unpack_dispatch(records: torch.Tensor, recv_counts: Sequence[int], *, H: int, local_experts: int,
+                    fmt: str = "e4m3", order: Optional[torch.Tensor] = None) -> ExpertRows:
+    """Group the received records by local expert (stable in arrival order),
+    or in the given record order, into codes + scales for the grouped GEMM."""
+    ops._require_device(records)
+    R, _, m_off = record_layout(H)
+    if records.dim() != 2 or records.shape[1] != R or records.dtype != torch.uint8:
+        raise ValueError(f"records must be uint8 [n, {R}]")
+    n = records.shape[0]
+    if sum(int(c) for c in recv_counts) != n:
+        raise ValueError("recv_counts must add up to the number of records")
+    dev = records.device
+    records = records.contiguous()
+    if order is None:
+        # keys: each record's local-expert int32, R bytes apart
+        _, order, counts, offsets = _partition(records.data_ptr() + m_off + 8, KEY_INT32, R, n, 1, local_experts, dev)
+    else:
+        order = order.to(dtype=torch.int32).contiguous()
+        counts = offsets = None
+    rows = order.numel()
+    T = cdiv(H, 128)
+    ldc = T * 128
+    rp = cdiv(max(rows, 1), 4) * 4
+    codes = torch.empty((rows, ldc), dtype=torch.uint8, device=dev)  # whole tiles come from the records
+    scales = torch.empty((T, rp), dtype=torch.float32, device=dev)
+    nan_rows = torch.empty(rows, dtype=torch.int32, device=dev)
+    token_idx = torch.empty(rows, dtype=torch.int32, device=dev)
+    slot_idx = torch.empty(rows, dtype=torch.int32, device=dev)
+    src_rank = torch.empty(rows, dtype=torch.int32, device=dev)
+    weight = torch.empty(rows, dtype=torch.float32, device=dev)
+    recv_offsets = torch.tensor([0] + list(_cumsum(recv_counts)), dtype=torch.int64, device=dev)
+    call("ntlb_ep_unpack_records", records.data_ptr(), rows, H, order.data_ptr(), recv_offsets.data_ptr(),
+         len(recv_counts), codes.data_ptr(), ldc, scales.data_ptr(), 1, rp, nan_rows.data_ptr(),
+         token_idx.data_ptr(), slot_idx.data_ptr(), src_rank.data_ptr(), weight.data_ptr(), ops._stream())
+    q = QTensor(codes, scales, 1, rp, 0, ops.grid_code(fmt), rows, H, nan_rows)
+    return ExpertRows(q, offsets, counts, token_idx, slot_idx, src_rank, weight, order)
+
+
+def _cumsum(xs: Sequence[int]) -> List[int]:
+    out, acc = [], 0
+    for x in xs:
+        acc += int(x)
+        out.append(acc)
+    return out

@@ -323,3 +323,53 @@ def emulated_linear_forward(x2d: np.ndarray, w: np.ndarray, *, grid: int = GRID_
     if bias is not None:
         y = y + bias.astype(np.float32)[None, :]
     return y.astype(out_dtype)
+
+
+# ----------------------------------------------------------------------------
+# expert-parallel dispatch (moe.py:670-717 _build_send_partitions,
+# :795-863 _dispatch_tokens, :905-923 the receive-side expert selection)
+# ----------------------------------------------------------------------------
+
+def ep_send_order(topk_idx: np.ndarray, experts_per_rank: int, ep_size: int):
+    """Assignment indices a = t*K + k in send order: destination rank
+    expert // experts_per_rank major, assignment order within a rank (the
+    reference's boolean masks over the flattened assignments, moe.py:698-706).
+    Returns (order, counts per destination)."""
+    e = np.asarray(topk_idx).reshape(-1)
+    dest = e // experts_per_rank
+    order = np.concatenate([np.nonzero(dest == r)[0] for r in range(ep_size)]) if e.size else np.zeros(0, np.int64)
+    counts = np.array([int((dest == r).sum()) for r in range(ep_size)], dtype=np.int64)
+    return order.astype(np.int64), counts
+
+
+def ep_dispatch(topk_by_rank, weights_by_rank, experts_per_rank: int, ep_size: int):
+    """What every rank receives from _dispatch_tokens, per receiving rank r:
+    dict with src_rank, token_idx, slot_idx, local_expert, sort_weight (each
+    [N_recv]) in arrival order (sources in rank order, the split order of
+    all_to_all_single), plus src_row (the sender's assignment index)."""
+    out = []
+    sends = [ep_send_order(t, experts_per_rank, ep_size) for t in topk_by_rank]
+    for r in range(ep_size):
+        parts = {k: [] for k in ("src_rank", "token_idx", "slot_idx", "local_expert", "sort_weight", "src_row")}
+        for s, (order, counts) in enumerate(sends):
+            K = np.asarray(topk_by_rank[s]).shape[1]
+            e = np.asarray(topk_by_rank[s]).reshape(-1)
+            w = np.asarray(weights_by_rank[s], dtype=np.float32).reshape(-1)
+            start = int(counts[:r].sum())
+            sel = order[start:start + int(counts[r])]
+            parts["src_rank"].append(np.full(sel.size, s, dtype=np.int64))
+            parts["token_idx"].append(sel // K)
+            parts["slot_idx"].append(sel % K)
+            parts["local_expert"].append(e[sel] % experts_per_rank)
+            parts["sort_weight"].append(w[sel])
+            parts["src_row"].append(sel)
+        out.append({k: np.concatenate(v) for k, v in parts.items()})
+    return out
+
+
+def ep_expert_order(local_expert: np.ndarray, local_experts: int):
+    """The receive-side selection of _run_local_experts without capacity drop:
+    for each local expert in order, its received rows in arrival order
+    ((recv_local_expert_idx == e).nonzero(), moe.py:905-909)."""
+    le = np.asarray(local_expert).reshape(-1)
+    return np.concatenate([np.nonzero(le == e)[0] for e in range(local_experts)]) if le.size else np.zeros(0, np.int64)

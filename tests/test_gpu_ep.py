@@ -1,0 +1,206 @@
+"""GPU parity of the expert-parallel dispatch wire format (moe.py:670-863,
+:905-923): the stable partition against numpy's stable sort, every send record
+(codes, scales, metadata) bit-exact against the oracle quantizer applied to the
+reference's send buffer, and an exchange between emulated ranks on one GPU
+(the all_to_all replaced by slicing) against the oracle's restatement of what
+_dispatch_tokens delivers, in _run_local_experts' expert order."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _gpu_util import assert_bits_equal, rel_fro_bf16, seeded, to_np32
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _routing(T, K, experts, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.stack([torch.randperm(experts, generator=g)[:K] for _ in range(T)]) if T else \
+        torch.zeros((0, K), dtype=torch.int64)
+    w = torch.rand((T, K), generator=g)
+    return idx, w
+
+
+def _decode(records: np.ndarray, H: int):
+    """codes, scales, (token, slot, local expert, nan flag), weight of records."""
+    from lowbit import ep
+
+    R, s_off, m_off = ep.record_layout(H)
+    T = -(-H // 128)
+    rec = np.ascontiguousarray(records).reshape(-1, R)
+    codes = rec[:, :H]
+    scales = rec[:, s_off:s_off + 4 * T].copy().view(np.float32)
+    meta = rec[:, m_off:m_off + 32].copy().view(np.int32)
+    return codes, scales, meta[:, :4], meta[:, 4].copy().view(np.float32), meta[:, 5:]
+
+
+@pytest.mark.parametrize("n", [0, 1, 300, 5000, 70000])
+@pytest.mark.parametrize("dtype,divisor,buckets", [(torch.int32, 1, 7), (torch.int64, 4, 8), (torch.int64, 1, 512)])
+def test_partition_is_a_stable_sort(gpu_device, n, dtype, divisor, buckets):
+    from lowbit import ep
+
+    g = torch.Generator().manual_seed(20261201 + n)
+    keys = torch.randint(0, buckets * divisor, (n,), generator=g).to(dtype)
+    pos, inv, counts, offsets = ep.partition(keys.to(gpu_device), divisor=divisor, buckets=buckets)
+    torch.cuda.synchronize()
+    b = keys.numpy() // divisor
+    want_inv = np.argsort(b, kind="stable")
+    want_pos = np.empty(n, dtype=np.int64)
+    want_pos[want_inv] = np.arange(n)
+    want_counts = np.bincount(b, minlength=buckets)
+    # np.array_equal keeps a failure report short (no element-wise diff of long lists)
+    assert np.array_equal(inv.cpu().numpy(), want_inv), "inv"
+    assert np.array_equal(pos.cpu().numpy(), want_pos), "pos"
+    assert np.array_equal(counts.cpu().numpy(), want_counts), "counts"
+    assert np.array_equal(offsets.cpu().numpy(), np.concatenate([[0], np.cumsum(want_counts)])), "offsets"
+
+
+def test_partition_clamps_out_of_range_keys(gpu_device):
+    from lowbit import ep
+
+    keys = torch.tensor([5, -3, 100, 2, 2], dtype=torch.int32, device=gpu_device)
+    _, inv, counts, _ = ep.partition(keys, divisor=1, buckets=4)
+    torch.cuda.synchronize()
+    # -3 -> bucket 0, 5 and 100 -> bucket 3
+    assert counts.cpu().tolist() == [1, 0, 2, 2]
+    assert inv.cpu().tolist() == [1, 3, 4, 0, 2]
+
+
+@pytest.mark.parametrize("fmt,grid", [("e4m3", O.GRID_E4M3), ("int_grid", O.GRID_INT)])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+@pytest.mark.parametrize("H", [1024, 200])
+def test_pack_records_match_oracle(gpu_device, fmt, grid, rounding, H):
+    from lowbit import ep
+
+    T, K, epr, ep_size = 96, 4, 3, 4
+    x = seeded((T, H), seed=20261202, outliers=0.01).to(gpu_device)
+    x[7, 5] = float("nan")
+    idx, w = _routing(T, K, epr * ep_size, 20261203)
+    send = ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=epr, ep_size=ep_size, fmt=fmt,
+                            rounding=rounding, seed=77, offset=5)
+    torch.cuda.synchronize()
+    order, counts = O.ep_send_order(idx.numpy(), epr, ep_size)
+    assert send.counts.cpu().numpy().tolist() == counts.tolist()
+    codes, scales, meta, weight, reserved = _decode(send.records.cpu().numpy(), H)
+    # the reference's send buffer: token rows in send order (moe.py:693, :805)
+    send_rows = to_np32(x)[order // K]
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    c_ref, s_ref, _, _ = O.quant_tile_1x128(send_rows, grid=grid, rounding=rc, seed=77, offset=5)
+    assert_bits_equal(codes, c_ref[:, :H], "record codes")
+    assert_bits_equal(scales, s_ref, "record scales")
+    assert np.array_equal(meta[:, 0], order // K), "token index"
+    assert np.array_equal(meta[:, 1], order % K), "slot"
+    assert np.array_equal(meta[:, 2], idx.numpy().reshape(-1)[order] % epr), "local expert"
+    # the flag of every record of token 7, whose row holds the NaN
+    assert np.array_equal(meta[:, 3], np.isnan(send_rows).any(axis=1).astype(np.int32)), "NaN flags"
+    assert_bits_equal(weight, w.numpy().reshape(-1)[order].astype(np.float32), "record weights")
+    assert not reserved.any()
+
+
+def _emulated_exchange(ep_size, epr, H, tokens_per_rank, K, seed, device, rounding="nearest"):
+    from lowbit import ep
+
+    xs, idxs, ws, sends = [], [], [], []
+    for r, T in enumerate(tokens_per_rank):
+        x = seeded((T, H), seed=seed + 10 * r).to(device)
+        idx, w = _routing(T, K, epr * ep_size, seed + 10 * r + 1)
+        xs.append(x), idxs.append(idx), ws.append(w)
+        sends.append(ep.pack_dispatch(x, idx.to(device), w.to(device), experts_per_rank=epr, ep_size=ep_size,
+                                      rounding=rounding, seed=seed, offset=r))
+    # all_to_all_single: receiver r gets, from each source s in rank order, s's slice for r
+    recv = []
+    for r in range(ep_size):
+        parts, counts = [], []
+        for s in range(ep_size):
+            c = sends[s].counts.cpu().tolist()
+            start = sum(c[:r])
+            parts.append(sends[s].records[start:start + c[r]])
+            counts.append(c[r])
+        recv.append((torch.cat(parts), counts))
+    return xs, idxs, ws, sends, recv
+
+
+def test_exchange_between_emulated_ranks(gpu_device):
+    from lowbit import ep
+
+    ep_size, epr, H, K = 4, 3, 512, 4
+    tokens = [40, 0, 77, 13]  # one rank sends nothing
+    xs, idxs, ws, sends, recv = _emulated_exchange(ep_size, epr, H, tokens, K, 20261210, gpu_device)
+    ref = O.ep_dispatch([i.numpy() for i in idxs], [w.numpy() for w in ws], epr, ep_size)
+    for r in range(ep_size):
+        records, counts = recv[r]
+        rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr)
+        torch.cuda.synchronize()
+        want = ref[r]
+        order = O.ep_expert_order(want["local_expert"], epr)
+        assert np.array_equal(rows.order.cpu().numpy(), order), "expert order"
+        assert np.array_equal(rows.counts.cpu().numpy(), np.bincount(want["local_expert"], minlength=epr)), "counts"
+        for key, got in (("src_rank", rows.src_rank), ("token_idx", rows.token_idx), ("slot_idx", rows.slot_idx)):
+            assert np.array_equal(got.cpu().numpy(), want[key][order]), key
+        assert_bits_equal(rows.weight.cpu().numpy(), want["sort_weight"][order], "weights")
+        # payload: each row's codes and scales are those its sender quantized
+        n = len(order)
+        if n == 0:
+            continue
+        q = rows.q
+        src = want["src_rank"][order]
+        for s in np.unique(src):
+            sel = np.nonzero(src == s)[0]
+            K_s = idxs[s].shape[1]
+            srow = want["src_row"][order][sel]
+            c_ref, s_ref, _, _ = O.quant_tile_1x128(to_np32(xs[s])[srow // K_s], grid=O.GRID_E4M3)
+            assert_bits_equal(q.codes.cpu().numpy()[sel, :H], c_ref[:, :H], "payload codes")
+            got_s = q.scales.cpu().numpy()[:, sel].T
+            assert_bits_equal(np.ascontiguousarray(got_s), s_ref, "payload scales")
+
+
+def test_grouped_gemm_on_received_rows(gpu_device):
+    """The unpacked rows feed the grouped GEMM directly (no dequantize /
+    re-quantize); checked per expert against the oracle GEMM."""
+    from lowbit import ep, moe, ops
+
+    ep_size, epr, H, K, N = 2, 4, 1024, 2, 384
+    xs, idxs, ws, sends, recv = _emulated_exchange(ep_size, epr, H, [200, 150], K, 20261220, gpu_device)
+    records, counts = recv[0]
+    rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr)
+    wts = seeded((epr, N, H), seed=20261221, std=0.02).to(gpu_device)
+    b_codes, b_scales, _ = moe.quantize_expert_weights(wts)
+    y = ops.gemm_grouped_blockscaled(rows.q, b_codes, b_scales, rows.offsets, N=N)
+    torch.cuda.synchronize()
+    ref = O.ep_dispatch([i.numpy() for i in idxs], [w.numpy() for w in ws], epr, ep_size)[0]
+    order = O.ep_expert_order(ref["local_expert"], epr)
+    src, srow, le = ref["src_rank"][order], ref["src_row"][order], ref["local_expert"][order]
+    x_rows = np.stack([to_np32(xs[s])[r // K] for s, r in zip(src, srow)])
+    xdq = O.quant_tile_1x128(x_rows, grid=O.GRID_E4M3)[3]
+    out = np.zeros((len(order), N))
+    for e in range(epr):
+        sel = le == e
+        wdq = O.quant_block_128x128(to_np32(wts[e]), grid=O.GRID_E4M3)[3]
+        out[sel] = O.gemm_ref(xdq[sel], wdq)
+    assert rel_fro_bf16(y, out) <= 1e-3
+
+
+def test_c4_size_records_feed_the_expert_path(gpu_device):
+    """Config 4 (4096 tokens, hidden 7168, top-8 of 32 experts): the records
+    received for all 32 experts (one rank) unpack to exactly the codes and
+    scales the existing expert path quantizes from the expert-sorted tokens."""
+    from lowbit import ep, moe, ops, workloads
+
+    tokens, routing, _, _ = workloads.c4_inputs(device="cpu")
+    idx = routing if isinstance(routing, torch.Tensor) else routing[0]
+    x = tokens.to(gpu_device)
+    w = torch.rand(idx.shape, generator=torch.Generator().manual_seed(20261230))
+    send = ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=32, ep_size=1)
+    rows = ep.unpack_dispatch(send.records, [send.records.shape[0]], H=7168, local_experts=32)
+    order, token_index, offsets = moe.sort_by_expert(idx.to(gpu_device), 32)
+    qx = ops.quant_tile_1x128(x[token_index.long()], fmt="e4m3", tile_major_scales=True)
+    torch.cuda.synchronize()
+    assert torch.equal(rows.offsets.cpu(), offsets.cpu().to(torch.int32))
+    assert torch.equal(rows.token_idx.cpu().long(), token_index.cpu().long())
+    assert torch.equal(rows.q.codes, qx.codes)
+    M = rows.q.rows
+    assert torch.equal(rows.q.scales[:, :M], qx.scales[:, :M])

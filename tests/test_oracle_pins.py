@@ -384,3 +384,31 @@ def test_fp8_persistent_matches_torch_formula():
     s = t.abs().amax(dim=1, keepdim=True)
     ref = (t / s).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy().reshape(-1)
     assert np.array_equal(codes, ref) and np.array_equal(scales, s.numpy().reshape(-1))
+
+
+def test_ep_dispatch_oracle_hand_example():
+    """_build_send_partitions / _dispatch_tokens order on a hand-worked case:
+    2 ranks, 2 experts per rank, top-2.  Rank 0's assignments (token, slot,
+    expert): (0,0,3) (0,1,0) (1,0,1) (1,1,2) (2,0,0) (2,1,3) go to ranks
+    1 0 0 1 0 1; rank 1's: (0,0,2) (0,1,1) (1,0,0) (1,1,3) go to 1 0 0 1."""
+    top0 = np.array([[3, 0], [1, 2], [0, 3]])
+    top1 = np.array([[2, 1], [0, 3]])
+    w0 = np.array([[0.1, 0.2], [0.3, 0.4], [0.5, 0.6]], dtype=np.float32)
+    w1 = np.array([[0.7, 0.8], [0.9, 1.0]], dtype=np.float32)
+    order, counts = O.ep_send_order(top0, 2, 2)
+    assert order.tolist() == [1, 2, 4, 0, 3, 5] and counts.tolist() == [3, 3]
+    recv = O.ep_dispatch([top0, top1], [w0, w1], 2, 2)
+    r0 = recv[0]
+    assert r0["src_rank"].tolist() == [0, 0, 0, 1, 1]
+    assert r0["token_idx"].tolist() == [0, 1, 2, 0, 1]
+    assert r0["slot_idx"].tolist() == [1, 0, 0, 1, 0]
+    assert r0["local_expert"].tolist() == [0, 1, 0, 1, 0]
+    np.testing.assert_array_equal(r0["sort_weight"], np.array([0.2, 0.3, 0.5, 0.8, 0.9], dtype=np.float32))
+    r1 = recv[1]
+    assert r1["src_rank"].tolist() == [0, 0, 0, 1, 1]
+    assert r1["token_idx"].tolist() == [0, 1, 2, 0, 1]
+    assert r1["slot_idx"].tolist() == [0, 1, 1, 0, 1]
+    assert r1["local_expert"].tolist() == [1, 0, 1, 0, 1]
+    # local expert 0 first, each in arrival order
+    assert O.ep_expert_order(r0["local_expert"], 2).tolist() == [0, 2, 4, 1, 3]
+    assert O.ep_expert_order(r1["local_expert"], 2).tolist() == [1, 3, 0, 2, 4]
