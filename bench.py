@@ -150,6 +150,24 @@ def other_config(args) -> dict:
                                                          want_h=False), args.steps, args.warmup, st)
         dn_ms = _time_ms(lambda i: ops.gemm_grouped_blockscaled(qh, down[0], down[1], offsets, N=H),
                          args.steps, args.warmup, st)
+        # expert-parallel wire format, one GPU's share of an 8-rank layout (4 experts per rank):
+        # pack every (token, slot) assignment into a record, unpack as many received records
+        from lowbit import ep
+
+        topk_w = torch.rand(routing.shape, generator=torch.Generator().manual_seed(4), dtype=torch.float32).to(dev)
+        send = ep.pack_dispatch(tokens, routing, topk_w, experts_per_rank=4, ep_size=8, fmt=fmt)
+        rcounts = send.counts.cpu().tolist()
+        pack_us = _time_ms(lambda i: ep.pack_dispatch(tokens, routing, topk_w, experts_per_rank=4, ep_size=8, fmt=fmt),
+                           args.steps, args.warmup, st) * 1e3
+        unpack_us = _time_ms(lambda i: ep.unpack_dispatch(send.records, rcounts, H=H, local_experts=4, fmt=fmt),
+                             args.steps, args.warmup, st) * 1e3
+        rec_b = send.records.shape[1]
+        n_rec = send.records.shape[0]
+        # pack: one bf16 token row read and one record written per assignment;
+        # unpack: one record read, codes + tile scales + 5 words of metadata written per row
+        pack_bytes = n_rec * (H * 2 + rec_b)
+        unpack_bytes = n_rec * (rec_b + ops.cdiv(H, 128) * 128 + ops.cdiv(H, 128) * 4 + 20)
+        del send
         fl = 2.0 * R * H * inter  # one projection
         comm_bytes = R * H * 3 + R * (H // 128) * 4
         res.update(value=round(3 * fl / (mlp * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(mlp, 4),
@@ -159,7 +177,10 @@ def other_config(args) -> dict:
                            "rows": R, "hidden": H, "inter": inter, "experts": 32, "top_k": 8},
                    gate_up_swiglu_tflops=round(2 * fl / (gu_ms * 1e-3) / 1e12, 2),
                    down_tflops=round(fl / (dn_ms * 1e-3) / 1e12, 2), quant_x_us=round(qx_us, 2),
-                   comm_quant_us=round(comm_us, 2), comm_quant_GBs=round(comm_bytes / comm_us / 1e3, 1))
+                   comm_quant_us=round(comm_us, 2), comm_quant_GBs=round(comm_bytes / comm_us / 1e3, 1),
+                   ep_dispatch={"records": n_rec, "record_bytes": rec_b, "pack_us": round(pack_us, 2),
+                                "pack_GBs": round(pack_bytes / pack_us / 1e3, 1), "unpack_us": round(unpack_us, 2),
+                                "unpack_GBs": round(unpack_bytes / unpack_us / 1e3, 1)})
         return res
     # c5
     x, w = workloads.c5_inputs(device="cpu")
