@@ -163,9 +163,9 @@ def other_config(args) -> dict:
                              args.steps, args.warmup, st) * 1e3
         rec_b = send.records.shape[1]
         n_rec = send.records.shape[0]
-        # pack: one bf16 token row read and one record written per assignment;
+        # pack: every bf16 token row read once, one record written per assignment;
         # unpack: one record read, codes + tile scales + 5 words of metadata written per row
-        pack_bytes = n_rec * (H * 2 + rec_b)
+        pack_bytes = tokens.shape[0] * H * 2 + n_rec * rec_b
         unpack_bytes = n_rec * (rec_b + ops.cdiv(H, 128) * 128 + ops.cdiv(H, 128) * 4 + 20)
         del send
         fl = 2.0 * R * H * inter  # one projection

@@ -389,32 +389,37 @@ int ntlb_ep_partition(const void* keys, int key_dtype, int64_t key_stride, int64
                       void* stream);
 
 /*
- * Write the T*K send records: record p holds assignment a = inv[p] (inv from
+ * Write the T*K send records: assignment a goes to record p = pos[a] (pos from
  * ntlb_ep_partition on topk_idx): token row a / K of tokens [T, H] (row
  * stride ldt) quantized per 1x128 tile with the quantizer arguments of
  * ntlb_quant_tile_1x128 (the SR element index is p*H + column, the row-major
  * index in the send buffer), slot a % K, local expert topk_idx[a] %
- * experts_per_rank, weight topk_w[a] (w_dtype) and the NaN flag.  topk_idx
- * int32 (idx_dtype 0) or int64 (1), [T, K] contiguous.  tokens bf16 or fp32,
- * H % 8 == 0, 16-byte aligned rows and records.
+ * experts_per_rank, weight topk_w[a] (w_dtype) and the NaN flag.  Each token
+ * row is read once and written to its K records.  topk_idx int32 (idx_dtype
+ * 0) or int64 (1), [T, K] contiguous.  tokens bf16 or fp32, H % 8 == 0,
+ * 16-byte aligned rows and records.
  */
-int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt, const int32_t* inv,
+int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt, const int32_t* pos,
                          const void* topk_idx, int idx_dtype, const void* topk_w, int w_dtype, int64_t K,
                          int64_t experts_per_rank, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
                          uint64_t offset, uint8_t* records, void* stream);
 
 /*
- * Receiver side: output row i is record inv[i] of the n received records
- * (inv from ntlb_ep_partition on their local-expert field, or any order the
- * caller chooses, e.g. after a capacity drop): codes (128*ceil(H/128)
+ * Receiver side: output row i < rows is record inv[i] of the n received
+ * records (inv from ntlb_ep_partition on their local-expert field with rows =
+ * n, or any selection the caller chooses, e.g. the rows kept by a capacity
+ * drop, moe.py:919-923, with rows <= n or repeats): codes (128*ceil(H/128)
  * bytes with their zero padding, ldc at least that) to codes + i*ldc,
  * scales to scales[i*s_row + t*s_col], and the optional NaN flag, token
  * index, slot, routing weight and source rank (the s with recv_offsets[s] <=
- * inv[i] < recv_offsets[s+1], int64 [ep_size + 1]) -- the tensors of
- * _DispatchedTokens (moe.py:49-58) in expert order, with the payload kept as
- * codes for the grouped GEMM.
+ * inv[i] < recv_offsets[s+1]) -- the tensors of _DispatchedTokens
+ * (moe.py:49-58) in expert order, with the payload kept as codes for the
+ * grouped GEMM.  recv_offsets is HOST memory, int64 [ep_size + 1], the prefix
+ * of the received counts from 0 to n (as recv_src_ranks is built from the
+ * counts, moe.py:851-854), read during the call; needed only with src_rank;
+ * ep_size <= 256.  n < 2^31.
  */
-int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv,
+int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv, int64_t rows,
                            const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc, float* scales,
                            int64_t s_row, int64_t s_col, int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,
                            int32_t* src_rank, float* weight, void* stream);

@@ -35,6 +35,8 @@ namespace ntlb {
 
 constexpr int EP_BLOCK = 256;  // keys per partition block
 constexpr int EP_MAX_BUCKETS = 4096;
+constexpr int EP_SCAN_THREADS = 1024;
+constexpr int EP_MAX_RANKS = 256;
 
 __device__ __forceinline__ int64_t ep_key(const uint8_t* keys, int key_dt, int64_t stride, int64_t i) {
   const uint8_t* p = keys + i * stride;
@@ -50,7 +52,9 @@ __device__ __forceinline__ int ep_bucket(const uint8_t* keys, int key_dt, int64_
   return (int)b;
 }
 
-// pass 1: histogram of each block of EP_BLOCK keys, hist[block][bucket]
+// pass 1: histogram of each block of EP_BLOCK keys, stored bucket-major,
+// hist[bucket * nb + block], so that one exclusive scan of the whole array
+// gives every (bucket, block) its first output position
 __global__ void __launch_bounds__(EP_BLOCK) ep_hist_kernel(const uint8_t* keys, int key_dt, int64_t stride, int64_t n,
                                                            int64_t divisor, int buckets, int32_t* hist) {
   extern __shared__ int32_t h[];
@@ -59,42 +63,73 @@ __global__ void __launch_bounds__(EP_BLOCK) ep_hist_kernel(const uint8_t* keys, 
   const int64_t i = (int64_t)blockIdx.x * EP_BLOCK + threadIdx.x;
   if (i < n) atomicAdd(&h[ep_bucket(keys, key_dt, stride, i, divisor, buckets)], 1);
   __syncthreads();
-  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK) hist[(int64_t)blockIdx.x * buckets + d] = h[d];
+  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK) hist[(int64_t)d * gridDim.x + blockIdx.x] = h[d];
 }
 
-// pass 2 (one workgroup): hist becomes each block's first position per
-// bucket; counts[d] and offsets[d] (exclusive scan, offsets[buckets] = n)
-__global__ void __launch_bounds__(EP_BLOCK) ep_scan_kernel(int32_t* hist, int64_t nb, int buckets, int64_t* counts,
-                                                           int32_t* offsets) {
-  __shared__ int32_t base[EP_MAX_BUCKETS + 1];
-  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK) {
-    int32_t run = 0;
-    for (int64_t b = 0; b < nb; ++b) {
-      const int32_t c = hist[b * buckets + d];
-      hist[b * buckets + d] = run;  // position of the block's first key within bucket d
-      run += c;
-    }
-    base[d] = run;  // bucket total for now
+// exclusive scan of one value per thread over a workgroup of EP_SCAN_THREADS;
+// *total = the sum of all values
+__device__ __forceinline__ int32_t ep_block_scan(int32_t v, int32_t* wsum, int32_t* total) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  int32_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int32_t y = __shfl_up(x, d, 64);
+    x += lane >= d ? y : 0;
   }
+  if (lane == 63) wsum[w] = x;
   __syncthreads();
   if (threadIdx.x == 0) {
-    int32_t acc = 0;
-    for (int d = 0; d < buckets; ++d) {
-      const int32_t c = base[d];
-      if (counts) counts[d] = c;
-      base[d] = acc;
-      acc += c;
+    int32_t a = 0;
+    for (int k = 0; k < EP_SCAN_THREADS / 64; ++k) {
+      const int32_t c = wsum[k];
+      wsum[k] = a;
+      a += c;
     }
-    base[buckets] = acc;
+    wsum[EP_SCAN_THREADS / 64] = a;
   }
   __syncthreads();
-  for (int d = threadIdx.x; d <= buckets; d += EP_BLOCK)
-    if (offsets) offsets[d] = base[d];
-  for (int d = threadIdx.x; d < buckets; d += EP_BLOCK)
-    for (int64_t b = 0; b < nb; ++b) hist[b * buckets + d] += base[d];
+  *total = wsum[EP_SCAN_THREADS / 64];
+  return wsum[w] + x - v;
 }
 
-// pass 3: pos[i] = first position of (block, bucket) + number of earlier keys
+// pass 2 (one workgroup): the bucket-major histogram becomes each (bucket,
+// block)'s first output position; counts[d] and offsets[d] (exclusive scan,
+// offsets[buckets] = n).  Each thread owns a contiguous segment: sum, scan of
+// the sums, then the segment rewritten with its running prefix.
+__global__ void __launch_bounds__(EP_SCAN_THREADS) ep_scan_kernel(int32_t* hist, int64_t nb, int buckets,
+                                                                  int64_t* counts, int32_t* offsets) {
+  __shared__ int32_t base[EP_MAX_BUCKETS + 1];
+  __shared__ int32_t wsum[EP_SCAN_THREADS / 64 + 1];
+  for (int d = threadIdx.x; d <= buckets; d += EP_SCAN_THREADS) base[d] = 0;  // n == 0: every offset is 0
+  const int64_t L = nb * buckets;
+  const int64_t seg = (L + EP_SCAN_THREADS - 1) / EP_SCAN_THREADS;
+  const int64_t lo = min<int64_t>(L, (int64_t)threadIdx.x * seg), hi = min<int64_t>(L, lo + seg);
+  int32_t s = 0;
+  for (int64_t j = lo; j < hi; ++j) s += hist[j];
+  int32_t total;
+  int32_t run = ep_block_scan(s, wsum, &total);  // its barriers also order the base[] clears above
+  if (nb > 0) {
+    int64_t d = (lo + nb - 1) / nb, next = d * nb;  // first bucket starting at or after lo
+    for (int64_t j = lo; j < hi; ++j) {
+      if (j == next) {
+        base[d] = run;  // bucket d starts with block 0
+        ++d;
+        next += nb;
+      }
+      const int32_t c = hist[j];
+      hist[j] = run;
+      run += c;
+    }
+  }
+  if (threadIdx.x == 0) base[buckets] = total;
+  __syncthreads();
+  for (int d = threadIdx.x; d <= buckets; d += EP_SCAN_THREADS) {
+    if (offsets) offsets[d] = base[d];
+    if (counts && d < buckets) counts[d] = base[d + 1] - base[d];
+  }
+}
+
+// pass 3: pos[i] = first position of (bucket, block) + number of earlier keys
 // of the block in the same bucket (stable); inv[pos[i]] = i
 __global__ void __launch_bounds__(EP_BLOCK) ep_place_kernel(const uint8_t* keys, int key_dt, int64_t stride,
                                                             int64_t n, int64_t divisor, int buckets,
@@ -107,46 +142,82 @@ __global__ void __launch_bounds__(EP_BLOCK) ep_place_kernel(const uint8_t* keys,
   if (i >= n) return;
   int rank = 0;
   for (int j = 0; j < (int)threadIdx.x; ++j) rank += kb[j] == b ? 1 : 0;
-  const int32_t p = start[(int64_t)blockIdx.x * buckets + b] + rank;
+  const int32_t p = start[(int64_t)b * gridDim.x + blockIdx.x] + rank;
   if (pos) pos[i] = p;
   if (inv) inv[p] = (int32_t)i;
 }
 
-// receiver gather: output row i is record inv[i]; codes, scales (at
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// prefix of the received counts per source rank, passed by value
+struct RankOffsets {
+  int32_t v[EP_MAX_RANKS + 1];
+};
+
+// receiver gather: output row i < rows is record inv[i] of the n records; codes, scales (at
 // scales[i*s_row + t*s_col]), NaN flag and metadata, and the source rank of
-// the record (recv_offsets: [ep_size + 1] prefix of the received counts)
+// the record (the s with ro.v[s] <= inv[i] < ro.v[s+1]).  A wave per row; the
+// vector path issues up to eight 16-byte loads per lane before their stores.
 template <bool VEC>
-__global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* rec, int64_t n, int64_t H, int64_t R,
-                                                        int64_t s_off, int64_t m_off, const int32_t* inv,
-                                                        const int64_t* recv_offsets, int ep_size, uint8_t* codes,
-                                                        int64_t ldc, float* scales, int64_t s_row, int64_t s_col,
+__global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* __restrict__ rec, int64_t n, int64_t rows,
+                                                        int64_t Hp,
+                                                        int64_t R, int64_t s_off, int64_t m_off,
+                                                        const int32_t* __restrict__ inv, RankOffsets ro, int ep_size,
+                                                        uint8_t* __restrict__ codes, int64_t ldc,
+                                                        float* __restrict__ scales, int64_t s_row, int64_t s_col,
                                                         int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,
                                                         int32_t* src_rank, float* weight) {
   const int64_t i = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // four rows per workgroup, a wave each
   const int lane = threadIdx.x & 63;
-  if (i >= n) return;
-  const int64_t src = min<int64_t>(max<int32_t>(inv[i], 0), n - 1);
+  if (i >= rows) return;
+  const int64_t src = min<int64_t>(max<int32_t>(inv[i], 0), n - 1);  // a record index, clamped into the n records
   const uint8_t* r = rec + src * R;
-  if constexpr (VEC) {
-    for (int64_t c = (int64_t)lane * 16; c < H; c += 64 * 16)
-      *reinterpret_cast<uint4*>(codes + i * ldc + c) = *reinterpret_cast<const uint4*>(r + c);
-  } else {
-    for (int64_t c = lane; c < H; c += 64) codes[i * ldc + c] = r[c];
-  }
-  const int64_t nt = (H + 127) >> 7;
+  uint8_t* out = codes + i * ldc;
+  const int64_t nt = Hp >> 7;
   const float* sc = reinterpret_cast<const float*>(r + s_off);
-  for (int64_t t = lane; t < nt; t += 64) scales[i * s_row + t * s_col] = sc[t];
-  if (lane == 0) {
-    const int32_t* m = reinterpret_cast<const int32_t*>(r + m_off);
-    if (token_idx) token_idx[i] = m[0];
-    if (slot_idx) slot_idx[i] = m[1];
-    if (nan_rows) nan_rows[i] = m[3];
-    if (weight) weight[i] = __int_as_float(m[4]);
-    if (src_rank) {
-      int s = 0;
-      while (s + 1 < ep_size && recv_offsets[s + 1] <= src) ++s;
-      src_rank[i] = s;
+  const int32_t* m = reinterpret_cast<const int32_t*>(r + m_off);
+  // lane l < nt takes tile scale l, lanes 0-4 the metadata words (token, slot,
+  // local expert, NaN flag, weight); both loads clamped into the record
+  float s_l = sc[min<int64_t>(lane, nt - 1)];
+  int32_t m_l = m[min(lane, 7)];
+  if constexpr (VEC) {
+    constexpr int U = 8;
+    for (int64_t c0 = 0; c0 < Hp; c0 += 64 * 16 * U) {
+      // offsets clamped into the row (Hp >= 128): a lane past the end loads and
+      // stores the row's last 16 bytes again, the same bytes to the same place,
+      // which keeps the eight loads unconditional and ahead of the stores
+      u32x4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = min<int64_t>(c0 + (int64_t)(u * 64 + lane) * 16, Hp - 16);
+        v[u] = *reinterpret_cast<const u32x4*>(r + c);
+      }
+      // the loads all complete here, before the first store (left alone, the
+      // scheduler pairs each load with its store and waits on each)
+      asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]),
+                   "+v"(v[7]), "+v"(s_l), "+v"(m_l));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t c = min<int64_t>(c0 + (int64_t)(u * 64 + lane) * 16, Hp - 16);
+        *reinterpret_cast<u32x4*>(out + c) = v[u];
+      }
     }
+  } else {
+    for (int64_t c = lane; c < Hp; c += 64) out[c] = r[c];
+  }
+  if (lane < nt) scales[i * s_row + lane * s_col] = s_l;
+  for (int64_t t = 64 + lane; t < nt; t += 64) scales[i * s_row + t * s_col] = sc[t];
+  if (lane == 0 && token_idx) token_idx[i] = m_l;
+  if (lane == 1 && slot_idx) slot_idx[i] = m_l;
+  if (lane == 3 && nan_rows) nan_rows[i] = m_l;
+  if (lane == 4 && weight) weight[i] = __int_as_float(m_l);
+  if (lane == 5 && src_rank) {
+    int lo = 0, hi = ep_size - 1;  // the last s with ro.v[s] <= src
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (ro.v[mid] <= src) lo = mid; else hi = mid - 1;
+    }
+    src_rank[i] = lo;
   }
 }
 
@@ -179,37 +250,48 @@ extern "C" int ntlb_ep_partition(const void* keys, int key_dtype, int64_t key_st
   if (n > 0)
     ep_hist_kernel<<<(unsigned)nb, EP_BLOCK, buckets * sizeof(int32_t), st>>>(k, key_dtype, key_stride, n, divisor,
                                                                              buckets, ws);
-  ep_scan_kernel<<<1, EP_BLOCK, 0, st>>>(ws, nb, buckets, counts, offsets);
+  ep_scan_kernel<<<1, EP_SCAN_THREADS, 0, st>>>(ws, nb, buckets, counts, offsets);
   if (n > 0)
     ep_place_kernel<<<(unsigned)nb, EP_BLOCK, 0, st>>>(k, key_dtype, key_stride, n, divisor, buckets, ws, pos, inv);
   return check_launch(fn);
 }
 
-extern "C" int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv,
+extern "C" int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv, int64_t rows,
                                       const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc,
                                       float* scales, int64_t s_row, int64_t s_col, int32_t* nan_rows,
                                       int32_t* token_idx, int32_t* slot_idx, int32_t* src_rank, float* weight,
                                       void* stream) {
   const char* fn = "ntlb_ep_unpack_records";
   const int64_t Hp = (H + 127) / 128 * 128;  // codes with their zero padding
-  if (n < 0 || H <= 0 || ldc < Hp || ep_size < 1) return fail(NTLB_EINVAL, "%s: bad shape (ldc >= 128*ceil(H/128))", fn);
-  if (n == 0) return NTLB_OK;
-  if (!records || !inv || !codes || !scales || (src_rank && !recv_offsets))
-    return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (n < 0 || n > 0x7FFFFFFF || rows < 0 || (rows > 0 && n == 0) || H <= 0 || ldc < Hp)
+    return fail(NTLB_EINVAL, "%s: bad shape (0 <= n < 2^31, rows >= 0 with records to read, ldc >= 128*ceil(H/128))",
+                fn);
+  RankOffsets ro{};
+  if (src_rank) {
+    if (!recv_offsets || ep_size < 1 || ep_size > EP_MAX_RANKS)
+      return fail(NTLB_EINVAL, "%s: src_rank needs recv_offsets and 1 <= ep_size <= %d", fn, EP_MAX_RANKS);
+    if (recv_offsets[0] != 0 || recv_offsets[ep_size] != n)
+      return fail(NTLB_EINVAL, "%s: recv_offsets must run from 0 to n", fn);
+    for (int s = 0; s <= ep_size; ++s) {
+      if (s > 0 && recv_offsets[s] < recv_offsets[s - 1])
+        return fail(NTLB_EINVAL, "%s: recv_offsets must not decrease", fn);
+      ro.v[s] = (int32_t)recv_offsets[s];
+    }
+  }
+  if (rows == 0) return NTLB_OK;
+  if (!records || !inv || !codes || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
   if (!aligned(records, 16)) return fail(NTLB_EINVAL, "%s: records must be 16-byte aligned", fn);
   const int64_t R = ntlb_ep_record_bytes(H);
   const int64_t s_off = Hp;
   const int64_t m_off = R - 32;
   const bool vec = aligned(codes, 16) && ldc % 16 == 0;
-  dim3 grd((unsigned)cdiv(n, 4)), blk(256);
+  dim3 grd((unsigned)cdiv(rows, 4)), blk(256);
   hipStream_t st = as_stream(stream);
   if (vec)
-    ep_gather_kernel<true><<<grd, blk, 0, st>>>(records, n, Hp, R, s_off, m_off, inv, recv_offsets, ep_size, codes,
-                                                 ldc, scales, s_row, s_col, nan_rows, token_idx, slot_idx, src_rank,
-                                                 weight);
+    ep_gather_kernel<true><<<grd, blk, 0, st>>>(records, n, rows, Hp, R, s_off, m_off, inv, ro, ep_size, codes, ldc, scales,
+                                                 s_row, s_col, nan_rows, token_idx, slot_idx, src_rank, weight);
   else
-    ep_gather_kernel<false><<<grd, blk, 0, st>>>(records, n, Hp, R, s_off, m_off, inv, recv_offsets, ep_size, codes,
-                                                  ldc, scales, s_row, s_col, nan_rows, token_idx, slot_idx, src_rank,
-                                                  weight);
+    ep_gather_kernel<false><<<grd, blk, 0, st>>>(records, n, rows, Hp, R, s_off, m_off, inv, ro, ep_size, codes, ldc, scales,
+                                                  s_row, s_col, nan_rows, token_idx, slot_idx, src_rank, weight);
   return check_launch(fn);
 }

@@ -37,11 +37,11 @@ struct QuantArgs {
   int dq_dtype;
   int64_t lddq;
   int32_t* nan_rows;
-  // fast 1x128 path only: output row r quantizes input row row_map[r] /
-  // row_div (clamped below rows_in; the expert-parallel send records), and its
-  // NaN flag is nan_rows[r * nan_stride]
-  const int32_t* row_map;
-  int64_t row_div, rows_in;
+  // fast 1x128 path, fan-out (the expert-parallel send records): input row r
+  // goes to the output rows fan_pos[r * fan_k + k], k < fan_k (clamped below
+  // fan_rows); output row p's NaN flag is nan_rows[p * nan_stride]
+  const int32_t* fan_pos;
+  int64_t fan_k, fan_rows;
   int64_t nan_stride;
 };
 
@@ -222,12 +222,11 @@ __device__ __forceinline__ void tile_loads(Chunk8<IN_DT> (&c)[TILE_TU], const Qu
 #pragma unroll
   for (int u = 0; u < TILE_TU; ++u) {
     const int64_t k0 = (int64_t)(t0 + u) * 128 + lane16 * 8;
-    const int64_t src = (a.row_map && r < a.R) ? min<int64_t>(max<int32_t>(a.row_map[r], 0) / a.row_div, a.rows_in - 1) : r;
-    chunk_load<IN_DT>(c[u], a.x, src * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
+    chunk_load<IN_DT>(c[u], a.x, r * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
   }
 }
 
-template <int IN_DT, int GRID, bool SR, bool DQ>
+template <int IN_DT, int GRID, bool SR, bool DQ, bool FAN>
 __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], const QuantArgs& a, int64_t r, int t0,
                                            int T, int lane16) {
 #pragma unroll
@@ -239,6 +238,25 @@ __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], co
     uint32_t m = row16_max_u32(chunk_amax<IN_DT>(c[u]));
     const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
     const int64_t k0 = (int64_t)t * 128 + lane16 * 8;
+    if constexpr (FAN) {
+      // one tile, fan_k output rows: round to nearest quantizes once; stochastic
+      // rounding draws each output row's bits from its own element index
+      uint32_t lo, hi, rb[8];
+      float q[8];
+      bool nan = false;
+      if constexpr (!SR) nan = quant8_tile<GRID, false, false>(v, m, s, a.qmaxf, rb, lo, hi, q);
+      for (int64_t k = 0; k < a.fan_k; ++k) {
+        const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + k], 0), a.fan_rows - 1);
+        if constexpr (SR) {
+          sr_words<true>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
+          nan = quant8_tile<GRID, true, false>(v, m, s, a.qmaxf, rb, lo, hi, q);
+        }
+        if (nan && a.nan_rows && lane16 == 0) atomicOr(a.nan_rows + p * a.nan_stride, 1);
+        *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo, hi);
+        if (lane16 == 0) a.scales[p * a.s_row + (int64_t)t * a.s_col] = s;
+      }
+      continue;
+    }
     uint32_t rb[8];
     sr_words<SR>((uint64_t)(r * a.K + k0), a.seed, a.offset, rb);
     uint32_t lo, hi;
@@ -254,7 +272,7 @@ __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], co
 // Workgroup (bx, by) covers tile columns [TU*by, TU*by+TU) of the row blocks
 // bx, bx + gridDim.x, ... (16 rows each); the loads of the next row block are
 // in flight while the current one is quantized.
-template <int IN_DT, int GRID, bool SR, bool DQ>
+template <int IN_DT, int GRID, bool SR, bool DQ, bool FAN = false>
 __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
   const int lane16 = threadIdx.x & 15;
   const int T = (int)((a.K + 127) >> 7);
@@ -272,7 +290,7 @@ __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
     // no prefetch: the lowest register count and the highest occupancy; the
     // loop only runs when the grid is capped below the number of row blocks
     for (;;) {
-      if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ>(cur, a, r, t0, T, lane16);
+      if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ, FAN>(cur, a, r, t0, T, lane16);
       rb += gxr;
       if (rb >= n_rb) return;
       r = rb * 16 + (threadIdx.x >> 4);
@@ -283,7 +301,7 @@ __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
     const int64_t rb_next = rb + gxr;
     const int64_t r_next = rb_next * 16 + (threadIdx.x >> 4);
     if (rb_next < n_rb) tile_loads<IN_DT>(nxt, a, r_next, t0, T, lane16);
-    if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ>(cur, a, r, t0, T, lane16);  // whole 16-lane rows
+    if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ, FAN>(cur, a, r, t0, T, lane16);  // whole 16-lane rows
     if (rb_next >= n_rb) break;
     rb = rb_next;
     r = r_next;
@@ -980,9 +998,9 @@ static QuantArgs make_args(const void* x, int64_t R, int64_t K, int64_t ldx, int
   a.dq_dtype = dq_dtype;
   a.lddq = lddq;
   a.nan_rows = nan_rows;
-  a.row_map = nullptr;
-  a.row_div = 1;
-  a.rows_in = R;
+  a.fan_pos = nullptr;
+  a.fan_k = 1;
+  a.fan_rows = R;
   a.nan_stride = 1;
   return a;
 }
@@ -1272,15 +1290,15 @@ extern "C" int ntlb_dequant(int grid, const uint8_t* codes, int64_t ldc, const f
 }
 
 // Expert-parallel send records (the record layout is described in ep.hip):
-// metadata of record p from assignment a = inv[p] (token a / K, slot a % K,
-// local expert topk_idx[a] % experts_per_rank, routing weight topk_w[a]),
-// with the NaN flag cleared for the quantizer to set.
+// assignment a goes to record p = pos[a], whose metadata is token a / K, slot
+// a % K, local expert topk_idx[a] % experts_per_rank and routing weight
+// topk_w[a], with the NaN flag cleared for the quantizer to set.
 __global__ void __launch_bounds__(256) ep_meta_kernel(uint8_t* rec, int64_t R, int64_t m_off, int64_t A,
-                                                      const int32_t* inv, const void* topk_idx, int idx_dt,
+                                                      const int32_t* pos, const void* topk_idx, int idx_dt,
                                                       const void* topk_w, int w_dt, int64_t K, int64_t epr) {
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p >= A) return;
-  const int64_t a = min<int64_t>(max<int32_t>(inv[p], 0), A - 1);
+  const int64_t a = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (a >= A) return;
+  const int64_t p = min<int64_t>(max<int32_t>(pos[a], 0), A - 1);
   const int64_t e = idx_dt == 1 ? reinterpret_cast<const int64_t*>(topk_idx)[a]
                                 : (int64_t) reinterpret_cast<const int32_t*>(topk_idx)[a];
   const float w = load_elem(topk_w, w_dt, a);
@@ -1290,7 +1308,7 @@ __global__ void __launch_bounds__(256) ep_meta_kernel(uint8_t* rec, int64_t R, i
 }
 
 extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
-                                    const int32_t* inv, const void* topk_idx, int idx_dtype, const void* topk_w,
+                                    const int32_t* pos, const void* topk_idx, int idx_dtype, const void* topk_w,
                                     int w_dtype, int64_t K, int64_t experts_per_rank, int grid, int qmax,
                                     int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
                                     void* stream) {
@@ -1299,29 +1317,30 @@ extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, 
     return fail(NTLB_EINVAL, "%s: bad argument", fn);
   const int64_t A = T * K;
   if (A > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
-  int rc = check_common(fn, tokens, x_dtype, A, H, ldt, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  int rc = check_common(fn, tokens, x_dtype, T, H, ldt, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
   if (rc) return rc;
   if (A == 0 || H == 0) return NTLB_OK;
-  if (!inv || !topk_idx || !topk_w || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (!pos || !topk_idx || !topk_w || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
   const int64_t R = ntlb_ep_record_bytes(H);
   const int64_t s_off = (H + 127) / 128 * 128, m_off = R - 32;
   const int64_t Tt = cdiv(H, 128);
   const bool vec = aligned(tokens, 16) && ((ldt * dtype_size(x_dtype)) % 16 == 0);
   if (!(vec && H % 8 == 0 && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) && aligned(records, 16) &&
-        cdiv(A, 16) <= 0x7FFFFFFF && cdiv(Tt, TILE_TU) <= 65535))
+        cdiv(Tt, TILE_TU) <= 65535))
     return fail(NTLB_EUNSUPPORTED, "%s: needs bf16/fp32 tokens, H %% 8 == 0, 16-byte aligned rows and records", fn);
   hipStream_t st = as_stream(stream);
-  ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, m_off, A, inv, topk_idx, idx_dtype, topk_w,
+  ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, m_off, A, pos, topk_idx, idx_dtype, topk_w,
                                                           w_dtype, K, experts_per_rank);
-  QuantArgs a = make_args(tokens, A, H, ldt, grid, qmax, scale_rule, seed, offset, records, R,
+  // one token row read, quantized, and written to its K records
+  QuantArgs a = make_args(tokens, T, H, ldt, grid, qmax, scale_rule, seed, offset, records, R,
                           reinterpret_cast<float*>(records + s_off), R / 4, 1, nullptr, 0, 0,
                           reinterpret_cast<int32_t*>(records + m_off + 12));
-  a.row_map = inv;
-  a.row_div = K;
-  a.rows_in = T;
+  a.fan_pos = pos;
+  a.fan_k = K;
+  a.fan_rows = A;
   a.nan_stride = R / 4;
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
-  const int64_t n_rb = cdiv(A, 16), n_tg = cdiv(Tt, TILE_TU);
+  const int64_t n_rb = cdiv(T, 16), n_tg = cdiv(Tt, TILE_TU);
   int64_t gx = n_rb;
   if (NTLB_TILE_PIPELINE) {
     gx = cdiv(n_rb, 4);
@@ -1330,9 +1349,9 @@ extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, 
   dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)n_tg, (unsigned)gx) : dim3((unsigned)gx, (unsigned)n_tg), fblk(256);
   NTLB_DISPATCH_GRID_SR(grid, sr, {
     if (x_dtype == NTLB_BF16)
-      quant_tile_1x128_fast<DT_BF16, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+      quant_tile_1x128_fast<DT_BF16, G_, S_, false, true><<<fgrd, fblk, 0, st>>>(a);
     else
-      quant_tile_1x128_fast<DT_F32, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+      quant_tile_1x128_fast<DT_F32, G_, S_, false, true><<<fgrd, fblk, 0, st>>>(a);
   });
   return check_launch(fn);
 }

@@ -20,11 +20,13 @@ dequantize/re-quantize round trip.
                     _DispatchedTokens (moe.py:49-58)
 
 Capacity dropping (moe.py:919-923) keeps the top-capacity rows of an expert by
-routing weight; unpack_dispatch takes an explicit row order for that case.
+routing weight: capacity_order selects them, and unpack_dispatch gathers that
+explicit record order.
 """
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import List, Optional, Sequence
 
@@ -95,11 +97,11 @@ def pack_dispatch(tokens: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Te
     w = topk_w.contiguous()
     if tokens.stride(-1) != 1 or tokens.stride(0) % 8 or tokens.data_ptr() % 16:
         tokens = tokens.contiguous()
-    _, inv, counts, _ = partition(idx, divisor=experts_per_rank, buckets=ep_size)
+    pos, _, counts, _ = partition(idx, divisor=experts_per_rank, buckets=ep_size)
     R, _, _ = record_layout(H)
     records = torch.empty((T * K, R), dtype=torch.uint8, device=tokens.device)
     call("ntlb_ep_pack_records", tokens.data_ptr(), ops._dtype_code(tokens.dtype), T, H, tokens.stride(0),
-         inv.data_ptr(), idx.data_ptr(), KEY_INT64 if idx.dtype == torch.int64 else KEY_INT32, w.data_ptr(),
+         pos.data_ptr(), idx.data_ptr(), KEY_INT64 if idx.dtype == torch.int64 else KEY_INT32, w.data_ptr(),
          ops._dtype_code(w.dtype), K, experts_per_rank, ops.grid_code(fmt), (1 << (bits - 1)) - 1,
          ops.rounding_code(rounding), scale_rule, seed, offset, records.data_ptr(), ops._stream())
     return SendBuffer(records, counts, H)
@@ -138,9 +140,12 @@ class ExpertRows:
 
 
 def unpack_dispatch(records: torch.Tensor, recv_counts: Sequence[int], *, H: int, local_experts: int,
-                    fmt: str = "e4m3", order: Optional[torch.Tensor] = None) -> ExpertRows:
+                    fmt: str = "e4m3", order: Optional[torch.Tensor] = None,
+                    order_counts: Optional[Sequence[int]] = None) -> ExpertRows:
     """Group the received records by local expert (stable in arrival order),
-    or in the given record order, into codes + scales for the grouped GEMM."""
+    or take the given record order (rows of expert e next to each other,
+    order_counts[e] of them, e.g. from capacity_order), into codes + scales
+    for the grouped GEMM."""
     ops._require_device(records)
     R, _, m_off = record_layout(H)
     if records.dim() != 2 or records.shape[1] != R or records.dtype != torch.uint8:
@@ -154,8 +159,13 @@ def unpack_dispatch(records: torch.Tensor, recv_counts: Sequence[int], *, H: int
         # keys: each record's local-expert int32, R bytes apart
         _, order, counts, offsets = _partition(records.data_ptr() + m_off + 8, KEY_INT32, R, n, 1, local_experts, dev)
     else:
-        order = order.to(dtype=torch.int32).contiguous()
+        order = order.to(device=dev, dtype=torch.int32).contiguous()
         counts = offsets = None
+        if order_counts is not None:
+            if len(order_counts) != local_experts or sum(int(c) for c in order_counts) != order.numel():
+                raise ValueError("order_counts needs one count per local expert, adding up to len(order)")
+            counts = torch.tensor([int(c) for c in order_counts], dtype=torch.int64).to(dev, non_blocking=True)
+            offsets = torch.tensor([0] + _cumsum(order_counts), dtype=torch.int32).to(dev, non_blocking=True)
     rows = order.numel()
     T = cdiv(H, 128)
     ldc = T * 128
@@ -167,12 +177,34 @@ def unpack_dispatch(records: torch.Tensor, recv_counts: Sequence[int], *, H: int
     slot_idx = torch.empty(rows, dtype=torch.int32, device=dev)
     src_rank = torch.empty(rows, dtype=torch.int32, device=dev)
     weight = torch.empty(rows, dtype=torch.float32, device=dev)
-    recv_offsets = torch.tensor([0] + list(_cumsum(recv_counts)), dtype=torch.int64, device=dev)
-    call("ntlb_ep_unpack_records", records.data_ptr(), rows, H, order.data_ptr(), recv_offsets.data_ptr(),
+    # host memory: the entry point reads the prefix at the call (no copy to the device)
+    recv_offsets = (ctypes.c_int64 * (len(recv_counts) + 1))(0, *_cumsum(recv_counts))
+    call("ntlb_ep_unpack_records", records.data_ptr(), n, H, order.data_ptr(), rows, ctypes.addressof(recv_offsets),
          len(recv_counts), codes.data_ptr(), ldc, scales.data_ptr(), 1, rp, nan_rows.data_ptr(),
          token_idx.data_ptr(), slot_idx.data_ptr(), src_rank.data_ptr(), weight.data_ptr(), ops._stream())
     q = QTensor(codes, scales, 1, rp, 0, ops.grid_code(fmt), rows, H, nan_rows)
     return ExpertRows(q, offsets, counts, token_idx, slot_idx, src_rank, weight, order)
+
+
+def capacity_order(rows: ExpertRows, capacity: int):
+    """The rows _run_local_experts keeps under an expert capacity
+    (moe.py:919-923): per local expert, the `capacity` rows of highest routing
+    weight, highest first (torch.topk, sorted), or all rows in arrival order
+    when there are no more than `capacity` (or capacity <= 0).  Returns (record
+    order, kept count per expert) for unpack_dispatch(order=, order_counts=)."""
+    if rows.offsets is None:
+        raise ValueError("capacity_order needs rows grouped by unpack_dispatch (offsets known)")
+    offs = [int(v) for v in rows.offsets.tolist()]
+    parts, kept = [], []
+    for e in range(len(offs) - 1):
+        a, b = offs[e], offs[e + 1]
+        sel = rows.order[a:b]
+        if 0 < capacity < b - a:
+            sel = sel[torch.topk(rows.weight[a:b], k=capacity, sorted=True).indices]
+        parts.append(sel)
+        kept.append(int(sel.numel()))
+    order = torch.cat(parts) if parts else rows.order[:0]
+    return order, kept
 
 
 def _cumsum(xs: Sequence[int]) -> List[int]:

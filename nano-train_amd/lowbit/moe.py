@@ -157,8 +157,13 @@ def grouped_linear(
 
     X is quantized per 1x128 tile over all rows at once; the experts' codes
     come from quantize_expert_weights()."""
-    qx = ops.quant_tile_1x128(x_sorted, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
-                              want_nan_rows=True)
+    if isinstance(x_sorted, ops.QTensor):
+        qx = x_sorted
+        out_dtype = out_dtype or torch.bfloat16
+    else:
+        qx = ops.quant_tile_1x128(x_sorted, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
+                                  want_nan_rows=True)
+        out_dtype = out_dtype or x_sorted.dtype
     return ops.gemm_grouped_blockscaled(qx, w_codes, w_scales, offsets, N=w_codes.shape[1],
                                         out_dtype=out_dtype or x_sorted.dtype, b_nan_rows=w_nan_rows)
 
@@ -204,10 +209,14 @@ def expert_mlp(
     seed: int = 0,
     offset: int = 0,
     want_h: bool = False,
+    out_dtype: torch.dtype = None,
 ):
     """ExpertMLP.forward (moe.py:190-193) for all local experts at once.
 
-    x_sorted [T, H] rows sorted by expert, offsets int32 [E+1]; gate_up is
+    x_sorted [T, H] rows sorted by expert, or those rows already as 1x128
+    codes (a QTensor with tile-major scales, e.g. the received rows of
+    ep.unpack_dispatch; out_dtype then defaults to bf16), offsets int32 [E+1];
+    gate_up is
     interleave_gate_up()'s (codes, scales, nan) of [E, 2I, Kp], down is
     quantize_expert_weights()'s (codes, scales, nan) of [E, H, Ip].  Three
     kernels: the 1x128 quantization of x, the gate/up GEMM with SwiGLU and the
@@ -217,11 +226,16 @@ def expert_mlp(
     when want_h)."""
     gu_codes, gu_scales, gu_nan = gate_up
     d_codes, d_scales, d_nan = down
-    qx = ops.quant_tile_1x128(x_sorted, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
-                              want_nan_rows=True)
+    if isinstance(x_sorted, ops.QTensor):
+        qx = x_sorted
+        out_dtype = out_dtype or torch.bfloat16
+    else:
+        qx = ops.quant_tile_1x128(x_sorted, fmt=fmt, bits=bits, rounding=rounding, seed=seed, offset=offset,
+                                  want_nan_rows=True)
+        out_dtype = out_dtype or x_sorted.dtype
     h, qh = ops.gemm_swiglu_quant(qx, gu_codes, gu_scales, offsets=offsets, fmt=fmt, bits=bits, rounding=rounding,
                                   seed=seed, offset=offset + 1, want_h=want_h, want_nan_rows=True,
                                   b_nan_rows=gu_nan)
-    out = ops.gemm_grouped_blockscaled(qh, d_codes, d_scales, offsets, N=d_codes.shape[1], out_dtype=x_sorted.dtype,
+    out = ops.gemm_grouped_blockscaled(qh, d_codes, d_scales, offsets, N=d_codes.shape[1], out_dtype=out_dtype,
                                        b_nan_rows=d_nan)
     return (out, h) if want_h else out

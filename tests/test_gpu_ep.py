@@ -39,7 +39,8 @@ def _decode(records: np.ndarray, H: int):
 
 
 @pytest.mark.parametrize("n", [0, 1, 300, 5000, 70000])
-@pytest.mark.parametrize("dtype,divisor,buckets", [(torch.int32, 1, 7), (torch.int64, 4, 8), (torch.int64, 1, 512)])
+@pytest.mark.parametrize("dtype,divisor,buckets", [(torch.int32, 1, 7), (torch.int64, 4, 8), (torch.int64, 1, 512),
+                                                   (torch.int32, 3, 4096)])
 def test_partition_is_a_stable_sort(gpu_device, n, dtype, divisor, buckets):
     from lowbit import ep
 
@@ -204,3 +205,74 @@ def test_c4_size_records_feed_the_expert_path(gpu_device):
     assert torch.equal(rows.q.codes, qx.codes)
     M = rows.q.rows
     assert torch.equal(rows.q.scales[:, :M], qx.scales[:, :M])
+
+
+def test_capacity_drop_keeps_top_weights(gpu_device):
+    """Capacity drop (moe.py:919-923): per local expert the `capacity` rows of
+    highest routing weight, highest first; the kept record indices run past
+    the number of kept rows, so every row must come from its own record."""
+    from lowbit import ep
+
+    ep_size, epr, H, K, cap = 2, 4, 384, 4, 9
+    _, _, _, _, recv = _emulated_exchange(ep_size, epr, H, [30, 25], K, 20261240, gpu_device)
+    records, counts = recv[1]
+    rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr)
+    order, kept = ep.capacity_order(rows, cap)
+    got = ep.unpack_dispatch(records, counts, H=H, local_experts=epr, order=order, order_counts=kept)
+    torch.cuda.synchronize()
+    rec = records.cpu().numpy()
+    codes, scales, meta, weight, _ = _decode(rec, H)
+    want, want_kept = [], []
+    for e in range(epr):
+        sel = np.nonzero(meta[:, 2] == e)[0]  # arrival order
+        if len(sel) > cap:
+            sel = sel[np.argsort(-weight[sel], kind="stable")[:cap]]
+        want.extend(sel.tolist())
+        want_kept.append(len(sel))
+    want = np.array(want)
+    assert kept == want_kept and sum(kept) < len(rec) and want.max() >= len(want)
+    assert np.array_equal(got.order.cpu().numpy(), want), "kept order"
+    assert np.array_equal(got.offsets.cpu().numpy(), np.concatenate([[0], np.cumsum(want_kept)])), "offsets"
+    assert_bits_equal(got.q.codes.cpu().numpy()[:, :H], codes[want], "kept codes")
+    assert_bits_equal(np.ascontiguousarray(got.q.scales.cpu().numpy()[:, :len(want)].T), scales[want], "kept scales")
+    assert np.array_equal(got.token_idx.cpu().numpy(), meta[want, 0]), "token index"
+    assert_bits_equal(got.weight.cpu().numpy(), weight[want], "weights")
+    src = np.searchsorted(np.cumsum(counts), want, side="right")
+    assert np.array_equal(got.src_rank.cpu().numpy(), src), "source rank"
+
+
+def test_unpack_rejects_bad_offsets(gpu_device):
+    from lowbit import ep
+
+    R, _, _ = ep.record_layout(256)
+    records = torch.zeros((6, R), dtype=torch.uint8, device=gpu_device)
+    with pytest.raises(ValueError):
+        ep.unpack_dispatch(records, [2, 3], H=256, local_experts=2)  # counts add up to 5, not 6
+    with pytest.raises(ValueError):
+        ep.unpack_dispatch(records, [1] * 6 + [0] * 251, H=256, local_experts=2)  # more than 256 ranks
+
+
+def test_expert_mlp_on_received_codes_equals_local_path(gpu_device):
+    """The received codes go straight into the expert MLP (no dequantize and
+    re-quantize): with round to nearest the codes are those the local path
+    quantizes from the expert-sorted tokens, so the output is bit-identical."""
+    from lowbit import ep, moe
+
+    T, H, I, E, K = 512, 1024, 256, 8, 4
+    x = seeded((T, H), seed=20261250, outliers=0.01).to(gpu_device)
+    idx, w = _routing(T, K, E, 20261251)
+    idx = idx.to(gpu_device)
+    wg, wu = seeded((E, I, H), seed=20261252, std=0.02).to(gpu_device), seeded((E, I, H), seed=20261253,
+                                                                                  std=0.02).to(gpu_device)
+    wd = seeded((E, H, I), seed=20261254, std=0.02).to(gpu_device)
+    g, u = moe.quantize_expert_weights(wg), moe.quantize_expert_weights(wu)
+    gate_up = moe.interleave_gate_up(g[0], g[1], u[0], u[1], g[2], u[2])
+    down = moe.quantize_expert_weights(wd)
+    send = ep.pack_dispatch(x, idx, w.to(gpu_device), experts_per_rank=E, ep_size=1)
+    rows = ep.unpack_dispatch(send.records, [send.records.shape[0]], H=H, local_experts=E)
+    got = moe.expert_mlp(rows.q, rows.offsets, gate_up, down)
+    _, token_index, offsets = moe.sort_by_expert(idx, E)
+    want = moe.expert_mlp(x[token_index.long()], offsets, gate_up, down)
+    torch.cuda.synchronize()
+    assert torch.equal(rows.token_idx.long(), token_index.long())
+    assert got.dtype == want.dtype and torch.equal(got, want)
