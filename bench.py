@@ -7,7 +7,9 @@ nearest), and the blockwise-scaled FP8 GEMM Y = X_dq W_dq^T (fp32 accumulate,
 bf16 out).  Inputs are resident in HBM before the timed region; three input
 sets rotate so that no step reads its inputs from the 256 MB Infinity Cache.
 
-`value` = GEMM FLOPs per step / step time (quantizers included).  The
+Before the W counted warm-up steps, the step runs untimed for SPIN_UP_S
+seconds so that the timed steps see the sustained clock, not the ramp from
+idle.  `value` = GEMM FLOPs per step / step time (quantizers included).  The
 `roofline` object is the GEMM kernel alone, timed with HIP events on the
 stream the kernels run on.  `cpu_baseline` times the CPU oracle (oracle/,
 numpy + C) on a 1024-row sample of the same workload.
@@ -30,6 +32,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 FP8_PEAK_TFLOPS = 5000.0  # dense fp8 (and int8 TOP/s) of MI355X
+SPIN_UP_S = 0.3  # untimed sustained load before the counted warm-up steps
 
 
 def parse_args():
@@ -48,9 +51,27 @@ def parse_args():
     return p.parse_args()
 
 
+def _spin_up(fn, seconds: float = SPIN_UP_S) -> None:
+    """Run fn untimed for `seconds` of wall time.  From idle, the clocks take
+    about 50 ms of sustained load to settle (a c2 GEMM runs 7-30% slower over
+    its first launches); the timed steps should see the sustained rate that a
+    training loop runs at."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end:
+        fn(i)
+        i += 1
+        if i % 4 == 0:
+            torch.cuda.synchronize()  # keep the host within a few launches of the GPU
+    torch.cuda.synchronize()
+
+
 def _time_ms(fn, n: int, warmup: int, stream) -> float:
     import torch
 
+    _spin_up(fn, SPIN_UP_S / 3)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -318,6 +339,7 @@ def main():
             ev[3].record(stream)
         return y
 
+    _spin_up(step)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -382,6 +404,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "spin_up_s": SPIN_UP_S,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",

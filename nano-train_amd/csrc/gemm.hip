@@ -382,30 +382,68 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
 #pragma unroll
     for (int tm = 0; tm < 8; ++tm) sam_all[tm] = s_cur[wm * 128 + tm * 16 + (lane & 15)];
     v8i af = load_frag(ta, wm * 128, lane);
+    if constexpr (GRID == GRID_E4M3 && B_UNIFORM) {
+      // The promotion is software pipelined: step tm issues group tm's four
+      // MFMAs and promotes group tm-1's results meanwhile, one MFMA then four
+      // FMAs at a time, so the FMAs never wait on the MFMA they depend on.
+      // (16 more VGPRs: the other variants would spill, and keep the plain order.)
+      v4f dp[4];
 #pragma unroll
-    for (int tm = 0; tm < 8; ++tm) {
-      v8i af_next;
-      if (tm + 1 < 8) af_next = load_frag(ta, wm * 128 + (tm + 1) * 16, lane);
-      const float sam = sam_all[tm];
-      // the next block's copies go out one group per 16-row step, spread
-      // over the first half of the MFMA phase
-      if (tm < 4) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kn, wave, tm);
-      v4f d[4];
+      for (int tm = 0; tm < 9; ++tm) {
+        v8i af_next;
+        v4f d[4];
+        if (tm < 8) {
+          if (tm + 1 < 8) af_next = load_frag(ta, wm * 128 + (tm + 1) * 16, lane);
+          // the next block's copies go out one group per 16-row step, spread
+          // over the first half of the MFMA phase
+          if (tm < 4) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kn, wave, tm);
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
+          for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
+        }
+        if (tm > 0) {
+          const float s = sam_all[tm - 1] * sbu;
 #pragma unroll
-      for (int tn = 0; tn < 4; ++tn) {
-        if constexpr (B_UNIFORM) {
-          const float s = sam * sbu;
-          acc[tm][tn] += d[tn] * s;
-        } else {
-          acc[tm][tn] += (d[tn] * sbv[tn]) * sam;
+          for (int tn = 0; tn < 4; ++tn) acc[tm - 1][tn] += dp[tn] * s;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+          }
+          // group tm-1's accumulators are final here, and no later LDS read
+          // moves above this point
+          asm volatile("" : "+v"(acc[tm - 1][0]), "+v"(acc[tm - 1][1]), "+v"(acc[tm - 1][2]),
+                       "+v"(acc[tm - 1][3])::"memory");
+        }
+        if (tm < 8) {
+#pragma unroll
+          for (int tn = 0; tn < 4; ++tn) dp[tn] = d[tn];
+          if (tm + 1 < 8) af = af_next;
         }
       }
-      // this group's accumulators are final here, and no later LDS read
-      // moves above this point
-      asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
-      if (tm + 1 < 8) af = af_next;
+    } else {
+#pragma unroll
+      for (int tm = 0; tm < 8; ++tm) {
+        v8i af_next;
+        if (tm + 1 < 8) af_next = load_frag(ta, wm * 128 + (tm + 1) * 16, lane);
+        const float sam = sam_all[tm];
+        if (tm < 4) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kn, wave, tm);
+        v4f d[4];
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
+#pragma unroll
+        for (int tn = 0; tn < 4; ++tn) {
+          if constexpr (B_UNIFORM) {
+            const float s = sam * sbu;
+            acc[tm][tn] += d[tn] * s;
+          } else {
+            acc[tm][tn] += (d[tn] * sbv[tn]) * sam;
+          }
+        }
+        // this group's accumulators are final here, and no later LDS read
+        // moves above this point
+        asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
+        if (tm + 1 < 8) af = af_next;
+      }
     }
     (BUF ? lds_s0 : lds_s1)[tid] = s_next;
     __builtin_amdgcn_s_waitcnt(0);
