@@ -184,6 +184,20 @@ def other_config(args) -> dict:
                              args.steps, args.warmup, st) * 1e3
         rec_b = send.records.shape[1]
         n_rec = send.records.shape[0]
+        # the return trip: every row's expert output back as a record, then the
+        # weighted sum into the 4096 token outputs
+        rows = ep.unpack_dispatch(send.records, rcounts, H=H, local_experts=4, fmt=fmt)
+        out_rows = torch.randn((n_rec, H), generator=torch.Generator().manual_seed(5), dtype=torch.float32)
+        out_rows = out_rows.to(dev, torch.bfloat16)
+        ret = ep.pack_return(out_rows, rows, ep_size=8, fmt=fmt)
+        w_b = topk_w.to(torch.bfloat16)
+        ret_us = _time_ms(lambda i: ep.pack_return(out_rows, rows, ep_size=8, fmt=fmt), args.steps, args.warmup,
+                          st) * 1e3
+        comb_us = _time_ms(lambda i: ep.combine(ret.records, routing, w_b, H=H, fmt=fmt), args.steps, args.warmup,
+                           st) * 1e3
+        ret_bytes = n_rec * (H * 2 + rec_b)
+        comb_bytes = n_rec * rec_b + tokens.shape[0] * H * 2
+        del rows, out_rows, ret
         # pack: every bf16 token row read once, one record written per assignment;
         # unpack: one record read, codes + tile scales + 5 words of metadata written per row
         pack_bytes = tokens.shape[0] * H * 2 + n_rec * rec_b
@@ -201,7 +215,9 @@ def other_config(args) -> dict:
                    comm_quant_us=round(comm_us, 2), comm_quant_GBs=round(comm_bytes / comm_us / 1e3, 1),
                    ep_dispatch={"records": n_rec, "record_bytes": rec_b, "pack_us": round(pack_us, 2),
                                 "pack_GBs": round(pack_bytes / pack_us / 1e3, 1), "unpack_us": round(unpack_us, 2),
-                                "unpack_GBs": round(unpack_bytes / unpack_us / 1e3, 1)})
+                                "unpack_GBs": round(unpack_bytes / unpack_us / 1e3, 1),
+                                "return_pack_us": round(ret_us, 2), "return_pack_GBs": round(ret_bytes / ret_us / 1e3, 1),
+                                "combine_us": round(comb_us, 2), "combine_GBs": round(comb_bytes / comb_us / 1e3, 1)})
         return res
     # c5
     x, w = workloads.c5_inputs(device="cpu")

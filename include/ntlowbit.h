@@ -405,6 +405,57 @@ int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, 
                          uint64_t offset, uint8_t* records, void* stream);
 
 /*
+ * ntlb_ep_pack_records with the reference's own comm-quant scales
+ * (_comm_quant_dequant, moe.py:79-143, applied to the send buffer by
+ * _dispatch_tokens, moe.py:805-814): one scale per gc-column group over all
+ * rows, from the group amaxes of ntlb_amax_grouped on tokens [T, H] with gr =
+ * T and the same gc (granularity tile_1x128 / block_128x128: gc = 128, one
+ * strip per tile; tensor: gc = H).  gc % 128 == 0 or gc >= H.  Every record's
+ * tile scales are its group's scale; codes as ntlb_quant_grouped writes them
+ * (grid, qmax, rounding, scale_rule as there; the reference uses the int grid,
+ * qmax 127 and NTLB_SCALE_BEFORE_DIVIDE).  amax_bits NULL gives
+ * ntlb_ep_pack_records.
+ */
+int ntlb_ep_pack_records_grouped(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
+                                 const int32_t* pos, const void* topk_idx, int idx_dtype, const void* topk_w,
+                                 int w_dtype, int64_t K, int64_t experts_per_rank, const uint32_t* amax_bits,
+                                 int64_t gc, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                 uint64_t offset, uint8_t* records, void* stream);
+
+/*
+ * Expert side of the combine (moe.py:926-962, _combine_remote_outputs
+ * :964-1038): row i of the expert outputs x [n, H] (row stride ldx) becomes
+ * record pos[i] (pos from ntlb_ep_partition on the rows' source ranks, so
+ * each destination's records keep expert order, as send_back_features_parts
+ * does), with token_idx[i], slot_idx[i], the optional local expert and
+ * weight, and the NaN flag.  Payload: per-row 1x128 tiles (amax_bits NULL,
+ * the quantizer of ntlb_quant_tile_1x128) or group scales from
+ * ntlb_amax_grouped on x with gr = n (as ntlb_ep_pack_records_grouped).  SR
+ * element index p*H + column.  x bf16 or fp32, H % 8 == 0, 16-byte aligned
+ * rows and records.
+ */
+int ntlb_ep_pack_return(const void* x, int x_dtype, int64_t n, int64_t H, int64_t ldx, const int32_t* pos,
+                        const int32_t* token_idx, const int32_t* slot_idx, const int32_t* local_expert,
+                        const float* weight, const uint32_t* amax_bits, int64_t gc, int grid, int qmax, int rounding,
+                        int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records, void* stream);
+
+/*
+ * Source side of the combine (moe.py:1021-1027): out[t] = the sum over token
+ * t's returned records of topk_w[t, slot] * dequant(record), as the
+ * reference's index_add_ into zeros forms it on the CPU: dequant = q * scale
+ * rounded to out_dtype, each product rounded to out_dtype, the products
+ * summed in fp32 in arrival order (for one token, ascending expert id
+ * topk_idx[t, slot]) and the sum rounded to out_dtype once.  Assignments without a record (capacity drops)
+ * add nothing; tokens without any stay zero.  n records of the grid's codes,
+ * topk_idx int32 (idx_dtype 0) or int64 (1) and topk_w (w_dtype) [T, K]
+ * contiguous, K <= 32, H % 8 == 0, out [T, ldo].  slot_map: int32 workspace
+ * of T*K elements.
+ */
+int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* topk_idx, int idx_dtype,
+                    const void* topk_w, int w_dtype, int64_t T, int64_t K, int grid, void* out, int out_dtype,
+                    int64_t ldo, int32_t* slot_map, void* stream);
+
+/*
  * Receiver side: output row i < rows is record inv[i] of the n received
  * records (inv from ntlb_ep_partition on their local-expert field with rows =
  * n, or any selection the caller chooses, e.g. the rows kept by a capacity

@@ -28,6 +28,8 @@
 // metadata in that order for the grouped GEMM.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 
@@ -221,6 +223,162 @@ __global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Combine (moe.py:964-1038): every returned record is the expert output of one
+// (token, slot) assignment; out[t] = sum over the token's slots of
+// w[t, slot] * dequant(record), formed as the reference's index_add_ into
+// zeros forms it on the CPU: each product rounded to the output dtype (a
+// tensor op of that dtype), the products summed in fp32 in arrival order --
+// for one token, ascending global expert id (ranks in order, local experts in
+// order) -- and the sum rounded once.
+// ---------------------------------------------------------------------------
+constexpr int EP_COMBINE_MAX_K = 32;
+
+__global__ void __launch_bounds__(256) ep_slot_fill_kernel(int32_t* slot_map, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) slot_map[i] = -1;
+}
+
+// slot_map[token * K + slot] = the record carrying that assignment; records
+// whose (token, slot) lies outside [0, T) x [0, K) are ignored
+__global__ void __launch_bounds__(256) ep_slot_scatter_kernel(const uint8_t* rec, int64_t n, int64_t R, int64_t m_off,
+                                                              int64_t T, int K, int32_t* slot_map) {
+  const int64_t r = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (r >= n) return;
+  const int32_t* m = reinterpret_cast<const int32_t*>(rec + r * R + m_off);
+  const int32_t t = m[0], k = m[1];
+  if (t >= 0 && t < T && k >= 0 && k < K) slot_map[(int64_t)t * K + k] = (int32_t)r;
+}
+
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+typedef float v2f __attribute__((ext_vector_type(2)));
+
+// two floats rounded to bf16 by the hardware pack-convert (v_cvt_pk_bf16_f32,
+// round to nearest even like f32_to_bf16_bits; a NaN stays a NaN), as their
+// packed bits
+__device__ __forceinline__ uint32_t bf16x2_bits(float a, float b) {
+  const v2bf p = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// the eight codes of two words as floats: e4m3 by the hardware converter
+// (v_cvt_pk_f32_fp8, OCP e4m3fn), the int grid as int8 with -128 the NaN code
+template <int GRID>
+__device__ __forceinline__ void decode8(uint2 cw, float (&q)[8]) {
+  const uint32_t wd[2] = {cw.x, cw.y};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if constexpr (GRID == GRID_E4M3) {
+      const v2f lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)wd[h], false);
+      const v2f hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)wd[h], true);
+      q[4 * h + 0] = lo[0];
+      q[4 * h + 1] = lo[1];
+      q[4 * h + 2] = hi[0];
+      q[4 * h + 3] = hi[1];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t c = (wd[h] >> (8 * i)) & 0xFFu;
+        q[4 * h + i] = c == 0x80u ? __uint_as_float(0x7FC00000u) : (float)(int8_t)c;
+      }
+    }
+  }
+}
+
+// eight values rounded to the output dtype (in place)
+template <int OUT_DT>
+__device__ __forceinline__ void round8(float (&v)[8]) {
+  if constexpr (OUT_DT == DT_BF16) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const uint32_t b = bf16x2_bits(v[i], v[i + 1]);
+      v[i] = __uint_as_float(b << 16);
+      v[i + 1] = __uint_as_float(b & 0xFFFF0000u);
+    }
+  } else if constexpr (OUT_DT == DT_F16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __half2float(__float2half(v[i]));
+  }
+}
+
+// one workgroup per token; thread j owns columns [8j + 2048i, +8)
+template <int GRID, int OUT_DT>
+__global__ void __launch_bounds__(256) ep_combine_kernel(const uint8_t* rec, int64_t n, int64_t R, int64_t s_off,
+                                                         int64_t H, const int32_t* slot_map, const void* topk_idx,
+                                                         int idx_dt, const void* topk_w, int w_dt, int K, void* out,
+                                                         int64_t ldo, int vec_out) {
+#pragma clang fp contract(off)  // each product and sum rounds on its own, as the reference's torch ops do
+  __shared__ int64_t s_e[EP_COMBINE_MAX_K];
+  __shared__ int32_t s_rec[EP_COMBINE_MAX_K];
+  __shared__ float s_w[EP_COMBINE_MAX_K];
+  const int64_t t = blockIdx.x;
+  const int k = threadIdx.x;
+  if (k < K) {
+    const int64_t a = t * K + k;
+    s_e[k] = idx_dt == 1 ? reinterpret_cast<const int64_t*>(topk_idx)[a]
+                         : (int64_t) reinterpret_cast<const int32_t*>(topk_idx)[a];
+  }
+  __syncthreads();
+  if (k < K) {
+    // slot k's place in ascending expert id (ties, which routing does not
+    // produce, keep slot order)
+    const int64_t ek = s_e[k];
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += (s_e[j] < ek || (s_e[j] == ek && j < k)) ? 1 : 0;
+    s_rec[rank] = slot_map[t * K + k];
+    s_w[rank] = load_elem(topk_w, w_dt, t * K + k);
+  }
+  __syncthreads();
+  for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; n > 0 && j0 < K; j0 += 8) {  // n == 0: nothing came back, the outputs are zero
+      // up to eight records' codes and scales in flight at once: slots past K
+      // or without a record read record 0 and are not added
+      uint2 cw[8];
+      float sc[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = min(j0 + u, K - 1);
+        const uint8_t* rp = rec + (int64_t)max(s_rec[j], 0) * R;
+        cw[u] = *reinterpret_cast<const uint2*>(rp + c0);
+        sc[u] = reinterpret_cast<const float*>(rp + s_off)[c0 >> 7];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
+        if (j >= K || s_rec[j] < 0) continue;  // past K, or dropped by a capacity limit: never returned
+        float v[8];
+        decode8<GRID>(cw[u], v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] * sc[u];
+        round8<OUT_DT>(v);  // the dequantized row in the output dtype
+        const float w = s_w[j];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = v[i] * w;
+        round8<OUT_DT>(v);  // the product, a tensor op of the output dtype
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+      }
+    }
+    // the one rounding of the sum
+    if constexpr (OUT_DT == DT_BF16) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pk[i] = bf16x2_bits(acc[2 * i], acc[2 * i + 1]);
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + t * ldo + c0;
+      if (vec_out) {
+        *reinterpret_cast<uint4*>(o) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (uint16_t)(pk[i >> 1] >> (16 * (i & 1)));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) store_elem(out, OUT_DT, t * ldo + c0 + i, acc[i]);
+    }
+  }
+}
+
 }  // namespace ntlb
 
 using namespace ntlb;
@@ -293,5 +451,42 @@ extern "C" int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t
   else
     ep_gather_kernel<false><<<grd, blk, 0, st>>>(records, n, rows, Hp, R, s_off, m_off, inv, ro, ep_size, codes, ldc, scales,
                                                   s_row, s_col, nan_rows, token_idx, slot_idx, src_rank, weight);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* topk_idx, int idx_dtype,
+                               const void* topk_w, int w_dtype, int64_t T, int64_t K, int grid, void* out,
+                               int out_dtype, int64_t ldo, int32_t* slot_map, void* stream) {
+  const char* fn = "ntlb_ep_combine";
+  if (n < 0 || n > 0x7FFFFFFF || T < 0 || K < 1 || K > EP_COMBINE_MAX_K || H <= 0 || H % 8 != 0 || ldo < H)
+    return fail(NTLB_EINVAL, "%s: bad shape (H %% 8 == 0, 1 <= K <= %d, ldo >= H)", fn, EP_COMBINE_MAX_K);
+  if ((idx_dtype != 0 && idx_dtype != 1) || !valid_dtype(w_dtype) || !valid_dtype(out_dtype) ||
+      (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3))
+    return fail(NTLB_EINVAL, "%s: bad dtype or grid", fn);
+  if (T == 0) return NTLB_OK;
+  if (!topk_idx || !topk_w || !out || !slot_map || (n > 0 && !records)) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (n > 0 && !aligned(records, 16)) return fail(NTLB_EINVAL, "%s: records must be 16-byte aligned", fn);
+  if (T * K > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
+  const int64_t R = ntlb_ep_record_bytes(H);
+  const int64_t s_off = (H + 127) / 128 * 128;
+  hipStream_t st = as_stream(stream);
+  ep_slot_fill_kernel<<<(unsigned)cdiv(T * K, 256), 256, 0, st>>>(slot_map, T * K);
+  if (n > 0)
+    ep_slot_scatter_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(records, n, R, R - 32, T, (int)K, slot_map);
+  const int vec = aligned(out, 16) && ldo % 8 == 0;
+  auto launch = [&](auto gridc, auto outc) {
+    ep_combine_kernel<decltype(gridc)::value, decltype(outc)::value><<<(unsigned)T, 256, 0, st>>>(
+        records, n, R, s_off, H, slot_map, topk_idx, idx_dtype, topk_w, w_dtype, (int)K, out, ldo, vec);
+  };
+  using I = std::integral_constant<int, GRID_INT>;
+  using E = std::integral_constant<int, GRID_E4M3>;
+  using B = std::integral_constant<int, DT_BF16>;
+  using F = std::integral_constant<int, DT_F32>;
+  using Hh = std::integral_constant<int, DT_F16>;
+  if (grid == NTLB_GRID_E4M3) {
+    if (out_dtype == NTLB_BF16) launch(E(), B()); else if (out_dtype == NTLB_F32) launch(E(), F()); else launch(E(), Hh());
+  } else {
+    if (out_dtype == NTLB_BF16) launch(I(), B()); else if (out_dtype == NTLB_F32) launch(I(), F()); else launch(I(), Hh());
+  }
   return check_launch(fn);
 }

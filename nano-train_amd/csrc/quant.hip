@@ -1307,40 +1307,90 @@ __global__ void __launch_bounds__(256) ep_meta_kernel(uint8_t* rec, int64_t R, i
   *reinterpret_cast<int4*>(m + 4) = make_int4(__float_as_int(w), 0, 0, 0);
 }
 
-extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
-                                    const int32_t* pos, const void* topk_idx, int idx_dtype, const void* topk_w,
-                                    int w_dtype, int64_t K, int64_t experts_per_rank, int grid, int qmax,
-                                    int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
-                                    void* stream) {
-  const char* fn = "ntlb_ep_pack_records";
-  if (K < 1 || experts_per_rank < 1 || T < 0 || (idx_dtype != 0 && idx_dtype != 1) || !valid_dtype(w_dtype))
-    return fail(NTLB_EINVAL, "%s: bad argument", fn);
-  const int64_t A = T * K;
-  if (A > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
-  int rc = check_common(fn, tokens, x_dtype, T, H, ldt, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
-  if (rc) return rc;
-  if (A == 0 || H == 0) return NTLB_OK;
-  if (!pos || !topk_idx || !topk_w || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+// Return records (the expert side of the combine, moe.py:926-962): row i of
+// the expert outputs goes to record p = pos[i] with token_idx[i], slot_idx[i],
+// the optional local expert and weight, and the NaN flag cleared.
+__global__ void __launch_bounds__(256) ep_meta_rows_kernel(uint8_t* rec, int64_t R, int64_t m_off, int64_t n,
+                                                           const int32_t* pos, const int32_t* token_idx,
+                                                           const int32_t* slot_idx, const int32_t* local_expert,
+                                                           const float* weight) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t p = min<int64_t>(max<int32_t>(pos[i], 0), n - 1);
+  int32_t* m = reinterpret_cast<int32_t*>(rec + p * R + m_off);
+  *reinterpret_cast<int4*>(m) = make_int4(token_idx[i], slot_idx[i], local_expert ? local_expert[i] : 0, 0);
+  *reinterpret_cast<int4*>(m + 4) = make_int4(weight ? __float_as_int(weight[i]) : 0, 0, 0, 0);
+}
+
+// Records quantized with the reference's comm-quant scales (moe.py:93-140):
+// one scale per gc-column group over all rows, from the group amaxes of
+// ntlb_amax_grouped, each element through the same quant_one as
+// quant_grouped_kernel.  A thread takes 8 columns of one input row (zero past
+// K, up to the record's whole tiles Hp) and writes them to the fan_k records
+// fan_pos[r * fan_k + f], each with its own SR bits (element index p*K + col).
+template <int IN_DT, int GRID, bool SR>
+__global__ void __launch_bounds__(256) ep_pack_grouped_kernel(QuantArgs a, const uint32_t* amax_bits, int64_t gc,
+                                                              int64_t n_gc, int64_t Hp) {
+  const int64_t cpr = Hp >> 3;
+  const int64_t total = a.R * cpr;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+    const int64_t r = c / cpr;
+    const int64_t k0 = (c - r * cpr) * 8;
+    float v[8];
+    load8<IN_DT, true>(a.x, r * a.ldx, k0, a.K, v);
+    // a group spans whole tiles (gc % 128 == 0) or all columns (n_gc == 1)
+    const float s = scale_from_amax_bits(amax_bits[min<int64_t>(k0 / gc, n_gc - 1)], a.qmaxf, a.scale_rule);
+    for (int64_t f = 0; f < a.fan_k; ++f) {
+      const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + f], 0), a.fan_rows - 1);
+      uint32_t rb[8];
+      sr_words<SR>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
+      uint32_t cb[8];
+      float q[8];
+      bool nan = false;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        cb[i] = quant_one<GRID, SR>(v[i], s, a.qmaxf, rb[i], q[i]);
+        nan |= (__float_as_uint(q[i]) & 0x7FFFFFFFu) > 0x7F800000u;
+      }
+      const uint32_t lo = cb[0] | (cb[1] << 8) | (cb[2] << 16) | (cb[3] << 24);
+      const uint32_t hi = cb[4] | (cb[5] << 8) | (cb[6] << 16) | (cb[7] << 24);
+      *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo, hi);
+      if ((k0 & 127) == 0) a.scales[p * a.s_row + (k0 >> 7)] = s;
+      if (nan && a.nan_rows) atomicOr(a.nan_rows + p * a.nan_stride, 1);
+    }
+  }
+}
+
+// Shared by the dispatch and return packs: rows x [n_in, H] quantized into
+// records (codes, tile scales, NaN flag; the metadata kernels run first),
+// input row r going to the fan_k records fan_pos[r * fan_k + f].
+static int ep_pack_payload(const char* fn, const void* x, int x_dtype, int64_t n_in, int64_t H, int64_t ldx,
+                           const int32_t* fan_pos, int64_t fan_k, int64_t n_rec, const uint32_t* amax_bits,
+                           int64_t gc, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                           uint64_t offset, uint8_t* records, hipStream_t st) {
   const int64_t R = ntlb_ep_record_bytes(H);
   const int64_t s_off = (H + 127) / 128 * 128, m_off = R - 32;
   const int64_t Tt = cdiv(H, 128);
-  const bool vec = aligned(tokens, 16) && ((ldt * dtype_size(x_dtype)) % 16 == 0);
-  if (!(vec && H % 8 == 0 && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) && aligned(records, 16) &&
-        cdiv(Tt, TILE_TU) <= 65535))
-    return fail(NTLB_EUNSUPPORTED, "%s: needs bf16/fp32 tokens, H %% 8 == 0, 16-byte aligned rows and records", fn);
-  hipStream_t st = as_stream(stream);
-  ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, m_off, A, pos, topk_idx, idx_dtype, topk_w,
-                                                          w_dtype, K, experts_per_rank);
-  // one token row read, quantized, and written to its K records
-  QuantArgs a = make_args(tokens, T, H, ldt, grid, qmax, scale_rule, seed, offset, records, R,
+  QuantArgs a = make_args(x, n_in, H, ldx, grid, qmax, scale_rule, seed, offset, records, R,
                           reinterpret_cast<float*>(records + s_off), R / 4, 1, nullptr, 0, 0,
                           reinterpret_cast<int32_t*>(records + m_off + 12));
-  a.fan_pos = pos;
-  a.fan_k = K;
-  a.fan_rows = A;
+  a.fan_pos = fan_pos;
+  a.fan_k = fan_k;
+  a.fan_rows = n_rec;
   a.nan_stride = R / 4;
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
-  const int64_t n_rb = cdiv(T, 16), n_tg = cdiv(Tt, TILE_TU);
+  if (amax_bits) {
+    dim3 grd(grid_for(n_in * (s_off >> 3), 256, 256 * 16)), blk(256);
+    const int64_t n_gc = cdiv(H, gc);
+    NTLB_DISPATCH_GRID_SR(grid, sr, {
+      if (x_dtype == NTLB_BF16)
+        ep_pack_grouped_kernel<DT_BF16, G_, S_><<<grd, blk, 0, st>>>(a, amax_bits, gc, n_gc, s_off);
+      else
+        ep_pack_grouped_kernel<DT_F32, G_, S_><<<grd, blk, 0, st>>>(a, amax_bits, gc, n_gc, s_off);
+    });
+    return check_launch(fn);
+  }
+  const int64_t n_rb = cdiv(n_in, 16), n_tg = cdiv(Tt, TILE_TU);
   int64_t gx = n_rb;
   if (NTLB_TILE_PIPELINE) {
     gx = cdiv(n_rb, 4);
@@ -1354,4 +1404,76 @@ extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, 
       quant_tile_1x128_fast<DT_F32, G_, S_, false, true><<<fgrd, fblk, 0, st>>>(a);
   });
   return check_launch(fn);
+}
+
+static int ep_check_payload(const char* fn, const void* x, int x_dtype, int64_t H, int64_t ldx,
+                            const uint32_t* amax_bits, int64_t gc, const uint8_t* records) {
+  const bool vec = aligned(x, 16) && ((ldx * dtype_size(x_dtype)) % 16 == 0);
+  if (!(vec && H % 8 == 0 && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) && aligned(records, 16) &&
+        cdiv(cdiv(H, 128), TILE_TU) <= 65535))
+    return fail(NTLB_EUNSUPPORTED, "%s: needs bf16/fp32 rows, H %% 8 == 0, 16-byte aligned rows and records", fn);
+  if (amax_bits && (gc < 1 || (gc % 128 != 0 && gc < H)))
+    return fail(NTLB_EINVAL, "%s: a scale group spans whole 128-column tiles (gc %% 128 == 0) or all H columns", fn);
+  return NTLB_OK;
+}
+
+extern "C" int ntlb_ep_pack_records_grouped(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
+                                            const int32_t* pos, const void* topk_idx, int idx_dtype,
+                                            const void* topk_w, int w_dtype, int64_t K, int64_t experts_per_rank,
+                                            const uint32_t* amax_bits, int64_t gc, int grid, int qmax, int rounding,
+                                            int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
+                                            void* stream) {
+  const char* fn = "ntlb_ep_pack_records";
+  if (K < 1 || experts_per_rank < 1 || T < 0 || (idx_dtype != 0 && idx_dtype != 1) || !valid_dtype(w_dtype))
+    return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  const int64_t A = T * K;
+  if (A > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
+  int rc = check_common(fn, tokens, x_dtype, T, H, ldt, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (A == 0 || H == 0) return NTLB_OK;
+  if (!pos || !topk_idx || !topk_w || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  rc = ep_check_payload(fn, tokens, x_dtype, H, ldt, amax_bits, gc, records);
+  if (rc) return rc;
+  const int64_t R = ntlb_ep_record_bytes(H);
+  hipStream_t st = as_stream(stream);
+  ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, R - 32, A, pos, topk_idx, idx_dtype, topk_w,
+                                                          w_dtype, K, experts_per_rank);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  // each token row read once, quantized, and written to its K records
+  return ep_pack_payload(fn, tokens, x_dtype, T, H, ldt, pos, K, A, amax_bits, gc, grid, qmax, rounding, scale_rule,
+                         seed, offset, records, st);
+}
+
+extern "C" int ntlb_ep_pack_records(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
+                                    const int32_t* pos, const void* topk_idx, int idx_dtype, const void* topk_w,
+                                    int w_dtype, int64_t K, int64_t experts_per_rank, int grid, int qmax,
+                                    int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
+                                    void* stream) {
+  return ntlb_ep_pack_records_grouped(tokens, x_dtype, T, H, ldt, pos, topk_idx, idx_dtype, topk_w, w_dtype, K,
+                                      experts_per_rank, nullptr, 0, grid, qmax, rounding, scale_rule, seed, offset,
+                                      records, stream);
+}
+
+extern "C" int ntlb_ep_pack_return(const void* x, int x_dtype, int64_t n, int64_t H, int64_t ldx, const int32_t* pos,
+                                   const int32_t* token_idx, const int32_t* slot_idx, const int32_t* local_expert,
+                                   const float* weight, const uint32_t* amax_bits, int64_t gc, int grid, int qmax,
+                                   int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
+                                   void* stream) {
+  const char* fn = "ntlb_ep_pack_return";
+  if (n < 0 || n > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: need 0 <= n < 2^31", fn);
+  int rc = check_common(fn, x, x_dtype, n, H, ldx, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (n == 0 || H == 0) return NTLB_OK;
+  if (!pos || !token_idx || !slot_idx || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  rc = ep_check_payload(fn, x, x_dtype, H, ldx, amax_bits, gc, records);
+  if (rc) return rc;
+  const int64_t R = ntlb_ep_record_bytes(H);
+  hipStream_t st = as_stream(stream);
+  ep_meta_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(records, R, R - 32, n, pos, token_idx, slot_idx,
+                                                               local_expert, weight);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  return ep_pack_payload(fn, x, x_dtype, n, H, ldx, pos, 1, n, amax_bits, gc, grid, qmax, rounding, scale_rule, seed,
+                         offset, records, st);
 }

@@ -12,12 +12,16 @@ all_to_all, and the receiver hands the codes to the grouped GEMM without a
 dequantize/re-quantize round trip.
 
   pack_dispatch     sender: destination order + records (kernels ntlb_ep_partition,
-                    ntlb_ep_pack_records)
+                    ntlb_ep_pack_records_grouped)
   exchange          the two all_to_alls (torch.distributed; one process per GPU)
   unpack_dispatch   receiver: rows grouped by local expert in arrival order, as
                     _run_local_experts selects them (moe.py:905-923), as a QTensor
                     for ops.gemm_grouped_blockscaled plus the metadata of
                     _DispatchedTokens (moe.py:49-58)
+  pack_return       expert side of the combine: the expert outputs as records
+                    back to their source ranks (ntlb_ep_pack_return)
+  combine           source side: the returned records summed into the token
+                    outputs with the routing weights (ntlb_ep_combine)
 
 Capacity dropping (moe.py:919-923) keeps the top-capacity rows of an expert by
 routing weight: capacity_order selects them, and unpack_dispatch gathers that
@@ -33,6 +37,7 @@ from typing import List, Optional, Sequence
 import torch
 
 from . import ops
+from . import _lib
 from ._lib import call, lib
 from .ops import QTensor, cdiv
 
@@ -77,16 +82,52 @@ class SendBuffer:
     H: int
 
 
+def _payload_mode(granularity: Optional[str], fmt: Optional[str], scale_rule: Optional[int], H: int):
+    """(grid code, scale rule, group columns or None) of a record payload.
+
+    granularity None: per-row 1x128 tiles (fmt e4m3 by default).  Otherwise
+    the reference's comm-quant granularity (moe.py:107-140): tile_1x128 and
+    block_128x128 give one scale per 128-column strip over all rows, tensor
+    one scale; the reference quantizes on the int grid with the scale rule
+    that checks the amax before dividing."""
+    if granularity is None:
+        return ops.grid_code(fmt or "e4m3"), (0 if scale_rule is None else scale_rule), None
+    if granularity in ("tile_1x128", "block_128x128"):
+        gc = 128
+    elif granularity == "tensor":
+        gc = H
+    else:
+        raise ValueError(f"granularity {granularity!r}: a record carries one scale per 128-column tile, which "
+                         "holds tile_1x128 / block_128x128 strips and tensor scales, not per-channel ones")
+    rule = _lib.SCALE_BEFORE_DIVIDE if scale_rule is None else scale_rule
+    return ops.grid_code(fmt or "int_grid"), rule, gc
+
+
+def _group_amax(x: torch.Tensor, gc: Optional[int]):
+    """Per-group |x| maxima (int32 bits) over all rows of x [n, H], or None."""
+    if gc is None or x.shape[0] == 0:
+        return None
+    n, H = x.shape
+    amax = torch.zeros(cdiv(H, gc), dtype=torch.int32, device=x.device)
+    call("ntlb_amax_grouped", x.data_ptr(), ops._dtype_code(x.dtype), n, H, x.stride(0), n, gc, amax.data_ptr(),
+         ops._stream())
+    return amax
+
+
 def pack_dispatch(tokens: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, *, experts_per_rank: int,
-                  ep_size: int, fmt: str = "e4m3", bits: int = 8, rounding: str = "nearest", seed: int = 0,
-                  offset: int = 0, scale_rule: int = 0) -> SendBuffer:
+                  ep_size: int, fmt: Optional[str] = None, bits: int = 8, rounding: str = "nearest", seed: int = 0,
+                  offset: int = 0, scale_rule: Optional[int] = None, granularity: Optional[str] = None) -> SendBuffer:
     """The send side of _dispatch_tokens (moe.py:795-814) as records.
 
     Assignment a = t*K + k goes to rank topk_idx[t, k] // experts_per_rank;
     within a rank, assignments keep their order (the reference's boolean
-    masks).  Each record carries token t's row quantized per 1x128 tile with
-    the stochastic-rounding element index p*H + column of its send position
-    p, and (t, k, local expert, weight)."""
+    masks).  Each record carries token t's row quantized with the
+    stochastic-rounding element index p*H + column of its send position p,
+    and (t, k, local expert, weight).  The payload is per-row 1x128 tiles
+    (granularity None, e4m3 by default), or the reference's own comm-quant of
+    the send buffer (granularity tile_1x128 / block_128x128 / tensor: int-grid
+    codes with strip or tensor scales, the codes and scales
+    _comm_quant_dequant computes)."""
     ops._require_device(tokens, topk_idx, topk_w)
     if tokens.dim() != 2 or topk_idx.shape != topk_w.shape or topk_idx.dim() != 2 \
             or topk_idx.shape[0] != tokens.shape[0]:
@@ -97,13 +138,15 @@ def pack_dispatch(tokens: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Te
     w = topk_w.contiguous()
     if tokens.stride(-1) != 1 or tokens.stride(0) % 8 or tokens.data_ptr() % 16:
         tokens = tokens.contiguous()
+    grid, rule, gc = _payload_mode(granularity, fmt, scale_rule, H)
     pos, _, counts, _ = partition(idx, divisor=experts_per_rank, buckets=ep_size)
     R, _, _ = record_layout(H)
     records = torch.empty((T * K, R), dtype=torch.uint8, device=tokens.device)
-    call("ntlb_ep_pack_records", tokens.data_ptr(), ops._dtype_code(tokens.dtype), T, H, tokens.stride(0),
+    amax = _group_amax(tokens, gc)
+    call("ntlb_ep_pack_records_grouped", tokens.data_ptr(), ops._dtype_code(tokens.dtype), T, H, tokens.stride(0),
          pos.data_ptr(), idx.data_ptr(), KEY_INT64 if idx.dtype == torch.int64 else KEY_INT32, w.data_ptr(),
-         ops._dtype_code(w.dtype), K, experts_per_rank, ops.grid_code(fmt), (1 << (bits - 1)) - 1,
-         ops.rounding_code(rounding), scale_rule, seed, offset, records.data_ptr(), ops._stream())
+         ops._dtype_code(w.dtype), K, experts_per_rank, None if amax is None else amax.data_ptr(), gc or 0, grid,
+         (1 << (bits - 1)) - 1, ops.rounding_code(rounding), rule, seed, offset, records.data_ptr(), ops._stream())
     return SendBuffer(records, counts, H)
 
 
@@ -184,6 +227,61 @@ def unpack_dispatch(records: torch.Tensor, recv_counts: Sequence[int], *, H: int
          token_idx.data_ptr(), slot_idx.data_ptr(), src_rank.data_ptr(), weight.data_ptr(), ops._stream())
     q = QTensor(codes, scales, 1, rp, 0, ops.grid_code(fmt), rows, H, nan_rows)
     return ExpertRows(q, offsets, counts, token_idx, slot_idx, src_rank, weight, order)
+
+
+def pack_return(expert_out: torch.Tensor, rows: ExpertRows, *, ep_size: int, fmt: Optional[str] = None, bits: int = 8,
+                rounding: str = "nearest", seed: int = 0, offset: int = 0, scale_rule: Optional[int] = None,
+                granularity: Optional[str] = None) -> SendBuffer:
+    """The expert side of the combine (moe.py:926-962) as records: row i of
+    expert_out [n, H] (the rows of `rows`, in their order) goes back to rank
+    rows.src_rank[i]; each destination's records keep the rows' order, which
+    is expert order as send_back_features_parts builds it.  Records carry
+    (token, slot, weight) and the payload as in pack_dispatch (granularity:
+    the reference's comm-quant of send_back_features, over all n rows)."""
+    ops._require_device(expert_out)
+    if expert_out.dim() != 2 or expert_out.shape[0] != rows.token_idx.numel():
+        raise ValueError("expert_out must be [rows, H], one row per received row")
+    n, H = expert_out.shape
+    if expert_out.stride(-1) != 1 or expert_out.stride(0) % 8 or expert_out.data_ptr() % 16:
+        expert_out = expert_out.contiguous()
+    grid, rule, gc = _payload_mode(granularity, fmt, scale_rule, H)
+    dev = expert_out.device
+    src = rows.src_rank.to(dtype=torch.int32).contiguous()
+    pos, _, counts, _ = _partition(src.data_ptr(), KEY_INT32, 4, n, 1, ep_size, dev)
+    R, _, _ = record_layout(H)
+    records = torch.empty((n, R), dtype=torch.uint8, device=dev)
+    amax = _group_amax(expert_out, gc)
+    call("ntlb_ep_pack_return", expert_out.data_ptr(), ops._dtype_code(expert_out.dtype), n, H, expert_out.stride(0),
+         pos.data_ptr(), rows.token_idx.data_ptr(), rows.slot_idx.data_ptr(), None, rows.weight.data_ptr(),
+         None if amax is None else amax.data_ptr(), gc or 0, grid, (1 << (bits - 1)) - 1,
+         ops.rounding_code(rounding), rule, seed, offset, records.data_ptr(), ops._stream())
+    return SendBuffer(records, counts, H)
+
+
+def combine(records: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, *, H: int, fmt: str = "e4m3",
+            out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """The source side of the combine (moe.py:1021-1027): the returned
+    records summed into the token outputs [T, H] with their routing weights,
+    as index_add_ into zeros sums them on the CPU (each product rounded to
+    out_dtype, the products added in fp32 in ascending expert id per token,
+    the sum rounded once).  fmt names the records'
+    code grid (int_grid for the reference's comm-quant granularities)."""
+    ops._require_device(records, topk_idx, topk_w)
+    R, _, _ = record_layout(H)
+    if records.dim() != 2 or records.shape[1] != R or records.dtype != torch.uint8:
+        raise ValueError(f"records must be uint8 [n, {R}]")
+    if topk_idx.dim() != 2 or topk_idx.shape != topk_w.shape:
+        raise ValueError("topk_idx and topk_w [T, K]")
+    T, K = topk_idx.shape
+    idx = topk_idx.contiguous()
+    w = topk_w.contiguous()
+    records = records.contiguous()
+    out = torch.empty((T, H), dtype=out_dtype, device=records.device)
+    slot_map = torch.empty(max(T * K, 1), dtype=torch.int32, device=records.device)
+    call("ntlb_ep_combine", records.data_ptr(), records.shape[0], H, idx.data_ptr(),
+         KEY_INT64 if idx.dtype == torch.int64 else KEY_INT32, w.data_ptr(), ops._dtype_code(w.dtype), T, K,
+         ops.grid_code(fmt), out.data_ptr(), ops._dtype_code(out_dtype), H, slot_map.data_ptr(), ops._stream())
+    return out
 
 
 def capacity_order(rows: ExpertRows, capacity: int):

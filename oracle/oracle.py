@@ -373,3 +373,29 @@ def ep_expert_order(local_expert: np.ndarray, local_experts: int):
     ((recv_local_expert_idx == e).nonzero(), moe.py:905-909)."""
     le = np.asarray(local_expert).reshape(-1)
     return np.concatenate([np.nonzero(le == e)[0] for e in range(local_experts)]) if le.size else np.zeros(0, np.int64)
+
+
+def ep_combine(feat: np.ndarray, token_idx: np.ndarray, slot_idx: np.ndarray, topk_idx: np.ndarray,
+               topk_w: np.ndarray, T: int, *, bf16: bool = True, per_add_rounding: bool = False) -> np.ndarray:
+    """The source side of _combine_remote_outputs (moe.py:1021-1027):
+    output_tokens = zeros; output_tokens.index_add_(0, token_idx, feat *
+    topk_w[token_idx, slot_idx]) on the CPU, with feat the returned rows in the
+    output dtype.  The product is a tensor op of the output dtype (each
+    element rounded to it); index_add_ on the CPU sums the rows in fp32 in
+    arrival order -- for one token, ascending expert id -- and rounds once
+    (bf16, or fp32 with bf16=False).  per_add_rounding rounds every partial
+    sum instead, the plausible misreading the tests rule out.  Returns fp32
+    [T, H] holding output-dtype values."""
+    rnd = round_bf16 if bf16 else (lambda v: np.asarray(v, dtype=np.float32))
+    feat = rnd(np.asarray(feat, dtype=np.float32))
+    token_idx = np.asarray(token_idx, dtype=np.int64)
+    slot_idx = np.asarray(slot_idx, dtype=np.int64)
+    w = rnd(np.asarray(topk_w, dtype=np.float32))
+    expert = np.asarray(topk_idx)[token_idx, slot_idx]
+    out = np.zeros((T, feat.shape[1]), dtype=np.float32)
+    for r in np.lexsort((expert, token_idx)):  # per token, ascending expert id
+        t = token_idx[r]
+        out[t] = out[t] + rnd(feat[r] * w[t, slot_idx[r]])
+        if per_add_rounding:
+            out[t] = rnd(out[t])
+    return rnd(out)

@@ -276,3 +276,163 @@ def test_expert_mlp_on_received_codes_equals_local_path(gpu_device):
     torch.cuda.synchronize()
     assert torch.equal(rows.token_idx.long(), token_index.long())
     assert got.dtype == want.dtype and torch.equal(got, want)
+
+
+@pytest.mark.parametrize("granularity", ["tile_1x128", "tensor"])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+@pytest.mark.parametrize("H", [1024, 200])
+def test_pack_records_with_reference_comm_quant(gpu_device, granularity, rounding, H):
+    """granularity mode: the records hold exactly the codes and the strip (or
+    tensor) scales of the reference's _comm_quant_dequant applied to the send
+    buffer (moe.py:79-143: int grid, qmax 127, amax checked before dividing).
+    The receiver's bf16(q * s) equals the value the reference puts on the
+    wire, tensor + (dq - tensor) in bf16, except for the sign of zero and for
+    elements where dq - tensor is inexact in bf16 (then one bf16 ulp)."""
+    from lowbit import ep
+
+    T, K, epr, ep_size = 96, 4, 3, 4
+    x = seeded((T, H), seed=20261270, outliers=0.01).to(gpu_device)
+    x[11, 3] = float("nan")
+    idx, w = _routing(T, K, epr * ep_size, 20261271)
+    send = ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=epr, ep_size=ep_size,
+                            granularity=granularity, rounding=rounding, seed=77, offset=5)
+    torch.cuda.synchronize()
+    order, counts = O.ep_send_order(idx.numpy(), epr, ep_size)
+    assert send.counts.cpu().numpy().tolist() == counts.tolist()
+    codes, scales, meta, weight, _ = _decode(send.records.cpu().numpy(), H)
+    send_rows = to_np32(x)[order // K]
+    gc = 128 if granularity == "tile_1x128" else H
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    c_ref, s_ref, q_ref, _ = O.quant_grouped(send_rows, len(order), gc, grid=O.GRID_INT, rounding=rc,
+                                             scale_rule=O.SCALE_BEFORE_DIVIDE, seed=77, offset=5)
+    assert_bits_equal(codes, c_ref, "record codes")
+    Tt = -(-H // 128)
+    tile_scale = s_ref[0, np.minimum(np.arange(Tt) * 128 // gc, s_ref.shape[1] - 1)]
+    assert_bits_equal(scales, np.broadcast_to(tile_scale, scales.shape), "record scales")
+    assert np.array_equal(meta[:, 3], np.isnan(send_rows).any(axis=1).astype(np.int32)), "NaN flags"
+    # the receiver's value against the reference's wire value
+    got = O.round_bf16(O.decode_codes(codes, O.GRID_INT) * np.repeat(scales, 128, axis=1)[:, :H])
+    t = torch.from_numpy(send_rows).to(torch.bfloat16)
+    dq = torch.from_numpy(q_ref * np.repeat(s_ref, gc, axis=1)[:, :H]).to(torch.bfloat16)
+    want = (t + (dq - t)).float().numpy()
+    both_nan = np.isnan(got) & np.isnan(want)
+    same = (got == want) | both_nan
+    assert np.isnan(got).sum() == np.isnan(want).sum()
+    bits_g = O.to_bf16_bits(got[~same]).astype(np.int32)
+    bits_w = O.to_bf16_bits(want[~same]).astype(np.int32)
+    assert np.all(np.abs(bits_g - bits_w) == 1), "differences beyond one bf16 ulp"
+    # stochastic rounding also rounds up values far below half a step, where
+    # dq - tensor needs more bits than bf16 holds; nearest rarely does
+    limit = 1e-2 if rounding == "stochastic" else 1e-3
+    assert (~same).mean() < limit, f"{(~same).sum()} of {same.size} elements differ by one ulp"
+
+
+@pytest.mark.parametrize("mode", ["row_e4m3", "strip_int"])
+@pytest.mark.parametrize("capacity", [0, 7])
+def test_return_and_combine_round_trip(gpu_device, mode, capacity):
+    """Dispatch between 3 emulated ranks, synthetic expert outputs, the return
+    records (their codes and scales against the oracle quantizer of the
+    send-back buffer in the reference's order), the emulated return exchange,
+    and the combine at every source rank bit-exact against the reference's
+    index_add_ on the CPU over the rows the records carry, in arrival order."""
+    from lowbit import ep
+
+    ep_size, epr, H, K = 3, 2, 384, 3
+    tokens = [50, 0, 37]
+    gran = None if mode == "row_e4m3" else "tile_1x128"
+    fmt = "e4m3" if mode == "row_e4m3" else "int_grid"
+    xs, idxs, ws, sends, recv = _emulated_exchange(ep_size, epr, H, tokens, K, 20261280, gpu_device)
+    ws = [w.to(torch.bfloat16) for w in ws]  # the routing weights in the tokens' dtype, as the reference has them
+    back = []  # per expert rank: the return records and their counts per source rank
+    for r in range(ep_size):
+        records, counts = recv[r]
+        rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr)
+        if capacity:
+            order, kept = ep.capacity_order(rows, capacity)
+            rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr, order=order, order_counts=kept)
+        out_rows = seeded((rows.token_idx.numel(), H), seed=20261290 + r, std=2.0).to(gpu_device)
+        sb = ep.pack_return(out_rows, rows, ep_size=ep_size, granularity=gran, fmt=fmt, seed=9, offset=r)
+        torch.cuda.synchronize()
+        # the reference's send-back order: per source rank, rows in expert (row) order
+        src = rows.src_rank.cpu().numpy()
+        ret_order = np.concatenate([np.nonzero(src == s)[0] for s in range(ep_size)])
+        assert sb.counts.cpu().numpy().tolist() == np.bincount(src, minlength=ep_size).tolist()
+        c, sc, meta, wt, _ = _decode(sb.records.cpu().numpy(), H)
+        ref_rows = to_np32(out_rows)[ret_order]
+        if gran is None:
+            c_ref, s_ref, _, _ = O.quant_tile_1x128(ref_rows, grid=O.GRID_E4M3, seed=9, offset=r)
+            assert_bits_equal(sc, s_ref, "return scales")
+        else:
+            c_ref, s_ref, _, _ = O.quant_grouped(ref_rows, len(ret_order), 128, grid=O.GRID_INT,
+                                                 scale_rule=O.SCALE_BEFORE_DIVIDE, seed=9, offset=r)
+            assert_bits_equal(sc, np.broadcast_to(s_ref[0], sc.shape), "return scales")
+        assert_bits_equal(c[:, :H], c_ref[:, :H], "return codes")
+        assert np.array_equal(meta[:, 0], rows.token_idx.cpu().numpy()[ret_order]), "token index"
+        assert np.array_equal(meta[:, 1], rows.slot_idx.cpu().numpy()[ret_order]), "slot"
+        back.append((sb.records, sb.counts.cpu().tolist()))
+    for s in range(ep_size):
+        # all_to_all_single back: source s receives, from each expert rank in order, that rank's slice for s
+        parts = []
+        for r in range(ep_size):
+            rec, cnt = back[r]
+            start = sum(cnt[:s])
+            parts.append(rec[start:start + cnt[s]])
+        got_rec = torch.cat(parts)
+        T = tokens[s]
+        out = ep.combine(got_rec, idxs[s].to(gpu_device), ws[s].to(gpu_device), H=H, fmt=fmt)
+        torch.cuda.synchronize()
+        assert out.shape == (T, H) and out.dtype == torch.bfloat16
+        c, sc, meta, _, _ = _decode(got_rec.cpu().numpy(), H)
+        feat = O.round_bf16(O.decode_codes(c[:, :H], O.GRID_E4M3 if gran is None else O.GRID_INT)
+                            * np.repeat(sc, 128, axis=1)[:, :H])
+        tok = torch.from_numpy(meta[:, 0].astype(np.int64))
+        slot = torch.from_numpy(meta[:, 1].astype(np.int64))
+        ref = torch.zeros((T, H), dtype=torch.bfloat16)
+        if len(tok):
+            ref.index_add_(0, tok, torch.from_numpy(feat).to(torch.bfloat16) * ws[s][tok, slot].unsqueeze(-1))
+        assert_bits_equal(out.float().cpu().numpy(), ref.float().numpy(), "combined tokens")
+        if T:
+            assert_bits_equal(out.float().cpu().numpy(),
+                              O.ep_combine(feat, meta[:, 0], meta[:, 1], idxs[s].numpy(), ws[s].float().numpy(), T),
+                              "combined tokens (oracle)")
+
+
+def test_combine_without_records_is_zero(gpu_device):
+    """Tokens none of whose assignments came back (all dropped) stay zero, as
+    index_add_ into zeros leaves them."""
+    from lowbit import ep
+
+    R, _, _ = ep.record_layout(256)
+    idx, w = _routing(5, 2, 4, 20261300)
+    out = ep.combine(torch.empty((0, R), dtype=torch.uint8, device=gpu_device), idx.to(gpu_device),
+                     w.to(gpu_device, torch.bfloat16), H=256)
+    torch.cuda.synchronize()
+    assert out.shape == (5, 256) and not out.float().abs().sum().item()
+    assert not torch.signbit(out.float()).any()
+
+
+@pytest.mark.parametrize("fmt,grid", [("e4m3", O.GRID_E4M3), ("int_grid", O.GRID_INT)])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_combine_decodes_every_code(gpu_device, fmt, grid, out_dtype):
+    """All 256 codes through the combine's decode (scale 1, weight 1, a
+    second all-zero record for the same token): the output is each code's
+    value added to zero, NaN codes included."""
+    from lowbit import ep
+
+    H = 256
+    R, s_off, m_off = ep.record_layout(H)
+    rec = np.zeros((2, R), dtype=np.uint8)
+    rec[0, :H] = np.arange(256, dtype=np.uint8)
+    rec[:, s_off:s_off + 8] = np.frombuffer(np.array([1.0, 1.0], dtype=np.float32).tobytes(), dtype=np.uint8)
+    rec[:, m_off:m_off + 8] = np.frombuffer(np.array([[0, 0], [0, 1]], dtype=np.int32).tobytes(),
+                                            dtype=np.uint8).reshape(2, 8)
+    idx = torch.tensor([[3, 1]], dtype=torch.int64)
+    w = torch.ones((1, 2), dtype=out_dtype)
+    out = ep.combine(torch.from_numpy(rec).to(gpu_device), idx.to(gpu_device), w.to(gpu_device), H=H, fmt=fmt,
+                     out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    want = O.decode_codes(np.arange(256, dtype=np.uint8), grid).astype(np.float32)
+    if out_dtype == torch.bfloat16:
+        want = O.round_bf16(want)
+    want = np.float32(0.0) + want  # the sum starts from zero: -0 comes out as +0, as from index_add_ into zeros
+    assert_bits_equal(out.float().cpu().numpy()[0], want, "decoded codes")

@@ -412,3 +412,33 @@ def test_ep_dispatch_oracle_hand_example():
     # local expert 0 first, each in arrival order
     assert O.ep_expert_order(r0["local_expert"], 2).tolist() == [0, 2, 4, 1, 3]
     assert O.ep_expert_order(r1["local_expert"], 2).tolist() == [1, 3, 0, 2, 4]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_ep_combine_oracle_matches_torch_index_add(dtype):
+    """The combine oracle against the reference's own op: index_add_ into
+    zeros on the CPU (moe.py:1021-1027) over returned rows in the order an
+    expert-parallel exchange delivers them (expert id major, then token), with
+    some assignments dropped by a capacity limit."""
+    g = torch.Generator().manual_seed(20261260)
+    T, K, E, H = 40, 4, 8, 64
+    topk = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    w = torch.rand((T, K), generator=g).to(dtype)
+    tok = torch.arange(T).repeat_interleave(K)
+    slot = torch.arange(K).repeat(T)
+    keep = torch.rand(T * K, generator=g) > 0.15
+    expert = topk.reshape(-1)
+    arrival = sorted([i for i in range(T * K) if keep[i]], key=lambda i: (int(expert[i]), int(tok[i])))
+    tok_a, slot_a = tok[arrival], slot[arrival]
+    feat = (torch.randn((len(arrival), H), generator=g) * 3).to(dtype)
+    ref = torch.zeros((T, H), dtype=dtype)
+    ref.index_add_(0, tok_a, feat * w[tok_a, slot_a].unsqueeze(-1))
+    got = O.ep_combine(feat.float().numpy(), tok_a.numpy(), slot_a.numpy(), topk.numpy(), w.float().numpy(), T,
+                       bf16=dtype == torch.bfloat16)
+    want = ref.float().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a plausible misreading -- rounding every partial sum to bf16 -- differs
+    if dtype == torch.bfloat16:
+        loose = O.ep_combine(feat.float().numpy(), tok_a.numpy(), slot_a.numpy(), topk.numpy(), w.float().numpy(), T,
+                             per_add_rounding=True)
+        assert not np.array_equal(loose.view(np.uint32), want.view(np.uint32))
