@@ -126,19 +126,22 @@ def other_config(args) -> dict:
         qx_t = ops.quant_tile_128x1_t(x, fmt=fmt)
         _, qw_t = ops.quant_block_128x128(w, fmt=fmt, want_transposed=True)
         t = {}
-        t["dy_1x128_us"] = _time_ms(lambda i: ops.quant_tile_1x128(dy, fmt=fmt), args.steps, args.warmup, st) * 1e3
-        t["dy_128x1_us"] = _time_ms(lambda i: ops.quant_tile_128x1_t(dy, fmt=fmt), args.steps, args.warmup, st) * 1e3
-        t["dy_dual_us"] = _time_ms(lambda i: ops.quant_dual_1x128_128x1(dy, fmt=fmt), args.steps, args.warmup,
-                                   st) * 1e3
-        qdy = ops.quant_tile_1x128(dy, fmt=fmt)
-        qdy_t = ops.quant_tile_128x1_t(dy, fmt=fmt)
+        rnd = dict(rounding=args.rounding, seed=3)  # the recipe's dY rounding (stochastic with --rounding)
+        t["dy_1x128_us"] = _time_ms(lambda i: ops.quant_tile_1x128(dy, fmt=fmt, **rnd), args.steps, args.warmup,
+                                    st) * 1e3
+        t["dy_128x1_us"] = _time_ms(lambda i: ops.quant_tile_128x1_t(dy, fmt=fmt, **rnd), args.steps, args.warmup,
+                                    st) * 1e3
+        t["dy_dual_us"] = _time_ms(lambda i: ops.quant_dual_1x128_128x1(dy, fmt=fmt, **rnd), args.steps,
+                                   args.warmup, st) * 1e3
+        qdy = ops.quant_tile_1x128(dy, fmt=fmt, **rnd)
+        qdy_t = ops.quant_tile_128x1_t(dy, fmt=fmt, **rnd)
         dg = _time_ms(lambda i: ops.gemm_blockscaled(qdy, qw_t), args.steps, args.warmup, st)
         wg = _time_ms(lambda i: ops.gemm_blockscaled(qdy_t, qx_t), args.steps, args.warmup, st)
         fl = 2.0 * M * N * K
         res.update(value=round(2 * fl / ((dg + wg) * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(dg + wg, 4),
                    dtype="fp8_e4m3" if fmt == "e4m3" else "int8",
                    config={"workload": "c3 backward GEMMs (dgrad + wgrad) of the c2 layer, fp8 recipe", "M": M,
-                           "N": N, "K": K},
+                           "N": N, "K": K, "dy_rounding": args.rounding},
                    dgrad_tflops=round(fl / (dg * 1e-3) / 1e12, 2), wgrad_tflops=round(fl / (wg * 1e-3) / 1e12, 2),
                    quantizers={k: round(v, 2) for k, v in t.items()},
                    dy_1x128_GBs=round((M * N * 3 + M * (N // 128) * 4) / t["dy_1x128_us"] / 1e3, 1),

@@ -431,7 +431,9 @@ __device__ __forceinline__ void block_quant(const Chunk8<IN_DT> (&ch)[BLK_RPT], 
   for (int w = 1; w < BLK_WAVES; ++w) m = max(m, red[w]);
   const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
   if (tid == 0) a.scales[nb * a.s_row + kb * a.s_col] = s;
-#pragma unroll
+  // fully unrolled even when the stochastic-rounding body is large: a rolled
+  // loop would index ch[] at run time and move it to scratch memory
+#pragma clang loop unroll(full)
   for (int i = 0; i < BLK_RPT; ++i) {
     const int64_t n = nb * 128 + rr + BLK_ROWS * i;
     float v[8];
@@ -807,8 +809,9 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
 
   if constexpr (DUAL) {
     // 1x128 tiles: tile cb of rows row0..row0+7; pad columns [K, ldc) get
-    // zero codes like every other 1x128 output
-#pragma unroll
+    // zero codes like every other 1x128 output (fully unrolled: c[] must stay
+    // in registers)
+#pragma clang loop unroll(full)
     for (int i = 0; i < 8; ++i) {
       const int64_t r = row0 + i;
       const int rl = rg * 8 + i;
@@ -831,12 +834,27 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
     }
   }
 
-  uint32_t rb[8][8];  // [row i][column j]
+  // SR words in two halves: columns 4h..4h+3 of every row share one Philox
+  // block (K % 8 == 0 and col0 % 8 == 0 align the element index), so only
+  // 32 words are live at a time
 #pragma unroll
-  for (int i = 0; i < 8; ++i) sr_words<SR>((uint64_t)((row0 + i) * a.K + col0), a.seed, a.offset, rb[i]);
+  for (int h = 0; h < 2; ++h) {
+  uint32_t rb[8][4];  // [row i][column j - 4h]
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (SR) {
+      const Philox4 p = philox4x32_10((((uint64_t)((row0 + i) * a.K + col0)) >> 2) + h, a.offset, a.seed);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rb[i][u] = p.v[u];
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rb[i][u] = 0;
+    }
+  }
 
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
+#pragma clang loop unroll(full)
+  for (int jj = 0; jj < 4; ++jj) {
+    const int j = 4 * h + jj;
     const int cl = cc * 8 + j;
     const int64_t col = col0 + j;
     const uint32_t mj = cm[cl];
@@ -853,7 +871,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
         const uint32_t b = (j >> 1) == 0 ? w.x : (j >> 1) == 1 ? w.y : (j >> 1) == 2 ? w.z : w.w;
         v[i] = __uint_as_float((j & 1) ? (b & 0xFFFF0000u) : (b << 16));
       }
-      rbj[i] = rb[i][j];
+      rbj[i] = rb[i][jj];
     }
     uint32_t lo, hi;
     float q[8];
@@ -870,6 +888,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
           if (row0 + i < a.R) store_elem(a.dq, a.dq_dtype, (row0 + i) * a.lddq + col, q[i] * s);
       }
     }
+  }
   }
   __syncthreads();
   // 128 transposed rows of 128 bytes (rows past R hold zero codes, inside ldct)

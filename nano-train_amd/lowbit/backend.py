@@ -186,8 +186,10 @@ def _fp8_recipe_backward(backend, dy2, x2, weight, base, needs):
     fmt, bits, rnd, seed = backend.code_format, backend.bits, backend._rounding_mode, backend.seed
     dx = dw = None
     qdy = qdyt = None
-    if needs[0] and needs[1]:
-        # one pass over dY for both operands
+    if needs[0] and needs[1] and rnd != "stochastic":
+        # one pass over dY for both operands.  Under stochastic rounding the
+        # passes are bound by their Philox draws, which a joint pass cannot
+        # share, and two separate passes run faster (c3 dY: 395 vs 460 us)
         qdy, qdyt = ops.quant_dual_1x128_128x1(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed,
                                                offset_rows=base + 2, offset_cols=base + 3, want_nan_rows=True)
     if needs[0]:
