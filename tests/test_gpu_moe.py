@@ -249,3 +249,34 @@ def test_expert_mlp_matches_oracle(gpu_device):
     assert rel_fro_bf16(h, h_ref) <= 1e-3
     assert rel_fro_bf16(out, out_from_gpu_h) <= 1e-3
     assert rel_fro_bf16(out, out_ref) <= 5e-3
+
+
+@pytest.mark.parametrize("fmt,grid", [("e4m3", O.GRID_E4M3), ("int_grid", O.GRID_INT)])
+def test_grouped_gemm_tile_boundaries(gpu_device, fmt, grid):
+    """Experts whose last 256-row tile has exactly 128 rows (its second half
+    is all padding), 129 rows (one row in the second half), 1 row, a whole
+    tile, none, and one and a half tiles, against the per-expert oracle."""
+    from lowbit import moe, ops
+
+    counts = [128, 129, 1, 256, 0, 384]
+    E, T, H, N = len(counts), sum(counts), 256, 384
+    x = seeded((T, H), seed=20261310, outliers=0.01).to(gpu_device)
+    w = seeded((E, N, H), seed=20261311, std=0.02).to(gpu_device)
+    wc, ws, wn = moe.quantize_expert_weights(w, fmt=fmt)
+    qx = ops.quant_tile_1x128(x, fmt=fmt, want_nan_rows=True)
+    offs = _offsets(counts, gpu_device)
+    y = ops.gemm_grouped_blockscaled(qx, wc, ws, offs, N=N, b_nan_rows=wn)
+    torch.cuda.synchronize()
+    _, _, _, xdq = O.quant_tile_1x128(to_np32(x), grid=grid)
+    ref = np.zeros((T, N))
+    lo = 0
+    for e, c in enumerate(counts):
+        if c:
+            _, _, _, wdq = O.quant_block_128x128(to_np32(w[e]), grid=grid)
+            ref[lo:lo + c] = O.gemm_ref(xdq[lo:lo + c], wdq)
+        lo += c
+    assert rel_fro_bf16(y, ref) <= 1e-3
+    for e, c in enumerate(counts):  # every expert on its own, so none hides in the total
+        lo = sum(counts[:e])
+        if c:
+            assert rel_fro_bf16(y[lo:lo + c], ref[lo:lo + c]) <= 1e-3, f"expert {e} ({c} rows)"
