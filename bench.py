@@ -266,7 +266,9 @@ def other_config(args) -> dict:
 
 
 def cpu_baseline(fmt: str, rounding: str, rows: int):
-    """The CPU oracle's emulated linear (te_backend.py:229-260 restated) on a row sample."""
+    """The CPU oracle's emulated linear (te_backend.py:229-260 restated) on a
+    row sample, and its 1x128 activation quantizer alone: median of 3 timed
+    runs after 1 warm-up each."""
     import numpy as np
     import torch
 
@@ -279,10 +281,20 @@ def cpu_baseline(fmt: str, rounding: str, rows: int):
     grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
     rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
     O.lib()
-    t0 = time.perf_counter()
-    y = O.emulated_linear_forward(xn, wn, grid=grid, rounding=rc)
-    dt = time.perf_counter() - t0
+
+    def median_s(fn, runs=3):
+        fn()  # warm-up
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[len(ts) // 2]
+
+    dt = median_s(lambda: O.emulated_linear_forward(xn, wn, grid=grid, rounding=rc))
+    dq = median_s(lambda: O.quant_tile_1x128(xn, grid=grid, rounding=rc))
     flops = 2.0 * rows * wn.shape[0] * wn.shape[1]
+    q_bytes = xn.shape[0] * xn.shape[1] * 3 + xn.shape[0] * (xn.shape[1] // 128) * 4
     threads = None
     try:
         from threadpoolctl import threadpool_info
@@ -290,15 +302,17 @@ def cpu_baseline(fmt: str, rounding: str, rows: int):
         threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
     except Exception:
         threads = os.cpu_count()
-    del y
     return {
         "value": round(flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": int(threads or 1),
         "kind": "port",
+        "quantizer_GB/s": round(q_bytes / dq / 1e9, 3),
         "sample": (f"oracle emulated linear (1x128 X quant + 128x128 W quant in C on 1 thread, "
                    f"fp32 dequant, numpy fp32 matmul on {threads} BLAS threads) over X rows [0, {rows}) "
-                   f"of config 2 with the full W [18432, 7168]; {dt:.2f} s; CPU {_cpu_model()}"),
+                   f"of config 2 with the full W [18432, 7168]: {dt:.2f} s; the X 1x128 quantizer alone "
+                   f"(C, 1 thread, same rows): {dq * 1e3:.1f} ms; medians of 3 runs after 1 warm-up; "
+                   f"CPU {_cpu_model()}"),
     }
 
 
