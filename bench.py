@@ -39,7 +39,7 @@ def parse_args():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--format", default="e4m3", choices=["e4m3", "int_grid"])
     p.add_argument("--rounding", default="nearest", choices=["nearest", "stochastic"])
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -460,6 +460,7 @@ def main():
             "traffic": traffic.get("gemm_blockscaled_kernel"),
             "traffic_source": f"profiles/c2_forward_{args.format}.md" if traffic else None,
             "avg_ms": round(avg(gm_ms), 4),
+            "median_ms": round(sorted(gm_ms)[len(gm_ms) // 2], 4),
             "min_hbm_bytes": gemm_min_bytes,
         },
         "quantizers": {
