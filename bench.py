@@ -265,6 +265,107 @@ def other_config(args) -> dict:
     return res
 
 
+def _median_s(fn, runs: int = 3) -> float:
+    """Median wall time of `runs` calls after one warm-up call."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+
+        return int(max((i.get("num_threads", 1) for i in threadpool_info()), default=1))
+    except Exception:
+        return int(os.cpu_count() or 1)
+
+
+def other_cpu_baseline(config: str, fmt: str) -> dict:
+    """The CPU oracle's restatement of a config's path on a bounded sample:
+    quantizers in C on one thread, fp32 matmuls through numpy's BLAS."""
+    import numpy as np
+
+    from lowbit import moe, workloads
+    from oracle import oracle as O
+
+    grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
+    O.lib()
+    f32 = lambda t: t.float().numpy()
+    if config == "c1":
+        x, w = workloads.c1_inputs(device="cpu")
+        xn, wn = f32(x), f32(w)
+        run = lambda: O.emulated_linear_forward(xn, wn, grid=grid)
+        flops = 2.0 * xn.shape[0] * wn.shape[0] * wn.shape[1]
+        what = "oracle emulated linear over all of config 1"
+    elif config == "c3":
+        rows = 512
+        x, w = workloads.c2_inputs(device="cpu", rows=rows)
+        dy = workloads.c3_grad(device="cpu")[:rows]
+        xn, wn, dyn = f32(x), f32(w), f32(dy)
+        wdq = O.quant_block_128x128(wn, grid=grid)[3]  # the weight's codes come from the forward
+
+        def run():
+            dx = O.quant_tile_1x128(dyn, grid=grid)[3] @ wdq
+            dw = O.quant_tile_128x1_t(dyn, grid=grid)[3].T @ O.quant_tile_128x1_t(xn, grid=grid)[3]
+            return dx, dw
+
+        flops = 4.0 * rows * wn.shape[0] * wn.shape[1]
+        what = (f"oracle recipe backward over rows [0, {rows}) of config 3: dY 1x128 and 128x1, X 128x1, "
+                "fp32 dgrad against the forward's 128x128 W and fp32 wgrad")
+    elif config == "c4":
+        rows = 1024
+        tokens, routing, _, _ = workloads.c4_inputs(device="cpu", experts=0)
+        n_exp = workloads.SHAPES[4]["experts"]
+        _, tok_idx, offsets = moe.sort_by_expert(routing, n_exp)
+        # weights of the experts the sample reaches only (leading slices of the full tensors)
+        reach = int(np.searchsorted(np.asarray(offsets.tolist()), rows, side="left"))
+        _, _, w_up, w_down = workloads.c4_inputs(device="cpu", experts=min(reach, n_exp))
+        w_gate = workloads.c4_gate(device="cpu", experts=min(reach, n_exp))
+        xs = f32(tokens[tok_idx[:rows]])
+        off = offsets.tolist()
+        parts = [(e, max(off[e], 0), min(off[e + 1], rows)) for e in range(len(off) - 1) if off[e] < rows]
+        parts = [p for p in parts if p[2] > p[1]]
+        dq = {e: [O.quant_block_128x128(f32(m[e]), grid=grid)[3] for m in (w_gate, w_up, w_down)]
+              for e, _, _ in parts}  # the weights' codes are made once, before the step
+
+        def run():
+            xdq = O.quant_tile_1x128(xs, grid=grid)[3]
+            out = np.empty((rows, w_down.shape[1]), dtype=np.float32)
+            for e, lo, hi in parts:
+                gdq, udq, ddq = dq[e]
+                g = O.round_bf16(xdq[lo:hi] @ gdq.T)
+                u = O.round_bf16(xdq[lo:hi] @ udq.T)
+                h = O.round_bf16(O.round_bf16(g / (1.0 + np.exp(-g))) * u)
+                out[lo:hi] = O.quant_tile_1x128(h, grid=grid)[3] @ ddq.T
+            return out
+
+        flops = 6.0 * rows * w_up.shape[2] * w_up.shape[1]
+        what = (f"oracle expert MLP over expert-sorted rows [0, {rows}) of config 4 ({len(parts)} expert(s)): 1x128 x, "
+                "fp32 gate, up and down GEMMs against 128x128 weights, SwiGLU, 1x128 h")
+    else:
+        rows = 512
+        x, w = workloads.c5_inputs(device="cpu")
+        xn, wn = f32(x[:rows]), f32(w)
+        N, K = wn.shape
+        packed, sc = O.nf4_quant(wn, 64)  # the persistent codes exist before the step
+
+        def run():
+            return xn @ O.nf4_dequant(packed, sc, N * K, 64).reshape(N, K).T
+
+        flops = 2.0 * rows * N * K
+        what = f"oracle NF4 (64-element blocks) dequantize and fp32 matmul over X rows [0, {rows}) of config 5"
+    dt = _median_s(run)
+    th = _blas_threads()
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": th, "kind": "port",
+            "sample": f"{what}; quantizers in C on 1 thread, numpy matmuls on {th} BLAS threads; {dt:.2f} s, "
+                      f"median of 3 runs after 1 warm-up; CPU {_cpu_model()}"}
+
+
 def cpu_baseline(fmt: str, rounding: str, rows: int):
     """The CPU oracle's emulated linear (te_backend.py:229-260 restated) on a
     row sample, and its 1x128 activation quantizer alone: median of 3 timed
@@ -282,26 +383,11 @@ def cpu_baseline(fmt: str, rounding: str, rows: int):
     rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
     O.lib()
 
-    def median_s(fn, runs=3):
-        fn()  # warm-up
-        ts = []
-        for _ in range(runs):
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return sorted(ts)[len(ts) // 2]
-
-    dt = median_s(lambda: O.emulated_linear_forward(xn, wn, grid=grid, rounding=rc))
-    dq = median_s(lambda: O.quant_tile_1x128(xn, grid=grid, rounding=rc))
+    dt = _median_s(lambda: O.emulated_linear_forward(xn, wn, grid=grid, rounding=rc))
+    dq = _median_s(lambda: O.quant_tile_1x128(xn, grid=grid, rounding=rc))
     flops = 2.0 * rows * wn.shape[0] * wn.shape[1]
     q_bytes = xn.shape[0] * xn.shape[1] * 3 + xn.shape[0] * (xn.shape[1] // 128) * 4
-    threads = None
-    try:
-        from threadpoolctl import threadpool_info
-
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:
-        threads = os.cpu_count()
+    threads = _blas_threads()
     return {
         "value": round(flops / dt / 1e12, 6),
         "unit": "TFLOP/s",
@@ -342,7 +428,10 @@ def main():
     if args.config != "c2":
         if args.calib_copy:
             _calibration_copy(dev)
-        print(json.dumps(other_config(args)))
+        res = other_config(args)
+        if not args.no_cpu_baseline:
+            res["cpu_baseline"] = other_cpu_baseline(args.config, args.format)
+        print(json.dumps(res))
         return
     shp = workloads.SHAPES[2]
     M, N, K = shp["M"], shp["N"], shp["K"]

@@ -92,21 +92,23 @@ def zipf_topk_routing(tokens: int, experts: int, top_k: int, *, s: float = 1.2, 
     return idx.to(device)
 
 
-def c4_inputs(device="cpu", dtype=torch.bfloat16):
+def c4_inputs(device="cpu", dtype=torch.bfloat16, experts: Optional[int] = None):
+    """experts: generate only the first `experts` experts' weights (the same
+    values as the full tensors' leading slices: generation runs in order)."""
     s = SHAPES[4]
+    ne = s["experts"] if experts is None else experts
     tokens = normal((s["tokens"], s["hidden"]), std=1.0, seed=seed_for(4, 0), device=device, dtype=dtype)
     routing = zipf_topk_routing(s["tokens"], s["experts"], s["top_k"], seed=seed_for(4, 1), device=device)
-    w_up = normal((s["experts"], s["inter"], s["hidden"]), std=0.006, seed=seed_for(4, 2), device=device,
-                  dtype=dtype)
-    w_down = normal((s["experts"], s["hidden"], s["inter"]), std=0.006, seed=seed_for(4, 3), device=device,
-                    dtype=dtype)
+    w_up = normal((ne, s["inter"], s["hidden"]), std=0.006, seed=seed_for(4, 2), device=device, dtype=dtype)
+    w_down = normal((ne, s["hidden"], s["inter"]), std=0.006, seed=seed_for(4, 3), device=device, dtype=dtype)
     return tokens, routing, w_up, w_down
 
 
-def c4_gate(device="cpu", dtype=torch.bfloat16):
+def c4_gate(device="cpu", dtype=torch.bfloat16, experts: Optional[int] = None):
     """The SwiGLU gate weight of config 4's experts (same shape and law as W_up)."""
     s = SHAPES[4]
-    return normal((s["experts"], s["inter"], s["hidden"]), std=0.006, seed=seed_for(4, 4), device=device, dtype=dtype)
+    ne = s["experts"] if experts is None else experts
+    return normal((ne, s["inter"], s["hidden"]), std=0.006, seed=seed_for(4, 4), device=device, dtype=dtype)
 
 
 def c5_inputs(device="cpu", dtype=torch.bfloat16):
