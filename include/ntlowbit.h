@@ -109,6 +109,21 @@ int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t 
                       uint32_t* amax_bits, void* stream);
 
 /*
+ * _comm_quant_dequant (moe.py:79-143) in one pass: x [R, K] quantized with one
+ * scale per (gr x gc) group (scales from the amaxes of ntlb_amax_grouped,
+ * scale_rule, qmax and grid as in ntlb_quant_grouped; the reference uses
+ * the int grid, qmax 2^(bits-1)-1 and NTLB_SCALE_BEFORE_DIVIDE), and out
+ * [R, ldo] (x's dtype) = the value the reference returns, tensor + (dq -
+ * tensor) evaluated in x's dtype with dq = q * scale rounded to that dtype.
+ * Granularities: tile_1x128 / block_128x128 (gr = R, gc = 128), channel
+ * (gr = R, gc = 1), tensor (gr = R, gc = K).  Autograd (the straight-through
+ * gradient) stays with the caller.
+ */
+int ntlb_comm_quant_dequant(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr, int64_t gc,
+                            const uint32_t* amax_bits, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                            uint64_t offset, void* out, int64_t ldo, void* stream);
+
+/*
  * Quantize with precomputed group amaxes (from ntlb_amax_grouped).  Writes
  * scales[(i/gr)*n_gc + k/gc] (fp32, computed from the amax with scale_rule),
  * codes [R, ldc] (ldc >= K), optional dq and nan_rows.

@@ -523,24 +523,51 @@ __global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArg
 // ---------------------------------------------------------------------------
 // grouped amax (tensor / channel / strip) and quantization with group scales
 // ---------------------------------------------------------------------------
-template <int IN_DT>
+// |x| maxima per (gr x gc) group.  Workgroup = 2048 columns (8 per thread)
+// of rows [r_begin, r_end).  Groups of at least 8 columns reduce in LDS
+// first, so the workgroup issues one global atomic per group it touches
+// (the strip and tensor groups of the comm payloads would otherwise put
+// every thread's atomic on a handful of addresses).
+constexpr int AMAX_LDS_GROUPS = 2048 / 8 + 2;
+
+template <int IN_DT, bool VEC>
 __global__ void __launch_bounds__(256) amax_grouped_kernel(const void* x, int64_t R, int64_t K, int64_t ldx,
                                                            int64_t gr, int64_t gc, int64_t n_gc,
                                                            int64_t rows_per_block, uint32_t* amax_bits) {
-  const int64_t kc = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;  // 8 columns per thread
+  __shared__ uint32_t sm[AMAX_LDS_GROUPS];
+  const int64_t col0 = (int64_t)blockIdx.x * 2048;
+  const int64_t kc = col0 + (int64_t)threadIdx.x * 8;  // 8 columns per thread
   const int64_t r_begin = (int64_t)blockIdx.y * rows_per_block;
   const int64_t r_end = min(R, r_begin + rows_per_block);
-  if (r_begin >= R) return;
+  if (r_begin >= R) return;  // the whole workgroup
+  const bool lds = gc >= 8;
+  const int64_t g0 = col0 / gc;
+  const int64_t ngb = lds ? (min(col0 + 2048, K) - 1) / gc + 1 - g0 : 0;  // groups this workgroup's columns touch
+  for (int64_t j = threadIdx.x; j < ngb; j += 256) sm[j] = 0;
+  __syncthreads();
   uint32_t m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  int64_t cur_g = r_begin / gr;
+  // every thread of the workgroup calls flush at the same rows (barriers inside)
   auto flush = [&](int64_t g) {
-    if (kc >= K) return;
-    if (gc == 1) {
+    if (lds) {
+      if (kc < K) {
+        if (gc % 8 == 0) {  // the 8 columns share one group
+          uint32_t mm = 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        if (kc + i < K && m[i]) atomicMax(amax_bits + g * n_gc + kc + i, m[i]);
-    } else {
-      // gc > 1: the 8 columns may straddle a group edge only if gc % 8 != 0
+          for (int i = 0; i < 8; ++i) mm = max(mm, m[i]);
+          if (mm) atomicMax(&sm[kc / gc - g0], mm);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (kc + i < K && m[i]) atomicMax(&sm[(kc + i) / gc - g0], m[i]);
+        }
+      }
+      __syncthreads();
+      for (int64_t j = threadIdx.x; j < ngb; j += 256) {
+        if (sm[j]) atomicMax(amax_bits + g * n_gc + g0 + j, sm[j]);
+        sm[j] = 0;
+      }
+      __syncthreads();
+    } else if (kc < K) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (kc + i < K && m[i]) atomicMax(amax_bits + g * n_gc + (kc + i) / gc, m[i]);
@@ -548,28 +575,108 @@ __global__ void __launch_bounds__(256) amax_grouped_kernel(const void* x, int64_
 #pragma unroll
     for (int i = 0; i < 8; ++i) m[i] = 0;
   };
+  int64_t cur_g = r_begin / gr;
+  int64_t next_b = (cur_g + 1) * gr;  // first row of the next row group
   for (int64_t r = r_begin; r < r_end; ++r) {
-    int64_t g = r / gr;
-    if (g != cur_g) {
+    if (r >= next_b) {
       flush(cur_g);
-      cur_g = g;
+      cur_g = r / gr;
+      next_b = (cur_g + 1) * gr;
     }
     if (kc < K) {
       float v[8];
-      load8<IN_DT, false>(x, r * ldx, kc, K, v);
+      load8<IN_DT, VEC>(x, r * ldx, kc, K, v);
 #pragma unroll
       for (int i = 0; i < 8; ++i) m[i] = max(m[i], abs_bits(v[i]));
     }
   }
-  if (gc > 1 && gc % 8 == 0) {
-    // all 8 columns share one group: fold them first to cut atomics
-    uint32_t mm = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) mm = max(mm, m[i]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) m[i] = (i == 0) ? mm : 0;
-  }
   flush(cur_g);
+}
+
+typedef __bf16 v2bf_q __attribute__((ext_vector_type(2)));
+
+// eight values rounded to a float dtype in place; bf16 by the hardware
+// pack-convert (v_cvt_pk_bf16_f32, round to nearest even as f32_to_bf16_bits,
+// a NaN stays a NaN)
+template <int DT>
+__device__ __forceinline__ void round8_dtype(float (&v)[8]) {
+  if constexpr (DT == DT_BF16) {
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const v2bf_q p = {(__bf16)v[i], (__bf16)v[i + 1]};
+      const uint32_t b = __builtin_bit_cast(uint32_t, p);
+      v[i] = __uint_as_float(b << 16);
+      v[i + 1] = __uint_as_float(b & 0xFFFF0000u);
+    }
+  } else if constexpr (DT == DT_F16) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __half2float(__float2half(v[i]));
+  }
+}
+
+// moe.py:79-143 in one pass: each element quantized with its group's scale
+// (from the group amaxes) and written as the value the reference's
+// straight-through expression forms, tensor + (dq - tensor) in the tensor's
+// dtype, with dq = q * scale rounded to that dtype.  One scale lookup per 8
+// elements when gc % 8 == 0.
+template <int IN_DT, int GRID, bool SR, bool VEC>
+__global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const uint32_t* amax_bits, int64_t gr,
+                                                             int64_t gc, int64_t n_gc, void* out, int64_t ldo) {
+#pragma clang fp contract(off)
+  const int64_t chunks_per_row = (a.K + 7) >> 3;
+  const int64_t total = a.R * chunks_per_row;
+  const bool chunk_scale = gc % 8 == 0;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
+    const int64_t r = c / chunks_per_row;
+    const int64_t k0 = (c - r * chunks_per_row) * 8;
+    float v[8];
+    load8<IN_DT, VEC>(a.x, r * a.ldx, k0, a.K, v);
+    uint32_t rb[8];
+    sr_words<SR>((uint64_t)(r * a.K + k0), a.seed, a.offset, rb);
+    const int64_t grow = (r / gr) * n_gc;
+    float q[8], sv[8];
+    if (chunk_scale) {
+      // one group for the chunk: the tile quantizers' path (exact reciprocal
+      // division where the group amax allows it, per element with a NaN)
+      const uint32_t m = amax_bits[grow + k0 / gc];
+      const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
+      const float rs = fast_div_ok<SR>(m) ? 1.0f / s : 1.0f;
+      uint32_t lo, hi;
+      (void)quant8_tile_rs<GRID, SR, true>(v, m, s, rs, a.qmaxf, rb, lo, hi, q);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = s;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t k = k0 + i;
+        sv[i] = scale_from_amax_bits(amax_bits[grow + min<int64_t>(gc == 1 ? k : k / gc, n_gc - 1)], a.qmaxf,
+                                     a.scale_rule);
+        (void)quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]);
+      }
+    }
+    // dq = q * scale in the tensor's dtype, then tensor + (dq - tensor) in it
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = q[i] * sv[i];
+    round8_dtype<IN_DT>(o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = o[i] - v[i];
+    round8_dtype<IN_DT>(o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = v[i] + o[i];
+    round8_dtype<IN_DT>(o);
+    if (VEC && IN_DT == DT_BF16 && k0 + 8 <= a.K) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16_bits(o[2 * i]) | ((uint32_t)f32_to_bf16_bits(o[2 * i + 1]) << 16);
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + r * ldo + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + i < a.K) store_elem(out, IN_DT, r * ldo + k0 + i, o[i]);
+    }
+  }
 }
 
 __global__ void scales_from_amax_kernel(const uint32_t* amax_bits, int64_t n, float qmaxf, int rule,
@@ -578,7 +685,7 @@ __global__ void scales_from_amax_kernel(const uint32_t* amax_bits, int64_t n, fl
   if (i < n) scales[i] = scale_from_amax_bits(amax_bits[i], qmaxf, rule);
 }
 
-template <int IN_DT, int GRID, bool SR>
+template <int IN_DT, int GRID, bool SR, bool VEC>
 __global__ void __launch_bounds__(256) quant_grouped_kernel(QuantArgs a, int64_t gr, int64_t gc, int64_t n_gc) {
   const int64_t chunks_per_row = (a.K + 7) >> 3;
   const int64_t total = a.R * chunks_per_row;
@@ -586,25 +693,45 @@ __global__ void __launch_bounds__(256) quant_grouped_kernel(QuantArgs a, int64_t
     int64_t r = c / chunks_per_row;
     int64_t k0 = (c - r * chunks_per_row) * 8;
     float v[8];
-    load8<IN_DT, false>(a.x, r * a.ldx, k0, a.K, v);
+    load8<IN_DT, VEC>(a.x, r * a.ldx, k0, a.K, v);
     uint32_t rb[8];
     sr_words<SR>((uint64_t)(r * a.K + k0), a.seed, a.offset, rb);
+    // scale index: one division per chunk when its 8 columns share a group
+    const float* srow = a.scales + (r / gr) * n_gc;
+    const float s0 = gc % 8 == 0 ? srow[k0 / gc] : 0.0f;
     uint32_t cb[8];
-    float q[8];
+    float q[8], sv[8];
     bool nan = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int64_t k = k0 + i;
-      float s = (k < a.K) ? a.scales[(r / gr) * n_gc + k / gc] : 1.0f;
-      cb[i] = (k < a.K) ? quant_one<GRID, SR>(v[i], s, a.qmaxf, rb[i], q[i]) : 0u;
-      if (k < a.K) {
-        nan |= (__float_as_uint(q[i]) & 0x7FFFFFFFu) > 0x7F800000u;
-        if (a.dq) store_elem(a.dq, a.dq_dtype, r * a.lddq + k, q[i] * s);
+      sv[i] = (k < a.K) ? (gc % 8 == 0 ? s0 : srow[gc == 1 ? k : k / gc]) : 1.0f;
+      cb[i] = (k < a.K) ? quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]) : 0u;
+      if (k < a.K) nan |= (__float_as_uint(q[i]) & 0x7FFFFFFFu) > 0x7F800000u;
+    }
+    if (VEC && k0 + 8 <= a.ldc) {
+      *reinterpret_cast<uint2*>(a.codes + r * a.ldc + k0) =
+          make_uint2(cb[0] | (cb[1] << 8) | (cb[2] << 16) | (cb[3] << 24), cb[4] | (cb[5] << 8) | (cb[6] << 16) | (cb[7] << 24));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (k0 + i < a.ldc) a.codes[r * a.ldc + k0 + i] = (uint8_t)cb[i];
+    }
+    if (a.dq) {
+      if (VEC && a.dq_dtype == DT_BF16 && k0 + 8 <= a.K && ((r * a.lddq + k0) & 7) == 0 &&
+          (reinterpret_cast<uintptr_t>(a.dq) & 15) == 0) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)f32_to_bf16_bits(q[2 * i] * sv[2 * i]) |
+                 ((uint32_t)f32_to_bf16_bits(q[2 * i + 1] * sv[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.dq) + r * a.lddq + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (k0 + i < a.K) store_elem(a.dq, a.dq_dtype, r * a.lddq + k0 + i, q[i] * sv[i]);
       }
     }
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (k0 + i < a.ldc) a.codes[r * a.ldc + k0 + i] = (uint8_t)cb[i];
     if (nan && a.nan_rows) atomicOr(a.nan_rows + r, 1);
   }
 }
@@ -1172,9 +1299,39 @@ extern "C" int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t 
   if (row_blocks > 65535 || col_blocks > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: shape too large", fn);
   dim3 grd((unsigned)col_blocks, (unsigned)row_blocks), blk(256);
   hipStream_t st = as_stream(stream);
+  const bool vec = K % 8 == 0 && ldx % 8 == 0 && aligned(x, 16);
   NTLB_DISPATCH_DT(x_dtype, {
-    amax_grouped_kernel<D_><<<grd, blk, 0, st>>>(x, R, K, ldx, gr, gc, n_gc, rpb, amax_bits);
+    if (vec)
+      amax_grouped_kernel<D_, true><<<grd, blk, 0, st>>>(x, R, K, ldx, gr, gc, n_gc, rpb, amax_bits);
+    else
+      amax_grouped_kernel<D_, false><<<grd, blk, 0, st>>>(x, R, K, ldx, gr, gc, n_gc, rpb, amax_bits);
   });
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_comm_quant_dequant(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
+                                       int64_t gc, const uint32_t* amax_bits, int grid, int qmax, int rounding,
+                                       int scale_rule, uint64_t seed, uint64_t offset, void* out, int64_t ldo,
+                                       void* stream) {
+  const char* fn = "ntlb_comm_quant_dequant";
+  int rc = check_common(fn, x, x_dtype, R, K, ldx, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (gr < 1 || gc < 1 || ldo < K) return fail(NTLB_EINVAL, "%s: bad group or ldo", fn);
+  if (R * K == 0) return NTLB_OK;
+  if (!amax_bits || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  QuantArgs a = make_args(x, R, K, ldx, grid, qmax, scale_rule, seed, offset, nullptr, 0, nullptr, 0, 0, nullptr, 0,
+                          0, nullptr);
+  const int64_t n_gc = cdiv(K, gc);
+  const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
+  const bool vec = K % 8 == 0 && ldx % 8 == 0 && ldo % 8 == 0 && aligned(x, 16) && aligned(out, 16);
+  dim3 grd(grid_for(R * cdiv(K, 8), 256, 256 * 16)), blk(256);
+  hipStream_t st = as_stream(stream);
+  NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
+    if (vec)
+      comm_quant_ste_kernel<D_, G_, S_, true><<<grd, blk, 0, st>>>(a, amax_bits, gr, gc, n_gc, out, ldo);
+    else
+      comm_quant_ste_kernel<D_, G_, S_, false><<<grd, blk, 0, st>>>(a, amax_bits, gr, gc, n_gc, out, ldo);
+  }));
   return check_launch(fn);
 }
 
@@ -1200,8 +1357,13 @@ extern "C" int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t
   if (rc) return rc;
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
   dim3 grd(grid_for(R * cdiv(K, 8), 256, 256 * 16)), blk(256);
+  // vector loads and 8-byte code stores where rows and pitches allow
+  const bool vec = K % 8 == 0 && ldx % 8 == 0 && ldc % 8 == 0 && aligned(x, 16) && aligned(codes, 8);
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
-    quant_grouped_kernel<D_, G_, S_><<<grd, blk, 0, st>>>(a, gr, gc, n_gc);
+    if (vec)
+      quant_grouped_kernel<D_, G_, S_, true><<<grd, blk, 0, st>>>(a, gr, gc, n_gc);
+    else
+      quant_grouped_kernel<D_, G_, S_, false><<<grd, blk, 0, st>>>(a, gr, gc, n_gc);
   }));
   // ldc > K: padding columns beyond the 8-aligned chunks are not touched; callers
   // pass zero-initialised code buffers when ldc > round_up(K, 8).

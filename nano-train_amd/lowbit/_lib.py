@@ -80,6 +80,8 @@ SIGNATURES = {
     "ntlb_ep_pack_return": [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _U64,
                             _U64, _P, _P],
     "ntlb_ep_combine": [_P, _I64, _I64, _P, _I32, _P, _I32, _I64, _I64, _I32, _P, _I32, _I64, _P, _P],
+    "ntlb_comm_quant_dequant": [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _I32, _I32, _U64, _U64, _P,
+                                _I64, _P],
     "ntlb_ep_unpack_records": [_P, _I64, _I64, _P, _I64, _P, _I32, _P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P],
 }
 

@@ -67,11 +67,32 @@ def comm_quant_dequant(
     else:
         gr, gc = R, K  # tensor, 1-D channel, or anything else (moe.py:107-110, :141-143)
     rounding = "stochastic" if rounding_mode == "stochastic" else "nearest"
-    _, _, dq, _ = ops.quant_grouped(
-        x2.detach(), gr, gc, fmt="int_grid", bits=bits, rounding=rounding, seed=seed, offset=offset,
-        scale_rule=_lib.SCALE_BEFORE_DIVIDE, want_dq=True, dq_dtype=tensor.dtype)
-    dq = dq.reshape(tensor.shape)
-    return tensor + (dq - tensor).detach()
+    x2 = x2.detach()
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    gr, gc = max(1, min(gr, R)), max(1, min(gc, K))
+    amax = torch.zeros(ops.cdiv(R, gr) * ops.cdiv(K, gc), dtype=torch.int32, device=tensor.device)
+    out = torch.empty((R, K), dtype=tensor.dtype, device=tensor.device)
+    xc = ops._dtype_code(x2.dtype)
+    _lib.call("ntlb_amax_grouped", x2.data_ptr(), xc, R, K, x2.stride(0), gr, gc, amax.data_ptr(), ops._stream())
+    # the kernel writes tensor + (dq - tensor) as the reference evaluates it
+    _lib.call("ntlb_comm_quant_dequant", x2.data_ptr(), xc, R, K, x2.stride(0), gr, gc, amax.data_ptr(),
+              ops.grid_code("int_grid"), (1 << (bits - 1)) - 1, ops.rounding_code(rounding),
+              _lib.SCALE_BEFORE_DIVIDE, seed, offset, out.data_ptr(), K, ops._stream())
+    return _StraightThrough.apply(tensor, out.reshape(tensor.shape))
+
+
+class _StraightThrough(torch.autograd.Function):
+    """The value of tensor + (dq - tensor).detach() with its gradient: the
+    identity to tensor (moe.py:110, :121, :141, :143)."""
+
+    @staticmethod
+    def forward(ctx, tensor, value):
+        return value
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, None
 
 
 @dataclass
