@@ -165,6 +165,9 @@ def other_config(args) -> dict:
         down = moe.quantize_expert_weights(w_down, fmt=fmt)
         del w_gate, w_up
         comm_us = _time_ms(lambda i: moe.comm_quant(xs, fmt=fmt), args.steps, args.warmup, st) * 1e3
+        payload = moe.comm_quant(xs, fmt=fmt)
+        dequant_us = _time_ms(lambda i: moe.comm_dequant(payload), args.steps, args.warmup, st) * 1e3
+        del payload
         # the reference's own comm-quant (_comm_quant_dequant, strip granularity) as a drop-in: the amax pass,
         # then the quantize pass writing tensor + (dq - tensor)
         ref_cq_us = _time_ms(lambda i: moe.comm_quant_dequant(xs, granularity="tile_1x128", rounding_mode="nearest",
@@ -220,6 +223,8 @@ def other_config(args) -> dict:
                    gate_up_swiglu_tflops=round(2 * fl / (gu_ms * 1e-3) / 1e12, 2),
                    down_tflops=round(fl / (dn_ms * 1e-3) / 1e12, 2), quant_x_us=round(qx_us, 2),
                    comm_quant_us=round(comm_us, 2), comm_quant_GBs=round(comm_bytes / comm_us / 1e3, 1),
+                   comm_dequant_us=round(dequant_us, 2),
+                   comm_dequant_GBs=round((R * H * 3 + R * (H // 128) * 4) / dequant_us / 1e3, 1),
                    reference_comm_quant_dequant_us=round(ref_cq_us, 2),
                    reference_comm_quant_dequant_GBs=round(R * H * 2 * 3 / ref_cq_us / 1e3, 1),
                    ep_dispatch={"records": n_rec, "record_bytes": rec_b, "pack_us": round(pack_us, 2),

@@ -14,6 +14,8 @@
 #include <algorithm>
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 #include "ntlb_quant8.h"
@@ -1063,6 +1065,53 @@ __global__ void __launch_bounds__(256) dequant_kernel(const uint8_t* codes, int6
     store_dq8(out, out_dtype, r * ldo, k0, K, v, 1.0f);
   }
 }
+// Dequantize, fast path: K and ldc multiples of 8, one scale per 128
+// columns (c_shift 7).  Thread = 8 columns, walking rows; no division.  e4m3
+// through the hardware converter (v_cvt_pk_f32_fp8), bf16 output in 16-byte
+// stores when BF16V (f32_to_bf16_bits rounding, as store_elem).
+typedef float v2f_q __attribute__((ext_vector_type(2)));
+
+template <int GRID, bool BF16V>
+__global__ void __launch_bounds__(256) dequant_fast_kernel(const uint8_t* codes, int64_t ldc, const float* scales,
+                                                           int64_t s_row, int64_t s_col, int r_shift, int64_t R,
+                                                           int64_t K, void* out, int out_dtype, int64_t ldo) {
+  const int64_t k0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (k0 >= K) return;
+  for (int64_t r = blockIdx.y; r < R; r += gridDim.y) {
+    const uint2 cw = *reinterpret_cast<const uint2*>(codes + r * ldc + k0);
+    const float s = scales[(r >> r_shift) * s_row + (k0 >> 7) * s_col];
+    float v[8];
+    const uint32_t wd[2] = {cw.x, cw.y};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if constexpr (GRID == GRID_E4M3) {
+        const v2f_q lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)wd[h], false);
+        const v2f_q hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)wd[h], true);
+        v[4 * h + 0] = lo[0] * s;
+        v[4 * h + 1] = lo[1] * s;
+        v[4 * h + 2] = hi[0] * s;
+        v[4 * h + 3] = hi[1] * s;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t c = (wd[h] >> (8 * i)) & 0xFFu;
+          v[4 * h + i] = (c == 0x80u ? __uint_as_float(0x7FC00000u) : (float)(int8_t)c) * s;
+        }
+      }
+    }
+    if constexpr (BF16V) {
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
+      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + r * ldo + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) store_elem(out, out_dtype, r * ldo + k0 + i, v[i]);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // dispatch helpers
 // ---------------------------------------------------------------------------
@@ -1460,6 +1509,26 @@ extern "C" int ntlb_dequant(int grid, const uint8_t* codes, int64_t ldc, const f
   if (R * K == 0) return NTLB_OK;
   if (!codes || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
   hipStream_t st = as_stream(stream);
+  if (c_shift == 7 && K % 8 == 0 && ldc % 8 == 0 && aligned(codes, 8)) {
+    const int64_t gx = cdiv(K / 8, 256);
+    const int64_t gy = std::min<int64_t>(R, std::max<int64_t>(1, (256 * 16) / gx));
+    dim3 fgrd((unsigned)gx, (unsigned)std::min<int64_t>(gy, 65535)), fblk(256);
+    const bool bf16v = out_dtype == NTLB_BF16 && ldo % 8 == 0 && aligned(out, 16);
+    auto launch = [&](auto gridc, auto vecc) {
+      dequant_fast_kernel<decltype(gridc)::value, decltype(vecc)::value><<<fgrd, fblk, 0, st>>>(
+          codes, ldc, scales, s_row, s_col, r_shift, R, K, out, out_dtype, ldo);
+    };
+    using E = std::integral_constant<int, GRID_E4M3>;
+    using I = std::integral_constant<int, GRID_INT>;
+    using T = std::true_type;
+    using F = std::false_type;
+    if (grid == NTLB_GRID_E4M3) {
+      if (bf16v) launch(E(), T()); else launch(E(), F());
+    } else {
+      if (bf16v) launch(I(), T()); else launch(I(), F());
+    }
+    return check_launch(fn);
+  }
   dim3 grd(grid_for(R * cdiv(K, 8), 256, 256 * 16)), blk(256);
   if (grid == NTLB_GRID_E4M3)
     dequant_kernel<GRID_E4M3><<<grd, blk, 0, st>>>(codes, ldc, scales, s_row, s_col, r_shift, c_shift, R, K, out,
