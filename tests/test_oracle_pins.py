@@ -6,12 +6,15 @@ is pinned here by an independent source: published known-answer vectors
 round-half-even), closed forms built into the inputs (per-tile amax values
 that fix every scale exactly), or the format's specification table (OCP e2m1).
 Each pin is chosen so that a plausible mistake (a dropped /qmax, a transposed
-block index, a wrong tie rule, swapped nibbles) fails it.
+block index, a wrong tie rule, swapped nibbles) fails it.  The published and
+library tables live in tests/golden/ (written by tests/golden/make_fixtures.py).
 """
 
 from __future__ import annotations
 
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -21,22 +24,20 @@ from oracle import oracle as O
 
 
 # ---------------------------------------------------------------------------
-# Philox4x32-10: known-answer vectors of Random123 (Salmon et al., SC'11)
+# Philox4x32-10: known-answer vectors of Random123 (Salmon et al., SC'11),
+# kept in tests/golden/philox4x32_10_kat.json
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize(
-    "ctr,key,expect",
-    [
-        ([0, 0, 0, 0], [0, 0], [0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8]),
-        ([0xFFFFFFFF] * 4, [0xFFFFFFFF] * 2, [0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD]),
-        (
-            [0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344],
-            [0xA4093822, 0x299F31D0],
-            [0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1],
-        ),
-    ],
-)
-def test_philox_known_answers(ctr, key, expect):
-    assert list(O.philox4x32_10(ctr, key)) == expect
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _golden(name):
+    with open(os.path.join(GOLDEN, name)) as fh:
+        return json.load(fh)
+
+
+@pytest.mark.parametrize("vec", _golden("philox4x32_10_kat.json")["vectors"])
+def test_philox_known_answers(vec):
+    assert list(O.philox4x32_10(vec["ctr"], vec["key"])) == vec["out"]
 
 
 def test_sr_bits_contract_layout():
@@ -76,6 +77,15 @@ def test_e4m3_encode_matches_torch_on_random_fp32():
         mine = O.e4m3_encode(arr)
         ref = torch.from_numpy(arr.copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
         assert np.array_equal(mine, ref)
+
+
+def test_e4m3_decode_matches_golden_table():
+    """Every code against tests/golden/e4m3fn_codes.json (torch's decoding)."""
+    want = np.array([int(b, 16) for b in _golden("e4m3fn_codes.json")["f32_bits"]], dtype=np.uint32).view(np.float32)
+    mine = O.decode_codes(np.arange(256, dtype=np.uint8), O.GRID_E4M3).astype(np.float32)
+    np.testing.assert_array_equal(np.isnan(mine), np.isnan(want))
+    ok = ~np.isnan(want)
+    assert np.array_equal(mine[ok].view(np.uint32), want[ok].view(np.uint32))
 
 
 def test_e4m3_decode_matches_torch():
