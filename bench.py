@@ -502,6 +502,13 @@ def main():
     # the GEMM's own minimum HBM traffic: both code matrices, their scales, bf16 out
     gemm_min_bytes = M * K + N * K + M * (K // 128) * 4 + (N // 128) * (K // 128) * 4 + M * N * 2
 
+    # each quantizer on its own over the same rotating inputs: inside the step it
+    # follows the previous GEMM, whose 0.3 GB of output is still being written back
+    qx_alone = _time_ms(lambda i: ops.quant_tile_1x128(sets[i % len(sets)][0], fmt=args.format, rounding=rounding,
+                                                       seed=1, offset=2 * i), args.steps, args.warmup, stream)
+    qw_alone = _time_ms(lambda i: ops.quant_block_128x128(sets[i % len(sets)][1], fmt=args.format, rounding=rounding,
+                                                          seed=1, offset=2 * i + 1), args.steps, args.warmup, stream)
+
     # achievable HBM rate on this box: a 1 GiB device-to-device copy (read + write)
     ca = torch.empty(1 << 29, dtype=torch.int16, device=dev)
     cb = torch.empty_like(ca)
@@ -565,10 +572,16 @@ def main():
         },
         "quantizers": {
             "x_tile_1x128": {"avg_us": round(avg(qx_ms) * 1e3, 2), "bytes": qx_bytes,
+                             "alone_us": round(qx_alone * 1e3, 2),
+                             "alone_GB/s": round(qx_bytes / (qx_alone * 1e-3) / 1e9, 1),
+                             "alone_frac_hbm": round(qx_bytes / (qx_alone * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                              "traffic": traffic.get("quant_tile_1x128"),
                              "GB/s": round(qx_bytes / (avg(qx_ms) * 1e-3) / 1e9, 1),
                              "frac_hbm": round(qx_bytes / (avg(qx_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
             "w_block_128x128": {"avg_us": round(avg(qw_ms) * 1e3, 2), "bytes": qw_bytes,
+                                "alone_us": round(qw_alone * 1e3, 2),
+                                "alone_GB/s": round(qw_bytes / (qw_alone * 1e-3) / 1e9, 1),
+                                "alone_frac_hbm": round(qw_bytes / (qw_alone * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                 "traffic": traffic.get("quant_block_128x128"),
                                 "GB/s": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9, 1),
                                 "frac_hbm": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
