@@ -771,7 +771,9 @@ static SplitPlan split_plan(int64_t tiles, int nk) {
   const int64_t full = (tiles / cus) * cus, rem = tiles - full;
   if (rem == 0 || rem * 2 > cus) return p;
   int s = (int)std::min<int64_t>(cus / rem, 8);
-  s = std::min(s, nk / 2);
+  // at least 9 K blocks per range: shorter ranges lose more to the partial
+  // tiles' round trip than they gain (K 1024: 25 us split, 16 unsplit)
+  s = std::min(s, nk / 9);
   if (s < 2) return p;
   p.base = (int)full;
   p.s = s;

@@ -36,7 +36,7 @@ def _splits(M, N, Kp):
     return int(_lib.lib().ntlb_gemm_workspace_bytes(M, N, Kp)) > 0
 
 
-@pytest.mark.parametrize("mnk", [(512, 1024, 1024), (256, 512, 896), (200, 300, 520), (640, 768, 2048)])
+@pytest.mark.parametrize("mnk", [(512, 1024, 2304), (256, 512, 2432), (200, 300, 2360), (640, 768, 4608)])
 @pytest.mark.parametrize("fmt,grid", [("int_grid", O.GRID_INT), ("e4m3", O.GRID_E4M3)])
 def test_split_matches_oracle_and_unsplit(gpu_device, mnk, fmt, grid):
     from lowbit import ops
@@ -54,13 +54,20 @@ def test_split_matches_oracle_and_unsplit(gpu_device, mnk, fmt, grid):
     assert rel_fro_bf16(yb, O.gemm_ref(xdq, wdq)) <= TOL
 
 
+def test_short_k_runs_unsplit():
+    """K of 2048 or less (16 blocks) takes no split: two 8-block ranges lose to
+    the partial tiles' round trip."""
+    assert not _splits(512, 1024, 1024) and not _splits(512, 1024, 2048)
+    assert _splits(512, 1024, 2304)
+
+
 def test_split_deterministic_and_workspace_resets(gpu_device):
     """Repeated calls give identical bits; a smaller shape in between, on the
     same workspace, leaves it ready for the larger one again."""
     from lowbit import ops
 
-    _, _, qx, qw = _operands(512, 1024, 1024, "e4m3", gpu_device, 20261102)
-    _, _, qx2, qw2 = _operands(256, 512, 896, "e4m3", gpu_device, 20261103)
+    _, _, qx, qw = _operands(512, 1024, 2304, "e4m3", gpu_device, 20261102)
+    _, _, qx2, qw2 = _operands(256, 512, 2432, "e4m3", gpu_device, 20261103)
     first = ops.gemm_blockscaled(qx, qw, out_dtype=torch.float32)
     small0 = ops.gemm_blockscaled(qx2, qw2, out_dtype=torch.float32, split_tail=False)
     for _ in range(3):
@@ -76,7 +83,7 @@ def test_split_bias_nan_rows_and_short_workspace(gpu_device):
     shorter than the shape needs runs the unsplit kernel (same bits)."""
     from lowbit import _lib, ops
 
-    M, N, K = 512, 768, 1024
+    M, N, K = 512, 768, 2304
     x = seeded((M, K), seed=20261104).to(gpu_device)
     w = seeded((N, K), seed=20261105, std=0.02).to(gpu_device)
     b = seeded((N,), seed=20261106, dtype=torch.float32).to(gpu_device)
@@ -145,9 +152,9 @@ def test_split_workspace_shared_across_plans(gpu_device):
     first again; every result matches the unsplit kernel."""
     from lowbit import ops
 
-    big = _operands(2560, 2560, 1024, "e4m3", gpu_device, 20261109)[2:]
-    small = _operands(512, 1024, 1024, "e4m3", gpu_device, 20261110)[2:]
-    assert _splits(2560, 2560, 1024) and _splits(512, 1024, 1024)
+    big = _operands(2560, 2560, 2304, "e4m3", gpu_device, 20261109)[2:]
+    small = _operands(512, 1024, 2304, "e4m3", gpu_device, 20261110)[2:]
+    assert _splits(2560, 2560, 2304) and _splits(512, 1024, 2304)
     stream = torch.cuda.Stream(device=gpu_device)  # its own workspace
     stream.wait_stream(torch.cuda.current_stream())  # the operands were quantized there
     with torch.cuda.stream(stream):
