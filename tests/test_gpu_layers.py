@@ -279,3 +279,39 @@ def test_c3_backward_full_size_sampled(gpu_device):
     xtd = O.quant_tile_128x1_t(np.ascontiguousarray(x.float().numpy()[:, kcols]), grid=O.GRID_E4M3)[3]
     dw_ref = dytd.T.astype(np.float64) @ xtd.astype(np.float64)
     assert rel_fro_bf16(wg.grad[ncols][:, kcols], dw_ref) <= 1e-3
+
+
+def test_forward_step_replays_in_a_hip_graph(gpu_device):
+    """The c1 forward (1x128 X, 128x128 W, blockwise GEMM) captured in a HIP
+    graph: every replay, with eager work on the same stream between replays,
+    gives the eager result bit for bit (new inputs copied into the captured
+    buffers before each replay)."""
+    from lowbit import ops
+
+    g = torch.Generator().manual_seed(20261320)
+    xs = [torch.randn(512, 1024, generator=g).to(gpu_device, torch.bfloat16) for _ in range(3)]
+    ws = [(torch.randn(1024, 1024, generator=g) * 0.02).to(gpu_device, torch.bfloat16) for _ in range(3)]
+
+    def step(x, w):
+        return ops.gemm_blockscaled(ops.quant_tile_1x128(x, fmt="e4m3"), ops.quant_block_128x128(w, fmt="e4m3")[0])
+
+    eager = [step(x, w) for x, w in zip(xs, ws)]
+    xin, win = xs[0].clone(), ws[0].clone()
+    side = torch.cuda.Stream(device=gpu_device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):  # warm the allocator and the libraries outside the capture
+            step(xin, win)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        yout = step(xin, win)
+    for rep in range(3):
+        for i in range(3):
+            xin.copy_(xs[i])
+            win.copy_(ws[i])
+            graph.replay()
+            junk = step(xs[(i + 1) % 3], ws[i])  # eager work between replays
+            torch.cuda.synchronize()
+            assert torch.equal(yout.view(torch.int16), eager[i].view(torch.int16)), f"replay {rep}, input {i}"
+            del junk
