@@ -228,9 +228,66 @@ __device__ __forceinline__ void tile_loads(Chunk8<IN_DT> (&c)[TILE_TU], const Qu
   }
 }
 
+// The fan-out form (expert-parallel send records): the TILE_TU tiles of input
+// row r, each written to the fan_k output rows fan_pos[r * fan_k + f].  Round
+// to nearest quantizes a tile once; stochastic rounding draws each output
+// row's bits from its own element index.  A record's adjacent tile scales go
+// out in one store.
+template <int IN_DT, int GRID, bool SR>
+__device__ __forceinline__ void tile_quant_fan(const Chunk8<IN_DT> (&c)[TILE_TU], const QuantArgs& a, int64_t r,
+                                               int t0, int T, int lane16) {
+  float v[TILE_TU][8], s[TILE_TU];
+  uint32_t m[TILE_TU], lo[TILE_TU], hi[TILE_TU];
+  bool nan[TILE_TU];
+#pragma unroll
+  for (int u = 0; u < TILE_TU; ++u) {
+    chunk_floats<IN_DT>(c[u], v[u]);
+    m[u] = row16_max_u32(chunk_amax<IN_DT>(c[u]));
+    s[u] = scale_from_amax_bits(m[u], a.qmaxf, a.scale_rule);
+    if constexpr (!SR) {
+      uint32_t rb[8];
+      float q[8];
+      nan[u] = quant8_tile<GRID, false, false>(v[u], m[u], s[u], a.qmaxf, rb, lo[u], hi[u], q);
+    }
+  }
+  const int nt = min(TILE_TU, T - t0);
+  for (int64_t f = 0; f < a.fan_k; ++f) {
+    const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + f], 0), a.fan_rows - 1);
+    bool any_nan = false;
+#pragma unroll
+    for (int u = 0; u < TILE_TU; ++u) {
+      if (u >= nt) break;
+      const int64_t k0 = (int64_t)(t0 + u) * 128 + lane16 * 8;
+      if constexpr (SR) {
+        uint32_t rb[8];
+        float q[8];
+        sr_words<true>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
+        nan[u] = quant8_tile<GRID, true, false>(v[u], m[u], s[u], a.qmaxf, rb, lo[u], hi[u], q);
+      }
+      any_nan |= nan[u];
+      *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo[u], hi[u]);
+    }
+    if (lane16 == 0) {
+      float* sp = a.scales + p * a.s_row + (int64_t)t0 * a.s_col;
+      if (TILE_TU == 2 && nt == 2 && a.s_col == 1 && (reinterpret_cast<uintptr_t>(sp) & 7) == 0) {
+        *reinterpret_cast<float2*>(sp) = make_float2(s[0], s[TILE_TU - 1]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < TILE_TU; ++u)
+          if (u < nt) sp[u * a.s_col] = s[u];
+      }
+      if (any_nan && a.nan_rows) atomicOr(a.nan_rows + p * a.nan_stride, 1);
+    }
+  }
+}
+
 template <int IN_DT, int GRID, bool SR, bool DQ, bool FAN>
 __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], const QuantArgs& a, int64_t r, int t0,
                                            int T, int lane16) {
+  if constexpr (FAN) {
+    tile_quant_fan<IN_DT, GRID, SR>(c, a, r, t0, T, lane16);
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < TILE_TU; ++u) {
     const int t = t0 + u;
@@ -240,25 +297,6 @@ __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], co
     uint32_t m = row16_max_u32(chunk_amax<IN_DT>(c[u]));
     const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
     const int64_t k0 = (int64_t)t * 128 + lane16 * 8;
-    if constexpr (FAN) {
-      // one tile, fan_k output rows: round to nearest quantizes once; stochastic
-      // rounding draws each output row's bits from its own element index
-      uint32_t lo, hi, rb[8];
-      float q[8];
-      bool nan = false;
-      if constexpr (!SR) nan = quant8_tile<GRID, false, false>(v, m, s, a.qmaxf, rb, lo, hi, q);
-      for (int64_t k = 0; k < a.fan_k; ++k) {
-        const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + k], 0), a.fan_rows - 1);
-        if constexpr (SR) {
-          sr_words<true>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
-          nan = quant8_tile<GRID, true, false>(v, m, s, a.qmaxf, rb, lo, hi, q);
-        }
-        if (nan && a.nan_rows && lane16 == 0) atomicOr(a.nan_rows + p * a.nan_stride, 1);
-        *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo, hi);
-        if (lane16 == 0) a.scales[p * a.s_row + (int64_t)t * a.s_col] = s;
-      }
-      continue;
-    }
     uint32_t rb[8];
     sr_words<SR>((uint64_t)(r * a.K + k0), a.seed, a.offset, rb);
     uint32_t lo, hi;
