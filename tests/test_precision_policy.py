@@ -85,6 +85,24 @@ def test_fp4_mode_uses_qmax_7_and_code_format_flag():
     assert b.code_format == "e4m3" and b.backward_recipe == "fp8"
 
 
+def test_comm_quant_recipe_defaults_and_overrides():
+    """test_moe_fp8_comm_quant.py:79-88: the deepseek_v3 recipe enables the MoE
+    payload quantization at block_128x128 with stochastic rounding, and
+    --fp8-comm-quant False turns it off; --fp8-comm-granularity replaces the
+    granularity (mixed_precision.py recipe overrides)."""
+    config, _ = _resolver(precision_recipe="deepseek_v3", fp8_backend="hip")
+    r = config.deepseek_v3_recipe
+    assert r.comm_quant_enabled is True
+    assert r.comm_quant_granularity == "block_128x128"
+    assert r.rounding_mode == "stochastic"
+    config, _ = _resolver(precision_recipe="deepseek_v3", fp8_backend="hip", fp8_comm_quant=False)
+    assert config.deepseek_v3_recipe.comm_quant_enabled is False
+    config, _ = _resolver(precision_recipe="deepseek_v3", fp8_backend="hip", fp8_comm_granularity="tensor")
+    assert config.deepseek_v3_recipe.comm_quant_granularity == "tensor"
+    with pytest.raises(ValueError):
+        _resolver(precision_recipe="deepseek_v3", fp8_backend="hip", fp8_comm_granularity="rows")
+
+
 def test_recipe_requires_fp8_and_high_precision_exceptions():
     from lowbit.precision import resolve_precision_config
 
