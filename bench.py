@@ -280,6 +280,9 @@ def other_config(args) -> dict:
                   st)
     f8 = _time_ms(lambda i: persistent.linear_fp8p(x, f8_vals, f8_scale), args.steps, args.warmup, st)
     bf = _time_ms(lambda i: torch.matmul(x, w.t()), args.steps, args.warmup, st)
+    # the unfused alternative: the NF4 dequant kernel to a bf16 weight, then torch's bf16 matmul
+    unf = _time_ms(lambda i: torch.matmul(x, persistent.dequantize_nf4_blocks(
+        pk, sc, num_values=N * K, block=64, target_dtype=torch.bfloat16).view(N, K).t()), args.steps, args.warmup, st)
     fl = 2.0 * M * N * K
     res.update(value=round(fl / (nf4 * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(nf4, 4), dtype="bf16",
                config={"workload": "c5 NF4 (64-element blocks) dequant-fused GEMM", "M": M, "N": N, "K": K},
@@ -289,7 +292,8 @@ def other_config(args) -> dict:
                fp8_persistent_tflops=round(fl / (f8 * 1e-3) / 1e12, 2),
                adamw_nf4_refresh={"fused_us": round(fused_ms * 1e3, 1), "two_pass_us": round(two_ms * 1e3, 1),
                                   "fused_GB/s": round(opt_bytes / (fused_ms * 1e-3) / 1e9, 1), "params": n},
-               torch_bf16_matmul_tflops=round(fl / (bf * 1e-3) / 1e12, 2))
+               torch_bf16_matmul_tflops=round(fl / (bf * 1e-3) / 1e12, 2),
+               nf4_dequant_then_torch_matmul_tflops=round(fl / (unf * 1e-3) / 1e12, 2))
     return res
 
 
