@@ -638,12 +638,12 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
         const uint8_t* src = stage_w + row * pitch + c * 16;
         uint8_t* ydst = reinterpret_cast<uint8_t*>(e_y) + (m * ldy + n) * esz;
         if constexpr (FULL) {
-          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+          store16_nt(ydst, src);
           continue;
         }
         if (m >= M || n >= N) continue;
         if ((e_misc & 1) && n + epc <= N) {
-          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+          store16_nt(ydst, src);
         } else {
           // ragged edge or unaligned output: element by element
           using E = std::conditional_t<esz == 4, uint32_t, uint16_t>;

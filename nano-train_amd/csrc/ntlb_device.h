@@ -19,6 +19,15 @@ enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
+// 16 bytes stored with the non-temporal hint (a vector store with the nt
+// bit).  For GEMM outputs the kernel never reads back: streaming them past L2
+// leaves its capacity to the operand tiles the neighbouring workgroups re-read.
+__device__ __forceinline__ void store16_nt(void* dst, const void* src) {
+  typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(1))) u32x4_nt* global_u32x4_nt;
+  __builtin_nontemporal_store(*reinterpret_cast<const u32x4_nt*>(src), (global_u32x4_nt)dst);
+}
+
 // a 64-bit value that is the same in every lane, as a scalar (lets values
 // the compiler cannot prove uniform be pinned in scalar registers)
 template <typename T>

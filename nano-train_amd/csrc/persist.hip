@@ -854,12 +854,12 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
         const uint8_t* src = stage_w + row * pitch + c * 16;
         uint8_t* ydst = reinterpret_cast<uint8_t*>(e_y) + (m * e_ldy + n) * esz;
         if constexpr (FULL) {
-          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+          store16_nt(ydst, src);
           continue;
         }
         if (m >= e_M || n >= e_N) continue;
         if (e_vec && n + epc <= e_N) {
-          *reinterpret_cast<uint4*>(ydst) = *reinterpret_cast<const uint4*>(src);
+          store16_nt(ydst, src);
         } else {
           using E = std::conditional_t<esz == 4, uint32_t, uint16_t>;
 #pragma nounroll
