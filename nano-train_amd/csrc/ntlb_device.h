@@ -20,8 +20,10 @@ enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
 // 16 bytes stored with the non-temporal hint (a vector store with the nt
-// bit).  For GEMM outputs the kernel never reads back: streaming them past L2
-// leaves its capacity to the operand tiles the neighbouring workgroups re-read.
+// bit), for GEMM outputs that the kernel never reads back.  Measured at the
+// c2 shape: the GEMM runs 4-5% faster with its read traffic unchanged, and
+// the quantizers launched after it no longer slow down behind its output
+// (X 1x128: 41 -> 32 us, W 128x128: 80 -> 70 us).
 __device__ __forceinline__ void store16_nt(void* dst, const void* src) {
   typedef unsigned int u32x4_nt __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(1))) u32x4_nt* global_u32x4_nt;
