@@ -19,6 +19,14 @@ enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
+// 8 bytes (two words) stored with the non-temporal hint
+__device__ __forceinline__ void store8_nt(void* dst, uint32_t lo, uint32_t hi) {
+  typedef unsigned int u32x2_nt __attribute__((ext_vector_type(2)));
+  typedef __attribute__((address_space(1))) u32x2_nt* global_u32x2_nt;
+  const u32x2_nt v = {lo, hi};
+  __builtin_nontemporal_store(v, (global_u32x2_nt)dst);
+}
+
 // 16 bytes stored with the non-temporal hint (a vector store with the nt
 // bit), for GEMM outputs that the kernel never reads back.  Measured at the
 // c2 shape: the GEMM runs 4-5% faster with its read traffic unchanged, and

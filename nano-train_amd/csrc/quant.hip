@@ -265,7 +265,13 @@ __device__ __forceinline__ void tile_quant_fan(const Chunk8<IN_DT> (&c)[TILE_TU]
         nan[u] = quant8_tile<GRID, true, false>(v[u], m[u], s[u], a.qmaxf, rb, lo[u], hi[u], q);
       }
       any_nan |= nan[u];
-      *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo[u], hi[u]);
+      // the dispatch records (fan_k > 1) go out with the non-temporal hint:
+      // 10% faster at c4 (76 -> 68 us); the send-back pack (fan_k == 1)
+      // measured 7% slower with it and stores normally
+      if (a.fan_k > 1)
+        store8_nt(a.codes + p * a.ldc + k0, lo[u], hi[u]);
+      else
+        *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo[u], hi[u]);
     }
     if (lane16 == 0) {
       float* sp = a.scales + p * a.s_row + (int64_t)t0 * a.s_col;
