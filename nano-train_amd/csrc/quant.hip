@@ -716,7 +716,8 @@ __global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const 
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         w[i] = (uint32_t)f32_to_bf16_bits(o[2 * i]) | ((uint32_t)f32_to_bf16_bits(o[2 * i + 1]) << 16);
-      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + r * ldo + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+      // non-temporal: the straight-through value at c4 takes 335 us instead of 365
+      store16_nt(reinterpret_cast<uint16_t*>(out) + r * ldo + k0, w);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
@@ -1148,7 +1149,8 @@ __global__ void __launch_bounds__(256) dequant_fast_kernel(const uint8_t* codes,
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         w[i] = (uint32_t)f32_to_bf16_bits(v[2 * i]) | ((uint32_t)f32_to_bf16_bits(v[2 * i + 1]) << 16);
-      *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + r * ldo + k0) = make_uint4(w[0], w[1], w[2], w[3]);
+      // non-temporal: the c4 payload dequant takes 120 us instead of 150
+      store16_nt(reinterpret_cast<uint16_t*>(out) + r * ldo + k0, w);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) store_elem(out, out_dtype, r * ldo + k0 + i, v[i]);
