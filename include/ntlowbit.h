@@ -227,6 +227,77 @@ int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda, const floa
 int64_t ntlb_gemm_workspace_bytes(int64_t M, int64_t N, int64_t Kp);
 
 /*
+ * GEMMs over the operands the reference actually multiplies.  The emulated
+ * backend casts every dequantized operand back to the input dtype
+ * (`.to(dtype=x.dtype)`, te_backend.py:173, :185, :193, :202) before its fp32
+ * F.linear (te_backend.py:253-259), so for bf16 inputs each operand is
+ * bf16(q * s).  These entry points decode codes + scales to exactly those
+ * values inside the GEMM's tile prologue (no dequantized tensor is written)
+ * and multiply them on bf16 MFMA (fp32 MFMA for op_dtype NTLB_F32) with fp32
+ * accumulation: products of bf16 values are exact in fp32, so the result is
+ * the reference's fp32 GEMM up to the order of the fp32 additions.
+ *   op_dtype  the dtype the reference rounds the dequantized operands to:
+ *             NTLB_BF16 or NTLB_F32 (NTLB_EUNSUPPORTED otherwise)
+ * Codes, scales and their indexing follow ntlb_gemm_blockscaled: scale of
+ * element (row, k) = s[(row >> shift) * s_row + (k >> 7) * s_col].  Int-grid
+ * code -128 (a NaN element) decodes to NaN.
+ */
+
+/* Forward of EmulatedLowBitBackend.linear (te_backend.py:229-260) with the
+ * reference's operand rounding: Y = bf16(dq(A)) . bf16(dq(B))^T + bias, cast
+ * to y_dtype.  Same arguments as ntlb_gemm_blockscaled without the NaN flags
+ * (NaN codes decode to NaN and propagate through the products). */
+int ntlb_gemm_dq_forward(int op_dtype, int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                         int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, const float* sb, int64_t sb_row,
+                         int64_t sb_col, int b_shift, int64_t M, int64_t N, int64_t Kp, const void* bias,
+                         int bias_dtype, void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* Input gradient of the straight-through estimator (autograd of
+ * te_backend.py:250-259): dX[M, K] = dY[M, N] . bf16(dq(W))[N, K], fp32
+ * accumulation, cast to dx_dtype.  dY is the unquantized bf16 gradient, row
+ * stride lddy >= N rounded up to 64 with ZERO pad columns [N, that), 16-byte
+ * rows; W the forward's codes [N, ldw] with its scales (w_shift, sw_row,
+ * sw_col as ntlb_gemm_blockscaled's B operand), read in place as the
+ * transposed operand.  op_dtype NTLB_BF16 only; N > 0 (M or K == 0: no-op). */
+int ntlb_gemm_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid, const uint8_t* w,
+                        int64_t ldw, const float* sw, int64_t sw_row, int64_t sw_col, int w_shift, int64_t K, void* dx,
+                        int dx_dtype, int64_t lddx, void* stream);
+
+/* Weight gradient of the straight-through estimator: dW[N, K] =
+ * dY[M, N]^T . bf16(dq(X))[M, K], fp32 accumulation over the M tokens, cast
+ * to dw_dtype.  dY bf16 [M, N] (lddy % 8 == 0) and X's codes [M, ldx] are both
+ * read in place as transposed operands; any M > 0 (the contraction is
+ * zero-padded inside the kernel).  op_dtype NTLB_BF16 only. */
+int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid, const uint8_t* x,
+                        int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col, int x_shift, int64_t K, void* dw,
+                        int dw_dtype, int64_t lddw, void* stream);
+
+/* Y[M, N] = A[M, K] . op(B) + bias over bf16 or fp32 matrices (op_dtype), for
+ * the dequantized tensors of granularities whose scales change along the
+ * contraction element by element (the activation "channel" granularity of
+ * te_backend.py:175-185).  A row-major [M, K] (a_trans must be 0); B [N, K]
+ * (b_trans 0) or [K, N] (b_trans 1).  K a multiple of 64 (bf16) / 32 (fp32),
+ * rows 16-byte aligned. */
+int ntlb_gemm_dense(int op_dtype, const void* a, int64_t lda, int a_trans, const void* b, int64_t ldb, int b_trans,
+                    int64_t M, int64_t N, int64_t K, const void* bias, int bias_dtype, void* y, int y_dtype,
+                    int64_t ldy, void* stream);
+
+/* Y[M, N] = A^T . B with A stored [K, M] and B stored [K, N] (the weight
+ * gradient dY^T . X_dq over dequantized tensors); any K. */
+int ntlb_gemm_dense_tn(int op_dtype, const void* a, int64_t lda, const void* b, int64_t ldb, int64_t M, int64_t N,
+                       int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
+
+/* Bias gradient of F.linear (te_backend.py:253-259 under autograd):
+ * out[n] = sum over m of x[m, n] in fp32, cast to out_dtype.  Deterministic:
+ * fp32 partials per 256-row chunk in `workspace` (fp32, at least
+ * ntlb_colsum_workspace_bytes(M, N) bytes), added in chunk order. */
+int ntlb_colsum(const void* x, int x_dtype, int64_t M, int64_t N, int64_t ldx, float* workspace, int64_t ws_bytes,
+                void* out, int out_dtype, void* stream);
+
+/* Workspace bytes of ntlb_colsum. */
+int64_t ntlb_colsum_workspace_bytes(int64_t M, int64_t N);
+
+/*
  * Grouped (per-expert) blockwise-scaled GEMM over a token-offset table.
  * Replaces the per-expert loop of _run_local_experts (moe.py:888-962) /
  * _forward_single_rank (moe.py:1062-1097) in which every expert's Linear runs

@@ -71,6 +71,14 @@ SIGNATURES = {
     "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_fp8p": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_workspace_bytes": [_I64, _I64, _I64],
+    "ntlb_gemm_dq_forward": [_I32, _I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64,
+                             _I64, _P, _I32, _P, _I32, _I64, _P],
+    "ntlb_gemm_ste_dgrad": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_ste_wgrad": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_dense": [_I32, _P, _I64, _I32, _P, _I64, _I32, _I64, _I64, _I64, _P, _I32, _P, _I32, _I64, _P],
+    "ntlb_gemm_dense_tn": [_I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_colsum": [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P],
+    "ntlb_colsum_workspace_bytes": [_I64, _I64],
     "ntlb_ep_record_bytes": [_I64],
     "ntlb_ep_partition": [_P, _I32, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P],
     "ntlb_ep_pack_records": [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P, _I32, _I64, _I64, _I32, _I32, _I32,
@@ -86,7 +94,7 @@ SIGNATURES = {
 }
 
 # entry points that return a value instead of a status
-RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64}
+RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64, "ntlb_colsum_workspace_bytes": _I64}
 
 _lib = None
 _lock = threading.Lock()

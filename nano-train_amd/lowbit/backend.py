@@ -9,22 +9,33 @@ for the availability probe of mixed_precision.py:759-760).
 
 Forward (te_backend.py:229-260): the activation is quantized with the
 activation granularity along its last axis, the weight with the weight
-granularity along axis 0, and Y = X_dq @ W_dq^T + bias is computed by the
-blockwise-scaled GEMM straight from codes and scales (fp32 accumulation), cast
-to the input dtype.  Codes and scales are bit-exact with the reference
-formulas; the GEMM matches the fp32 dequantize-then-matmul result.
+granularity along axis 0.  Two forward modes:
+
+- ``forward="blockscaled"`` (default): Y = X_dq @ W_dq^T + bias on the
+  blockwise-scaled GEMM straight from codes and scales (fp8 or int8 MFMA per
+  128-K block, scales applied in fp32), i.e. the fp32 q * s operands;
+- ``forward="reference"``: the operands the reference multiplies, each
+  dequantized value rounded to the input dtype (bf16(q * s),
+  te_backend.py:173-202), decoded inside a bf16-MFMA GEMM (fp32 for fp32
+  inputs).
+
+Codes and scales are bit-exact with the reference formulas in both modes.
 
 Backward: ``backward="ste"`` (default) is the reference's straight-through
-estimator (te_backend.py:250-251): dX = dY @ W_dq and dW = dY^T @ X_dq with dY
-unquantized, as plain GEMMs over the dequantized operands the forward
-quantizers wrote.  ``backward="fp8"`` is the DeepSeek-V3 recipe of BASELINE
-config 3 (no reference counterpart): dY is quantized per 1x128 tile for dgrad,
-dY^T and X^T per 128x1 tile for wgrad, and both run on the blockwise GEMM.
+estimator (te_backend.py:250-259 under autograd): dX = dY @ W_q and
+dW = dY^T @ X_q with dY unquantized and W_q, X_q the dequantized operands in
+the input dtypes.  For bf16 layers both GEMMs decode the forward's codes
+inside the kernel (no dequantized tensor is written); other dtypes multiply
+the dequantized tensors on the fp32-MFMA GEMM.  db is a HIP column sum.
+``backward="fp8"`` is the DeepSeek-V3 recipe of BASELINE config 3 (no
+reference counterpart): dY is quantized per 1x128 tile for dgrad, dY^T and
+X^T per 128x1 tile for wgrad, and both run on the blockwise GEMM.
 
-Granularities that are not expressible as per-row or per-128-block scales of
-a contraction block (the activation "channel" granularity scales each K
-column separately) dequantize both operands with the HIP quantizers and
-multiply the fp32 dequantized operands with a plain library GEMM.
+The activation "channel" granularity scales each K column separately, which
+cannot be factored out of a contraction block: both operands are
+dequantized by the HIP quantizers and multiplied on the dense GEMM of
+ntlb_gemm_dense (fp32 operands in blockscaled mode, the input dtypes in
+reference mode).
 
 There is no CPU path: CPU tensors raise.
 """
@@ -36,7 +47,7 @@ import threading
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
+import torch.nn.functional as F  # noqa: F401  (the empty-input path)
 
 from . import _lib
 from . import ops
@@ -90,7 +101,7 @@ def quantize_operand(
                                                        want_nan_rows=True, **common)
             return QTensor(codes, scales, 1, 0, 0, ops.grid_code(fmt), R, K, nan, dq), dq
         # axis -1: one scale per K column over all rows -> not a GEMM-side scale
-        _, _, dq, _ = ops.quant_grouped(t2d, R, 1, want_dq=True, dq_dtype=torch.float32, **common)
+        _, _, dq, _ = ops.quant_grouped(t2d, R, 1, want_dq=True, dq_dtype=dq_dtype, **common)
         return None, dq
     # any other granularity string: _ste_fake_quantize (te_backend.py:40-58):
     # per-tensor, round to nearest, amax checked before the division
@@ -98,6 +109,13 @@ def quantize_operand(
         t2d, R, K, ldc=Kp, fmt=fmt, bits=bits, rounding="nearest", seed=seed, offset=offset,
         scale_rule=_lib.SCALE_BEFORE_DIVIDE, want_dq=want_dq, dq_dtype=dq_dtype, want_nan_rows=True)
     return QTensor(codes, scales, 0, 0, 0, ops.grid_code(fmt), R, K, nan, dq), dq
+
+
+def _gemm_op_dtype(*dts: torch.dtype) -> torch.dtype:
+    """The MFMA operand type that carries the reference's values exactly:
+    bf16 when every operand is bf16, else fp32 (bf16, fp16 and fp32 values
+    are all exact in fp32, where the reference runs its F.linear)."""
+    return torch.bfloat16 if all(d == torch.bfloat16 for d in dts) else torch.float32
 
 
 class _HipLowBitLinear(torch.autograd.Function):
@@ -114,39 +132,51 @@ class _HipLowBitLinear(torch.autograd.Function):
         need_x_grad = ctx.needs_input_grad[0]
         need_w_grad = ctx.needs_input_grad[1]
         ste = backend.backward_recipe == "ste"
+        xdt, wdt = x.dtype, weight.dtype
+        act_channel = backend._activation_granularity == "channel"
+        # the straight-through gradients decode the forward's codes when the
+        # reference's operands are bf16 (dY and X_q in x's dtype, W_q in w's)
+        dgrad_codes = ste and need_x_grad and xdt == torch.bfloat16 and wdt == torch.bfloat16
+        wgrad_codes = ste and need_w_grad and xdt == torch.bfloat16 and not act_channel
+        ref_fwd = backend.forward_mode == "reference"
+        ref_codes = ref_fwd and xdt == wdt and xdt in (torch.bfloat16, torch.float32)
+        fwd_dq = act_channel or (ref_fwd and not ref_codes)
+        # dequantized tensors: for the forward, in the input dtypes (reference
+        # mode, te_backend.py:173-202) or fp32 (blockscaled mode's q * s
+        # operands); the backward rounds them to the input dtypes
+        x_dq_dt = xdt if (ref_fwd or not fwd_dq) else torch.float32
+        w_dq_dt = wdt if (ref_fwd or not fwd_dq) else torch.float32
+        want_xdq = fwd_dq or (ste and need_w_grad and not wgrad_codes)
+        want_wdq = fwd_dq or (ste and need_x_grad and not dgrad_codes)
         qx, xdq = quantize_operand(
             x2, backend._activation_granularity, is_weight=False, original_dim=x.dim(), fmt=fmt, bits=bits,
-            rounding=rnd, seed=seed, offset=base + 0, want_dq=ste and need_w_grad, dq_dtype=x.dtype)
+            rounding=rnd, seed=seed, offset=base + 0, want_dq=want_xdq, dq_dtype=x_dq_dt)
         qw, wdq = quantize_operand(
             weight, backend._weight_granularity, is_weight=True, original_dim=weight.dim(), fmt=fmt, bits=bits,
-            rounding=rnd, seed=seed, offset=base + 1, want_dq=(ste and need_x_grad) or qx is None,
-            dq_dtype=torch.float32 if qx is None else weight.dtype)
-        if qx is not None and qw is not None:
-            y2 = ops.gemm_blockscaled(qx, qw, bias=bias, out_dtype=out_dtype)
+            rounding=rnd, seed=seed, offset=base + 1, want_dq=want_wdq, dq_dtype=w_dq_dt)
+        if fwd_dq:
+            # multiplied in fp32 (bf16 MFMA when both operands are bf16)
+            op = _gemm_op_dtype(xdq.dtype, wdq.dtype)
+            y2 = ops.gemm_dense(xdq.to(op), wdq.to(op), bias=bias, out_dtype=out_dtype)
+        elif ref_fwd:
+            y2 = ops.gemm_dq_forward(qx, qw, bias=bias, out_dtype=out_dtype, op_dtype=xdt)
         else:
-            # activation 'channel' granularity: per-K-column scales cannot be
-            # promoted per contraction block; multiply the fp32 dequantized operands
-            if wdq is None or wdq.dtype != torch.float32:
-                _, wdq32 = quantize_operand(
-                    weight, backend._weight_granularity, is_weight=True, original_dim=weight.dim(), fmt=fmt,
-                    bits=bits, rounding=rnd, seed=seed, offset=base + 1, want_dq=True, dq_dtype=torch.float32)
-            else:
-                wdq32 = wdq
-            with torch.autocast(device_type="cuda", enabled=False):
-                y2 = F.linear(xdq.float(), wdq32, None if bias is None else bias.float()).to(out_dtype)
-            if xdq is not None:
-                xdq = xdq.to(x.dtype)
-            wdq = wdq32.to(weight.dtype)
+            y2 = ops.gemm_blockscaled(qx, qw, bias=bias, out_dtype=out_dtype)
         y = y2.reshape(*x.shape[:-1], N)
         ctx.backend = backend
         ctx.has_bias = bias is not None
         ctx.bias_dtype = None if bias is None else bias.dtype
         ctx.x_shape = x.shape
-        ctx.x_dtype = x.dtype
-        ctx.w_dtype = weight.dtype
+        ctx.x_dtype = xdt
+        ctx.w_dtype = wdt
         ctx.offset = base
         if ste:
-            ctx.save_for_backward(xdq if need_w_grad else None, wdq if need_x_grad else None)
+            # codes (and dequantized tensors where the codes path does not
+            # apply) are intermediates of this call, kept on ctx
+            ctx.qx = qx if wgrad_codes else None
+            ctx.qw = qw if dgrad_codes else None
+            ctx.xdq = xdq if (need_w_grad and not wgrad_codes) else None
+            ctx.wdq = wdq if (need_x_grad and not dgrad_codes) else None
         else:
             ctx.save_for_backward(x2, weight)
         return y
@@ -154,21 +184,31 @@ class _HipLowBitLinear(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         backend: HipLowBitBackend = ctx.backend
-        K = ctx.x_shape[-1]
         dy2 = dy.reshape(-1, dy.shape[-1])
         if dy2.stride(-1) != 1:
             dy2 = dy2.contiguous()
         dx = dw = db = None
         if backend.backward_recipe == "ste":
-            xdq, wdq = ctx.saved_tensors
-            # te_backend.py:250-259 under autograd: fp32 GEMMs over the
-            # dequantized operands, results cast to the input / weight dtype
-            cdt = dy2.dtype if dy2.dtype in (torch.bfloat16, torch.float16, torch.float32) else torch.float32
-            with torch.autocast(device_type="cuda", enabled=False):
-                if ctx.needs_input_grad[0]:
-                    dx = torch.matmul(dy2.to(cdt), wdq.to(cdt)).to(ctx.x_dtype).reshape(ctx.x_shape)
-                if ctx.needs_input_grad[1]:
-                    dw = torch.matmul(dy2.t().to(cdt), xdq.to(cdt)).to(ctx.w_dtype)
+            # te_backend.py:250-259 under autograd: dX = dY @ W_q and
+            # dW = dY^T @ X_q in fp32 over the operands the forward multiplied,
+            # cast to the input / weight dtype
+            if ctx.needs_input_grad[0]:
+                if ctx.qw is not None and dy2.dtype == torch.bfloat16:
+                    dx = ops.ste_dgrad(dy2, ctx.qw, out_dtype=ctx.x_dtype)
+                else:
+                    # W_q in the weight dtype, then the fp32 (or all-bf16) GEMM
+                    wdq = ctx.wdq.to(ctx.w_dtype) if ctx.wdq is not None else ops.dequant(ctx.qw, out_dtype=ctx.w_dtype)
+                    op = _gemm_op_dtype(dy2.dtype, wdq.dtype)
+                    dx = ops.gemm_dense(dy2.to(op), wdq.to(op), b_transposed=True, out_dtype=ctx.x_dtype)
+                dx = dx.reshape(ctx.x_shape)
+            if ctx.needs_input_grad[1]:
+                if ctx.qx is not None and dy2.dtype == torch.bfloat16:
+                    dw = ops.ste_wgrad(dy2, ctx.qx, out_dtype=ctx.w_dtype)
+                else:
+                    xdq = ctx.xdq.to(ctx.x_dtype) if ctx.xdq is not None else ops.dequant(ctx.qx, out_dtype=ctx.x_dtype)
+                    op = _gemm_op_dtype(dy2.dtype, xdq.dtype)
+                    dw = ops.gemm_dense_tn(dy2.to(op), xdq.to(op), out_dtype=ctx.w_dtype)
+            ctx.qx = ctx.qw = ctx.xdq = ctx.wdq = None
         else:
             x2, weight = ctx.saved_tensors
             dx, dw = _fp8_recipe_backward(backend, dy2, x2, weight, ctx.offset, ctx.needs_input_grad)
@@ -177,7 +217,7 @@ class _HipLowBitLinear(torch.autograd.Function):
             if dw is not None:
                 dw = dw.to(ctx.w_dtype)
         if ctx.has_bias and ctx.needs_input_grad[2]:
-            db = dy2.float().sum(dim=0).to(ctx.bias_dtype)
+            db = ops.colsum(dy2, out_dtype=ctx.bias_dtype)
         return dx, dw, db, None
 
 
@@ -221,6 +261,7 @@ class HipLowBitBackend:
         kernel_spec=None,
         code_format: str = "int_grid",
         backward: str = "ste",
+        forward: str = "blockscaled",
         seed: Optional[int] = None,
     ) -> None:
         if mode not in ("fp8", "fp4"):
@@ -231,11 +272,14 @@ class HipLowBitBackend:
             raise ValueError("the e4m3 code format needs fp8 mode")
         if backward not in ("ste", "fp8"):
             raise ValueError("backward must be ste or fp8")
+        if forward not in ("blockscaled", "reference"):
+            raise ValueError("forward must be blockscaled or reference")
         _lib.lib()  # fail loudly at construction when the kernels are missing
         self.mode = mode
         self.bits = _bits_for_mode(mode)
         self.code_format = code_format
         self.backward_recipe = backward
+        self.forward_mode = forward
         # te_backend.py:221-227: defaults and kernel-spec overrides
         self._activation_granularity = "tensor"
         self._weight_granularity = "tensor"
@@ -280,5 +324,6 @@ def build_hip_backend(config, *, mode: str, kernel_spec) -> HipLowBitBackend:
         kernel_spec=kernel_spec,
         code_format=str(getattr(config, "lowbit_code_format", "int_grid")),
         backward=str(getattr(config, "lowbit_backward", "ste")),
+        forward=str(getattr(config, "lowbit_forward", "blockscaled")),
         seed=getattr(config, "lowbit_seed", None),
     )

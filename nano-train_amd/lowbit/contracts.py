@@ -32,6 +32,7 @@ PrecisionRecipeName = Literal["default", "deepseek_v3"]
 # MI355X backend only: how codes are represented on the wire and in the GEMM
 LowBitCodeFormat = Literal["int_grid", "e4m3"]
 LowBitBackwardRecipe = Literal["ste", "fp8"]
+LowBitForwardMode = Literal["blockscaled", "reference"]
 
 
 @dataclass(frozen=True)
@@ -141,5 +142,6 @@ class PrecisionConfig:
     # MI355X backend: code format and backward recipe (no reference counterpart)
     lowbit_code_format: LowBitCodeFormat = "int_grid"
     lowbit_backward: LowBitBackwardRecipe = "ste"
+    lowbit_forward: LowBitForwardMode = "blockscaled"
     lowbit_seed: Optional[int] = None
     extra: dict = field(default_factory=dict)

@@ -489,3 +489,166 @@ def gemm_swiglu_quant(
         call("ntlb_gemm_swiglu_quant", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
              a.s_col, a.shift, b_codes.data_ptr(), b_codes.stride(0), b_scales.data_ptr(), tb, 1, M, N, a.Kp, *tail)
     return h, QTensor(hc, hs, 1, rp, 0, a.grid, M, I, hn, None)
+
+
+# ---------------------------------------------------------------------------
+# GEMMs over the operands the reference multiplies: bf16(q * s) (or fp32)
+# decoded inside the GEMM, plus plain GEMMs over dequantized tensors
+# ---------------------------------------------------------------------------
+_OP_DTYPES = {torch.bfloat16: _lib.BF16, torch.float32: _lib.F32}
+
+
+def op_dtype_code(dt: torch.dtype) -> int:
+    """The MFMA operand type for a reference dtype: bf16 or fp32 only."""
+    try:
+        return _OP_DTYPES[dt]
+    except KeyError as exc:
+        raise TypeError(f"the dequantized-operand GEMMs take bfloat16 or float32 operands, not {dt}") from exc
+
+
+def _kstep(op_dtype: torch.dtype) -> int:
+    return 64 if op_dtype == torch.bfloat16 else 32
+
+
+def _pad_cols(t: torch.Tensor, mult: int) -> torch.Tensor:
+    """t [R, C] with C rounded up to `mult` (zero columns) and 16-byte rows."""
+    R, C = t.shape
+    Cp = cdiv(max(C, 1), mult) * mult
+    if Cp == C and t.stride(-1) == 1 and (t.stride(0) * t.element_size()) % 16 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    out = torch.zeros((R, Cp), dtype=t.dtype, device=t.device)
+    out[:, :C] = t
+    return out
+
+
+def gemm_dq_forward(a: QTensor, b: QTensor, *, bias: Optional[torch.Tensor] = None,
+                    out_dtype: torch.dtype = torch.bfloat16, op_dtype: torch.dtype = torch.bfloat16,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Y[M, N] = op(dq(a)) @ op(dq(b))^T + bias with op = rounding to op_dtype
+    (te_backend.py:229-260 as the reference runs it: each dequantized operand
+    cast to the input dtype, then an fp32 GEMM)."""
+    _require_device(a.codes, b.codes, bias)
+    if a.grid != b.grid:
+        raise ValueError("operands must share a code format")
+    if a.K != b.K:
+        raise ValueError(f"contraction mismatch: {a.K} vs {b.K}")
+    M, N, Kp = a.rows, b.rows, a.Kp
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=a.codes.device)
+    if bias is not None and bias.stride(-1) != 1:
+        bias = bias.contiguous()
+    call("ntlb_gemm_dq_forward", op_dtype_code(op_dtype), a.grid, a.codes.data_ptr(), a.codes.stride(0),
+         a.scales.data_ptr(), a.s_row, a.s_col, a.shift, b.codes.data_ptr(), b.codes.stride(0), b.scales.data_ptr(),
+         b.s_row, b.s_col, b.shift, M, N, Kp, _ptr(bias), _dtype_code(bias.dtype) if bias is not None else 0,
+         out.data_ptr(), _dtype_code(out.dtype), out.stride(0), _stream())
+    return out
+
+
+def ste_dgrad(dy: torch.Tensor, w: QTensor, *, out_dtype: torch.dtype) -> torch.Tensor:
+    """dX[M, K] = dY[M, N] @ bf16(dq(w))[N, K] (the straight-through input
+    gradient of te_backend.py:250-259), decoded from the forward's weight codes."""
+    _require_device(dy, w.codes)
+    if dy.dtype != torch.bfloat16:
+        raise TypeError("ste_dgrad takes a bfloat16 dY")
+    M, N = dy.shape
+    if N != w.rows:
+        raise ValueError(f"dY has {N} columns, the weight {w.rows} rows")
+    dyp = _pad_cols(dy, 64)
+    out = torch.empty((M, w.K), dtype=out_dtype, device=dy.device)
+    call("ntlb_gemm_ste_dgrad", _lib.BF16, dyp.data_ptr(), dyp.stride(0), M, N, w.grid, w.codes.data_ptr(),
+         w.codes.stride(0), w.scales.data_ptr(), w.s_row, w.s_col, w.shift, w.K, out.data_ptr(),
+         _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def ste_wgrad(dy: torch.Tensor, x: QTensor, *, out_dtype: torch.dtype) -> torch.Tensor:
+    """dW[N, K] = dY[M, N]^T @ bf16(dq(x))[M, K] (the straight-through weight
+    gradient), decoded from the forward's activation codes."""
+    _require_device(dy, x.codes)
+    if dy.dtype != torch.bfloat16:
+        raise TypeError("ste_wgrad takes a bfloat16 dY")
+    M, N = dy.shape
+    if M != x.rows:
+        raise ValueError(f"dY has {M} rows, the activation {x.rows}")
+    if dy.stride(-1) != 1 or dy.stride(0) % 8 or dy.data_ptr() % 16:
+        dy = _pad_cols(dy, 8)
+    out = torch.empty((N, x.K), dtype=out_dtype, device=dy.device)
+    call("ntlb_gemm_ste_wgrad", _lib.BF16, dy.data_ptr(), dy.stride(0), M, N, x.grid, x.codes.data_ptr(),
+         x.codes.stride(0), x.scales.data_ptr(), x.s_row, x.s_col, x.shift, x.K, out.data_ptr(),
+         _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def gemm_dense(a: torch.Tensor, b: torch.Tensor, *, b_transposed: bool = False, bias: Optional[torch.Tensor] = None,
+               out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Y = a @ b^T (b [N, K]) or a @ b (b_transposed: b [K, N]) + bias over
+    bf16 or fp32 matrices of one dtype, fp32 accumulation."""
+    _require_device(a, b, bias)
+    if a.dtype != b.dtype:
+        raise TypeError(f"operand dtypes differ: {a.dtype} vs {b.dtype}")
+    code = op_dtype_code(a.dtype)
+    M, K = a.shape
+    step = _kstep(a.dtype)
+    ap = _pad_cols(a, step)
+    if b_transposed:
+        if b.shape[0] != K:
+            raise ValueError(f"contraction mismatch: {K} vs {b.shape[0]}")
+        N = b.shape[1]
+        bp = _pad_cols(b, 16 // b.element_size())
+        # rows of B past K are zero inside the kernel; A's pad columns are zero
+        bp_rows = torch.zeros((ap.shape[1], bp.shape[1]), dtype=b.dtype, device=b.device) if ap.shape[1] != K else bp
+        if bp_rows is not bp:
+            bp_rows[:K] = bp
+        bp = bp_rows
+    else:
+        if b.shape[1] != K:
+            raise ValueError(f"contraction mismatch: {K} vs {b.shape[1]}")
+        N = b.shape[0]
+        bp = _pad_cols(b, step)
+    if bias is not None and bias.stride(-1) != 1:
+        bias = bias.contiguous()
+    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    call("ntlb_gemm_dense", code, ap.data_ptr(), ap.stride(0), 0, bp.data_ptr(), bp.stride(0), int(b_transposed), M, N,
+         ap.shape[1], _ptr(bias), _dtype_code(bias.dtype) if bias is not None else 0, out.data_ptr(),
+         _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def gemm_dense_tn(a: torch.Tensor, b: torch.Tensor, *, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Y[M, N] = a^T @ b for a [K, M], b [K, N] (the weight gradient over
+    dequantized tensors), fp32 accumulation."""
+    _require_device(a, b)
+    if a.dtype != b.dtype:
+        raise TypeError(f"operand dtypes differ: {a.dtype} vs {b.dtype}")
+    code = op_dtype_code(a.dtype)
+    K, M = a.shape
+    if b.shape[0] != K:
+        raise ValueError(f"contraction mismatch: {K} vs {b.shape[0]}")
+    N = b.shape[1]
+    mult = 16 // a.element_size()
+    ap, bp = _pad_cols(a, mult), _pad_cols(b, mult)
+    out = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    call("ntlb_gemm_dense_tn", code, ap.data_ptr(), ap.stride(0), bp.data_ptr(), bp.stride(0), M, N, K,
+         out.data_ptr(), _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+_colsum_ws: dict = {}
+
+
+def colsum(x: torch.Tensor, *, out_dtype: torch.dtype) -> torch.Tensor:
+    """sum over rows of x [M, N] in fp32, cast to out_dtype (F.linear's bias
+    gradient), in a fixed order."""
+    _require_device(x)
+    x2 = _as_2d(x)
+    M, N = x2.shape
+    out = torch.empty((N,), dtype=out_dtype, device=x.device)
+    need = int(_lib.lib().ntlb_colsum_workspace_bytes(M, N))
+    key = (x.device.index, _stream())
+    ws = _colsum_ws.get(key)
+    if ws is None or ws.numel() * 4 < max(need, 4):
+        ws = torch.empty((max(need, 4) + 3) // 4, dtype=torch.float32, device=x.device)
+        _colsum_ws[key] = ws
+    call("ntlb_colsum", x2.data_ptr(), _dtype_code(x2.dtype), M, N, x2.stride(0), ws.data_ptr(), ws.numel() * 4,
+         out.data_ptr(), _dtype_code(out_dtype), _stream())
+    return out

@@ -4,13 +4,18 @@ This restates the precision-policy surface of nano-train (src/runtime/
 precision_args.py:13-228 and src/runtime/mixed_precision.py:222-762) so that
 the same command lines select the same modules and recipes; the one addition
 is the backend name "hip" for --fp8-backend / --fp4-backend, which builds
-lowbit.backend.HipLowBitBackend, plus three knobs the MI355X backend reads:
+lowbit.backend.HipLowBitBackend, plus four knobs the MI355X backend reads:
 
   --lowbit-code-format {int_grid,e4m3}  int_grid reproduces the emulated
                                         backend's integer grid (qmax = 127 / 7);
                                         e4m3 is the DeepSeek-V3 amax/448 format
   --lowbit-backward {ste,fp8}           ste = the reference's straight-through
                                         backward; fp8 = quantized dgrad/wgrad
+  --lowbit-forward {blockscaled,reference}
+                                        blockscaled = codes on fp8/int8 MFMA with
+                                        the scales applied per 128-K block;
+                                        reference = the reference's operands,
+                                        bf16(q*s), on bf16 MFMA
   --lowbit-seed INT                     seed of the stochastic-rounding stream
 
 The loss-scaling controller and the Transformer Engine backend of the
@@ -96,6 +101,7 @@ def add_mixed_precision_args(parser: argparse.ArgumentParser) -> None:
     # MI355X backend knobs
     a("--lowbit-code-format", type=str, default="int_grid", choices=["int_grid", "e4m3"])
     a("--lowbit-backward", type=str, default="ste", choices=["ste", "fp8"])
+    a("--lowbit-forward", type=str, default="blockscaled", choices=["blockscaled", "reference"])
     a("--lowbit-seed", type=int, default=None)
 
 
@@ -310,6 +316,9 @@ def resolve_precision_config(args, device: torch.device) -> PrecisionConfig:
     backward = str(getattr(args, "lowbit_backward", "ste") or "ste")
     if backward not in ("ste", "fp8"):
         raise ValueError("--lowbit-backward must be ste or fp8")
+    forward = str(getattr(args, "lowbit_forward", "blockscaled") or "blockscaled")
+    if forward not in ("blockscaled", "reference"):
+        raise ValueError("--lowbit-forward must be blockscaled or reference")
 
     config = PrecisionConfig(
         mode=mode,
@@ -342,6 +351,7 @@ def resolve_precision_config(args, device: torch.device) -> PrecisionConfig:
         loss_scale_max=float(getattr(args, "loss_scale_max", 16777216.0)),
         lowbit_code_format=code_format,
         lowbit_backward=backward,
+        lowbit_forward=forward,
         lowbit_seed=getattr(args, "lowbit_seed", None),
     )
     if config.loss_scale_init <= 0:
