@@ -134,6 +134,24 @@ int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t
                        int64_t lddq, int32_t* nan_rows, void* stream);
 
 /*
+ * ntlb_amax_grouped followed by ntlb_quant_grouped without the amax
+ * workspace.  It has no counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and outputs as
+ * ntlb_quant_grouped minus amax_bits (the caller still passes x, codes,
+ * scales and the optional dq and nan_rows).  The group amaxes accumulate in a
+ * file-scope device array of 65536 words (256 KiB on each GPU the library
+ * runs on, held until the process ends), cleared by a kernel at the start of
+ * every call; more than 65536 scale groups (ceil(R/gr) * ceil(K/gc)) is
+ * NTLB_EINVAL.  Every call on a GPU shares that GPU's array: calls that may
+ * overlap on one GPU (different streams) race.  Allocates nothing.
+ */
+int ntlb_quant_grouped_noalloc(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr, int64_t gc,
+                               int grid, int qmax, int rounding, int scale_rule, uint64_t seed, uint64_t offset,
+                               uint8_t* codes, int64_t ldc, float* scales, void* dq, int dq_dtype, int64_t lddq,
+                               int32_t* nan_rows, void* stream);
+
+/*
  * 128x1 tile quantizer with transposed codes: groups of 128 consecutive rows
  * of one column share a scale, and the codes are written transposed,
  * codes_t [K, ldct] (ldct >= ceil(R/128)*128, a multiple of 16).  These are

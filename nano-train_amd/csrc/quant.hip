@@ -13,6 +13,7 @@
 #include <hip/hip_fp16.h>
 #include <algorithm>
 #include <hip/hip_runtime.h>
+#include <mutex>
 
 #include <type_traits>
 
@@ -1384,13 +1385,9 @@ extern "C" int ntlb_quant_block_128x128(const void* w, int w_dtype, int64_t N, i
   return check_launch(fn);
 }
 
-extern "C" int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
-                                 int64_t gc, uint32_t* amax_bits, void* stream) {
-  const char* fn = "ntlb_amax_grouped";
-  if (!valid_dtype(x_dtype)) return fail(NTLB_EINVAL, "%s: bad dtype", fn);
-  if (R < 0 || K < 0 || ldx < K || gr < 1 || gc < 1) return fail(NTLB_EINVAL, "%s: bad shape/group", fn);
-  if (R * K == 0) return NTLB_OK;
-  if (!x || !amax_bits) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+// the grouped amax pass into amax_bits (validated, non-empty shapes)
+static int amax_grouped_launch(const char* fn, const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx,
+                               int64_t gr, int64_t gc, uint32_t* amax_bits, hipStream_t st) {
   const int64_t n_gc = cdiv(K, gc);
   const int64_t col_blocks = cdiv(cdiv(K, 8), 256);
   // rows per workgroup: enough to amortize the atomics, enough groups to fill the GPU
@@ -1399,7 +1396,6 @@ extern "C" int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t 
   const int64_t row_blocks = cdiv(R, rpb);
   if (row_blocks > 65535 || col_blocks > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: shape too large", fn);
   dim3 grd((unsigned)col_blocks, (unsigned)row_blocks), blk(256);
-  hipStream_t st = as_stream(stream);
   const bool vec = K % 8 == 0 && ldx % 8 == 0 && aligned(x, 16);
   NTLB_DISPATCH_DT(x_dtype, {
     if (vec)
@@ -1408,6 +1404,16 @@ extern "C" int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t 
       amax_grouped_kernel<D_, false><<<grd, blk, 0, st>>>(x, R, K, ldx, gr, gc, n_gc, rpb, amax_bits);
   });
   return check_launch(fn);
+}
+
+extern "C" int ntlb_amax_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
+                                 int64_t gc, uint32_t* amax_bits, void* stream) {
+  const char* fn = "ntlb_amax_grouped";
+  if (!valid_dtype(x_dtype)) return fail(NTLB_EINVAL, "%s: bad dtype", fn);
+  if (R < 0 || K < 0 || ldx < K || gr < 1 || gc < 1) return fail(NTLB_EINVAL, "%s: bad shape/group", fn);
+  if (R * K == 0) return NTLB_OK;
+  if (!x || !amax_bits) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  return amax_grouped_launch(fn, x, x_dtype, R, K, ldx, gr, gc, amax_bits, as_stream(stream));
 }
 
 extern "C" int ntlb_comm_quant_dequant(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
@@ -1436,25 +1442,32 @@ extern "C" int ntlb_comm_quant_dequant(const void* x, int x_dtype, int64_t R, in
   return check_launch(fn);
 }
 
-extern "C" int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
-                                  int64_t gc, const uint32_t* amax_bits, int grid, int qmax, int rounding,
-                                  int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes, int64_t ldc,
-                                  float* scales, void* dq, int dq_dtype, int64_t lddq, int32_t* nan_rows,
-                                  void* stream) {
-  const char* fn = "ntlb_quant_grouped";
+// arguments of the grouped quantizer shared by its two entry points
+static int quant_grouped_check(const char* fn, const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx,
+                               int64_t gr, int64_t gc, int grid, int qmax, int rounding, int scale_rule,
+                               const uint8_t* codes, int64_t ldc, const float* scales, void* dq, int dq_dtype,
+                               int64_t lddq) {
   int rc = check_common(fn, x, x_dtype, R, K, ldx, grid, qmax, rounding, scale_rule, dq, dq_dtype, lddq);
   if (rc) return rc;
   if (gr < 1 || gc < 1) return fail(NTLB_EINVAL, "%s: bad group", fn);
   if (ldc < K) return fail(NTLB_EINVAL, "%s: ldc < K", fn);
   if (R * K == 0) return NTLB_OK;
-  if (!codes || !scales || !amax_bits) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (!codes || !scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  return NTLB_OK;
+}
+
+// scales from the group amaxes, then the codes (validated, non-empty shapes)
+static int quant_grouped_launch(const char* fn, const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx,
+                                int64_t gr, int64_t gc, const uint32_t* amax_bits, int grid, int qmax, int rounding,
+                                int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes, int64_t ldc,
+                                float* scales, void* dq, int dq_dtype, int64_t lddq, int32_t* nan_rows,
+                                hipStream_t st) {
   const int64_t n_gr = cdiv(R, gr), n_gc = cdiv(K, gc);
   QuantArgs a = make_args(x, R, K, ldx, grid, qmax, scale_rule, seed, offset, codes, ldc, scales, 0, 0, dq, dq_dtype,
                           lddq, nan_rows);
-  hipStream_t st = as_stream(stream);
   const int64_t ns = n_gr * n_gc;
   scales_from_amax_kernel<<<grid_for(ns, 256, 1 << 20), 256, 0, st>>>(amax_bits, ns, a.qmaxf, scale_rule, scales);
-  rc = check_launch(fn);
+  int rc = check_launch(fn);
   if (rc) return rc;
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
   dim3 grd(grid_for(R * cdiv(K, 8), 256, 256 * 16)), blk(256);
@@ -1469,6 +1482,80 @@ extern "C" int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t
   // ldc > K: padding columns beyond the 8-aligned chunks are not touched; callers
   // pass zero-initialised code buffers when ldc > round_up(K, 8).
   return check_launch(fn);
+}
+
+extern "C" int ntlb_quant_grouped(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
+                                  int64_t gc, const uint32_t* amax_bits, int grid, int qmax, int rounding,
+                                  int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes, int64_t ldc,
+                                  float* scales, void* dq, int dq_dtype, int64_t lddq, int32_t* nan_rows,
+                                  void* stream) {
+  const char* fn = "ntlb_quant_grouped";
+  int rc = quant_grouped_check(fn, x, x_dtype, R, K, ldx, gr, gc, grid, qmax, rounding, scale_rule, codes, ldc,
+                               scales, dq, dq_dtype, lddq);
+  if (rc || R * K == 0) return rc;
+  if (!amax_bits) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  return quant_grouped_launch(fn, x, x_dtype, R, K, ldx, gr, gc, amax_bits, grid, qmax, rounding, scale_rule, seed,
+                              offset, codes, ldc, scales, dq, dq_dtype, lddq, nan_rows, as_stream(stream));
+}
+
+// ---------------------------------------------------------------------------
+// The grouped quantizer without a caller workspace, for callers that cannot
+// allocate (code under graph capture, serving loops): the amax accumulator
+// lives in `scratch`, one copy per GPU, held until the process ends.  Every
+// call on a GPU shares that GPU's copy, so calls that overlap on one GPU
+// (concurrent streams) race; calls in one stream order are safe.
+// ---------------------------------------------------------------------------
+constexpr int64_t NOALLOC_MAX_GROUPS = 1 << 16;  // 256 KiB of uint32 amaxes
+static __device__ __align__(256) uint32_t scratch[NOALLOC_MAX_GROUPS];
+
+__global__ void __launch_bounds__(256) fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = v;
+}
+
+// device address of `scratch` on the current device, looked up once per device
+static int scratch_on_current_device(const char* fn, uint32_t** out) {
+  static std::mutex mu;
+  static uint32_t* addr[64] = {nullptr};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= 64) return fail(NTLB_ELAUNCH, "%s: no current device", fn);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(NTLB_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed: %s", fn, hipGetErrorString(e));
+    addr[dev] = reinterpret_cast<uint32_t*>(p);
+  }
+  *out = addr[dev];
+  return NTLB_OK;
+}
+
+extern "C" int ntlb_quant_grouped_noalloc(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int64_t gr,
+                                          int64_t gc, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                          uint64_t offset, uint8_t* codes, int64_t ldc, float* scales, void* dq,
+                                          int dq_dtype, int64_t lddq, int32_t* nan_rows, void* stream) {
+  const char* fn = "ntlb_quant_grouped_noalloc";
+  int rc = quant_grouped_check(fn, x, x_dtype, R, K, ldx, gr, gc, grid, qmax, rounding, scale_rule, codes, ldc,
+                               scales, dq, dq_dtype, lddq);
+  if (rc || R * K == 0) return rc;
+  const int64_t groups = cdiv(R, gr) * cdiv(K, gc);
+  if (groups > NOALLOC_MAX_GROUPS)
+    return fail(NTLB_EINVAL, "%s: %lld scale groups exceed the %lld this entry point holds (use ntlb_amax_grouped + "
+                "ntlb_quant_grouped with a workspace)", fn, (long long)groups, (long long)NOALLOC_MAX_GROUPS);
+  uint32_t* amax = nullptr;
+  rc = scratch_on_current_device(fn, &amax);
+  if (rc) return rc;
+  hipStream_t st = as_stream(stream);
+  // the previous call's amaxes are still there: clear what this call uses
+  // (a fill kernel, so the call can also be captured in a graph)
+  fill_u32_kernel<<<grid_for(groups, 256, 1024), 256, 0, st>>>(amax, groups, 0u);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  rc = amax_grouped_launch(fn, x, x_dtype, R, K, ldx, gr, gc, amax, st);
+  if (rc) return rc;
+  return quant_grouped_launch(fn, x, x_dtype, R, K, ldx, gr, gc, amax, grid, qmax, rounding, scale_rule, seed,
+                              offset, codes, ldc, scales, dq, dq_dtype, lddq, nan_rows, st);
 }
 
 extern "C" int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx, int grid,

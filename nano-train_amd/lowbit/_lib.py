@@ -43,6 +43,8 @@ SIGNATURES = {
     "ntlb_amax_grouped": [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P],
     "ntlb_quant_grouped": [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _I32, _I32, _U64, _U64, _P, _I64,
                            _P, _P, _I32, _I64, _P, _P],
+    "ntlb_quant_grouped_noalloc": [_P, _I32, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _U64, _U64, _P,
+                                   _I64, _P, _P, _I32, _I64, _P, _P],
     "ntlb_quant_tile_128x1_t": [_P, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _U64, _U64, _P, _I64, _P, _I64,
                                 _I64, _P, _I32, _I64, _P, _P],
     "ntlb_quant_dual_1x128_128x1": [_P, _I32, _I64, _I64, _I64, _I32, _I32, _I32, _I32, _U64, _U64, _U64, _P, _I64,
