@@ -11,11 +11,13 @@ Before the W counted warm-up steps, the step runs untimed for SPIN_UP_S
 seconds so that the timed steps see the sustained clock, not the ramp from
 idle.  `value` = GEMM FLOPs per step / step time (quantizers included).  The
 `roofline` object is the GEMM kernel alone, timed with HIP events on the
-stream the kernels run on.  `cpu_baseline` times the CPU oracle (oracle/,
-numpy + C) on a 1024-row sample of the same workload.
+stream the kernels run on.  `cpu_baseline` times the reference's emulated
+path as its own torch op sequence (oracle/torch_emulated.py) on the host's
+cores, over a 1024-row sample of the same workload.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--format e4m3|int_grid]
                   [--rounding nearest|stochastic] [--no-cpu-baseline]
+                  [--config c1|c2|c3|c4|c5] [--backward fp8|ste]
 """
 
 from __future__ import annotations
@@ -50,6 +52,12 @@ def parse_args():
                    help="also launch a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                    help="c2 (default) is the headline; c1/c3/c4/c5 measure the other BASELINE configurations")
+    p.add_argument("--no-library-compare", action="store_true",
+                   help="skip the library GEMMs timed for comparison (hipBLASLt through torch.matmul), so that a "
+                        "kernel trace holds this build's kernels only")
+    p.add_argument("--backward", default="fp8", choices=["fp8", "ste"],
+                   help="c3: fp8 = the quantized dgrad/wgrad recipe of the configuration; ste = the reference's "
+                        "straight-through backward (dY unquantized, operands bf16(q*s) decoded in the GEMM)")
     a = p.parse_args()
     if a.rounding is None:
         a.rounding = "stochastic" if a.config == "c3" else "nearest"
@@ -140,6 +148,8 @@ def other_config(args) -> dict:
         x, w, dy = x.to(dev), w.to(dev), dy.to(dev)
         M, K = x.shape
         N = w.shape[0]
+        if args.backward == "ste":
+            return _c3_ste(args, res, x, w, dy, st)
         qx_t = ops.quant_tile_128x1_t(x, fmt=fmt)
         _, qw_t = ops.quant_block_128x128(w, fmt=fmt, want_transposed=True)
         t = {}
@@ -279,11 +289,14 @@ def other_config(args) -> dict:
     mx = _time_ms(lambda i: persistent.linear_mxfp4(x, mx_packed, mx_scales, out_features=N), args.steps, args.warmup,
                   st)
     f8 = _time_ms(lambda i: persistent.linear_fp8p(x, f8_vals, f8_scale), args.steps, args.warmup, st)
-    bf = _time_ms(lambda i: torch.matmul(x, w.t()), args.steps, args.warmup, st)
-    # the unfused alternative: the NF4 dequant kernel to a bf16 weight, then torch's bf16 matmul
-    unf = _time_ms(lambda i: torch.matmul(x, persistent.dequantize_nf4_blocks(
-        pk, sc, num_values=N * K, block=64, target_dtype=torch.bfloat16).view(N, K).t()), args.steps, args.warmup, st)
     fl = 2.0 * M * N * K
+    bf = unf = None
+    if not args.no_library_compare:
+        bf = _time_ms(lambda i: torch.matmul(x, w.t()), args.steps, args.warmup, st)
+        # the unfused alternative: the NF4 dequant kernel to a bf16 weight, then torch's bf16 matmul
+        unf = _time_ms(lambda i: torch.matmul(x, persistent.dequantize_nf4_blocks(
+            pk, sc, num_values=N * K, block=64, target_dtype=torch.bfloat16).view(N, K).t()), args.steps,
+            args.warmup, st)
     res.update(value=round(fl / (nf4 * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(nf4, 4), dtype="bf16",
                config={"workload": "c5 NF4 (64-element blocks) dequant-fused GEMM", "M": M, "N": N, "K": K},
                roofline={"bound": "mfma", "achieved": round(fl / (nf4 * 1e-3) / 1e12, 2), "peak": 2500.0,
@@ -292,8 +305,78 @@ def other_config(args) -> dict:
                fp8_persistent_tflops=round(fl / (f8 * 1e-3) / 1e12, 2),
                adamw_nf4_refresh={"fused_us": round(fused_ms * 1e3, 1), "two_pass_us": round(two_ms * 1e3, 1),
                                   "fused_GB/s": round(opt_bytes / (fused_ms * 1e-3) / 1e9, 1), "params": n},
-               torch_bf16_matmul_tflops=round(fl / (bf * 1e-3) / 1e12, 2),
-               nf4_dequant_then_torch_matmul_tflops=round(fl / (unf * 1e-3) / 1e12, 2))
+               torch_bf16_matmul_tflops=None if bf is None else round(fl / (bf * 1e-3) / 1e12, 2),
+               nf4_dequant_then_torch_matmul_tflops=None if unf is None else round(fl / (unf * 1e-3) / 1e12, 2))
+    return res
+
+
+def _c3_ste(args, res: dict, x, w, dy, st) -> dict:
+    """c3 shapes with the reference's straight-through backward
+    (te_backend.py:250-259 under autograd): dX = dY @ bf16(W_dq),
+    dW = dY^T @ bf16(X_dq), db = sum dY, from the forward's codes."""
+    import torch
+
+    from lowbit import ops
+    from lowbit.backend import HipLowBitBackend
+    from lowbit.contracts import LowBitKernelSpec
+
+    fmt = args.format
+    M, K = x.shape
+    N = w.shape[0]
+    qx = ops.quant_tile_1x128(x, fmt=fmt)
+    qw, _ = ops.quant_block_128x128(w, fmt=fmt)
+    bf = torch.bfloat16
+    # each kernel alone, HIP events on the stream it runs on
+    dg = _time_ms(lambda i: ops.ste_dgrad(dy, qw, out_dtype=bf), args.steps, args.warmup, st)
+    wg = _time_ms(lambda i: ops.ste_wgrad(dy, qx, out_dtype=bf), args.steps, args.warmup, st)
+    db = _time_ms(lambda i: ops.colsum(dy, out_dtype=bf), args.steps, args.warmup, st)
+    # the whole layer step through the backend's autograd function: both
+    # quantizers, the forward GEMM, dgrad, wgrad and db
+    spec = LowBitKernelSpec("linear", K, N, True, "tile_1x128", "block_128x128", "nearest")
+    be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format=fmt, seed=7)
+    xg = x.detach().clone().requires_grad_(True)
+    wg_ = w.detach().clone().requires_grad_(True)
+    b = torch.zeros(N, device=x.device, dtype=bf, requires_grad=True)
+
+    def layer(i):
+        xg.grad = wg_.grad = b.grad = None
+        be.linear(xg, wg_, b).backward(dy)
+
+    layer_ms = _time_ms(layer, args.steps, args.warmup, st)
+    fwd_ms = _time_ms(lambda i: be.linear(x, w, None), args.steps, args.warmup, st)
+    fl = 2.0 * M * N * K
+    tf = lambda ms: round(fl / (ms * 1e-3) / 1e12, 2)
+    # HBM bytes per dgrad launch from the committed FETCH_SIZE / WRITE_SIZE runs
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "c3_backward_ste.json")
+    if fmt == "e4m3" and os.path.exists(prof):
+        with open(prof) as fh:
+            for kname, tv in json.load(fh).get("traffic", {}).items():
+                if "gemm_dq_kernel<0, 0, 3, 1" in kname:
+                    traffic = int(tv["total_bytes"])
+    lib = None
+    if not args.no_library_compare:
+        # the same two products as library GEMMs over dequantized bf16
+        # operands (what this path replaced: hipBLASLt through torch.matmul)
+        wdq = ops.dequant(qw, out_dtype=bf)
+        xdq = ops.dequant(qx, out_dtype=bf)
+        lib_dg = _time_ms(lambda i: torch.matmul(dy, wdq), args.steps, args.warmup, st)
+        lib_wg = _time_ms(lambda i: torch.matmul(dy.t(), xdq), args.steps, args.warmup, st)
+        del wdq, xdq
+        lib = {"dgrad_tflops": tf(lib_dg), "wgrad_tflops": tf(lib_wg)}
+    res.update(value=round(2 * fl / ((dg + wg) * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(dg + wg, 4),
+               dtype="bf16",
+               config={"workload": "c3 shapes, the reference's straight-through backward: dX = dY bf16(W_dq), "
+                                   "dW = dY^T bf16(X_dq) decoded from the forward's codes, db = sum dY",
+                       "M": M, "N": N, "K": K, "code_format": fmt},
+               roofline={"bound": "mfma", "kernel": "gemm_dq_kernel (dgrad)", "achieved": tf(dg), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(fl / (dg * 1e-3) / 1e12 / 2500.0, 4), "traffic": traffic,
+                         "traffic_source": "profiles/c3_backward_ste.md" if traffic else None,
+                         "min_hbm_bytes": M * N * 2 + N * K + M * K * 2, "avg_ms": round(dg, 4)},
+               dgrad_tflops=tf(dg), wgrad_tflops=tf(wg), wgrad_frac_bf16_peak=round(tf(wg) / 2500.0, 4),
+               db_colsum_us=round(db * 1e3, 2), db_colsum_GBs=round(M * N * 2 / (db * 1e-3) / 1e9, 1),
+               layer_forward_backward_ms=round(layer_ms, 4), layer_forward_ms=round(fwd_ms, 4),
+               hipblaslt_on_dequantized_bf16=lib)
     return res
 
 
@@ -308,130 +391,123 @@ def _median_s(fn, runs: int = 3) -> float:
     return sorted(ts)[len(ts) // 2]
 
 
-def _blas_threads() -> int:
+def _host_threads() -> int:
+    """CPU threads this process may run on (its affinity mask)."""
     try:
-        from threadpoolctl import threadpool_info
-
-        return int(max((i.get("num_threads", 1) for i in threadpool_info()), default=1))
-    except Exception:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
         return int(os.cpu_count() or 1)
 
 
-def other_cpu_baseline(config: str, fmt: str) -> dict:
-    """The CPU oracle's restatement of a config's path on a bounded sample:
-    quantizers in C on one thread, fp32 matmuls through numpy's BLAS."""
-    import numpy as np
-
-    from lowbit import moe, workloads
-    from oracle import oracle as O
-
-    grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
-    O.lib()
-    f32 = lambda t: t.float().numpy()
-    if config == "c1":
-        x, w = workloads.c1_inputs(device="cpu")
-        xn, wn = f32(x), f32(w)
-        run = lambda: O.emulated_linear_forward(xn, wn, grid=grid)
-        flops = 2.0 * xn.shape[0] * wn.shape[0] * wn.shape[1]
-        what = "oracle emulated linear over all of config 1"
-    elif config == "c3":
-        rows = 512
-        x, w = workloads.c2_inputs(device="cpu", rows=rows)
-        dy = workloads.c3_grad(device="cpu")[:rows]
-        xn, wn, dyn = f32(x), f32(w), f32(dy)
-        wdq = O.quant_block_128x128(wn, grid=grid)[3]  # the weight's codes come from the forward
-
-        def run():
-            dx = O.quant_tile_1x128(dyn, grid=grid)[3] @ wdq
-            dw = O.quant_tile_128x1_t(dyn, grid=grid)[3].T @ O.quant_tile_128x1_t(xn, grid=grid)[3]
-            return dx, dw
-
-        flops = 4.0 * rows * wn.shape[0] * wn.shape[1]
-        what = (f"oracle recipe backward over rows [0, {rows}) of config 3: dY 1x128 and 128x1, X 128x1, "
-                "fp32 dgrad against the forward's 128x128 W and fp32 wgrad")
-    elif config == "c4":
-        rows = 1024
-        tokens, routing, _, _ = workloads.c4_inputs(device="cpu", experts=0)
-        n_exp = workloads.SHAPES[4]["experts"]
-        _, tok_idx, offsets = moe.sort_by_expert(routing, n_exp)
-        # weights of the experts the sample reaches only (leading slices of the full tensors)
-        reach = int(np.searchsorted(np.asarray(offsets.tolist()), rows, side="left"))
-        _, _, w_up, w_down = workloads.c4_inputs(device="cpu", experts=min(reach, n_exp))
-        w_gate = workloads.c4_gate(device="cpu", experts=min(reach, n_exp))
-        xs = f32(tokens[tok_idx[:rows]])
-        off = offsets.tolist()
-        parts = [(e, max(off[e], 0), min(off[e + 1], rows)) for e in range(len(off) - 1) if off[e] < rows]
-        parts = [p for p in parts if p[2] > p[1]]
-        dq = {e: [O.quant_block_128x128(f32(m[e]), grid=grid)[3] for m in (w_gate, w_up, w_down)]
-              for e, _, _ in parts}  # the weights' codes are made once, before the step
-
-        def run():
-            xdq = O.quant_tile_1x128(xs, grid=grid)[3]
-            out = np.empty((rows, w_down.shape[1]), dtype=np.float32)
-            for e, lo, hi in parts:
-                gdq, udq, ddq = dq[e]
-                g = O.round_bf16(xdq[lo:hi] @ gdq.T)
-                u = O.round_bf16(xdq[lo:hi] @ udq.T)
-                h = O.round_bf16(O.round_bf16(g / (1.0 + np.exp(-g))) * u)
-                out[lo:hi] = O.quant_tile_1x128(h, grid=grid)[3] @ ddq.T
-            return out
-
-        flops = 6.0 * rows * w_up.shape[2] * w_up.shape[1]
-        what = (f"oracle expert MLP over expert-sorted rows [0, {rows}) of config 4 ({len(parts)} expert(s)): 1x128 x, "
-                "fp32 gate, up and down GEMMs against 128x128 weights, SwiGLU, 1x128 h")
-    else:
-        rows = 512
-        x, w = workloads.c5_inputs(device="cpu")
-        xn, wn = f32(x[:rows]), f32(w)
-        N, K = wn.shape
-        packed, sc = O.nf4_quant(wn, 64)  # the persistent codes exist before the step
-
-        def run():
-            return xn @ O.nf4_dequant(packed, sc, N * K, 64).reshape(N, K).T
-
-        flops = 2.0 * rows * N * K
-        what = f"oracle NF4 (64-element blocks) dequantize and fp32 matmul over X rows [0, {rows}) of config 5"
-    dt = _median_s(run)
-    th = _blas_threads()
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": th, "kind": "port",
-            "sample": f"{what}; quantizers in C on 1 thread, numpy matmuls on {th} BLAS threads; {dt:.2f} s, "
-                      f"median of 3 runs after 1 warm-up; CPU {_cpu_model()}"}
-
-
-def cpu_baseline(fmt: str, rounding: str, rows: int):
-    """The CPU oracle's emulated linear (te_backend.py:229-260 restated) on a
-    row sample, and its 1x128 activation quantizer alone: median of 3 timed
-    runs after 1 warm-up each."""
+def cpu_baseline(args) -> dict:
+    """The reference's emulated path as its own torch op sequence
+    (oracle/torch_emulated.py restates te_backend.py:40-260 and
+    layers.py:142-184) on the host's cores, over a bounded sample of the
+    configuration: median of 3 timed runs after 1 warm-up.  The C oracle's
+    one-thread 1x128 quantizer is reported beside it (c2)."""
     import numpy as np
     import torch
 
-    from lowbit import workloads
-    from oracle import oracle as O
+    from lowbit import moe, workloads
+    from oracle import torch_emulated as T
 
-    x, w = workloads.c2_inputs(device="cpu", rows=rows)
-    xn = x.float().numpy()
-    wn = w.float().numpy()
-    grid = O.GRID_E4M3 if fmt == "e4m3" else O.GRID_INT
-    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
-    O.lib()
+    threads = _host_threads()
+    torch.set_num_threads(threads)
+    config = args.config
+    extra = {}
+    if config in ("c1", "c2"):
+        rows = args.cpu_sample_rows
+        x, w = workloads.c1_inputs(device="cpu") if config == "c1" else workloads.c2_inputs(device="cpu", rows=rows)
+        rnd = args.rounding
 
-    dt = _median_s(lambda: O.emulated_linear_forward(xn, wn, grid=grid, rounding=rc))
-    dq = _median_s(lambda: O.quant_tile_1x128(xn, grid=grid, rounding=rc))
-    flops = 2.0 * rows * wn.shape[0] * wn.shape[1]
-    q_bytes = xn.shape[0] * xn.shape[1] * 3 + xn.shape[0] * (xn.shape[1] // 128) * 4
-    threads = _blas_threads()
-    return {
-        "value": round(flops / dt / 1e12, 6),
-        "unit": "TFLOP/s",
-        "cores": int(threads or 1),
-        "kind": "port",
-        "quantizer_GB/s": round(q_bytes / dq / 1e9, 3),
-        "sample": (f"oracle emulated linear (1x128 X quant + 128x128 W quant in C on 1 thread, "
-                   f"fp32 dequant, numpy fp32 matmul on {threads} BLAS threads) over X rows [0, {rows}) "
-                   f"of config 2 with the full W [18432, 7168]: {dt:.2f} s; the X 1x128 quantizer alone "
-                   f"(C, 1 thread, same rows): {dq * 1e3:.1f} ms; medians of 3 runs after 1 warm-up; "
-                   f"CPU {_cpu_model()}"),
-    }
+        def run():
+            with torch.no_grad():
+                return T.emulated_linear(x, w, None, act="tile_1x128", wgt="block_128x128", rounding=rnd)
+
+        flops = 2.0 * x.shape[0] * w.shape[0] * w.shape[1]
+        what = (f"the reference's emulated linear (1x128 X and 128x128 W fake quantization, int grid, {rnd}, "
+                f"fp32 F.linear) over X rows [0, {x.shape[0]}) of config {config[1]} with the full W "
+                f"{list(w.shape)}")
+        q_t = _median_s(lambda: T.quantize_dequantize(x, bits=8, granularity="tile_1x128", rounding=rnd,
+                                                      channel_axis=-1))
+        q_bytes = x.numel() * 3 + x.shape[0] * (x.shape[1] // 128) * 4
+        extra["quantizer_GB/s"] = round(q_bytes / q_t / 1e9, 3)
+        if config == "c2":
+            from oracle import oracle as O
+
+            O.lib()
+            xn = x.float().numpy()
+            grid = O.GRID_E4M3 if args.format == "e4m3" else O.GRID_INT
+            c_t = _median_s(lambda: O.quant_tile_1x128(xn, grid=grid))
+            extra["oracle_c_1thread"] = {"quantizer_GB/s": round(q_bytes / c_t / 1e9, 3),
+                                         "what": "the C oracle's 1x128 quantizer on 1 thread, same rows"}
+    elif config == "c3":
+        rows = 512
+        x, w = workloads.c2_inputs(device="cpu", rows=rows)
+        dy = workloads.c3_grad(device="cpu")[:rows].contiguous()
+        xg = x.clone().requires_grad_(True)
+        wg = w.clone().requires_grad_(True)
+        y = T.emulated_linear(xg, wg, None, act="tile_1x128", wgt="block_128x128", rounding="nearest")
+
+        def run():
+            return torch.autograd.grad(y, (xg, wg), dy, retain_graph=True)
+
+        flops = 4.0 * rows * w.shape[0] * w.shape[1]
+        what = (f"the reference's straight-through backward (autograd of the emulated linear: fp32 dX = dY W_q, "
+                f"dW = dY^T X_q) over rows [0, {rows}) of config 3; the reference has no quantized-gradient "
+                f"recipe, so this is its backward for both --backward modes")
+    elif config == "c4":
+        rows = 512
+        tokens, routing, _, _ = workloads.c4_inputs(device="cpu", experts=0)
+        n_exp = workloads.SHAPES[4]["experts"]
+        _, tok_idx, offsets = moe.sort_by_expert(routing, n_exp)
+        off = offsets.tolist()
+        reach = int(np.searchsorted(np.asarray(off), rows, side="left"))
+        _, _, w_up, w_down = workloads.c4_inputs(device="cpu", experts=min(reach, n_exp))
+        w_gate = workloads.c4_gate(device="cpu", experts=min(reach, n_exp))
+        xs = tokens[tok_idx[:rows]]
+        parts = [(e, max(off[e], 0), min(off[e + 1], rows)) for e in range(len(off) - 1) if off[e] < rows]
+        parts = [p for p in parts if p[2] > p[1]]
+
+        def run():
+            with torch.no_grad():
+                outs = []
+                for e, lo, hi in parts:  # moe.py:888-962 with ExpertMLP (moe.py:146-193) per expert
+                    xe = xs[lo:hi]
+                    g = T.emulated_linear(xe, w_gate[e], None)
+                    u = T.emulated_linear(xe, w_up[e], None)
+                    h = torch.nn.functional.silu(g) * u
+                    outs.append(T.emulated_linear(h, w_down[e], None))
+                return outs
+
+        flops = 6.0 * rows * w_up.shape[2] * w_up.shape[1]
+        what = (f"the reference's per-expert loop over expert-sorted rows [0, {rows}) of config 4 "
+                f"({len(parts)} expert(s)): gate, up and down emulated Linears (1x128 / 128x128, int grid, "
+                f"each weight quantized per call) and F.silu(gate) * up")
+    else:
+        rows = 256
+        x, w = workloads.c5_inputs(device="cpu")
+        xs = x[:rows].contiguous()
+        N, K = w.shape
+        from oracle import oracle as O
+
+        packed, sc = O.nf4_quant(w.float().numpy(), 64)  # the persistent codes exist before the step
+        pk, sct = torch.from_numpy(packed), torch.from_numpy(sc)
+
+        def run():
+            with torch.no_grad():
+                wd = T.nf4_dequantize(pk, sct, numel=N * K, block=64, dtype=torch.bfloat16).view(N, K)
+                return torch.nn.functional.linear(xs, wd)
+
+        flops = 2.0 * rows * N * K
+        what = (f"the reference's persistent NF4 forward: unpack, codebook times 64-block scale, cast to bf16 "
+                f"(layers.py:142-184), then a bf16 F.linear, over X rows [0, {rows}) of config 5")
+    dt = _median_s(run)
+    out = {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+           "sample": f"{what}: {dt:.3f} s, median of 3 runs after 1 warm-up; torch CPU ops on {threads} threads "
+                     f"(the process's affinity; os.cpu_count() = {os.cpu_count()}); CPU {_cpu_model()}"}
+    out.update(extra)
+    return out
 
 
 def _cpu_model() -> str:
@@ -462,7 +538,7 @@ def main():
             _calibration_copy(dev)
         res = other_config(args)
         if not args.no_cpu_baseline:
-            res["cpu_baseline"] = other_cpu_baseline(args.config, args.format)
+            res["cpu_baseline"] = cpu_baseline(args)
         print(json.dumps(res))
         return
     shp = workloads.SHAPES[2]
@@ -529,6 +605,21 @@ def main():
                                                        seed=1, offset=2 * i), args.steps, args.warmup, stream)
     qw_alone = _time_ms(lambda i: ops.quant_block_128x128(sets[i % len(sets)][1], fmt=args.format, rounding=rounding,
                                                           seed=1, offset=2 * i + 1), args.steps, args.warmup, stream)
+
+    # the other two GEMMs of the same forward on the same inputs: the
+    # reference-exact mode (bf16(q*s) operands decoded in the GEMM, bf16 MFMA)
+    # and the int-grid codes of the reference's numerics on int8 MFMA
+    xq0 = ops.quant_tile_1x128(sets[0][0], fmt=args.format)
+    wq0, _ = ops.quant_block_128x128(sets[0][1], fmt=args.format)
+    ref_ms = _time_ms(lambda i: ops.gemm_dq_forward(xq0, wq0), args.steps, args.warmup, stream)
+    del xq0, wq0
+    other_fmt = "int_grid" if args.format == "e4m3" else "e4m3"
+    xq1 = ops.quant_tile_1x128(sets[0][0], fmt=other_fmt)
+    wq1, _ = ops.quant_block_128x128(sets[0][1], fmt=other_fmt)
+    other_ms = _time_ms(lambda i: ops.gemm_blockscaled(xq1, wq1), args.steps, args.warmup, stream)
+    del xq1, wq1
+    ref_tf = flops / (ref_ms * 1e-3) / 1e12
+    other_tf = flops / (other_ms * 1e-3) / 1e12
 
     # achievable HBM rate on this box: a 1 GiB device-to-device copy (read + write)
     ca = torch.empty(1 << 29, dtype=torch.int16, device=dev)
@@ -607,12 +698,17 @@ def main():
                                 "GB/s": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9, 1),
                                 "frac_hbm": round(qw_bytes / (avg(qw_ms) * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
         },
+        "reference_forward_gemm": {"kernel": "gemm_dq_kernel (codes decoded to bf16(q*s), bf16 MFMA)",
+                                   "tflops": round(ref_tf, 2), "frac_bf16_peak": round(ref_tf / 2500.0, 4),
+                                   "avg_ms": round(ref_ms, 4)},
+        f"{other_fmt}_gemm": {"kernel": "gemm_blockscaled_kernel", "tflops": round(other_tf, 2),
+                              "frac_peak": round(other_tf / FP8_PEAK_TFLOPS, 4), "avg_ms": round(other_ms, 4)},
         "hbm_copy_GB/s": round(copy_gbs, 1),
         "event_ms_per_step": round(avg(step_ms), 4),
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.format, rounding, args.cpu_sample_rows)
+        result["cpu_baseline"] = cpu_baseline(args)
     print(json.dumps(result))
 
 

@@ -1,0 +1,102 @@
+"""Pins for oracle/torch_emulated.py, the torch-op restatement of the
+reference's emulated path that bench.py times as its CPU baseline.  It must
+give the C oracle's dequantized values bit for bit (the C oracle is pinned in
+test_oracle_pins.py) for every granularity, special values and ragged shapes
+included, and its forward and autograd gradients must equal float64 products
+of those values."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from oracle import torch_emulated as T
+
+
+def _x(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=g) * std
+    x = torch.where(torch.rand(*shape, generator=g) < 0.01, x * 50, x)
+    return x
+
+
+def _bits_equal(a: torch.Tensor, b: np.ndarray) -> bool:
+    a = a.float().numpy().astype(np.float32)
+    b = b.astype(np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all((a.view(np.uint32) == b.view(np.uint32)) | nan))
+
+
+GRAN_GROUPS = {  # granularity, channel axis -> oracle (gr, gc) on a 2-D operand [R, K]
+    ("tile_1x128", -1): lambda R, K: (1, 128),
+    ("block_128x128", 0): lambda R, K: (128, 128),
+    ("tensor", -1): lambda R, K: (R, K),
+    ("channel", -1): lambda R, K: (R, 1),
+    ("channel", 0): lambda R, K: (1, K),
+}
+
+
+@pytest.mark.parametrize("gran,axis", list(GRAN_GROUPS))
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("shape", [(256, 384), (129, 257), (3, 70)])
+def test_quantize_dequantize_matches_c_oracle(gran, axis, bits, shape):
+    x = _x(shape, 20263001 + shape[0])
+    x[1, 2] = float("nan")
+    x[2, 5] = float("inf")
+    x[0, :] = 0.0
+    R, K = shape
+    gr, gc = GRAN_GROUPS[(gran, axis)](R, K)
+    got = T.quantize_dequantize(x, bits=bits, granularity=gran, rounding="nearest", channel_axis=axis)
+    want = O.quant_grouped(x.numpy(), gr, gc, bits=bits)[3]
+    assert _bits_equal(got, want)
+
+
+def test_unknown_granularity_is_the_scale_first_tensor_rule():
+    """_ste_fake_quantize (te_backend.py:40-58): amax checked before the
+    division, so a subnormal amax gives scale amax/qmax, and zero gives 1."""
+    x = torch.full((4, 130), 1e-39)
+    got = T.quantize_dequantize(x, bits=8, granularity="other", rounding="nearest", channel_axis=-1)
+    want = O.quant_grouped(x.numpy(), 4, 130, scale_rule=O.SCALE_BEFORE_DIVIDE)[3]
+    assert _bits_equal(got, want)
+
+
+def test_bf16_operand_is_the_rounded_fp32_dq():
+    x = _x((64, 256), 20263011).to(torch.bfloat16)
+    got = T.quantize_dequantize(x, bits=8, granularity="tile_1x128", rounding="nearest", channel_axis=-1)
+    want = O.round_bf16(O.quant_tile_1x128(x.float().numpy())[3])
+    assert got.dtype == torch.bfloat16 and _bits_equal(got, want)
+
+
+def test_stochastic_rounding_brackets():
+    x = _x((64, 256), 20263021)
+    dq = T.quantize_dequantize(x, bits=8, granularity="tile_1x128", rounding="stochastic", channel_axis=-1)
+    lo = O.quant_tile_1x128(x.numpy())[3]  # nearest: within one scale step of the stochastic value
+    s = O.quant_tile_1x128(x.numpy())[1].repeat(128, axis=1)[:, :256]
+    assert np.all(np.abs(dq.numpy() - lo) <= s * 1.001)  # at most one scale step (fp32 products aside)
+
+
+def test_linear_forward_and_straight_through_gradients():
+    x = _x((96, 384), 20263031).requires_grad_(True)
+    w = (_x((160, 384), 20263032) * 0.02).requires_grad_(True)
+    b = _x((160,), 20263033).requires_grad_(True)
+    dy = _x((96, 160), 20263034) * 1e-3
+    y = T.emulated_linear(x, w, b)
+    y.backward(dy)
+    xd = O.quant_tile_1x128(x.detach().numpy())[3].astype(np.float64)
+    wd = O.quant_block_128x128(w.detach().numpy())[3].astype(np.float64)
+    ref = xd @ wd.T + b.detach().numpy().astype(np.float64)
+    assert O.rel_frobenius(y.detach().numpy(), ref) <= 1e-6
+    d = dy.numpy().astype(np.float64)
+    assert O.rel_frobenius(x.grad.numpy(), d @ wd) <= 1e-6
+    assert O.rel_frobenius(w.grad.numpy(), d.T @ xd) <= 1e-6
+    assert np.allclose(b.grad.numpy(), d.sum(0), rtol=1e-5, atol=1e-7)
+
+
+def test_nf4_dequantize_matches_c_oracle():
+    w = _x((64, 256), 20263041) * 0.02
+    packed, scales = O.nf4_quant(w.numpy(), 64)
+    got = T.nf4_dequantize(torch.from_numpy(packed), torch.from_numpy(scales), numel=w.numel(), block=64,
+                           dtype=torch.float32)
+    assert _bits_equal(got, O.nf4_dequant(packed, scales, w.numel(), 64))
