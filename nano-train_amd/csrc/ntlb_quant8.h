@@ -116,8 +116,11 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
       for (int i = 0; i < 8; ++i) {
         float t;
         if constexpr (SR) {
+          // the reference clamps after rounding (te_backend.py:102-106): at
+          // the clamp, qmax + u rounds to qmax + 1 in fp32 when u >= 1 - 2^-18
           const float uu = sr_uniform(rb[i]);
           t = (vq[i] >= 0.0f) ? __builtin_floorf(vq[i] + uu) : __builtin_ceilf(vq[i] - uu);
+          t = __builtin_amdgcn_fmed3f(t, -qmaxf, qmaxf);
         } else {
           t = __builtin_rintf(vq[i]);
         }

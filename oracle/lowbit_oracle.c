@@ -231,9 +231,16 @@ float ntlo_code_value(uint8_t code, int grid) {
 /* q_out / dq: [R, K] floats (q and q*scale in fp32), may be NULL.       */
 /* SR bits are drawn for the source element index i*K + k.               */
 /* ------------------------------------------------------------------ */
-int ntlo_quant_grouped(const float* x, int64_t R, int64_t K, int64_t gr, int64_t gc, int grid, int qmax,
-                       int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes,
-                       int64_t ldc, float* scales, float* q_out, float* dq) {
+/* Element (i, k) of x draws the stochastic-rounding bits of source index
+ * e_base + i * e_row + k (e_row = 0 means K): a slice of a larger [R', K']
+ * matrix -- rows [r0, r1) with e_base = r0 * K', or columns [c0, c1) with
+ * e_base = c0 and e_row = K' -- then gets the bits of its place in that
+ * matrix, and groups that do not cross the slice's edge give that matrix's
+ * codes. */
+int ntlo_quant_grouped_at(const float* x, int64_t R, int64_t K, int64_t gr, int64_t gc, int grid, int qmax,
+                          int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes,
+                          int64_t ldc, float* scales, float* q_out, float* dq, uint64_t e_base, uint64_t e_row) {
+  if (e_row == 0) e_row = (uint64_t)K;
   if (R < 0 || K < 0 || gr <= 0 || gc <= 0 || ldc < K) return -1;
   int64_t nsr = (R + gr - 1) / gr, nsc = (K + gc - 1) / gc;
   float qmaxf = grid_qmax(grid, qmax);
@@ -252,7 +259,8 @@ int ntlo_quant_grouped(const float* x, int64_t R, int64_t K, int64_t gr, int64_t
         continue;
       }
       float s = scales[(i / gr) * nsc + (k / gc)];
-      uint32_t r = rounding == ROUND_STOCHASTIC ? ntlo_sr_bits(seed, offset, (uint64_t)(i * K + k)) : 0u;
+      uint32_t r = rounding == ROUND_STOCHASTIC ? ntlo_sr_bits(seed, offset, e_base + (uint64_t)i * e_row + (uint64_t)k)
+                                                : 0u;
       uint8_t c;
       float q = quant_one(x[i * K + k], s, grid, qmax, rounding, r, &c);
       codes[i * ldc + k] = c;
@@ -261,6 +269,13 @@ int ntlo_quant_grouped(const float* x, int64_t R, int64_t K, int64_t gr, int64_t
     }
   }
   return 0;
+}
+
+int ntlo_quant_grouped(const float* x, int64_t R, int64_t K, int64_t gr, int64_t gc, int grid, int qmax,
+                       int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* codes,
+                       int64_t ldc, float* scales, float* q_out, float* dq) {
+  return ntlo_quant_grouped_at(x, R, K, gr, gc, grid, qmax, rounding, scale_rule, seed, offset, codes, ldc, scales,
+                               q_out, dq, 0, 0);
 }
 
 /* Comm-quant 'channel' granularity loops over columns with one scale per

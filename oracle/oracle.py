@@ -67,6 +67,9 @@ def lib():
         L.ntlo_e2m1_encode_array.argtypes = [P, i64, P]
         L.ntlo_quant_grouped.argtypes = [P, i64, i64, i64, i64, i32, i32, i32, i32, u64, u64, P, i64, P, P, P]
         L.ntlo_quant_grouped.restype = i32
+        L.ntlo_quant_grouped_at.argtypes = [P, i64, i64, i64, i64, i32, i32, i32, i32, u64, u64, P, i64, P, P, P,
+                                            u64, u64]
+        L.ntlo_quant_grouped_at.restype = i32
         L.ntlo_nf4_quant.argtypes = [P, i64, i64, P, P]
         L.ntlo_nf4_quant.restype = i32
         L.ntlo_nf4_dequant.argtypes = [P, P, i64, i64, P]
@@ -156,11 +159,17 @@ def quant_grouped(
     seed: int = 0,
     offset: int = 0,
     ldc: Optional[int] = None,
+    elem_base: int = 0,
+    elem_row: int = 0,
 ):
     """Quantize a [R, K] fp32 matrix with one scale per (gr x gc) group.
 
     Returns (codes uint8 [R, ldc], scales fp32 [ceil(R/gr), ceil(K/gc)],
-    q fp32 [R, K], dq fp32 [R, K]).
+    q fp32 [R, K], dq fp32 [R, K]).  When x is a slice of a larger matrix,
+    element (i, k) draws the stochastic-rounding bits of source index
+    elem_base + i * elem_row + k (elem_row 0 = K): rows [r0, r1) of an
+    [R', K'] matrix use elem_base = r0 * K', columns [c0, c1) use
+    elem_base = c0 and elem_row = K'.
     """
     x = np.ascontiguousarray(x, dtype=np.float32)
     assert x.ndim == 2
@@ -173,9 +182,9 @@ def quant_grouped(
     scales = np.zeros((nsr, nsc), dtype=np.float32)
     q = np.zeros((R, K), dtype=np.float32)
     dq = np.zeros((R, K), dtype=np.float32)
-    rc = lib().ntlo_quant_grouped(
+    rc = lib().ntlo_quant_grouped_at(
         _ptr(x), R, K, gr, gc, grid, qmax_for_bits(bits), rounding, scale_rule,
-        seed, offset, _ptr(codes), ldc, _ptr(scales), _ptr(q), _ptr(dq),
+        seed, offset, _ptr(codes), ldc, _ptr(scales), _ptr(q), _ptr(dq), elem_base, elem_row,
     )
     if rc != 0:
         raise ValueError(f"ntlo_quant_grouped failed rc={rc}")

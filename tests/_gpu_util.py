@@ -60,3 +60,56 @@ def rel_fro_bf16(y_gpu: torch.Tensor, y_ref64: np.ndarray) -> float:
     a = y_gpu.detach().float().cpu().numpy()
     b = O.round_bf16(y_ref64.astype(np.float32))
     return O.rel_frobenius(a, b)
+
+
+def _pool_size() -> int:
+    import os
+
+    return max(1, min(16, os.cpu_count() or 1))  # the GPU box's CPU share
+
+
+def oracle_tile_1x128_rows(x: np.ndarray, **kw):
+    """O.quant_tile_1x128 of a large [R, K] matrix, row chunks in parallel
+    threads (ctypes releases the GIL), each keyed at its place in x.
+    Returns (codes, scales)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    R, K = x.shape
+    step = -(-R // _pool_size())
+    chunks = [(r0, min(R, r0 + step)) for r0 in range(0, R, step)]
+
+    def run(c):
+        r0, r1 = c
+        out = O.quant_tile_1x128(np.ascontiguousarray(x[r0:r1]), elem_base=r0 * K, **kw)
+        return out[0], out[1]
+
+    with ThreadPoolExecutor(len(chunks)) as ex:
+        parts = list(ex.map(run, chunks))
+    return np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts])
+
+
+def oracle_128x1_t_cols(x: np.ndarray, cols=None, **kw):
+    """O.quant_tile_128x1_t of the columns `cols` (all when None) of a large
+    [R, K] matrix, column chunks in parallel threads, each keyed at its place
+    in x.  Returns (codes_t [len(cols), ceil(R/128)*128], scales_t)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    R, K = x.shape
+    cols = np.arange(K) if cols is None else np.asarray(cols)
+    # runs of consecutive columns, cut into pool-sized chunks
+    runs, start = [], 0
+    for i in range(1, len(cols) + 1):
+        if i == len(cols) or cols[i] != cols[i - 1] + 1:
+            runs.append((int(cols[start]), int(cols[i - 1]) + 1))
+            start = i
+    step = max(1, -(-len(cols) // _pool_size()))
+    chunks = [(c0 + j, min(c1, c0 + j + step)) for c0, c1 in runs for j in range(0, c1 - c0, step)]
+
+    def run(c):
+        c0, c1 = c
+        out = O.quant_tile_128x1_t(np.ascontiguousarray(x[:, c0:c1]), elem_base=c0, elem_row=K, **kw)
+        return out[0], out[1]
+
+    with ThreadPoolExecutor(min(len(chunks), _pool_size())) as ex:
+        parts = list(ex.map(run, chunks))
+    return np.concatenate([p[0] for p in parts]), np.concatenate([p[1] for p in parts])

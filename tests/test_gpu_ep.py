@@ -205,6 +205,15 @@ def test_c4_size_records_feed_the_expert_path(gpu_device):
     assert torch.equal(rows.q.codes, qx.codes)
     M = rows.q.rows
     assert torch.equal(rows.q.scales[:, :M], qx.scales[:, :M])
+    # a sample of the send records against the oracle: each record's codes
+    # and tile scales are the 1x128 quantization of its token row
+    rec = send.records.cpu().numpy()
+    pick = np.sort(np.random.default_rng(20261231).choice(rec.shape[0], 64, replace=False))
+    codes, scales, meta, _, _ = _decode(rec[pick], 7168)
+    tok = meta[:, 0]
+    c_ref, s_ref, _, _ = O.quant_tile_1x128(tokens.float().numpy()[tok], grid=O.GRID_E4M3)
+    assert_bits_equal(codes, c_ref[:, :7168], "sampled c4 record codes")
+    assert_bits_equal(scales, s_ref, "sampled c4 record scales")
 
 
 def test_capacity_drop_keeps_top_weights(gpu_device):

@@ -312,31 +312,45 @@ def test_persistent_nf4_fused_matches_materialized_and_trains(gpu_device):
     assert int(layer._persistent_numel.item()) == 256 * 512
 
 
-def test_c3_backward_full_size_sampled(gpu_device):
-    """BASELINE config 3 at full size with the fp8 backward recipe; dgrad and
-    wgrad checked on sampled rows/columns against the oracle."""
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_c3_backward_full_size_sampled(gpu_device, rounding):
+    """BASELINE config 3 at full size with the fp8 backward recipe, under
+    round to nearest and under the seeded stochastic rounding the
+    configuration names; dgrad and wgrad checked on sampled rows and columns
+    against the oracle, each slice quantized with the stochastic-rounding
+    bits of its place in the full matrix."""
     from lowbit import workloads
     from lowbit.backend import HipLowBitBackend
     from lowbit.contracts import LowBitKernelSpec
 
     x, w = workloads.c2_inputs(device="cpu")
     dy = workloads.c3_grad(device="cpu")
-    spec = LowBitKernelSpec("linear", 7168, 18432, False, "tile_1x128", "block_128x128", "nearest")
+    spec = LowBitKernelSpec("linear", 7168, 18432, False, "tile_1x128", "block_128x128", rounding)
     be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format="e4m3", backward="fp8", seed=5)
     xg = x.to(gpu_device).requires_grad_(True)
     wg = w.to(gpu_device).requires_grad_(True)
     y = be.linear(xg, wg, None)
     y.backward(dy.to(gpu_device))
     torch.cuda.synchronize()
-    rows = np.random.default_rng(0).choice(8192, 16, replace=False)
-    kcols = np.random.default_rng(1).choice(7168, 128, replace=False)
-    dyd = O.quant_tile_1x128(dy.float().numpy()[rows], grid=O.GRID_E4M3)[3]
-    wd = O.quant_block_128x128(w.float().numpy(), grid=O.GRID_E4M3)[3]
-    dx_ref = dyd.astype(np.float64) @ wd[:, kcols].astype(np.float64)
+    M, K = x.shape
+    N = w.shape[0]
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    kw = dict(grid=O.GRID_E4M3, rounding=rc, seed=5)
+    # the backend's offsets on its first call: X 0, W 1, dY 1x128 2, dY 128x1 3, X 128x1 4
+    rows = np.sort(np.random.default_rng(0).choice(M, 16, replace=False))
+    kblocks = [3, 40]  # two 128-column blocks of K
+    kcols = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in kblocks])
+    ncols = np.sort(np.random.default_rng(2).choice(N, 16, replace=False))
+    dyn, xn, wn = dy.float().numpy(), x.float().numpy(), w.float().numpy()
+    dyd = np.concatenate([O.quant_tile_1x128(dyn[r:r + 1], elem_base=int(r) * N, offset=2, **kw)[3] for r in rows])
+    wd = np.concatenate([O.quant_block_128x128(np.ascontiguousarray(wn[:, b * 128:b * 128 + 128]), elem_base=b * 128,
+                                               elem_row=K, offset=1, **kw)[3] for b in kblocks], axis=1)
+    dx_ref = dyd.astype(np.float64) @ wd.astype(np.float64)
     assert rel_fro_bf16(xg.grad[rows][:, kcols], dx_ref) <= 1e-3
-    ncols = np.random.default_rng(2).choice(18432, 16, replace=False)
-    dytd = O.quant_tile_128x1_t(np.ascontiguousarray(dy.float().numpy()[:, ncols]), grid=O.GRID_E4M3)[3]
-    xtd = O.quant_tile_128x1_t(np.ascontiguousarray(x.float().numpy()[:, kcols]), grid=O.GRID_E4M3)[3]
+    dytd = np.concatenate([O.quant_tile_128x1_t(np.ascontiguousarray(dyn[:, n:n + 1]), elem_base=int(n), elem_row=N,
+                                                offset=3, **kw)[3] for n in ncols], axis=1)
+    xtd = np.concatenate([O.quant_tile_128x1_t(np.ascontiguousarray(xn[:, b * 128:b * 128 + 128]), elem_base=b * 128,
+                                               elem_row=K, offset=4, **kw)[3] for b in kblocks], axis=1)
     dw_ref = dytd.T.astype(np.float64) @ xtd.astype(np.float64)
     assert rel_fro_bf16(wg.grad[ncols][:, kcols], dw_ref) <= 1e-3
 

@@ -133,6 +133,27 @@ def test_c5_nf4_fused_gemm_full_size_sampled(gpu_device):
     assert rel_fro_bf16(y[rows][:, cols], ref) <= 1e-3
 
 
+def test_c5_mxfp4_fused_gemm_full_size_sampled(gpu_device):
+    """BASELINE config 5 as MXFP4 (32-element blocks, e8m0 scales): W
+    [14336, 4096], X [4096, 4096]; codes and scales bit for bit, the fused
+    GEMM on sampled rows and columns against the oracle."""
+    from lowbit import persistent as P, workloads
+
+    x, w = workloads.c5_inputs(device="cpu")
+    xg, wg = x.to(gpu_device), w.to(gpu_device)
+    packed, scales = P.quantize_mxfp4(wg)
+    y = P.linear_mxfp4(xg, packed, scales, out_features=14336)
+    torch.cuda.synchronize()
+    p_ref, s_ref = O.mxfp4_quant(w.float().numpy())
+    assert_bits_equal(packed.cpu().numpy(), p_ref, "c5 mxfp4 codes")
+    assert_bits_equal(scales.cpu().numpy(), s_ref, "c5 mxfp4 scales")
+    rows = np.random.default_rng(3).choice(4096, 32, replace=False)
+    cols = np.random.default_rng(4).choice(14336, 256, replace=False)
+    wdq = O.round_bf16(O.mxfp4_dequant(p_ref, s_ref, 14336 * 4096)).reshape(14336, 4096)
+    ref = O.gemm_ref(x.float().numpy()[rows], wdq[cols])
+    assert rel_fro_bf16(y[rows][:, cols], ref) <= 1e-3
+
+
 @pytest.mark.parametrize("per_tensor", [False, True])
 def test_fp8p_fused_gemm_dequant_exact_all_codes(gpu_device, per_tensor):
     """X = I makes the fused GEMM return deq(W)^T exactly (one nonzero product

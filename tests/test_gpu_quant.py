@@ -7,7 +7,8 @@ import numpy as np
 import pytest
 import torch
 
-from _gpu_util import assert_bits_equal, scales_row_major, seeded, to_np32
+from _gpu_util import (assert_bits_equal, oracle_128x1_t_cols, oracle_tile_1x128_rows, scales_row_major, seeded,
+                       to_np32)
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -174,6 +175,116 @@ def test_c3_dy_128x1_full_size(gpu_device):
     ct, st, _, _ = O.quant_tile_128x1_t(dy.float().numpy(), grid=O.GRID_E4M3)
     assert_bits_equal(q.codes.cpu().numpy(), ct, "codes_t")
     assert_bits_equal(scales_row_major(q, dy.shape[1], st.shape[1]), st, "scales")
+
+
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+def test_c3_dy_full_size_stochastic_rounding(gpu_device, fmt, grid):
+    """BASELINE config 3 with its seeded stochastic rounding, at full size:
+    dY [8192, 18432] per 1x128 tile (the dgrad operand) and per 128x1 tile
+    (dY^T for wgrad), single passes and the dual pass, codes and scales bit
+    for bit against the oracle.  The offsets use the Philox counter's high
+    offset word (offset >= 2^32)."""
+    from lowbit import ops, workloads
+
+    dy = workloads.c3_grad(device="cpu")
+    dyn = dy.float().numpy()
+    dyg = dy.to(gpu_device)
+    o_rows, o_cols = (1 << 32) + 2, (1 << 32) + 3
+    kw = dict(grid=grid, rounding=O.ROUND_STOCHASTIC, seed=3)
+    q1 = ops.quant_tile_1x128(dyg, fmt=fmt, rounding="stochastic", seed=3, offset=o_rows, tile_major_scales=False)
+    torch.cuda.synchronize()
+    c, s = oracle_tile_1x128_rows(dyn, offset=o_rows, **kw)
+    assert_bits_equal(q1.codes.cpu().numpy(), c, "dY 1x128 codes")
+    assert_bits_equal(q1.scales.cpu().numpy(), s, "dY 1x128 scales")
+    del c, s
+    q2 = ops.quant_tile_128x1_t(dyg, fmt=fmt, rounding="stochastic", seed=3, offset=o_cols)
+    torch.cuda.synchronize()
+    ct, st = oracle_128x1_t_cols(dyn, offset=o_cols, **kw)
+    assert_bits_equal(q2.codes.cpu().numpy(), ct, "dY 128x1 codes")
+    assert_bits_equal(scales_row_major(q2, dy.shape[1], st.shape[1]), st, "dY 128x1 scales")
+    del ct, st
+    qd, qdt = ops.quant_dual_1x128_128x1(dyg, fmt=fmt, rounding="stochastic", seed=3, offset_rows=o_rows,
+                                         offset_cols=o_cols)
+    torch.cuda.synchronize()
+    assert torch.equal(qd.codes, q1.codes) and torch.equal(qdt.codes, q2.codes)
+    R, K = dy.shape
+    assert torch.equal(qd.scales[:, :R].t(), q1.scales) and torch.equal(qdt.scales[:, :K], q2.scales[:, :K])
+
+
+@pytest.mark.parametrize("fmt,grid", GRIDS)
+def test_sr_uses_both_high_counter_words(gpu_device, fmt, grid):
+    """Stochastic rounding with every word of the Philox counter in play:
+    offset >= 2^32 (counter word 3) and element indices >= 2^34, i.e.
+    element/4 >= 2^32 (counter word 1).  x is [2^24 + 64, 1024] bf16 (32 GiB);
+    its last 64 rows, whose element indices all pass 2^34, carry seeded data
+    and are checked bit for bit against the oracle keyed at their place."""
+    from lowbit import ops
+
+    R, K = (1 << 24) + 64, 1024
+    tail = seeded((64, K), seed=20260311, outliers=0.01)
+    x = torch.zeros((R, K), dtype=torch.bfloat16, device=gpu_device)
+    x[R - 64:] = tail.to(gpu_device)
+    seed, offset = 0x123456789ABC, (1 << 33) + 7
+    q = ops.quant_tile_1x128(x, fmt=fmt, rounding="stochastic", seed=seed, offset=offset, tile_major_scales=False)
+    torch.cuda.synchronize()
+    codes, scales = q.codes[R - 64:].cpu().numpy(), q.scales[R - 64:].cpu().numpy()
+    del q, x
+    torch.cuda.empty_cache()
+    assert (R - 64) * K >= 1 << 34
+    c, s, _, _ = O.quant_tile_1x128(tail.float().numpy(), grid=grid, rounding=O.ROUND_STOCHASTIC, seed=seed,
+                                    offset=offset, elem_base=(R - 64) * K)
+    assert_bits_equal(codes, c, "codes at element index >= 2^34")
+    assert_bits_equal(scales, s, "scales")
+
+
+def _clamp_hits(seed: int, offset: int, idx: np.ndarray) -> np.ndarray:
+    """Which source indices draw u >= 1 - 2^-18, the draws for which
+    qmax + u rounds to qmax + 1 in fp32."""
+    words = O.sr_bits(seed, offset, 0, int(idx.max()) + 1)[idx]
+    return (words >> 8) >= (1 << 24) - 64
+
+
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_sr_clamps_after_rounding_at_the_tile_amax(gpu_device, sign):
+    """Regression: the reference clamps after rounding (te_backend.py:102-106).
+    With a tile amax of 127 the scale is 1 and the amax element's v is
+    exactly +-127; where its draw u >= 1 - 2^-18, +-127 + u rounds to +-128
+    in fp32 and must clamp back to +-127 (int grid), not wrap to the NaN
+    code -128.  Elements with such draws are found with the oracle's SR bits
+    and given the amax, in 1x128 tiles (each row's element 0) and in 128x1
+    tiles (one row per column)."""
+    from lowbit import ops
+
+    seed, offset = 77, 5
+    # 1x128: rows of 8; element 0 of row r has source index 8r
+    R = 1 << 20
+    hit_rows = np.nonzero(_clamp_hits(seed, offset, np.arange(R) * 8))[0]
+    assert len(hit_rows) > 0
+    x = torch.full((R, 8), 0.5)
+    x[:, 0] = 127.0 * sign
+    xg = x.to(torch.bfloat16).to(gpu_device)
+    q = ops.quant_tile_1x128(xg, fmt="int_grid", rounding="stochastic", seed=seed, offset=offset)
+    torch.cuda.synchronize()
+    codes = q.codes.cpu().numpy()
+    assert np.all(codes[hit_rows, 0] == (127 if sign > 0 else 0x81))
+    c_ref = O.quant_tile_1x128(x.numpy(), rounding=O.ROUND_STOCHASTIC, seed=seed, offset=offset)[0]
+    assert_bits_equal(codes, c_ref, "1x128 codes")
+    # 128x1: column k's amax at a row m whose index m*K + k draws such a u
+    K = 8192
+    m_idx = np.arange(128)[:, None] * K + np.arange(K)[None, :]
+    hits = _clamp_hits(seed, offset, m_idx.reshape(-1)).reshape(128, K)
+    cols = np.nonzero(hits.any(axis=0))[0]
+    assert len(cols) > 0
+    rows_at = np.where(hits.any(axis=0), hits.argmax(axis=0), 0)
+    xt = torch.full((128, K), 0.5)
+    xt[rows_at, np.arange(K)] = 127.0 * sign
+    qt = ops.quant_tile_128x1_t(xt.to(torch.bfloat16).to(gpu_device), fmt="int_grid", rounding="stochastic",
+                                seed=seed, offset=offset)
+    torch.cuda.synchronize()
+    ct = qt.codes.cpu().numpy()
+    assert np.all(ct[cols, rows_at[cols]] == (127 if sign > 0 else 0x81))
+    ct_ref = O.quant_tile_128x1_t(xt.numpy(), rounding=O.ROUND_STOCHASTIC, seed=seed, offset=offset)[0]
+    assert_bits_equal(ct, ct_ref, "128x1 codes")
 
 
 @pytest.mark.parametrize("kind", ["tensor", "channel_last", "channel_rows", "strip"])

@@ -452,3 +452,20 @@ def test_ep_combine_oracle_matches_torch_index_add(dtype):
         loose = O.ep_combine(feat.float().numpy(), tok_a.numpy(), slot_a.numpy(), topk.numpy(), w.float().numpy(), T,
                              per_add_rounding=True)
         assert not np.array_equal(loose.view(np.uint32), want.view(np.uint32))
+
+
+def test_slice_index_base_reproduces_rows_and_columns_under_sr():
+    """quant_grouped(elem_base, elem_row) on a slice draws the stochastic-
+    rounding bits of the slice's place in the full matrix: a row slice and a
+    column slice reproduce the full matrix's codes, and the bits do move with
+    the base (a slice quantized as if it started at 0 differs)."""
+    rng = np.random.default_rng(20263101)
+    x = rng.standard_normal((256, 300)).astype(np.float32)
+    kw = dict(grid=O.GRID_E4M3, rounding=O.ROUND_STOCHASTIC, seed=5, offset=(1 << 33) + 9)
+    full = O.quant_tile_1x128(x, **kw)
+    rows = O.quant_tile_1x128(x[17:31], elem_base=17 * 300, **kw)
+    assert np.array_equal(rows[0], full[0][17:31]) and np.array_equal(rows[1], full[1][17:31])
+    assert not np.array_equal(O.quant_tile_1x128(x[17:31], **kw)[0], full[0][17:31])
+    full_t = O.quant_tile_128x1_t(x, **kw)
+    cols = O.quant_tile_128x1_t(np.ascontiguousarray(x[:, 40:45]), elem_base=40, elem_row=300, **kw)
+    assert np.array_equal(cols[0], full_t[0][40:45]) and np.array_equal(cols[1], full_t[1][40:45])
