@@ -10,9 +10,6 @@
 
 namespace ntlb {
 
-#ifndef NTLB_HW_FP8_CVT
-#define NTLB_HW_FP8_CVT 1
-#endif
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 // v_pk_max_u16 on two packed halves
 __device__ __forceinline__ uint32_t pk_max_u16(uint32_t a, uint32_t b) {
@@ -68,7 +65,7 @@ __device__ __forceinline__ bool quant8(const float (&v)[8], float s, float qmaxf
 // Quantize 8 values of a tile with scale s whose amax bits are m.  A tile
 // holding a NaN takes the per-element reference path (and reports it); every
 // other tile clamps with min/max, divides with the fast exact sequence when
-// its amax allows, and rounds to e4m3 in hardware when enabled.
+// its amax allows, and rounds to e4m3 in hardware under round to nearest.
 // The fast division is taken for round-to-nearest tiles whose amax bits lie in
 // [0x1A000000, 0x7B800000] (no NaN, no inf).
 template <bool SR>
@@ -131,7 +128,7 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
       hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
     } else {
       uint32_t c[8];
-      if constexpr (!SR && NTLB_HW_FP8_CVT) {
+      if constexpr (!SR) {
         lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[0], vq[1], 0, false);
         lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[2], vq[3], (int)lo, true);
         hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4], vq[5], 0, false);

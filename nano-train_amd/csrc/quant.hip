@@ -147,22 +147,12 @@ __global__ void __launch_bounds__(256) quant_tile_1x128_kernel(QuantArgs a) {
 // contiguously in the tile-major layout.  The amax runs on packed bf16 bits
 // (one op per two elements).  A tile whose amax is NaN takes the per-element
 // path of the reference semantics; every other tile clamps with min/max.
-// With NTLB_HW_FP8_CVT the e4m3 rounding uses v_cvt_pk_fp8_f32 (checked
+// Under round to nearest the e4m3 rounding uses v_cvt_pk_fp8_f32 (checked
 // bit-exact against the software rounding on every fp32 input with
-// |v| <= 448).
+// |v| <= 448).  Grids put the tile groups in x, so consecutive workgroups
+// walk along a row and concurrent reads stay within the same DRAM pages.
 // ---------------------------------------------------------------------------
-#ifndef NTLB_TILE_TU
-#define NTLB_TILE_TU 2
-#endif
-// workgroup order: 1 = consecutive workgroups walk along a row (column
-// blocks fastest), which keeps concurrent reads within the same DRAM pages
-#ifndef NTLB_COL_FASTEST
-#define NTLB_COL_FASTEST 1
-#endif
-#ifndef NTLB_TILE_PIPELINE
-#define NTLB_TILE_PIPELINE 0
-#endif
-constexpr int TILE_TU = NTLB_TILE_TU;
+constexpr int TILE_TU = 2;
 
 // 8 consecutive elements as fp32 plus their |x| max (bits), from a chunk
 // loaded raw: bf16 keeps 4 registers per chunk and reduces on packed halves.
@@ -316,44 +306,25 @@ __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], co
   }
 }
 
-// Workgroup (bx, by) covers tile columns [TU*by, TU*by+TU) of the row blocks
-// bx, bx + gridDim.x, ... (16 rows each); the loads of the next row block are
-// in flight while the current one is quantized.
+// Workgroup (bx, by) covers tile columns [TU*bx, TU*bx+TU) of the row blocks
+// by, by + gridDim.y, ... (16 rows each).  No prefetch: the lowest register
+// count and the highest occupancy; the loop only runs when the grid is capped
+// below the number of row blocks.
 template <int IN_DT, int GRID, bool SR, bool DQ, bool FAN = false>
 __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
   const int lane16 = threadIdx.x & 15;
   const int T = (int)((a.K + 127) >> 7);
-  const unsigned bx = NTLB_COL_FASTEST ? blockIdx.y : blockIdx.x;  // row-block index
-  const unsigned by = NTLB_COL_FASTEST ? blockIdx.x : blockIdx.y;  // tile-group index
-  const unsigned gxr = NTLB_COL_FASTEST ? gridDim.y : gridDim.x;
-  const int t0 = by * TILE_TU;
+  const int t0 = blockIdx.x * TILE_TU;
   const int64_t n_rb = (a.R + 15) >> 4;
-  int64_t rb = bx;
+  int64_t rb = blockIdx.y;  // row-block index
   if (rb >= n_rb) return;
-  Chunk8<IN_DT> cur[TILE_TU], nxt[TILE_TU];
-  int64_t r = rb * 16 + (threadIdx.x >> 4);
-  tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
-  if constexpr (!NTLB_TILE_PIPELINE) {
-    // no prefetch: the lowest register count and the highest occupancy; the
-    // loop only runs when the grid is capped below the number of row blocks
-    for (;;) {
-      if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ, FAN>(cur, a, r, t0, T, lane16);
-      rb += gxr;
-      if (rb >= n_rb) return;
-      r = rb * 16 + (threadIdx.x >> 4);
-      tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
-    }
-  }
+  Chunk8<IN_DT> cur[TILE_TU];
   for (;;) {
-    const int64_t rb_next = rb + gxr;
-    const int64_t r_next = rb_next * 16 + (threadIdx.x >> 4);
-    if (rb_next < n_rb) tile_loads<IN_DT>(nxt, a, r_next, t0, T, lane16);
+    const int64_t r = rb * 16 + (threadIdx.x >> 4);
+    tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
     if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ, FAN>(cur, a, r, t0, T, lane16);  // whole 16-lane rows
-    if (rb_next >= n_rb) break;
-    rb = rb_next;
-    r = r_next;
-#pragma unroll
-    for (int u = 0; u < TILE_TU; ++u) cur[u] = nxt[u];
+    rb += gridDim.y;
+    if (rb >= n_rb) return;
   }
 }
 
@@ -436,16 +407,8 @@ __global__ void __launch_bounds__(256) quant_block_128x128_kernel(BlockArgs ba) 
 }
 
 // 128x128 blocks, fast path (bf16/fp32, K % 8 == 0, 16-byte aligned rows):
-// one workgroup per block; thread (rr, sub) holds rows rr + 16*i, columns
-// sub*8 .. sub*8+7 as raw chunks between the amax pass and the quantize pass
-// (one HBM read).
-#ifndef NTLB_BLOCK_THREADS
-#define NTLB_BLOCK_THREADS 512
-#endif
-#ifndef NTLB_BLOCK_PIPELINE
-#define NTLB_BLOCK_PIPELINE 0
-#endif
-constexpr int BLK_THREADS = NTLB_BLOCK_THREADS;
+// one workgroup of 512 threads per block.
+constexpr int BLK_THREADS = 512;
 constexpr int BLK_ROWS = BLK_THREADS / 16;  // rows covered by one pass of the workgroup
 constexpr int BLK_RPT = 128 / BLK_ROWS;     // rows per thread
 constexpr int BLK_WAVES = BLK_THREADS / 64;
@@ -531,8 +494,8 @@ __device__ __forceinline__ void block_quant(const Chunk8<IN_DT> (&ch)[BLK_RPT], 
 // 128x128 blocks, fast path (bf16/fp32, K % 8 == 0, 16-byte aligned rows):
 // thread (rr, sub) holds rows rr + BLK_ROWS*i, columns sub*8 .. sub*8+7 of a
 // block as raw chunks between the amax pass and the quantize pass (one HBM
-// read).  Workgroups walk column blocks fastest; with NTLB_BLOCK_PIPELINE the
-// next block's loads are in flight while the current one is quantized.
+// read).  Workgroup (kb, nb0) covers column block kb of the row blocks nb0,
+// nb0 + gridDim.y, ...: consecutive workgroups walk column blocks.
 template <int IN_DT, int GRID, bool SR, bool DQ>
 __global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArgs ba) {
   __shared__ uint32_t red[BLK_WAVES];
@@ -540,30 +503,15 @@ __global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArg
   const int tid = threadIdx.x;
   const int sub = tid & 15, rr = tid >> 4;
   const int64_t NB = (ba.q.R + 127) >> 7;
-  const int64_t kb = NTLB_COL_FASTEST ? blockIdx.x : blockIdx.y;
-  const unsigned gnb = NTLB_COL_FASTEST ? gridDim.y : gridDim.x;
-  int64_t nb = NTLB_COL_FASTEST ? blockIdx.y : blockIdx.x;
+  const int64_t kb = blockIdx.x;
+  int64_t nb = blockIdx.y;
   if (nb >= NB) return;
   Chunk8<IN_DT> cur[BLK_RPT];
-  block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
-  if constexpr (!NTLB_BLOCK_PIPELINE) {
-    for (;;) {
-      block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
-      nb += gnb;
-      if (nb >= NB) return;
-      block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
-    }
-  } else {
-    Chunk8<IN_DT> nxt[BLK_RPT];
-    for (;;) {
-      const int64_t nb_next = nb + gnb;
-      if (nb_next < NB) block_loads<IN_DT>(nxt, ba.q, nb_next, kb, rr, sub);
-      block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
-      if (nb_next >= NB) break;
-      nb = nb_next;
-#pragma unroll
-      for (int i = 0; i < BLK_RPT; ++i) cur[i] = nxt[i];
-    }
+  for (;;) {
+    block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
+    block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
+    nb += gridDim.y;
+    if (nb >= NB) return;
   }
 }
 
@@ -882,12 +830,6 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // thread's chunks is 8 columns of one 1x128 tile, whose other 120 columns are
 // held by the 15 lanes of the same row group, so a 16-lane max gives the tile
 // amax.  One read of dY feeds both the dgrad and the wgrad operands.
-// workgroup order of the 128x1 kernels: groups of T128_GM row blocks walk
-// one column block before the next (T128_GM consecutive workgroups write
-// adjacent 128-byte pieces of the same transposed rows)
-#ifndef NTLB_T128_GM
-#define NTLB_T128_GM 1
-#endif
 template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false>
 __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, QuantArgs ar = QuantArgs()) {
   constexpr int TP = 144;  // staged transposed row pitch (bytes)
@@ -902,16 +844,8 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
   __shared__ __attribute__((aligned(16))) uint8_t tcodes[128 * TP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cc = tid & 15, rg = tid >> 4;
-  const int64_t n_cb = (a.K + 127) / 128, n_mb = (a.R + 127) / 128;
-  int64_t mb, cb;
-  {
-    constexpr int GM = NTLB_T128_GM;
-    const int64_t pid = blockIdx.x;
-    const int64_t group = pid / (GM * n_cb), within = pid - group * GM * n_cb;
-    const int64_t gsize = min<int64_t>(GM, n_mb - group * GM);
-    mb = group * GM + within % gsize;
-    cb = within / gsize;
-  }
+  const int64_t n_cb = (a.K + 127) / 128;
+  const int64_t mb = (int64_t)blockIdx.x / n_cb, cb = (int64_t)blockIdx.x - mb * n_cb;
   const int64_t col0 = cb * 128 + cc * 8;
   const int64_t row0 = mb * 128 + rg * 8;
   const bool col_in = col0 < a.K;  // K % 8 == 0: a chunk is wholly in or out
@@ -1279,18 +1213,12 @@ extern "C" int ntlb_quant_tile_1x128(const void* x, int x_dtype, int64_t R, int6
   hipStream_t st = as_stream(stream);
   const bool fast_ok = vec && (K % 8 == 0) && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) &&
                        (!dq || (dq_dtype == NTLB_BF16 && aligned(dq, 16) && (lddq % 8) == 0)) &&
-                       cdiv(R, 16) <= 0x7FFFFFFF && cdiv(T, TILE_TU) <= 65535;  // either order fits
+                       cdiv(T, TILE_TU) <= 0x7FFFFFFF;
   if (fast_ok) {
-    // pipelined: about 4 row blocks per workgroup so loads overlap the math;
-    // otherwise one row block per workgroup
+    // one row block per workgroup, up to 65535 in y; the kernel's row-block
+    // loop covers the rest
     const int64_t n_rb = cdiv(R, 16), n_tg = cdiv(T, TILE_TU);
-    int64_t gx = n_rb;
-    if (NTLB_TILE_PIPELINE) {
-      gx = cdiv(n_rb, 4);
-      if (gx * n_tg < 256 * 8) gx = std::min<int64_t>(n_rb, cdiv(256 * 8, n_tg));
-    }
-    if (gx > 65535 && NTLB_COL_FASTEST) gx = 65535;  // grid-stride loop covers the rest
-    dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)n_tg, (unsigned)gx) : dim3((unsigned)gx, (unsigned)n_tg);
+    dim3 fgrd((unsigned)n_tg, (unsigned)std::min<int64_t>(n_rb, 65535));
     dim3 fblk(256);
     if (dq) {
       NTLB_DISPATCH_GRID_SR(grid, sr, {
@@ -1348,15 +1276,11 @@ extern "C" int ntlb_quant_block_128x128(const void* w, int w_dtype, int64_t N, i
   hipStream_t st = as_stream(stream);
   const bool fast_ok = vec && (K % 8 == 0) && (w_dtype == NTLB_BF16 || w_dtype == NTLB_F32) &&
                        (!dq || (dq_dtype == NTLB_BF16 && aligned(dq, 16) && (lddq % 8) == 0)) &&
-                       NB <= 0x7FFFFFFF && T <= 65535;
+                       T <= 0x7FFFFFFF;
   if (fast_ok) {
-    int64_t gx = NB;
-    if (NTLB_BLOCK_PIPELINE) {
-      gx = cdiv(NB, 4);
-      if (gx * T < 256 * 8) gx = std::min<int64_t>(NB, cdiv(256 * 8, T));
-    }
-    if (gx > 65535 && NTLB_COL_FASTEST) gx = 65535;
-    dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)T, (unsigned)gx) : dim3((unsigned)gx, (unsigned)T);
+    // one row block per workgroup, up to 65535 in y; the kernel's row-block
+    // loop covers the rest
+    dim3 fgrd((unsigned)T, (unsigned)std::min<int64_t>(NB, 65535));
     dim3 fblk(BLK_THREADS);
     if (dq) {
       NTLB_DISPATCH_GRID_SR(grid, sr, {
@@ -1780,12 +1704,7 @@ static int ep_pack_payload(const char* fn, const void* x, int x_dtype, int64_t n
     return check_launch(fn);
   }
   const int64_t n_rb = cdiv(n_in, 16), n_tg = cdiv(Tt, TILE_TU);
-  int64_t gx = n_rb;
-  if (NTLB_TILE_PIPELINE) {
-    gx = cdiv(n_rb, 4);
-    if (gx * n_tg < 256 * 8) gx = std::min<int64_t>(n_rb, cdiv(256 * 8, n_tg));
-  }
-  dim3 fgrd = NTLB_COL_FASTEST ? dim3((unsigned)n_tg, (unsigned)gx) : dim3((unsigned)gx, (unsigned)n_tg), fblk(256);
+  dim3 fgrd((unsigned)n_tg, (unsigned)std::min<int64_t>(n_rb, 65535)), fblk(256);
   NTLB_DISPATCH_GRID_SR(grid, sr, {
     if (x_dtype == NTLB_BF16)
       quant_tile_1x128_fast<DT_BF16, G_, S_, false, true><<<fgrd, fblk, 0, st>>>(a);
