@@ -27,6 +27,7 @@ import json
 import os
 import sys
 import time
+from typing import Optional
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "nano-train_amd"))
@@ -38,6 +39,7 @@ SPIN_UP_S = 0.3  # untimed sustained load before the counted warm-up steps
 
 
 def parse_args():
+    global SPIN_UP_S
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
@@ -58,19 +60,25 @@ def parse_args():
     p.add_argument("--backward", default="fp8", choices=["fp8", "ste"],
                    help="c3: fp8 = the quantized dgrad/wgrad recipe of the configuration; ste = the reference's "
                         "straight-through backward (dY unquantized, operands bf16(q*s) decoded in the GEMM)")
+    p.add_argument("--spin-up-s", type=float, default=SPIN_UP_S,
+                   help="seconds of untimed sustained load before the counted warm-up steps; 0 times the steps "
+                        "from an idle GPU, inside the clock ramp")
     a = p.parse_args()
+    SPIN_UP_S = a.spin_up_s
     if a.rounding is None:
         a.rounding = "stochastic" if a.config == "c3" else "nearest"
     return a
 
 
-def _spin_up(fn, seconds: float = SPIN_UP_S) -> None:
+def _spin_up(fn, seconds: Optional[float] = None) -> None:
     """Run fn untimed for `seconds` of wall time.  From idle, the clocks take
     about 50 ms of sustained load to settle (a c2 GEMM runs 7-30% slower over
     its first launches); the timed steps should see the sustained rate that a
     training loop runs at."""
     import torch
 
+    if seconds is None:
+        seconds = SPIN_UP_S
     t_end = time.perf_counter() + seconds
     i = 0
     while time.perf_counter() < t_end:
@@ -179,10 +187,18 @@ def other_config(args) -> dict:
     if args.config == "c4":
         tokens, routing, w_up, w_down = workloads.c4_inputs(device="cpu")
         w_gate = workloads.c4_gate(device="cpu")
+        # the dispatched rows for the comm-quant lines, gathered on the host
+        # (set-up, not a timed step)
+        order = torch.sort(routing.reshape(-1), stable=True).indices
+        xs = tokens[order // routing.shape[1]].to(dev)
+        del order
         tokens, routing = tokens.to(dev), routing.to(dev)
         w_up, w_down, w_gate = w_up.to(dev), w_down.to(dev), w_gate.to(dev)
-        order, tok_idx, offsets = moe.sort_by_expert(routing, 32)
-        xs = tokens[tok_idx].contiguous()
+        route = moe.route_by_expert(routing, 32)
+        offsets = route.offsets
+        # routing weights in the token dtype, as the reference's router returns them
+        topk_w = torch.rand(routing.shape, generator=torch.Generator().manual_seed(4), dtype=torch.float32).to(dev)
+        w_b = topk_w.to(torch.bfloat16)
         R, H = xs.shape
         inter = w_up.shape[1]
         qg = moe.quantize_expert_weights(w_gate, fmt=fmt)
@@ -199,8 +215,20 @@ def other_config(args) -> dict:
         # then the quantize pass writing tensor + (dq - tensor)
         ref_cq_us = _time_ms(lambda i: moe.comm_quant_dequant(xs, granularity="tile_1x128", rounding_mode="nearest",
                                                               seed=1, offset=i), args.steps, args.warmup, st) * 1e3
+        # the step: the single-rank expert loop's forward on HIP kernels, from
+        # the token rows and the routing to the token outputs
+        layer = _time_ms(lambda i: moe.local_moe_forward(tokens, routing, w_b, gate_up, down, n_experts=32, fmt=fmt),
+                         args.steps, args.warmup, st)
         mlp = _time_ms(lambda i: moe.expert_mlp(xs, offsets, gate_up, down, fmt=fmt), args.steps, args.warmup, st)
-        # the three kernels of one step, timed alone
+        # the kernels of one step, timed alone
+        route_us = _time_ms(lambda i: moe.route_by_expert(routing, 32), args.steps, args.warmup, st) * 1e3
+        fan_us = _time_ms(lambda i: ops.quant_tile_1x128_fanout(tokens, route.pos, 8, route.rows, fmt=fmt,
+                                                                want_nan_rows=True), args.steps, args.warmup,
+                          st) * 1e3
+        y_rows = moe.expert_mlp(xs, offsets, gate_up, down, fmt=fmt)
+        comb_rows_us = _time_ms(lambda i: moe.combine_rows(y_rows, route, routing, w_b, tokens.shape[0]), args.steps,
+                                args.warmup, st) * 1e3
+        del y_rows
         qx = ops.quant_tile_1x128(xs, fmt=fmt)
         _, qh = ops.gemm_swiglu_quant(qx, gate_up[0], gate_up[1], offsets=offsets, fmt=fmt, want_h=False)
         qx_us = _time_ms(lambda i: ops.quant_tile_1x128(xs, fmt=fmt), args.steps, args.warmup, st) * 1e3
@@ -212,7 +240,6 @@ def other_config(args) -> dict:
         # pack every (token, slot) assignment into a record, unpack as many received records
         from lowbit import ep
 
-        topk_w = torch.rand(routing.shape, generator=torch.Generator().manual_seed(4), dtype=torch.float32).to(dev)
         send = ep.pack_dispatch(tokens, routing, topk_w, experts_per_rank=4, ep_size=8, fmt=fmt)
         rcounts = send.counts.cpu().tolist()
         pack_us = _time_ms(lambda i: ep.pack_dispatch(tokens, routing, topk_w, experts_per_rank=4, ep_size=8, fmt=fmt),
@@ -227,7 +254,6 @@ def other_config(args) -> dict:
         out_rows = torch.randn((n_rec, H), generator=torch.Generator().manual_seed(5), dtype=torch.float32)
         out_rows = out_rows.to(dev, torch.bfloat16)
         ret = ep.pack_return(out_rows, rows, ep_size=8, fmt=fmt)
-        w_b = topk_w.to(torch.bfloat16)
         ret_us = _time_ms(lambda i: ep.pack_return(out_rows, rows, ep_size=8, fmt=fmt), args.steps, args.warmup,
                           st) * 1e3
         comb_us = _time_ms(lambda i: ep.combine(ret.records, routing, w_b, H=H, fmt=fmt), args.steps, args.warmup,
@@ -242,11 +268,34 @@ def other_config(args) -> dict:
         del send
         fl = 2.0 * R * H * inter  # one projection
         comm_bytes = R * H * 3 + R * (H // 128) * 4
-        res.update(value=round(3 * fl / (mlp * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(mlp, 4),
+        T_tok = tokens.shape[0]
+        # HBM bytes per gate/up launch from the committed FETCH_SIZE / WRITE_SIZE runs
+        traffic = None
+        prof = os.path.join(ROOT, "profiles", f"c4_moe_experts_{fmt}.json")
+        gu_name = f"gemm_blockscaled_kernel<{1 if fmt == 'e4m3' else 0}, true, true, 1>"
+        if os.path.exists(prof):
+            with open(prof) as fh:
+                for kname, tv in json.load(fh).get("traffic", {}).items():
+                    if gu_name in kname:
+                        traffic = int(tv["total_bytes"])
+        res.update(value=round(3 * fl / (layer * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(layer, 4),
                    dtype="fp8_e4m3" if fmt == "e4m3" else "int8",
-                   config={"workload": "c4 MoE local experts, ExpertMLP forward for all 32 experts: 1x128 x, "
-                                       "gate+up GEMM with SwiGLU and 1x128 h in the epilogue, down GEMM",
-                           "rows": R, "hidden": H, "inter": inter, "experts": 32, "top_k": 8},
+                   config={"workload": "c4 MoE local experts, the single-rank expert loop's forward for all 32 "
+                                       "experts: routing sort, 1x128 quantization of the token rows gathered by "
+                                       "expert, gate+up GEMM with SwiGLU and 1x128 h in the epilogue, down GEMM, "
+                                       "weighted combine into token order",
+                           "tokens": T_tok, "rows": R, "hidden": H, "inter": inter, "experts": 32, "top_k": 8},
+                   roofline={"bound": "mfma", "kernel": "gemm_blockscaled_kernel (gate+up with SwiGLU)",
+                             "achieved": round(2 * fl / (gu_ms * 1e-3) / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(2 * fl / (gu_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                             "traffic": traffic,
+                             "traffic_source": f"profiles/c4_moe_experts_{fmt}.md" if traffic else None,
+                             "avg_ms": round(gu_ms, 4)},
+                   expert_mlp_ms=round(mlp, 4),
+                   route_us=round(route_us, 2), gather_quant_x_us=round(fan_us, 2),
+                   gather_quant_x_GBs=round((T_tok * H * 2 + R * H + R * (H // 128) * 4) / fan_us / 1e3, 1),
+                   combine_rows_us=round(comb_rows_us, 2),
+                   combine_rows_GBs=round((R * H * 2 + T_tok * H * 2) / comb_rows_us / 1e3, 1),
                    gate_up_swiglu_tflops=round(2 * fl / (gu_ms * 1e-3) / 1e12, 2),
                    down_tflops=round(fl / (dn_ms * 1e-3) / 1e12, 2), quant_x_us=round(qx_us, 2),
                    comm_quant_us=round(comm_us, 2), comm_quant_GBs=round(comm_bytes / comm_us / 1e3, 1),
@@ -460,8 +509,11 @@ def cpu_baseline(args) -> dict:
         rows = 512
         tokens, routing, _, _ = workloads.c4_inputs(device="cpu", experts=0)
         n_exp = workloads.SHAPES[4]["experts"]
-        _, tok_idx, offsets = moe.sort_by_expert(routing, n_exp)
-        off = offsets.tolist()
+        # the rows of each expert in the reference's nonzero() order (a stable
+        # sort by expert) and the offset table, on the host
+        flat = routing.reshape(-1)
+        tok_idx = torch.sort(flat, stable=True).indices // routing.shape[1]
+        off = [0] + torch.bincount(flat, minlength=n_exp).cumsum(0).tolist()
         reach = int(np.searchsorted(np.asarray(off), rows, side="left"))
         _, _, w_up, w_down = workloads.c4_inputs(device="cpu", experts=min(reach, n_exp))
         w_gate = workloads.c4_gate(device="cpu", experts=min(reach, n_exp))
@@ -523,8 +575,8 @@ def _cpu_model() -> str:
 def main():
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build covers one GPU only; run with --gpus 1 "
-                                   "(the sharding design is described in DESIGN.md)"}))
+        print(json.dumps({"error": "this build measures one GPU only (the kernels run on one GPU's share of a "
+                                   "sharded layer); run with --gpus 1"}))
         sys.exit(2)
 
     import torch
@@ -621,6 +673,31 @@ def main():
     ref_tf = flops / (ref_ms * 1e-3) / 1e12
     other_tf = flops / (other_ms * 1e-3) / 1e12
 
+    # library ceilings at the same shape: hipBLASLt's FP8 GEMM through
+    # torch._scaled_mm with one scale per tensor and with row-wise scales (one
+    # per row of X, one per row of W, applied once in the epilogue).  Blockwise
+    # 1x128 / 128x128 scales inside K are not offered by the library.
+    lib_fp8 = None
+    if args.format == "e4m3" and not args.no_library_compare:
+        lib_fp8 = {}
+        xq0 = ops.quant_tile_1x128(sets[0][0], fmt="e4m3")
+        wq0, _ = ops.quant_block_128x128(sets[0][1], fmt="e4m3")
+        a8 = xq0.codes[:, :K].view(torch.float8_e4m3fn)
+        b8 = wq0.codes[:, :K].view(torch.float8_e4m3fn).t()
+        one = torch.ones((), device=dev, dtype=torch.float32)
+        sa_row = torch.rand(M, 1, device=dev, dtype=torch.float32) + 0.5
+        sb_col = torch.rand(1, N, device=dev, dtype=torch.float32) + 0.5
+        for name, sa_, sb_ in (("tensorwise", one, one), ("rowwise", sa_row, sb_col)):
+            try:
+                ms = _time_ms(lambda i: torch._scaled_mm(a8, b8, scale_a=sa_, scale_b=sb_, out_dtype=torch.bfloat16),
+                              args.steps, args.warmup, stream)
+                lib_fp8[name] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+                                 "frac_peak": round(flops / (ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                                 "avg_ms": round(ms, 4)}
+            except (RuntimeError, NotImplementedError) as exc:
+                lib_fp8[name] = {"error": str(exc).splitlines()[0][:160]}
+        del xq0, wq0, a8, b8
+
     # achievable HBM rate on this box: a 1 GiB device-to-device copy (read + write)
     ca = torch.empty(1 << 29, dtype=torch.int16, device=dev)
     cb = torch.empty_like(ca)
@@ -644,9 +721,15 @@ def main():
     if rounding == "nearest" and os.path.exists(prof):
         with open(prof) as fh:
             pj = json.load(fh)
+        # the kernels of this format (template argument GRID: 1 = e4m3, 0 = int
+        # grid); the line also runs the other format's GEMM once
+        g = 1 if args.format == "e4m3" else 0
+        names = {"gemm_blockscaled_kernel": f"gemm_blockscaled_kernel<{g}, true, false, 0>",
+                 "quant_tile_1x128": f"quant_tile_1x128_fast<1, {g}, false, false, false>",
+                 "quant_block_128x128": f"quant_block_128x128_fast<1, {g}, false, false>"}
         for kname, tv in pj.get("traffic", {}).items():
-            for short in ("gemm_blockscaled_kernel", "quant_tile_1x128", "quant_block_128x128"):
-                if short in kname:
+            for short, full in names.items():
+                if full in kname:
                     traffic[short] = int(tv["total_bytes"])
 
     result = {
@@ -703,6 +786,7 @@ def main():
                                    "avg_ms": round(ref_ms, 4)},
         f"{other_fmt}_gemm": {"kernel": "gemm_blockscaled_kernel", "tflops": round(other_tf, 2),
                               "frac_peak": round(other_tf / FP8_PEAK_TFLOPS, 4), "avg_ms": round(other_ms, 4)},
+        "hipblaslt_fp8_scaled_mm": lib_fp8,
         "hbm_copy_GB/s": round(copy_gbs, 1),
         "event_ms_per_step": round(avg(step_ms), 4),
         "cpu_baseline": None,

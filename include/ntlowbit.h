@@ -85,6 +85,25 @@ int ntlb_quant_tile_1x128(const void* x, int x_dtype, int64_t R, int64_t K, int6
                           int64_t lddq, int32_t* nan_rows, void* stream);
 
 /*
+ * ntlb_quant_tile_1x128 of the token rows gathered by expert: the gather
+ * tokens[token_indices] of the per-expert loop (moe.py:1081, :484) fused into
+ * the quantizer.  Token row r of x [T, K] (row stride ldx) becomes output row
+ * pos[r*fan_k + f] for f < fan_k (pos from ntlb_ep_partition on topk_idx
+ * [T, fan_k] with divisor 1 and one bucket per expert), each token row read
+ * once.  Codes, scales (s_row, s_col), nan_rows and the SR element index
+ * (p*K + column) are those ntlb_quant_tile_1x128 writes for row p of the
+ * gathered matrix [rows, K], bit for bit.  A negative pos entry (an
+ * assignment a capacity limit dropped) writes nothing, and output rows that
+ * no entry names are left as they are; entries at or past rows are clamped
+ * to rows - 1.  x bf16 or fp32, K % 8 == 0, 16-byte aligned rows, codes
+ * 8-byte aligned, ldc >= ceil(K/128)*128 and a multiple of 8.
+ */
+int ntlb_quant_tile_1x128_fanout(const void* x, int x_dtype, int64_t T, int64_t K, int64_t ldx, const int32_t* pos,
+                                 int64_t fan_k, int64_t rows, int grid, int qmax, int rounding, int scale_rule,
+                                 uint64_t seed, uint64_t offset, uint8_t* codes, int64_t ldc, float* scales,
+                                 int64_t s_row, int64_t s_col, int32_t* nan_rows, void* stream);
+
+/*
  * 128x128 block quantizer for a 2-D weight.  Replaces _block_quant_dequant
  * (te_backend.py:113-149).
  *   w [N, K] (row stride ldw); codes [N, ldc]; scales [ceil(N/128), T] via
@@ -574,6 +593,23 @@ int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* to
  * counts, moe.py:851-854), read during the call; needed only with src_rank;
  * ep_size <= 256.  n < 2^31.
  */
+/*
+ * Single-rank combine of the local experts' outputs (moe.py:1087-1088,
+ * LocalRoutedMoE :489-490): out[t] starts at zero and, for token t's slots in
+ * ascending expert id (the reference's expert loop order), takes
+ * out[t] += y[pos[t*K + s]] * topk_w[t, s], the product in torch's promoted
+ * dtype of (y, w) and the sum in the output dtype, each rounded on its own.
+ * y [n, H] (row stride ldy) holds the expert outputs in the output dtype, rows
+ * in expert order (pos from ntlb_ep_partition on topk_idx, the order of
+ * ntlb_quant_tile_1x128_fanout); a negative pos entry (dropped) adds nothing,
+ * entries at or past n are clamped to n - 1.  topk_idx int32 (idx_dtype 0)
+ * or int64 (1) and topk_w (w_dtype) [T, K] contiguous, 1 <= K <= 32, out
+ * [T, ldo].
+ */
+int ntlb_moe_combine_rows(const void* y, int64_t ldy, int64_t n, const int32_t* pos, const void* topk_idx,
+                          int idx_dtype, const void* topk_w, int w_dtype, int64_t T, int64_t K, int64_t H, void* out,
+                          int out_dtype, int64_t ldo, void* stream);
+
 int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv, int64_t rows,
                            const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc, float* scales,
                            int64_t s_row, int64_t s_col, int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,

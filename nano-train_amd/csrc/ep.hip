@@ -379,6 +379,97 @@ __global__ void __launch_bounds__(256) ep_combine_kernel(const uint8_t* rec, int
   }
 }
 
+// Single-rank combine of the local expert outputs (moe.py:1087-1088 and
+// :489-490, `output[token_indices] += expert_out * weights` once per expert in
+// ascending expert id): one workgroup per token t; thread j owns columns
+// [8j + 2048i, +8).  Slot s of t names row pos[t*K + s] of y (rows in expert
+// order, clamped below n; negative: dropped by a capacity limit, adds
+// nothing).  Per expert,
+// the product is rounded to the promoted dtype of y and w (ROUND_P: both the
+// output dtype) and the sum to the output dtype, as the two torch ops do.
+template <int OUT_DT, bool ROUND_P>
+__global__ void __launch_bounds__(256) moe_combine_rows_kernel(const void* y, int64_t ldy, int64_t n,
+                                                               const int32_t* pos,
+                                                               const void* topk_idx, int idx_dt, const void* topk_w,
+                                                               int w_dt, int K, int64_t H, void* out, int64_t ldo,
+                                                               int vec) {
+#pragma clang fp contract(off)  // each product and sum rounds on its own
+  __shared__ int64_t s_e[EP_COMBINE_MAX_K];
+  __shared__ int32_t s_row[EP_COMBINE_MAX_K];
+  __shared__ float s_w[EP_COMBINE_MAX_K];
+  const int64_t t = blockIdx.x;
+  const int k = threadIdx.x;
+  if (k < K) {
+    const int64_t a = t * K + k;
+    s_e[k] = idx_dt == 1 ? reinterpret_cast<const int64_t*>(topk_idx)[a]
+                         : (int64_t) reinterpret_cast<const int32_t*>(topk_idx)[a];
+  }
+  __syncthreads();
+  if (k < K) {
+    // slot k's place in ascending expert id (ties, which routing does not
+    // produce, keep slot order)
+    const int64_t ek = s_e[k];
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += (s_e[j] < ek || (s_e[j] == ek && j < k)) ? 1 : 0;
+    s_row[rank] = pos[t * K + k];
+    s_w[rank] = load_elem(topk_w, w_dt, t * K + k);
+  }
+  __syncthreads();
+  for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < K; j0 += 8) {
+      // up to eight rows in flight at once: slots past K or dropped read row
+      // 0 of y and are not added
+      float v[8][8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = min(j0 + u, K - 1);
+        const int64_t off = min<int64_t>(max(s_row[j], 0), n - 1) * ldy + c0;
+        if constexpr (OUT_DT == DT_BF16) {
+          if (vec) {
+            const uint4 w = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(y) + off);
+            const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              v[u][2 * i] = __uint_as_float(ww[i] << 16);
+              v[u][2 * i + 1] = __uint_as_float(ww[i] & 0xFFFF0000u);
+            }
+            continue;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[u][i] = c0 + i < H ? load_elem(y, OUT_DT, off + i) : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u;
+        if (j >= K || s_row[j] < 0) continue;
+        const float w = s_w[j];
+        float p[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) p[i] = v[u][i] * w;
+        if constexpr (ROUND_P) round8<OUT_DT>(p);  // expert_out * weights in the output dtype
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = acc[i] + p[i];
+        round8<OUT_DT>(acc);  // output[token_indices] += ..., an op of the output dtype
+      }
+    }
+    if constexpr (OUT_DT == DT_BF16) {
+      if (vec) {
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = bf16x2_bits(acc[2 * i], acc[2 * i + 1]);
+        *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + t * ldo + c0) =
+            make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        continue;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (c0 + i < H) store_elem(out, OUT_DT, t * ldo + c0 + i, acc[i]);
+  }
+}
+
 }  // namespace ntlb
 
 using namespace ntlb;
@@ -487,6 +578,41 @@ extern "C" int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, con
     if (out_dtype == NTLB_BF16) launch(E(), B()); else if (out_dtype == NTLB_F32) launch(E(), F()); else launch(E(), Hh());
   } else {
     if (out_dtype == NTLB_BF16) launch(I(), B()); else if (out_dtype == NTLB_F32) launch(I(), F()); else launch(I(), Hh());
+  }
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_moe_combine_rows(const void* y, int64_t ldy, int64_t n, const int32_t* pos, const void* topk_idx,
+                                     int idx_dtype, const void* topk_w, int w_dtype, int64_t T, int64_t K,
+                                     int64_t H, void* out, int out_dtype, int64_t ldo, void* stream) {
+  const char* fn = "ntlb_moe_combine_rows";
+  if (T < 0 || H < 0 || n < 0 || K < 1 || K > EP_COMBINE_MAX_K || (idx_dtype != 0 && idx_dtype != 1) ||
+      !valid_dtype(w_dtype) || !valid_dtype(out_dtype))
+    return fail(NTLB_EINVAL, "%s: bad argument (1 <= K <= %d)", fn, EP_COMBINE_MAX_K);
+  if (ldy < H || ldo < H) return fail(NTLB_EINVAL, "%s: ldy and ldo must be >= H", fn);
+  if (T == 0 || H == 0) return NTLB_OK;
+  if (!out || !pos || !topk_idx || !topk_w || (n > 0 && !y)) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (n == 0) return fail(NTLB_EINVAL, "%s: no expert rows for %lld tokens", fn, (long long)T);
+  hipStream_t st = as_stream(stream);
+  const int vec = aligned(y, 16) && aligned(out, 16) && ldy % 8 == 0 && ldo % 8 == 0 && H % 8 == 0;
+  // the product rounds to the output dtype when torch's promotion of (y, w)
+  // is that dtype: w of the same dtype, which is not fp32
+  const bool round_p = w_dtype == out_dtype && out_dtype != NTLB_F32;
+  auto launch = [&](auto outc, auto rpc) {
+    moe_combine_rows_kernel<decltype(outc)::value, decltype(rpc)::value><<<(unsigned)T, 256, 0, st>>>(
+        y, ldy, n, pos, topk_idx, idx_dtype, topk_w, w_dtype, (int)K, H, out, ldo, vec);
+  };
+  using B = std::integral_constant<int, DT_BF16>;
+  using F = std::integral_constant<int, DT_F32>;
+  using Hh = std::integral_constant<int, DT_F16>;
+  using Y = std::integral_constant<bool, true>;
+  using N = std::integral_constant<bool, false>;
+  if (out_dtype == NTLB_BF16) {
+    if (round_p) launch(B(), Y()); else launch(B(), N());
+  } else if (out_dtype == NTLB_F16) {
+    if (round_p) launch(Hh(), Y()); else launch(Hh(), N());
+  } else {
+    launch(F(), N());
   }
   return check_launch(fn);
 }

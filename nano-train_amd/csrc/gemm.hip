@@ -142,6 +142,35 @@ __device__ __forceinline__ v4f mma_block(const v8i& p, const v8i& q) {
   }
 }
 
+// The raw MFMA result of one 16x16 block over one K block (fp32 for e4m3,
+// int32 for the int grid: at most 128 * 127^2 in magnitude, exact in fp32)
+// and its conversion, so that a pipelined promotion can keep the raw form
+// until it is consumed.
+template <int GRID>
+using raw_t = typename std::conditional<GRID == GRID_E4M3, v4f, v4i>::type;
+
+template <int GRID>
+__device__ __forceinline__ raw_t<GRID> mma_raw(const v8i& p, const v8i& q) {
+  if constexpr (GRID == GRID_E4M3) {
+    return mma_block<GRID>(p, q);
+  } else {
+    v4i z = {0, 0, 0, 0};
+    v4i p0 = {p[0], p[1], p[2], p[3]}, p1 = {p[4], p[5], p[6], p[7]};
+    v4i q0 = {q[0], q[1], q[2], q[3]}, q1 = {q[4], q[5], q[6], q[7]};
+    v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(p0, q0, z, 0, 0, 0);
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(p1, q1, s, 0, 0, 0);
+  }
+}
+
+template <int GRID>
+__device__ __forceinline__ v4f raw_f32(const raw_t<GRID>& r) {
+  if constexpr (GRID == GRID_E4M3) {
+    return r;
+  } else {
+    return (v4f){(float)r[0], (float)r[1], (float)r[2], (float)r[3]};
+  }
+}
+
 // Direct-to-LDS copies of one K block through buffer resources: wave w moves
 // the 8-row groups w, w+8, w+16, w+24 (1 KiB each) of A and of B, so bit 3 of
 // every row it writes equals w & 1.  Lane i lands at byte 16*i of its group
@@ -382,32 +411,36 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
 #pragma unroll
     for (int tm = 0; tm < 8; ++tm) sam_all[tm] = s_cur[wm * 128 + tm * 16 + (lane & 15)];
     v8i af = load_frag(ta, wm * 128, lane);
-    if constexpr (GRID == GRID_E4M3 && B_UNIFORM) {
+    if constexpr (B_UNIFORM) {
       // The promotion is software pipelined: step tm issues group tm's four
-      // MFMAs and promotes group tm-1's results meanwhile, one MFMA then four
-      // FMAs at a time, so the FMAs never wait on the MFMA they depend on.
-      // (16 more VGPRs: the other variants would spill, and keep the plain order.)
-      v4f dp[4];
+      // blocks of MFMAs and promotes group tm-1's results meanwhile, one
+      // block's MFMAs then one block's VALU work at a time (e4m3: 1 MFMA, 4
+      // FMAs; int grid: 2 MFMAs, 4 converts and 4 FMAs), so the VALU never
+      // waits on the MFMA it depends on.  The int32 partials stay raw until
+      // then.  The per-column B scales of the other variant would spill here,
+      // so that variant keeps the plain order.
+      constexpr int MF = GRID == GRID_E4M3 ? 1 : 2, VA = GRID == GRID_E4M3 ? 4 : 8;
+      raw_t<GRID> dp[4];
 #pragma unroll
       for (int tm = 0; tm < 9; ++tm) {
         v8i af_next;
-        v4f d[4];
+        raw_t<GRID> d[4];
         if (tm < 8) {
           if (tm + 1 < 8) af_next = load_frag(ta, wm * 128 + (tm + 1) * 16, lane);
           // the next block's copies go out one group per 16-row step, spread
           // over the first half of the MFMA phase
           if (tm < 4) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kn, wave, tm);
 #pragma unroll
-          for (int tn = 0; tn < 4; ++tn) d[tn] = mma_block<GRID>(bf[tn], af);
+          for (int tn = 0; tn < 4; ++tn) d[tn] = mma_raw<GRID>(bf[tn], af);
         }
         if (tm > 0) {
           const float s = sam_all[tm - 1] * sbu;
 #pragma unroll
-          for (int tn = 0; tn < 4; ++tn) acc[tm - 1][tn] += dp[tn] * s;
+          for (int tn = 0; tn < 4; ++tn) acc[tm - 1][tn] += raw_f32<GRID>(dp[tn]) * s;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+            __builtin_amdgcn_sched_group_barrier(0x008, MF, 0);  // one block's MFMAs
+            __builtin_amdgcn_sched_group_barrier(0x002, VA, 0);  // one block's promotion
           }
           // group tm-1's accumulators are final here, and no later LDS read
           // moves above this point

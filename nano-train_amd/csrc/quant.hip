@@ -40,12 +40,15 @@ struct QuantArgs {
   int dq_dtype;
   int64_t lddq;
   int32_t* nan_rows;
-  // fast 1x128 path, fan-out (the expert-parallel send records): input row r
-  // goes to the output rows fan_pos[r * fan_k + k], k < fan_k (clamped below
-  // fan_rows); output row p's NaN flag is nan_rows[p * nan_stride]
+  // fast 1x128 path, fan-out (the expert-parallel send records and the
+  // gather by expert): input row r goes to the output rows
+  // fan_pos[r * fan_k + k], k < fan_k (clamped below fan_rows; a negative
+  // entry writes nothing); output row p's NaN flag is nan_rows[p * nan_stride];
+  // fan_nt stores the codes with the non-temporal hint
   const int32_t* fan_pos;
   int64_t fan_k, fan_rows;
   int64_t nan_stride;
+  bool fan_nt;
 };
 
 // Load 8 consecutive elements [k0, k0+8) of a row as fp32, zero past K.
@@ -243,7 +246,9 @@ __device__ __forceinline__ void tile_quant_fan(const Chunk8<IN_DT> (&c)[TILE_TU]
   }
   const int nt = min(TILE_TU, T - t0);
   for (int64_t f = 0; f < a.fan_k; ++f) {
-    const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + f], 0), a.fan_rows - 1);
+    const int32_t pr = a.fan_pos[r * a.fan_k + f];
+    if (pr < 0) continue;  // an assignment a capacity limit dropped
+    const int64_t p = min<int64_t>(pr, a.fan_rows - 1);
     bool any_nan = false;
 #pragma unroll
     for (int u = 0; u < TILE_TU; ++u) {
@@ -256,10 +261,11 @@ __device__ __forceinline__ void tile_quant_fan(const Chunk8<IN_DT> (&c)[TILE_TU]
         nan[u] = quant8_tile<GRID, true, false>(v[u], m[u], s[u], a.qmaxf, rb, lo[u], hi[u], q);
       }
       any_nan |= nan[u];
-      // the dispatch records (fan_k > 1) go out with the non-temporal hint:
-      // 10% faster at c4 (76 -> 68 us); the send-back pack (fan_k == 1)
-      // measured 7% slower with it and stores normally
-      if (a.fan_k > 1)
+      // the dispatch records go out with the non-temporal hint: 10% faster
+      // at c4 (76 -> 68 us); the send-back pack measured 7% slower with it,
+      // and the rows gathered by expert feed the next GEMM, so both store
+      // normally
+      if (a.fan_nt)
         store8_nt(a.codes + p * a.ldc + k0, lo[u], hi[u]);
       else
         *reinterpret_cast<uint2*>(a.codes + p * a.ldc + k0) = make_uint2(lo[u], hi[u]);
@@ -319,12 +325,16 @@ __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
   int64_t rb = blockIdx.y;  // row-block index
   if (rb >= n_rb) return;
   Chunk8<IN_DT> cur[TILE_TU];
+  int64_t r = rb * 16 + (threadIdx.x >> 4);
+  // the loads at the end of the body, not at its head: head-first, the
+  // compiler gave the stochastic-rounding and dq variants 4-13 more VGPRs
+  tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
   for (;;) {
-    const int64_t r = rb * 16 + (threadIdx.x >> 4);
-    tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
     if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ, FAN>(cur, a, r, t0, T, lane16);  // whole 16-lane rows
     rb += gridDim.y;
     if (rb >= n_rb) return;
+    r = rb * 16 + (threadIdx.x >> 4);
+    tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
   }
 }
 
@@ -507,11 +517,14 @@ __global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArg
   int64_t nb = blockIdx.y;
   if (nb >= NB) return;
   Chunk8<IN_DT> cur[BLK_RPT];
+  // loads at the end of the body, as in the 1x128 kernel (head-first took
+  // 59 -> 83 VGPRs and halved the resident workgroups)
+  block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
   for (;;) {
-    block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
     block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
     nb += gridDim.y;
     if (nb >= NB) return;
+    block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
   }
 }
 
@@ -945,8 +958,9 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
 
   // SR words in two halves: columns 4h..4h+3 of every row share one Philox
   // block (K % 8 == 0 and col0 % 8 == 0 align the element index), so only
-  // 32 words are live at a time
-#pragma unroll
+  // 32 words are live at a time.  Fully unrolled: a rolled loop would index
+  // c[] by h at run time and move it to scratch memory
+#pragma clang loop unroll(full)
   for (int h = 0; h < 2; ++h) {
   uint32_t rb[8][4];  // [row i][column j - 4h]
 #pragma unroll
@@ -1184,6 +1198,7 @@ static QuantArgs make_args(const void* x, int64_t R, int64_t K, int64_t ldx, int
   a.fan_k = 1;
   a.fan_rows = R;
   a.nan_stride = 1;
+  a.fan_nt = false;
   return a;
 }
 
@@ -1244,6 +1259,42 @@ extern "C" int ntlb_quant_tile_1x128(const void* x, int x_dtype, int64_t R, int6
     else
       quant_tile_1x128_kernel<D_, G_, S_, false><<<grd, blk, 0, st>>>(a);
   }));
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_quant_tile_1x128_fanout(const void* x, int x_dtype, int64_t T, int64_t K, int64_t ldx,
+                                            const int32_t* pos, int64_t fan_k, int64_t rows, int grid, int qmax,
+                                            int rounding, int scale_rule, uint64_t seed, uint64_t offset,
+                                            uint8_t* codes, int64_t ldc, float* scales, int64_t s_row, int64_t s_col,
+                                            int32_t* nan_rows, void* stream) {
+  const char* fn = "ntlb_quant_tile_1x128_fanout";
+  int rc = check_common(fn, x, x_dtype, T, K, ldx, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (fan_k < 1 || rows < 0 || T * fan_k > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: bad fan_k or rows", fn);
+  const int64_t Tt = cdiv(K, 128);
+  if (ldc < Tt * 128 || (ldc & 7)) return fail(NTLB_EINVAL, "%s: ldc must be >= ceil(K/128)*128 and a multiple of 8", fn);
+  if (T == 0 || rows == 0 || K == 0) return NTLB_OK;
+  if (!codes || !scales || !pos) return fail(NTLB_EINVAL, "%s: codes/scales/pos NULL", fn);
+  const bool vec = aligned(x, 16) && ((ldx * dtype_size(x_dtype)) % 16 == 0);
+  if (!(vec && K % 8 == 0 && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) && aligned(codes, 8) &&
+        ldc % 8 == 0))
+    return fail(NTLB_EUNSUPPORTED, "%s: needs bf16/fp32 rows, K %% 8 == 0, 16-byte aligned rows, 8-byte aligned codes",
+                fn);
+  QuantArgs a = make_args(x, T, K, ldx, grid, qmax, scale_rule, seed, offset, codes, ldc, scales, s_row, s_col,
+                          nullptr, 0, 0, nan_rows);
+  a.fan_pos = pos;
+  a.fan_k = fan_k;
+  a.fan_rows = rows;
+  const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
+  hipStream_t st = as_stream(stream);
+  const int64_t n_rb = cdiv(T, 16), n_tg = cdiv(Tt, TILE_TU);
+  dim3 fgrd((unsigned)n_tg, (unsigned)std::min<int64_t>(n_rb, 65535)), fblk(256);
+  NTLB_DISPATCH_GRID_SR(grid, sr, {
+    if (x_dtype == NTLB_BF16)
+      quant_tile_1x128_fast<DT_BF16, G_, S_, false, true><<<fgrd, fblk, 0, st>>>(a);
+    else
+      quant_tile_1x128_fast<DT_F32, G_, S_, false, true><<<fgrd, fblk, 0, st>>>(a);
+  });
   return check_launch(fn);
 }
 
@@ -1691,6 +1742,7 @@ static int ep_pack_payload(const char* fn, const void* x, int x_dtype, int64_t n
   a.fan_k = fan_k;
   a.fan_rows = n_rec;
   a.nan_stride = R / 4;
+  a.fan_nt = fan_k > 1;
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
   if (amax_bits) {
     dim3 grd(grid_for(n_in * (s_off >> 3), 256, 256 * 16)), blk(256);

@@ -82,6 +82,9 @@ SIGNATURES = {
     "ntlb_colsum": [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P],
     "ntlb_colsum_workspace_bytes": [_I64, _I64],
     "ntlb_ep_record_bytes": [_I64],
+    "ntlb_quant_tile_1x128_fanout": [_P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _I32, _I32, _I32, _I32, _U64, _U64,
+                                     _P, _I64, _P, _I64, _I64, _P, _P],
+    "ntlb_moe_combine_rows": [_P, _I64, _I64, _P, _P, _I32, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_ep_partition": [_P, _I32, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P, _I64, _P],
     "ntlb_ep_pack_records": [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P, _I32, _I64, _I64, _I32, _I32, _I32,
                              _I32, _U64, _U64, _P, _P],

@@ -15,9 +15,16 @@ all-to-all would carry (codes plus per-row 1x128 scales, e4m3 or int grid);
 the reference has no counterpart (it all-to-alls the dequantized bf16 tensor,
 moe.py:787-793).
 
-sort_by_expert() builds the token-offset table and grouped_linear() runs one
-Linear per expert over the rows sorted by expert (moe.py:888-962 loops over
-experts in Python instead).
+route_by_expert() orders the (token, slot) assignments by expert with one
+stable counting sort on the GPU (ntlb_ep_partition), which gives the rows of
+each expert in the order the reference's per-expert nonzero() selects them
+(moe.py:1077, :478) and the token-offset table.  local_moe_forward() is the
+single-rank expert loop (moe.py:1062-1093, LocalRoutedMoE :476-491) on HIP
+kernels only: the routing sort, the 1x128 quantization of the token rows
+gathered by expert (one read per token), the gate/up GEMM with SwiGLU and
+h's quantization in its epilogue, the down GEMM, and the weighted combine into
+token order.  grouped_linear() runs one Linear per expert over rows already
+sorted by expert.
 """
 
 from __future__ import annotations
@@ -131,19 +138,47 @@ def comm_dequant(payload: CommPayload, dtype: Optional[torch.dtype] = None) -> t
     return out.reshape(payload.shape)
 
 
+@dataclass
+class ExpertRouting:
+    """The (token, slot) assignments of top-k routing ordered by expert.
+
+    pos[a] is assignment a's row in expert order (a = token * top_k + slot),
+    inv[row] the assignment of a row; rows of one expert keep assignment
+    order, as the reference's (topk_indices == e).nonzero() lists them.
+    offsets int32 [E+1] is the token-offset table of the grouped GEMMs."""
+
+    pos: torch.Tensor  # int32 [T*top_k]
+    inv: torch.Tensor  # int32 [T*top_k]
+    counts: torch.Tensor  # int64 [E]
+    offsets: torch.Tensor  # int32 [E+1]
+    top_k: int
+
+    @property
+    def rows(self) -> int:
+        return self.pos.numel()
+
+
+def route_by_expert(expert_ids: torch.Tensor, n_experts: int) -> ExpertRouting:
+    """One stable counting sort of expert_ids [T, k] (int32 or int64) by
+    expert on the GPU (ntlb_ep_partition: three kernels, no host sync)."""
+    from . import ep
+
+    if expert_ids.dim() != 2:
+        raise ValueError("expert_ids must be [tokens, top_k]")
+    pos, inv, counts, offsets = ep.partition(expert_ids.reshape(-1), divisor=1, buckets=n_experts)
+    return ExpertRouting(pos, inv, counts, offsets, expert_ids.shape[1])
+
+
 def sort_by_expert(expert_ids: torch.Tensor, n_experts: int):
     """Token-offset table for top-k routing.
 
     expert_ids [T, k] int -> (order [T*k] int64 indices into the flattened
     (token, slot) pairs sorted by expert, stable; token_index [T*k] the source
-    token of each sorted row; offsets int32 [E+1])."""
-    flat = expert_ids.reshape(-1).to(torch.int64)
-    order = torch.sort(flat, stable=True).indices
-    counts = torch.bincount(flat, minlength=n_experts)
-    offsets = torch.zeros(n_experts + 1, dtype=torch.int32, device=expert_ids.device)
-    offsets[1:] = torch.cumsum(counts, 0).to(torch.int32)
-    token_index = order // expert_ids.shape[1]
-    return order, token_index, offsets
+    token of each sorted row; offsets int32 [E+1]).  route_by_expert() holds
+    the same order without the int64 index tensors."""
+    r = route_by_expert(expert_ids, n_experts)
+    order = r.inv.to(torch.int64)
+    return order, order // expert_ids.shape[1], r.offsets
 
 
 def quantize_expert_weights(w: torch.Tensor, *, fmt: str = "e4m3", bits: int = 8, rounding: str = "nearest",
@@ -260,3 +295,61 @@ def expert_mlp(
     out = ops.gemm_grouped_blockscaled(qh, d_codes, d_scales, offsets, N=d_codes.shape[1], out_dtype=out_dtype,
                                        b_nan_rows=d_nan)
     return (out, h) if want_h else out
+
+
+def combine_rows(y: torch.Tensor, routing: ExpertRouting, expert_ids: torch.Tensor, topk_w: torch.Tensor,
+                 n_tokens: int) -> torch.Tensor:
+    """out[t] = sum over token t's slots, in ascending expert id, of
+    y[pos[t*k + s]] * topk_w[t, s], formed as the reference's expert loop forms
+    it (moe.py:1087-1088, :489-490: `output[token_indices] += expert_out *
+    weights`, each product and each sum rounded to its torch dtype).  y [rows,
+    H] holds the expert outputs in expert order, in the output dtype."""
+    ops._require_device(y)
+    if y.dim() != 2 or y.stride(-1) != 1:
+        raise ValueError("y must be a row-major [rows, H] tensor")
+    if expert_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError("expert_ids must be int32 or int64")
+    k = routing.top_k
+    if expert_ids.numel() != n_tokens * k or topk_w.numel() != n_tokens * k:
+        raise ValueError("expert_ids and topk_w must be [tokens, top_k]")
+    H = y.shape[1]
+    out = torch.empty((n_tokens, H), dtype=y.dtype, device=y.device)
+    ids = expert_ids.contiguous()
+    w = topk_w.contiguous()
+    _lib.call("ntlb_moe_combine_rows", y.data_ptr(), y.stride(0), y.shape[0], routing.pos.data_ptr(), ids.data_ptr(),
+              1 if ids.dtype == torch.int64 else 0, w.data_ptr(), ops._dtype_code(w.dtype), n_tokens, k, H,
+              out.data_ptr(), ops._dtype_code(out.dtype), out.stride(0), ops._stream())
+    return out
+
+
+def local_moe_forward(
+    tokens: torch.Tensor,
+    expert_ids: torch.Tensor,
+    topk_w: torch.Tensor,
+    gate_up,
+    down,
+    *,
+    n_experts: int,
+    fmt: str = "e4m3",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    routing: Optional[ExpertRouting] = None,
+):
+    """The single-rank routed expert loop (moe.py:1062-1093, LocalRoutedMoE
+    :476-491 without capacity drop) for all local experts at once: returns
+    the token outputs [T, H] in tokens.dtype.
+
+    Kernels: the routing sort (skipped when `routing` is given), the 1x128
+    quantization of the token rows gathered by expert (each token row read
+    once), the gate/up GEMM with SwiGLU and h's 1x128 quantization in its
+    epilogue, the down GEMM, and the weighted combine into token order.  gate_up
+    and down are as for expert_mlp()."""
+    if routing is None:
+        routing = route_by_expert(expert_ids, n_experts)
+    qx = ops.quant_tile_1x128_fanout(tokens, routing.pos, routing.top_k, routing.rows, fmt=fmt, bits=bits,
+                                     rounding=rounding, seed=seed, offset=offset, want_nan_rows=True)
+    y = expert_mlp(qx, routing.offsets, gate_up, down, fmt=fmt, bits=bits, rounding=rounding, seed=seed,
+                   offset=offset, out_dtype=tokens.dtype)
+    return combine_rows(y, routing, expert_ids, topk_w, tokens.shape[0])

@@ -139,6 +139,50 @@ def quant_tile_1x128(
     return QTensor(codes, scales, s_row, s_col, 0, grid_code(fmt), R, K, nan_rows, dq)
 
 
+def quant_tile_1x128_fanout(
+    x: torch.Tensor,
+    pos: torch.Tensor,
+    fan_k: int,
+    rows: int,
+    *,
+    fmt: str = "int_grid",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+    scale_rule: int = _lib.SCALE_AFTER_DIVIDE,
+    want_nan_rows: bool = False,
+) -> QTensor:
+    """quant_tile_1x128 of the rows of x [T, K] gathered by expert, without the
+    gathered copy: row pos[r*fan_k + f] of the result is token row r (the
+    gather tokens[token_indices] of moe.py:1081 / :484 fused into the
+    quantizer).  pos is int32 [T*fan_k] (ep.partition of topk_idx with divisor
+    1); codes, tile-major scales and SR bits equal quant_tile_1x128 of the
+    gathered [rows, K] matrix.  A negative pos entry writes nothing, so the
+    rows it would have named hold no codes."""
+    _require_device(x)
+    if x.dim() != 2:
+        raise ValueError("x must be [T, K]")
+    if pos.dtype != torch.int32 or pos.numel() != x.shape[0] * fan_k:
+        raise ValueError(f"pos must be int32 with T*fan_k = {x.shape[0] * fan_k} entries")
+    x2 = x if x.stride(-1) == 1 else x.contiguous()
+    pos = pos.contiguous()
+    T_in, K = x2.shape
+    T = cdiv(K, 128)
+    ldc = T * 128
+    dev = x.device
+    codes = torch.empty((rows, ldc), dtype=torch.uint8, device=dev)
+    rp = cdiv(max(rows, 1), 4) * 4
+    scales = torch.empty((T, rp), dtype=torch.float32, device=dev)
+    nan_rows = torch.zeros(rows, dtype=torch.int32, device=dev) if want_nan_rows else None
+    call(
+        "ntlb_quant_tile_1x128_fanout", x2.data_ptr(), _dtype_code(x2.dtype), T_in, K, x2.stride(0), pos.data_ptr(),
+        fan_k, rows, grid_code(fmt), (1 << (bits - 1)) - 1, rounding_code(rounding), scale_rule, seed, offset,
+        codes.data_ptr(), ldc, scales.data_ptr(), 1, rp, _ptr(nan_rows), _stream(),
+    )
+    return QTensor(codes, scales, 1, rp, 0, grid_code(fmt), rows, K, nan_rows, None)
+
+
 def quant_block_128x128(
     w: torch.Tensor,
     *,
