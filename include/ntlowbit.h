@@ -480,6 +480,30 @@ int ntlb_gemm_fp8p(const void* x, int64_t ldx, const uint8_t* w_codes, const flo
                    int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream);
 
 /*
+ * The dequant-fused GEMMs with a bias and a workspace: fmt NTLB_LOWBIT_NF4
+ * (w packed nibbles, fp32 block scales, block as ntlb_gemm_nf4),
+ * NTLB_LOWBIT_FP8P (w e4m3 bytes, block as ntlb_gemm_fp8p) or
+ * NTLB_LOWBIT_MXFP4 (w packed e2m1, e8m0 scales; block ignored).  bias
+ * optional [N] (bias_dtype), added in fp32 before the output rounding, as
+ * F.linear(x, weight, bias) does in the persistent forward
+ * (layers.py:595-632).  workspace (256-byte aligned, zeroed before its first
+ * use; every call leaves it zeroed) of ws_bytes >=
+ * ntlb_gemm_lowbit_workspace_bytes(M, N, K) enables the split-K tail: the
+ * output tiles past the last whole wave of the grid are cut into 2-8 K ranges
+ * when they would fill at most half the chip; NULL runs every tile whole.
+ * Concurrent calls need separate workspaces.  No counterpart in the
+ * reference beyond the fused forward (the bias and the workspace are this
+ * interface's own).
+ */
+#define NTLB_LOWBIT_NF4 0
+#define NTLB_LOWBIT_MXFP4 1
+#define NTLB_LOWBIT_FP8P 2
+int64_t ntlb_gemm_lowbit_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int ntlb_gemm_lowbit_ws(int fmt, const void* x, int64_t ldx, const uint8_t* w, const void* w_scales, int64_t block,
+                        const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K, void* y, int y_dtype,
+                        int64_t ldy, void* workspace, int64_t ws_bytes, void* stream);
+
+/*
  * Expert-parallel dispatch wire format: one fixed-size record per routed
  * (token, slot) assignment, so that a single byte all-to-all replaces the
  * payload and four metadata all-to-alls of _dispatch_tokens

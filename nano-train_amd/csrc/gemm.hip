@@ -27,6 +27,7 @@
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 #include "ntlb_quant8.h"
+#include "ntlb_splitk.h"
 
 namespace ntlb {
 
@@ -99,6 +100,7 @@ constexpr int EPI_ROWS = 32;
 constexpr int EPI_PITCH_F32 = 64 * 4 + 16;  // bytes per staged row (fp32)
 constexpr int EPI_PITCH_16 = 64 * 2 + 16;   // bytes per staged row (bf16 / fp16)
 static_assert(EPI_ROWS * EPI_PITCH_F32 <= TILE_A / 2, "epilogue slice exceeds half an operand buffer");
+static_assert(NTHREADS == SPLIT_THREADS, "the split-K exchange assumes 512 threads and acc[8][4]");
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -214,35 +216,6 @@ __device__ __forceinline__ uint8_t* slab_row(uint8_t* s0, uint8_t* s1, uint8_t* 
   return (k == 0 ? s0 : k == 1 ? s1 : k == 2 ? s2 : s3) + (r & 63) * 512;
 }
 
-// acc = sum over chunks c = 0..s-1, in that order, of the partial tiles at
-// part + c * NTHREADS * 32 (float4 units, this thread's slot 0):
-// ((p0 + p1) + p2) + ...  Rounds of 16 loads (four slots of four chunks)
-// are in flight at once; one instance serves every s.
-__device__ __forceinline__ void sum_partials(v4f (&acc)[8][4], const float4* part, int s) {
-  for (int c0 = 0; c0 < s; c0 += 4) {
-#pragma unroll
-    for (int r = 0; r < 32; r += 4) {
-      float4 v[4][4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int cc = min(c0 + c, s - 1);  // in bounds; chunks past s are not added
-#pragma unroll
-        for (int k = 0; k < 4; ++k) v[c][k] = part[(int64_t)cc * NTHREADS * 32 + (r + k) * NTHREADS];
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        v4f& a = acc[(r + k) >> 2][(r + k) & 3];
-        v4f t = (v4f){v[0][k].x, v[0][k].y, v[0][k].z, v[0][k].w};
-        if (c0 > 0) t = a + t;
-#pragma unroll
-        for (int c = 1; c < 4; ++c)
-          if (c0 + c < s) t += (v4f){v[c][k].x, v[c][k].y, v[c][k].z, v[c][k].w};
-        a = t;
-      }
-    }
-  }
-}
-
 template <int GRID, bool B_UNIFORM, bool GROUPED, int EPI = EPI_STORE>
 __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t lds_a0[TILE_A];
@@ -309,14 +282,10 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     g.sb += (int64_t)e * g.sb_estride;
     if (g.nan_b) g.nan_b += (int64_t)e * g.N;
   } else {
-    if (g.split_s > 1 && pid >= g.split_base) {
-      const int q = pid - g.split_base;
-      split_tail = q / g.split_s;
-      split_chunk = q - split_tail * g.split_s;
-      pid = g.split_base + split_tail;
-    } else {
-      pid = xcd_local(pid, g.split_s > 1 ? g.split_base : (int)gridDim.x);
-    }
+    const SplitWork sw = split_work(pid, g.split_base, g.split_s);
+    split_tail = sw.tail;
+    split_chunk = sw.chunk;
+    pid = sw.tail >= 0 ? sw.pid : xcd_local(pid, g.split_s > 1 ? g.split_base : (int)gridDim.x);
     const int num_m = (int)((g.M + BM - 1) / BM);
     constexpr int GROUP_M = 4;
     const int group = pid / (GROUP_M * num_n);
@@ -489,31 +458,8 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   }
 
   if constexpr (!GROUPED && EPI != EPI_SWIGLU) {
-    if (split_tail >= 0) {
-      // publish this chunk's partial tile; the last chunk to arrive sums all
-      // of them in chunk order (the same order every call) and stores the tile
-      constexpr int PART4 = NTHREADS * 32;  // float4 per partial tile
-      float4* part = reinterpret_cast<float4*>(g.ws) + (int64_t)split_tail * g.split_s * PART4 + tid;
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          part[(int64_t)split_chunk * PART4 + (i * 4 + j) * NTHREADS] =
-              make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
-      // every wave's stores are complete in this XCD's L2 after the barrier;
-      // one agent-scope release then writes them back before the count
-      __syncthreads();
-      __shared__ int last;
-      if (tid == 0)
-        last = __hip_atomic_fetch_add(g.ws_count + split_tail, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT) ==
-               (uint32_t)(g.split_s - 1);
-      __syncthreads();
-      if (!last) return;
-      if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __syncthreads();
-      sum_partials(acc, part, g.split_s);
-      if (tid == 0) atomicExch(g.ws_count + split_tail, 0u);  // ready for the next call
-    }
+    // the last chunk to arrive sums all of them in chunk order and stores the tile
+    if (split_tail >= 0 && !split_exchange(acc, g.ws, g.ws_count, split_tail, g.split_s, split_chunk, tid)) return;
   }
 
   if constexpr (EPI == EPI_SWIGLU) {
@@ -779,58 +725,15 @@ static void launch_store(const GemmArgs& g, dim3 grd, dim3 blk, hipStream_t st) 
     gemm_blockscaled_kernel<GRID, B_UNIFORM, GROUPED, EPI_STORE><<<grd, blk, 0, st>>>(g);
 }
 
-// Split plan of the tail of a dense tiling: tiles past the last whole wave
-// (one workgroup per CU) are cut into split_s K chunks when that fills the
-// idle CUs; split_s = 1 means no split.
-struct SplitPlan {
-  int base, s, tail;
-};
-
-static int device_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cus[dev]) {
-    int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
-    cus[dev] = c;
-  }
-  return cus[dev];
-}
-
-static SplitPlan split_plan(int64_t tiles, int nk) {
-  SplitPlan p{(int)tiles, 1, 0};
-  const int64_t cus = device_cus();
-  const int64_t full = (tiles / cus) * cus, rem = tiles - full;
-  if (rem == 0 || rem * 2 > cus) return p;
-  int s = (int)std::min<int64_t>(cus / rem, 8);
-  // at least 9 K blocks per range: shorter ranges lose more to the partial
-  // tiles' round trip than they gain (K 1024: 25 us split, 16 unsplit)
-  s = std::min(s, nk / 9);
-  if (s < 2) return p;
-  p.base = (int)full;
-  p.s = s;
-  p.tail = (int)rem;
-  return p;
-}
-
-// Workspace layout: the tile counters, then the fp32 partials
-// [tail][s][NTHREADS * 128].  The counter area is the same for every plan on
-// a device (one uint32 per possible tail tile: a plan's tail is at most half
-// the compute units), so calls of different shapes on one workspace find
-// their counters where the previous call left them, at zero.
-static int64_t split_count_bytes(const SplitPlan&) { return ((int64_t)device_cus() / 2 * 4 + 255) / 256 * 256; }
-
-static int64_t split_ws_bytes(const SplitPlan& p) {
-  if (p.s < 2) return 0;
-  return split_count_bytes(p) + (int64_t)p.tail * p.s * NTHREADS * 128 * 4;
-}
+// the split-K tail's minimum K blocks per range (K 1024, 8 blocks: 25 us
+// split, 16 unsplit)
+constexpr int SPLIT_MIN_BLOCKS = 9;
 
 extern "C" int64_t ntlb_gemm_workspace_bytes(int64_t M, int64_t N, int64_t Kp) {
   if (M <= 0 || N <= 0 || Kp <= 0 || Kp % BK) return 0;
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7FFFFFFF) return 0;
-  return split_ws_bytes(split_plan(tiles, (int)(Kp / BK)));
+  return split_ws_bytes(split_plan(tiles, (int)(Kp / BK), SPLIT_MIN_BLOCKS));
 }
 
 extern "C" int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
@@ -870,11 +773,11 @@ extern "C" int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda,
   int64_t grid_wgs = tiles;
   if (workspace) {
     if (!aligned(workspace, 256)) return fail(NTLB_EINVAL, "%s: workspace must be 256-byte aligned", fn);
-    const SplitPlan plan = split_plan(tiles, (int)(Kp / BK));
+    const SplitPlan plan = split_plan(tiles, (int)(Kp / BK), SPLIT_MIN_BLOCKS);
     if (plan.s > 1 && ws_bytes >= split_ws_bytes(plan)) {
       g.split_base = plan.base; g.split_s = plan.s;
       g.ws_count = reinterpret_cast<uint32_t*>(workspace);
-      g.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + split_count_bytes(plan));
+      g.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + split_count_bytes());
       grid_wgs = (int64_t)plan.base + (int64_t)plan.tail * plan.s;
     }
   }

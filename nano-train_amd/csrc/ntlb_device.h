@@ -77,9 +77,11 @@ __device__ __forceinline__ Philox4 philox4x32_10(uint64_t group, uint64_t offset
     uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
     uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0;
     uint32_t hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
-    c0 = hi1 ^ c1 ^ k0;
+    // three-input xor in one v_bitop3_b32 (truth table 0x96), where two
+    // v_xor_b32 would otherwise follow every product
+    c0 = __builtin_amdgcn_bitop3_b32(hi1, c1, k0, 0x96);
     c1 = lo1;
-    c2 = hi0 ^ c3 ^ k1;
+    c2 = __builtin_amdgcn_bitop3_b32(hi0, c3, k1, 0x96);
     c3 = lo0;
     k0 += 0x9E3779B9u;
     k1 += 0xBB67AE85u;
@@ -138,6 +140,24 @@ __device__ __forceinline__ uint32_t e4m3_sr(float v, float u) {
   float t = __uint_as_float((ab & 0x7FFFFFu) | (130u << 23));  // a / ulp, in [8, 16)
   float n = __builtin_floorf(t + u);                             // 8 .. 16
   return sign | (((e8 - 120u) << 3) + (uint32_t)n - 8u);
+}
+
+// e4m3_sr for finite |v| <= 448 (the tile paths clamp first), without
+// branches: both the subnormal and the normal candidate are formed and one is
+// selected.  |v|*512 is exact, so fma(|v|, 512, u) rounds |v|*512 + u once as
+// the two-step form does; the candidates are non-negative, so the truncating
+// convert is the floor.  At |v| = 448, t + u can round up to the next binade
+// (480, no e4m3 code); the result clamps to 448 after rounding, as e4m3_sr
+// does.
+__device__ __forceinline__ uint32_t e4m3_sr_fin(float v, float u) {
+#pragma clang fp contract(off)
+  const uint32_t bits = __float_as_uint(v);
+  const uint32_t ns = (uint32_t)__builtin_fmaf(__builtin_fabsf(v), 512.0f, u);  // subnormal spacing 2^-9: 0 .. 8
+  const float t = __uint_as_float((bits & 0x7FFFFFu) | (130u << 23));         // |v| / ulp, in [8, 16)
+  const uint32_t nn = (uint32_t)(t + u);                                        // 8 .. 16
+  const uint32_t e8 = (bits >> 23) & 0xFFu;
+  const uint32_t cn = min(e8 * 8u + nn - 968u, 0x7Eu);                          // ((e8 - 120) << 3) + nn - 8
+  return ((bits >> 24) & 0x80u) | (e8 < 121u ? ns : cn);                        // |v| < 2^-6: subnormal
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {

@@ -66,11 +66,20 @@ __device__ __forceinline__ bool quant8(const float (&v)[8], float s, float qmaxf
 // holding a NaN takes the per-element reference path (and reports it); every
 // other tile clamps with min/max, divides with the fast exact sequence when
 // its amax allows, and rounds to e4m3 in hardware under round to nearest.
-// The fast division is taken for round-to-nearest tiles whose amax bits lie in
-// [0x1A000000, 0x7B800000] (no NaN, no inf).
+//
+// The fast sequence y = x*r, e = fma(-y, s, x), q = fma(e, r, y) with
+// r = RN(1/s) equals RN(x/s) for every pair of fp32 significands (all 2^46
+// pairs checked on the CPU by tests/cpu/division_check.c) as long as no
+// intermediate underflows or overflows.  Round to nearest takes it for amax bits in
+// [0x1A000000, 0x7B800000] (2^-75 .. 2^120): there every quotient that can
+// move a code (|x/s| >= 2^-11) has a normal residual.  Stochastic rounding
+// needs the quotient exactly wherever v + u can round differently, down to
+// |x/s| = 2^-34 (e4m3 subnormals: 512*v + u), so it takes the sequence for
+// amax bits in [0x30000000, 0x7B800000] (2^-31 .. 2^120), where those
+// residuals are normal; smaller quotients stay below 2^-34 either way.
 template <bool SR>
 __device__ __forceinline__ bool fast_div_ok(uint32_t m) {
-  return !SR && m >= 0x1A000000u && m <= 0x7B800000u;
+  return m >= (SR ? 0x30000000u : 0x1A000000u) && m <= 0x7B800000u;
 }
 
 // rs is 1/s (IEEE, correctly rounded) wherever fast_div_ok(m) holds; it is
@@ -85,13 +94,11 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
     return true;
   } else {
     float vq[8];
-    // Round-to-nearest tiles with amax in [2^-75, 2^120]: x/s as
-    // y = x*r, e = fma(-y, s, x), q = fma(e, r, y) with r = 1/s and the sign
-    // of x; this equals the correctly rounded quotient wherever it can move
-    // a code (checked exhaustively on random operands).  Other tiles, and
-    // stochastic rounding, divide.
-    // no NaN reaches the clamp here (NaN tiles took the path above; x/s
-    // is finite or +-inf), so the single-instruction median is the clamp
+    // x/s by the fast sequence (with the sign of x, so that -0 and signed
+    // tiny quotients keep their sign) where fast_div_ok holds, else by IEEE
+    // division.  No NaN reaches the clamp here (NaN tiles took the path
+    // above; x/s is finite or +-inf), so the single-instruction median is
+    // the clamp
     if (fast_div_ok<SR>(m)) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -113,10 +120,15 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
       for (int i = 0; i < 8; ++i) {
         float t;
         if constexpr (SR) {
-          // the reference clamps after rounding (te_backend.py:102-106): at
-          // the clamp, qmax + u rounds to qmax + 1 in fp32 when u >= 1 - 2^-18
+          // floor(v + u) for v >= 0 and ceil(v - u) = -floor(|v| + u) below
+          // (round to nearest is symmetric), so one floor, negated for
+          // v < 0 (te_backend.py:61-65); v = -0 counts as v >= 0 there and
+          // gives +0, so the sign comes from the comparison, not from v.
+          // The reference clamps after rounding (:102-106): at the clamp,
+          // qmax + u rounds to qmax + 1 in fp32 when u >= 1 - 2^-18
           const float uu = sr_uniform(rb[i]);
-          t = (vq[i] >= 0.0f) ? __builtin_floorf(vq[i] + uu) : __builtin_ceilf(vq[i] - uu);
+          const float w = __builtin_floorf(__builtin_fabsf(vq[i]) + uu);
+          t = vq[i] >= 0.0f ? w : -w;
           t = __builtin_amdgcn_fmed3f(t, -qmaxf, qmaxf);
         } else {
           t = __builtin_rintf(vq[i]);
@@ -137,7 +149,7 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
         c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) c[i] = SR ? e4m3_sr(vq[i], sr_uniform(rb[i])) : e4m3_rne(vq[i]);
+        for (int i = 0; i < 8; ++i) c[i] = e4m3_sr_fin(vq[i], sr_uniform(rb[i]));
         lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
         hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
       }

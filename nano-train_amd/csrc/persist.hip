@@ -21,6 +21,7 @@
 
 #include "ntlb_device.h"
 #include "ntlb_host.h"
+#include "ntlb_splitk.h"
 
 #pragma clang fp contract(off)
 
@@ -510,6 +511,13 @@ struct FusedArgs {
   int y_dtype;
   int64_t ldy;
   int vec_out;
+  const void* bias;  // optional [N], added in fp32 before the output rounding
+  int bias_dtype;
+  // split-K tail (ntlb_splitk.h): workgroups at or past split_base take K
+  // range (q % split_s) of tile split_base + q / split_s
+  int split_base, split_s;
+  float* ws;
+  uint32_t* ws_count;
 };
 
 // Scales of one weight row: the scale of the 32 weights [k0, k0+32) is
@@ -672,9 +680,12 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   const int wm = wave >> 2, wn = wave & 3;
   const int num_n = (int)((g.N + FBN - 1) / FBN);
   const int num_m = (int)((g.M + FBM - 1) / FBM);
-  const int nwg = num_m * num_n;
-  int pid = blockIdx.x;
-  {
+  // the whole-wave tiles are renumbered so each XCD walks a contiguous range;
+  // the split tail's ranges keep their tile
+  const SplitWork sw = split_work(blockIdx.x, g.split_base, g.split_s);
+  int pid = sw.pid;
+  if (sw.tail < 0) {
+    const int nwg = g.split_s > 1 ? g.split_base : num_m * num_n;
     const int xcd = pid & 7, local = pid >> 3;
     const int per = nwg >> 3, extra = nwg & 7;
     pid = xcd * per + min(xcd, extra) + local;
@@ -709,13 +720,19 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   const RowScales wsc = fused_row_scales<FMT>(g, bn);
 
   const int nk = (int)(g.K / FBK);
+  // K blocks [kb0, kb1) of this workgroup: all of them, or one split range
+  const int kb0 = sw.tail >= 0 ? (int)((int64_t)sw.chunk * nk / g.split_s) : 0;
+  const int kb1 = sw.tail >= 0 ? (int)((int64_t)(sw.chunk + 1) * nk / g.split_s) : nk;
   // the epilogue's arguments, kept in scalar registers through the K loop
-  uintptr_t e_y = reinterpret_cast<uintptr_t>(g.y);
+  uintptr_t e_y = reinterpret_cast<uintptr_t>(g.y), e_bias = reinterpret_cast<uintptr_t>(g.bias);
   int64_t e_ldy = g.ldy, e_M = g.M, e_N = g.N;
-  int e_f32 = g.y_dtype == DT_F32, e_vec = g.vec_out;
+  int e_f32 = g.y_dtype == DT_F32, e_vec = g.vec_out, e_bdt = g.bias_dtype;
   e_y = uniform64(e_y); e_ldy = uniform64(e_ldy); e_M = uniform64(e_M); e_N = uniform64(e_N);
+  e_bias = uniform64(e_bias);
   e_f32 = __builtin_amdgcn_readfirstlane(e_f32); e_vec = __builtin_amdgcn_readfirstlane(e_vec);
+  e_bdt = __builtin_amdgcn_readfirstlane(e_bdt);
   asm volatile("" : "+s"(e_y), "+s"(e_ldy), "+s"(e_M), "+s"(e_N), "+s"(e_f32), "+s"(e_vec));
+  asm volatile("" : "+s"(e_bias), "+s"(e_bdt));
   v4f acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -723,7 +740,7 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
-  for (int j = 0; j < 4; ++j) issue_x(fx0, 0, j);
+  for (int j = 0; j < 4; ++j) issue_x(fx0, kb0, j);
   // packed weight bytes and scale of block kt+1 travel in registers during
   // step kt-1 and step kt: they are loaded at the middle of step kt-1, after
   // that step's X copies, and may stay in flight across its closing barrier.
@@ -743,12 +760,12 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   {
     Raw32 raw0;
     float s0;
-    w_load(0, raw0, s0);
+    w_load(kb0, raw0, s0);
     const StepDecode<FMT> d0 = decode_begin<FMT>(s0);
 #pragma unroll
     for (int j = 0; j < 4; ++j) decode_chunk<FMT>(d0, raw0, j, fw0, br, bh);
   }
-  w_load(min(1, nk - 1), raw_pf1, sc_pf1);
+  w_load(min(kb0 + 1, kb1 - 1), raw_pf1, sc_pf1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -760,7 +777,7 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     uint8_t* wb_next = BUF ? fw0 : fw1;
     // unconditional copies of block kn (the last step reloads itself into
     // the idle stage) keep the step one basic block
-    const int kn = min(kt + 1, nk - 1);
+    const int kn = min(kt + 1, kb1 - 1);
 
     StepDecode<FMT> dec;
     v8i bf[4];
@@ -786,7 +803,7 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
       if (tm & 1) decode_chunk<FMT>(dec, r, tm >> 1, wb_next, br, bh);
       // block kn+1's loads go out after this step's X copies, as the last
       // vector-memory operations of the step
-      if (tm == 4) w_load(min(kt + 2, nk - 1), BUF ? raw_pf1 : raw_pf0, BUF ? sc_pf1 : sc_pf0);
+      if (tm == 4) w_load(min(kt + 2, kb1 - 1), BUF ? raw_pf1 : raw_pf0, BUF ? sc_pf1 : sc_pf0);
 #pragma unroll
       for (int tn = 0; tn < 4; ++tn) acc[tm][tn] = mma_bf16_64(bf[tn], af, acc[tm][tn]);
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
@@ -799,10 +816,13 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
     __syncthreads();
   };
 
-  for (int kt = 0; kt < nk; kt += 2) {
+  for (int kt = kb0; kt < kb1; kt += 2) {
     step(std::integral_constant<int, 0>(), kt);
-    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+    if (kt + 1 < kb1) step(std::integral_constant<int, 1>(), kt + 1);
   }
+  // a split range publishes its partial; the last to arrive sums them in
+  // range order and stores the tile
+  if (sw.tail >= 0 && !split_exchange(acc, g.ws, g.ws_count, sw.tail, g.split_s, sw.chunk, tid)) return;
 
   // the tile origin and lane pass through an empty asm so that no epilogue
   // address arithmetic is hoisted above the K loop, where every register is
@@ -817,6 +837,19 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
   // the K loop (re-loading them after it costs scalar-cache misses).
   const int slab = wave >> 1;
   uint8_t* stage_w = (slab == 0 ? fx0 : slab == 1 ? fw0 : slab == 2 ? fx1 : fw1) + (wave & 1) * (FT / 2);
+  // bias of this lane's 16 output columns (4 per 16-column block), in fp32
+  if (e_bias) {
+#pragma unroll
+    for (int tn = 0; tn < 4; ++tn) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = min<int64_t>(n0e + wn * 64 + tn * 16 + (lane_e >> 4) * 4 + i, e_N - 1);
+        const float b = load_elem(reinterpret_cast<const void*>(e_bias), e_bdt, n);
+#pragma unroll
+        for (int tm = 0; tm < 8; ++tm) acc[tm][tn][i] = acc[tm][tn][i] + b;
+      }
+    }
+  }
   auto store_tile = [&](auto f32c, auto fullc) {
     constexpr bool OUT_F32 = decltype(f32c)::value;
     constexpr bool FULL = decltype(fullc)::value;
@@ -962,9 +995,12 @@ extern "C" int ntlb_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, 
   return check_launch(fn);
 }
 
+// the split-K tail's minimum K blocks (64 bf16 each) per range
+constexpr int FUSED_SPLIT_MIN_BLOCKS = 9;
+
 static int fused_launch(int fmt, const char* fn, const void* x, int64_t ldx, const uint8_t* w, const void* scales,
-                        int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
-                        void* stream) {
+                        int64_t block, const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K, void* y,
+                        int y_dtype, int64_t ldy, void* workspace, int64_t ws_bytes, void* stream) {
   if (M < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
   if (M == 0 || N == 0) return NTLB_OK;
   if (!x || !w || !scales || !y) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
@@ -976,12 +1012,27 @@ static int fused_launch(int fmt, const char* fn, const void* x, int64_t ldx, con
   if (fmt != FMT_MXFP4 && block != 0 && (K % block || block % 32))
     return fail(NTLB_EUNSUPPORTED, "%s: the scale block must divide K and be a multiple of 32 (or 0 = tensor)", fn);
   if ((M + FBM) * ldx * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: X exceeds 2 GiB", fn);
+  if (bias && !valid_dtype(bias_dtype)) return fail(NTLB_EINVAL, "%s: bad bias dtype", fn);
   const int64_t tiles = ((M + FBM - 1) / FBM) * ((N + FBN - 1) / FBN);
+  if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
   FusedArgs g;
   g.x = reinterpret_cast<const uint16_t*>(x); g.ldx = ldx; g.w = w; g.scales = scales; g.block = block;
   g.M = M; g.N = N; g.K = K; g.y = y; g.y_dtype = y_dtype; g.ldy = ldy;
   g.vec_out = aligned(y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
-  dim3 grd((unsigned)tiles), blk(512);
+  g.bias = bias; g.bias_dtype = bias_dtype;
+  g.split_base = (int)tiles; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
+  int64_t grid_wgs = tiles;
+  if (workspace) {
+    if (!aligned(workspace, 256)) return fail(NTLB_EINVAL, "%s: workspace must be 256-byte aligned", fn);
+    const SplitPlan plan = split_plan(tiles, (int)(K / FBK), FUSED_SPLIT_MIN_BLOCKS);
+    if (plan.s > 1 && ws_bytes >= split_ws_bytes(plan)) {
+      g.split_base = plan.base; g.split_s = plan.s;
+      g.ws_count = reinterpret_cast<uint32_t*>(workspace);
+      g.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + split_count_bytes());
+      grid_wgs = (int64_t)plan.base + (int64_t)plan.tail * plan.s;
+    }
+  }
+  dim3 grd((unsigned)grid_wgs), blk(512);
   if (fmt == FMT_NF4)
     gemm_lowbit_fused_kernel<FMT_NF4><<<grd, blk, 0, as_stream(stream)>>>(g);
   else if (fmt == FMT_MXFP4)
@@ -994,22 +1045,44 @@ static int fused_launch(int fmt, const char* fn, const void* x, int64_t ldx, con
 extern "C" int ntlb_gemm_nf4(const void* x, int64_t ldx, const uint8_t* w_packed, const float* w_scales,
                              int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
                              void* stream) {
-  return fused_launch(FMT_NF4, "ntlb_gemm_nf4", x, ldx, w_packed, w_scales, block, M, N, K, y, y_dtype, ldy,
-                      stream);
+  return fused_launch(FMT_NF4, "ntlb_gemm_nf4", x, ldx, w_packed, w_scales, block, nullptr, 0, M, N, K, y, y_dtype,
+                      ldy, nullptr, 0, stream);
 }
 
 extern "C" int ntlb_gemm_fp8p(const void* x, int64_t ldx, const uint8_t* w_codes, const float* w_scales,
                               int64_t block, int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy,
                               void* stream) {
-  return fused_launch(FMT_FP8P, "ntlb_gemm_fp8p", x, ldx, w_codes, w_scales, block, M, N, K, y, y_dtype, ldy,
-                      stream);
+  return fused_launch(FMT_FP8P, "ntlb_gemm_fp8p", x, ldx, w_codes, w_scales, block, nullptr, 0, M, N, K, y,
+                      y_dtype, ldy, nullptr, 0, stream);
 }
 
 extern "C" int ntlb_gemm_mxfp4(const void* x, int64_t ldx, const uint8_t* w_packed, const uint8_t* w_scales,
                                int64_t M, int64_t N, int64_t K, void* y, int y_dtype, int64_t ldy, void* stream) {
   if (K % 32) return fail(NTLB_EUNSUPPORTED, "ntlb_gemm_mxfp4: K must be a multiple of 32");
-  return fused_launch(FMT_MXFP4, "ntlb_gemm_mxfp4", x, ldx, w_packed, w_scales, 32, M, N, K, y, y_dtype, ldy,
-                      stream);
+  return fused_launch(FMT_MXFP4, "ntlb_gemm_mxfp4", x, ldx, w_packed, w_scales, 32, nullptr, 0, M, N, K, y,
+                      y_dtype, ldy, nullptr, 0, stream);
+}
+
+extern "C" int64_t ntlb_gemm_lowbit_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % FBK) return 0;
+  const int64_t tiles = ((M + FBM - 1) / FBM) * ((N + FBN - 1) / FBN);
+  if (tiles > 0x7FFFFFFF) return 0;
+  return split_ws_bytes(split_plan(tiles, (int)(K / FBK), FUSED_SPLIT_MIN_BLOCKS));
+}
+
+extern "C" int ntlb_gemm_lowbit_ws(int fmt, const void* x, int64_t ldx, const uint8_t* w, const void* w_scales,
+                                   int64_t block, const void* bias, int bias_dtype, int64_t M, int64_t N, int64_t K,
+                                   void* y, int y_dtype, int64_t ldy, void* workspace, int64_t ws_bytes,
+                                   void* stream) {
+  const char* fn = "ntlb_gemm_lowbit_ws";
+  if (fmt == NTLB_LOWBIT_MXFP4) {
+    if (K % 32) return fail(NTLB_EUNSUPPORTED, "%s: MXFP4 needs K %% 32 == 0", fn);
+    return fused_launch(FMT_MXFP4, fn, x, ldx, w, w_scales, 32, bias, bias_dtype, M, N, K, y, y_dtype, ldy,
+                        workspace, ws_bytes, stream);
+  }
+  if (fmt != NTLB_LOWBIT_NF4 && fmt != NTLB_LOWBIT_FP8P) return fail(NTLB_EINVAL, "%s: bad format %d", fn, fmt);
+  return fused_launch(fmt == NTLB_LOWBIT_NF4 ? FMT_NF4 : FMT_FP8P, fn, x, ldx, w, w_scales, block, bias, bias_dtype,
+                      M, N, K, y, y_dtype, ldy, workspace, ws_bytes, stream);
 }
 
 extern "C" int ntlb_fp8_persistent_quant(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws,

@@ -831,12 +831,20 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // of a wave, LDS across the four waves.  Each of the thread's columns then
 // quantizes its 8 consecutive rows as one quant8_tile group (fast division and
 // the hardware e4m3 convert where they apply), whose 8 codes are 8
-// consecutive bytes of the transposed row.  They are staged in LDS (8-byte
-// slot rg ^ 2*(cc & 7) of a 144-byte row: 2-cycle writes, near-minimal
-// 16-byte reads) and leave as full 128-byte transposed rows, 16 bytes per
-// lane; direct 8-byte stores would scatter 32-byte pieces over 16 rows per
-// instruction.  Workgroups walk column blocks fastest.  nan_rows, when given, is indexed by transposed row
-// (source column).
+// consecutive bytes of the transposed row.  They are staged in LDS and leave
+// as full 128-byte transposed rows, 16 bytes per lane; direct 8-byte stores
+// would scatter 32-byte pieces over 16 rows per instruction.  Staging layout
+// (128-byte rows, no padding; 64 banks of 4 bytes): transposed row cl sits at
+// row cl ^ ((cl >> 3) & 1) and its 8-byte slot for row group rg at
+// rg ^ 2*((cl >> 4) & 7).  A half-wave's writes (16 columns cl = 8*cc + j of
+// one parity j, 2 row groups) then cover both 128-byte halves of a 256-byte
+// bank window, 16 distinct slots in each: conflict-free.  Each 16-lane phase
+// of the 16-byte reads takes 8 pieces of two adjacent rows, one from each
+// half: conflict-free too.  The per-column arrays (maxima, scales,
+// reciprocals) skip one word after column 63, so that the 16 columns cc*8 + j
+// a wave reads at once fall on 16 banks.  Workgroups walk column blocks
+// fastest.  nan_rows, when given, is indexed by transposed row (source
+// column).
 //
 // With DUAL the same pass also writes the 1x128 tiles of x, described by ar
 // (codes, ldc, scales, s_row, s_col, nan_rows and the SR offset): row i of a
@@ -845,16 +853,21 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // amax.  One read of dY feeds both the dgrad and the wgrad operands.
 template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false>
 __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, QuantArgs ar = QuantArgs()) {
-  constexpr int TP = 144;  // staged transposed row pitch (bytes)
-  __shared__ uint32_t wmax[4][128];
+  // staged transposed row of column cl, its 8-byte slot for row group rg and
+  // its 16-byte piece k; per-column array index of column c
+  auto trow = [](int cl) { return cl ^ ((cl >> 3) & 1); };
+  auto tslot = [](int cl, int rg) { return rg ^ (2 * ((cl >> 4) & 7)); };
+  auto tpiece = [](int cl, int k) { return k ^ ((cl >> 4) & 7); };
+  auto pc = [](int c) { return c + (c >> 6); };
+  __shared__ uint32_t wmax[4][130];
   __shared__ uint32_t rmax[128];
   // per column (and, with DUAL, per row tile): amax bits, scale, 1/scale,
   // computed once per workgroup by one thread each
-  __shared__ __attribute__((aligned(16))) uint32_t cm[128];
-  __shared__ __attribute__((aligned(16))) float cs[128], crs[128];
+  __shared__ __attribute__((aligned(16))) uint32_t cm[130];
+  __shared__ __attribute__((aligned(16))) float cs[130], crs[130];
   __shared__ __attribute__((aligned(16))) uint32_t rm[128];
   __shared__ __attribute__((aligned(16))) float rs_[128], rrs[128];
-  __shared__ __attribute__((aligned(16))) uint8_t tcodes[128 * TP];
+  __shared__ __attribute__((aligned(16))) uint8_t tcodes[128 * 128];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cc = tid & 15, rg = tid >> 4;
   const int64_t n_cb = (a.K + 127) / 128;
@@ -882,7 +895,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
       }
       mm = max(mm, (uint32_t)__shfl_xor((int)mm, 16));
       mm = max(mm, (uint32_t)__shfl_xor((int)mm, 32));
-      if (lane < 16) wmax[wave][cc * 8 + j] = mm;
+      if (lane < 16) wmax[wave][pc(cc * 8 + j)] = mm;
     }
   } else {
     uint32_t m2[4] = {0, 0, 0, 0};
@@ -898,8 +911,8 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
       m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 16));
       m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 32));
       if (lane < 16) {
-        wmax[wave][cc * 8 + 2 * k] = m2[k] << 16;
-        wmax[wave][cc * 8 + 2 * k + 1] = m2[k] & 0xFFFF0000u;
+        wmax[wave][pc(cc * 8 + 2 * k)] = m2[k] << 16;
+        wmax[wave][pc(cc * 8 + 2 * k + 1)] = m2[k] & 0xFFFF0000u;
       }
     }
   }
@@ -914,11 +927,12 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
   }
   __syncthreads();
   if (tid < 128) {
-    const uint32_t mm = max(max(wmax[0][tid], wmax[1][tid]), max(wmax[2][tid], wmax[3][tid]));
+    const int c = pc(tid);
+    const uint32_t mm = max(max(wmax[0][c], wmax[1][c]), max(wmax[2][c], wmax[3][c]));
     const float sc = scale_from_amax_bits(mm, a.qmaxf, a.scale_rule);
-    cm[tid] = mm;
-    cs[tid] = sc;
-    crs[tid] = fast_div_ok<SR>(mm) ? 1.0f / sc : 1.0f;
+    cm[c] = mm;
+    cs[c] = sc;
+    crs[c] = fast_div_ok<SR>(mm) ? 1.0f / sc : 1.0f;
   } else if (DUAL) {
     const int r = tid - 128;
     const uint32_t mm = rmax[r];
@@ -980,8 +994,8 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
     const int j = 4 * h + jj;
     const int cl = cc * 8 + j;
     const int64_t col = col0 + j;
-    const uint32_t mj = cm[cl];
-    const float s = cs[cl];
+    const uint32_t mj = cm[pc(cl)];
+    const float s = cs[pc(cl)];
     float v[8];
     uint32_t rbj[8];
 #pragma unroll
@@ -998,8 +1012,8 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
     }
     uint32_t lo, hi;
     float q[8];
-    const bool nan = quant8_tile_rs<GRID, SR, DQ>(v, mj, s, crs[cl], a.qmaxf, rbj, lo, hi, q);
-    *reinterpret_cast<uint2*>(tcodes + cl * TP + ((rg ^ (2 * (cc & 7))) * 8)) = make_uint2(lo, hi);
+    const bool nan = quant8_tile_rs<GRID, SR, DQ>(v, mj, s, crs[pc(cl)], a.qmaxf, rbj, lo, hi, q);
+    *reinterpret_cast<uint2*>(tcodes + trow(cl) * 128 + tslot(cl, rg) * 8) = make_uint2(lo, hi);
     if (col_in) {
       if (rg == 0) {
         a.scales[col * a.s_row + mb * a.s_col] = s;
@@ -1021,7 +1035,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
     const int cl = qi >> 3, k = qi & 7;
     const int64_t col = cb * 128 + cl;
     if (col < a.K) {
-      const uint4 v = *reinterpret_cast<const uint4*>(tcodes + cl * TP + (((2 * k) ^ (2 * ((cl >> 3) & 7))) * 8));
+      const uint4 v = *reinterpret_cast<const uint4*>(tcodes + trow(cl) * 128 + tpiece(cl, k) * 16);
       // the single-output pass stores its transposed rows with the
       // non-temporal hint (c3 dY: 100 -> 88 us); the dual pass, which also
       // writes the 1x128 codes, measured slower with it (128 -> 136 us)

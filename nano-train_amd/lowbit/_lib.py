@@ -72,6 +72,8 @@ SIGNATURES = {
     "ntlb_gemm_nf4": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_mxfp4": [_P, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_fp8p": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_lowbit_workspace_bytes": [_I64, _I64, _I64],
+    "ntlb_gemm_lowbit_ws": [_I32, _P, _I64, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _I64, _P],
     "ntlb_gemm_workspace_bytes": [_I64, _I64, _I64],
     "ntlb_gemm_dq_forward": [_I32, _I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64,
                              _I64, _P, _I32, _P, _I32, _I64, _P],
@@ -99,7 +101,8 @@ SIGNATURES = {
 }
 
 # entry points that return a value instead of a status
-RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64, "ntlb_colsum_workspace_bytes": _I64}
+RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64, "ntlb_colsum_workspace_bytes": _I64,
+            "ntlb_gemm_lowbit_workspace_bytes": _I64}
 
 _lib = None
 _lock = threading.Lock()

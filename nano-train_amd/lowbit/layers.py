@@ -26,6 +26,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import ops
 from . import persistent as P
 from .contracts import LowBitKernelSpec
 from .precision import dtype_alias_to_torch
@@ -34,37 +35,43 @@ _PERSISTENT_SUFFIXES = ("_persistent_fp8_weight", "_persistent_fp4_codes", "_per
 
 
 class _FusedPersistentLinear(torch.autograd.Function):
-    """Forward: dequant-fused GEMM over the persistent NF4 or FP8 weight.
-    Backward: straight-through to the master weight (layers.py:409-436)."""
+    """Forward: dequant-fused GEMM over the persistent NF4 or FP8 weight, with
+    the bias added in fp32 before the output rounding (F.linear(x, w_q, b),
+    layers.py:595-632).  Backward: straight-through to the master weight
+    (layers.py:409-436) on the library's bf16 GEMMs: dX = dY . w_q with w_q
+    dequantized by its kernel, dW = dY^T . X, db = the column sum of dY."""
 
     @staticmethod
-    def forward(ctx, x, weight, codes, scale, block, fmt):
+    def forward(ctx, x, weight, bias, codes, scale, block, fmt):
         N, K = weight.shape
         if fmt == "nf4":
-            y = P.linear_nf4(x, codes, scale, out_features=N, block=block)
+            y = P.linear_nf4(x, codes, scale, out_features=N, block=block, bias=bias)
         else:
-            y = P.linear_fp8p(x, codes, scale)
+            y = P.linear_fp8p(x, codes, scale, bias=bias)
         ctx.save_for_backward(x, codes, scale)
-        ctx.meta = (N, K, block, weight.dtype, fmt)
+        ctx.meta = (N, K, block, weight.dtype, fmt, None if bias is None else bias.dtype)
         return y
 
     @staticmethod
     def backward(ctx, dy):
         x, codes, scale = ctx.saved_tensors
-        N, K, block, wdt, fmt = ctx.meta
-        dx = dw = None
+        N, K, block, wdt, fmt, bdt = ctx.meta
+        dx = dw = db = None
         dy2 = dy.reshape(-1, N)
-        with torch.autocast(device_type="cuda", enabled=False):
-            if ctx.needs_input_grad[0]:
-                if fmt == "nf4":
-                    w_deq = P.dequantize_nf4_blocks(codes, scale, num_values=N * K, block=block,
-                                                    target_dtype=wdt).reshape(N, K)
-                else:
-                    w_deq = P.dequantize_fp8_persistent(codes, scale, target_dtype=wdt).reshape(N, K)
-                dx = torch.matmul(dy2, w_deq.to(dy2.dtype)).reshape(x.shape)
-            if ctx.needs_input_grad[1]:
-                dw = torch.matmul(dy2.t(), x.reshape(-1, K).to(dy2.dtype)).to(wdt)
-        return dx, dw, None, None, None, None
+        if dy2.stride(-1) != 1:
+            dy2 = dy2.contiguous()
+        if ctx.needs_input_grad[0]:
+            if fmt == "nf4":
+                w_deq = P.dequantize_nf4_blocks(codes, scale, num_values=N * K, block=block,
+                                                target_dtype=dy2.dtype).reshape(N, K)
+            else:
+                w_deq = P.dequantize_fp8_persistent(codes, scale, target_dtype=dy2.dtype).reshape(N, K)
+            dx = ops.gemm_dense(dy2, w_deq, b_transposed=True, out_dtype=x.dtype).reshape(x.shape)
+        if ctx.needs_input_grad[1]:
+            dw = ops.gemm_dense_tn(dy2, x.reshape(-1, K).to(dy2.dtype), out_dtype=wdt)
+        if ctx.needs_input_grad[2]:
+            db = ops.colsum(dy2, out_dtype=bdt)
+        return dx, dw, db, None, None, None, None
 
 
 class LowBitLinearMixin:
@@ -201,14 +208,14 @@ class LowBitLinearMixin:
             raise ValueError(f"Unsupported persistent low-bit mode: {mode}")
         return self.weight + (deq - self.weight).detach()
 
-    def _fused_persistent_forward(self, x: torch.Tensor) -> Optional[torch.Tensor]:
+    def _fused_persistent_forward(self, x: torch.Tensor, bias: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
         """NF4 or FP8 persistent weight, no low-bit backend, bf16 everywhere:
         dequant inside the GEMM instead of materializing the bf16 weight."""
         mode = self._persistent_mode()
         if (mode not in ("fp4", "fp8") or self._compute_lowbit_mode() is not None
                 or self._compute_dtype_override() is not None or x.dtype != torch.bfloat16
                 or self.weight.dtype != torch.bfloat16 or x.device.type != "cuda" or self.weight.dim() != 2
-                or self.weight.shape[1] % 64):
+                or self.weight.shape[1] % 64 or (bias is not None and bias.dtype != torch.bfloat16)):
             return None
         N, K = self.weight.shape
         if mode == "fp4":
@@ -216,12 +223,12 @@ class LowBitLinearMixin:
                 self.refresh_persistent_lowbit_params()
             scale = self._persistent_scale
             block = (N * K) if scale.numel() <= 1 else K
-            return _FusedPersistentLinear.apply(x, self.weight, self._persistent_fp4_codes, scale.float(), block,
+            return _FusedPersistentLinear.apply(x, self.weight, bias, self._persistent_fp4_codes, scale.float(), block,
                                                 "nf4")
         if self._persistent_fp8_weight.numel() != self.weight.numel():
             self.refresh_persistent_lowbit_params()
         scale = self._persistent_scale
-        return _FusedPersistentLinear.apply(x, self.weight, self._persistent_fp8_weight, scale.float(),
+        return _FusedPersistentLinear.apply(x, self.weight, bias, self._persistent_fp8_weight, scale.float(),
                                             0 if scale.numel() <= 1 else K, "fp8")
 
     def _dispatch_lowbit_linear(self, *, x: torch.Tensor, weight: torch.Tensor,
@@ -243,10 +250,9 @@ class LowBitLinearMixin:
         return F.linear(x.to(dt), weight.to(dt), None if bias is None else bias.to(dt))
 
     def _lowbit_forward(self, x: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
-        if bias is None:
-            fused = self._fused_persistent_forward(x)
-            if fused is not None:
-                return fused
+        fused = self._fused_persistent_forward(x, bias)
+        if fused is not None:
+            return fused
         weight = self._persistent_weight_ste()
         out = self._dispatch_lowbit_linear(x=x, weight=weight, bias=bias)
         if out is not None:

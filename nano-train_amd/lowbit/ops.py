@@ -361,10 +361,17 @@ _workspaces: dict = {}
 
 def gemm_workspace(M: int, N: int, Kp: int, device: torch.device) -> Optional[torch.Tensor]:
     """The zeroed split-K workspace of the current stream on `device`, grown to
-    what an (M, N, Kp) product needs; None when that shape runs unsplit.  The
-    kernels leave it zeroed, and calls on one stream never overlap, so one
-    buffer per stream serves every GEMM issued there."""
-    need = int(_lib.lib().ntlb_gemm_workspace_bytes(M, N, Kp))
+    what an (M, N, Kp) blockwise-scaled product needs; None when that shape
+    runs unsplit."""
+    return split_workspace(int(_lib.lib().ntlb_gemm_workspace_bytes(M, N, Kp)), device)
+
+
+def split_workspace(need: int, device: torch.device) -> Optional[torch.Tensor]:
+    """The zeroed split-K workspace of the current stream on `device`, grown
+    to `need` bytes; None when need is 0.  Every split-K GEMM (the
+    blockwise-scaled and the dequant-fused ones) leaves it zeroed with its
+    tile counters at one fixed place, and calls on one stream never overlap,
+    so one buffer per stream serves every GEMM issued there."""
     if need <= 0:
         return None
     key = (device.index, _stream())

@@ -23,7 +23,7 @@ from typing import Optional
 
 import torch
 
-from . import ops
+from . import _lib, ops
 from ._lib import call
 
 NF4_CODEBOOK = (
@@ -151,26 +151,44 @@ def _x2(x: torch.Tensor, K: int) -> torch.Tensor:
     return x2
 
 
+_LOWBIT_NF4, _LOWBIT_MXFP4, _LOWBIT_FP8P = 0, 1, 2
+
+
+def _fused(fmt: int, x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, block: int, bias, M: int, N: int,
+           K: int, out_dtype) -> torch.Tensor:
+    """ntlb_gemm_lowbit_ws with the current stream's split-K workspace."""
+    if bias is not None:
+        ops._require_device(bias)
+        if bias.numel() != N:
+            raise ValueError(f"bias must have {N} entries, got {bias.numel()}")
+        bias = bias.reshape(-1).contiguous()
+    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x2.device)
+    ws = ops.split_workspace(int(_lib.lib().ntlb_gemm_lowbit_workspace_bytes(M, N, K)), x2.device)
+    call("ntlb_gemm_lowbit_ws", fmt, x2.data_ptr(), x2.stride(0), w.data_ptr(), scales.data_ptr(), block,
+         ops._ptr(bias), ops._dtype_code(bias.dtype) if bias is not None else 0, M, N, K, y.data_ptr(),
+         ops._dtype_code(y.dtype), y.stride(0), ops._ptr(ws), ws.numel() if ws is not None else 0, ops._stream())
+    return y
+
+
 def linear_nf4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, out_features: int, block: int,
-               out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """Y = x @ deq(W)^T with W [out_features, K] in NF4, dequantized inside the GEMM.
+               bias: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Y = x @ deq(W)^T (+ bias) with W [out_features, K] in NF4, dequantized inside the GEMM.
 
     block: elements per scale (K for per_channel, 0 or numel for per_tensor, 64...)."""
     K = x.shape[-1]
     x2 = _x2(x, K)
     M, N = x2.shape[0], out_features
-    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x.device)
     blk = 0 if block >= N * K else block
-    call("ntlb_gemm_nf4", x2.data_ptr(), x2.stride(0), packed.data_ptr(), scales.reshape(-1).contiguous().data_ptr(),
-         blk, M, N, K, y.data_ptr(), ops._dtype_code(y.dtype), y.stride(0), ops._stream())
+    y = _fused(_LOWBIT_NF4, x2, packed, scales.reshape(-1).contiguous(), blk, bias, M, N, K, out_dtype)
     return y.reshape(*x.shape[:-1], N)
 
 
 def linear_fp8p(x: torch.Tensor, fp8_values: torch.Tensor, scale: torch.Tensor, *,
-                out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """Y = x @ deq(W)^T with W the persistent FP8 weight [N, K] (float8_e4m3fn
-    values and a per_channel [N, 1] or per_tensor scale), dequantized inside
-    the GEMM as _dequantize_fp8_persistent does (layers.py:120-127)."""
+                bias: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Y = x @ deq(W)^T (+ bias) with W the persistent FP8 weight [N, K]
+    (float8_e4m3fn values and a per_channel [N, 1] or per_tensor scale),
+    dequantized inside the GEMM as _dequantize_fp8_persistent does
+    (layers.py:120-127)."""
     ops._require_device(fp8_values, scale)
     N, K = fp8_values.shape
     x2 = _x2(x, K)
@@ -180,19 +198,15 @@ def linear_fp8p(x: torch.Tensor, fp8_values: torch.Tensor, scale: torch.Tensor, 
     block = 0 if sc.numel() <= 1 else K
     if block and sc.numel() != N:
         raise ValueError(f"scale must be per_tensor or one per row, got {tuple(scale.shape)}")
-    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x.device)
-    call("ntlb_gemm_fp8p", x2.data_ptr(), x2.stride(0), codes.data_ptr(), sc.data_ptr(), block, M, N, K,
-         y.data_ptr(), ops._dtype_code(y.dtype), y.stride(0), ops._stream())
+    y = _fused(_LOWBIT_FP8P, x2, codes, sc, block, bias, M, N, K, out_dtype)
     return y.reshape(*x.shape[:-1], N)
 
 
 def linear_mxfp4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, out_features: int,
-                 out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
-    """Y = x @ deq(W)^T with W [out_features, K] in MXFP4, dequantized inside the GEMM."""
+                 bias: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Y = x @ deq(W)^T (+ bias) with W [out_features, K] in MXFP4, dequantized inside the GEMM."""
     K = x.shape[-1]
     x2 = _x2(x, K)
     M, N = x2.shape[0], out_features
-    y = torch.empty((M, N), dtype=out_dtype or torch.bfloat16, device=x.device)
-    call("ntlb_gemm_mxfp4", x2.data_ptr(), x2.stride(0), packed.data_ptr(), scales.data_ptr(), M, N, K, y.data_ptr(),
-         ops._dtype_code(y.dtype), y.stride(0), ops._stream())
+    y = _fused(_LOWBIT_MXFP4, x2, packed, scales, 32, bias, M, N, K, out_dtype)
     return y.reshape(*x.shape[:-1], N)

@@ -265,7 +265,7 @@ def test_persistent_fp8_fused_forward_and_ste_backward(gpu_device, gran):
     refresh_persistent_lowbit_params(torch.nn.Sequential(layer))
     x = seeded((48, 512), seed=52).to(gpu_device).requires_grad_(True)
     y = layer(x)
-    assert layer._fused_persistent_forward(x.detach()) is not None
+    assert layer._fused_persistent_forward(x.detach(), None) is not None
     w_deq = P.dequantize_fp8_persistent(layer._persistent_fp8_weight, layer._persistent_scale,
                                         target_dtype=torch.bfloat16)
     xr = x.detach().clone().requires_grad_(True)
@@ -389,3 +389,41 @@ def test_forward_step_replays_in_a_hip_graph(gpu_device):
             torch.cuda.synchronize()
             assert torch.equal(yout.view(torch.int16), eager[i].view(torch.int16)), f"replay {rep}, input {i}"
             del junk
+
+
+@pytest.mark.parametrize("mode", ["fp4", "fp8"])
+def test_persistent_fused_forward_with_bias_and_ste_backward(gpu_device, mode):
+    """A biased persistent layer also runs the dequant-fused GEMM (bias added
+    in fp32 before the output rounding); the straight-through gradients of x,
+    the weight and the bias come from the library's bf16 GEMMs and column sum
+    and match F.linear on the materialized dequantized weight."""
+    from lowbit import persistent as P
+    from lowbit.precision import refresh_persistent_lowbit_params
+
+    kw = dict(fp4_param=True) if mode == "fp4" else dict(fp8_param=True)
+    _, res = _resolver(bf16=True, persistent_lowbit_include=["fc"], compute_lowbit_mode=None, **kw)
+    layer = _linear(res, 512, 320, path="fc")
+    with torch.no_grad():
+        layer.bias.copy_(seeded((320,), seed=61, std=0.5))
+    refresh_persistent_lowbit_params(torch.nn.Sequential(layer))
+    x = seeded((48, 512), seed=62).to(gpu_device).requires_grad_(True)
+    assert layer._fused_persistent_forward(x.detach(), layer.bias) is not None
+    y = layer(x)
+    if mode == "fp4":
+        w_deq = P.dequantize_nf4_persistent(layer._persistent_fp4_codes, layer._persistent_scale,
+                                            num_values=320 * 512, target_shape=(320, 512), target_dtype=torch.bfloat16)
+    else:
+        w_deq = P.dequantize_fp8_persistent(layer._persistent_fp8_weight, layer._persistent_scale,
+                                            target_dtype=torch.bfloat16)
+    ref = O.gemm_ref(to_np32(x), to_np32(w_deq), to_np32(layer.bias))
+    assert rel_fro_bf16(y, ref) <= 1e-3
+    xr = x.detach().clone().requires_grad_(True)
+    wr = layer.weight.detach().clone().requires_grad_(True)
+    br = layer.bias.detach().clone().requires_grad_(True)
+    y_mat = torch.nn.functional.linear(xr.float(), (wr + (w_deq - wr).detach()).float(), br.float())
+    dy = seeded((48, 320), seed=63).to(gpu_device)
+    y.backward(dy)
+    y_mat.backward(dy.float())
+    assert rel_fro_bf16(x.grad, xr.grad.double().cpu().numpy()) <= 2e-3
+    assert rel_fro_bf16(layer.weight.grad, wr.grad.double().cpu().numpy()) <= 2e-3
+    assert rel_fro_bf16(layer.bias.grad, br.grad.double().cpu().numpy()) <= 2e-3

@@ -101,6 +101,72 @@ def test_nf4_fused_gemm(gpu_device, M, N, K, block):
     assert rel_fro_bf16(y, O.gemm_ref(to_np32(x), wdq)) <= 1e-3
 
 
+def _fused_unsplit(fmt, x, w, scales, block, N, out_dtype):
+    """The fused GEMM through the entry points without a workspace (every
+    tile whole)."""
+    from lowbit import ops
+    from lowbit._lib import call
+
+    M, K = x.shape
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if fmt == "nf4":
+        call("ntlb_gemm_nf4", x.data_ptr(), x.stride(0), w.data_ptr(), scales.data_ptr(), block, M, N, K,
+             y.data_ptr(), ops._dtype_code(out_dtype), y.stride(0), ops._stream())
+    elif fmt == "mxfp4":
+        call("ntlb_gemm_mxfp4", x.data_ptr(), x.stride(0), w.data_ptr(), scales.data_ptr(), M, N, K, y.data_ptr(),
+             ops._dtype_code(out_dtype), y.stride(0), ops._stream())
+    else:
+        call("ntlb_gemm_fp8p", x.data_ptr(), x.stride(0), w.data_ptr(), scales.data_ptr(), block, M, N, K,
+             y.data_ptr(), ops._dtype_code(out_dtype), y.stride(0), ops._stream())
+    return y
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4", "fp8p"])
+def test_fused_gemm_split_tail_and_bias(gpu_device, fmt):
+    """M 4096, N 5120, K 2048: 320 tiles on 256 compute units, so the 64 tail
+    tiles run as 3 K ranges each.  The split GEMM (fp32 out, no bias) equals
+    the unsplit one within fp32 reassociation, repeats bit for bit (the
+    workspace counters reset), and with a bias matches the oracle."""
+    from lowbit import _lib, persistent as P
+
+    M, N, K = 4096, 5120, 2048
+    if int(_lib.lib().ntlb_gemm_lowbit_workspace_bytes(M, N, K)) == 0:
+        pytest.skip("this device runs the shape unsplit")
+    x = seeded((M, K), seed=20260510).to(gpu_device)
+    w = seeded((N, K), seed=20260511, std=0.02).to(gpu_device)
+    bias = seeded((N,), seed=20260512, std=0.5).to(gpu_device)
+    if fmt == "nf4":
+        codes, scales = P.quantize_nf4_blocks(w, 64)
+        run = lambda b, od: P.linear_nf4(x, codes, scales, out_features=N, block=64, bias=b, out_dtype=od)
+        sc, blk = scales.reshape(-1).contiguous(), 64
+        p_ref, s_ref = O.nf4_quant(to_np32(w), 64)
+        wdq = O.round_bf16(O.nf4_dequant(p_ref, s_ref, N * K, 64)).reshape(N, K)
+    elif fmt == "mxfp4":
+        codes, scales = P.quantize_mxfp4(w)
+        run = lambda b, od: P.linear_mxfp4(x, codes, scales, out_features=N, bias=b, out_dtype=od)
+        sc, blk = scales, 32
+        p_ref, s_ref = O.mxfp4_quant(to_np32(w))
+        wdq = O.round_bf16(O.mxfp4_dequant(p_ref, s_ref, N * K)).reshape(N, K)
+    else:
+        vals, scale = P.quantize_fp8_persistent(w, granularity="per_channel")
+        run = lambda b, od: P.linear_fp8p(x, vals, scale, bias=b, out_dtype=od)
+        codes, sc, blk = vals.view(torch.uint8), scale.reshape(-1).contiguous().float(), K
+        c, s = O.fp8_persistent_quant(to_np32(w), K)
+        wdq = O.round_bf16((O.decode_codes(c, O.GRID_E4M3) * np.repeat(s, K)).reshape(N, K))
+    y_split = run(None, torch.float32)
+    y_again = run(None, torch.float32)
+    y_whole = _fused_unsplit(fmt, x, codes, sc, blk, N, torch.float32)
+    y_bias = run(bias, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(y_split, y_again)
+    d = (y_split.double() - y_whole.double()).norm() / y_whole.double().norm()
+    assert float(d) <= 1e-6, float(d)
+    rows = np.random.default_rng(5).choice(M, 48, replace=False)
+    rows[:8] = np.arange(M - 8, M)  # the last row tile is a split tail tile
+    ref = O.gemm_ref(to_np32(x)[rows], wdq, to_np32(bias))
+    assert rel_fro_bf16(y_bias[rows], ref) <= 1e-3
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 256, 256), (130, 200, 320), (512, 512, 2048)])
 def test_mxfp4_fused_gemm(gpu_device, M, N, K):
     from lowbit import persistent as P

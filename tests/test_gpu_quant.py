@@ -287,6 +287,45 @@ def test_sr_clamps_after_rounding_at_the_tile_amax(gpu_device, sign):
     assert_bits_equal(ct, ct_ref, "128x1 codes")
 
 
+@pytest.mark.parametrize("sign", [1.0, -1.0])
+def test_e4m3_sr_clamps_after_rounding_at_448(gpu_device, sign):
+    """The e4m3 counterpart: with every element at +-448 the scale is 1 and
+    v = +-448 = 1.75 * 2^8, whose spacing-scaled mantissa is t = 14; where
+    u >= 1 - 2^-21, 14 + u rounds to 15 in fp32 (the tie goes to even), one
+    binade past the largest finite code.  The result must clamp to 0x7E /
+    0xFE, not land on the NaN code 0x7F.  Checked in 1x128 tiles (2^24
+    elements: 7 such draws with this seed) and in 128x1 tiles (128 x 65536: 4)
+    against the oracle."""
+    from lowbit import ops
+
+    seed, offset = 77, 5
+    code = 0x7E if sign > 0 else 0xFE
+    R = 1 << 21
+    words = O.sr_bits(seed, offset, 0, R * 8)
+    assert int(((words >> 8) >= (1 << 24) - 8).sum()) > 0
+    x = torch.full((R, 8), 448.0 * sign)
+    q = ops.quant_tile_1x128(x.to(torch.bfloat16).to(gpu_device), fmt="e4m3", rounding="stochastic", seed=seed,
+                             offset=offset)
+    torch.cuda.synchronize()
+    codes = q.codes.cpu().numpy()[:, :8]
+    assert np.all(codes == code)
+    c_ref = O.quant_tile_1x128(x.numpy(), grid=O.GRID_E4M3, rounding=O.ROUND_STOCHASTIC, seed=seed,
+                               offset=offset)[0]
+    assert_bits_equal(codes, c_ref[:, :8], "1x128 codes")
+    K = 65536
+    words = O.sr_bits(seed, offset, 0, 128 * K)
+    assert int(((words >> 8) >= (1 << 24) - 8).sum()) > 0
+    xt = torch.full((128, K), 448.0 * sign)
+    qt = ops.quant_tile_128x1_t(xt.to(torch.bfloat16).to(gpu_device), fmt="e4m3", rounding="stochastic",
+                                seed=seed, offset=offset)
+    torch.cuda.synchronize()
+    ct = qt.codes.cpu().numpy()
+    assert np.all(ct == code)
+    ct_ref = O.quant_tile_128x1_t(xt.numpy(), grid=O.GRID_E4M3, rounding=O.ROUND_STOCHASTIC, seed=seed,
+                                  offset=offset)[0]
+    assert_bits_equal(ct, ct_ref, "128x1 codes")
+
+
 @pytest.mark.parametrize("kind", ["tensor", "channel_last", "channel_rows", "strip"])
 @pytest.mark.parametrize("fmt,grid", GRIDS)
 @pytest.mark.parametrize("rname,rcode", ROUNDS)
