@@ -842,9 +842,8 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // of the 16-byte reads takes 8 pieces of two adjacent rows, one from each
 // half: conflict-free too.  The per-column arrays (maxima, scales,
 // reciprocals) skip one word after column 63, so that the 16 columns cc*8 + j
-// a wave reads at once fall on 16 banks.  Workgroups walk column blocks
-// fastest.  nan_rows, when given, is indexed by transposed row (source
-// column).
+// a wave reads at once fall on 16 banks.  nan_rows, when given, is indexed
+// by transposed row (source column).
 //
 // With DUAL the same pass also writes the 1x128 tiles of x, described by ar
 // (codes, ldc, scales, s_row, s_col, nan_rows and the SR offset): row i of a
@@ -871,7 +870,16 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int cc = tid & 15, rg = tid >> 4;
   const int64_t n_cb = (a.K + 127) / 128;
-  const int64_t mb = (int64_t)blockIdx.x / n_cb, cb = (int64_t)blockIdx.x - mb * n_cb;
+  // workgroup pid takes column block pid % n_cb of row block
+  // (pid / n_cb + 7 * column block) mod n_mb: consecutive workgroups walk the
+  // column blocks, and the skew spreads the row blocks that run at one time
+  // over all of them, so concurrent transposed stores land at many offsets of
+  // the transposed rows instead of a few (c3 dY: 87 -> 82 us).  The dual pass
+  // keeps the plain walk (row block pid / n_cb): its row-major 1x128 stores
+  // want concurrent workgroups on the same rows (skewed: 128 -> 137 us)
+  const int64_t n_mb = (a.R + 127) / 128;
+  const int64_t q = (int64_t)blockIdx.x / n_cb, cb = (int64_t)blockIdx.x - q * n_cb;
+  const int64_t mb = DUAL ? q : (q + 7 * cb) % n_mb;
   const int64_t col0 = cb * 128 + cc * 8;
   const int64_t row0 = mb * 128 + rg * 8;
   const bool col_in = col0 < a.K;  // K % 8 == 0: a chunk is wholly in or out
