@@ -381,14 +381,17 @@ __global__ void __launch_bounds__(256) ep_combine_kernel(const uint8_t* rec, int
 
 // Single-rank combine of the local expert outputs (moe.py:1087-1088 and
 // :489-490, `output[token_indices] += expert_out * weights` once per expert in
-// ascending expert id): one workgroup per token t; thread j owns columns
-// [8j + 2048i, +8).  Slot s of t names row pos[t*K + s] of y (rows in expert
+// ascending expert id): one workgroup of 128 threads per token t; thread j
+// owns columns [8j + 1024i, +8) (H 7168: seven chunks each, none idle; 256
+// threads left half the last pass idle).  Slot s of t names row pos[t*K + s] of y (rows in expert
 // order, clamped below n; negative: dropped by a capacity limit, adds
 // nothing).  Per expert,
 // the product is rounded to the promoted dtype of y and w (ROUND_P: both the
 // output dtype) and the sum to the output dtype, as the two torch ops do.
+constexpr int COMBINE_ROWS_THREADS = 128;
+
 template <int OUT_DT, bool ROUND_P>
-__global__ void __launch_bounds__(256) moe_combine_rows_kernel(const void* y, int64_t ldy, int64_t n,
+__global__ void __launch_bounds__(COMBINE_ROWS_THREADS) moe_combine_rows_kernel(const void* y, int64_t ldy, int64_t n,
                                                                const int32_t* pos,
                                                                const void* topk_idx, int idx_dt, const void* topk_w,
                                                                int w_dt, int K, int64_t H, void* out, int64_t ldo,
@@ -415,7 +418,7 @@ __global__ void __launch_bounds__(256) moe_combine_rows_kernel(const void* y, in
     s_w[rank] = load_elem(topk_w, w_dt, t * K + k);
   }
   __syncthreads();
-  for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+  for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < H; c0 += COMBINE_ROWS_THREADS * 8) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int j0 = 0; j0 < K; j0 += 8) {
       // up to eight rows in flight at once: slots past K or dropped read row
@@ -599,7 +602,7 @@ extern "C" int ntlb_moe_combine_rows(const void* y, int64_t ldy, int64_t n, cons
   // is that dtype: w of the same dtype, which is not fp32
   const bool round_p = w_dtype == out_dtype && out_dtype != NTLB_F32;
   auto launch = [&](auto outc, auto rpc) {
-    moe_combine_rows_kernel<decltype(outc)::value, decltype(rpc)::value><<<(unsigned)T, 256, 0, st>>>(
+    moe_combine_rows_kernel<decltype(outc)::value, decltype(rpc)::value><<<(unsigned)T, COMBINE_ROWS_THREADS, 0, st>>>(
         y, ldy, n, pos, topk_idx, idx_dtype, topk_w, w_dtype, (int)K, H, out, ldo, vec);
   };
   using B = std::integral_constant<int, DT_BF16>;
