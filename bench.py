@@ -173,10 +173,24 @@ def other_config(args) -> dict:
         dg = _time_ms(lambda i: ops.gemm_blockscaled(qdy, qw_t), args.steps, args.warmup, st)
         wg = _time_ms(lambda i: ops.gemm_blockscaled(qdy_t, qx_t), args.steps, args.warmup, st)
         fl = 2.0 * M * N * K
+        # HBM bytes per dgrad launch (uniform B scales: template <GRID, true, false, 0>) from the committed profile
+        traffic = None
+        prof = os.path.join(ROOT, "profiles", f"c3_backward_{fmt}.json")
+        dg_name = f"gemm_blockscaled_kernel<{1 if fmt == 'e4m3' else 0}, true, false, 0>"
+        if os.path.exists(prof):
+            with open(prof) as fh:
+                for kname, tv in json.load(fh).get("traffic", {}).items():
+                    if dg_name in kname:
+                        traffic = int(tv["total_bytes"])
         res.update(value=round(2 * fl / ((dg + wg) * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(dg + wg, 4),
                    dtype="fp8_e4m3" if fmt == "e4m3" else "int8",
                    config={"workload": "c3 backward GEMMs (dgrad + wgrad) of the c2 layer, fp8 recipe", "M": M,
                            "N": N, "K": K, "dy_rounding": args.rounding},
+                   roofline={"bound": "mfma", "kernel": "gemm_blockscaled_kernel (dgrad, split-K tail)",
+                             "achieved": round(fl / (dg * 1e-3) / 1e12, 2), "peak": FP8_PEAK_TFLOPS,
+                             "unit": "TFLOP/s", "frac": round(fl / (dg * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4),
+                             "traffic": traffic, "traffic_source": f"profiles/c3_backward_{fmt}.md" if traffic else None,
+                             "avg_ms": round(dg, 4)},
                    dgrad_tflops=round(fl / (dg * 1e-3) / 1e12, 2), wgrad_tflops=round(fl / (wg * 1e-3) / 1e12, 2),
                    quantizers={k: round(v, 2) for k, v in t.items()},
                    dy_1x128_GBs=round((M * N * 3 + M * (N // 128) * 4) / t["dy_1x128_us"] / 1e3, 1),
@@ -339,6 +353,14 @@ def other_config(args) -> dict:
                   st)
     f8 = _time_ms(lambda i: persistent.linear_fp8p(x, f8_vals, f8_scale), args.steps, args.warmup, st)
     fl = 2.0 * M * N * K
+    # HBM bytes per NF4 fused launch from the committed profile
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", "c5_persistent_fused.json")
+    if os.path.exists(prof):
+        with open(prof) as fh:
+            for kname, tv in json.load(fh).get("traffic", {}).items():
+                if "gemm_lowbit_fused_kernel<0>" in kname:
+                    traffic = int(tv["total_bytes"])
     bf = unf = None
     if not args.no_library_compare:
         bf = _time_ms(lambda i: torch.matmul(x, w.t()), args.steps, args.warmup, st)
@@ -348,8 +370,11 @@ def other_config(args) -> dict:
             args.warmup, st)
     res.update(value=round(fl / (nf4 * 1e-3) / 1e12, 2), unit="TFLOP/s", ms_per_step=round(nf4, 4), dtype="bf16",
                config={"workload": "c5 NF4 (64-element blocks) dequant-fused GEMM", "M": M, "N": N, "K": K},
-               roofline={"bound": "mfma", "achieved": round(fl / (nf4 * 1e-3) / 1e12, 2), "peak": 2500.0,
-                         "unit": "TFLOP/s", "frac": round(fl / (nf4 * 1e-3) / 1e12 / 2500.0, 4), "traffic": None},
+               roofline={"bound": "mfma", "kernel": "gemm_lowbit_fused_kernel<NF4> (split-K tail)",
+                         "achieved": round(fl / (nf4 * 1e-3) / 1e12, 2), "peak": 2500.0,
+                         "unit": "TFLOP/s", "frac": round(fl / (nf4 * 1e-3) / 1e12 / 2500.0, 4), "traffic": traffic,
+                         "traffic_source": "profiles/c5_persistent_fused.md" if traffic else None,
+                         "avg_ms": round(nf4, 4)},
                mxfp4_tflops=round(fl / (mx * 1e-3) / 1e12, 2),
                fp8_persistent_tflops=round(fl / (f8 * 1e-3) / 1e12, 2),
                adamw_nf4_refresh={"fused_us": round(fused_ms * 1e3, 1), "two_pass_us": round(two_ms * 1e3, 1),
