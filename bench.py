@@ -92,7 +92,9 @@ def _spin_up(fn, seconds: Optional[float] = None) -> None:
 def _time_ms(fn, n: int, warmup: int, stream) -> float:
     import torch
 
-    _spin_up(fn, SPIN_UP_S / 3)
+    # the full spin-up before every timed op: hipBLASLt's GEMMs (the library
+    # comparisons) read up to 25% slow for the first ~0.1 s at a new shape
+    _spin_up(fn, SPIN_UP_S)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()

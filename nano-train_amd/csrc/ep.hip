@@ -297,7 +297,7 @@ __device__ __forceinline__ void round8(float (&v)[8]) {
     }
   } else if constexpr (OUT_DT == DT_F16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __half2float(__float2half(v[i]));
+    for (int i = 0; i < 8; ++i) v[i] = __half2float(f32_to_f16(v[i]));
   }
 }
 

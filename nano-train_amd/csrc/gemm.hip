@@ -598,7 +598,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
             *reinterpret_cast<uint2*>(dst) =
                 make_uint2(__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1));
           } else {
-            __half h[4] = {__float2half(v[0]), __float2half(v[1]), __float2half(v[2]), __float2half(v[3])};
+            __half h[4] = {f32_to_f16(v[0]), f32_to_f16(v[1]), f32_to_f16(v[2]), f32_to_f16(v[3])};
             *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(h);
           }
         }

@@ -560,7 +560,7 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
           } else if constexpr (ODT == DT_BF16) {
             *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
           } else {
-            __half h[4] = {__float2half(v[0]), __float2half(v[1]), __float2half(v[2]), __float2half(v[3])};
+            __half h[4] = {f32_to_f16(v[0]), f32_to_f16(v[1]), f32_to_f16(v[2]), f32_to_f16(v[3])};
             *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(h);
           }
         }

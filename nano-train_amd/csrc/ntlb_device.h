@@ -248,6 +248,17 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
+// v to f16 (round to nearest even) from the fp32 value as it stands.  The
+// fence keeps the compiler from folding a preceding fp32 multiply or add into
+// a mixed-precision instruction (v_fma_mixlo_f16), which rounds the exact
+// result once instead of rounding to fp32 and then to f16 as fp32 arithmetic
+// followed by a cast does: -38.078125 is an f16 tie only after the fp32
+// rounding of the product that gives it.
+__device__ __forceinline__ __half f32_to_f16(float v) {
+  asm("" : "+v"(v));
+  return __float2half(v);
+}
+
 __device__ __forceinline__ float load_elem(const void* p, int dtype, int64_t idx) {
   if (dtype == DT_BF16) return bf16_bits_to_f32(((const uint16_t*)p)[idx]);
   if (dtype == DT_F16) return __half2float(((const __half*)p)[idx]);
@@ -258,7 +269,7 @@ __device__ __forceinline__ float load_elem(const void* p, int dtype, int64_t idx
 // and widened back to fp32
 __device__ __forceinline__ float round_to_dtype(float v, int dtype) {
   if (dtype == DT_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
-  if (dtype == DT_F16) return __half2float(__float2half(v));
+  if (dtype == DT_F16) return __half2float(f32_to_f16(v));
   return v;
 }
 
@@ -266,7 +277,7 @@ __device__ __forceinline__ void store_elem(void* p, int dtype, int64_t idx, floa
   if (dtype == DT_BF16) {
     ((uint16_t*)p)[idx] = f32_to_bf16_bits(v);
   } else if (dtype == DT_F16) {
-    ((__half*)p)[idx] = __float2half(v);
+    ((__half*)p)[idx] = f32_to_f16(v);
   } else {
     ((float*)p)[idx] = v;
   }

@@ -182,6 +182,78 @@ __global__ void __launch_bounds__(256) lowbit_dequant_kernel(const uint8_t* pack
   }
 }
 
+// The same dequantization, 16 consecutive weights per thread (e0 % 16 == 0)
+// under one scale (the scale block is a multiple of 16; MXFP4's 32-element
+// blocks always are): one 8- or 16-byte code load, the scale once, and
+// 16-byte stores.  The 4-bit code values come from a 16-entry table in LDS
+// (one entry per bank, so any mix of codes reads without conflicts).  Each
+// value is computed as above -- codebook value times scale in fp32 (NF4),
+// e2m1 value times 2^(e - 127) (MXFP4), e4m3 value times scale (FP8P) -- and
+// rounded to the output dtype by the same functions, so the output is
+// bit-identical to the element-wise kernels.  POW2: the block is 2^bshift
+// elements (a shift finds the scale), else a 64-bit division.
+template <int FMT, int OUT_DT, bool POW2>
+__global__ void __launch_bounds__(256) dequant16_kernel(const uint8_t* codes, const void* scales, int64_t n16,
+                                                        int64_t block, int bshift, void* out) {
+  __shared__ float table[16];
+  if (threadIdx.x < 16) {
+    if constexpr (FMT == FMT_NF4) table[threadIdx.x] = kNF4[threadIdx.x];
+    else table[threadIdx.x] = e2m1_value(threadIdx.x);
+  }
+  __syncthreads();
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= n16) return;
+  const int64_t e0 = t * 16;
+  float v[16];
+  if constexpr (FMT == FMT_FP8P) {
+    const uint4 q = *reinterpret_cast<const uint4*>(codes + e0);
+    const float s = reinterpret_cast<const float*>(scales)[POW2 ? (e0 >> bshift) : (e0 / block)];
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = e4m3_to_f32((w[i >> 2] >> (8 * (i & 3))) & 0xFFu) * s;
+  } else {
+    const uint2 q = *reinterpret_cast<const uint2*>(codes + (e0 >> 1));
+    const uint32_t w[2] = {q.x, q.y};
+    float s = 0.0f;
+    int ex = 0;
+    bool nan_block = false;
+    if constexpr (FMT == FMT_NF4) {
+      s = reinterpret_cast<const float*>(scales)[POW2 ? (e0 >> bshift) : (e0 / block)];
+    } else {
+      const uint32_t sb = reinterpret_cast<const uint8_t*>(scales)[e0 >> 5];
+      nan_block = sb == 0xFFu;
+      ex = (int)sb - 127;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float c = table[(w[i >> 3] >> (4 * (i & 7))) & 15u];
+      if constexpr (FMT == FMT_NF4)
+        v[i] = c * s;
+      else
+        v[i] = nan_block ? __uint_as_float(0x7FC00000u) : ldexpf(c, ex);
+    }
+  }
+  if constexpr (OUT_DT == DT_F32) {
+    float4* o = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + e0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+  } else {
+    uint32_t h[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (OUT_DT == DT_BF16) {
+        h[j] = (uint32_t)f32_to_bf16_bits(v[2 * j]) | ((uint32_t)f32_to_bf16_bits(v[2 * j + 1]) << 16);
+      } else {
+        h[j] = (uint32_t)__half_as_ushort(f32_to_f16(v[2 * j])) |
+               ((uint32_t)__half_as_ushort(f32_to_f16(v[2 * j + 1])) << 16);
+      }
+    }
+    uint4* o = reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + e0);
+    o[0] = make_uint4(h[0], h[1], h[2], h[3]);
+    o[1] = make_uint4(h[4], h[5], h[6], h[7]);
+  }
+}
+
 // MXFP4 refresh: 4 lanes (a DPP quad) per 32-element block
 template <int IN_DT>
 __global__ void __launch_bounds__(256) mxfp4_quant_kernel(const void* w, int64_t n, uint8_t* packed,
@@ -241,6 +313,41 @@ __global__ void __launch_bounds__(256) fp8p_dequant_kernel(const uint8_t* codes,
     if (e >= n) break;
     store_elem(out, out_dtype, e, e4m3_to_f32(codes[e]) * scales[e / block]);
   }
+}
+
+// Dequantize n weights: the 16-per-thread kernel when n, the scale block and
+// the pointers allow it, else the element-wise kernel.
+template <int FMT>
+static void launch_dequant(const uint8_t* codes, const void* scales, int64_t n, int64_t block, void* out,
+                           int out_dtype, hipStream_t st) {
+  const bool vec = n % 16 == 0 && block % 16 == 0 && aligned(out, 16) && aligned(codes, FMT == FMT_FP8P ? 16 : 8) &&
+                   cdiv(n / 16, 256) <= 0x7FFFFFFF;
+  if (!vec) {
+    if constexpr (FMT == FMT_FP8P)
+      fp8p_dequant_kernel<<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, st>>>(codes, reinterpret_cast<const float*>(
+                                                                              scales), n, block, out, out_dtype);
+    else
+      lowbit_dequant_kernel<FMT><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, st>>>(codes, scales, n, block, out,
+                                                                                   out_dtype);
+    return;
+  }
+  const int64_t n16 = n / 16;
+  const bool pow2 = (block & (block - 1)) == 0;
+  const int bshift = pow2 ? __builtin_ctzll((unsigned long long)block) : 0;
+  const dim3 grd((unsigned)cdiv(n16, 256)), blk(256);
+  auto go = [&](auto outc) {
+    constexpr int ODT = decltype(outc)::value;
+    if (pow2)
+      dequant16_kernel<FMT, ODT, true><<<grd, blk, 0, st>>>(codes, scales, n16, block, bshift, out);
+    else
+      dequant16_kernel<FMT, ODT, false><<<grd, blk, 0, st>>>(codes, scales, n16, block, bshift, out);
+  };
+  if (out_dtype == NTLB_BF16)
+    go(std::integral_constant<int, DT_BF16>());
+  else if (out_dtype == NTLB_F16)
+    go(std::integral_constant<int, DT_F16>());
+  else
+    go(std::integral_constant<int, DT_F32>());
 }
 
 // ---------------------------------------------------------------------------
@@ -962,8 +1069,7 @@ extern "C" int ntlb_nf4_dequant(const uint8_t* packed, const float* scales, int6
   if (!valid_dtype(out_dtype) || n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad argument", fn);
   if (n == 0) return NTLB_OK;
   if (!packed || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
-  lowbit_dequant_kernel<FMT_NF4><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(packed, scales, n,
-                                                                                                 block, out, out_dtype);
+  launch_dequant<FMT_NF4>(packed, scales, n, block, out, out_dtype, as_stream(stream));
   return check_launch(fn);
 }
 
@@ -990,8 +1096,7 @@ extern "C" int ntlb_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, 
   if (!valid_dtype(out_dtype) || n < 0) return fail(NTLB_EINVAL, "%s: bad argument", fn);
   if (n == 0) return NTLB_OK;
   if (!packed || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
-  lowbit_dequant_kernel<FMT_MXFP4><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(
-      packed, scales, n, 32, out, out_dtype);
+  launch_dequant<FMT_MXFP4>(packed, scales, n, 32, out, out_dtype, as_stream(stream));
   return check_launch(fn);
 }
 
@@ -1122,8 +1227,7 @@ extern "C" int ntlb_fp8_persistent_dequant(const uint8_t* codes, const float* sc
   if (!valid_dtype(out_dtype) || n < 0 || block < 1) return fail(NTLB_EINVAL, "%s: bad argument", fn);
   if (n == 0) return NTLB_OK;
   if (!codes || !scales || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
-  fp8p_dequant_kernel<<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, as_stream(stream)>>>(codes, scales, n, block, out,
-                                                                                     out_dtype);
+  launch_dequant<FMT_FP8P>(codes, scales, n, block, out, out_dtype, as_stream(stream));
   return check_launch(fn);
 }
 

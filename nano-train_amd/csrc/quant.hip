@@ -378,7 +378,9 @@ __global__ void __launch_bounds__(256) quant_block_128x128_kernel(BlockArgs ba) 
   m = max(max(red[0], red[1]), max(red[2], red[3]));
   const float s = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
   if (tid == 0) a.scales[nb * a.s_row + kb * a.s_col] = s;
-#pragma unroll
+  // fully unrolled so that v[i] stays in registers (a rolled loop indexes it
+  // in scratch memory)
+#pragma clang loop unroll(full)
   for (int i = 0; i < 8; ++i) {
     int64_t n = nb * 128 + rr + 16 * i;
     uint32_t rb[8];
@@ -618,7 +620,7 @@ __device__ __forceinline__ void round8_dtype(float (&v)[8]) {
     }
   } else if constexpr (DT == DT_F16) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __half2float(__float2half(v[i]));
+    for (int i = 0; i < 8; ++i) v[i] = __half2float(f32_to_f16(v[i]));
   }
 }
 

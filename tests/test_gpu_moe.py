@@ -33,8 +33,11 @@ def _ref_comm(x: torch.Tensor, granularity: str, rounding: int, bits: int, seed:
 @pytest.mark.parametrize("granularity", ["block_128x128", "tile_1x128", "channel", "tensor"])
 @pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
 @pytest.mark.parametrize("shape,dtype", [((7, 257), torch.float32), ((64, 1024), torch.bfloat16),
-                                         ((3, 5, 300), torch.bfloat16)])
+                                         ((3, 5, 300), torch.bfloat16), ((128, 2048), torch.float16)])
 def test_comm_quant_dequant_parity(gpu_device, granularity, rounding, shape, dtype):
+    """Every rounding step of the reference's straight-through expression in
+    the input dtype, float16 included (dq = q*s rounded to fp32 and then to
+    f16, not in one step)."""
     from lowbit import moe
 
     x = seeded(shape, seed=20260401, dtype=dtype, outliers=0.01).to(gpu_device).requires_grad_(True)

@@ -342,3 +342,70 @@ def test_mxfp4_fused_gemm_dequant_exact_all_codes(gpu_device):
     assert np.isnan(got[nan_row]).all()
     keep = [r for r in range(N) if r != nan_row]
     np.testing.assert_array_equal(got[keep], want[keep])
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "mxfp4", "fp8p"])
+@pytest.mark.parametrize("block", [64, 96, 0])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequant_vector_path_matches_elementwise_and_oracle(gpu_device, fmt, block, out_dtype):
+    """The 16-weights-per-thread dequant (aligned output, n and block multiples
+    of 16) against the element-wise kernel (the same call on an output offset
+    by one element, which that path requires) and against the oracle: every
+    code byte, scales across many binades, MXFP4 NaN blocks (e8m0 0xFF), a
+    non-power-of-two block (96) and a tensor-wide one (0 = n)."""
+    from lowbit import _lib, ops
+
+    if fmt == "mxfp4" and block != 64:
+        pytest.skip("MXFP4 blocks are always 32 elements")
+    # whole scale blocks (and whole 32-element MXFP4 blocks), as a weight of K % block == 0 has
+    n = {64: 64 * 1025, 96: 96 * 683, 0: 16 * 4099}[block]
+    blk = n if block == 0 else block
+    rng = np.random.default_rng(20261202 + blk)
+    if fmt == "fp8p":
+        codes = rng.integers(0, 256, n, dtype=np.uint8)
+        nscale = n // blk
+        scales = np.float32(2.0) ** rng.integers(-30, 30, nscale).astype(np.float32) * rng.uniform(
+            1, 2, nscale).astype(np.float32)
+        want = (torch.from_numpy(codes).view(torch.float8_e4m3fn).float() *
+                torch.from_numpy(np.repeat(scales, blk))).numpy()
+    else:
+        codes = rng.integers(0, 256, n // 2, dtype=np.uint8)
+        if fmt == "nf4":
+            nscale = n // blk
+            scales = np.float32(2.0) ** rng.integers(-30, 30, nscale).astype(np.float32) * rng.uniform(
+                1, 2, nscale).astype(np.float32)
+            want = O.nf4_dequant(codes, scales, n, blk)
+        else:
+            assert n % 32 == 0
+            scales = rng.integers(0, 256, n // 32, dtype=np.uint8)
+            scales[::17] = 0xFF
+            scales[1::23] = 0
+            want = O.mxfp4_dequant(codes, scales, n)
+    want_t = torch.from_numpy(want).to(out_dtype)
+    c_d = torch.from_numpy(codes).to(gpu_device)
+    s_d = torch.from_numpy(scales).to(gpu_device)
+    outs = []
+    for off in (0, 1):
+        buf = torch.zeros(n + 8, dtype=out_dtype, device=gpu_device)
+        out = buf[off:off + n]
+        st = ops._stream()
+        if fmt == "nf4":
+            _lib.call("ntlb_nf4_dequant", c_d.data_ptr(), s_d.data_ptr(), n, blk, out.data_ptr(),
+                      ops._dtype_code(out_dtype), st)
+        elif fmt == "mxfp4":
+            _lib.call("ntlb_mxfp4_dequant", c_d.data_ptr(), s_d.data_ptr(), n, out.data_ptr(),
+                      ops._dtype_code(out_dtype), st)
+        else:
+            _lib.call("ntlb_fp8_persistent_dequant", c_d.data_ptr(), s_d.data_ptr(), n, blk, out.data_ptr(),
+                      ops._dtype_code(out_dtype), st)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+        # nothing written outside [off, off + n)
+        assert not buf.cpu()[:off].any() and not buf.cpu()[off + n:].any()
+    bits = torch.int32 if out_dtype == torch.float32 else torch.int16
+    assert torch.equal(outs[0].view(bits), outs[1].view(bits))
+    # NaNs (e4m3 codes 0x7F / 0xFF, MXFP4 NaN blocks) by position, every other value bit for bit
+    nan = torch.isnan(want_t)
+    assert torch.equal(torch.isnan(outs[0]), nan)
+    assert torch.equal(outs[0][~nan].view(bits), want_t[~nan].view(bits))
+    assert fmt == "nf4" or nan.any()
