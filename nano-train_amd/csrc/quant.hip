@@ -164,7 +164,20 @@ struct Chunk8 {
   uint4 w[IN_DT == DT_F32 ? 2 : 1];
 };
 
-template <int IN_DT>
+// NTL: loads with the non-temporal hint, for inputs read once and too large
+// to stay in the caches
+typedef unsigned int u32x4_ld __attribute__((ext_vector_type(4)));
+template <bool NTL>
+__device__ __forceinline__ uint4 load16(const void* p) {
+  if constexpr (NTL) {
+    const u32x4_ld v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_ld*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const uint4*>(p);
+  }
+}
+
+template <int IN_DT, bool NTL = false>
 __device__ __forceinline__ void chunk_load(Chunk8<IN_DT>& c, const void* base, int64_t off, bool in) {
   if (!in) {
     c.w[0] = make_uint4(0, 0, 0, 0);
@@ -172,11 +185,11 @@ __device__ __forceinline__ void chunk_load(Chunk8<IN_DT>& c, const void* base, i
     return;
   }
   if constexpr (IN_DT == DT_F32) {
-    const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const float*>(base) + off);
-    c.w[0] = p[0];
-    c.w[1] = p[1];
+    const float* p = reinterpret_cast<const float*>(base) + off;
+    c.w[0] = load16<NTL>(p);
+    c.w[1] = load16<NTL>(p + 4);
   } else {
-    c.w[0] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(base) + off);
+    c.w[0] = load16<NTL>(reinterpret_cast<const uint16_t*>(base) + off);
   }
 }
 
@@ -212,13 +225,13 @@ __device__ __forceinline__ void chunk_floats(const Chunk8<IN_DT>& c, float (&v)[
   }
 }
 
-template <int IN_DT>
+template <int IN_DT, bool NTL = false>
 __device__ __forceinline__ void tile_loads(Chunk8<IN_DT> (&c)[TILE_TU], const QuantArgs& a, int64_t r, int t0,
                                            int T, int lane16) {
 #pragma unroll
   for (int u = 0; u < TILE_TU; ++u) {
     const int64_t k0 = (int64_t)(t0 + u) * 128 + lane16 * 8;
-    chunk_load<IN_DT>(c[u], a.x, r * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
+    chunk_load<IN_DT, NTL>(c[u], a.x, r * a.ldx + k0, r < a.R && t0 + u < T && k0 < a.K);
   }
 }
 
@@ -316,7 +329,7 @@ __device__ __forceinline__ void tile_quant(const Chunk8<IN_DT> (&c)[TILE_TU], co
 // by, by + gridDim.y, ... (16 rows each).  No prefetch: the lowest register
 // count and the highest occupancy; the loop only runs when the grid is capped
 // below the number of row blocks.
-template <int IN_DT, int GRID, bool SR, bool DQ, bool FAN = false>
+template <int IN_DT, int GRID, bool SR, bool DQ, bool FAN = false, bool NTL = false>
 __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
   const int lane16 = threadIdx.x & 15;
   const int T = (int)((a.K + 127) >> 7);
@@ -328,13 +341,13 @@ __global__ void __launch_bounds__(256) quant_tile_1x128_fast(QuantArgs a) {
   int64_t r = rb * 16 + (threadIdx.x >> 4);
   // the loads at the end of the body, not at its head: head-first, the
   // compiler gave the stochastic-rounding and dq variants 4-13 more VGPRs
-  tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
+  tile_loads<IN_DT, NTL>(cur, a, r, t0, T, lane16);
   for (;;) {
     if (r < a.R) tile_quant<IN_DT, GRID, SR, DQ, FAN>(cur, a, r, t0, T, lane16);  // whole 16-lane rows
     rb += gridDim.y;
     if (rb >= n_rb) return;
     r = rb * 16 + (threadIdx.x >> 4);
-    tile_loads<IN_DT>(cur, a, r, t0, T, lane16);
+    tile_loads<IN_DT, NTL>(cur, a, r, t0, T, lane16);
   }
 }
 
@@ -425,14 +438,14 @@ constexpr int BLK_ROWS = BLK_THREADS / 16;  // rows covered by one pass of the w
 constexpr int BLK_RPT = 128 / BLK_ROWS;     // rows per thread
 constexpr int BLK_WAVES = BLK_THREADS / 64;
 
-template <int IN_DT>
+template <int IN_DT, bool NTL = false>
 __device__ __forceinline__ void block_loads(Chunk8<IN_DT> (&ch)[BLK_RPT], const QuantArgs& a, int64_t nb, int64_t kb,
                                             int rr, int sub) {
   const int64_t k0 = kb * 128 + sub * 8;
 #pragma unroll
   for (int i = 0; i < BLK_RPT; ++i) {
     const int64_t n = nb * 128 + rr + BLK_ROWS * i;
-    chunk_load<IN_DT>(ch[i], a.x, n * a.ldx + k0, n < a.R && k0 < a.K);
+    chunk_load<IN_DT, NTL>(ch[i], a.x, n * a.ldx + k0, n < a.R && k0 < a.K);
   }
 }
 
@@ -508,7 +521,7 @@ __device__ __forceinline__ void block_quant(const Chunk8<IN_DT> (&ch)[BLK_RPT], 
 // block as raw chunks between the amax pass and the quantize pass (one HBM
 // read).  Workgroup (kb, nb0) covers column block kb of the row blocks nb0,
 // nb0 + gridDim.y, ...: consecutive workgroups walk column blocks.
-template <int IN_DT, int GRID, bool SR, bool DQ>
+template <int IN_DT, int GRID, bool SR, bool DQ, bool NTL = false>
 __global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArgs ba) {
   __shared__ uint32_t red[BLK_WAVES];
   __shared__ uint8_t tile_t[128][128 + 4];
@@ -521,12 +534,12 @@ __global__ void __launch_bounds__(BLK_THREADS) quant_block_128x128_fast(BlockArg
   Chunk8<IN_DT> cur[BLK_RPT];
   // loads at the end of the body, as in the 1x128 kernel (head-first took
   // 59 -> 83 VGPRs and halved the resident workgroups)
-  block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
+  block_loads<IN_DT, NTL>(cur, ba.q, nb, kb, rr, sub);
   for (;;) {
     block_quant<IN_DT, GRID, SR, DQ>(cur, ba, nb, kb, tid, red, tile_t);
     nb += gridDim.y;
     if (nb >= NB) return;
-    block_loads<IN_DT>(cur, ba.q, nb, kb, rr, sub);
+    block_loads<IN_DT, NTL>(cur, ba.q, nb, kb, rr, sub);
   }
 }
 
@@ -1140,6 +1153,37 @@ __global__ void __launch_bounds__(256) dequant_fast_kernel(const uint8_t* codes,
 // ---------------------------------------------------------------------------
 // dispatch helpers
 // ---------------------------------------------------------------------------
+// Round-to-nearest inputs larger than this stream through the caches with
+// the non-temporal load hint.  At c2/c3: W (264 MB) 77 -> 66 us in the
+// 128x128 pass, dY (302 MB) 79 -> 72 us in the 1x128 pass; X at c2 (117 MB)
+// measured 31 -> 33 us with it and keeps plain loads.  The 128x1 pass reads
+// 16-column strips that share cache lines with the neighbouring strips, and
+// the hint slowed it (83 -> 91-96 us), so it has none.  Stochastic rounding
+// is VALU-bound and keeps plain loads.
+constexpr int64_t NT_LOAD_MIN_BYTES = (int64_t)128 << 20;
+
+template <int DT, int G, bool S>
+static void launch_tile_fast_nodq(bool ntl, dim3 grd, dim3 blk, hipStream_t st, const QuantArgs& a) {
+  if constexpr (!S) {
+    if (ntl) {
+      quant_tile_1x128_fast<DT, G, S, false, false, true><<<grd, blk, 0, st>>>(a);
+      return;
+    }
+  }
+  quant_tile_1x128_fast<DT, G, S, false><<<grd, blk, 0, st>>>(a);
+}
+
+template <int DT, int G, bool S>
+static void launch_block_fast_nodq(bool ntl, dim3 grd, dim3 blk, hipStream_t st, const BlockArgs& ba) {
+  if constexpr (!S) {
+    if (ntl) {
+      quant_block_128x128_fast<DT, G, S, false, true><<<grd, blk, 0, st>>>(ba);
+      return;
+    }
+  }
+  quant_block_128x128_fast<DT, G, S, false><<<grd, blk, 0, st>>>(ba);
+}
+
 #define NTLB_DISPATCH_GRID_SR(GRIDV, SRV, ...)                         \
   do {                                                                  \
     if ((GRIDV) == GRID_INT) {                                          \
@@ -1267,11 +1311,12 @@ extern "C" int ntlb_quant_tile_1x128(const void* x, int x_dtype, int64_t R, int6
           quant_tile_1x128_fast<DT_F32, G_, S_, true><<<fgrd, fblk, 0, st>>>(a);
       });
     } else {
+      const bool ntl = R * ldx * dtype_size(x_dtype) > NT_LOAD_MIN_BYTES;
       NTLB_DISPATCH_GRID_SR(grid, sr, {
         if (x_dtype == NTLB_BF16)
-          quant_tile_1x128_fast<DT_BF16, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+          launch_tile_fast_nodq<DT_BF16, G_, S_>(ntl, fgrd, fblk, st, a);
         else
-          quant_tile_1x128_fast<DT_F32, G_, S_, false><<<fgrd, fblk, 0, st>>>(a);
+          launch_tile_fast_nodq<DT_F32, G_, S_>(ntl, fgrd, fblk, st, a);
       });
     }
     return check_launch(fn);
@@ -1365,11 +1410,12 @@ extern "C" int ntlb_quant_block_128x128(const void* w, int w_dtype, int64_t N, i
           quant_block_128x128_fast<DT_F32, G_, S_, true><<<fgrd, fblk, 0, st>>>(ba);
       });
     } else {
+      const bool ntl = N * ldw * dtype_size(w_dtype) > NT_LOAD_MIN_BYTES;
       NTLB_DISPATCH_GRID_SR(grid, sr, {
         if (w_dtype == NTLB_BF16)
-          quant_block_128x128_fast<DT_BF16, G_, S_, false><<<fgrd, fblk, 0, st>>>(ba);
+          launch_block_fast_nodq<DT_BF16, G_, S_>(ntl, fgrd, fblk, st, ba);
         else
-          quant_block_128x128_fast<DT_F32, G_, S_, false><<<fgrd, fblk, 0, st>>>(ba);
+          launch_block_fast_nodq<DT_F32, G_, S_>(ntl, fgrd, fblk, st, ba);
       });
     }
     return check_launch(fn);
