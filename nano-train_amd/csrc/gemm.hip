@@ -341,6 +341,10 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  // whether any of this wave's rows m0 + wm*128 .. +127 is below M (for a
+  // grouped tile, the expert's end); uniform per wave
+  bool rows_live = true;
+  if constexpr (B_UNIFORM) rows_live = __builtin_amdgcn_readfirstlane((int)(m0 + wm * 128 < g.M)) != 0;
 
 #pragma unroll
   for (int j = 0; j < 4; ++j) issue_group(src, lds_a0, lds_b0, kb0, wave, j);
@@ -360,6 +364,14 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     const int kn = min(kt + 1, kb1 - 1);
     const float s_next = s_src[(int64_t)kn * s_step];
 
+    if (B_UNIFORM && !rows_live) {
+      // none of this wave's 128 rows is in the matrix (the last row tile of
+      // an expert or of M): its share of the next block's copies only, no
+      // fragments and no MFMAs; its accumulators stay zero and are never
+      // stored.  The wave sharing its SIMD then has the matrix core alone.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) issue_group(src, BUF ? lds_a0 : lds_a1, BUF ? lds_b0 : lds_b1, kn, wave, j);
+    } else {
     v8i bf[4];
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) bf[tn] = load_frag(tb, wn * 64 + tn * 16, lane);
@@ -446,6 +458,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
         asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
         if (tm + 1 < 8) af = af_next;
       }
+    }
     }
     (BUF ? lds_s0 : lds_s1)[tid] = s_next;
     __builtin_amdgcn_s_waitcnt(0);
