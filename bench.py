@@ -1,6 +1,6 @@
 """Benchmark of the low-bit linear hot path on one MI355X.
 
-One step = one emulated-FP8 Linear forward of BASELINE config 2 (the
+One step = one emulated-FP8 Linear forward of benchmark config 2 (the
 DeepSeek-V3 dense MLP up-projection): quantize X [8192, 7168] per 1x128 tile,
 quantize W [18432, 7168] per 128x128 block (e4m3, amax/448 scales, round to
 nearest), and the blockwise-scaled FP8 GEMM Y = X_dq W_dq^T (fp32 accumulate,
@@ -47,13 +47,13 @@ def parse_args():
     p.add_argument("--format", default="e4m3", choices=["e4m3", "int_grid"])
     p.add_argument("--rounding", default=None, choices=["nearest", "stochastic"],
                    help="default: nearest, except c3, whose dY quantizers use the seeded stochastic rounding "
-                        "its BASELINE configuration names")
+                        "its benchmark configuration names")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-sample-rows", type=int, default=1024)
     p.add_argument("--calib-copy", action="store_true",
                    help="also launch a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     p.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
-                   help="c2 (default) is the headline; c1/c3/c4/c5 measure the other BASELINE configurations")
+                   help="c2 (default) is the headline; c1/c3/c4/c5 measure the other benchmark configurations")
     p.add_argument("--no-library-compare", action="store_true",
                    help="skip the library GEMMs timed for comparison (hipBLASLt through torch.matmul), so that a "
                         "kernel trace holds this build's kernels only")
@@ -119,7 +119,7 @@ def _calibration_copy(dev) -> None:
 
 
 def other_config(args) -> dict:
-    """One line for BASELINE configs 1, 3, 4, 5 (kernel times by HIP events)."""
+    """One line for benchmark configs 1, 3, 4, 5 (kernel times by HIP events)."""
     import torch
 
     from lowbit import moe, ops, persistent, workloads
@@ -772,7 +772,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8_e4m3" if args.format == "e4m3" else "int8",
-        "data": "synthetic (seeded, BASELINE config 2 distributions); 3 rotating input sets",
+        "data": "synthetic (seeded, benchmark config 2 distributions); 3 rotating input sets",
         "config": {
             "workload": "c2 DeepSeek-V3 dense MLP up-projection forward: quant X 1x128 + quant W 128x128 + "
                         "blockwise-scaled GEMM",

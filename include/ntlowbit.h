@@ -413,7 +413,7 @@ int ntlb_nf4_dequant(const uint8_t* packed, const float* scales, int64_t n, int6
  * MXFP4 (OCP MX v1.0) refresh: 32-element blocks, e8m0 scale
  * X = 2^(floor(log2 amax) - 2) (exponent clamped to [-127, 127]; 0xFF when the
  * block holds a NaN or inf), e2m1 codes rounded to nearest even with
- * saturation, packed as NF4.  No reference function.
+ * saturation, packed as NF4.  No reference function (benchmark config 5).
  */
 int ntlb_mxfp4_quant(const void* w, int w_dtype, int64_t n, uint8_t* packed, uint8_t* scales, void* stream);
 int ntlb_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, int64_t n, void* out, int out_dtype,

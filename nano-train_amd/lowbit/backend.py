@@ -27,7 +27,7 @@ dW = dY^T @ X_q with dY unquantized and W_q, X_q the dequantized operands in
 the input dtypes.  For bf16 layers both GEMMs decode the forward's codes
 inside the kernel (no dequantized tensor is written); other dtypes multiply
 the dequantized tensors on the fp32-MFMA GEMM.  db is a HIP column sum.
-``backward="fp8"`` is the DeepSeek-V3 recipe of BASELINE config 3 (no
+``backward="fp8"`` is the DeepSeek-V3 recipe of benchmark config 3 (no
 reference counterpart): dY is quantized per 1x128 tile for dgrad, dY^T and
 X^T per 128x1 tile for wgrad, and both run on the blockwise GEMM.
 
@@ -222,7 +222,7 @@ class _HipLowBitLinear(torch.autograd.Function):
 
 
 def _fp8_recipe_backward(backend, dy2, x2, weight, base, needs):
-    """DeepSeek-V3 recipe backward: quantized dgrad / wgrad."""
+    """DeepSeek-V3 recipe backward (benchmark config 3): quantized dgrad / wgrad."""
     fmt, bits, rnd, seed = backend.code_format, backend.bits, backend._rounding_mode, backend.seed
     dx = dw = None
     qdy = qdyt = None

@@ -11,7 +11,7 @@ float8_e4m3fn values and `_persistent_scale` fp32 layout, layers.py:235-246):
   quantize_fp8_persistent       layers.py:104-117
   dequantize_fp8_persistent     layers.py:120-127
 
-plus the BASELINE config 5 formats that have no reference function: NF4 with
+plus the benchmark config 5 formats that have no reference function: NF4 with
 one scale per 64 elements, MXFP4 (e2m1 + e8m0 per 32), and the GEMMs with the
 dequantization fused into the weight-tile prologue (linear_nf4, linear_mxfp4,
 and linear_fp8p for the persistent FP8 weight).

@@ -1,5 +1,5 @@
 """GPU parity of the blockwise-scaled GEMM against the fp32-dequantize-then-float64
-matmul oracle.  The bar (BASELINE): relative Frobenius error <= 1e-3, both
+matmul oracle.  The bar: relative Frobenius error <= 1e-3, both
 sides rounded to bf16."""
 
 from __future__ import annotations

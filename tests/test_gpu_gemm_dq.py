@@ -250,7 +250,7 @@ def test_colsum_matches_float64(gpu_device, M, N):
 
 
 def test_dq_forward_c2_full_size_sampled(gpu_device):
-    """BASELINE config 2 at full size: the reference-exact forward against the
+    """benchmark config 2 at full size: the reference-exact forward against the
     bf16-operand oracle on sampled rows and columns."""
     from lowbit import workloads
 
@@ -269,7 +269,7 @@ def test_dq_forward_c2_full_size_sampled(gpu_device):
 
 
 def test_ste_backward_c3_full_size_sampled(gpu_device):
-    """BASELINE config 3 shapes with the reference's straight-through backward:
+    """benchmark config 3 shapes with the reference's straight-through backward:
     dX = dY @ bf16(W_dq) and dW = dY^T @ bf16(X_dq) from the forward's e4m3
     codes, on sampled rows / columns against the oracle."""
     from lowbit import workloads

@@ -197,7 +197,7 @@ def test_ste_backward_matches_reference_math(gpu_device, fmt):
 
 @pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
 def test_fp8_recipe_backward(gpu_device, rounding):
-    """BASELINE config 3 recipe: dY 1x128 for dgrad; dY^T, X^T per 128x1 for wgrad."""
+    """benchmark config 3 recipe: dY 1x128 for dgrad; dY^T, X^T per 128x1 for wgrad."""
     from lowbit.backend import HipLowBitBackend
     from lowbit.contracts import LowBitKernelSpec
 
@@ -314,7 +314,7 @@ def test_persistent_nf4_fused_matches_materialized_and_trains(gpu_device):
 
 @pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
 def test_c3_backward_full_size_sampled(gpu_device, rounding):
-    """BASELINE config 3 at full size with the fp8 backward recipe, under
+    """benchmark config 3 at full size with the fp8 backward recipe, under
     round to nearest and under the seeded stochastic rounding the
     configuration names; dgrad and wgrad checked on sampled rows and columns
     against the oracle, each slice quantized with the stochastic-rounding

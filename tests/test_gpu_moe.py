@@ -134,7 +134,7 @@ def test_sort_by_expert_offsets(gpu_device):
 
 
 def test_c4_grouped_up_projection_full_size_sampled(gpu_device):
-    """4096 tokens, top-8 of 32 experts, W_up [2048, 7168]."""
+    """benchmark config 4: 4096 tokens, top-8 of 32 experts, W_up [2048, 7168]."""
     from lowbit import moe, workloads
 
     tokens, routing, w_up, _ = workloads.c4_inputs(device="cpu")

@@ -172,7 +172,7 @@ def test_local_moe_forward_equals_its_composition(gpu_device, fmt):
 
 
 def test_c4_fanout_and_combine_full_size(gpu_device):
-    """4096 tokens, top-8 of 32 experts, hidden 7168."""
+    """benchmark config 4: 4096 tokens, top-8 of 32 experts, hidden 7168."""
     from lowbit import moe, ops, workloads
 
     tokens, routing, _, _ = workloads.c4_inputs(device="cpu", experts=1)

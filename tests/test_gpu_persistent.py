@@ -182,7 +182,7 @@ def test_mxfp4_fused_gemm(gpu_device, M, N, K):
 
 
 def test_c5_nf4_fused_gemm_full_size_sampled(gpu_device):
-    """W [14336, 4096] NF4 (64-element blocks), X [4096, 4096]."""
+    """benchmark config 5: W [14336, 4096] NF4 (64-element blocks), X [4096, 4096]."""
     from lowbit import persistent as P, workloads
 
     x, w = workloads.c5_inputs(device="cpu")
@@ -200,7 +200,7 @@ def test_c5_nf4_fused_gemm_full_size_sampled(gpu_device):
 
 
 def test_c5_mxfp4_fused_gemm_full_size_sampled(gpu_device):
-    """BASELINE config 5 as MXFP4 (32-element blocks, e8m0 scales): W
+    """benchmark config 5 as MXFP4 (32-element blocks, e8m0 scales): W
     [14336, 4096], X [4096, 4096]; codes and scales bit for bit, the fused
     GEMM on sampled rows and columns against the oracle."""
     from lowbit import persistent as P, workloads

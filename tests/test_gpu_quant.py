@@ -166,7 +166,7 @@ def test_dual_1x128_128x1_parity(gpu_device, shape, dtype, fmt, grid, rname, rco
 
 
 def test_c3_dy_128x1_full_size(gpu_device):
-    """dY [8192, 18432] 128x1 tiles (the wgrad operand dY^T)."""
+    """benchmark config 3: dY [8192, 18432] 128x1 tiles (the wgrad operand dY^T)."""
     from lowbit import ops, workloads
 
     dy = workloads.c3_grad(device="cpu")
@@ -179,7 +179,7 @@ def test_c3_dy_128x1_full_size(gpu_device):
 
 @pytest.mark.parametrize("fmt,grid", GRIDS)
 def test_c3_dy_full_size_stochastic_rounding(gpu_device, fmt, grid):
-    """BASELINE config 3 with its seeded stochastic rounding, at full size:
+    """benchmark config 3 with its seeded stochastic rounding, at full size:
     dY [8192, 18432] per 1x128 tile (the dgrad operand) and per 128x1 tile
     (dY^T for wgrad), single passes and the dual pass, codes and scales bit
     for bit against the oracle.  The offsets use the Philox counter's high
@@ -364,7 +364,7 @@ def test_strip_subnormal_amax_rule(gpu_device):
 
 @pytest.mark.parametrize("fmt,grid", GRIDS)
 def test_full_size_c2_activation_and_weight(gpu_device, fmt, grid):
-    """Bit-exact at the DeepSeek-V3 MLP shapes of BASELINE config 2."""
+    """Bit-exact at the DeepSeek-V3 MLP shapes of benchmark config 2."""
     from lowbit import ops
 
     x = seeded((8192, 7168), seed=20260201, heavy_channels=True).to(gpu_device)
