@@ -222,7 +222,7 @@ float ntlo_code_value(uint8_t code, int grid) {
 /* count as zeros (the F.pad of te_backend.py:94-95, :134-135).          */
 /*   tile_1x128     gr = 1,   gc = 128   (te_backend.py:82-110)          */
 /*   block_128x128  gr = 128, gc = 128   (te_backend.py:113-149)         */
-/*   128x1          gr = 128, gc = 1     (BASELINE c3 recipe)            */
+/*   128x1          gr = 128, gc = 1     (benchmark c3 recipe)           */
 /*   tensor         gr = R,   gc = K     (te_backend.py:165-173)         */
 /*   channel ax -1  gr = R,   gc = 1     (te_backend.py:175-185)         */
 /*   channel ax 0   gr = 1,   gc = K                                     */
@@ -344,7 +344,7 @@ int ntlo_nf4_dequant(const uint8_t* packed, const float* scales, int64_t n, int6
 
 /* ------------------------------------------------------------------ */
 /* MXFP4: OCP Microscaling v1.0, e2m1 elements, e8m0 shared scale per  */
-/* 32 elements.  No reference function (BASELINE c5).                   */
+/* 32 elements.  No reference function (benchmark c5).                  */
 /*   X = 2^(floor(log2 amax) - 2), exponent clamped to [-127, 127],     */
 /*   stored biased by 127; a block whose amax is NaN or inf stores the  */
 /*   NaN scale 0xFF and zero codes; an all-zero block stores 2^-127.    */
