@@ -839,25 +839,30 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 
 
 // 128x1 tiles with transposed codes, for 8-aligned K and 16-byte aligned rows.
-// A workgroup covers 128 rows x 128 columns; thread t owns columns
-// cb*128 + 8*(t & 15) + [0, 8) of rows mb*128 + 8*(t >> 4) + [0, 8), read as
-// eight 16-byte row chunks (a wave reads four full 256-byte row segments per
-// load).  Column amax: packed per thread, shuffles across the four row groups
-// of a wave, LDS across the four waves.  Each of the thread's columns then
-// quantizes its 8 consecutive rows as one quant8_tile group (fast division and
-// the hardware e4m3 convert where they apply), whose 8 codes are 8
-// consecutive bytes of the transposed row.  They are staged in LDS and leave
-// as full 128-byte transposed rows, 16 bytes per lane; direct 8-byte stores
-// would scatter 32-byte pieces over 16 rows per instruction.  Staging layout
+// A workgroup covers 128 rows x 8*CW columns (CW = 16 or 32) with 16*CW
+// threads; thread t owns columns cb*8*CW + 8*(t % CW) + [0, 8) of rows
+// mb*128 + 8*(t / CW) + [0, 8), read as eight 16-byte row chunks (a wave reads
+// 64/CW full 16*CW-byte row segments per load).  The single-output pass takes
+// CW = 32 under round to nearest: its 512-byte row segments read faster than
+// 256-byte ones (c3 dY: 83.5 -> 78.0 us; 1024-byte segments, with one
+// 1024-thread workgroup per CU, 106 us).  Column amax: packed per thread, shuffles across the row groups of
+// a wave, LDS across the waves.  Each of the thread's columns then quantizes
+// its 8 consecutive rows as one quant8_tile group (fast division and the
+// hardware e4m3 convert where they apply), whose 8 codes are 8 consecutive
+// bytes of the transposed row.  They are staged in LDS and leave as full
+// 128-byte transposed rows, 16 bytes per lane; direct 8-byte stores would
+// scatter 32-byte pieces over 16 rows per instruction.  Staging layout
 // (128-byte rows, no padding; 64 banks of 4 bytes): transposed row cl sits at
 // row cl ^ ((cl >> 3) & 1) and its 8-byte slot for row group rg at
-// rg ^ 2*((cl >> 4) & 7).  A half-wave's writes (16 columns cl = 8*cc + j of
-// one parity j, 2 row groups) then cover both 128-byte halves of a 256-byte
-// bank window, 16 distinct slots in each: conflict-free.  Each 16-lane phase
-// of the 16-byte reads takes 8 pieces of two adjacent rows, one from each
-// half: conflict-free too.  The per-column arrays (maxima, scales,
-// reciprocals) skip one word after column 63, so that the 16 columns cc*8 + j
-// a wave reads at once fall on 16 banks.  nan_rows, when given, is indexed
+// rg ^ (2*((cl >> 4) & 7) | ((cl >> 7) & 1)).  A 32-lane phase of the 8-byte
+// writes (one column parity j; 16 columns of 2 row groups, or 32 columns of
+// one) then covers both 128-byte halves of a 256-byte bank window, 16
+// distinct slots in each: conflict-free.  16-byte piece k of a row holds row
+// groups 2k and 2k+1, swapped when bit 7 of cl is set.  Each 16-lane phase of
+// the 16-byte reads takes 8 pieces of two adjacent rows, one from each half:
+// conflict-free too.  The per-column arrays (maxima, scales, reciprocals) skip
+// one word after every 64 columns, so that the 16 columns cc*8 + j a
+// half-wave reads at once fall on 16 banks.  nan_rows, when given, is indexed
 // by transposed row (source column).
 //
 // With DUAL the same pass also writes the 1x128 tiles of x, described by ar
@@ -865,26 +870,29 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // thread's chunks is 8 columns of one 1x128 tile, whose other 120 columns are
 // held by the 15 lanes of the same row group, so a 16-lane max gives the tile
 // amax.  One read of dY feeds both the dgrad and the wgrad operands.
-template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false>
-__global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, QuantArgs ar = QuantArgs()) {
+template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false, int CW = 16>
+__global__ void __launch_bounds__(16 * CW) quant_tile_128x1_t_fast(QuantArgs a, QuantArgs ar = QuantArgs()) {
+  static_assert(CW == 16 || (CW == 32 && !DUAL), "128 or 256 columns per workgroup; the dual pass takes 128");
+  constexpr int NCOL = 8 * CW, NW = CW / 4;  // columns and waves of the workgroup
+  constexpr int NPC = NCOL + NCOL / 64;      // per-column array length (pc() skips a word per 64)
   // staged transposed row of column cl, its 8-byte slot for row group rg and
   // its 16-byte piece k; per-column array index of column c
   auto trow = [](int cl) { return cl ^ ((cl >> 3) & 1); };
-  auto tslot = [](int cl, int rg) { return rg ^ (2 * ((cl >> 4) & 7)); };
+  auto tslot = [](int cl, int rg) { return rg ^ ((2 * ((cl >> 4) & 7)) | ((cl >> 7) & 1)); };
   auto tpiece = [](int cl, int k) { return k ^ ((cl >> 4) & 7); };
   auto pc = [](int c) { return c + (c >> 6); };
-  __shared__ uint32_t wmax[4][130];
-  __shared__ uint32_t rmax[128];
+  __shared__ uint32_t wmax[NW][NPC];
+  __shared__ uint32_t rmax[DUAL ? 128 : 1];
   // per column (and, with DUAL, per row tile): amax bits, scale, 1/scale,
   // computed once per workgroup by one thread each
-  __shared__ __attribute__((aligned(16))) uint32_t cm[130];
-  __shared__ __attribute__((aligned(16))) float cs[130], crs[130];
-  __shared__ __attribute__((aligned(16))) uint32_t rm[128];
-  __shared__ __attribute__((aligned(16))) float rs_[128], rrs[128];
-  __shared__ __attribute__((aligned(16))) uint8_t tcodes[128 * 128];
+  __shared__ __attribute__((aligned(16))) uint32_t cm[NPC];
+  __shared__ __attribute__((aligned(16))) float cs[NPC], crs[NPC];
+  __shared__ __attribute__((aligned(16))) uint32_t rm[DUAL ? 128 : 1];
+  __shared__ __attribute__((aligned(16))) float rs_[DUAL ? 128 : 1], rrs[DUAL ? 128 : 1];
+  __shared__ __attribute__((aligned(16))) uint8_t tcodes[NCOL * 128];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cc = tid & 15, rg = tid >> 4;
-  const int64_t n_cb = (a.K + 127) / 128;
+  const int cc = tid & (CW - 1), rg = tid / CW;
+  const int64_t n_cb = (a.K + NCOL - 1) / NCOL;
   // workgroup pid takes column block pid % n_cb of row block
   // (pid / n_cb + 7 * column block) mod n_mb: consecutive workgroups walk the
   // column blocks, and the skew spreads the row blocks that run at one time
@@ -895,7 +903,7 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
   const int64_t n_mb = (a.R + 127) / 128;
   const int64_t q = (int64_t)blockIdx.x / n_cb, cb = (int64_t)blockIdx.x - q * n_cb;
   const int64_t mb = DUAL ? q : (q + 7 * cb) % n_mb;
-  const int64_t col0 = cb * 128 + cc * 8;
+  const int64_t col0 = cb * NCOL + cc * 8;
   const int64_t row0 = mb * 128 + rg * 8;
   const bool col_in = col0 < a.K;  // K % 8 == 0: a chunk is wholly in or out
 
@@ -904,8 +912,8 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
   for (int i = 0; i < 8; ++i) chunk_load<IN_DT>(c[i], a.x, (row0 + i) * a.ldx + col0, col_in && row0 + i < a.R);
 
   // column |x| maxima as fp32 bit patterns (NaN above every finite value):
-  // per thread, then across the four row groups of the wave, then (in LDS)
-  // across the four waves
+  // per thread, then across the row groups of the wave, then (in LDS) across
+  // the waves
   if constexpr (IN_DT == DT_F32) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -916,9 +924,9 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
         const uint32_t b = (j & 3) == 0 ? w.x : (j & 3) == 1 ? w.y : (j & 3) == 2 ? w.z : w.w;
         mm = max(mm, b & 0x7FFFFFFFu);
       }
-      mm = max(mm, (uint32_t)__shfl_xor((int)mm, 16));
+      if constexpr (CW == 16) mm = max(mm, (uint32_t)__shfl_xor((int)mm, 16));
       mm = max(mm, (uint32_t)__shfl_xor((int)mm, 32));
-      if (lane < 16) wmax[wave][pc(cc * 8 + j)] = mm;
+      if (lane < CW) wmax[wave][pc(cc * 8 + j)] = mm;
     }
   } else {
     uint32_t m2[4] = {0, 0, 0, 0};
@@ -931,9 +939,9 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 16));
+      if constexpr (CW == 16) m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 16));
       m2[k] = pk_max_u16(m2[k], (uint32_t)__shfl_xor((int)m2[k], 32));
-      if (lane < 16) {
+      if (lane < CW) {
         wmax[wave][pc(cc * 8 + 2 * k)] = m2[k] << 16;
         wmax[wave][pc(cc * 8 + 2 * k + 1)] = m2[k] & 0xFFFF0000u;
       }
@@ -949,9 +957,11 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
     }
   }
   __syncthreads();
-  if (tid < 128) {
+  if (tid < NCOL) {
     const int c = pc(tid);
-    const uint32_t mm = max(max(wmax[0][c], wmax[1][c]), max(wmax[2][c], wmax[3][c]));
+    uint32_t mm = wmax[0][c];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mm = max(mm, wmax[w][c]);
     const float sc = scale_from_amax_bits(mm, a.qmaxf, a.scale_rule);
     cm[c] = mm;
     cs[c] = sc;
@@ -1051,14 +1061,15 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_fast(QuantArgs a, Quan
   }
   }
   __syncthreads();
-  // 128 transposed rows of 128 bytes (rows past R hold zero codes, inside ldct)
+  // NCOL transposed rows of 128 bytes (rows past R hold zero codes, inside ldct)
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const int qi = p * 256 + tid;
+    const int qi = p * 16 * CW + tid;
     const int cl = qi >> 3, k = qi & 7;
-    const int64_t col = cb * 128 + cl;
+    const int64_t col = cb * NCOL + cl;
     if (col < a.K) {
-      const uint4 v = *reinterpret_cast<const uint4*>(tcodes + trow(cl) * 128 + tpiece(cl, k) * 16);
+      uint4 v = *reinterpret_cast<const uint4*>(tcodes + trow(cl) * 128 + tpiece(cl, k) * 16);
+      if (CW > 16 && (cl & 128)) v = make_uint4(v.z, v.w, v.x, v.y);  // row groups 2k, 2k+1 in order
       // the single-output pass stores its transposed rows with the
       // non-temporal hint (c3 dY: 100 -> 88 us); the dual pass, which also
       // writes the 1x128 codes, measured slower with it (128 -> 136 us)
@@ -1622,18 +1633,29 @@ extern "C" int ntlb_quant_tile_128x1_t(const void* x, int x_dtype, int64_t R, in
   hipStream_t st = as_stream(stream);
   if (K % 8 == 0 && ldx % 8 == 0 && aligned(x, 16) && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) &&
       cdiv(R, 128) * cdiv(K, 128) <= 0x7FFFFFFF) {
-    dim3 grd((unsigned)(cdiv(R, 128) * cdiv(K, 128))), blk(256);
+    // round to nearest: 256-column workgroups (CW = 32); stochastic
+    // rounding, whose Philox work makes it VALU-bound, keeps 128 columns
+    // (CW = 16), since at 512 threads its register use allows one workgroup
+    // per CU (c3 dY: 156 -> 222 us)
+    const int cw = sr ? 16 : 32;
+    dim3 grd((unsigned)(cdiv(R, 128) * cdiv(K, 8 * cw))), blk(16 * cw);
+#define NTLB_T128(DT_, DQ_)                                                                      \
+  do {                                                                                           \
+    if constexpr (S_) quant_tile_128x1_t_fast<DT_, G_, S_, DQ_, false, 16><<<grd, blk, 0, st>>>(a); \
+    else quant_tile_128x1_t_fast<DT_, G_, S_, DQ_, false, 32><<<grd, blk, 0, st>>>(a);              \
+  } while (0)
     if (x_dtype == NTLB_BF16) {
       NTLB_DISPATCH_GRID_SR(grid, sr, {
-        if (dq) quant_tile_128x1_t_fast<DT_BF16, G_, S_, true><<<grd, blk, 0, st>>>(a);
-        else quant_tile_128x1_t_fast<DT_BF16, G_, S_, false><<<grd, blk, 0, st>>>(a);
+        if (dq) NTLB_T128(DT_BF16, true);
+        else NTLB_T128(DT_BF16, false);
       });
     } else {
       NTLB_DISPATCH_GRID_SR(grid, sr, {
-        if (dq) quant_tile_128x1_t_fast<DT_F32, G_, S_, true><<<grd, blk, 0, st>>>(a);
-        else quant_tile_128x1_t_fast<DT_F32, G_, S_, false><<<grd, blk, 0, st>>>(a);
+        if (dq) NTLB_T128(DT_F32, true);
+        else NTLB_T128(DT_F32, false);
       });
     }
+#undef NTLB_T128
     return check_launch(fn);
   }
   dim3 grd((unsigned)(MB * CB)), blk(256);
