@@ -753,26 +753,39 @@ __global__ void scales_from_amax_kernel(const uint32_t* amax_bits, int64_t n, fl
 }
 
 template <int IN_DT, int GRID, bool SR, bool VEC>
+// Thread (x, t) owns the 8-column chunk blockIdx.x*256 + t of rows
+// blockIdx.y, blockIdx.y + gridDim.y, ..., as the comm-quant pass: column
+// groups fixed per thread, one 32-bit division per row for the row group, and
+// the chunk's scales read again only when the row group changes.
 __global__ void __launch_bounds__(256) quant_grouped_kernel(QuantArgs a, int64_t gr, int64_t gc, int64_t n_gc) {
   const int64_t chunks_per_row = (a.K + 7) >> 3;
-  const int64_t total = a.R * chunks_per_row;
-  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
-    int64_t r = c / chunks_per_row;
-    int64_t k0 = (c - r * chunks_per_row) * 8;
+  const int64_t kc = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (kc >= chunks_per_row) return;
+  const int64_t k0 = kc * 8;
+  int kg[8];  // the host keeps n_gc below 2^31
+#pragma unroll
+  for (int i = 0; i < 8; ++i) kg[i] = (int)min<int64_t>(gc == 1 ? k0 + i : (k0 + i) / gc, n_gc - 1);
+  const uint32_t gr32 = (uint32_t)gr;
+  uint32_t gcur = 0xFFFFFFFFu;
+  float sv[8];
+  for (int64_t r = blockIdx.y; r < a.R; r += gridDim.y) {
     float v[8];
     load8<IN_DT, VEC>(a.x, r * a.ldx, k0, a.K, v);
     uint32_t rb[8];
     sr_words<SR>((uint64_t)(r * a.K + k0), a.seed, a.offset, rb);
-    // scale index: one division per chunk when its 8 columns share a group
-    const float* srow = a.scales + (r / gr) * n_gc;
-    const float s0 = gc % 8 == 0 ? srow[k0 / gc] : 0.0f;
+    const uint32_t g = (uint32_t)r / gr32;
+    if (g != gcur) {
+      gcur = g;
+      const float* srow = a.scales + (int64_t)g * n_gc;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) sv[i] = (k0 + i < a.K) ? srow[kg[i]] : 1.0f;
+    }
     uint32_t cb[8];
-    float q[8], sv[8];
+    float q[8];
     bool nan = false;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       int64_t k = k0 + i;
-      sv[i] = (k < a.K) ? (gc % 8 == 0 ? s0 : srow[gc == 1 ? k : k / gc]) : 1.0f;
       cb[i] = (k < a.K) ? quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]) : 0u;
       if (k < a.K) nan |= (__float_as_uint(q[i]) & 0x7FFFFFFFu) > 0x7F800000u;
     }
@@ -1578,7 +1591,13 @@ static int quant_grouped_launch(const char* fn, const void* x, int x_dtype, int6
   int rc = check_launch(fn);
   if (rc) return rc;
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
-  dim3 grd(grid_for(R * cdiv(K, 8), 256, 256 * 16)), blk(256);
+  if (R >= ((int64_t)1 << 31) || n_gc >= ((int64_t)1 << 31))
+    return fail(NTLB_EUNSUPPORTED, "%s: 2^31 or more rows or column groups", fn);
+  if (gr > R) gr = R;  // one row group either way; the kernel divides in 32 bits
+  const int64_t gx = cdiv(cdiv(K, 8), 256);
+  if (gx > 0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: rows too long", fn);
+  dim3 grd((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(R, std::min<int64_t>(65535, 4096 / gx)))),
+      blk(256);
   // vector loads and 8-byte code stores where rows and pitches allow
   const bool vec = K % 8 == 0 && ldx % 8 == 0 && ldc % 8 == 0 && aligned(x, 16) && aligned(codes, 8);
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
