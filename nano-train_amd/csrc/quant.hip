@@ -1502,8 +1502,11 @@ static int amax_grouped_launch(const char* fn, const void* x, int x_dtype, int64
                                int64_t gr, int64_t gc, uint32_t* amax_bits, hipStream_t st) {
   const int64_t n_gc = cdiv(K, gc);
   const int64_t col_blocks = cdiv(cdiv(K, 8), 256);
-  // rows per workgroup: enough to amortize the atomics, enough groups to fill the GPU
-  int64_t rpb = cdiv(R, cdiv(2048, col_blocks));
+  // rows per workgroup: enough to amortize the atomics, enough groups to fill
+  // the GPU.  About 1024 workgroups (c4 payload with the straight-through
+  // pass: strip groups 282 us, channel groups 373; 2048: 283 and 416; 512:
+  // 336 and 411; 8192: 285 and 610)
+  int64_t rpb = cdiv(R, cdiv(1024, col_blocks));
   if (rpb < 16) rpb = 16;
   const int64_t row_blocks = cdiv(R, rpb);
   if (row_blocks > 65535 || col_blocks > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: shape too large", fn);
