@@ -1551,10 +1551,13 @@ extern "C" int ntlb_comm_quant_dequant(const void* x, int x_dtype, int64_t R, in
   if (R >= ((int64_t)1 << 31) || n_gc >= ((int64_t)1 << 31))
     return fail(NTLB_EUNSUPPORTED, "%s: 2^31 or more rows or column groups", fn);
   if (gr > R) gr = R;
-  // x: 256 chunks of 8 columns per workgroup; y: rows, strided
+  // x: 256 chunks of 8 columns per workgroup; y: rows, strided; about 8192
+  // workgroups (c4 payload with the amax pass, strip groups: 271-277 us;
+  // 4096: 282-289, 2048: 290-296, 16384: 265-273 but channel groups 381-384
+  // against 368-370)
   const int64_t gx = cdiv(cdiv(K, 8), 256);
   if (gx > 0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: rows too long", fn);
-  dim3 grd((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(R, std::min<int64_t>(65535, 4096 / gx)))),
+  dim3 grd((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(R, std::min<int64_t>(65535, 8192 / gx)))),
       blk(256);
   hipStream_t st = as_stream(stream);
   NTLB_DISPATCH_DT(x_dtype, NTLB_DISPATCH_GRID_SR(grid, sr, {
