@@ -48,6 +48,37 @@ def test_nf4_special_values_and_ties(gpu_device):
     assert_bits_equal(scale.reshape(-1).cpu().numpy(), s_ref, "nf4 scale")
 
 
+def test_nf4_index_around_every_bracket_edge(gpu_device):
+    """Every codebook entry and every midpoint between neighbours, and the 64
+    floats on each side of each, with a unit scale (the tensor holds 1.0), so
+    the kernel's codebook search meets each bracket boundary and each
+    distance tie at float resolution; codes against the oracle's argmin."""
+    from lowbit import persistent as P
+
+    cb = O.NF4_CODEBOOK.astype(np.float32)
+    edges = list(cb) + [(cb[i] + cb[i + 1]) / np.float32(2) for i in range(15)]
+    vals = [np.float32(1.0)]
+    for e in edges:
+        up = dn = np.float32(e)
+        vals.append(up)
+        for _ in range(64):
+            up = np.nextafter(up, np.float32(2))
+            dn = np.nextafter(dn, np.float32(-2))
+            vals += [up, dn]
+    w = torch.from_numpy(np.clip(np.array(vals, dtype=np.float32), -1, 1)).to(gpu_device)
+    packed, scale = P.quantize_nf4_persistent(w, granularity="per_tensor")
+    p_ref, s_ref = O.nf4_quant(to_np32(w), w.numel())
+    assert float(s_ref.reshape(-1)[0]) == 1.0
+    assert_bits_equal(packed.cpu().numpy(), p_ref, "nf4 packed")
+    # the 64-element block quantizer shares the search
+    wb = torch.nn.functional.pad(w, (0, (-w.numel()) % 64))
+    wb[::64] = 1.0
+    pb, sb = P.quantize_nf4_blocks(wb, 64)
+    pb_ref, sb_ref = O.nf4_quant(to_np32(wb), 64)
+    assert_bits_equal(pb.cpu().numpy(), pb_ref, "nf4 blocks packed")
+    assert_bits_equal(sb.reshape(-1).cpu().numpy(), sb_ref, "nf4 blocks scales")
+
+
 @pytest.mark.parametrize("shape", [(64, 128), (129, 256), (8, 96)])
 @pytest.mark.parametrize("granularity", ["per_channel", "per_tensor"])
 def test_fp8_persistent_parity(gpu_device, shape, granularity):
