@@ -375,8 +375,9 @@ def test_mxfp4_fused_gemm_dequant_exact_all_codes(gpu_device):
     np.testing.assert_array_equal(got[keep], want[keep])
 
 
-@pytest.mark.parametrize("fmt", ["nf4", "mxfp4", "fp8p"])
-@pytest.mark.parametrize("block", [64, 96, 0])
+# MXFP4 blocks are always 32 elements: its one size is the 64-weight case
+@pytest.mark.parametrize("fmt,block", [("nf4", 64), ("nf4", 96), ("nf4", 0), ("mxfp4", 64), ("fp8p", 64),
+                                       ("fp8p", 96), ("fp8p", 0)])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_dequant_vector_path_matches_elementwise_and_oracle(gpu_device, fmt, block, out_dtype):
     """The 16-weights-per-thread dequant (aligned output, n and block multiples
@@ -386,8 +387,6 @@ def test_dequant_vector_path_matches_elementwise_and_oracle(gpu_device, fmt, blo
     non-power-of-two block (96) and a tensor-wide one (0 = n)."""
     from lowbit import _lib, ops
 
-    if fmt == "mxfp4" and block != 64:
-        pytest.skip("MXFP4 blocks are always 32 elements")
     # whole scale blocks (and whole 32-element MXFP4 blocks), as a weight of K % block == 0 has
     n = {64: 64 * 1025, 96: 96 * 683, 0: 16 * 4099}[block]
     blk = n if block == 0 else block
