@@ -665,7 +665,8 @@ __device__ __forceinline__ void round8_dtype(float (&v)[8]) {
 // scales are looked up again only when the row group changes.  A grid-stride
 // walk over flat chunk indices paid three 64-bit divisions and a scale lookup
 // per chunk and was VALU-bound (c4 payload, strip groups: 240 us at 98% VALU
-// busy; with the amax pass, 337 -> 288 us, and channel groups 651 -> 406 us).
+// busy; with the amax pass and the workgroup counts below, 337 -> 274 us, and
+// channel groups 651 -> 370 us).
 template <int IN_DT, int GRID, bool SR, bool VEC>
 __global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const uint32_t* amax_bits, int64_t gr,
                                                              int64_t gc, int64_t n_gc, void* out, int64_t ldo) {
