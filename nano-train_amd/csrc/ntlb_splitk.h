@@ -73,10 +73,22 @@ struct SplitWork {
   int chunk;  // K range index within the tile
 };
 
+// Workgroup pid runs on XCD pid % 8.  When base % 8 == 0, tail unit q runs
+// on XCD q % 8 too, and q is renumbered so that each XCD walks a contiguous
+// range of tail units: the chunks of one tail tile and the tiles next to it in
+// the raster then share that XCD's L2 (c3 dgrad: 2278 -> 2316 TFLOP/s).  The
+// renumbering only moves units between workgroups: every tile's chunks, and
+// the order they are summed in, stay the same.
 __device__ __forceinline__ SplitWork split_work(int pid, int base, int s) {
   SplitWork w{pid, -1, 0};
   if (s > 1 && pid >= base) {
-    const int q = pid - base;
+    int q = pid - base;
+    if ((base & 7) == 0) {
+      const int n = (int)gridDim.x - base;
+      const int xcd = q & 7, local = q >> 3;
+      const int per = n >> 3, extra = n & 7;
+      q = xcd * per + min(xcd, extra) + local;
+    }
     w.tail = q / s;
     w.chunk = q - w.tail * s;
     w.pid = base + w.tail;
