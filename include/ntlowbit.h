@@ -300,6 +300,22 @@ int ntlb_gemm_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, i
                         int64_t ldw, const float* sw, int64_t sw_row, int64_t sw_col, int w_shift, int64_t K, void* dx,
                         int dx_dtype, int64_t lddx, void* stream);
 
+/* ntlb_gemm_ste_dgrad with a split-K workspace (same interface as
+ * ntlb_gemm_blockscaled_ws's): the output tiles past the last whole wave of
+ * workgroups run as K ranges whose fp32 partials are summed in range order.
+ * The workspace is 256-byte aligned, zeroed before its first use and left
+ * zeroed; ws_bytes >= ntlb_gemm_dq_workspace_bytes(op_dtype, M, K, N), else
+ * (or with NULL) the call runs unsplit.  Same autograd of te_backend.py:250-259. */
+int ntlb_gemm_ste_dgrad_ws(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
+                           const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_row, int64_t sw_col, int w_shift,
+                           int64_t K, void* dx, int dx_dtype, int64_t lddx, void* workspace, int64_t ws_bytes,
+                           void* stream);
+
+/* Split-K workspace bytes of a dequantized-operand GEMM with an [M, N] output
+ * and contraction Kc (0: the shape runs unsplit).  No counterpart in the
+ * reference: the workspace serves ntlb_gemm_ste_dgrad_ws. */
+int64_t ntlb_gemm_dq_workspace_bytes(int op_dtype, int64_t M, int64_t N, int64_t Kc);
+
 /* Weight gradient of the straight-through estimator: dW[N, K] =
  * dY[M, N]^T . bf16(dq(X))[M, K], fp32 accumulation over the M tokens, cast
  * to dw_dtype.  dY bf16 [M, N] (lddy % 8 == 0) and X's codes [M, ldx] are both

@@ -44,6 +44,7 @@
 
 #include "ntlb_device.h"
 #include "ntlb_host.h"
+#include "ntlb_splitk.h"
 
 namespace ntlb {
 namespace gdq {
@@ -140,6 +141,12 @@ struct DqArgs {
   int y_dtype;
   int64_t ldy;
   int vec_out;
+  // split-K tail (the blockwise GEMM's scheme): workgroups at or past
+  // split_base take one of split_s K ranges of a tail tile; the last range to
+  // finish sums the fp32 partials in range order and stores the tile
+  int split_base, split_s;
+  float* ws;
+  uint32_t* ws_count;
 };
 
 // 4 codes (byte i = element i) times s in fp32: the reference's q * scale
@@ -407,13 +414,15 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
 
-  // workgroup -> tile: each XCD walks a contiguous range of tiles, grouped
-  // raster of GROUP_M row tiles
+  // workgroup -> tile: each XCD walks a contiguous range of the whole tiles,
+  // grouped raster of GROUP_M row tiles; the split tail's ranges keep their
+  // tile
   const int num_n = (int)((g.N + TN - 1) / TN);
   const int num_m = (int)((g.M + TM - 1) / TM);
-  const int nwg = num_m * num_n;
-  int pid = blockIdx.x;
-  {
+  const SplitWork sw = split_work(blockIdx.x, g.split_base, g.split_s);
+  int pid = sw.pid;
+  if (sw.tail < 0) {
+    const int nwg = g.split_s > 1 ? g.split_base : num_m * num_n;
     const int xcd = pid & 7, local = pid >> 3;
     const int per = nwg >> 3, extra = nwg & 7;
     pid = xcd * per + min(xcd, extra) + local;
@@ -435,6 +444,9 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   sb.init(g.b, n0, tid, lane);
 
   const int nk = (int)(g.Kc / ElemT<EL>::kstep);
+  // K steps [kb0, kb1) of this workgroup: all of them, or one split range
+  const int kb0 = sw.tail >= 0 ? (int)((int64_t)sw.chunk * nk / g.split_s) : 0;
+  const int kb1 = sw.tail >= 0 ? (int)((int64_t)(sw.chunk + 1) * nk / g.split_s) : nk;
   // the epilogue's arguments, kept in scalar registers through the K loop
   uintptr_t e_y = reinterpret_cast<uintptr_t>(g.y), e_bias = reinterpret_cast<uintptr_t>(g.bias);
   int64_t e_ldy = g.ldy, e_M = g.M, e_N = g.N;
@@ -450,20 +462,20 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  // prologue: block 0 into stage 0, block 1's raw data into registers
+  // prologue: block kb0 into stage 0, block kb0+1's raw data into registers
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if constexpr (SA == SRC_DIRECT) da.issue(la0, 0, wave, j);
-    if constexpr (SB == SRC_DIRECT) db.issue(lb0, 0, wave, j);
+    if constexpr (SA == SRC_DIRECT) da.issue(la0, kb0, wave, j);
+    if constexpr (SB == SRC_DIRECT) db.issue(lb0, kb0, wave, j);
   }
-  sa.load(g.a, 0);
-  sb.load(g.b, 0);
+  sa.load(g.a, kb0);
+  sb.load(g.b, kb0);
   sa.template decode_half<0>(g.a, la0);
   sb.template decode_half<0>(g.b, lb0);
   sa.template decode_half<1>(g.a, la0);
   sb.template decode_half<1>(g.b, lb0);
-  sa.load(g.a, min(1, nk - 1));
-  sb.load(g.b, min(1, nk - 1));
+  sa.load(g.a, min(kb0 + 1, kb1 - 1));
+  sb.load(g.b, min(kb0 + 1, kb1 - 1));
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -476,7 +488,7 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     const uint8_t* tb = BUF ? lb1 : lb0;
     uint8_t* na = BUF ? la0 : la1;
     uint8_t* nb = BUF ? lb0 : lb1;
-    const int kn = min(kt + 1, nk - 1);
+    const int kn = min(kt + 1, kb1 - 1);
     v8i bf[4];
 #pragma unroll
     for (int tn = 0; tn < 4; ++tn) bf[tn] = frag(tb, wn * 64 + tn * 16, lane);
@@ -505,16 +517,19 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     // every copy of this step has landed (vmcnt(0)); then block kt+2's raw
     // data goes out and stays in flight across the barrier
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    sa.load(g.a, min(kt + 2, nk - 1));
-    sb.load(g.b, min(kt + 2, nk - 1));
+    sa.load(g.a, min(kt + 2, kb1 - 1));
+    sb.load(g.b, min(kt + 2, kb1 - 1));
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the decode's LDS writes are done
     __syncthreads();
   };
 
-  for (int kt = 0; kt < nk; kt += 2) {
+  for (int kt = kb0; kt < kb1; kt += 2) {
     step(std::integral_constant<int, 0>(), kt);
-    if (kt + 1 < nk) step(std::integral_constant<int, 1>(), kt + 1);
+    if (kt + 1 < kb1) step(std::integral_constant<int, 1>(), kt + 1);
   }
+  // a split range: the last one to arrive sums all of them in range order
+  // and stores the tile
+  if (sw.tail >= 0 && !split_exchange(acc, g.ws, g.ws_count, sw.tail, g.split_s, sw.chunk, tid)) return;
 
   // ---------------------------------------------------------------- epilogue
   int64_t m0e = uniform64(m0), n0e = uniform64(n0);
@@ -680,7 +695,8 @@ namespace {
 template <int EL, int SA, int SB, int GRID, int SCM = SC_SHARED>
 void launch(const DqArgs& g, hipStream_t st) {
   const int64_t tiles = ((g.M + TM - 1) / TM) * ((g.N + TN - 1) / TN);
-  gemm_dq_kernel<EL, SA, SB, GRID, SCM><<<dim3((unsigned)tiles), dim3(NT), 0, st>>>(g);
+  const int64_t wgs = g.split_s > 1 ? (int64_t)g.split_base + (tiles - g.split_base) * g.split_s : tiles;
+  gemm_dq_kernel<EL, SA, SB, GRID, SCM><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
 }
 
 // the source combinations this library instantiates
@@ -741,11 +757,31 @@ int check_codes(const char* fn, const char* what, const uint8_t* codes, int64_t 
   return NTLB_OK;
 }
 
-int finish(const char* fn, DqArgs& g, int el, int sa, int sb, int y_dtype, int64_t ldy, void* stream) {
+// the split-K tail's minimum K steps per range, as for the blockwise GEMM
+// (a K step here is 128 bytes per row, the MFMA work of one of its blocks)
+constexpr int DQ_SPLIT_MIN_STEPS = 9;
+
+SplitPlan dq_plan(int64_t M, int64_t N, int64_t Kc, int el) {
+  const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  return split_plan(tiles, (int)(Kc / (el == EL_BF16 ? 64 : 32)), DQ_SPLIT_MIN_STEPS);
+}
+
+int finish(const char* fn, DqArgs& g, int el, int sa, int sb, int y_dtype, int64_t ldy, void* stream,
+           void* workspace = nullptr, int64_t ws_bytes = 0) {
   if (!valid_dtype(y_dtype) || ldy < g.N) return fail(NTLB_EINVAL, "%s: bad output dtype or ld", fn);
   if (g.bias && !valid_dtype(g.bias_dtype)) return fail(NTLB_EINVAL, "%s: bad bias dtype", fn);
   const int64_t tiles = ((g.M + TM - 1) / TM) * ((g.N + TN - 1) / TN);
   if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  g.split_base = (int)tiles; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
+  if (workspace) {
+    if (!aligned(workspace, 256)) return fail(NTLB_EINVAL, "%s: workspace must be 256-byte aligned", fn);
+    const SplitPlan plan = dq_plan(g.M, g.N, g.Kc, el);
+    if (plan.s > 1 && ws_bytes >= split_ws_bytes(plan)) {
+      g.split_base = plan.base; g.split_s = plan.s;
+      g.ws_count = reinterpret_cast<uint32_t*>(workspace);
+      g.ws = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + split_count_bytes());
+    }
+  }
   g.y_dtype = y_dtype;
   g.ldy = ldy;
   g.vec_out = aligned(g.y, 16) && ((ldy * dtype_size(y_dtype)) % 16 == 0);
@@ -796,9 +832,19 @@ extern "C" int ntlb_gemm_dq_forward(int op_dtype, int grid, const uint8_t* a, in
   return finish(fn, g, el, SRC_CODES, SRC_CODES, y_dtype, ldy, stream);
 }
 
-extern "C" int ntlb_gemm_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
-                                   const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_row, int64_t sw_col,
-                                   int w_shift, int64_t K, void* dx, int dx_dtype, int64_t lddx, void* stream) {
+extern "C" int64_t ntlb_gemm_dq_workspace_bytes(int op_dtype, int64_t M, int64_t N, int64_t Kc) {
+  if (M <= 0 || N <= 0 || Kc <= 0) return 0;
+  const int el = op_dtype == NTLB_F32 ? EL_F32 : EL_BF16;
+  const int64_t kstep = el == EL_BF16 ? 64 : 32;
+  const int64_t tiles = ((M + TM - 1) / TM) * ((N + TN - 1) / TN);
+  if (tiles > 0x7FFFFFFF) return 0;
+  return split_ws_bytes(dq_plan(M, N, (Kc + kstep - 1) / kstep * kstep, el));
+}
+
+extern "C" int ntlb_gemm_ste_dgrad_ws(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
+                                      const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_row, int64_t sw_col,
+                                      int w_shift, int64_t K, void* dx, int dx_dtype, int64_t lddx, void* workspace,
+                                      int64_t ws_bytes, void* stream) {
   const char* fn = "ntlb_gemm_ste_dgrad";
   int el;
   if (int rc = elem_of(op_dtype, fn, el)) return rc;
@@ -823,7 +869,14 @@ extern "C" int ntlb_gemm_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, i
   if (int rc = tcodes_scales(fn, g.b)) return rc;
   g.M = M; g.N = K; g.Kc = Nc;
   g.bias = nullptr; g.bias_dtype = 0; g.y = dx;
-  return finish(fn, g, el, SRC_DIRECT, SRC_TCODES, dx_dtype, lddx, stream);
+  return finish(fn, g, el, SRC_DIRECT, SRC_TCODES, dx_dtype, lddx, stream, workspace, ws_bytes);
+}
+
+extern "C" int ntlb_gemm_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
+                                   const uint8_t* w, int64_t ldw, const float* sw, int64_t sw_row, int64_t sw_col,
+                                   int w_shift, int64_t K, void* dx, int dx_dtype, int64_t lddx, void* stream) {
+  return ntlb_gemm_ste_dgrad_ws(op_dtype, dy, lddy, M, N, grid, w, ldw, sw, sw_row, sw_col, w_shift, K, dx, dx_dtype,
+                                lddx, nullptr, 0, stream);
 }
 
 extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,

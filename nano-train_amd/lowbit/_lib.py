@@ -78,6 +78,9 @@ SIGNATURES = {
     "ntlb_gemm_dq_forward": [_I32, _I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64,
                              _I64, _P, _I32, _P, _I32, _I64, _P],
     "ntlb_gemm_ste_dgrad": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_ste_dgrad_ws": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64,
+                               _P, _I64, _P],
+    "ntlb_gemm_dq_workspace_bytes": [_I32, _I64, _I64, _I64],
     "ntlb_gemm_ste_wgrad": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_dense": [_I32, _P, _I64, _I32, _P, _I64, _I32, _I64, _I64, _I64, _P, _I32, _P, _I32, _I64, _P],
     "ntlb_gemm_dense_tn": [_I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
@@ -102,7 +105,7 @@ SIGNATURES = {
 
 # entry points that return a value instead of a status
 RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64, "ntlb_colsum_workspace_bytes": _I64,
-            "ntlb_gemm_lowbit_workspace_bytes": _I64}
+            "ntlb_gemm_lowbit_workspace_bytes": _I64, "ntlb_gemm_dq_workspace_bytes": _I64}
 
 _lib = None
 _lock = threading.Lock()

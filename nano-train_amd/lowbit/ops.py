@@ -606,9 +606,11 @@ def ste_dgrad(dy: torch.Tensor, w: QTensor, *, out_dtype: torch.dtype) -> torch.
         raise ValueError(f"dY has {N} columns, the weight {w.rows} rows")
     dyp = _pad_cols(dy, 64)
     out = torch.empty((M, w.K), dtype=out_dtype, device=dy.device)
-    call("ntlb_gemm_ste_dgrad", _lib.BF16, dyp.data_ptr(), dyp.stride(0), M, N, w.grid, w.codes.data_ptr(),
+    # the tiles past the last whole wave run as summed K ranges (split-K tail)
+    ws = split_workspace(int(_lib.lib().ntlb_gemm_dq_workspace_bytes(_lib.BF16, M, w.K, N)), dy.device)
+    call("ntlb_gemm_ste_dgrad_ws", _lib.BF16, dyp.data_ptr(), dyp.stride(0), M, N, w.grid, w.codes.data_ptr(),
          w.codes.stride(0), w.scales.data_ptr(), w.s_row, w.s_col, w.shift, w.K, out.data_ptr(),
-         _dtype_code(out_dtype), out.stride(0), _stream())
+         _dtype_code(out_dtype), out.stride(0), _ptr(ws), ws.numel() if ws is not None else 0, _stream())
     return out
 
 

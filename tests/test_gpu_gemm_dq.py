@@ -293,3 +293,42 @@ def test_ste_backward_c3_full_size_sampled(gpu_device):
     xd = O.round_bf16(O.quant_tile_1x128(x.float().numpy(), grid=O.GRID_E4M3)[3])
     e2 = rel_fro_bf16(dw[ncols][:, kcols], dyn[:, ncols].T.astype(np.float64) @ xd[:, kcols].astype(np.float64))
     assert e1 <= 1e-3 and e2 <= 1e-3, (e1, e2)
+
+
+@pytest.mark.parametrize("fmt", list(GRIDS))
+def test_ste_dgrad_split_tail_matches_unsplit(gpu_device, fmt):
+    """dX [8192, 2304] (288 output tiles: one whole wave of 256 compute units
+    plus a 32-tile tail) with the split-K workspace: the tail tiles' K ranges
+    summed in a fixed order equal the unsplit product up to fp32 summation
+    order and repeat bit for bit; a NaN code's column stays NaN through the
+    split.  (The oracle bar itself is checked by the tests above.)"""
+    ops = _ops()
+    from lowbit import _lib
+    from lowbit._lib import call
+
+    M, N, K = 8192, 4096, 2304  # contraction 4096: 64 K steps, split seven ways
+    tiles = (M // 256) * (K // 256)
+    assert int(_lib.lib().ntlb_gemm_dq_workspace_bytes(_lib.BF16, M, K, N)) > 0, "the shape should split"
+    w = seeded((N, K), seed=20262051, std=0.02)
+    if fmt == "int_grid":
+        w[3, 2300] = float("nan")  # a column of the last (split) tile column
+    qw, _ = ops.quant_block_128x128(w.to(gpu_device), fmt=fmt)
+    dy = seeded((M, N), seed=20262052, std=1e-3).to(gpu_device)
+    dx = ops.ste_dgrad(dy, qw, out_dtype=torch.float32)
+    dx2 = ops.ste_dgrad(dy, qw, out_dtype=torch.float32)
+    ref = torch.empty_like(dx)
+    call("ntlb_gemm_ste_dgrad", _lib.BF16, dy.data_ptr(), dy.stride(0), M, N, qw.grid, qw.codes.data_ptr(),
+         qw.codes.stride(0), qw.scales.data_ptr(), qw.s_row, qw.s_col, qw.shift, qw.K, ref.data_ptr(),
+         ops._dtype_code(torch.float32), ref.stride(0), ops._stream())
+    torch.cuda.synchronize()
+    assert tiles == 288
+    assert torch.equal(dx.view(torch.int32), dx2.view(torch.int32)), "split results must repeat bit for bit"
+    nan = torch.isnan(ref)
+    assert torch.equal(nan, torch.isnan(dx))
+    if fmt == "int_grid":
+        assert nan[:, 2300].all() and nan.any(0).sum() == 1
+    a, b = dx[~nan].double(), ref[~nan].double()
+    assert float((a - b).norm() / b.norm()) <= 1e-6
+    # the tail tiles lie in row tiles 28-31 (the last group of the grouped
+    # raster); every tile above them runs whole in both calls, bit for bit
+    assert torch.equal(dx[:7168].view(torch.int32), ref[:7168].view(torch.int32))
