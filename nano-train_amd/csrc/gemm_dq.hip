@@ -643,7 +643,27 @@ __global__ void __launch_bounds__(256) colsum_partial_kernel(const void* x, int6
   float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   constexpr int esz = IN_DT == DT_F32 ? 4 : 2;
   const bool vec = n + 8 <= N && ((uintptr_t)x % 16 == 0) && ((ld * esz) % 16 == 0);
-  for (int64_t r = r_lo + wave; r < r_hi; r += 4) {
+  int64_t r = r_lo + wave;
+  if (vec && IN_DT != DT_F32) {
+    // four of this wave's rows loaded before their sums, which stay in row
+    // order (the same additions as one row at a time)
+    for (; r + 12 < r_hi; r += 16) {
+      uint4 a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        a[u] = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint8_t*>(x) + ((r + 4 * u) * ld + n) * esz);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t w[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t h = (w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu;
+          s[e] += IN_DT == DT_BF16 ? bf16_bits_to_f32(h) : __half2float(__ushort_as_half((unsigned short)h));
+        }
+      }
+    }
+  }
+  for (; r < r_hi; r += 4) {
     const uint8_t* row = reinterpret_cast<const uint8_t*>(x) + (r * ld + n) * esz;
     if (vec) {
       if constexpr (IN_DT == DT_F32) {
