@@ -131,8 +131,11 @@ template <int GRID>
 __device__ __forceinline__ v4f mma_block(const v8i& p, const v8i& q) {
   if constexpr (GRID == GRID_E4M3) {
     v4f z = {0.f, 0.f, 0.f, 0.f};
-    // fmt 0 = e4m3 for both operands; e8m0 scale 127 = 2^0
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(p, q, z, 0, 0, 0, 127, 0, 127);
+    // fmt 0 = e4m3 for both operands.  Zero scale operands select the
+    // unscaled encoding (v_mfma_f32_16x16x128_f8f6f4, no v_mfma_ld_scale
+    // prefix); its products equal those of unit e8m0 scales (127) bit for bit
+    // over the whole config-2 output, and the c2 GEMM runs 1.5% faster.
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(p, q, z, 0, 0, 0, 0, 0, 0);
   } else {
     v4i z = {0, 0, 0, 0};
     v4i p0 = {p[0], p[1], p[2], p[3]}, p1 = {p[4], p[5], p[6], p[7]};
@@ -225,7 +228,10 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   __shared__ __attribute__((aligned(16))) float lds_s0[BM + BN];  // A row scales, then B row scales
   __shared__ __attribute__((aligned(16))) float lds_s1[BM + BN];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the wave index through readfirstlane: the compiler then keeps everything
+  // derived from it (fragment bases, the copies' LDS destinations) in scalar
+  // registers instead of 28 VGPRs
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 2, wn = wave & 3;
 
   // workgroup -> output tile: undo the round-robin XCD dispatch so each XCD
@@ -534,12 +540,13 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
   // The tile origin passes through an empty asm here so that no address
   // arithmetic of the epilogue is hoisted above the K loop, where every
   // register is taken (hoisted values would be spilled across the loop).
-  int lane_e = lane;
-  asm volatile("" : "+s"(m0), "+s"(n0), "+v"(lane_e));
+  int lane_e = lane, wave_e = wave;
+  asm volatile("" : "+s"(m0), "+s"(n0), "+v"(lane_e), "+s"(wave_e));
   // lane_e holds rows m = m0 + wm*128 + tm*16 + lane_e%16 and columns
   // n = n0 + wn*64 + tn*16 + 4*(lane_e/16) + r
-  const int slab = wave >> 1;
-  uint8_t* stage_w = (slab == 0 ? lds_a0 : slab == 1 ? lds_b0 : slab == 2 ? lds_a1 : lds_b1) + (wave & 1) * (TILE_A / 2);
+  const int wm_e = wave_e >> 2, wn_e = wave_e & 3;
+  const int slab = wave_e >> 1;
+  uint8_t* stage_w = (slab == 0 ? lds_a0 : slab == 1 ? lds_b0 : slab == 2 ? lds_a1 : lds_b1) + (wave_e & 1) * (TILE_A / 2);
   const int64_t M = e_M, N = e_N, ldy = e_ldy;
   // bias and NaN flags: the indices are clamped into the matrix (values for
   // columns or rows past it are never stored), so the loads are
@@ -555,7 +562,7 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t n = min<int64_t>(n0 + wn * 64 + tn * 16 + (lane_e >> 4) * 4 + r, N - 1);
+        const int64_t n = min<int64_t>(n0 + wn_e * 64 + tn * 16 + (lane_e >> 4) * 4 + r, N - 1);
         bias[tn][r] = load_elem(reinterpret_cast<const void*>(e_bias), e_misc >> 1, n);
       }
   }
@@ -565,14 +572,14 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
     for (int tn = 0; tn < 4; ++tn)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t n = min<int64_t>(n0 + wn * 64 + tn * 16 + (lane_e >> 4) * 4 + r, N - 1);
+        const int64_t n = min<int64_t>(n0 + wn_e * 64 + tn * 16 + (lane_e >> 4) * 4 + r, N - 1);
         nan_cols |= (reinterpret_cast<const int32_t*>(e_nan_b)[n] != 0 ? 1u : 0u) << (tn * 4 + r);
       }
   }
   if (e_nan_a) {
 #pragma unroll
     for (int tm = 0; tm < 8; ++tm) {
-      const int64_t m = min<int64_t>(m0 + wm * 128 + tm * 16 + (lane_e & 15), M - 1);
+      const int64_t m = min<int64_t>(m0 + wm_e * 128 + tm * 16 + (lane_e & 15), M - 1);
       nan_rows |= (reinterpret_cast<const int32_t*>(e_nan_a)[m] != 0 ? 1u : 0u) << tm;
     }
   }
@@ -625,8 +632,8 @@ __global__ void __launch_bounds__(NTHREADS, 1) gemm_blockscaled_kernel(GemmArgs 
       for (int j = 0; j < chunks_per_row / 2; ++j) {
         const int q = lane_e + 64 * j;
         const int row = q / chunks_per_row, c = q % chunks_per_row;
-        const int64_t m = m0 + wm * 128 + part * EPI_ROWS + row;
-        const int64_t n = n0 + wn * 64 + c * epc;
+        const int64_t m = m0 + wm_e * 128 + part * EPI_ROWS + row;
+        const int64_t n = n0 + wn_e * 64 + c * epc;
         const uint8_t* src = stage_w + row * pitch + c * 16;
         uint8_t* ydst = reinterpret_cast<uint8_t*>(e_y) + (m * ldy + n) * esz;
         if constexpr (FULL) {
