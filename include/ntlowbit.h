@@ -350,6 +350,14 @@ int ntlb_colsum(const void* x, int x_dtype, int64_t M, int64_t N, int64_t ldx, f
 /* Workspace bytes of ntlb_colsum. */
 int64_t ntlb_colsum_workspace_bytes(int64_t M, int64_t N);
 
+/* The straight-through operand of EmulatedLowBitBackend.linear
+ * (te_backend.py:250-251: `input + (input_dq - input).detach()`, and the same
+ * for the weight): out[i] = t[i] + (t_dq[i] - t[i]) over n contiguous
+ * elements of `dtype`, each operation in fp32 rounded to the dtype as torch
+ * rounds it.  Equal to t_dq under round to nearest; under stochastic
+ * rounding it is the operand the reference multiplies. */
+int ntlb_ste_value(int dtype, const void* t, const void* t_dq, void* out, int64_t n, void* stream);
+
 /*
  * Grouped (per-expert) blockwise-scaled GEMM over a token-offset table.
  * Replaces the per-expert loop of _run_local_experts (moe.py:888-962) /

@@ -86,6 +86,7 @@ SIGNATURES = {
     "ntlb_gemm_dense_tn": [_I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_colsum": [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P],
     "ntlb_colsum_workspace_bytes": [_I64, _I64],
+    "ntlb_ste_value": [_I32, _P, _P, _P, _I64, _P],
     "ntlb_ep_record_bytes": [_I64],
     "ntlb_quant_tile_1x128_fanout": [_P, _I32, _I64, _I64, _I64, _P, _I64, _I64, _I32, _I32, _I32, _I32, _U64, _U64,
                                      _P, _I64, _P, _I64, _I64, _P, _P],

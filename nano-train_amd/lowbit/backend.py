@@ -118,6 +118,31 @@ def _gemm_op_dtype(*dts: torch.dtype) -> torch.dtype:
     return torch.bfloat16 if all(d == torch.bfloat16 for d in dts) else torch.float32
 
 
+def _stash(saved: list, q: Optional[QTensor]):
+    """Append a QTensor's tensors to `saved` (for ctx.save_for_backward) and
+    return the metadata that rebuilds it, or None."""
+    if q is None:
+        return None
+    i = len(saved)
+    saved.extend([q.codes, q.scales, q.nan_rows])
+    return (i, q.s_row, q.s_col, q.shift, q.grid, q.rows, q.K)
+
+
+def _unstash(saved, meta) -> Optional[QTensor]:
+    if meta is None:
+        return None
+    i, s_row, s_col, shift, grid, rows, K = meta
+    return QTensor(saved[i], saved[i + 1], s_row, s_col, shift, grid, rows, K, saved[i + 2], None)
+
+
+def _reference_operand(t: torch.Tensor, dq: torch.Tensor, dtype: torch.dtype, sr: bool) -> torch.Tensor:
+    """The operand the reference multiplies: t + (t_dq - t) in t's dtype with
+    t_dq = bf16(q * s) (te_backend.py:250-251).  Under round to nearest that
+    is t_dq itself; stochastic rounding evaluates the expression."""
+    dq = dq.to(dtype)
+    return ops.ste_value(t, dq) if sr else dq
+
+
 class _HipLowBitLinear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias, backend: "HipLowBitBackend"):
@@ -134,12 +159,18 @@ class _HipLowBitLinear(torch.autograd.Function):
         ste = backend.backward_recipe == "ste"
         xdt, wdt = x.dtype, weight.dtype
         act_channel = backend._activation_granularity == "channel"
+        # Under stochastic rounding the reference's operand t + (t_dq - t)
+        # can differ from bf16(q * s) (_reference_operand), so the paths that
+        # multiply the reference's operands take the evaluated expression
+        # instead of decoding codes.  The blockscaled forward multiplies the
+        # fp32 q * s values either way.
+        sr = rnd == "stochastic"
         # the straight-through gradients decode the forward's codes when the
         # reference's operands are bf16 (dY and X_q in x's dtype, W_q in w's)
-        dgrad_codes = ste and need_x_grad and xdt == torch.bfloat16 and wdt == torch.bfloat16
-        wgrad_codes = ste and need_w_grad and xdt == torch.bfloat16 and not act_channel
+        dgrad_codes = ste and need_x_grad and xdt == torch.bfloat16 and wdt == torch.bfloat16 and not sr
+        wgrad_codes = ste and need_w_grad and xdt == torch.bfloat16 and not act_channel and not sr
         ref_fwd = backend.forward_mode == "reference"
-        ref_codes = ref_fwd and xdt == wdt and xdt in (torch.bfloat16, torch.float32)
+        ref_codes = ref_fwd and xdt == wdt and xdt in (torch.bfloat16, torch.float32) and not sr
         fwd_dq = act_channel or (ref_fwd and not ref_codes)
         # dequantized tensors: for the forward, in the input dtypes (reference
         # mode, te_backend.py:173-202) or fp32 (blockscaled mode's q * s
@@ -154,10 +185,21 @@ class _HipLowBitLinear(torch.autograd.Function):
         qw, wdq = quantize_operand(
             weight, backend._weight_granularity, is_weight=True, original_dim=weight.dim(), fmt=fmt, bits=bits,
             rounding=rnd, seed=seed, offset=base + 1, want_dq=want_wdq, dq_dtype=w_dq_dt)
+        # the reference's operands in the input dtypes, where a path multiplies them
+        xq = wq = None
+        if ste and need_w_grad and not wgrad_codes:
+            xq = _reference_operand(x2, xdq, xdt, sr)
+        if ste and need_x_grad and not dgrad_codes:
+            wq = _reference_operand(weight, wdq, wdt, sr)
         if fwd_dq:
+            if ref_fwd:
+                xf = xq if xq is not None else _reference_operand(x2, xdq, xdt, sr)
+                wf = wq if wq is not None else _reference_operand(weight, wdq, wdt, sr)
+            else:
+                xf, wf = xdq, wdq
             # multiplied in fp32 (bf16 MFMA when both operands are bf16)
-            op = _gemm_op_dtype(xdq.dtype, wdq.dtype)
-            y2 = ops.gemm_dense(xdq.to(op), wdq.to(op), bias=bias, out_dtype=out_dtype)
+            op = _gemm_op_dtype(xf.dtype, wf.dtype)
+            y2 = ops.gemm_dense(xf.to(op), wf.to(op), bias=bias, out_dtype=out_dtype)
         elif ref_fwd:
             y2 = ops.gemm_dq_forward(qx, qw, bias=bias, out_dtype=out_dtype, op_dtype=xdt)
         else:
@@ -171,12 +213,15 @@ class _HipLowBitLinear(torch.autograd.Function):
         ctx.w_dtype = wdt
         ctx.offset = base
         if ste:
-            # codes (and dequantized tensors where the codes path does not
-            # apply) are intermediates of this call, kept on ctx
-            ctx.qx = qx if wgrad_codes else None
-            ctx.qw = qw if dgrad_codes else None
-            ctx.xdq = xdq if (need_w_grad and not wgrad_codes) else None
-            ctx.wdq = wdq if (need_x_grad and not dgrad_codes) else None
+            # the codes (or the reference's operands, where the codes path
+            # does not apply) go through save_for_backward, so saved-tensor
+            # hooks see them and a retained graph can run backward again
+            saved = []
+            ctx.qx_meta = _stash(saved, qx if wgrad_codes else None)
+            ctx.qw_meta = _stash(saved, qw if dgrad_codes else None)
+            ctx.xq_idx = len(saved)
+            saved.extend([xq, wq])
+            ctx.save_for_backward(*saved)
         else:
             ctx.save_for_backward(x2, weight)
         return y
@@ -192,23 +237,25 @@ class _HipLowBitLinear(torch.autograd.Function):
             # te_backend.py:250-259 under autograd: dX = dY @ W_q and
             # dW = dY^T @ X_q in fp32 over the operands the forward multiplied,
             # cast to the input / weight dtype
+            saved = ctx.saved_tensors
+            qx, qw = _unstash(saved, ctx.qx_meta), _unstash(saved, ctx.qw_meta)
+            xq, wq = saved[ctx.xq_idx], saved[ctx.xq_idx + 1]
             if ctx.needs_input_grad[0]:
-                if ctx.qw is not None and dy2.dtype == torch.bfloat16:
-                    dx = ops.ste_dgrad(dy2, ctx.qw, out_dtype=ctx.x_dtype)
+                if qw is not None and dy2.dtype == torch.bfloat16:
+                    dx = ops.ste_dgrad(dy2, qw, out_dtype=ctx.x_dtype)
                 else:
                     # W_q in the weight dtype, then the fp32 (or all-bf16) GEMM
-                    wdq = ctx.wdq.to(ctx.w_dtype) if ctx.wdq is not None else ops.dequant(ctx.qw, out_dtype=ctx.w_dtype)
+                    wdq = wq if wq is not None else ops.dequant(qw, out_dtype=ctx.w_dtype)
                     op = _gemm_op_dtype(dy2.dtype, wdq.dtype)
                     dx = ops.gemm_dense(dy2.to(op), wdq.to(op), b_transposed=True, out_dtype=ctx.x_dtype)
                 dx = dx.reshape(ctx.x_shape)
             if ctx.needs_input_grad[1]:
-                if ctx.qx is not None and dy2.dtype == torch.bfloat16:
-                    dw = ops.ste_wgrad(dy2, ctx.qx, out_dtype=ctx.w_dtype)
+                if qx is not None and dy2.dtype == torch.bfloat16:
+                    dw = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype)
                 else:
-                    xdq = ctx.xdq.to(ctx.x_dtype) if ctx.xdq is not None else ops.dequant(ctx.qx, out_dtype=ctx.x_dtype)
+                    xdq = xq if xq is not None else ops.dequant(qx, out_dtype=ctx.x_dtype)
                     op = _gemm_op_dtype(dy2.dtype, xdq.dtype)
                     dw = ops.gemm_dense_tn(dy2.to(op), xdq.to(op), out_dtype=ctx.w_dtype)
-            ctx.qx = ctx.qw = ctx.xdq = ctx.wdq = None
         else:
             x2, weight = ctx.saved_tensors
             dx, dw = _fp8_recipe_backward(backend, dy2, x2, weight, ctx.offset, ctx.needs_input_grad)

@@ -87,6 +87,11 @@ class LowBitLinearMixin:
         self.register_buffer("_persistent_fp4_codes", torch.empty(0, dtype=torch.uint8, device=dev), persistent=True)
         self.register_buffer("_persistent_scale", torch.empty(0, device=dev), persistent=True)
         self.register_buffer("_persistent_numel", torch.zeros((), dtype=torch.int64, device=dev), persistent=True)
+        # host copy of _persistent_numel, kept in step with the buffer, so the
+        # forward's "is the persistent copy current" test reads no device memory
+        # (no device-to-host copy and stream sync per call; the forward can be
+        # captured in a HIP graph)
+        self._persistent_numel_host = 0
         bind = getattr(self._module_precision_state.lowbit_backend, "bind_parameters", None)
         if callable(bind):
             bind(self.weight, self.bias)
@@ -133,6 +138,7 @@ class LowBitLinearMixin:
                               error_msgs) -> None:
         super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,  # type: ignore
                                       unexpected_keys, error_msgs)
+        self._persistent_numel_host = int(self._persistent_numel.item())  # once per load, not per forward
         optional = {prefix + s for s in _PERSISTENT_SUFFIXES}
         missing_keys[:] = [k for k in missing_keys if k not in optional]
 
@@ -143,6 +149,7 @@ class LowBitLinearMixin:
         self._persistent_fp4_codes = torch.empty(0, dtype=torch.uint8, device=dev)
         self._persistent_scale = torch.empty(0, device=dev)
         self._persistent_numel = torch.zeros((), dtype=torch.int64, device=dev)
+        self._persistent_numel_host = 0
 
     @torch.no_grad()
     def refresh_persistent_lowbit_params(self) -> None:
@@ -161,6 +168,7 @@ class LowBitLinearMixin:
             self._persistent_fp4_codes = torch.empty(0, dtype=torch.uint8, device=dev)
             self._persistent_scale = scale
             self._persistent_numel = numel
+            self._persistent_numel_host = int(self.weight.numel())
             return
         if mode == "fp4":
             fmt = str(getattr(self.module_precision_assignment, "fp4_persistent_format", "nf4"))
@@ -171,6 +179,7 @@ class LowBitLinearMixin:
             self._persistent_fp8_weight = torch.empty(0, device=dev)
             self._persistent_scale = scale
             self._persistent_numel = numel
+            self._persistent_numel_host = int(self.weight.numel())
             return
         raise ValueError(f"Unsupported persistent low-bit mode: {mode}")
 
@@ -181,6 +190,7 @@ class LowBitLinearMixin:
         _, shape = P._block_and_scale_shape(self.weight, self._persistent_granularity())
         self._persistent_scale = scales.reshape(shape)
         self._persistent_numel = torch.tensor(int(self.weight.numel()), dtype=torch.int64, device=dev)
+        self._persistent_numel_host = int(self.weight.numel())
         if mode == "fp8":
             self._persistent_fp8_weight = codes.view(torch.float8_e4m3fn).reshape(self.weight.shape)
             self._persistent_fp4_codes = torch.empty(0, dtype=torch.uint8, device=dev)
@@ -199,7 +209,7 @@ class LowBitLinearMixin:
             deq = P.dequantize_fp8_persistent(self._persistent_fp8_weight, self._persistent_scale,
                                               target_dtype=self.weight.dtype)
         elif mode == "fp4":
-            if int(self._persistent_numel.item()) != int(self.weight.numel()):
+            if self._persistent_numel_host != int(self.weight.numel()):
                 self.refresh_persistent_lowbit_params()
             deq = P.dequantize_nf4_persistent(self._persistent_fp4_codes, self._persistent_scale,
                                               num_values=int(self.weight.numel()), target_shape=self.weight.shape,
@@ -219,7 +229,7 @@ class LowBitLinearMixin:
             return None
         N, K = self.weight.shape
         if mode == "fp4":
-            if int(self._persistent_numel.item()) != int(self.weight.numel()):
+            if self._persistent_numel_host != int(self.weight.numel()):
                 self.refresh_persistent_lowbit_params()
             scale = self._persistent_scale
             block = (N * K) if scale.numel() <= 1 else K

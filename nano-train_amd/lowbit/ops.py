@@ -689,6 +689,18 @@ def gemm_dense_tn(a: torch.Tensor, b: torch.Tensor, *, out_dtype: torch.dtype = 
 _colsum_ws: dict = {}
 
 
+def ste_value(t: torch.Tensor, t_dq: torch.Tensor) -> torch.Tensor:
+    """t + (t_dq - t) in t's dtype (te_backend.py:250-251): the operand the
+    reference multiplies; it differs from t_dq only under stochastic rounding."""
+    _require_device(t, t_dq)
+    if t.dtype != t_dq.dtype or t.shape != t_dq.shape:
+        raise ValueError(f"ste_value operands differ: {t.dtype}{tuple(t.shape)} vs {t_dq.dtype}{tuple(t_dq.shape)}")
+    t, t_dq = t.contiguous(), t_dq.contiguous()
+    out = torch.empty_like(t)
+    call("ntlb_ste_value", _dtype_code(t.dtype), t.data_ptr(), t_dq.data_ptr(), out.data_ptr(), t.numel(), _stream())
+    return out
+
+
 def colsum(x: torch.Tensor, *, out_dtype: torch.dtype) -> torch.Tensor:
     """sum over rows of x [M, N] in fp32, cast to out_dtype (F.linear's bias
     gradient), in a fixed order."""

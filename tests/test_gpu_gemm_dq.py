@@ -296,23 +296,30 @@ def test_ste_backward_c3_full_size_sampled(gpu_device):
 
 
 @pytest.mark.parametrize("fmt", list(GRIDS))
-def test_ste_dgrad_split_tail_matches_unsplit(gpu_device, fmt):
-    """dX [8192, 2304] (288 output tiles: one whole wave of 256 compute units
+@pytest.mark.parametrize("wscale,K", [("block", 2304), ("tile", 2304), ("tile", 2300), ("block", 2300)])
+def test_ste_dgrad_split_tail_matches_unsplit(gpu_device, fmt, wscale, K):
+    """dX [8192, K] (288 output tiles: one whole wave of 256 compute units
     plus a 32-tile tail) with the split-K workspace: the tail tiles' K ranges
     summed in a fixed order equal the unsplit product up to fp32 summation
     order and repeat bit for bit; a NaN code's column stays NaN through the
-    split.  (The oracle bar itself is checked by the tests above.)"""
+    split.  W's scales are 128x128 blocks (one scale per wave) or 1x128 tiles
+    (contiguous per-row scales), and K = 2300 leaves the last tile column
+    ragged.  (The oracle bar itself is checked by the tests above.)"""
     ops = _ops()
     from lowbit import _lib
     from lowbit._lib import call
 
-    M, N, K = 8192, 4096, 2304  # contraction 4096: 64 K steps, split seven ways
-    tiles = (M // 256) * (K // 256)
+    M, N = 8192, 4096  # contraction 4096: 64 K steps, split seven ways
+    tiles = (M // 256) * (-(-K // 256))
     assert int(_lib.lib().ntlb_gemm_dq_workspace_bytes(_lib.BF16, M, K, N)) > 0, "the shape should split"
     w = seeded((N, K), seed=20262051, std=0.02)
+    nan_col = 2299
     if fmt == "int_grid":
-        w[3, 2300] = float("nan")  # a column of the last (split) tile column
-    qw, _ = ops.quant_block_128x128(w.to(gpu_device), fmt=fmt)
+        w[3, nan_col] = float("nan")  # a column of the last (split) tile column
+    if wscale == "block":
+        qw, _ = ops.quant_block_128x128(w.to(gpu_device), fmt=fmt)
+    else:
+        qw = ops.quant_tile_1x128(w.to(gpu_device), fmt=fmt)
     dy = seeded((M, N), seed=20262052, std=1e-3).to(gpu_device)
     dx = ops.ste_dgrad(dy, qw, out_dtype=torch.float32)
     dx2 = ops.ste_dgrad(dy, qw, out_dtype=torch.float32)
@@ -326,7 +333,7 @@ def test_ste_dgrad_split_tail_matches_unsplit(gpu_device, fmt):
     nan = torch.isnan(ref)
     assert torch.equal(nan, torch.isnan(dx))
     if fmt == "int_grid":
-        assert nan[:, 2300].all() and nan.any(0).sum() == 1
+        assert nan[:, nan_col].all() and nan.any(0).sum() == 1
     a, b = dx[~nan].double(), ref[~nan].double()
     assert float((a - b).norm() / b.norm()) <= 1e-6
     # the tail tiles lie in row tiles 28-31 (the last group of the grouped

@@ -100,3 +100,33 @@ def test_nf4_dequantize_matches_c_oracle():
     got = T.nf4_dequantize(torch.from_numpy(packed), torch.from_numpy(scales), numel=w.numel(), block=64,
                            dtype=torch.float32)
     assert _bits_equal(got, O.nf4_dequant(packed, scales, w.numel(), 64))
+
+
+@pytest.mark.parametrize("grid", [O.GRID_INT, O.GRID_E4M3])
+@pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_reference_operand_is_the_dequant_only_under_nearest(grid, gr, gc, dtype):
+    """The reference multiplies x + (x_dq - x) in x's dtype (te_backend.py:250-251),
+    x_dq = dtype(q * s).  Under round to nearest that is x_dq itself (q * s and
+    x lie within a factor of two, so the difference is exact), which is why
+    the kernels may decode dtype(q * s) from codes.  Under stochastic rounding
+    a code can land far from x / s; the difference then rounds and the
+    expression differs from x_dq, exactly where dtype(x_dq - x) is inexact."""
+    # outliers x1000 make large scales, so many x / s sit in e4m3's
+    # subnormal range, where a stochastic code can be several times x / s
+    g = torch.Generator().manual_seed(20262341)
+    x = torch.randn(256, 512, generator=g)
+    x = torch.where(torch.rand(256, 512, generator=g) < 0.01, x * 1000, x).to(dtype)
+    x32 = x.float().numpy()
+    for rounding in (O.ROUND_NEAREST, O.ROUND_STOCHASTIC):
+        dq = O.quant_grouped(x32, gr, gc, grid=grid, rounding=rounding, seed=5, offset=2)[3]
+        dq_t = torch.from_numpy(dq).to(dtype)
+        xq = x + (dq_t - x)
+        same = (xq.float() == dq_t.float()) | (torch.isnan(xq.float()) & torch.isnan(dq_t.float()))
+        if rounding == O.ROUND_NEAREST:
+            assert bool(same.all())
+        else:
+            assert 0 < int((~same).sum()) < 0.05 * x.numel()
+            diff64 = dq_t.double() - x.double()
+            inexact = (dq_t - x).double() != diff64
+            assert bool(inexact[~same].all())
