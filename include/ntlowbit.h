@@ -325,6 +325,44 @@ int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, i
                         int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col, int x_shift, int64_t K, void* dw,
                         int dw_dtype, int64_t lddw, void* stream);
 
+/* The straight-through dgrad of every expert's Linear at once (the input
+ * gradient of te_backend.py:250-259 for each expert of the single-rank loop,
+ * moe.py:1062-1093 / LocalRoutedMoE :476-491): rows sorted by expert, expert e
+ * owning rows [offsets[e], offsets[e+1]) (offsets int32 [n_experts + 1]);
+ * dX[rows of e] = dY[rows of e] . bf16(dq(W_e)), W_e the codes [N, ldw] at
+ * w + e*w_estride with 128x128 block (or tensor) scales at sw + e*sw_estride
+ * (scale(n, k) = sw[(n >> w_shift)*sw_row + (k >> 7)*sw_col]).  dY bf16 [R, ldy]
+ * with ld >= N rounded up to 64 and zero pad columns; dX [R, lddx] of
+ * dx_dtype.  op_dtype NTLB_BF16 only. */
+int ntlb_gemm_grouped_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                const int32_t* offsets, int n_experts, int grid, const uint8_t* w, int64_t ldw,
+                                int64_t w_estride, const float* sw, int64_t sw_row, int64_t sw_col, int w_shift,
+                                int64_t sw_estride, int64_t K, void* dx, int dx_dtype, int64_t lddx, void* stream);
+
+/* The input gradient of every expert's gate and up Linears (moe.py:190-193)
+ * as autograd forms it: dX = bf16(dX_gate) + bf16(dX_up), added in bf16, with
+ * dX_gate = d_gate . bf16(dq(W_gate)) and dX_up = d_up . bf16(dq(W_up)) over
+ * the interleaved gate/up layout: d_gate_up bf16 [R, 2I] and the codes
+ * [2I, ldw] of each expert (at w + e*w_estride, 128x128 block scales at sw +
+ * e*sw_estride) hold 128-wide blocks alternating gate block t and up block t.
+ * Rows sorted by expert (offsets int32 [n_experts + 1]); dX bf16 [R, lddx]. */
+int ntlb_gemm_grouped_ste_dgrad_gate_up(int op_dtype, const void* dgu, int64_t lddgu, int64_t R, int64_t I,
+                                        const int32_t* offsets, int n_experts, int grid, const uint8_t* w,
+                                        int64_t ldw, int64_t w_estride, const float* sw, int64_t sw_row,
+                                        int64_t sw_col, int64_t sw_estride, int64_t K, void* dx, int64_t lddx,
+                                        void* stream);
+
+/* The straight-through wgrad of every expert's Linear at once: dW_e[N, K] =
+ * dY[rows of e]^T . bf16(dq(X[rows of e])) with the contraction over expert
+ * e's rows only, for every expert (an expert without rows gets zeros); dW_e at
+ * dw + e*dw_estride BYTES, row stride lddw.  X's codes [R, ldx] carry per-row
+ * 1x128 scales in the tile-major layout (sx_row 1, sx_col a multiple of 4,
+ * x_shift 0).  op_dtype NTLB_BF16 only. */
+int ntlb_gemm_grouped_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                const int32_t* offsets, int n_experts, int grid, const uint8_t* x, int64_t ldx,
+                                const float* sx, int64_t sx_row, int64_t sx_col, int x_shift, int64_t K, void* dw,
+                                int dw_dtype, int64_t lddw, int64_t dw_estride, void* stream);
+
 /* Y[M, N] = A[M, K] . op(B) + bias over bf16 or fp32 matrices (op_dtype), for
  * the dequantized tensors of granularities whose scales change along the
  * contraction element by element (the activation "channel" granularity of
@@ -414,6 +452,20 @@ int ntlb_gemm_grouped_swiglu_quant(int grid, const uint8_t* a, int64_t lda, cons
                                    const int32_t* nan_a, const int32_t* nan_b, uint16_t* h, int64_t ldh, uint8_t* hc,
                                    int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col, int32_t* h_nan, int qmax,
                                    int rounding, int scale_rule, uint64_t seed, uint64_t offset, void* stream);
+
+/* ntlb_gemm_grouped_swiglu_quant that also stores the projections' bf16
+ * outputs (gate and up, each rounded to bf16 as the reference's Linears
+ * return them) into gu [M_total, ldgu] in B's interleaved column order, for
+ * the SwiGLU backward of ntlb_swiglu_backward (the activations autograd keeps
+ * for F.silu(gate) * up, moe.py:190-193).  gu NULL stores nothing. */
+int ntlb_gemm_grouped_swiglu_quant_gu(int grid, const uint8_t* a, int64_t lda, const float* sa, int64_t sa_row,
+                                      int64_t sa_col, int a_shift, const uint8_t* b, int64_t ldb, int64_t b_estride,
+                                      const float* sb, int64_t sb_row, int64_t sb_col, int64_t sb_estride,
+                                      const int32_t* offsets, int n_experts, int64_t M_total, int64_t N, int64_t Kp,
+                                      const int32_t* nan_a, const int32_t* nan_b, uint16_t* h, int64_t ldh,
+                                      uint8_t* hc, int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col,
+                                      int32_t* h_nan, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                      uint64_t offset, uint16_t* gu, int64_t ldgu, void* stream);
 
 /*
  * NF4 refresh of a persistent weight (the flat tensor of n elements):
@@ -654,6 +706,59 @@ int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* to
  * or int64 (1) and topk_w (w_dtype) [T, K] contiguous, 1 <= K <= 32, out
  * [T, ldo].
  */
+/*
+ * Capacity keep of the single-rank expert loop (moe.py:1077-1081,
+ * LocalRoutedMoE :482-486: keep_rel = torch.topk(sort_weights, k=capacity,
+ * sorted=True).indices when an expert has more than `capacity` rows).  In:
+ * the rows sorted by expert (inv [rows]: row -> assignment t*K + s, offsets
+ * int32 [n_experts + 1], as ntlb_ep_partition gives them) and topk_w
+ * (w_dtype, n_assign = T*K entries).  Out: the kept rows, each expert's
+ * highest weight first (equal weights keep row order), as pos_out
+ * [n_assign] (assignment -> kept row, -1 dropped), inv_out [rows] (kept row
+ * -> assignment; entries past the kept count are not written), offsets_out
+ * [n_experts + 1] and counts_out int64 [n_experts].  capacity <= 0 keeps every
+ * row in its order.
+ */
+int ntlb_moe_capacity_keep(const int32_t* inv, const int32_t* offsets, int n_experts, int64_t rows, int64_t n_assign,
+                           const void* topk_w, int w_dtype, int64_t capacity, int32_t* pos_out, int32_t* inv_out,
+                           int32_t* offsets_out, int64_t* counts_out, void* stream);
+
+/*
+ * Backward of the single-rank combine `output[token_indices] += expert_out *
+ * weights` (moe.py:1087-1088, :489-490): for token t's slot s with row r =
+ * pos[t*K + s] >= 0, dy[r] = d_out[t] * topk_w[t, s] rounded to `dtype` (the
+ * gradient of expert_out) and d_w[t, s] = sum over H of d_out[t] * y[r] in
+ * fp32, stored in w_dtype (the gradient of the routing weight); a dropped slot
+ * (r < 0) gets d_w = 0 and writes no row.  d_out [T, ldo], y [n, ldy] and dy
+ * [n, lddy] share `dtype`; 1 <= K <= 8.
+ */
+int ntlb_moe_combine_backward(const void* d_out, int64_t ldo, const void* y, int64_t ldy, int dtype,
+                              const int32_t* pos, const void* topk_w, int w_dtype, int64_t T, int64_t K, int64_t H,
+                              void* dy, int64_t lddy, void* d_w, void* stream);
+
+/*
+ * Backward of gated = F.silu(gate) * up over bf16 tensors (ExpertMLP.forward,
+ * moe.py:190-193): with s = bf16(silu(g)), d_up = bf16(d * s), d_s = bf16(d *
+ * u) and d_gate = bf16(d_s * sig * (1 + g * (1 - sig))) (sig = 1 / (1 +
+ * exp(-g)), torch's silu backward in fp32).  dh bf16 [R, I]; gu and dgu bf16
+ * [R, 2I] in the interleaved column order of the fused gate/up GEMM (h column
+ * j: gate column 256*(j/128) + j%128, up column that + 128); I % 128 == 0.
+ */
+/*
+ * The token gradient of the single-rank loop's gather `tokens[token_indices]`
+ * (moe.py:1086, :488) under autograd: out[t] = the rows dx[pos[t*K + s]] of
+ * token t's kept slots, summed in descending expert id with each add rounded
+ * to `dtype` (the order in which autograd accumulates them: the later
+ * experts' backward runs first); zero for a token with no kept slot.  dx and
+ * out share `dtype`; topk_idx int32 (idx_dtype 0) or int64 (1) [T, K], 1 <= K
+ * <= 8.
+ */
+int ntlb_moe_token_grad(const void* dx, int64_t lddx, int dtype, const int32_t* pos, const void* topk_idx,
+                        int idx_dtype, int64_t T, int64_t K, int64_t H, void* out, int64_t ldo, void* stream);
+
+int ntlb_swiglu_backward(const uint16_t* dh, int64_t lddh, const uint16_t* gu, int64_t ldgu, int64_t R, int64_t I,
+                         uint16_t* dgu, int64_t lddgu, void* stream);
+
 int ntlb_moe_combine_rows(const void* y, int64_t ldy, int64_t n, const int32_t* pos, const void* topk_idx,
                           int idx_dtype, const void* topk_w, int w_dtype, int64_t T, int64_t K, int64_t H, void* out,
                           int out_dtype, int64_t ldo, void* stream);

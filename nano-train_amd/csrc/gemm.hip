@@ -73,6 +73,8 @@ struct GemmArgs {
   float* hs;      // h scales: hs[row * hs_row + tile * hs_col]
   int64_t hs_row, hs_col;
   int32_t* h_nan;  // optional per-row NaN flags of h
+  uint16_t* gu;   // optional bf16 gate / up outputs [M, 2I] in B's interleaved column order, row stride ldgu
+  int64_t ldgu;
   float h_qmaxf;
   int h_sr, h_scale_rule;
   uint64_t h_seed, h_offset;
@@ -691,6 +693,12 @@ __device__ __forceinline__ void swiglu_quant_rows(const GemmArgs& g, const uint8
     uint8_t* gp = rowp + (((hh * 8 + k) ^ (r & 15)) << 4);
     const uint4 gw = *reinterpret_cast<const uint4*>(gp);
     const uint4 uw = *reinterpret_cast<const uint4*>(rowp + (((16 + hh * 8 + k) ^ (r & 15)) << 4));
+    if (g.gu && m < g.M) {
+      // the projections' bf16 outputs, kept for the SwiGLU backward
+      uint16_t* gup = g.gu + m * g.ldgu + n0 + hh * 64 + k * 8;
+      *reinterpret_cast<uint4*>(gup) = gw;
+      *reinterpret_cast<uint4*>(gup + 128) = uw;
+    }
     const uint32_t gg[4] = {gw.x, gw.y, gw.z, gw.w}, uu[4] = {uw.x, uw.y, uw.z, uw.w};
     uint32_t hb[4];
 #pragma unroll
@@ -780,7 +788,7 @@ extern "C" int ntlb_gemm_blockscaled_ws(int grid, const uint8_t* a, int64_t lda,
   // buffer resources address each operand with 32-bit byte offsets
   if ((M + BM) * lda >= (int64_t)0x7FFFFFFF || (N + BN) * ldb >= (int64_t)0x7FFFFFFF)
     return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
-  GemmArgs g;
+  GemmArgs g{};
   g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
   g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = b_shift;
   g.M = M; g.N = N; g.Kp = Kp;
@@ -854,7 +862,7 @@ extern "C" int ntlb_gemm_grouped_blockscaled(int grid, const uint8_t* a, int64_t
     return fail(NTLB_EUNSUPPORTED, "%s: more than %d experts", fn, TILE_A / 4 - 1);
   const int64_t tiles = ((M_total + BM - 1) / BM + n_experts) * ((N + BN - 1) / BN);
   if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
-  GemmArgs g;
+  GemmArgs g{};
   g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
   g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = b_shift;
   g.M = M_total; g.N = N; g.Kp = Kp;
@@ -931,7 +939,7 @@ extern "C" int ntlb_gemm_swiglu_quant(int grid, const uint8_t* a, int64_t lda, c
     return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB of codes", fn);
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
-  GemmArgs g;
+  GemmArgs g{};
   g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
   g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = 7;
   g.M = M; g.N = N; g.Kp = Kp;
@@ -959,6 +967,21 @@ extern "C" int ntlb_gemm_grouped_swiglu_quant(int grid, const uint8_t* a, int64_
                                               uint8_t* hc, int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col,
                                               int32_t* h_nan, int qmax, int rounding, int scale_rule, uint64_t seed,
                                               uint64_t offset, void* stream) {
+  return ntlb_gemm_grouped_swiglu_quant_gu(grid, a, lda, sa, sa_row, sa_col, a_shift, b, ldb, b_estride, sb, sb_row,
+                                           sb_col, sb_estride, offsets, n_experts, M_total, N, Kp, nan_a, nan_b, h,
+                                           ldh, hc, ldhc, hs, hs_row, hs_col, h_nan, qmax, rounding, scale_rule, seed,
+                                           offset, nullptr, 0, stream);
+}
+
+extern "C" int ntlb_gemm_grouped_swiglu_quant_gu(int grid, const uint8_t* a, int64_t lda, const float* sa,
+                                                 int64_t sa_row, int64_t sa_col, int a_shift, const uint8_t* b,
+                                                 int64_t ldb, int64_t b_estride, const float* sb, int64_t sb_row,
+                                                 int64_t sb_col, int64_t sb_estride, const int32_t* offsets,
+                                                 int n_experts, int64_t M_total, int64_t N, int64_t Kp,
+                                                 const int32_t* nan_a, const int32_t* nan_b, uint16_t* h, int64_t ldh,
+                                                 uint8_t* hc, int64_t ldhc, float* hs, int64_t hs_row, int64_t hs_col,
+                                                 int32_t* h_nan, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                                 uint64_t offset, uint16_t* gu, int64_t ldgu, void* stream) {
   const char* fn = "ntlb_gemm_grouped_swiglu_quant";
   if (grid != NTLB_GRID_INT && grid != NTLB_GRID_E4M3) return fail(NTLB_EINVAL, "%s: bad grid %d", fn, grid);
   if (M_total < 0 || N < 0 || Kp < 0 || n_experts < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
@@ -976,13 +999,16 @@ extern "C" int ntlb_gemm_grouped_swiglu_quant(int grid, const uint8_t* a, int64_
     return fail(NTLB_EUNSUPPORTED, "%s: more than %d experts", fn, TILE_A / 4 - 1);
   const int64_t tiles = ((M_total + BM - 1) / BM + n_experts) * ((N + BN - 1) / BN);
   if (tiles > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
-  GemmArgs g;
+  GemmArgs g{};
   g.a = a; g.lda = lda; g.sa = sa; g.sa_row = sa_row; g.sa_col = sa_col; g.a_shift = a_shift;
   g.b = b; g.ldb = ldb; g.sb = sb; g.sb_row = sb_row; g.sb_col = sb_col; g.b_shift = 7;
   g.M = M_total; g.N = N; g.Kp = Kp;
   g.nan_a = nan_a; g.nan_b = nan_b;
   g.offsets = offsets; g.n_experts = n_experts; g.b_estride = b_estride; g.sb_estride = sb_estride;
   g.split_base = 0; g.split_s = 1; g.ws = nullptr; g.ws_count = nullptr;
+  if (gu && (ldgu < N || ldgu % 8 || !aligned(gu, 16)))
+    return fail(NTLB_EINVAL, "%s: the gate/up output needs ld >= N, ld %% 8 == 0 and 16-byte alignment", fn);
+  g.gu = gu; g.ldgu = ldgu;
   int rc = swiglu_common(fn, g, grid, N, h, ldh, hc, ldhc, hs, hs_row, hs_col, h_nan, qmax, rounding, scale_rule,
                          seed, offset);
   if (rc) return rc;

@@ -147,7 +147,27 @@ struct DqArgs {
   int split_base, split_s;
   float* ws;
   uint32_t* ws_count;
+  // grouped (per-expert) modes, the GRP template parameter; offsets int32
+  // [n_experts + 1] into rows sorted by expert:
+  //   GRP_ROWS: expert e owns the rows [offsets[e], offsets[e+1]) of A and of
+  //     Y and multiplies its own B, at b.p + e*b_estride bytes with scales at
+  //     b.s + e*bs_estride (the dgrad of every expert's Linear at once);
+  //   GRP_K: the contraction of expert e runs over those rows of both
+  //     (transposed) operands, and its Y, of M x N, lies at y + e*y_estride
+  //     bytes (the wgrad of every expert's Linear at once).
+  const int32_t* offsets;
+  int n_experts;
+  int64_t b_estride, bs_estride, y_estride;
+  // IL kernels: the contraction is one half of a gate / up interleaved
+  // operand (128-wide blocks alternating gate block t and up block t): logical
+  // K step kt reads physical step 4*(kt/2) + kt%2 + 2*il_half of both operands
+  int il_half;
+  // add the bf16 output to what y holds: y = bf16(y + bf16(acc)), the sum of
+  // two Linears' input gradients as autograd forms it
+  int accum;
 };
+
+constexpr int GRP_NONE = 0, GRP_ROWS = 1, GRP_K = 2;
 
 // 4 codes (byte i = element i) times s in fp32: the reference's q * scale
 template <int GRID>
@@ -404,36 +424,91 @@ struct Direct {
   }
 };
 
-template <int EL, int SA, int SB, int GRID, int SCM>
+template <int EL, int SA, int SB, int GRID, int SCM, int GRP = GRP_NONE, bool IL = false>
 __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t la0[TILE];
   __shared__ __attribute__((aligned(16))) uint8_t lb0[TILE];
   __shared__ __attribute__((aligned(16))) uint8_t la1[TILE];
   __shared__ __attribute__((aligned(16))) uint8_t lb1[TILE];
   constexpr int EB = ElemT<EL>::bytes;
+  constexpr int KSTEP = ElemT<EL>::kstep;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
 
   // workgroup -> tile: each XCD walks a contiguous range of the whole tiles,
   // grouped raster of GROUP_M row tiles; the split tail's ranges keep their
   // tile
+  constexpr int GROUP_M = 4;
+  auto xcd_local = [](int p, int nwg) {
+    const int xcd = p & 7, local = p >> 3;
+    const int per = nwg >> 3, extra = nwg & 7;
+    return xcd * per + min(xcd, extra) + local;
+  };
+  // tile l of a num_m x num_n raster of GROUP_M row tiles
+  auto raster = [](int l, int num_m, int num_n, int64_t& m0, int64_t& n0) {
+    const int group = l / (GROUP_M * num_n);
+    const int first_m = group * GROUP_M;
+    const int gsize = min(num_m - first_m, GROUP_M);
+    const int in_group = l - group * GROUP_M * num_n;
+    m0 = (int64_t)(first_m + in_group % gsize) * TM;
+    n0 = (int64_t)(in_group / gsize) * TN;
+  };
   const int num_n = (int)((g.N + TN - 1) / TN);
   const int num_m = (int)((g.M + TM - 1) / TM);
-  const SplitWork sw = split_work(blockIdx.x, g.split_base, g.split_s);
-  int pid = sw.pid;
-  if (sw.tail < 0) {
-    const int nwg = g.split_s > 1 ? g.split_base : num_m * num_n;
-    const int xcd = pid & 7, local = pid >> 3;
-    const int per = nwg >> 3, extra = nwg & 7;
-    pid = xcd * per + min(xcd, extra) + local;
+  SplitWork sw{(int)blockIdx.x, -1, 0};
+  int64_t m0, n0;
+  int nk = (int)(g.Kc / KSTEP);
+  if constexpr (GRP == GRP_ROWS) {
+    // experts in order, each one's row tiles in the raster of the dense case;
+    // the grid is an upper bound on the tile count (the offset table is read
+    // into LDS, free until the first copy, and the tiles counted there)
+    int32_t* tab = reinterpret_cast<int32_t*>(la0);
+    for (int i = tid; i <= g.n_experts; i += NT) tab[i] = g.offsets[i];
+    __syncthreads();
+    int total = 0;
+    for (int i = 0; i < g.n_experts; ++i) total += (int)((tab[i + 1] - tab[i] + TM - 1) / TM) * num_n;
+    int pid = (int)blockIdx.x;
+    if (pid < total) pid = xcd_local(pid, total);
+    int e = 0, before = 0, tiles_m = 0;
+    int64_t lo = 0, hi = 0;
+    for (; e < g.n_experts; ++e) {
+      lo = tab[e];
+      hi = tab[e + 1];
+      tiles_m = (int)((hi - lo + TM - 1) / TM);
+      if (pid < before + tiles_m * num_n) break;
+      before += tiles_m * num_n;
+    }
+    __syncthreads();  // the table's LDS is a copy target from here on
+    if (e >= g.n_experts) return;  // past the last expert's tiles
+    raster(pid - before, tiles_m, num_n, m0, n0);
+    m0 += lo;
+    g.M = hi;  // rows at or past the expert's end are not stored
+    g.b.p += (int64_t)e * g.b_estride;
+    g.b.s += (int64_t)e * g.bs_estride;
+  } else if constexpr (GRP == GRP_K) {
+    // every expert has the num_m x num_n tiles of its own Y; its contraction
+    // is its rows, so both operands start at row offsets[e] and hold
+    // offsets[e+1] - offsets[e] valid rows (zero past them, through the
+    // buffer resources); an expert without rows stores zeros
+    const int per = num_m * num_n;
+    const int pid = xcd_local((int)blockIdx.x, per * g.n_experts);
+    const int e = pid / per;
+    raster(pid - e * per, num_m, num_n, m0, n0);
+    const int64_t lo = g.offsets[e], rows_e = g.offsets[e + 1] - lo;
+    g.a.p += lo * g.a.ld * EB;
+    g.a.kvalid = rows_e;
+    g.b.p += lo * g.b.ld;
+    g.b.s += lo;  // per-row scales, consecutive along the contraction
+    g.b.s_extent -= lo;
+    g.b.kvalid = rows_e;
+    nk = max(1, (int)((rows_e + KSTEP - 1) / KSTEP));
+    g.y = reinterpret_cast<uint8_t*>(g.y) + (int64_t)e * g.y_estride;
+  } else {
+    sw = split_work(blockIdx.x, g.split_base, g.split_s);
+    int pid = sw.pid;
+    if (sw.tail < 0) pid = xcd_local(pid, g.split_s > 1 ? g.split_base : num_m * num_n);
+    raster(pid, num_m, num_n, m0, n0);
   }
-  constexpr int GROUP_M = 4;
-  const int group = pid / (GROUP_M * num_n);
-  const int first_m = group * GROUP_M;
-  const int gsize = min(num_m - first_m, GROUP_M);
-  const int in_group = pid - group * GROUP_M * num_n;
-  const int64_t m0 = (int64_t)(first_m + in_group % gsize) * TM;
-  const int64_t n0 = (int64_t)(in_group / gsize) * TN;
 
   Direct da, db;
   if constexpr (SA == SRC_DIRECT) da.init(g.a, m0, wave, lane, EB);
@@ -443,14 +518,17 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   sa.init(g.a, m0, tid, lane);
   sb.init(g.b, n0, tid, lane);
 
-  const int nk = (int)(g.Kc / ElemT<EL>::kstep);
+  // logical K step -> the step the loaders read (IL: one half of the
+  // interleaved gate / up contraction)
+  const int il_half = g.il_half;
+  auto kmap = [il_half](int kt) { return IL ? ((kt >> 1) << 2) + (kt & 1) + 2 * il_half : kt; };
   // K steps [kb0, kb1) of this workgroup: all of them, or one split range
   const int kb0 = sw.tail >= 0 ? (int)((int64_t)sw.chunk * nk / g.split_s) : 0;
   const int kb1 = sw.tail >= 0 ? (int)((int64_t)(sw.chunk + 1) * nk / g.split_s) : nk;
   // the epilogue's arguments, kept in scalar registers through the K loop
   uintptr_t e_y = reinterpret_cast<uintptr_t>(g.y), e_bias = reinterpret_cast<uintptr_t>(g.bias);
   int64_t e_ldy = g.ldy, e_M = g.M, e_N = g.N;
-  int e_misc = (g.vec_out ? 1 : 0) | (g.bias_dtype << 1) | (g.y_dtype << 4);
+  int e_misc = (g.vec_out ? 1 : 0) | (g.bias_dtype << 1) | (g.y_dtype << 4) | (g.accum ? 128 : 0);
   e_y = uniform64(e_y); e_bias = uniform64(e_bias);
   e_ldy = uniform64(e_ldy); e_M = uniform64(e_M); e_N = uniform64(e_N);
   e_misc = __builtin_amdgcn_readfirstlane(e_misc);
@@ -465,17 +543,17 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   // prologue: block kb0 into stage 0, block kb0+1's raw data into registers
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    if constexpr (SA == SRC_DIRECT) da.issue(la0, kb0, wave, j);
-    if constexpr (SB == SRC_DIRECT) db.issue(lb0, kb0, wave, j);
+    if constexpr (SA == SRC_DIRECT) da.issue(la0, kmap(kb0), wave, j);
+    if constexpr (SB == SRC_DIRECT) db.issue(lb0, kmap(kb0), wave, j);
   }
-  sa.load(g.a, kb0);
-  sb.load(g.b, kb0);
+  sa.load(g.a, kmap(kb0));
+  sb.load(g.b, kmap(kb0));
   sa.template decode_half<0>(g.a, la0);
   sb.template decode_half<0>(g.b, lb0);
   sa.template decode_half<1>(g.a, la0);
   sb.template decode_half<1>(g.b, lb0);
-  sa.load(g.a, min(kb0 + 1, kb1 - 1));
-  sb.load(g.b, min(kb0 + 1, kb1 - 1));
+  sa.load(g.a, kmap(min(kb0 + 1, kb1 - 1)));
+  sb.load(g.b, kmap(min(kb0 + 1, kb1 - 1)));
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -498,8 +576,8 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
       v8i af_next;
       if (tm + 1 < 8) af_next = frag(ta, wm * 128 + (tm + 1) * 16, lane);
       if (tm < 4) {
-        if constexpr (SA == SRC_DIRECT) da.issue(na, kn, wave, tm);
-        if constexpr (SB == SRC_DIRECT) db.issue(nb, kn, wave, tm);
+        if constexpr (SA == SRC_DIRECT) da.issue(na, kmap(kn), wave, tm);
+        if constexpr (SB == SRC_DIRECT) db.issue(nb, kmap(kn), wave, tm);
       }
       if (tm == 4) {
         sa.template decode_half<0>(g.a, na);
@@ -517,8 +595,8 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     // every copy of this step has landed (vmcnt(0)); then block kt+2's raw
     // data goes out and stays in flight across the barrier
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    sa.load(g.a, min(kt + 2, kb1 - 1));
-    sb.load(g.b, min(kt + 2, kb1 - 1));
+    sa.load(g.a, kmap(min(kt + 2, kb1 - 1)));
+    sb.load(g.b, kmap(min(kt + 2, kb1 - 1)));
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the decode's LDS writes are done
     __syncthreads();
   };
@@ -592,6 +670,20 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
         const int64_t n = n0e + wn * 64 + c * epc;
         const uint8_t* src = stage_w + row * pitch + c * 16;
         uint8_t* ydst = reinterpret_cast<uint8_t*>(e_y) + (m * e_ldy + n) * esz;
+        if constexpr (ODT == DT_BF16) {
+          if (e_misc & 128) {
+            // y = bf16(y + bf16(acc)) (bf16 output only)
+            if (!FULL && (m >= e_M || n >= e_N)) continue;
+            const int cnt = FULL ? epc : (int)min<int64_t>(epc, e_N - n);
+#pragma nounroll
+            for (int e = 0; e < cnt; ++e) {
+              uint16_t* yp = reinterpret_cast<uint16_t*>(ydst) + e;
+              const float a = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[e]);
+              *yp = f32_to_bf16_bits(bf16_bits_to_f32(*yp) + a);
+            }
+            continue;
+          }
+        }
         if constexpr (FULL) {
           store16_nt(ydst, src);
           continue;
@@ -756,6 +848,18 @@ int dispatch(int el, int sa, int sb, const DqArgs& g, hipStream_t st) {
   return fail(NTLB_EUNSUPPORTED, "gemm_dq: operand sources (%d, %d) are not built for element type %d", sa, sb, el);
 }
 
+// the grouped GEMMs of the expert MLP backward: bf16 operands, the weights'
+// 128x128 block scales (dgrad) or the activations' per-row 1x128 scales
+// (wgrad)
+template <int SA, int SB, int SCM, int GRP, bool IL = false>
+void launch_grouped(const DqArgs& g, int64_t wgs, hipStream_t st) {
+  const int grid = SB == SRC_TCODES ? g.b.grid : g.a.grid;
+  if (grid == GRID_E4M3)
+    gemm_dq_kernel<EL_BF16, SA, SB, GRID_E4M3, SCM, GRP, IL><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
+  else
+    gemm_dq_kernel<EL_BF16, SA, SB, GRID_INT, SCM, GRP, IL><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
+}
+
 int elem_of(int op_dtype, const char* fn, int& el) {
   if (op_dtype == NTLB_BF16) el = EL_BF16;
   else if (op_dtype == NTLB_F32) el = EL_F32;
@@ -844,7 +948,7 @@ extern "C" int ntlb_gemm_dq_forward(int op_dtype, int grid, const uint8_t* a, in
   if (!y) return fail(NTLB_EINVAL, "%s: NULL output", fn);
   if (int rc = check_codes(fn, "A", a, lda, M, Kp, sa, a_shift, grid)) return rc;
   if (int rc = check_codes(fn, "B", b, ldb, N, Kp, sb, b_shift, grid)) return rc;
-  DqArgs g;
+  DqArgs g{};
   g.a = Operand{a, lda, M, Kp, sa, sa_row, sa_col, a_shift, 7, grid, 0, 0};
   g.b = Operand{b, ldb, N, Kp, sb, sb_row, sb_col, b_shift, 7, grid, 0, 0};
   g.M = M; g.N = N; g.Kc = Kp;
@@ -882,7 +986,7 @@ extern "C" int ntlb_gemm_ste_dgrad_ws(int op_dtype, const void* dy, int64_t lddy
   const int64_t Kp = (K + 127) / 128 * 128;
   if (int rc = check_codes(fn, "W", w, ldw, N, Kp, sw, w_shift, grid)) return rc;
   if (ldw % 4) return fail(NTLB_EINVAL, "%s: W ld must be a multiple of 4", fn);
-  DqArgs g;
+  DqArgs g{};
   g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, M, Nc, nullptr, 0, 0, 0, 0, 0, 0, 0};
   // W^T as the B operand: element (r = k, c = n) of the codes [N, ldw]
   g.b = Operand{w, ldw, Kp, N, sw, sw_col, sw_row, 7, w_shift, grid, 0, 0};
@@ -916,7 +1020,7 @@ extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, i
   const int64_t Kp = (K + 127) / 128 * 128;
   if (int rc = check_codes(fn, "X", x, ldx, M, Kp, sx, x_shift, grid)) return rc;
   const int64_t Mc = (M + 63) / 64 * 64;  // contraction over the tokens, zero past M
-  DqArgs g;
+  DqArgs g{};
   // dY^T as the A operand: element (r = n, c = m) at dy[m * lddy + n]
   g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, N, M, nullptr, 0, 0, 0, 0, 0, 0, 0};
   // X^T as the B operand: element (r = k, c = m) of the codes [M, ldx]
@@ -925,6 +1029,138 @@ extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, i
   g.M = N; g.N = K; g.Kc = Mc;
   g.bias = nullptr; g.bias_dtype = 0; g.y = dw;
   return finish(fn, g, el, SRC_TDIRECT, SRC_TCODES, dw_dtype, lddw, stream);
+}
+
+// offset table of rows sorted by expert, as the grouped kernels read it
+static int check_offsets(const char* fn, const int32_t* offsets, int n_experts) {
+  if (!offsets) return fail(NTLB_EINVAL, "%s: NULL offsets", fn);
+  if (n_experts < 1 || n_experts >= TILE / 4) return fail(NTLB_EINVAL, "%s: n_experts must be in [1, %d)", fn, TILE / 4);
+  return NTLB_OK;
+}
+
+extern "C" int ntlb_gemm_grouped_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                           const int32_t* offsets, int n_experts, int grid, const uint8_t* w,
+                                           int64_t ldw, int64_t w_estride, const float* sw, int64_t sw_row,
+                                           int64_t sw_col, int w_shift, int64_t sw_estride, int64_t K, void* dx,
+                                           int dx_dtype, int64_t lddx, void* stream) {
+  const char* fn = "ntlb_gemm_grouped_ste_dgrad";
+  int el;
+  if (int rc = elem_of(op_dtype, fn, el)) return rc;
+  if (el != EL_BF16) return fail(NTLB_EUNSUPPORTED, "%s: coded W needs bf16 operands", fn);
+  if (R < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (R == 0 || K == 0) return NTLB_OK;
+  if (N == 0) return fail(NTLB_EUNSUPPORTED, "%s: N == 0 (dX is zero)", fn);
+  if (!dy || !dx) return fail(NTLB_EINVAL, "%s: NULL dY or dX", fn);
+  if (int rc = check_offsets(fn, offsets, n_experts)) return rc;
+  const int kstep = 64, eb = 2;
+  const int64_t Nc = (N + kstep - 1) / kstep * kstep;
+  if (lddy < Nc || !aligned(dy, 16) || (lddy * eb) % 16)
+    return fail(NTLB_EINVAL, "%s: dY needs ld >= N rounded up to %d (zero pad columns), 16-byte rows and alignment",
+                fn, kstep);
+  if ((R + 256) * lddy * eb >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: dY exceeds 2 GiB", fn);
+  const int64_t Kp = (K + 127) / 128 * 128;
+  if (int rc = check_codes(fn, "W", w, ldw, N, Kp, sw, w_shift, grid)) return rc;
+  if (ldw % 4 || w_estride < N * ldw || w_estride % 16) return fail(NTLB_EINVAL, "%s: bad W ld or expert stride", fn);
+  if (!valid_dtype(dx_dtype) || lddx < K) return fail(NTLB_EINVAL, "%s: bad dX dtype or ld", fn);
+  DqArgs g{};
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, R, Nc, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  // W_e^T as the B operand: element (r = k, c = n) of expert e's codes [N, ldw]
+  g.b = Operand{w, ldw, Kp, N, sw, sw_col, sw_row, 7, w_shift, grid, 0, 0};
+  if (int rc = tcodes_scales(fn, g.b)) return rc;
+  if (g.b.smode != SC_SHARED) return fail(NTLB_EUNSUPPORTED, "%s: W needs block or tensor scales", fn);
+  g.M = R; g.N = K; g.Kc = Nc;
+  g.y = dx; g.y_dtype = dx_dtype; g.ldy = lddx;
+  g.vec_out = aligned(dx, 16) && ((lddx * dtype_size(dx_dtype)) % 16 == 0);
+  g.offsets = offsets; g.n_experts = n_experts;
+  g.b_estride = w_estride; g.bs_estride = sw_estride;
+  const int64_t num_n = (K + TN - 1) / TN;
+  const int64_t wgs = ((R + TM - 1) / TM + n_experts) * num_n;  // at least every expert's row tiles
+  if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  launch_grouped<SRC_DIRECT, SRC_TCODES, SC_SHARED, GRP_ROWS>(g, wgs, as_stream(stream));
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_grouped_ste_dgrad_gate_up(int op_dtype, const void* dgu, int64_t lddgu, int64_t R,
+                                                   int64_t I, const int32_t* offsets, int n_experts, int grid,
+                                                   const uint8_t* w, int64_t ldw, int64_t w_estride, const float* sw,
+                                                   int64_t sw_row, int64_t sw_col, int64_t sw_estride, int64_t K,
+                                                   void* dx, int64_t lddx, void* stream) {
+  const char* fn = "ntlb_gemm_grouped_ste_dgrad_gate_up";
+  int el;
+  if (int rc = elem_of(op_dtype, fn, el)) return rc;
+  if (el != EL_BF16) return fail(NTLB_EUNSUPPORTED, "%s: coded W needs bf16 operands", fn);
+  if (R < 0 || I < 0 || K < 0 || I % 128) return fail(NTLB_EINVAL, "%s: bad shape (I %% 128 == 0)", fn);
+  if (R == 0 || K == 0) return NTLB_OK;
+  if (I == 0) return fail(NTLB_EUNSUPPORTED, "%s: I == 0 (dX is zero)", fn);
+  if (!dgu || !dx) return fail(NTLB_EINVAL, "%s: NULL dY or dX", fn);
+  if (int rc = check_offsets(fn, offsets, n_experts)) return rc;
+  const int64_t N = 2 * I, eb = 2;
+  if (lddgu < N || !aligned(dgu, 16) || (lddgu * eb) % 16)
+    return fail(NTLB_EINVAL, "%s: d_gate_up needs ld >= 2I, 16-byte rows and alignment", fn);
+  if ((R + 256) * lddgu * eb >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: dY exceeds 2 GiB", fn);
+  const int64_t Kp = (K + 127) / 128 * 128;
+  if (int rc = check_codes(fn, "W", w, ldw, N, Kp, sw, 7, grid)) return rc;
+  if (ldw % 4 || w_estride < N * ldw || w_estride % 16) return fail(NTLB_EINVAL, "%s: bad W ld or expert stride", fn);
+  if (lddx < K) return fail(NTLB_EINVAL, "%s: bad dX ld", fn);
+  DqArgs g{};
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dgu), lddgu, R, N, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.b = Operand{w, ldw, Kp, N, sw, sw_col, sw_row, 7, 7, grid, 0, 0};
+  if (int rc = tcodes_scales(fn, g.b)) return rc;
+  if (g.b.smode != SC_SHARED) return fail(NTLB_EUNSUPPORTED, "%s: W needs block scales", fn);
+  g.M = R; g.N = K; g.Kc = I;  // one half of the interleaved contraction per launch
+  g.y = dx; g.y_dtype = DT_BF16; g.ldy = lddx;
+  g.vec_out = aligned(dx, 16) && ((lddx * 2) % 16 == 0);
+  g.offsets = offsets; g.n_experts = n_experts;
+  g.b_estride = w_estride; g.bs_estride = sw_estride;
+  const int64_t num_n = (K + TN - 1) / TN;
+  const int64_t wgs = ((R + TM - 1) / TM + n_experts) * num_n;
+  if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  hipStream_t st = as_stream(stream);
+  // the gate Linear's input gradient, then the up Linear's added to it in bf16
+  g.il_half = 0; g.accum = 0;
+  launch_grouped<SRC_DIRECT, SRC_TCODES, SC_SHARED, GRP_ROWS, true>(g, wgs, st);
+  g.il_half = 1; g.accum = 1;
+  launch_grouped<SRC_DIRECT, SRC_TCODES, SC_SHARED, GRP_ROWS, true>(g, wgs, st);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_grouped_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                           const int32_t* offsets, int n_experts, int grid, const uint8_t* x,
+                                           int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col, int x_shift,
+                                           int64_t K, void* dw, int dw_dtype, int64_t lddw, int64_t dw_estride,
+                                           void* stream) {
+  const char* fn = "ntlb_gemm_grouped_ste_wgrad";
+  int el;
+  if (int rc = elem_of(op_dtype, fn, el)) return rc;
+  if (el != EL_BF16) return fail(NTLB_EUNSUPPORTED, "%s: coded X needs bf16 operands", fn);
+  if (R < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (N == 0 || K == 0) return NTLB_OK;
+  if (!dy || !dw) return fail(NTLB_EINVAL, "%s: NULL dY or dW", fn);
+  if (int rc = check_offsets(fn, offsets, n_experts)) return rc;
+  if (lddy < N || !aligned(dy, 16) || lddy % 8)
+    return fail(NTLB_EINVAL, "%s: dY needs ld >= N, ld %% 8 == 0 and 16-byte alignment", fn);
+  if ((R + 64) * lddy * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: dY exceeds 2 GiB", fn);
+  const int64_t Kp = (K + 127) / 128 * 128;
+  if (int rc = check_codes(fn, "X", x, ldx, R, Kp, sx, x_shift, grid)) return rc;
+  if (!valid_dtype(dw_dtype) || lddw < K) return fail(NTLB_EINVAL, "%s: bad dW dtype or ld", fn);
+  if (dw_estride < N * lddw * dtype_size(dw_dtype)) return fail(NTLB_EINVAL, "%s: dW expert stride too small", fn);
+  DqArgs g{};
+  // dY^T as the A operand: element (r = n, c = m) at dy[m * lddy + n]; the
+  // kernel moves both operands to the expert's first row
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, N, R, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  // X^T as the B operand: element (r = k, c = m) of the codes [R, ldx]
+  g.b = Operand{x, ldx, Kp, R, sx, sx_col, sx_row, 7, x_shift, grid, 0, 0};
+  if (int rc = tcodes_scales(fn, g.b)) return rc;
+  if (g.b.smode != SC_CONTIG) return fail(NTLB_EUNSUPPORTED, "%s: X needs per-row (1x128) scales", fn);
+  g.M = N; g.N = K; g.Kc = (R + 63) / 64 * 64;
+  g.y = dw; g.y_dtype = dw_dtype; g.ldy = lddw;
+  g.vec_out = aligned(dw, 16) && ((lddw * dtype_size(dw_dtype)) % 16 == 0) && dw_estride % 16 == 0;
+  g.offsets = offsets; g.n_experts = n_experts;
+  g.y_estride = dw_estride;
+  const int64_t wgs = ((N + TM - 1) / TM) * ((K + TN - 1) / TN) * n_experts;
+  if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  launch_grouped<SRC_TDIRECT, SRC_TCODES, SC_CONTIG, GRP_K>(g, wgs, as_stream(stream));
+  return check_launch(fn);
 }
 
 extern "C" int ntlb_gemm_dense(int op_dtype, const void* a, int64_t lda, int a_trans, const void* b, int64_t ldb,
@@ -942,7 +1178,7 @@ extern "C" int ntlb_gemm_dense(int op_dtype, const void* a, int64_t lda, int a_t
   if (K == 0 || K % kstep) return fail(NTLB_EUNSUPPORTED, "%s: K must be a positive multiple of %d", fn, kstep);
   if (lda < K || !aligned(a, 16) || (lda * eb) % 16) return fail(NTLB_EINVAL, "%s: A needs ld >= K, 16-byte rows", fn);
   if ((M + 256) * lda * eb >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: A exceeds 2 GiB", fn);
-  DqArgs g;
+  DqArgs g{};
   g.a = Operand{reinterpret_cast<const uint8_t*>(a), lda, M, K, nullptr, 0, 0, 0, 0, 0, 0, 0};
   int sb;
   if (b_trans) {
@@ -976,7 +1212,7 @@ extern "C" int ntlb_gemm_dense_tn(int op_dtype, const void* a, int64_t lda, cons
   if ((K + 64) * lda * eb >= (int64_t)0x7FFFFFFF || (K + 64) * ldb * eb >= (int64_t)0x7FFFFFFF)
     return fail(NTLB_EUNSUPPORTED, "%s: an operand exceeds 2 GiB", fn);
   const int kstep = el == EL_BF16 ? 64 : 32;
-  DqArgs g;
+  DqArgs g{};
   // Y[M,N] = A^T B with A stored [K, M] and B stored [K, N]: both operands transposed
   g.a = Operand{reinterpret_cast<const uint8_t*>(a), lda, M, K, nullptr, 0, 0, 0, 0, 0, 0, 0};
   g.b = Operand{reinterpret_cast<const uint8_t*>(b), ldb, N, K, nullptr, 0, 0, 0, 0, 0, 0, 0};

@@ -101,6 +101,19 @@ SIGNATURES = {
     "ntlb_ep_combine": [_P, _I64, _I64, _P, _I32, _P, _I32, _I64, _I64, _I32, _P, _I32, _I64, _P, _P],
     "ntlb_comm_quant_dequant": [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _I32, _I32, _U64, _U64, _P,
                                 _I64, _P],
+    "ntlb_gemm_grouped_ste_dgrad": [_I32, _P, _I64, _I64, _I64, _P, _I32, _I32, _P, _I64, _I64, _P, _I64, _I64, _I32,
+                                    _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_grouped_ste_dgrad_gate_up": [_I32, _P, _I64, _I64, _I64, _P, _I32, _I32, _P, _I64, _I64, _P, _I64,
+                                            _I64, _I64, _I64, _P, _I64, _P],
+    "ntlb_gemm_grouped_ste_wgrad": [_I32, _P, _I64, _I64, _I64, _P, _I32, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64,
+                                    _P, _I32, _I64, _I64, _P],
+    "ntlb_gemm_grouped_swiglu_quant_gu": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I64,
+                                          _P, _I32, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _P,
+                                          _I32, _I32, _I32, _U64, _U64, _P, _I64, _P],
+    "ntlb_moe_capacity_keep": [_P, _P, _I32, _I64, _I64, _P, _I32, _I64, _P, _P, _P, _P, _P],
+    "ntlb_moe_combine_backward": [_P, _I64, _P, _I64, _I32, _P, _P, _I32, _I64, _I64, _I64, _P, _I64, _P, _P],
+    "ntlb_moe_token_grad": [_P, _I64, _I32, _P, _P, _I32, _I64, _I64, _I64, _P, _I64, _P],
+    "ntlb_swiglu_backward": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P],
     "ntlb_ep_unpack_records": [_P, _I64, _I64, _P, _I64, _P, _I32, _P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P],
 }
 

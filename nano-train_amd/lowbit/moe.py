@@ -30,6 +30,7 @@ sorted by expert.
 from __future__ import annotations
 
 import itertools
+import math
 from dataclasses import dataclass
 from typing import Optional
 
@@ -143,30 +144,73 @@ class ExpertRouting:
     """The (token, slot) assignments of top-k routing ordered by expert.
 
     pos[a] is assignment a's row in expert order (a = token * top_k + slot),
-    inv[row] the assignment of a row; rows of one expert keep assignment
-    order, as the reference's (topk_indices == e).nonzero() lists them.
-    offsets int32 [E+1] is the token-offset table of the grouped GEMMs."""
+    or -1 when a capacity dropped it; inv[row] the assignment of a row; rows
+    of one expert keep assignment order, as the reference's
+    (topk_indices == e).nonzero() lists them, or under a capacity the kept
+    rows highest routing weight first (torch.topk(sorted=True)).  offsets
+    int32 [E+1] is the token-offset table of the grouped GEMMs; counts int64
+    [E] the rows per expert (the reference's token_counts / local_counts).
+    Buffers over rows are sized for every assignment (`rows`); under a
+    capacity the rows past offsets[E] are unused, so no host sync is needed."""
 
     pos: torch.Tensor  # int32 [T*top_k]
     inv: torch.Tensor  # int32 [T*top_k]
     counts: torch.Tensor  # int64 [E]
     offsets: torch.Tensor  # int32 [E+1]
     top_k: int
+    capacity: int = 0
 
     @property
     def rows(self) -> int:
         return self.pos.numel()
 
+    def dropped(self) -> int:
+        """Assignments a capacity dropped (moe.py:1082; a device-to-host read)."""
+        return self.rows - int(self.counts.sum().item())
 
-def route_by_expert(expert_ids: torch.Tensor, n_experts: int) -> ExpertRouting:
+
+def compute_capacity(capacity_factor: float, num_tokens: int, top_k: int, num_experts: int) -> int:
+    """Per-expert capacity of LocalRoutedMoE._compute_capacity (moe.py:432-439):
+    ceil(capacity_factor * tokens * top_k / experts), at least 1; 0 tokens -> 0."""
+    if capacity_factor <= 0:
+        raise ValueError("capacity_factor must be positive")
+    if num_tokens <= 0:
+        return 0
+    expected = (num_tokens * top_k) / float(num_experts)
+    return max(int(math.ceil(capacity_factor * expected)), 1)
+
+
+def route_by_expert(expert_ids: torch.Tensor, n_experts: int, *, capacity: int = 0,
+                    topk_w: Optional[torch.Tensor] = None) -> ExpertRouting:
     """One stable counting sort of expert_ids [T, k] (int32 or int64) by
-    expert on the GPU (ntlb_ep_partition: three kernels, no host sync)."""
+    expert on the GPU (ntlb_ep_partition: three kernels, no host sync).
+
+    capacity > 0 keeps, per expert with more rows than that, the `capacity`
+    rows of highest routing weight topk_w [T, k], highest first
+    (ntlb_moe_capacity_keep: moe.py:1077-1081 / :482-486,
+    torch.topk(sort_weights, k=capacity, sorted=True); equal weights keep
+    row order)."""
     from . import ep
 
     if expert_ids.dim() != 2:
         raise ValueError("expert_ids must be [tokens, top_k]")
     pos, inv, counts, offsets = ep.partition(expert_ids.reshape(-1), divisor=1, buckets=n_experts)
-    return ExpertRouting(pos, inv, counts, offsets, expert_ids.shape[1])
+    k = expert_ids.shape[1]
+    if capacity <= 0:
+        return ExpertRouting(pos, inv, counts, offsets, k)
+    if topk_w is None or topk_w.shape != expert_ids.shape:
+        raise ValueError("a capacity needs the routing weights topk_w [tokens, top_k]")
+    ops._require_device(topk_w)
+    w = topk_w.detach().contiguous()
+    n = pos.numel()
+    pos2 = torch.empty_like(pos)
+    inv2 = torch.empty_like(inv)
+    offsets2 = torch.empty_like(offsets)
+    counts2 = torch.empty_like(counts)
+    _lib.call("ntlb_moe_capacity_keep", inv.data_ptr(), offsets.data_ptr(), n_experts, n, n, w.data_ptr(),
+              ops._dtype_code(w.dtype), capacity, pos2.data_ptr(), inv2.data_ptr(), offsets2.data_ptr(),
+              counts2.data_ptr(), ops._stream())
+    return ExpertRouting(pos2, inv2, counts2, offsets2, k, capacity)
 
 
 def sort_by_expert(expert_ids: torch.Tensor, n_experts: int):
@@ -336,10 +380,12 @@ def local_moe_forward(
     seed: int = 0,
     offset: int = 0,
     routing: Optional[ExpertRouting] = None,
+    capacity: int = 0,
 ):
     """The single-rank routed expert loop (moe.py:1062-1093, LocalRoutedMoE
-    :476-491 without capacity drop) for all local experts at once: returns
-    the token outputs [T, H] in tokens.dtype.
+    :476-491) for all local experts at once, forward only: returns the token
+    outputs [T, H] in tokens.dtype.  capacity > 0 drops, per expert, all but
+    the `capacity` rows of highest routing weight (route_by_expert).
 
     Kernels: the routing sort (skipped when `routing` is given), the 1x128
     quantization of the token rows gathered by expert (each token row read
@@ -347,9 +393,161 @@ def local_moe_forward(
     epilogue, the down GEMM, and the weighted combine into token order.  gate_up
     and down are as for expert_mlp()."""
     if routing is None:
-        routing = route_by_expert(expert_ids, n_experts)
+        routing = route_by_expert(expert_ids, n_experts, capacity=capacity, topk_w=topk_w)
     qx = ops.quant_tile_1x128_fanout(tokens, routing.pos, routing.top_k, routing.rows, fmt=fmt, bits=bits,
                                      rounding=rounding, seed=seed, offset=offset, want_nan_rows=True)
     y = expert_mlp(qx, routing.offsets, gate_up, down, fmt=fmt, bits=bits, rounding=rounding, seed=seed,
                    offset=offset, out_dtype=tokens.dtype)
     return combine_rows(y, routing, expert_ids, topk_w, tokens.shape[0])
+
+
+def stack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """Gate and up weights [E, I, H] (the experts' gate_proj / up_proj,
+    moe.py:160-177) as the one [E, 2I, H] tensor that local_moe() trains:
+    128-row blocks alternating gate block t and up block t, the row order of
+    interleave_gate_up()'s codes.  A copy; split_gate_up() gives the two back
+    as views."""
+    if w_gate.shape != w_up.shape or w_gate.dim() != 3:
+        raise ValueError("gate and up weights must both be [E, I, H]")
+    E, I, H = w_gate.shape
+    if I % 128:
+        raise ValueError(f"intermediate size {I} must be a multiple of 128")
+    nb = I // 128
+    return torch.stack([w_gate.reshape(E, nb, 128, H), w_up.reshape(E, nb, 128, H)], dim=2).reshape(E, 2 * I, H)
+
+
+def split_gate_up(w_gate_up: torch.Tensor):
+    """(gate, up) views [E, I/128, 128, H] of stack_gate_up()'s layout."""
+    E, N2, H = w_gate_up.shape
+    v = w_gate_up.reshape(E, N2 // 256, 2, 128, H)
+    return v[:, :, 0], v[:, :, 1]
+
+
+class _LocalMoE(torch.autograd.Function):
+    """The single-rank expert loop with its backward on HIP kernels.
+
+    Forward: local_moe_forward's kernels, with the two projections' bf16
+    outputs kept for the SwiGLU backward.  Backward, the autograd of the
+    reference's loop (moe.py:1062-1093: tokens[token_indices] -> ExpertMLP ->
+    `output[token_indices] += expert_out * weights`, each expert Linear the
+    straight-through estimator of te_backend.py:250-259):
+      ntlb_moe_combine_backward   dY rows = d_out[token] * w, and the
+                                  routing-weight gradient sum_H d_out * y;
+      ntlb_gemm_grouped_ste_dgrad dH = dY . bf16(dq(W_down[e])) per expert;
+      ntlb_swiglu_backward        d_gate, d_up through F.silu(gate) * up;
+      ntlb_gemm_grouped_ste_dgrad_gate_up  dX rows = bf16(d_gate . W_gate_q) +
+                                  bf16(d_up . W_up_q), added in bf16 (x feeds
+                                  both Linears);
+      ntlb_moe_token_grad         the token gradient: each token's rows in
+                                  descending expert id, each add rounded
+                                  (autograd's order over the loop);
+      ntlb_gemm_grouped_ste_wgrad dW_down[e] = dY^T . bf16(dq(h)), dW_gate_up[e]
+                                  = [d_gate | d_up]^T . bf16(dq(x)) over the
+                                  expert's rows only."""
+
+    @staticmethod
+    def forward(ctx, tokens, topk_w, w_gate_up, w_down, expert_ids, n_experts, capacity, cfg):
+        fmt, bits, rounding, seed, offset = cfg
+        T, H = tokens.shape
+        E, N2, _ = w_gate_up.shape
+        I = N2 // 2
+        routing = route_by_expert(expert_ids, n_experts, capacity=capacity, topk_w=topk_w)
+        gu_codes, gu_scales, gu_nan = quantize_expert_weights(w_gate_up.detach(), fmt=fmt, bits=bits,
+                                                              rounding=rounding, seed=seed, offset=offset + 2)
+        d_codes, d_scales, d_nan = quantize_expert_weights(w_down.detach(), fmt=fmt, bits=bits, rounding=rounding,
+                                                           seed=seed, offset=offset + 3)
+        qx = ops.quant_tile_1x128_fanout(tokens.detach(), routing.pos, routing.top_k, routing.rows, fmt=fmt,
+                                         bits=bits, rounding=rounding, seed=seed, offset=offset, want_nan_rows=True)
+        train = any(ctx.needs_input_grad[:4])
+        gu = torch.empty((routing.rows, N2), dtype=torch.bfloat16, device=tokens.device) if train else None
+        _, qh = ops.gemm_swiglu_quant(qx, gu_codes, gu_scales, offsets=routing.offsets, fmt=fmt, bits=bits,
+                                      rounding=rounding, seed=seed, offset=offset + 1, want_h=False,
+                                      want_nan_rows=True, b_nan_rows=gu_nan, gu_out=gu)
+        y = ops.gemm_grouped_blockscaled(qh, d_codes, d_scales, routing.offsets, N=H, out_dtype=tokens.dtype,
+                                         b_nan_rows=d_nan)
+        out = combine_rows(y, routing, expert_ids, topk_w.detach(), T)
+        ctx.meta = (T, H, E, I, routing.top_k, routing.rows, qx.grid, qx.s_col, qh.s_col, tokens.dtype,
+                    w_gate_up.dtype, w_down.dtype)
+        ctx.save_for_backward(routing.pos, routing.inv, routing.counts, routing.offsets, expert_ids, topk_w.detach(),
+                              qx.codes, qx.scales, gu, qh.codes, qh.scales, y, gu_codes, gu_scales, d_codes, d_scales)
+        return out
+
+    @staticmethod
+    def backward(ctx, d_out):
+        (pos, inv, counts, offsets, expert_ids, topk_w, xc, xs, gu, hc, hs, y, gu_codes, gu_scales, d_codes,
+         d_scales) = ctx.saved_tensors
+        T, H, E, I, k, R, grid, x_rp, h_rp, tdt, gudt, ddt = ctx.meta
+        d_out = d_out.contiguous()
+        dev = d_out.device
+        routing = ExpertRouting(pos, inv, counts, offsets, k)
+        # combine: dY rows (y's dtype) and the routing-weight gradient
+        ld = ops.cdiv(H, 64) * 64  # the dgrad reads whole 64-column K steps: zero pad columns
+        dyr = (torch.zeros if ld != H else torch.empty)((R, ld), dtype=y.dtype, device=dev)
+        d_w = torch.empty(topk_w.shape, dtype=topk_w.dtype, device=dev)
+        _lib.call("ntlb_moe_combine_backward", d_out.data_ptr(), d_out.stride(0), y.data_ptr(), y.stride(0),
+                  ops._dtype_code(y.dtype), pos.data_ptr(), topk_w.data_ptr(), ops._dtype_code(topk_w.dtype), T, k, H,
+                  dyr.data_ptr(), ld, d_w.data_ptr(), ops._stream())
+        dyr = dyr[:, :H]
+        # down projection, then the SwiGLU
+        dh = ops.grouped_ste_dgrad(dyr, offsets, d_codes, d_scales, grid=grid, K=I, out_dtype=torch.bfloat16)
+        d_gu = torch.empty((R, 2 * I), dtype=torch.bfloat16, device=dev)
+        _lib.call("ntlb_swiglu_backward", dh.data_ptr(), dh.stride(0), gu.data_ptr(), gu.stride(0), R, I,
+                  d_gu.data_ptr(), d_gu.stride(0), ops._stream())
+        d_tok = dw_gu = dw_down = None
+        if ctx.needs_input_grad[0]:
+            dxr = ops.grouped_ste_dgrad_gate_up(d_gu, offsets, gu_codes, gu_scales, grid=grid, K=H)
+            d_tok = torch.empty((T, H), dtype=tdt, device=dev)
+            ids = expert_ids.contiguous()
+            _lib.call("ntlb_moe_token_grad", dxr.data_ptr(), dxr.stride(0), ops._dtype_code(dxr.dtype),
+                      pos.data_ptr(), ids.data_ptr(), 1 if ids.dtype == torch.int64 else 0, T, k, H,
+                      d_tok.data_ptr(), d_tok.stride(0), ops._stream())
+        if ctx.needs_input_grad[3]:
+            qh = QTensor(hc, hs, 1, h_rp, 0, grid, R, I, None, None)
+            dw_down = ops.grouped_ste_wgrad(dyr, offsets, qh, E, out_dtype=ddt)
+        if ctx.needs_input_grad[2]:
+            qx = QTensor(xc, xs, 1, x_rp, 0, grid, R, H, None, None)
+            dw_gu = ops.grouped_ste_wgrad(d_gu, offsets, qx, E, out_dtype=gudt)
+        return d_tok, (d_w if ctx.needs_input_grad[1] else None), dw_gu, dw_down, None, None, None, None
+
+
+def local_moe(
+    tokens: torch.Tensor,
+    expert_ids: torch.Tensor,
+    topk_w: torch.Tensor,
+    w_gate_up: torch.Tensor,
+    w_down: torch.Tensor,
+    *,
+    capacity: int = 0,
+    fmt: str = "e4m3",
+    bits: int = 8,
+    rounding: str = "nearest",
+    seed: int = 0,
+    offset: int = 0,
+) -> torch.Tensor:
+    """The single-rank routed expert loop, trainable (moe.py:1062-1093,
+    LocalRoutedMoE.forward :476-491, ExpertMLP.forward :190-193): returns the
+    token outputs [T, H] and, under autograd, the gradients of the tokens,
+    the routing weights and the expert weights.
+
+    tokens bf16 [T, H]; expert_ids [T, k] int32/int64 and topk_w [T, k] (the
+    router's topk_indices / topk_weights); w_gate_up bf16 [E, 2I, H] in
+    stack_gate_up()'s row order; w_down bf16 [E, H, I]; I and H multiples of
+    128.  capacity > 0 keeps per expert the `capacity` rows of highest
+    routing weight (compute_capacity() gives the reference's value); the
+    dropped assignments add nothing and get a zero routing-weight gradient.
+    Forward arithmetic: the blockwise-scaled GEMMs (fp32 q * s operands);
+    backward: the straight-through gradients over the reference's bf16(q * s)
+    operands.  An expert that receives no rows gets a zero weight gradient
+    (the reference's separate Linears would get none)."""
+    if tokens.dim() != 2 or expert_ids.dim() != 2 or topk_w.shape != expert_ids.shape:
+        raise ValueError("tokens must be [T, H], expert_ids and topk_w [T, k]")
+    if tokens.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:
+        raise TypeError("local_moe trains bf16 tokens and bf16 expert weights")
+    E, N2, H = w_gate_up.shape
+    if H != tokens.shape[1] or w_down.shape != (E, H, N2 // 2) or N2 % 256:
+        raise ValueError(f"weights must be w_gate_up [E, 2I, H] (2I % 256 == 0) and w_down [E, H, I]; got "
+                         f"{tuple(w_gate_up.shape)}, {tuple(w_down.shape)}")
+    if expert_ids.shape[1] > 8:
+        raise ValueError("local_moe supports top_k <= 8")
+    return _LocalMoE.apply(tokens, topk_w, w_gate_up, w_down, expert_ids, E, int(capacity),
+                           (fmt, bits, rounding, seed, offset))

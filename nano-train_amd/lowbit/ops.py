@@ -494,13 +494,16 @@ def gemm_swiglu_quant(
     want_h: bool = True,
     want_nan_rows: bool = False,
     b_nan_rows: Optional[torch.Tensor] = None,
+    gu_out: Optional[torch.Tensor] = None,
 ):
     """h = silu(X W_gate^T) * (X W_up^T) and its 1x128 quantization, in one GEMM.
 
     b_codes / b_scales hold the gate and up weights interleaved in 128-row
     blocks (moe.interleave_gate_up): [2I, Kp] and [2I/128, Kp/128], or per
     expert [E, 2I, Kp] and [E, 2I/128, Kp/128] with rows of a sorted by expert
-    and offsets int32 [E+1].  Returns (h bf16 [M, I] or None, QTensor of h)."""
+    and offsets int32 [E+1].  gu_out (grouped only), bf16 [M, 2I], receives
+    the two projections' bf16 outputs in that interleaved column order.
+    Returns (h bf16 [M, I] or None, QTensor of h)."""
     _require_device(a.codes, b_codes, b_scales)
     grouped = offsets is not None
     if grouped:
@@ -532,10 +535,17 @@ def gemm_swiglu_quant(
     if grouped:
         E = b_codes.shape[0]
         nb, tb = b_scales.shape[1], b_scales.shape[2]
-        call("ntlb_gemm_grouped_swiglu_quant", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(),
+        if gu_out is not None:
+            _require_device(gu_out)
+            if gu_out.dtype != torch.bfloat16 or gu_out.shape != (M, N) or gu_out.stride(-1) != 1:
+                raise ValueError(f"gu_out must be a row-major bf16 [{M}, {N}] tensor")
+        call("ntlb_gemm_grouped_swiglu_quant_gu", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(),
              a.s_row, a.s_col, a.shift, b_codes.data_ptr(), b_codes.stride(1), b_codes.stride(0),
-             b_scales.data_ptr(), tb, 1, nb * tb, offsets.data_ptr(), E, M, N, a.Kp, *tail)
+             b_scales.data_ptr(), tb, 1, nb * tb, offsets.data_ptr(), E, M, N, a.Kp, *tail[:-1], _ptr(gu_out),
+             gu_out.stride(0) if gu_out is not None else 0, _stream())
     else:
+        if gu_out is not None:
+            raise ValueError("gu_out needs the grouped (per-expert) form")
         tb = b_scales.shape[1]
         call("ntlb_gemm_swiglu_quant", a.grid, a.codes.data_ptr(), a.codes.stride(0), a.scales.data_ptr(), a.s_row,
              a.s_col, a.shift, b_codes.data_ptr(), b_codes.stride(0), b_scales.data_ptr(), tb, 1, M, N, a.Kp, *tail)
@@ -629,6 +639,70 @@ def ste_wgrad(dy: torch.Tensor, x: QTensor, *, out_dtype: torch.dtype) -> torch.
     call("ntlb_gemm_ste_wgrad", _lib.BF16, dy.data_ptr(), dy.stride(0), M, N, x.grid, x.codes.data_ptr(),
          x.codes.stride(0), x.scales.data_ptr(), x.s_row, x.s_col, x.shift, x.K, out.data_ptr(),
          _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def grouped_ste_dgrad(dy: torch.Tensor, offsets: torch.Tensor, w_codes: torch.Tensor, w_scales: torch.Tensor, *,
+                      grid: int, K: int, out_dtype: torch.dtype) -> torch.Tensor:
+    """dX[rows of e] = dY[rows of e] @ bf16(dq(W_e)) for rows sorted by expert
+    (offsets int32 [E+1]); W_e the 128x128-block codes [E, N, Kp] and scales
+    [E, N/128, Kp/128] of moe.quantize_expert_weights.  dX [R, K]."""
+    _require_device(dy, offsets, w_codes, w_scales)
+    if dy.dtype != torch.bfloat16:
+        raise TypeError("grouped_ste_dgrad takes a bfloat16 dY")
+    E, N, ldw = w_codes.shape
+    if dy.shape[1] != N or offsets.numel() != E + 1 or offsets.dtype != torch.int32:
+        raise ValueError("dY columns must match the weights' rows and offsets must be int32 [E+1]")
+    w_codes, w_scales = w_codes.contiguous(), w_scales.contiguous()
+    R = dy.shape[0]
+    dyp = _pad_cols(dy, 64)
+    out = torch.empty((R, K), dtype=out_dtype, device=dy.device)
+    tb = w_scales.shape[2]
+    call("ntlb_gemm_grouped_ste_dgrad", _lib.BF16, dyp.data_ptr(), dyp.stride(0), R, N, offsets.data_ptr(), E, grid,
+         w_codes.data_ptr(), ldw, w_codes.stride(0), w_scales.data_ptr(), tb, 1, 7, w_scales.stride(0), K,
+         out.data_ptr(), _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def grouped_ste_dgrad_gate_up(d_gu: torch.Tensor, offsets: torch.Tensor, w_codes: torch.Tensor,
+                              w_scales: torch.Tensor, *, grid: int, K: int) -> torch.Tensor:
+    """The gate and up Linears' summed input gradient of every expert:
+    bf16(dX_gate) + bf16(dX_up) added in bf16, over the interleaved gate/up
+    layout (d_gu bf16 [R, 2I], codes [E, 2I, Kp], scales [E, 2I/128, Kp/128]).
+    dX bf16 [R, K]."""
+    _require_device(d_gu, offsets, w_codes, w_scales)
+    if d_gu.dtype != torch.bfloat16:
+        raise TypeError("grouped_ste_dgrad_gate_up takes a bfloat16 d_gate_up")
+    E, N2, ldw = w_codes.shape
+    R = d_gu.shape[0]
+    if d_gu.shape[1] != N2 or offsets.numel() != E + 1 or offsets.dtype != torch.int32:
+        raise ValueError("d_gate_up columns must match the weights' rows and offsets must be int32 [E+1]")
+    w_codes, w_scales = w_codes.contiguous(), w_scales.contiguous()
+    d_gu = _pad_cols(d_gu, 64)
+    out = torch.empty((R, K), dtype=torch.bfloat16, device=d_gu.device)
+    call("ntlb_gemm_grouped_ste_dgrad_gate_up", _lib.BF16, d_gu.data_ptr(), d_gu.stride(0), R, N2 // 2,
+         offsets.data_ptr(), E, grid, w_codes.data_ptr(), ldw, w_codes.stride(0), w_scales.data_ptr(),
+         w_scales.shape[2], 1, w_scales.stride(0), K, out.data_ptr(), out.stride(0), _stream())
+    return out
+
+
+def grouped_ste_wgrad(dy: torch.Tensor, offsets: torch.Tensor, x: QTensor, n_experts: int, *,
+                      out_dtype: torch.dtype) -> torch.Tensor:
+    """dW[e] = dY[rows of e]^T @ bf16(dq(X[rows of e])) for every expert (zero
+    for an expert without rows); X's codes carry per-row 1x128 tile-major
+    scales.  dW [E, N, K]."""
+    _require_device(dy, offsets, x.codes)
+    if dy.dtype != torch.bfloat16:
+        raise TypeError("grouped_ste_wgrad takes a bfloat16 dY")
+    R, N = dy.shape
+    if R != x.rows or offsets.numel() != n_experts + 1 or offsets.dtype != torch.int32:
+        raise ValueError("dY and X must have the same rows and offsets must be int32 [E+1]")
+    if dy.stride(-1) != 1 or dy.stride(0) % 8 or dy.data_ptr() % 16:
+        dy = _pad_cols(dy, 8)
+    out = torch.empty((n_experts, N, x.K), dtype=out_dtype, device=dy.device)
+    call("ntlb_gemm_grouped_ste_wgrad", _lib.BF16, dy.data_ptr(), dy.stride(0), R, N, offsets.data_ptr(), n_experts,
+         x.grid, x.codes.data_ptr(), x.codes.stride(0), x.scales.data_ptr(), x.s_row, x.s_col, x.shift, x.K,
+         out.data_ptr(), _dtype_code(out_dtype), out.stride(1), out.stride(0) * out.element_size(), _stream())
     return out
 
 

@@ -123,3 +123,104 @@ def nf4_dequantize(packed: torch.Tensor, scales: torch.Tensor, *, numel: int, bl
     cb = torch.from_numpy(NF4_CODEBOOK.astype("float32"))
     vals = cb[idx] * scales.reshape(-1).repeat_interleave(block)[:numel]
     return vals.to(dtype)
+
+
+class _LinearFwd32Ste(torch.autograd.Function):
+    """A Linear whose forward multiplies fp32 q * s operands (the blockwise
+    GEMM's numerics) and whose backward is the reference's straight-through
+    gradient over its bf16(q * s) operands (te_backend.py:250-259 under
+    autograd): dX = dY . W_q, dW = dY^T . X_q, in fp32, cast to the input dtypes."""
+
+    @staticmethod
+    def forward(ctx, x, w, x_dq32, w_dq32, x_q, w_q):
+        ctx.save_for_backward(x_q, w_q)
+        ctx.dts = (x.dtype, w.dtype)
+        return F.linear(x_dq32, w_dq32).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x_q, w_q = ctx.saved_tensors
+        dyf = dy.float()
+        dx = (dyf @ w_q.float()).to(ctx.dts[0])
+        dw = (dyf.t() @ x_q.float()).to(ctx.dts[1])
+        return dx, dw, None, None, None, None
+
+
+def _linear_for_moe(x: torch.Tensor, w: torch.Tensor, *, forward: str, qdq) -> torch.Tensor:
+    """One expert Linear: x quantized per 1x128 tile, w per 128x128 block
+    (qdq(t_fp32, gr, gc) gives the fp32 dq values)."""
+    x32 = qdq(x.float(), 1, 128)
+    w32 = qdq(w.float(), 128, 128)
+    x_q = x + (x32.to(x.dtype) - x).detach()
+    w_q = w + (w32.to(w.dtype) - w).detach()
+    if forward == "reference":
+        # te_backend.py:250-260
+        return F.linear(x_q.to(torch.float32), w_q.to(torch.float32)).to(x.dtype)
+    return _LinearFwd32Ste.apply(x, w, x32, w32, x_q.detach(), w_q.detach())
+
+
+class _ValueOf(torch.autograd.Function):
+    """`value` in the forward, the gradient of `computed` in the backward."""
+
+    @staticmethod
+    def forward(ctx, computed, value):
+        return value.clone()
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, None
+
+
+def local_moe_loop(tokens: torch.Tensor, topk_idx: torch.Tensor, topk_w: torch.Tensor, w_gate_up: torch.Tensor,
+                   w_down: torch.Tensor, *, capacity: int = 0, forward: str = "reference", bits: int = 8,
+                   qdq=None, gate_up_values=None) -> torch.Tensor:
+    """The reference's single-rank routed expert loop as torch CPU ops, with
+    autograd: moe.py:1062-1093 (LocalRoutedMoE.forward :476-491), each expert
+    an ExpertMLP (moe.py:146-193: silu(gate_proj(x)) * up_proj(x) -> down_proj)
+    of emulated low-bit Linears, round to nearest.
+
+    w_gate_up [E, 2I, H] holds each expert's gate and up weights in 128-row
+    blocks, alternating (gate block t, up block t); w_down [E, H, I].
+    forward="reference": each Linear is EmulatedLowBitBackend.linear (bf16(q*s)
+    operands, te_backend.py:229-260) with 1x128 activation tiles and 128x128
+    weight blocks; forward="fp32_dq": the forward multiplies fp32 q * s
+    operands (the blockwise-scaled GEMM's numerics) while the backward keeps
+    the reference's straight-through gradients.  qdq(t_fp32_2d, gr, gc)
+    quantizes with one scale per (gr x gc) group and returns the fp32 dq
+    values; the default is the reference's int grid (grouped_qdq).
+    gate_up_values(e) -> (gate, up) replaces the forward values of expert e's
+    two projections (its rows in the loop's order) while their gradients stay
+    those of the Linears: the same bf16 projections as another implementation
+    whose fp32 sums run in another order, so that the re-quantization of h
+    does not turn their last-bit differences into whole code steps."""
+    if qdq is None:
+        qdq = lambda t, gr, gc: grouped_qdq(t, bits=bits, gr=gr, gc=gc)
+    T, H = tokens.shape
+    E, N2, _ = w_gate_up.shape
+    I = N2 // 2
+    output = torch.zeros_like(tokens)
+    v = w_gate_up.reshape(E, I // 128, 2, 128, H)
+    for e in range(E):
+        selected = (topk_idx == e).nonzero(as_tuple=False)
+        if selected.numel() == 0:
+            continue
+        token_indices = selected[:, 0]
+        slot_indices = selected[:, 1]
+        sort_weights = topk_w[token_indices, slot_indices].detach()
+        if capacity > 0 and token_indices.numel() > capacity:
+            keep_rel = torch.topk(sort_weights, k=capacity, sorted=True).indices
+            token_indices = token_indices[keep_rel]
+            slot_indices = slot_indices[keep_rel]
+        x = tokens[token_indices]
+        wg = v[e, :, 0].reshape(I, H)
+        wu = v[e, :, 1].reshape(I, H)
+        lin = lambda a, b: _linear_for_moe(a, b, forward=forward, qdq=qdq)
+        g, u = lin(x, wg), lin(x, wu)
+        if gate_up_values is not None:
+            gv, uv = gate_up_values(e)
+            g, u = _ValueOf.apply(g, gv), _ValueOf.apply(u, uv)
+        gated = F.silu(g) * u
+        expert_out = lin(gated, w_down[e])
+        weights = topk_w[token_indices, slot_indices].unsqueeze(-1)
+        output[token_indices] += expert_out * weights
+    return output

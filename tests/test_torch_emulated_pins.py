@@ -130,3 +130,36 @@ def test_reference_operand_is_the_dequant_only_under_nearest(grid, gr, gc, dtype
             diff64 = dq_t.double() - x.double()
             inexact = (dq_t - x).double() != diff64
             assert bool(inexact[~same].all())
+
+
+def test_autograd_accumulates_gathered_token_gradients_in_descending_expert_order():
+    """The reference's loop gathers tokens[token_indices] once per expert
+    (moe.py:1086, :488); autograd runs the later experts' backward first, so a
+    token's gradient is its experts' contributions added in descending expert
+    id, each add rounded to bf16 (ntlb_moe_token_grad mirrors this order).  An
+    ascending order or one fp32 sum gives other bits."""
+    torch.manual_seed(0)
+    T, H, E, k = 64, 32, 5, 3
+    tok = torch.randn(T, H).bfloat16().requires_grad_(True)
+    idx = torch.stack([torch.randperm(E)[:k] for _ in range(T)])
+    contrib = {}
+    out = torch.zeros_like(tok)
+    for e in range(E):
+        ti = (idx == e).nonzero()[:, 0]
+        c = (torch.randn(ti.numel(), H) * 1.37).bfloat16()
+        contrib[e] = (ti, c)
+        out[ti] += tok[ti] * c
+    d = torch.randn(T, H).bfloat16()
+    out.backward(d)
+
+    def accum(order):
+        acc = None
+        for e in order:
+            ti, c = contrib[e]
+            full = torch.zeros(T, H, dtype=torch.bfloat16)
+            full[ti] = d[ti] * c
+            acc = full if acc is None else acc + full
+        return acc
+
+    assert torch.equal(accum(range(E - 1, -1, -1)), tok.grad)
+    assert not torch.equal(accum(range(E)), tok.grad)
