@@ -222,6 +222,7 @@ def other_config(args) -> dict:
         gate_up = moe.interleave_gate_up(qg[0], qg[1], qu[0], qu[1], qg[2], qu[2])
         del qg, qu
         down = moe.quantize_expert_weights(w_down, fmt=fmt)
+        w_gu = moe.stack_gate_up(w_gate, w_up)  # the trainable loop's [E, 2I, H] master weights
         del w_gate, w_up
         comm_us = _time_ms(lambda i: moe.comm_quant(xs, fmt=fmt), args.steps, args.warmup, st) * 1e3
         payload = moe.comm_quant(xs, fmt=fmt)
@@ -252,6 +253,37 @@ def other_config(args) -> dict:
                                                          want_h=False), args.steps, args.warmup, st)
         dn_ms = _time_ms(lambda i: ops.gemm_grouped_blockscaled(qh, down[0], down[1], offsets, N=H),
                          args.steps, args.warmup, st)
+        # the trainable loop (moe.local_moe): quantize the bf16 expert weights,
+        # forward, and the backward to the tokens, the routing weights and the
+        # expert weights; and its grouped straight-through GEMMs alone
+        leaves = [t.clone().requires_grad_(True) for t in (tokens, topk_w, w_gu, w_down)]
+        d_out = (torch.randn(tokens.shape, generator=torch.Generator().manual_seed(6)) * 1e-2).to(dev, torch.bfloat16)
+
+        def train_fwd(i):
+            return moe.local_moe(leaves[0], routing, leaves[1], leaves[2], leaves[3], fmt=fmt)
+
+        def train_step(i):
+            for t in leaves:
+                t.grad = None
+            train_fwd(i).backward(d_out)
+
+        train_ms = _time_ms(train_step, args.steps, args.warmup, st)
+        train_fwd_ms = _time_ms(train_fwd, args.steps, args.warmup, st)
+        for t in leaves:
+            t.grad = None
+        del leaves
+        dyr = (torch.randn((R, H), generator=torch.Generator().manual_seed(7)) * 1e-3).to(dev, torch.bfloat16)
+        d_gu = (torch.randn((R, 2 * inter), generator=torch.Generator().manual_seed(8)) * 1e-3).to(dev, torch.bfloat16)
+        grid_c = ops.grid_code(fmt)
+        dg_dn_ms = _time_ms(lambda i: ops.grouped_ste_dgrad(dyr, offsets, down[0], down[1], grid=grid_c, K=inter,
+                                                            out_dtype=torch.bfloat16), args.steps, args.warmup, st)
+        dg_gu_ms = _time_ms(lambda i: ops.grouped_ste_dgrad_gate_up(d_gu, offsets, gate_up[0], gate_up[1],
+                                                                    grid=grid_c, K=H), args.steps, args.warmup, st)
+        wg_dn_ms = _time_ms(lambda i: ops.grouped_ste_wgrad(dyr, offsets, qh, 32, out_dtype=torch.bfloat16),
+                            args.steps, args.warmup, st)
+        wg_gu_ms = _time_ms(lambda i: ops.grouped_ste_wgrad(d_gu, offsets, qx, 32, out_dtype=torch.bfloat16),
+                            args.steps, args.warmup, st)
+        del dyr, d_gu, w_gu
         # expert-parallel wire format, one GPU's share of an 8-rank layout (4 experts per rank):
         # pack every (token, slot) assignment into a record, unpack as many received records
         from lowbit import ep
@@ -308,6 +340,16 @@ def other_config(args) -> dict:
                              "traffic_source": f"profiles/c4_moe_experts_{fmt}.md" if traffic else None,
                              "avg_ms": round(gu_ms, 4)},
                    expert_mlp_ms=round(mlp, 4),
+                   train={"what": "moe.local_moe forward + backward (the reference loop under autograd): bf16 "
+                                  "expert weights quantized each step, gradients of tokens, routing weights and "
+                                  "both weight stacks",
+                          "step_ms": round(train_ms, 4), "forward_ms": round(train_fwd_ms, 4),
+                          "tflops": round(9 * fl / (train_ms * 1e-3) / 1e12, 2),
+                          "dgrad_down_tflops": round(fl / (dg_dn_ms * 1e-3) / 1e12, 2),
+                          "dgrad_gate_up_tflops": round(2 * fl / (dg_gu_ms * 1e-3) / 1e12, 2),
+                          "wgrad_down_tflops": round(fl / (wg_dn_ms * 1e-3) / 1e12, 2),
+                          "wgrad_gate_up_tflops": round(2 * fl / (wg_gu_ms * 1e-3) / 1e12, 2),
+                          "peak_bf16_tflops": 2500.0},
                    route_us=round(route_us, 2), gather_quant_x_us=round(fan_us, 2),
                    gather_quant_x_GBs=round((T_tok * H * 2 + R * H + R * (H // 128) * 4) / fan_us / 1e3, 1),
                    combine_rows_us=round(comb_rows_us, 2),

@@ -489,11 +489,33 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     // every expert has the num_m x num_n tiles of its own Y; its contraction
     // is its rows, so both operands start at row offsets[e] and hold
     // offsets[e+1] - offsets[e] valid rows (zero past them, through the
-    // buffer resources); an expert without rows stores zeros
+    // buffer resources); an expert without rows stores zeros.  A tile's work
+    // is its expert's row count, which routing skews (Zipf at config 4: 263
+    // to 4019 rows): the experts go out longest first, and consecutive tiles
+    // go to consecutive XCDs (no contiguous per-XCD ranges, which would hand
+    // one XCD all of the popular experts' tiles)
     const int per = num_m * num_n;
-    const int pid = xcd_local((int)blockIdx.x, per * g.n_experts);
-    const int e = pid / per;
-    raster(pid - e * per, num_m, num_n, m0, n0);
+    const int q = (int)blockIdx.x / per;  // rank of the expert by row count
+    int e = q;
+    if (g.n_experts <= NT) {
+      int32_t* tab = reinterpret_cast<int32_t*>(la0);
+      for (int i = tid; i <= g.n_experts; i += NT) tab[i] = g.offsets[i];
+      __syncthreads();
+      int* who = reinterpret_cast<int*>(la0) + NT + 1;
+      if (tid < g.n_experts) {
+        const int ni = tab[tid + 1] - tab[tid];
+        int rank = 0;
+        for (int j = 0; j < g.n_experts; ++j) {
+          const int nj = tab[j + 1] - tab[j];
+          rank += (nj > ni || (nj == ni && j < tid)) ? 1 : 0;
+        }
+        who[rank] = tid;
+      }
+      __syncthreads();
+      e = who[q];
+      __syncthreads();  // the LDS is a copy target from here on
+    }
+    raster((int)blockIdx.x - q * per, num_m, num_n, m0, n0);
     const int64_t lo = g.offsets[e], rows_e = g.offsets[e + 1] - lo;
     g.a.p += lo * g.a.ld * EB;
     g.a.kvalid = rows_e;
@@ -674,12 +696,24 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
           if (e_misc & 128) {
             // y = bf16(y + bf16(acc)) (bf16 output only)
             if (!FULL && (m >= e_M || n >= e_N)) continue;
-            const int cnt = FULL ? epc : (int)min<int64_t>(epc, e_N - n);
+            if (FULL || ((e_misc & 1) && n + epc <= e_N)) {
+              const uint4 o = *reinterpret_cast<const uint4*>(ydst);
+              const uint4 a = *reinterpret_cast<const uint4*>(src);
+              const uint32_t ow[4] = {o.x, o.y, o.z, o.w}, aw[4] = {a.x, a.y, a.z, a.w};
+              uint32_t rw[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                rw[q] = pack_bf16(bf16_bits_to_f32(ow[q] & 0xFFFFu) + bf16_bits_to_f32(aw[q] & 0xFFFFu),
+                                  bf16_bits_to_f32(ow[q] >> 16) + bf16_bits_to_f32(aw[q] >> 16));
+              *reinterpret_cast<uint4*>(ydst) = make_uint4(rw[0], rw[1], rw[2], rw[3]);
+            } else {
+              const int cnt = (int)min<int64_t>(epc, e_N - n);
 #pragma nounroll
-            for (int e = 0; e < cnt; ++e) {
-              uint16_t* yp = reinterpret_cast<uint16_t*>(ydst) + e;
-              const float a = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[e]);
-              *yp = f32_to_bf16_bits(bf16_bits_to_f32(*yp) + a);
+              for (int e = 0; e < cnt; ++e) {
+                uint16_t* yp = reinterpret_cast<uint16_t*>(ydst) + e;
+                const float a = bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(src)[e]);
+                *yp = f32_to_bf16_bits(bf16_bits_to_f32(*yp) + a);
+              }
             }
             continue;
           }
