@@ -121,43 +121,32 @@ __device__ __forceinline__ uint32_t e4m3_rne(float v) {
   return sign | code;
 }
 
-// Stochastic rounding onto the e4m3 grid: the te_backend.py:61-65 rule
-// floor(|v| + u) applied in units of the local e4m3 spacing, sign kept.
-// |v| <= 448 on entry (the callers clamp first).
-__device__ __forceinline__ uint32_t e4m3_sr(float v, float u) {
-#pragma clang fp contract(off)
-  uint32_t bits = __float_as_uint(v);
-  uint32_t sign = (bits >> 24) & 0x80u;
-  uint32_t ab = bits & 0x7FFFFFFFu;
-  float a = __uint_as_float(ab);
-  if (ab > 0x7F800000u) return sign | 0x7Fu;
-  if (a >= 448.0f) return sign | 0x7Eu;
-  if (a < 0x1p-6f) {
-    float n = __builtin_floorf(a * 512.0f + u);
-    return sign | (uint32_t)n;
-  }
-  uint32_t e8 = ab >> 23;
-  float t = __uint_as_float((ab & 0x7FFFFFu) | (130u << 23));  // a / ulp, in [8, 16)
-  float n = __builtin_floorf(t + u);                             // 8 .. 16
-  return sign | (((e8 - 120u) << 3) + (uint32_t)n - 8u);
-}
-
-// e4m3_sr for finite |v| <= 448 (the tile paths clamp first), without
-// branches: both the subnormal and the normal candidate are formed and one is
-// selected.  |v|*512 is exact, so fma(|v|, 512, u) rounds |v|*512 + u once as
-// the two-step form does; the candidates are non-negative, so the truncating
-// convert is the floor.  At |v| = 448, t + u can round up to the next binade
-// (480, no e4m3 code); the result clamps to 448 after rounding, as e4m3_sr
-// does.
-__device__ __forceinline__ uint32_t e4m3_sr_fin(float v, float u) {
-#pragma clang fp contract(off)
+// Stochastic rounding onto the e4m3 grid (the e4m3 counterpart of the
+// te_backend.py:61-65 rule): the 20 bits of |v| just below its e4m3 spacing
+// (truncated) plus the top 20 bits of the Philox word r carry into the code,
+// i.e. |v| rounds away from zero iff frac20 + (r >> 12) >= 2^20, sign kept.
+// This is the rounding of gfx950's v_cvt_sr_fp8_f32, which the tile paths use
+// (tests/hip/fp8_sr_cvt_probe.hip compares the two over every fp32 |v| <=
+// 448).  |v| <= 448 on entry (the callers clamp first); there frac20 is 0 at
+// 448, so no draw rounds past the largest finite code.
+__device__ __forceinline__ uint32_t e4m3_sr(float v, uint32_t r) {
   const uint32_t bits = __float_as_uint(v);
-  const uint32_t ns = (uint32_t)__builtin_fmaf(__builtin_fabsf(v), 512.0f, u);  // subnormal spacing 2^-9: 0 .. 8
-  const float t = __uint_as_float((bits & 0x7FFFFFu) | (130u << 23));         // |v| / ulp, in [8, 16)
-  const uint32_t nn = (uint32_t)(t + u);                                        // 8 .. 16
-  const uint32_t e8 = (bits >> 23) & 0xFFu;
-  const uint32_t cn = min(e8 * 8u + nn - 968u, 0x7Eu);                          // ((e8 - 120) << 3) + nn - 8
-  return ((bits >> 24) & 0x80u) | (e8 < 121u ? ns : cn);                        // |v| < 2^-6: subnormal
+  const uint32_t sign = (bits >> 24) & 0x80u;
+  const uint32_t ab = bits & 0x7FFFFFFFu;
+  if (ab > 0x7F800000u) return sign | 0x7Fu;
+  if (ab >= 0x43E00000u) return sign | 0x7Eu;  // >= 448
+  const uint32_t e8 = ab >> 23;
+  uint32_t trunc, f20;
+  if (e8 >= 121u) {  // |v| >= 2^-6: 3 mantissa bits, then 20
+    trunc = ((e8 - 120u) << 3) + ((ab >> 20) & 7u);
+    f20 = ab & 0xFFFFFu;
+  } else {  // subnormal e4m3 (spacing 2^-9): |v| * 512 = m >> sh, fp32 denormals as exponent 1
+    const uint32_t m = (ab & 0x7FFFFFu) | (e8 ? 0x800000u : 0u);
+    const uint32_t sh = 141u - (e8 ? e8 : 1u);  // 21 .. 140
+    trunc = sh < 32u ? m >> sh : 0u;
+    f20 = sh - 20u < 32u ? (m >> (sh - 20u)) & 0xFFFFFu : 0u;
+  }
+  return sign | min(trunc + ((f20 + (r >> 12)) >> 20), 0x7Eu);
 }
 
 __device__ __forceinline__ float e4m3_to_f32(uint32_t c) {
@@ -219,7 +208,7 @@ __device__ __forceinline__ uint32_t quant_one(float x, float s, float qmaxf, uin
     v = (v > 448.0f) ? 448.0f : v;
     uint32_t c;
     if constexpr (SR) {
-      c = e4m3_sr(v, sr_uniform(rbits));
+      c = e4m3_sr(v, rbits);
     } else {
       c = e4m3_rne(v);
     }

@@ -44,16 +44,18 @@ __device__ __forceinline__ void sr_words(uint64_t e0, uint64_t seed, uint64_t of
   }
 }
 
-// Quantize 8 values with one scale; returns the codes packed in two words
-// and whether any q was NaN.  Writes dq when requested.
-template <int GRID, bool SR>
-__device__ __forceinline__ bool quant8(const float (&v)[8], float s, float qmaxf, const uint32_t (&rb)[8],
-                                       uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+// Quantize N (8 or 4) values with one scale; returns the codes packed in two
+// words (hi is 0 for N = 4) and whether any q was NaN.  Writes dq when
+// requested.
+template <int GRID, bool SR, int N>
+__device__ __forceinline__ bool quant8(const float (&v)[N], float s, float qmaxf, const uint32_t (&rb)[N],
+                                       uint32_t& lo, uint32_t& hi, float (&q)[N]) {
 #pragma clang fp contract(off)
-  uint32_t c[8];
+  static_assert(N == 8 || N == 4, "8 or 4 values");
+  uint32_t c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   bool nan = false;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < N; ++i) {
     c[i] = quant_one<GRID, SR>(v[i], s, qmaxf, rb[i], q[i]);
     nan |= (__float_as_uint(q[i]) & 0x7FFFFFFFu) > 0x7F800000u;
   }
@@ -84,16 +86,17 @@ __device__ __forceinline__ bool fast_div_ok(uint32_t m) {
 
 // rs is 1/s (IEEE, correctly rounded) wherever fast_div_ok(m) holds; it is
 // not read otherwise.
-template <int GRID, bool SR, bool DQ>
-__device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, float s, float rs, float qmaxf,
-                                               const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi, float (&q)[8]) {
+template <int GRID, bool SR, bool DQ, int N>
+__device__ __forceinline__ bool quant8_tile_rs(const float (&v)[N], uint32_t m, float s, float rs, float qmaxf,
+                                               const uint32_t (&rb)[N], uint32_t& lo, uint32_t& hi, float (&q)[N]) {
 #pragma clang fp contract(off)
+  static_assert(N == 8 || N == 4, "8 or 4 values");
   if (m > 0x7F800000u) {
     // NaN in the tile: reference semantics element by element
     quant8<GRID, SR>(v, s, qmaxf, rb, lo, hi, q);
     return true;
   } else {
-    float vq[8];
+    float vq[N];
     // x/s by the fast sequence (with the sign of x, so that -0 and signed
     // tiny quotients keep their sign) where fast_div_ok holds, else by IEEE
     // division.  No NaN reaches the clamp here (NaN tiles took the path
@@ -101,7 +104,7 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
     // the clamp
     if (fast_div_ok<SR>(m)) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < N; ++i) {
         const float y = v[i] * rs;
         const float e = __builtin_fmaf(-y, s, v[i]);
         float z = __builtin_copysignf(__builtin_fmaf(e, rs, y), v[i]);
@@ -109,15 +112,15 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < N; ++i) {
         float z = v[i] / s;
         vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
       }
     }
     if constexpr (GRID == GRID_INT) {
-      uint32_t c[8];
+      uint32_t c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < N; ++i) {
         float t;
         if constexpr (SR) {
           // floor(v + u) for v >= 0 and ceil(v - u) = -floor(|v| + u) below
@@ -137,25 +140,36 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[8], uint32_t m, 
         c[i] = (uint32_t)(int32_t)t & 0xFFu;
       }
       lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+      hi = N == 8 ? (c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)) : 0u;
     } else {
       uint32_t c[8];
+      hi = 0;
       if constexpr (!SR) {
         lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[0], vq[1], 0, false);
         lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[2], vq[3], (int)lo, true);
-        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4], vq[5], 0, false);
-        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[6], vq[7], (int)hi, true);
-        c[0] = lo & 0xFF; c[1] = (lo >> 8) & 0xFF; c[2] = (lo >> 16) & 0xFF; c[3] = lo >> 24;
-        c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
+        if constexpr (N == 8) {
+          hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4 % N], vq[5 % N], 0, false);
+          hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[6 % N], vq[7 % N], (int)hi, true);
+        }
       } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) c[i] = e4m3_sr_fin(vq[i], sr_uniform(rb[i]));
-        lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-        hi = c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24);
+        // the hardware stochastic convert, whose rounding is e4m3_sr's (the
+        // clamped quotients are finite and at most 448)
+        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[0], (int)rb[0], 0, 0);
+        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[1], (int)rb[1], (int)lo, 1);
+        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[2], (int)rb[2], (int)lo, 2);
+        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[3], (int)rb[3], (int)lo, 3);
+        if constexpr (N == 8) {
+          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[4 % N], (int)rb[4 % N], 0, 0);
+          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[5 % N], (int)rb[5 % N], (int)hi, 1);
+          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[6 % N], (int)rb[6 % N], (int)hi, 2);
+          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[7 % N], (int)rb[7 % N], (int)hi, 3);
+        }
       }
+      c[0] = lo & 0xFF; c[1] = (lo >> 8) & 0xFF; c[2] = (lo >> 16) & 0xFF; c[3] = lo >> 24;
+      c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
       if constexpr (DQ) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) q[i] = e4m3_to_f32(c[i]);
+        for (int i = 0; i < N; ++i) q[i] = e4m3_to_f32(c[i]);
       }
     }
   }

@@ -927,7 +927,12 @@ __global__ void __launch_bounds__(256) quant_tile_128x1_t_kernel(QuantArgs a) {
 // thread's chunks is 8 columns of one 1x128 tile, whose other 120 columns are
 // held by the 15 lanes of the same row group, so a 16-lane max gives the tile
 // amax.  One read of dY feeds both the dgrad and the wgrad operands.
-template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false, int CW = 16>
+//
+// With SHARED (stochastic rounding, both outputs keyed at the same seed and
+// offset) an element's word is the same for both layouts, so each Philox
+// block is drawn once: the 1x128 codes are formed four columns at a time
+// inside the 128x1 pass's two halves, from the same words.
+template <int IN_DT, int GRID, bool SR, bool DQ, bool DUAL = false, int CW = 16, bool SHARED = false>
 __global__ void __launch_bounds__(16 * CW) quant_tile_128x1_t_fast(QuantArgs a, QuantArgs ar = QuantArgs()) {
   static_assert(CW == 16 || (CW == 32 && !DUAL), "128 or 256 columns per workgroup; the dual pass takes 128");
   constexpr int NCOL = 8 * CW, NW = CW / 4;  // columns and waves of the workgroup
@@ -1033,7 +1038,7 @@ __global__ void __launch_bounds__(16 * CW) quant_tile_128x1_t_fast(QuantArgs a, 
   }
   __syncthreads();
 
-  if constexpr (DUAL) {
+  if constexpr (DUAL && !SHARED) {
     // 1x128 tiles: tile cb of rows row0..row0+7; pad columns [K, ldc) get
     // zero codes like every other 1x128 output (fully unrolled: c[] must stay
     // in registers)
@@ -1064,6 +1069,8 @@ __global__ void __launch_bounds__(16 * CW) quant_tile_128x1_t_fast(QuantArgs a, 
   // block (K % 8 == 0 and col0 % 8 == 0 align the element index), so only
   // 32 words are live at a time.  Fully unrolled: a rolled loop would index
   // c[] by h at run time and move it to scratch memory
+  uint32_t dlo[8];     // SHARED: each row's 1x128 codes of columns 0..3
+  uint32_t dnan = 0;   // SHARED: NaN seen in row i's tile (bit i)
 #pragma clang loop unroll(full)
   for (int h = 0; h < 2; ++h) {
   uint32_t rb[8][4];  // [row i][column j - 4h]
@@ -1076,6 +1083,33 @@ __global__ void __launch_bounds__(16 * CW) quant_tile_128x1_t_fast(QuantArgs a, 
     } else {
 #pragma unroll
       for (int u = 0; u < 4; ++u) rb[i][u] = 0;
+    }
+  }
+  if constexpr (DUAL && SHARED) {
+    // the 1x128 codes of columns 4h..4h+3 of each row, from the same words
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int rl = rg * 8 + i;
+      float v8[8];
+      chunk_floats<IN_DT>(c[i], v8);
+      const float v4[4] = {v8[4 * h], v8[4 * h + 1], v8[4 * h + 2], v8[4 * h + 3]};
+      const uint32_t rb4[4] = {rb[i][0], rb[i][1], rb[i][2], rb[i][3]};
+      uint32_t w, w_unused;
+      float q4[4];
+      const bool nan = quant8_tile_rs<GRID, SR, false>(v4, rm[rl], rs_[rl], rrs[rl], ar.qmaxf, rb4, w, w_unused, q4);
+      if (h == 0) {
+        dlo[i] = w;
+        dnan |= (nan ? 1u : 0u) << i;
+      } else {
+        const int64_t r = row0 + i;
+        if (r < a.R) {
+          *reinterpret_cast<uint2*>(ar.codes + r * ar.ldc + col0) = make_uint2(dlo[i], w);
+          if (cc == 0) {
+            ar.scales[r * ar.s_row + cb * ar.s_col] = rs_[rl];
+            if ((nan || ((dnan >> i) & 1u)) && ar.nan_rows) atomicOr(ar.nan_rows + r, 1);
+          }
+        }
+      }
     }
   }
 
@@ -1769,6 +1803,21 @@ extern "C" int ntlb_quant_dual_1x128_128x1(const void* x, int x_dtype, int64_t R
   const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
   hipStream_t st = as_stream(stream);
   dim3 grd((unsigned)(MB * T)), blk(256);
+  if (sr && offset_rows == offset_cols) {
+    // one Philox draw per element for both layouts
+    if (x_dtype == NTLB_BF16) {
+      if (grid == NTLB_GRID_E4M3)
+        quant_tile_128x1_t_fast<DT_BF16, GRID_E4M3, true, false, true, 16, true><<<grd, blk, 0, st>>>(ac, ar);
+      else
+        quant_tile_128x1_t_fast<DT_BF16, GRID_INT, true, false, true, 16, true><<<grd, blk, 0, st>>>(ac, ar);
+    } else {
+      if (grid == NTLB_GRID_E4M3)
+        quant_tile_128x1_t_fast<DT_F32, GRID_E4M3, true, false, true, 16, true><<<grd, blk, 0, st>>>(ac, ar);
+      else
+        quant_tile_128x1_t_fast<DT_F32, GRID_INT, true, false, true, 16, true><<<grd, blk, 0, st>>>(ac, ar);
+    }
+    return check_launch(fn);
+  }
   if (x_dtype == NTLB_BF16) {
     NTLB_DISPATCH_GRID_SR(grid, sr, {
       quant_tile_128x1_t_fast<DT_BF16, G_, S_, false, true><<<grd, blk, 0, st>>>(ac, ar);

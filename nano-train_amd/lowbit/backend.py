@@ -273,12 +273,12 @@ def _fp8_recipe_backward(backend, dy2, x2, weight, base, needs):
     fmt, bits, rnd, seed = backend.code_format, backend.bits, backend._rounding_mode, backend.seed
     dx = dw = None
     qdy = qdyt = None
-    if needs[0] and needs[1] and rnd != "stochastic":
-        # one pass over dY for both operands.  Under stochastic rounding the
-        # passes are bound by their Philox draws, which a joint pass cannot
-        # share, and two separate passes run faster (c3 dY: 395 vs 460 us)
+    # dY's 1x128 and 128x1 quantizations share one Philox offset, so an
+    # element draws the same word in both layouts: one pass over dY writes
+    # both operands and, under stochastic rounding, draws each word once
+    if needs[0] and needs[1]:
         qdy, qdyt = ops.quant_dual_1x128_128x1(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed,
-                                               offset_rows=base + 2, offset_cols=base + 3, want_nan_rows=True)
+                                               offset_rows=base + 2, offset_cols=base + 2, want_nan_rows=True)
     if needs[0]:
         if qdy is None:
             qdy = ops.quant_tile_1x128(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 2,
@@ -288,7 +288,7 @@ def _fp8_recipe_backward(backend, dy2, x2, weight, base, needs):
         dx = ops.gemm_blockscaled(qdy, qwt, out_dtype=torch.float32 if dy2.dtype == torch.float32 else dy2.dtype)
     if needs[1]:
         if qdyt is None:
-            qdyt = ops.quant_tile_128x1_t(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 3,
+            qdyt = ops.quant_tile_128x1_t(dy2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 2,
                                           want_nan_rows=True)
         qxt = ops.quant_tile_128x1_t(x2, fmt=fmt, bits=bits, rounding=rnd, seed=seed, offset=base + 4,
                                      want_nan_rows=True)

@@ -129,31 +129,33 @@ float ntlo_e4m3_to_f32(uint8_t c) {
   return sign ? -v : v;
 }
 
-/* Stochastic rounding onto the e4m3 grid.  No reference function exists;
- * this applies the reference rule floor(v+u) / ceil(v-u) (te_backend.py:61-65)
- * in units of the local e4m3 spacing: with a = |v| and ulp the e4m3 spacing
- * at a (2^-9 below 2^-6, else 2^(floor(log2 a)-3)), t = a/ulp is exact and the
- * magnitude is floor(fp32(t + u)) * ulp; the sign of v is kept.  Inputs are
- * already clamped to [-448, 448]. */
-static uint8_t e4m3_stochastic(float v, float u) {
+/* Stochastic rounding onto the e4m3 grid, the integer form: with |v| in
+ * [8, 16) units of its e4m3 spacing, the 20 bits of |v| just below the
+ * spacing (truncated) plus the top 20 bits of the contract word r carry into
+ * the code: |v| rounds away from zero iff frac20 + (r >> 12) >= 2^20.  In the
+ * subnormal range (spacing 2^-9) frac20 is the 20 bits of |v| * 512 just
+ * below the integer part.  The sign of v is kept; inputs are already clamped
+ * to [-448, 448] (at 448 frac20 is 0). */
+static uint8_t e4m3_stochastic(float v, uint32_t r) {
   if (isnan(v)) return ntlo_e4m3_from_f32(v);
-  float a = fabsf(v);
   uint32_t bits;
   memcpy(&bits, &v, 4);
   uint8_t sign = (uint8_t)((bits >> 24) & 0x80u);
-  if (a >= 448.0f) return (uint8_t)(sign | 0x7E);
-  int sh; /* ulp = 2^sh */
-  if (a < 0x1p-6f) {
-    sh = -9;
+  uint32_t ab = bits & 0x7FFFFFFFu;
+  if (ab >= 0x43E00000u) return (uint8_t)(sign | 0x7E); /* >= 448 */
+  uint32_t e8 = ab >> 23, trunc, f20;
+  if (e8 >= 121u) {
+    trunc = ((e8 - 120u) << 3) + ((ab >> 20) & 7u);
+    f20 = ab & 0xFFFFFu;
   } else {
-    int e;
-    frexpf(a, &e); /* a in [2^(e-1), 2^e) */
-    sh = (e - 1) - 3;
+    uint64_t m = (ab & 0x7FFFFFu) | (e8 ? 0x800000u : 0u);
+    uint32_t sh = 141u - (e8 ? e8 : 1u); /* |v| * 512 = m / 2^sh */
+    trunc = sh < 64u ? (uint32_t)(m >> sh) : 0u;
+    f20 = sh - 20u < 64u ? (uint32_t)((m >> (sh - 20u)) & 0xFFFFFu) : 0u;
   }
-  float t = ldexpf(a, -sh);
-  float n = floorf(t + u);
-  float r = ldexpf(n, sh);
-  return (uint8_t)(sign | ntlo_e4m3_from_f32(r));
+  uint32_t c = trunc + ((f20 + (r >> 12)) >> 20);
+  if (c > 0x7Eu) c = 0x7Eu;
+  return (uint8_t)(sign | c);
 }
 
 /* ------------------------------------------------------------------ */
@@ -202,7 +204,7 @@ static float quant_one(float x, float s, int grid, int qmax, int rounding, uint3
   /* e4m3: clamp to the finite range first (layers.py:115), then cast */
   if (v < -448.0f) v = -448.0f;
   if (v > 448.0f) v = 448.0f;
-  uint8_t c = (rounding == ROUND_STOCHASTIC) ? e4m3_stochastic(v, sr_uniform(r)) : ntlo_e4m3_from_f32(v);
+  uint8_t c = (rounding == ROUND_STOCHASTIC) ? e4m3_stochastic(v, r) : ntlo_e4m3_from_f32(v);
   *code = c;
   return ntlo_e4m3_to_f32(c);
 }
@@ -459,7 +461,7 @@ void ntlo_e4m3_sr_encode_array(const float* v, const uint32_t* r, int64_t n, uin
     float x = v[i];
     if (x < -448.0f) x = -448.0f;
     if (x > 448.0f) x = 448.0f;
-    out[i] = e4m3_stochastic(x, sr_uniform(r[i]));
+    out[i] = e4m3_stochastic(x, r[i]);
   }
 }
 

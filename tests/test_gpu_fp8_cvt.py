@@ -50,3 +50,22 @@ def test_hw_bf16_convert_matches_software_rounding(gpu_device):
     assert int(fields["non_nan_mismatches"]) == 0, res.stdout
     assert int(fields["nan_not_nan"]) == 0, res.stdout
     assert res.returncode == 0
+
+
+SR_PROBE = os.path.join(ROOT, "tests", "hip", "fp8_sr_cvt_probe")
+
+
+def test_hw_fp8_stochastic_convert_matches_software_rule(gpu_device):
+    """The stochastic-rounding tile paths round to e4m3 with v_cvt_sr_fp8_f32;
+    its rounding must be e4m3_sr's (and the oracle's) for every fp32 |v| <=
+    448, with random words and with the words at and just below the carry
+    threshold."""
+    if not os.path.exists(SR_PROBE):
+        pytest.fail("tests/hip/fp8_sr_cvt_probe is not built; run __graft_entry__.build()")
+    res = subprocess.run([SR_PROBE], capture_output=True, text=True, timeout=120)
+    line = res.stdout.splitlines()[0]
+    assert line.startswith("status=no error"), res.stdout
+    fields = dict(re.findall(r"(\w+)=(\d+)", line))
+    assert int(fields["checked"]) > 8_000_000_000
+    assert int(fields["mismatches"]) == 0, res.stdout
+    assert res.returncode == 0

@@ -214,7 +214,7 @@ def test_fp8_recipe_backward(gpu_device, rounding):
     wd = O.quant_block_128x128(to_np32(w), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 1)[3]
     dx_ref = dyd.astype(np.float64) @ wd.astype(np.float64)
     assert rel_fro_bf16(x.grad, dx_ref) <= 1e-3
-    dytd = O.quant_tile_128x1_t(to_np32(dy), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 3)[3]
+    dytd = O.quant_tile_128x1_t(to_np32(dy), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 2)[3]
     xtd = O.quant_tile_128x1_t(to_np32(x), grid=O.GRID_E4M3, rounding=rc, seed=77, offset=base + 4)[3]
     dw_ref = dytd.T.astype(np.float64) @ xtd.astype(np.float64)
     assert rel_fro_bf16(w.grad, dw_ref) <= 1e-3
@@ -336,7 +336,7 @@ def test_c3_backward_full_size_sampled(gpu_device, rounding):
     N = w.shape[0]
     rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
     kw = dict(grid=O.GRID_E4M3, rounding=rc, seed=5)
-    # the backend's offsets on its first call: X 0, W 1, dY 1x128 2, dY 128x1 3, X 128x1 4
+    # the backend's offsets on its first call: X 0, W 1, dY 2 (1x128 and 128x1), X 128x1 4
     rows = np.sort(np.random.default_rng(0).choice(M, 16, replace=False))
     kblocks = [3, 40]  # two 128-column blocks of K
     kcols = np.concatenate([np.arange(b * 128, b * 128 + 128) for b in kblocks])
@@ -348,7 +348,7 @@ def test_c3_backward_full_size_sampled(gpu_device, rounding):
     dx_ref = dyd.astype(np.float64) @ wd.astype(np.float64)
     assert rel_fro_bf16(xg.grad[rows][:, kcols], dx_ref) <= 1e-3
     dytd = np.concatenate([O.quant_tile_128x1_t(np.ascontiguousarray(dyn[:, n:n + 1]), elem_base=int(n), elem_row=N,
-                                                offset=3, **kw)[3] for n in ncols], axis=1)
+                                                offset=2, **kw)[3] for n in ncols], axis=1)
     xtd = np.concatenate([O.quant_tile_128x1_t(np.ascontiguousarray(xn[:, b * 128:b * 128 + 128]), elem_base=b * 128,
                                                elem_row=K, offset=4, **kw)[3] for b in kblocks], axis=1)
     dw_ref = dytd.T.astype(np.float64) @ xtd.astype(np.float64)

@@ -135,9 +135,12 @@ def test_tile_128x1_fast_path_special_columns(gpu_device, shape, dtype, fmt, gri
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("fmt,grid", GRIDS)
 @pytest.mark.parametrize("rname,rcode", ROUNDS)
-def test_dual_1x128_128x1_parity(gpu_device, shape, dtype, fmt, grid, rname, rcode):
+@pytest.mark.parametrize("o_cols", [3, 2])
+def test_dual_1x128_128x1_parity(gpu_device, shape, dtype, fmt, grid, rname, rcode, o_cols):
     """The one-pass dY quantizer writes exactly the 1x128 and the 128x1
-    outputs of the oracle (and of the two single-output kernels)."""
+    outputs of the oracle (and of the two single-output kernels), with the
+    two layouts keyed at different offsets, or at one offset, where the
+    stochastic-rounding pass draws each word once for both."""
     from lowbit import ops
 
     R, K = shape
@@ -146,7 +149,7 @@ def test_dual_1x128_128x1_parity(gpu_device, shape, dtype, fmt, grid, rname, rco
     x[0, 3] = float("inf")
     x[:, 5] = 0.0
     x = x.to(dtype).to(gpu_device)
-    qr, qc = ops.quant_dual_1x128_128x1(x, fmt=fmt, rounding=rname, seed=9, offset_rows=2, offset_cols=3,
+    qr, qc = ops.quant_dual_1x128_128x1(x, fmt=fmt, rounding=rname, seed=9, offset_rows=2, offset_cols=o_cols,
                                         want_nan_rows=True)
     torch.cuda.synchronize()
     xn = to_np32(x)
@@ -154,12 +157,12 @@ def test_dual_1x128_128x1_parity(gpu_device, shape, dtype, fmt, grid, rname, rco
     assert_bits_equal(qr.codes.cpu().numpy(), codes, "1x128 codes")
     assert_bits_equal(scales_row_major(qr, R, scales.shape[1]), scales, "1x128 scales")
     assert np.array_equal(qr.nan_rows.cpu().numpy(), np.isnan(qv).any(axis=1).astype(np.int32))
-    ct, st, _, _ = O.quant_tile_128x1_t(xn, grid=grid, rounding=rcode, seed=9, offset=3)
+    ct, st, _, _ = O.quant_tile_128x1_t(xn, grid=grid, rounding=rcode, seed=9, offset=o_cols)
     assert_bits_equal(qc.codes.cpu().numpy(), ct, "128x1 codes_t")
     assert_bits_equal(scales_row_major(qc, K, st.shape[1]), st, "128x1 scales")
     assert np.array_equal(qc.nan_rows.cpu().numpy(), np.isnan(xn).any(axis=0).astype(np.int32))
     q1 = ops.quant_tile_1x128(x, fmt=fmt, rounding=rname, seed=9, offset=2)
-    q2 = ops.quant_tile_128x1_t(x, fmt=fmt, rounding=rname, seed=9, offset=3)
+    q2 = ops.quant_tile_128x1_t(x, fmt=fmt, rounding=rname, seed=9, offset=o_cols)
     assert torch.equal(q1.codes, qr.codes) and torch.equal(q2.codes, qc.codes)
     # tile-major scale arrays pad rows to a multiple of 4; compare what is written
     assert torch.equal(q1.scales[:, :R], qr.scales[:, :R]) and torch.equal(q2.scales[:, :K], qc.scales[:, :K])
@@ -209,6 +212,15 @@ def test_c3_dy_full_size_stochastic_rounding(gpu_device, fmt, grid):
     assert torch.equal(qd.codes, q1.codes) and torch.equal(qdt.codes, q2.codes)
     R, K = dy.shape
     assert torch.equal(qd.scales[:, :R].t(), q1.scales) and torch.equal(qdt.scales[:, :K], q2.scales[:, :K])
+    del qd, qdt, q2
+    # one offset for both layouts (the recipe backward's keying): the dual
+    # pass draws each word once and matches the single passes at that offset
+    qd, qdt = ops.quant_dual_1x128_128x1(dyg, fmt=fmt, rounding="stochastic", seed=3, offset_rows=o_rows,
+                                         offset_cols=o_rows)
+    q3 = ops.quant_tile_128x1_t(dyg, fmt=fmt, rounding="stochastic", seed=3, offset=o_rows)
+    torch.cuda.synchronize()
+    assert torch.equal(qd.codes, q1.codes) and torch.equal(qdt.codes, q3.codes)
+    assert torch.equal(qdt.scales[:, :K], q3.scales[:, :K])
 
 
 @pytest.mark.parametrize("fmt,grid", GRIDS)
@@ -290,19 +302,18 @@ def test_sr_clamps_after_rounding_at_the_tile_amax(gpu_device, sign):
 @pytest.mark.parametrize("sign", [1.0, -1.0])
 def test_e4m3_sr_clamps_after_rounding_at_448(gpu_device, sign):
     """The e4m3 counterpart: with every element at +-448 the scale is 1 and
-    v = +-448 = 1.75 * 2^8, whose spacing-scaled mantissa is t = 14; where
-    u >= 1 - 2^-21, 14 + u rounds to 15 in fp32 (the tie goes to even), one
-    binade past the largest finite code.  The result must clamp to 0x7E /
-    0xFE, not land on the NaN code 0x7F.  Checked in 1x128 tiles (2^24
-    elements: 7 such draws with this seed) and in 128x1 tiles (128 x 65536: 4)
-    against the oracle."""
+    v = +-448 = 1.75 * 2^8 sits on a code, so the 20 bits below its spacing
+    are zero and no word carries it up, not even one with r >> 12 = 2^20 - 1:
+    every code is 0x7E / 0xFE, never the NaN code 0x7F.  Checked in 1x128
+    tiles (2^24 elements, several such words with this seed) and in 128x1
+    tiles (128 x 65536) against the oracle."""
     from lowbit import ops
 
     seed, offset = 77, 5
     code = 0x7E if sign > 0 else 0xFE
     R = 1 << 21
     words = O.sr_bits(seed, offset, 0, R * 8)
-    assert int(((words >> 8) >= (1 << 24) - 8).sum()) > 0
+    assert int(((words >> 12) == (1 << 20) - 1).sum()) > 0
     x = torch.full((R, 8), 448.0 * sign)
     q = ops.quant_tile_1x128(x.to(torch.bfloat16).to(gpu_device), fmt="e4m3", rounding="stochastic", seed=seed,
                              offset=offset)
@@ -314,7 +325,7 @@ def test_e4m3_sr_clamps_after_rounding_at_448(gpu_device, sign):
     assert_bits_equal(codes, c_ref[:, :8], "1x128 codes")
     K = 65536
     words = O.sr_bits(seed, offset, 0, 128 * K)
-    assert int(((words >> 8) >= (1 << 24) - 8).sum()) > 0
+    assert int(((words >> 12) == (1 << 20) - 1).sum()) > 0
     xt = torch.full((128, K), 448.0 * sign)
     qt = ops.quant_tile_128x1_t(xt.to(torch.bfloat16).to(gpu_device), fmt="e4m3", rounding="stochastic",
                                 seed=seed, offset=offset)

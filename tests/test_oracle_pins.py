@@ -469,3 +469,53 @@ def test_slice_index_base_reproduces_rows_and_columns_under_sr():
     full_t = O.quant_tile_128x1_t(x, **kw)
     cols = O.quant_tile_128x1_t(np.ascontiguousarray(x[:, 40:45]), elem_base=40, elem_row=300, **kw)
     assert np.array_equal(cols[0], full_t[0][40:45]) and np.array_equal(cols[1], full_t[1][40:45])
+
+
+def test_sr_e4m3_rule_against_exact_rationals():
+    """The oracle's e4m3 stochastic rounding, pinned against the rule stated
+    with exact rationals: x = |v| / spacing (spacing 2^(e-3) for |v| in
+    [2^e, 2^(e+1)), 2^-9 below 2^-6), f20 = floor(frac(x) * 2^20); the code
+    rounds away from zero iff f20 + (r >> 12) >= 2^20.  Random |v| over the
+    whole e4m3 range (subnormals, tiny values, up to 448), random words, and
+    the words at and just below each carry threshold."""
+    from fractions import Fraction
+
+    rng = np.random.default_rng(20262501)
+    n = 3000
+    e = rng.uniform(-40, np.log2(448.0), size=n)
+    v = (np.exp2(e) * rng.choice([-1.0, 1.0], size=n)).astype(np.float32)
+    v = np.clip(v, np.float32(-448.0), np.float32(448.0))
+    r = rng.integers(0, 2**32, size=n, dtype=np.uint64).astype(np.uint32)
+
+    def parts(x):
+        a = Fraction(abs(float(x)))
+        spacing = Fraction(1, 512)
+        if a >= Fraction(1, 64):
+            ex = 0
+            while Fraction(2) ** ex > a:
+                ex -= 1
+            while Fraction(2) ** (ex + 1) <= a:
+                ex += 1
+            spacing = Fraction(2) ** (ex - 3)
+        q = a / spacing
+        k = q.numerator // q.denominator
+        return k, ((q - k) * (1 << 20)).__floor__(), spacing
+
+    cases = []
+    for x, w in zip(v, r):
+        _, f20, _ = parts(x)
+        at = (((1 << 20) - f20) % (1 << 20)) << 12
+        cases += [(x, int(w)), (x, at)] + ([(x, at - 4096)] if at >= 4096 else [])
+    vs = np.array([c[0] for c in cases], dtype=np.float32)
+    ws = np.array([c[1] for c in cases], dtype=np.uint32)
+    codes = O.e4m3_sr_encode(vs, ws)
+    vals = O.decode_codes(codes, O.GRID_E4M3)
+    ups = 0
+    for x, w, c, val in zip(vs, ws, codes, vals):
+        k, f20, spacing = parts(x)
+        up = f20 + (int(w) >> 12) >= (1 << 20)
+        ups += up
+        assert Fraction(abs(float(val))) == (k + up) * spacing, (float(x), hex(int(w)), hex(int(c)))
+        if k + up:
+            assert bool(c & 0x80) == bool(np.signbit(x))
+    assert 0 < ups < len(cases)
