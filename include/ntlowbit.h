@@ -728,7 +728,9 @@ int ntlb_moe_capacity_keep(const int32_t* inv, const int32_t* offsets, int n_exp
  * weights` (moe.py:1087-1088, :489-490): for token t's slot s with row r =
  * pos[t*K + s] >= 0, dy[r] = d_out[t] * topk_w[t, s] rounded to `dtype` (the
  * gradient of expert_out) and d_w[t, s] = sum over H of d_out[t] * y[r] in
- * fp32, stored in w_dtype (the gradient of the routing weight); a dropped slot
+ * fp32, stored in w_dtype (the gradient of the routing weight; when w_dtype
+ * is dtype's 16-bit type, each product is rounded to it first, as torch's mul
+ * backward forms them); a dropped slot
  * (r < 0) gets d_w = 0 and writes no row.  d_out [T, ldo], y [n, ldy] and dy
  * [n, lddy] share `dtype`; 1 <= K <= 8.
  */

@@ -9,7 +9,9 @@
 //     assignment -> row map (-1 for a dropped assignment);
 //   moe_combine_backward: the gradient of the combine: dY[row] =
 //     d_out[token] * w in y's dtype and d_w = sum over H of d_out[token] *
-//     y[row] in fp32;
+//     y[row] in fp32, each product first rounded to y's dtype when w has
+//     that 16-bit dtype (autograd's mul backward forms the bf16 products,
+//     then sums them);
 //   swiglu_backward: the gradient of gated = silu(gate) * up through torch's
 //     bf16 op sequence (F.silu, mul), in B's interleaved gate / up columns.
 #include <hip/hip_runtime.h>
@@ -96,6 +98,9 @@ __global__ void __launch_bounds__(CB_THREADS) combine_backward_kernel(const void
   __shared__ float red[CB_MAX_K][CB_THREADS / 64];
   const int64_t t = blockIdx.x;
   const int tid = threadIdx.x;
+  // w of y's 16-bit dtype: the products d * y are that dtype's (mul of two
+  // bf16 tensors), rounded before the sum
+  const bool rnd_prod = DT != DT_F32 && w_dt == DT;
   int32_t row[CB_MAX_K];
   float w[CB_MAX_K], dot[CB_MAX_K];
 #pragma unroll
@@ -140,7 +145,7 @@ __global__ void __launch_bounds__(CB_THREADS) combine_backward_kernel(const void
         }
         uint32_t o[4];
 #pragma unroll
-        for (int q = 0; q < per; ++q) dot[s] += d[q] * yy[q];
+        for (int q = 0; q < per; ++q) dot[s] += rnd_prod ? round_to_dtype(d[q] * yy[q], DT) : d[q] * yy[q];
         if constexpr (DT == DT_F32) {
 #pragma unroll
           for (int q = 0; q < 4; ++q) o[q] = __float_as_uint(d[q] * w[s]);
@@ -163,7 +168,7 @@ __global__ void __launch_bounds__(CB_THREADS) combine_backward_kernel(const void
       for (int s = 0; s < CB_MAX_K; ++s) {
         if (row[s] < 0) continue;
         const float yy = load_elem(y, DT, (int64_t)row[s] * ldy + c);
-        dot[s] += d * yy;
+        dot[s] += rnd_prod ? round_to_dtype(d * yy, DT) : d * yy;
         store_elem(dy, DT, (int64_t)row[s] * lddy + c, d * w[s]);
       }
     }

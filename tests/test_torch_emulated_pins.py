@@ -163,3 +163,62 @@ def test_autograd_accumulates_gathered_token_gradients_in_descending_expert_orde
 
     assert torch.equal(accum(range(E - 1, -1, -1)), tok.grad)
     assert not torch.equal(accum(range(E)), tok.grad)
+
+
+def _rel(a: torch.Tensor, b: torch.Tensor) -> float:
+    a, b = a.double(), b.double()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+@pytest.mark.parametrize("forward", ["reference", "fp32_dq"])
+@pytest.mark.parametrize("capacity", [0, 5])
+def test_local_moe_loop_matches_a_dense_restatement(forward, capacity):
+    """local_moe_loop (the reference's gather / ExpertMLP / index-add loop
+    under autograd) against a dense float64 restatement with no gathers:
+    out[t] = sum over kept slots s of w[t, s] * down_e(silu(gate_e(x_t)) *
+    up_e(x_t)), e = idx[t, s], where gate row j of w_gate_up is row
+    256 * (j // 128) + j % 128 and up row j is 128 rows after it, and a slot is
+    kept when fewer than `capacity` assignments of its expert have a larger
+    weight.  The quantizer is the identity here, so the straight-through
+    gradients are the function's exact gradients; the bar is bf16's rounding
+    of the loop's intermediates.  A swapped gate/up block, a dropped routing
+    weight or a wrong capacity choice is off by O(1)."""
+    Tn, H, I, E, k = 24, 128, 256, 4, 2
+    g = torch.Generator().manual_seed(20262531)
+    tokens = torch.randn(Tn, H, generator=g).bfloat16()
+    idx = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(Tn)])
+    w = torch.softmax(torch.randn(Tn, k, generator=g) * 2, dim=-1)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * H ** -0.5).bfloat16()
+    wd = (torch.randn(E, H, I, generator=g) * I ** -0.5).bfloat16()
+    leaves = [t.clone().requires_grad_(True) for t in (tokens, w, wgu, wd)]
+    out = T.local_moe_loop(leaves[0], idx, leaves[1], leaves[2], leaves[3], capacity=capacity, forward=forward,
+                           qdq=lambda t, gr, gc: t)
+    d_out = torch.randn(Tn, H, generator=g).bfloat16()
+    out.backward(d_out)
+    # the dense restatement
+    ref = [t.detach().double().requires_grad_(True) for t in (tokens, w, wgu, wd)]
+    x64, w64, gu64, d64 = ref
+    j = torch.arange(I)
+    gate_rows = 256 * (j // 128) + j % 128
+    kept = torch.ones(Tn, k, dtype=torch.bool)
+    if capacity > 0:
+        for t in range(Tn):
+            for s in range(k):
+                same = idx == idx[t, s]
+                kept[t, s] = int((same & (w > w[t, s])).sum()) < capacity
+        assert not bool(kept.all())
+    rows = []
+    for t in range(Tn):
+        acc = torch.zeros(H, dtype=torch.float64)
+        for s in range(k):
+            if kept[t, s]:
+                e = int(idx[t, s])
+                gt = gu64[e, gate_rows] @ x64[t]
+                up = gu64[e, gate_rows + 128] @ x64[t]
+                acc = acc + w64[t, s] * (d64[e] @ (torch.nn.functional.silu(gt) * up))
+        rows.append(acc)
+    out64 = torch.stack(rows)
+    out64.backward(d_out.double())
+    assert _rel(out.detach(), out64.detach()) < 1e-2
+    for a, b in zip(leaves, ref):
+        assert _rel(a.grad, b.grad) < 1e-2
