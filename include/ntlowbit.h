@@ -580,6 +580,45 @@ int ntlb_gemm_lowbit_ws(int fmt, const void* x, int64_t ldx, const uint8_t* w, c
                         int64_t ldy, void* workspace, int64_t ws_bytes, void* stream);
 
 /*
+ * The input gradient of a persistent layer, dX[M, K] = dY[M, N] . deq(W),
+ * with the weight decoded inside the GEMM instead of dequantized to a copy:
+ * the straight-through backward of _persistent_weight_ste (layers.py:409-436,
+ * dX = dY . w_q under autograd) for fmt NTLB_LOWBIT_NF4 (W's nibbles flat as
+ * _quantize_nf4_persistent packs them, layers.py:130-169) or NTLB_LOWBIT_FP8P
+ * (float8_e4m3fn codes [N, K], layers.py:104-127).  op_dtype NTLB_BF16: each
+ * weight is codebook value (or e4m3 value) times scale in fp32, rounded to
+ * bf16 as _dequantize_*_persistent(..., target_dtype=bf16) rounds it, on bf16
+ * MFMA; NTLB_F32: the fp32 values on fp32 MFMA.  dY [M, lddy] in op_dtype with
+ * lddy >= N rounded up to 64 (bf16) or 32 (fp32) and zero pad columns;
+ * w_scales fp32, 16-byte aligned: one per weight row (block = K) or one for
+ * all (block 0 or N*K); K % 4 == 0.  workspace as for ntlb_gemm_ste_dgrad_ws
+ * (sized by ntlb_gemm_dq_workspace_bytes(op_dtype, M, K, N)); NULL runs
+ * every tile whole.
+ */
+int ntlb_gemm_lowbit_dgrad_ws(int fmt, int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N,
+                              const uint8_t* w, const float* w_scales, int64_t block, int64_t K, void* dx,
+                              int dx_dtype, int64_t lddx, void* workspace, int64_t ws_bytes, void* stream);
+
+/*
+ * The persistent forward Y[M, N] = x[M, K] . deq(W)^T (+ bias) where
+ * ntlb_gemm_lowbit_ws does not apply: fp32 activations (op_dtype NTLB_F32,
+ * fp32 weight values on fp32 MFMA) or bf16 activations with K % 64 != 0
+ * (F.linear(x, _persistent_weight_ste(), bias), layers.py:409-436 and
+ * :595-632, without the dequantized copy).  fmt NTLB_LOWBIT_NF4 or
+ * NTLB_LOWBIT_FP8P as for ntlb_gemm_lowbit_dgrad_ws, one scale per weight row
+ * (block = K) or one for all (0 or N*K), K % 4 == 0.  x [M, ldx] in op_dtype
+ * with ldx >= K rounded up to 64 (bf16) or 32 (fp32) and zero pad columns;
+ * the weight's codes past K (the next row's) are masked out of the
+ * contraction.  bias (optional, any float dtype) is added in fp32 before the
+ * output rounding.  workspace sized by ntlb_gemm_dq_workspace_bytes(op_dtype,
+ * M, N, K); NULL runs every tile whole.
+ */
+int ntlb_gemm_lowbit_dq_forward_ws(int fmt, int op_dtype, const void* x, int64_t ldx, int64_t M, const uint8_t* w,
+                                   const float* w_scales, int64_t block, int64_t N, int64_t K, const void* bias,
+                                   int bias_dtype, void* y, int y_dtype, int64_t ldy, void* workspace,
+                                   int64_t ws_bytes, void* stream);
+
+/*
  * Expert-parallel dispatch wire format: one fixed-size record per routed
  * (token, slot) assignment, so that a single byte all-to-all replaces the
  * payload and four metadata all-to-alls of _dispatch_tokens

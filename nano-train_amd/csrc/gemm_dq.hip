@@ -15,6 +15,7 @@
 //   the straight-through wgrad       dW = dY^T . bf16(dq(X))
 //   plain GEMMs over dequantized tensors (granularities whose scales vary
 //   along the contraction element by element)
+//   the persistent layers' dgrad       dX = dY . deq(W)                     (layers.py:409-436 straight through)
 //
 // Operand sources (one per operand, a template parameter):
 //   SRC_DIRECT : bf16/fp32 [rows, >= Kc] row-major, contraction contiguous;
@@ -28,6 +29,16 @@
 //                it transposed
 //   SRC_TCODES : codes stored transposed, (r, c) at codes[c*ldc + r] (W for
 //                dgrad, X for wgrad), decoded and written transposed
+//   SRC_TNF4   : a persistent NF4 weight stored transposed, its nibbles flat
+//                row-major over [contraction, rows] (two per byte, the even
+//                element low): codebook value times scale, for the dgrad of
+//                a persistent layer without a dequantized copy
+//   SRC_PCODES : a persistent NF4 or FP8 weight [rows, K] row-major (NF4
+//                nibbles flat, two per byte), contraction contiguous, one
+//                scale per row or one for all; values past K are zero (the
+//                next row's codes follow in memory): the forward of a
+//                persistent layer over fp32 activations or a K that is not
+//                a multiple of 64
 // Scales of a coded operand: s(r, c) = s[(r >> r_shift)*s_r + (c >> c_shift)*s_c].
 //
 // Tiling: 256x256 output tile per workgroup, K step of 128 bytes per row (64
@@ -57,7 +68,12 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int SRC_DIRECT = 0, SRC_CODES = 1, SRC_TDIRECT = 2, SRC_TCODES = 3;
+constexpr int SRC_DIRECT = 0, SRC_CODES = 1, SRC_TDIRECT = 2, SRC_TCODES = 3, SRC_TNF4 = 4, SRC_PCODES = 5;
+// the code format of a SRC_PCODES operand (the GRID parameter): e4m3 codes,
+// or NF4 nibbles
+constexpr int GRID_NF4 = 2;
+
+constexpr float kNF4v[16] = NTLB_NF4_CODEBOOK;
 constexpr int EL_BF16 = 0, EL_F32 = 1;
 
 constexpr int TM = 256, TN = 256;  // output tile
@@ -371,14 +387,17 @@ struct Stager<SRC_TCODES, EL, GRID, SCM> {
       sc1 = __uint_as_float(
           __builtin_amdgcn_raw_buffer_load_b32(rss, (int)((soff + (uint32_t)((c >> o.c_shift) * o.s_c)) * 4), 0, 0));
     } else {
-      // scales of rows past kvalid read as zero (or as the next scale row):
-      // their codes are zero
+      // rows past kvalid hold zero codes, but the scale slots there are the
+      // array's padding or the next rows' scales, which can be NaN or inf:
+      // their scales are taken as zero so that 0 * scale adds nothing
 #pragma unroll
       for (int k = 0; k < CPW / 4; ++k) {
         const uint4 v = __builtin_bit_cast(
             uint4, __builtin_amdgcn_raw_buffer_load_b128(rss, (int)((soff + (uint32_t)cbase + 4 * k) * 4), 0, 0));
-        sc[4 * k] = __uint_as_float(v.x); sc[4 * k + 1] = __uint_as_float(v.y);
-        sc[4 * k + 2] = __uint_as_float(v.z); sc[4 * k + 3] = __uint_as_float(v.w);
+        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sc[4 * k + i] = (int64_t)(cbase + 4 * k + i) < o.kvalid ? __uint_as_float(vv[i]) : 0.f;
       }
     }
   }
@@ -388,6 +407,150 @@ struct Stager<SRC_TCODES, EL, GRID, SCM> {
     float v[CPW][2];
 #pragma unroll
     for (int j = 0; j < CPW; ++j) decode2<GRID, H>(w[j], SCM == SC_SHARED ? sc1 : sc[j], v[j][0], v[j][1]);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii) {
+      const int i = 2 * h + ii;
+      uint4 out;
+      if constexpr (EL == EL_BF16) {
+        out = make_uint4(pack_bf16(v[0][ii], v[1][ii]), pack_bf16(v[2][ii], v[3][ii]), pack_bf16(v[4][ii], v[5][ii]),
+                         pack_bf16(v[6][ii], v[7][ii]));
+      } else {
+        out = make_uint4(__float_as_uint(v[0][ii]), __float_as_uint(v[1][ii]), __float_as_uint(v[2][ii]),
+                         __float_as_uint(v[3][ii]));
+      }
+      *reinterpret_cast<uint4*>(tile + sw(4 * l + i, cw)) = out;
+    }
+  }
+};
+
+// PCODES: thread t decodes row t/2, half t%2 of the K block (as CODES), from
+// a buffer resource over the whole weight: NF4 as 2-byte loads of four
+// nibbles (the rows start at K/2-byte offsets, K % 4 == 0), e4m3 as 4-byte
+// loads of four codes (K % 4 == 0).  The row's scale is loaded once.  Columns
+// at or past K (kvalid) decode to 0: the loads there return the next row's
+// codes, or zero past the buffer.
+template <int EL, int GRID, int SCM>
+struct Stager<SRC_PCODES, EL, GRID, SCM> {
+  static constexpr int span = ElemT<EL>::kstep / 2;  // elements per thread per K step: 32 or 16
+  static constexpr int NWD = span / 4;                 // words of four codes
+  uint32_t w[NWD];
+  float sc;
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t rowb;  // byte offset of the row
+  int br, bh;
+  int lim;        // elements of the loaded block inside K (0 .. span)
+  const float* cb;  // NF4: the codebook in LDS, set by the kernel
+  __device__ void init(const Operand& o, int64_t r0, int tid, int) {
+    br = tid >> 1;
+    bh = tid & 1;
+    const int64_t r = min<int64_t>(r0 + br, o.rows - 1);  // rows past the end feed outputs never stored
+    rs = __builtin_amdgcn_make_buffer_rsrc((void*)o.p, (short)0, (int)(o.rows * o.ld), 0x00020000);
+    rowb = (uint32_t)(r * o.ld);
+    sc = o.s[(r >> o.r_shift) * o.s_r];
+  }
+  __device__ void load(const Operand& o, int kt) {
+    const uint32_t c0 = (uint32_t)(kt * ElemT<EL>::kstep + bh * span);
+    lim = (int)max<int64_t>(0, min<int64_t>(o.kvalid - (int64_t)c0, span));
+#pragma unroll
+    for (int j = 0; j < NWD; ++j) {
+      if constexpr (GRID == GRID_NF4)
+        w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)(rowb + ((c0 + 4 * j) >> 1)), 0, 0);
+      else
+        w[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(rowb + c0 + 4 * j), 0, 0);
+    }
+  }
+  // the four values of word j (elements c0 + 4j .. c0 + 4j + 3)
+  __device__ void value4(const Operand& o, int j, int lim, float (&v)[4]) {
+#pragma clang fp contract(off)
+    if constexpr (GRID == GRID_NF4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = cb[(w[j] >> (4 * i)) & 0xF] * sc;
+    } else {
+      decode4<GRID_E4M3>(w[j], sc, v);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = 4 * j + i < lim ? v[i] : 0.f;
+  }
+  template <int H>
+  __device__ void decode_half(const Operand& o, uint8_t* tile) {
+    constexpr int h = H;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * h + jj;  // chunk of this thread's span
+      uint4 out;
+      if constexpr (EL == EL_BF16) {
+        float a[4], b[4];
+        value4(o, 2 * j, lim, a);
+        value4(o, 2 * j + 1, lim, b);
+        out = make_uint4(pack_bf16(a[0], a[1]), pack_bf16(a[2], a[3]), pack_bf16(b[0], b[1]), pack_bf16(b[2], b[3]));
+      } else {
+        float a[4];
+        value4(o, j, lim, a);
+        out = make_uint4(__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]), __float_as_uint(a[3]));
+      }
+      *reinterpret_cast<uint4*>(tile + sw(br, bh * 4 + j)) = out;
+    }
+  }
+};
+
+// TNF4: the TCODES walk over 4-bit codes.  The weight's nibbles run flat
+// over its [kvalid, rows] storage (ld = bytes per stored row = rows / 2), so
+// a lane's four operand rows of one contraction row are one 2-byte load.
+// Value = codebook[nibble] * scale in fp32 (layers.py:172-184), the codebook
+// read from LDS (16 floats, one per bank); rows past kvalid get scale 0 and
+// so the value 0 (nibble 0 is the code value -1, not 0).
+template <int EL, int GRID, int SCM>
+struct Stager<SRC_TNF4, EL, GRID, SCM> {
+  static constexpr int CPW = EL == EL_BF16 ? 8 : 4;
+  uint32_t w[CPW];
+  float sc[CPW];
+  __amdgpu_buffer_rsrc_t rs, rss;
+  uint32_t roff, rstep, soff;
+  int cw, l;
+  const float* cb;  // the codebook in LDS, set by the kernel
+  __device__ void init(const Operand& o, int64_t r0, int tid, int) {
+    cw = __builtin_amdgcn_readfirstlane(tid >> 6);
+    l = tid & 63;
+    const int64_t r = r0 + 4 * l;
+    rs = trows_rsrc(o, 1);
+    roff = (uint32_t)(r >> 1);
+    rstep = (uint32_t)o.ld;
+    rss = __builtin_amdgcn_make_buffer_rsrc((void*)o.s, (short)0, (int)(o.s_extent * 4), 0x00020000);
+    soff = (uint32_t)((min<int64_t>(r, o.rows - 1) >> o.r_shift) * o.s_r);
+  }
+  __device__ void load(const Operand& o, int kt) {
+    const int cbase = kt * ElemT<EL>::kstep + cw * CPW;  // uniform over the wave
+#pragma unroll
+    for (int j = 0; j < CPW; ++j)
+      w[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, (int)((uint32_t)(cbase + j) * rstep + roff), 0, 0);
+    if constexpr (SCM == SC_SHARED) {
+      const int64_t c = min<int64_t>(cbase, o.kvalid - 1);
+      const float s1 = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rss, (int)((soff + (uint32_t)((c >> o.c_shift) * o.s_c)) * 4), 0, 0));
+#pragma unroll
+      for (int j = 0; j < CPW; ++j) sc[j] = (int64_t)(cbase + j) < o.kvalid ? s1 : 0.f;
+    } else {
+#pragma unroll
+      for (int k = 0; k < CPW / 4; ++k) {
+        const uint4 v = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rss, (int)((soff + (uint32_t)cbase + 4 * k) * 4), 0, 0));
+        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sc[4 * k + i] = (int64_t)(cbase + 4 * k + i) < o.kvalid ? __uint_as_float(vv[i]) : 0.f;
+      }
+    }
+  }
+  template <int H>
+  __device__ void decode_half(const Operand& o, uint8_t* tile) {
+#pragma clang fp contract(off)
+    constexpr int h = H;
+    float v[CPW][2];
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      v[j][0] = cb[(w[j] >> (8 * h)) & 0xF] * sc[j];
+      v[j][1] = cb[(w[j] >> (8 * h + 4)) & 0xF] * sc[j];
+    }
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii) {
       const int i = 2 * h + ii;
@@ -539,6 +702,12 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   Stager<SB, EL, GRID, SCM> sb;
   sa.init(g.a, m0, tid, lane);
   sb.init(g.b, n0, tid, lane);
+  if constexpr (SB == SRC_TNF4 || (SB == SRC_PCODES && GRID == GRID_NF4)) {
+    __shared__ float nf4_tab[16];
+    if (tid < 16) nf4_tab[tid] = kNF4v[tid];
+    __syncthreads();
+    sb.cb = nf4_tab;
+  }
 
   // logical K step -> the step the loaders read (IL: one half of the
   // interleaved gate / up contraction)
@@ -847,8 +1016,8 @@ void launch(const DqArgs& g, hipStream_t st) {
 
 // the source combinations this library instantiates
 int dispatch(int el, int sa, int sb, const DqArgs& g, hipStream_t st) {
-  const int grid = (sa == SRC_CODES || sa == SRC_TCODES) ? g.a.grid : g.b.grid;
-  const int scm = sb == SRC_TCODES ? g.b.smode : SC_SHARED;
+  const int grid = (sa == SRC_CODES || sa == SRC_TCODES) ? g.a.grid : g.b.grid;  // PCODES: B's format
+  const int scm = (sb == SRC_TCODES || sb == SRC_TNF4) ? g.b.smode : SC_SHARED;
 #define NTLB_DQ_CASE(E, A, B, G)                                \
   if (el == E && sa == A && sb == B && (grid == G || G < 0)) {  \
     launch<E, A, B, (G < 0 ? 0 : G)>(g, st);                    \
@@ -869,6 +1038,16 @@ int dispatch(int el, int sa, int sb, const DqArgs& g, hipStream_t st) {
   NTLB_DQ_CASE_SC(EL_BF16, SRC_TDIRECT, SRC_TCODES, GRID_E4M3, SC_SHARED)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_TDIRECT, SRC_TCODES, GRID_INT, SC_CONTIG)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_TDIRECT, SRC_TCODES, GRID_E4M3, SC_CONTIG)
+  NTLB_DQ_CASE_SC(EL_BF16, SRC_DIRECT, SRC_TNF4, GRID_E4M3, SC_SHARED)
+  NTLB_DQ_CASE_SC(EL_BF16, SRC_DIRECT, SRC_TNF4, GRID_E4M3, SC_CONTIG)
+  NTLB_DQ_CASE_SC(EL_F32, SRC_DIRECT, SRC_TNF4, GRID_E4M3, SC_SHARED)
+  NTLB_DQ_CASE_SC(EL_F32, SRC_DIRECT, SRC_TNF4, GRID_E4M3, SC_CONTIG)
+  NTLB_DQ_CASE_SC(EL_F32, SRC_DIRECT, SRC_TCODES, GRID_E4M3, SC_SHARED)
+  NTLB_DQ_CASE_SC(EL_F32, SRC_DIRECT, SRC_TCODES, GRID_E4M3, SC_CONTIG)
+  NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_PCODES, GRID_NF4)
+  NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_PCODES, GRID_E4M3)
+  NTLB_DQ_CASE(EL_F32, SRC_DIRECT, SRC_PCODES, GRID_NF4)
+  NTLB_DQ_CASE(EL_F32, SRC_DIRECT, SRC_PCODES, GRID_E4M3)
   NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_DIRECT, -1)
   NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_TDIRECT, -1)
   NTLB_DQ_CASE(EL_BF16, SRC_TDIRECT, SRC_TDIRECT, -1)
@@ -1035,6 +1214,82 @@ extern "C" int ntlb_gemm_ste_dgrad(int op_dtype, const void* dy, int64_t lddy, i
                                    int w_shift, int64_t K, void* dx, int dx_dtype, int64_t lddx, void* stream) {
   return ntlb_gemm_ste_dgrad_ws(op_dtype, dy, lddy, M, N, grid, w, ldw, sw, sw_row, sw_col, w_shift, K, dx, dx_dtype,
                                 lddx, nullptr, 0, stream);
+}
+
+extern "C" int ntlb_gemm_lowbit_dgrad_ws(int fmt, int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N,
+                                         const uint8_t* w, const float* w_scales, int64_t block, int64_t K, void* dx,
+                                         int dx_dtype, int64_t lddx, void* workspace, int64_t ws_bytes,
+                                         void* stream) {
+  const char* fn = "ntlb_gemm_lowbit_dgrad";
+  int el;
+  if (int rc = elem_of(op_dtype, fn, el)) return rc;
+  if (fmt != NTLB_LOWBIT_NF4 && fmt != NTLB_LOWBIT_FP8P)
+    return fail(NTLB_EUNSUPPORTED, "%s: NF4 or persistent FP8 weights only (format %d)", fn, fmt);
+  if (M < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (M == 0 || K == 0) return NTLB_OK;
+  if (!dy || !dx || !w || !w_scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (N == 0) return fail(NTLB_EUNSUPPORTED, "%s: N == 0 (dX is zero)", fn);
+  const bool per_row = block == K && N > 1;
+  if (!(block == K || block == 0 || block == N * K))
+    return fail(NTLB_EUNSUPPORTED, "%s: scales must be per weight row (block = K) or per tensor (0 or N*K)", fn);
+  if (K % 4) return fail(NTLB_EUNSUPPORTED, "%s: K must be a multiple of 4", fn);
+  const int kstep = el == EL_BF16 ? 64 : 32, eb = el == EL_BF16 ? 2 : 4;
+  const int64_t Nc = (N + kstep - 1) / kstep * kstep;  // the contraction, zero past N
+  if (lddy < Nc || !aligned(dy, 16) || (lddy * eb) % 16)
+    return fail(NTLB_EINVAL, "%s: dY needs ld >= N rounded up to %d (zero pad columns), 16-byte rows and alignment",
+                fn, kstep);
+  if ((M + 256) * lddy * eb >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: dY exceeds 2 GiB", fn);
+  // bytes per stored weight row: K nibbles or K e4m3 codes
+  const int64_t ldw = fmt == NTLB_LOWBIT_NF4 ? K / 2 : K;
+  if (!aligned(w, fmt == NTLB_LOWBIT_NF4 ? 2 : 4) || !aligned(w_scales, 16))
+    return fail(NTLB_EINVAL, "%s: W needs 2-byte (NF4) or 4-byte (FP8) alignment, its scales 16-byte", fn);
+  if ((N + 64) * ldw >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: W exceeds 2 GiB", fn);
+  DqArgs g{};
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, M, Nc, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  // W^T as the B operand: element (r = k, c = n); one scale per stored row n
+  // (contiguous along the contraction) or one for all
+  g.b = Operand{w, ldw, K, N, w_scales, 0, per_row ? 1 : 0, 0, 0, GRID_E4M3, 0, 0};
+  if (int rc = tcodes_scales(fn, g.b)) return rc;
+  g.M = M; g.N = K; g.Kc = Nc;
+  g.bias = nullptr; g.bias_dtype = 0; g.y = dx;
+  return finish(fn, g, el, SRC_DIRECT, fmt == NTLB_LOWBIT_NF4 ? SRC_TNF4 : SRC_TCODES, dx_dtype, lddx, stream,
+                workspace, ws_bytes);
+}
+
+extern "C" int ntlb_gemm_lowbit_dq_forward_ws(int fmt, int op_dtype, const void* x, int64_t ldx, int64_t M,
+                                              const uint8_t* w, const float* w_scales, int64_t block, int64_t N,
+                                              int64_t K, const void* bias, int bias_dtype, void* y, int y_dtype,
+                                              int64_t ldy, void* workspace, int64_t ws_bytes, void* stream) {
+  const char* fn = "ntlb_gemm_lowbit_dq_forward";
+  int el;
+  if (int rc = elem_of(op_dtype, fn, el)) return rc;
+  if (fmt != NTLB_LOWBIT_NF4 && fmt != NTLB_LOWBIT_FP8P)
+    return fail(NTLB_EUNSUPPORTED, "%s: NF4 or persistent FP8 weights only (format %d)", fn, fmt);
+  if (M < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (M == 0 || N == 0) return NTLB_OK;
+  if (K == 0) return fail(NTLB_EUNSUPPORTED, "%s: K == 0", fn);
+  if (!x || !y || !w || !w_scales) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  const bool per_row = block == K && N > 1;
+  if (!(block == K || block == 0 || block == N * K))
+    return fail(NTLB_EUNSUPPORTED, "%s: scales must be per weight row (block = K) or per tensor (0 or N*K)", fn);
+  if (K % 4) return fail(NTLB_EUNSUPPORTED, "%s: K must be a multiple of 4", fn);
+  const int kstep = el == EL_BF16 ? 64 : 32, eb = el == EL_BF16 ? 2 : 4;
+  const int64_t Kc = (K + kstep - 1) / kstep * kstep;  // the contraction, zero past K
+  if (ldx < Kc || !aligned(x, 16) || (ldx * eb) % 16)
+    return fail(NTLB_EINVAL, "%s: x needs ld >= K rounded up to %d (zero pad columns), 16-byte rows and alignment",
+                fn, kstep);
+  if ((M + 256) * ldx * eb >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: x exceeds 2 GiB", fn);
+  const int64_t ldw = fmt == NTLB_LOWBIT_NF4 ? K / 2 : K;  // bytes per weight row
+  if (!aligned(w, fmt == NTLB_LOWBIT_NF4 ? 2 : 4))
+    return fail(NTLB_EINVAL, "%s: W needs 2-byte (NF4) or 4-byte (FP8) alignment", fn);
+  if (N * ldw >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: W exceeds 2 GiB", fn);
+  DqArgs g{};
+  g.a = Operand{reinterpret_cast<const uint8_t*>(x), ldx, M, Kc, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.b = Operand{w, ldw, N, K, w_scales, per_row ? 1 : 0, 0, 0, 0,
+                fmt == NTLB_LOWBIT_NF4 ? GRID_NF4 : GRID_E4M3, 0, 0};
+  g.M = M; g.N = N; g.Kc = Kc;
+  g.bias = bias; g.bias_dtype = bias_dtype; g.y = y;
+  return finish(fn, g, el, SRC_DIRECT, SRC_PCODES, y_dtype, ldy, stream, workspace, ws_bytes);
 }
 
 extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,

@@ -17,6 +17,11 @@ enum Rounding : int { ROUND_NEAREST = 0, ROUND_STOCHASTIC = 1 };
 enum ScaleRule : int { SCALE_AFTER_DIVIDE = 0, SCALE_BEFORE_DIVIDE = 1 };
 enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 
+// the 16 NF4 code values of src/layers.py:60-83, as fp32
+#define NTLB_NF4_CODEBOOK                                                                                          \
+  {-1.0f,       -0.6961928f, -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f, -0.09105004f, 0.0f,         \
+   0.0795803f,  0.1609302f,  0.2461123f,   0.33791524f, 0.44070983f,  0.562617f,    0.72295684f,  1.0f}
+
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) { return __uint_as_float(b16 << 16); }
 
 // 8 bytes (two words) stored with the non-temporal hint

@@ -27,10 +27,7 @@
 
 namespace ntlb {
 
-// layers.py:60-83, as fp32
-#define NTLB_NF4_CODEBOOK                                                                                          \
-  {-1.0f,       -0.6961928f, -0.52507305f, -0.3949175f, -0.28444138f, -0.18477343f, -0.09105004f, 0.0f,         \
-   0.0795803f,  0.1609302f,  0.2461123f,   0.33791524f, 0.44070983f,  0.562617f,    0.72295684f,  1.0f}
+// the NF4 codebook (NTLB_NF4_CODEBOOK, ntlb_device.h)
 __constant__ float kNF4[16] = NTLB_NF4_CODEBOOK;
 // the same values as compile-time constants (folded into immediates)
 constexpr float kNF4c[16] = NTLB_NF4_CODEBOOK;

@@ -74,6 +74,10 @@ SIGNATURES = {
     "ntlb_gemm_fp8p": [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_gemm_lowbit_workspace_bytes": [_I64, _I64, _I64],
     "ntlb_gemm_lowbit_ws": [_I32, _P, _I64, _P, _P, _I64, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P, _I64, _P],
+    "ntlb_gemm_lowbit_dq_forward_ws": [_I32, _I32, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, _I32, _P, _I32,
+                                       _I64, _P, _I64, _P],
+    "ntlb_gemm_lowbit_dgrad_ws": [_I32, _I32, _P, _I64, _I64, _I64, _P, _P, _I64, _I64, _P, _I32, _I64, _P, _I64,
+                                  _P],
     "ntlb_gemm_workspace_bytes": [_I64, _I64, _I64],
     "ntlb_gemm_dq_forward": [_I32, _I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _I64,
                              _I64, _P, _I32, _P, _I32, _I64, _P],

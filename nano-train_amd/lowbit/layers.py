@@ -10,10 +10,11 @@ and tolerance of legacy checkpoints that lack the persistent buffers.
 
 Persistent NF4/FP8 weights are refreshed and dequantized by the HIP kernels of
 lowbit.persistent.  When a module stores NF4 or FP8 weights, has no low-bit
-compute backend, and both activation and master weight are bf16, the forward
-runs the dequant-fused GEMM instead of materializing the bf16 weight; its
-backward is the reference's straight-through rule (dX = dY . W_deq,
-dW = dY^T . X).
+compute backend, and activation and master weight share a dtype (bf16 or
+fp32), the forward decodes the weight inside the GEMM instead of
+materializing it; its
+backward is the reference's straight-through rule (dX = dY . W_deq with the
+weight decoded inside the GEMM, dW = dY^T . X).
 
 One GPU: the tensor-parallel classes accept tp_size == 1 only.
 """
@@ -38,8 +39,9 @@ class _FusedPersistentLinear(torch.autograd.Function):
     """Forward: dequant-fused GEMM over the persistent NF4 or FP8 weight, with
     the bias added in fp32 before the output rounding (F.linear(x, w_q, b),
     layers.py:595-632).  Backward: straight-through to the master weight
-    (layers.py:409-436) on the library's bf16 GEMMs: dX = dY . w_q with w_q
-    dequantized by its kernel, dW = dY^T . X, db = the column sum of dY."""
+    (layers.py:409-436) on the library's GEMMs: dX = dY . w_q with w_q decoded
+    inside the GEMM (no dequantized copy), dW = dY^T . X, db = the column sum
+    of dY."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, codes, scale, block, fmt):
@@ -61,12 +63,9 @@ class _FusedPersistentLinear(torch.autograd.Function):
         if dy2.stride(-1) != 1:
             dy2 = dy2.contiguous()
         if ctx.needs_input_grad[0]:
-            if fmt == "nf4":
-                w_deq = P.dequantize_nf4_blocks(codes, scale, num_values=N * K, block=block,
-                                                target_dtype=dy2.dtype).reshape(N, K)
-            else:
-                w_deq = P.dequantize_fp8_persistent(codes, scale, target_dtype=dy2.dtype).reshape(N, K)
-            dx = ops.gemm_dense(dy2, w_deq, b_transposed=True, out_dtype=x.dtype).reshape(x.shape)
+            # the weight is decoded inside the GEMM: no dequantized copy of W
+            dx = P.dgrad(dy2, codes, scale, fmt=fmt, out_features=N, in_features=K,
+                         out_dtype=x.dtype).reshape(x.shape)
         if ctx.needs_input_grad[1]:
             dw = ops.gemm_dense_tn(dy2, x.reshape(-1, K).to(dy2.dtype), out_dtype=wdt)
         if ctx.needs_input_grad[2]:
@@ -219,13 +218,16 @@ class LowBitLinearMixin:
         return self.weight + (deq - self.weight).detach()
 
     def _fused_persistent_forward(self, x: torch.Tensor, bias: Optional[torch.Tensor]) -> Optional[torch.Tensor]:
-        """NF4 or FP8 persistent weight, no low-bit backend, bf16 everywhere:
-        dequant inside the GEMM instead of materializing the bf16 weight."""
+        """NF4 or FP8 persistent weight, no low-bit backend, activation, weight
+        and bias of one dtype, bf16 or fp32, K % 4 == 0: the weight is decoded
+        inside the GEMM (the dequant-fused kernel for bf16 with K % 64 == 0,
+        else the dequantized-operand GEMM) instead of materialized."""
         mode = self._persistent_mode()
+        dt = self.weight.dtype
         if (mode not in ("fp4", "fp8") or self._compute_lowbit_mode() is not None
-                or self._compute_dtype_override() is not None or x.dtype != torch.bfloat16
-                or self.weight.dtype != torch.bfloat16 or x.device.type != "cuda" or self.weight.dim() != 2
-                or self.weight.shape[1] % 64 or (bias is not None and bias.dtype != torch.bfloat16)):
+                or self._compute_dtype_override() is not None or dt not in (torch.bfloat16, torch.float32)
+                or x.dtype != dt or x.device.type != "cuda" or self.weight.dim() != 2
+                or self.weight.shape[1] % 4 or (bias is not None and bias.dtype != dt)):
             return None
         N, K = self.weight.shape
         if mode == "fp4":

@@ -170,16 +170,52 @@ def _fused(fmt: int, x2: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bl
     return y
 
 
+def _dq_forward(fmt: int, x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, block: int, bias, N: int, K: int,
+                out_dtype) -> torch.Tensor:
+    """ntlb_gemm_lowbit_dq_forward_ws: the weight decoded into the dequantized-
+    operand GEMM (bf16 or fp32 activations, K % 4 == 0, one scale per row or
+    one for all)."""
+    ops._require_device(x, w, scales, bias)
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("the persistent-weight GEMM takes bf16 or fp32 activations")
+    x2 = ops._pad_cols(x.reshape(-1, K), 64 if x.dtype == torch.bfloat16 else 32)
+    M = x2.shape[0]
+    if bias is not None:
+        if bias.numel() != N:
+            raise ValueError(f"bias must have {N} entries, got {bias.numel()}")
+        bias = bias.reshape(-1).contiguous()
+    y = torch.empty((M, N), dtype=out_dtype or x.dtype, device=x.device)
+    op = _lib.BF16 if x.dtype == torch.bfloat16 else _lib.F32
+    ws = ops.split_workspace(int(_lib.lib().ntlb_gemm_dq_workspace_bytes(op, M, N, K)), x.device)
+    call("ntlb_gemm_lowbit_dq_forward_ws", fmt, op, x2.data_ptr(), x2.stride(0), M, w.data_ptr(), scales.data_ptr(),
+         block, N, K, ops._ptr(bias), ops._dtype_code(bias.dtype) if bias is not None else 0, y.data_ptr(),
+         ops._dtype_code(y.dtype), y.stride(0), ops._ptr(ws), ws.numel() if ws is not None else 0, ops._stream())
+    return y
+
+
+def _fused_kernel_fits(x: torch.Tensor, K: int) -> bool:
+    """the dequant-fused kernel: bf16 activations and K % 64 == 0; otherwise the
+    dequantized-operand GEMM decodes the weight (fp32 activations, ragged K)"""
+    return x.dtype == torch.bfloat16 and K % 64 == 0
+
+
 def linear_nf4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, out_features: int, block: int,
                bias: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """Y = x @ deq(W)^T (+ bias) with W [out_features, K] in NF4, dequantized inside the GEMM.
 
-    block: elements per scale (K for per_channel, 0 or numel for per_tensor, 64...)."""
+    block: elements per scale (K for per_channel, 0 or numel for per_tensor, 64...).  bf16 x with
+    K % 64 == 0 runs the dequant-fused kernel; fp32 x, or K % 64 != 0 (K % 4 == 0), the
+    dequantized-operand GEMM, which takes per-row or per-tensor scales."""
     K = x.shape[-1]
-    x2 = _x2(x, K)
-    M, N = x2.shape[0], out_features
+    N = out_features
     blk = 0 if block >= N * K else block
-    y = _fused(_LOWBIT_NF4, x2, packed, scales.reshape(-1).contiguous(), blk, bias, M, N, K, out_dtype)
+    sc = scales.reshape(-1).contiguous()
+    if not _fused_kernel_fits(x, K):
+        y = _dq_forward(_LOWBIT_NF4, x, packed, sc.float(), blk, bias, N, K, out_dtype)
+        return y.reshape(*x.shape[:-1], N)
+    x2 = _x2(x, K)
+    M = x2.shape[0]
+    y = _fused(_LOWBIT_NF4, x2, packed, sc, blk, bias, M, N, K, out_dtype)
     return y.reshape(*x.shape[:-1], N)
 
 
@@ -191,15 +227,48 @@ def linear_fp8p(x: torch.Tensor, fp8_values: torch.Tensor, scale: torch.Tensor, 
     (layers.py:120-127)."""
     ops._require_device(fp8_values, scale)
     N, K = fp8_values.shape
-    x2 = _x2(x, K)
-    M = x2.shape[0]
     codes = fp8_values.contiguous().view(torch.uint8)
     sc = scale.reshape(-1).contiguous().float()
     block = 0 if sc.numel() <= 1 else K
     if block and sc.numel() != N:
         raise ValueError(f"scale must be per_tensor or one per row, got {tuple(scale.shape)}")
+    if not _fused_kernel_fits(x, K):
+        y = _dq_forward(_LOWBIT_FP8P, x, codes, sc, block, bias, N, K, out_dtype)
+        return y.reshape(*x.shape[:-1], N)
+    x2 = _x2(x, K)
+    M = x2.shape[0]
     y = _fused(_LOWBIT_FP8P, x2, codes, sc, block, bias, M, N, K, out_dtype)
     return y.reshape(*x.shape[:-1], N)
+
+
+def dgrad(dy: torch.Tensor, codes: torch.Tensor, scale: torch.Tensor, *, fmt: str, out_features: int,
+          in_features: int, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """dX [M, K] = dY [M, N] @ deq(W) for a persistent weight W [N, K], decoded
+    inside the GEMM (ntlb_gemm_lowbit_dgrad_ws): the straight-through input
+    gradient of the persistent layers (layers.py:409-436), with no dequantized
+    copy of W.  fmt "nf4" (packed nibbles, per_channel [N, 1] or per_tensor
+    scale) or "fp8" (float8_e4m3fn values [N, K]).  dY bf16 multiplies the
+    bf16-rounded weight values on bf16 MFMA, dY fp32 the fp32 values."""
+    ops._require_device(dy, codes, scale)
+    N, K = out_features, in_features
+    if dy.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("dgrad takes a bf16 or fp32 dY")
+    dy2 = dy.reshape(-1, N)
+    M = dy2.shape[0]
+    dy2 = ops._pad_cols(dy2, 64 if dy.dtype == torch.bfloat16 else 32)
+    sc = scale.reshape(-1).float().contiguous()
+    if sc.numel() not in (1, N):
+        raise ValueError(f"scale must be per_tensor or one per row, got {tuple(scale.shape)}")
+    block = K if sc.numel() == N and N > 1 else 0
+    w = codes.contiguous().view(torch.uint8)
+    f = _LOWBIT_NF4 if fmt == "nf4" else _LOWBIT_FP8P
+    dx = torch.empty((M, K), dtype=out_dtype or dy.dtype, device=dy.device)
+    op = _lib.BF16 if dy.dtype == torch.bfloat16 else _lib.F32
+    ws = ops.split_workspace(int(_lib.lib().ntlb_gemm_dq_workspace_bytes(op, M, K, N)), dy.device)
+    call("ntlb_gemm_lowbit_dgrad_ws", f, op, dy2.data_ptr(), dy2.stride(0), M, N, w.data_ptr(), sc.data_ptr(), block,
+         K, dx.data_ptr(), ops._dtype_code(dx.dtype), dx.stride(0), ops._ptr(ws), ws.numel() if ws is not None else 0,
+         ops._stream())
+    return dx.reshape(*dy.shape[:-1], K)
 
 
 def linear_mxfp4(x: torch.Tensor, packed: torch.Tensor, scales: torch.Tensor, *, out_features: int,

@@ -181,6 +181,34 @@ def test_ste_dgrad_wgrad_match_oracle(gpu_device, fmt, M, N, K):
     assert e1 <= 1e-3 and e2 <= 1e-3, (e1, e2)
 
 
+@pytest.mark.parametrize("fmt", list(GRIDS))
+@pytest.mark.parametrize("which", ["dgrad", "wgrad"])
+def test_per_row_scales_past_the_last_contraction_row_add_nothing(gpu_device, fmt, which):
+    """An operand with per-row 1x128 scales (X in wgrad, a 1x128-scaled W in
+    dgrad) is contracted over its 97 rows in steps of 64: the scale slots of
+    rows 97-127 are the tile-major array's padding (set to NaN here) and the
+    first rows of the next 128-column block, whose row 0 is given a NaN
+    scale here.  Their codes are zero and they must add nothing: NaN comes
+    out in that tile's 128 columns and nowhere else."""
+    ops = _ops()
+    R, C, K = 97, 256, 384
+    t = seeded((R, K), seed=20262045, outliers=0.01).to(gpu_device)
+    q = ops.quant_tile_1x128(t, fmt=fmt)
+    q.scales[:, R:] = float("nan")  # the padding slots of every 128-column block
+    q.scales[1, 0] = float("nan")  # row 0's tile of columns 128-255: all its values NaN
+    other = seeded((R, C), seed=20262046, std=1e-3).to(gpu_device)
+    # dgrad: dX = other^T . bf16(dq(t)); wgrad: dW = other^T . bf16(dq(t)); the same product
+    out = ops.ste_dgrad(other.t().contiguous(), q, out_dtype=torch.bfloat16) if which == "dgrad" else \
+        ops.ste_wgrad(other, q, out_dtype=torch.bfloat16)
+    out = out.float().cpu()
+    nan_cols = torch.isnan(out).any(0)
+    assert nan_cols[128:256].all() and not nan_cols[:128].any() and not nan_cols[256:].any()
+    td = O.round_bf16(O.quant_tile_1x128(to_np32(t), grid=GRIDS[fmt])[3]).astype(np.float64)
+    ref = to_np32(other).astype(np.float64).T @ td
+    keep = np.r_[0:128, 256:K]
+    assert rel_fro_bf16(out[:, keep], ref[:, keep]) <= 1e-3
+
+
 @pytest.mark.parametrize("gran", ["tensor", "channel"])
 def test_ste_dgrad_wgrad_tensor_and_channel_scales(gpu_device, gran):
     """Weight scales per tensor or per output row, activation scales per

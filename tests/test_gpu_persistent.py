@@ -439,3 +439,173 @@ def test_dequant_vector_path_matches_elementwise_and_oracle(gpu_device, fmt, blo
     assert torch.equal(torch.isnan(outs[0]), nan)
     assert torch.equal(outs[0][~nan].view(bits), want_t[~nan].view(bits))
     assert fmt == "nf4" or nan.any()
+
+
+def _nf4_all_codes(N: int, K: int, rng) -> np.ndarray:
+    """packed nibbles of an [N, K] weight whose rows hold every NF4 code"""
+    idx = np.stack([rng.permutation(np.tile(np.arange(16), K // 16)) for _ in range(N)]).astype(np.uint8)
+    flat = idx.reshape(-1)
+    return (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "fp8"])
+@pytest.mark.parametrize("per_tensor", [False, True])
+@pytest.mark.parametrize("op_dtype", [torch.bfloat16, torch.float32])
+def test_lowbit_dgrad_decodes_every_code_exactly(gpu_device, fmt, per_tensor, op_dtype):
+    """dY = I makes dX = deq(W): every NF4 code (or every finite e4m3 code)
+    times its row or tensor scale, over scales spanning many binades, bit for
+    bit against the oracle's dequantization, rounded to bf16 for bf16 dY and
+    exact for fp32 dY (_dequantize_*_persistent with the layer's dtype)."""
+    from lowbit import persistent as P
+
+    N, K = 192, 256
+    rng = np.random.default_rng(20262601)
+    scales = np.exp(rng.uniform(np.log(1e-30), np.log(1e30), 1 if per_tensor else N)).astype(np.float32)
+    if fmt == "nf4":
+        codes = _nf4_all_codes(N, K, rng)
+        want = O.nf4_dequant(codes, scales, N * K, N * K if per_tensor else K).reshape(N, K)
+    else:
+        c = ((np.arange(N)[:, None] + np.arange(K)[None, :]) % 256).astype(np.uint8)
+        c[(c & 0x7F) == 0x7F] = 0  # the NaN codes
+        codes = c
+        vals = torch.from_numpy(c).view(torch.float8_e4m3fn).float().numpy()
+        want = (vals * (scales[0] if per_tensor else scales[:, None])).astype(np.float32)
+    if op_dtype == torch.bfloat16:
+        want = O.round_bf16(want)
+    dy = torch.eye(N, dtype=op_dtype, device=gpu_device)
+    sc = torch.from_numpy(scales).to(gpu_device).reshape(-1, 1)
+    dx = P.dgrad(dy, torch.from_numpy(codes).to(gpu_device), sc, fmt=fmt, out_features=N, in_features=K,
+                 out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(dx.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "fp8"])
+@pytest.mark.parametrize("op_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K,per_tensor", [(300, 200, 388, False), (64, 129, 256, True), (1000, 640, 1152, False),
+                                              (7, 64, 4, False)])
+def test_lowbit_dgrad_matches_oracle(gpu_device, fmt, op_dtype, M, N, K, per_tensor):
+    """dX = dY @ deq(W) over the persistent quantizer's own codes, against
+    float64 over the oracle's dequantized weight (rounded to bf16 for a bf16
+    layer): ragged N (the contraction) and K (not a multiple of 64)."""
+    from lowbit import persistent as P
+
+    gran = "per_tensor" if per_tensor else "per_channel"
+    w = seeded((N, K), seed=20262611 + K, std=0.05, outliers=0.01).to(gpu_device, op_dtype)
+    dy = seeded((M, N), seed=20262612 + M, std=1e-2).to(gpu_device, op_dtype)
+    if fmt == "nf4":
+        codes, scale = P.quantize_nf4_persistent(w, granularity=gran)
+        wd = O.nf4_dequant(codes.cpu().numpy(), scale.cpu().numpy().reshape(-1), N * K,
+                           N * K if per_tensor else K).reshape(N, K)
+    else:
+        codes, scale = P.quantize_fp8_persistent(w, granularity=gran)
+        wd = codes.float().cpu().numpy() * scale.float().cpu().numpy().reshape(-1, 1 if not per_tensor else 1)
+        wd = wd.astype(np.float32)
+    if op_dtype == torch.bfloat16:
+        wd = O.round_bf16(wd)
+    dx = P.dgrad(dy, codes, scale, fmt=fmt, out_features=N, in_features=K, out_dtype=torch.float32)
+    ref = to_np32(dy).astype(np.float64) @ wd.astype(np.float64)
+    err = O.rel_frobenius(dx.cpu().numpy(), ref)
+    assert err <= (1e-5 if op_dtype == torch.bfloat16 else 1e-5), err
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "fp8"])
+def test_lowbit_dgrad_split_tail_matches_unsplit(gpu_device, fmt):
+    """272 tiles leave 16 past the last whole wave: with the workspace they
+    run as K ranges whose fp32 partials are summed in range order; the result
+    equals the unsplit call's within fp32 reassociation, and repeats are
+    bit-identical (the workspace resets itself)."""
+    from lowbit import _lib, ops, persistent as P
+
+    M, N, K = 4352, 2304, 4096
+    w = seeded((N, K), seed=20262621, std=0.05).to(gpu_device)
+    dy = seeded((M, N), seed=20262622, std=1e-2).to(gpu_device)
+    if fmt == "nf4":
+        codes, scale = P.quantize_nf4_persistent(w, granularity="per_channel")
+    else:
+        codes, scale = P.quantize_fp8_persistent(w, granularity="per_channel")
+    assert int(_lib.lib().ntlb_gemm_dq_workspace_bytes(_lib.BF16, M, K, N)) > 0
+    split1 = P.dgrad(dy, codes, scale, fmt=fmt, out_features=N, in_features=K, out_dtype=torch.float32)
+    split2 = P.dgrad(dy, codes, scale, fmt=fmt, out_features=N, in_features=K, out_dtype=torch.float32)
+    whole = torch.empty_like(split1)
+    sc = scale.reshape(-1).float().contiguous()
+    _lib.call("ntlb_gemm_lowbit_dgrad_ws", 0 if fmt == "nf4" else 2, _lib.BF16, dy.data_ptr(), dy.stride(0), M, N,
+              codes.contiguous().view(torch.uint8).data_ptr(), sc.data_ptr(), K, K, whole.data_ptr(), _lib.F32,
+              whole.stride(0), None, 0, ops._stream())
+    torch.cuda.synchronize()
+    assert torch.equal(split1, split2)
+    assert O.rel_frobenius(split1.cpu().numpy(), whole.cpu().numpy().astype(np.float64)) <= 1e-6
+
+
+def _persistent_oracle(fmt: str, codes: torch.Tensor, scale: torch.Tensor, N: int, K: int, per_tensor: bool):
+    """fp32 values of a persistent weight from its codes (the oracle's NF4
+    dequantization, or e4m3 value times scale)"""
+    if fmt == "nf4":
+        return O.nf4_dequant(codes.cpu().numpy(), scale.float().cpu().numpy().reshape(-1), N * K,
+                             N * K if per_tensor else K).reshape(N, K)
+    vals = codes.cpu().view(torch.float8_e4m3fn).float().numpy() if codes.dtype == torch.uint8 else \
+        codes.float().cpu().numpy()
+    return (vals * scale.float().cpu().numpy().reshape(-1, 1)).astype(np.float32)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("M,N,K,per_tensor", [(300, 200, 388, False), (64, 129, 256, True), (5, 64, 100, False),
+                                              (1000, 640, 1152, False)])
+def test_persistent_forward_fp32_and_ragged_k_match_oracle(gpu_device, fmt, dtype, M, N, K, per_tensor):
+    """Y = x @ deq(W)^T + b through linear_nf4 / linear_fp8p where the fused
+    kernel does not apply (fp32 activations, or K not a multiple of 64): the
+    dequantized-operand GEMM decodes the codes (masked past K), against
+    float64 over the oracle's values (bf16-rounded for a bf16 layer)."""
+    from lowbit import persistent as P
+
+    gran = "per_tensor" if per_tensor else "per_channel"
+    w = seeded((N, K), seed=20262631 + K, std=0.05, outliers=0.01).to(gpu_device, dtype)
+    x = seeded((M, K), seed=20262632 + M).to(gpu_device, dtype)
+    b = seeded((N,), seed=20262633, std=0.5).to(gpu_device, dtype)
+    if fmt == "nf4":
+        codes, scale = P.quantize_nf4_persistent(w, granularity=gran)
+        y = P.linear_nf4(x, codes, scale, out_features=N, block=N * K if per_tensor else K, bias=b,
+                         out_dtype=torch.float32)
+    else:
+        codes, scale = P.quantize_fp8_persistent(w, granularity=gran)
+        y = P.linear_fp8p(x, codes, scale, bias=b, out_dtype=torch.float32)
+    wd = _persistent_oracle(fmt, codes, scale, N, K, per_tensor)
+    if dtype == torch.bfloat16:
+        wd = O.round_bf16(wd)
+    ref = O.gemm_ref(to_np32(x), wd, to_np32(b))
+    err = O.rel_frobenius(y.cpu().numpy(), ref)
+    assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "fp8"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_persistent_forward_ragged_k_decodes_every_code_exactly(gpu_device, fmt, dtype):
+    """x = I with K = 100 returns deq(W)^T exactly: every NF4 code (or every
+    finite e4m3 code) times its row scale, with the codes of the next row
+    (which follow each row's 100 in memory) masked out of the contraction."""
+    from lowbit import persistent as P
+
+    N, K = 80, 100
+    rng = np.random.default_rng(20262641)
+    scales = np.exp(rng.uniform(np.log(1e-20), np.log(1e20), N)).astype(np.float32)
+    if fmt == "nf4":
+        idx = np.stack([np.resize(rng.permutation(16), K) for _ in range(N)]).astype(np.uint8)
+        flat = idx.reshape(-1)
+        codes = torch.from_numpy((flat[0::2] | (flat[1::2] << 4)).astype(np.uint8))
+    else:
+        c = ((np.arange(N)[:, None] * 7 + np.arange(K)[None, :]) % 256).astype(np.uint8)
+        c[(c & 0x7F) == 0x7F] = 0
+        codes = torch.from_numpy(c).view(torch.float8_e4m3fn)
+    sc = torch.from_numpy(scales).reshape(N, 1)
+    want = _persistent_oracle(fmt, codes if fmt == "nf4" else codes.view(torch.uint8), sc, N, K, False)
+    if dtype == torch.bfloat16:
+        want = O.round_bf16(want)
+    x = torch.eye(K, dtype=dtype, device=gpu_device)
+    if fmt == "nf4":
+        y = P.linear_nf4(x, codes.to(gpu_device), sc.to(gpu_device), out_features=N, block=K,
+                         out_dtype=torch.float32)
+    else:
+        y = P.linear_fp8p(x, codes.to(gpu_device), sc.to(gpu_device), out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy().T, want)
