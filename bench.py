@@ -448,8 +448,13 @@ def _c3_ste(args, res: dict, x, w, dy, st) -> dict:
     dg = _time_ms(lambda i: ops.ste_dgrad(dy, qw, out_dtype=bf), args.steps, args.warmup, st)
     wg = _time_ms(lambda i: ops.ste_wgrad(dy, qx, out_dtype=bf), args.steps, args.warmup, st)
     db = _time_ms(lambda i: ops.colsum(dy, out_dtype=bf), args.steps, args.warmup, st)
+    # e4m3: the wgrad kernel that also forms db from its staged dY tiles (what
+    # the layer step runs); its extra time against the plain wgrad
+    wg_db = None
+    if fmt == "e4m3":
+        wg_db = _time_ms(lambda i: ops.ste_wgrad(dy, qx, out_dtype=bf, db_dtype=bf), args.steps, args.warmup, st)
     # the whole layer step through the backend's autograd function: both
-    # quantizers, the forward GEMM, dgrad, wgrad and db
+    # quantizers, the forward GEMM, dgrad, wgrad and db (e4m3: db inside the wgrad)
     spec = LowBitKernelSpec("linear", K, N, True, "tile_1x128", "block_128x128", "nearest")
     be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format=fmt, seed=7)
     xg = x.detach().clone().requires_grad_(True)
@@ -493,6 +498,8 @@ def _c3_ste(args, res: dict, x, w, dy, st) -> dict:
                          "min_hbm_bytes": M * N * 2 + N * K + M * K * 2, "avg_ms": round(dg, 4)},
                dgrad_tflops=tf(dg), wgrad_tflops=tf(wg), wgrad_frac_bf16_peak=round(tf(wg) / 2500.0, 4),
                db_colsum_us=round(db * 1e3, 2), db_colsum_GBs=round(M * N * 2 / (db * 1e-3) / 1e9, 1),
+               wgrad_with_db_us=None if wg_db is None else round(wg_db * 1e3, 2),
+               db_in_wgrad_extra_us=None if wg_db is None else round((wg_db - wg) * 1e3, 2),
                layer_forward_backward_ms=round(layer_ms, 4), layer_forward_ms=round(fwd_ms, 4),
                hipblaslt_on_dequantized_bf16=lib)
     return res

@@ -25,8 +25,12 @@
  *   rounding: NTLB_ROUND_NEAREST (torch.round, half to even) or
  *             NTLB_ROUND_STOCHASTIC: element e uses r = word e%4 of
  *             Philox4x32-10(counter {lo(e/4), hi(e/4), lo(offset), hi(offset)},
- *             key {lo(seed), hi(seed)}), u = (r >> 8) * 2^-24, and rounds
- *             floor(v+u) for v >= 0, ceil(v-u) for v < 0 (te_backend.py:61-65).
+ *             key {lo(seed), hi(seed)}).  Int grid: u = (r >> 8) * 2^-24,
+ *             and v rounds to floor(v+u) for v >= 0, ceil(v-u) for v < 0
+ *             (te_backend.py:61-65).  e4m3: |v| rounds away from zero exactly
+ *             when f + (r >> 12) >= 2^20, f being the 20 bits of |v|'s
+ *             significand below the e4m3 spacing (for subnormal results, of
+ *             |v| * 512 below its integer part): gfx950's v_cvt_sr_fp8_f32.
  *             e is the row-major index of the element in the source matrix.
  *   codes   : uint8 [rows, ldc], ldc >= ceil(K/128)*128 where tiles pad K;
  *             padding columns are written as 0.
@@ -324,6 +328,18 @@ int64_t ntlb_gemm_dq_workspace_bytes(int op_dtype, int64_t M, int64_t N, int64_t
 int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid, const uint8_t* x,
                         int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col, int x_shift, int64_t K, void* dw,
                         int dw_dtype, int64_t lddw, void* stream);
+
+/* The same weight gradient, also writing the bias gradient db[N] = the sum
+ * of dY over its M rows (F.linear's bias gradient under autograd of
+ * te_backend.py:253-259), accumulated in fp32 from the dY tiles the kernel
+ * stages anyway (no separate pass over dY) and stored in db_dtype; db NULL
+ * skips it.  The sum runs in a fixed order (each 8-row group of a 64-row
+ * step, the steps in order, then the eight waves' partials in order), so
+ * repeated calls are bit-identical.  e4m3 codes only (grid NTLB_GRID_E4M3;
+ * the int grid's decode leaves no registers for it: NTLB_EUNSUPPORTED). */
+int ntlb_gemm_ste_wgrad_db(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
+                           const uint8_t* x, int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col, int x_shift,
+                           int64_t K, void* dw, int dw_dtype, int64_t lddw, void* db, int db_dtype, void* stream);
 
 /* The straight-through dgrad of every expert's Linear at once (the input
  * gradient of te_backend.py:250-259 for each expert of the single-rank loop,

@@ -181,6 +181,11 @@ struct DqArgs {
   // add the bf16 output to what y holds: y = bf16(y + bf16(acc)), the sum of
   // two Linears' input gradients as autograd forms it
   int accum;
+  // TDIRECT A (the wgrad's dY^T), ungrouped: the workgroups of the first
+  // output column tile also store db[r] = the sum of A's row r over the
+  // contraction (the column sums of dY: the bias gradient), in db_dtype
+  void* db;
+  int db_dtype;
 };
 
 constexpr int GRP_NONE = 0, GRP_ROWS = 1, GRP_K = 2;
@@ -352,6 +357,19 @@ struct Stager<SRC_TDIRECT, EL, GRID, SCM> {
       *reinterpret_cast<uint4*>(tile + sw(4 * l + i, cw)) = out;
     }
   }
+  // bf16: adds the staged block's CPW contraction values of operand row
+  // 4l + i to s[i] (an LDS slot), in row order, one row at a time
+  __device__ void colsum(float* s) {
+    if constexpr (EL == EL_BF16) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float t = s[i];
+#pragma unroll
+        for (int j = 0; j < CPW; ++j) t += bf16_bits_to_f32((w[j][i >> 1] >> (16 * (i & 1))) & 0xFFFFu);
+        s[i] = t;
+      }
+    }
+  }
 };
 
 // TCODES: as TDIRECT, with one code byte per element (one 4-byte load per
@@ -389,15 +407,18 @@ struct Stager<SRC_TCODES, EL, GRID, SCM> {
     } else {
       // rows past kvalid hold zero codes, but the scale slots there are the
       // array's padding or the next rows' scales, which can be NaN or inf:
-      // their scales are taken as zero so that 0 * scale adds nothing
+      // their scales are taken as zero so that 0 * scale adds nothing (cbase
+      // is uniform over the wave, so only the last step's waves select)
 #pragma unroll
       for (int k = 0; k < CPW / 4; ++k) {
         const uint4 v = __builtin_bit_cast(
             uint4, __builtin_amdgcn_raw_buffer_load_b128(rss, (int)((soff + (uint32_t)cbase + 4 * k) * 4), 0, 0));
-        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+        sc[4 * k] = __uint_as_float(v.x); sc[4 * k + 1] = __uint_as_float(v.y);
+        sc[4 * k + 2] = __uint_as_float(v.z); sc[4 * k + 3] = __uint_as_float(v.w);
+      }
+      if ((int64_t)(cbase + CPW) > o.kvalid) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          sc[4 * k + i] = (int64_t)(cbase + 4 * k + i) < o.kvalid ? __uint_as_float(vv[i]) : 0.f;
+        for (int j = 0; j < CPW; ++j) sc[j] = (int64_t)(cbase + j) < o.kvalid ? sc[j] : 0.f;
       }
     }
   }
@@ -587,7 +608,7 @@ struct Direct {
   }
 };
 
-template <int EL, int SA, int SB, int GRID, int SCM, int GRP = GRP_NONE, bool IL = false>
+template <int EL, int SA, int SB, int GRID, int SCM, int GRP = GRP_NONE, bool IL = false, bool DB = false>
 __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t la0[TILE];
   __shared__ __attribute__((aligned(16))) uint8_t lb0[TILE];
@@ -709,6 +730,31 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     sb.cb = nf4_tab;
   }
 
+  // the bias gradient rides on the wgrad's dY stream: the tiles of the first
+  // output column tile sum their A rows over the contraction (each staged
+  // block once, in block order; the waves' sums added in wave order)
+  const bool do_db = DB && n0 == 0;
+  static_assert(!DB || (SA == SRC_TDIRECT && EL == EL_BF16 && GRP == GRP_NONE), "db rides on a bf16 dY^T stream");
+  // each thread's running sums of its four operand rows live in LDS slots it
+  // alone touches (registers here made the int-grid variants spill)
+  // (the slot address is recomputed where it is used, from the scalar wave
+  // index and the lane id, so that no register holds it through the loop)
+  __shared__ float db_part[DB ? 8 * 256 : 1];
+  auto db_slot = [&]() -> float* {
+    const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    return db_part + wave * 256 + 4 * ln;
+  };
+  if constexpr (DB) {
+    if (do_db) {
+      float* d = db_slot();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = 0.f;
+    }
+  }
+  auto db_add = [&]() {
+    if constexpr (DB) sa.colsum(db_slot());
+  };
+
   // logical K step -> the step the loaders read (IL: one half of the
   // interleaved gate / up contraction)
   const int il_half = g.il_half;
@@ -743,6 +789,9 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   sb.template decode_half<0>(g.b, lb0);
   sa.template decode_half<1>(g.a, la0);
   sb.template decode_half<1>(g.b, lb0);
+  if constexpr (DB) {
+    if (do_db) db_add();
+  }
   sa.load(g.a, kmap(min(kb0 + 1, kb1 - 1)));
   sb.load(g.b, kmap(min(kb0 + 1, kb1 - 1)));
   __builtin_amdgcn_s_waitcnt(0);
@@ -783,6 +832,12 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
       asm volatile("" : "+v"(acc[tm][0]), "+v"(acc[tm][1]), "+v"(acc[tm][2]), "+v"(acc[tm][3])::"memory");
       if (tm + 1 < 8) af = af_next;
     }
+    // the staged block kt+1 still sits in the A stager's registers, and the
+    // fragments are dead: add it to the bias gradient (once: the last steps
+    // reload the last block)
+    if constexpr (DB) {
+      if (do_db && kt + 1 < kb1) db_add();
+    }
     // every copy of this step has landed (vmcnt(0)); then block kt+2's raw
     // data goes out and stays in flight across the barrier
     __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -799,6 +854,18 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   // a split range: the last one to arrive sums all of them in range order
   // and stores the tile
   if (sw.tail >= 0 && !split_exchange(acc, g.ws, g.ws_count, sw.tail, g.split_s, sw.chunk, tid)) return;
+  if constexpr (DB) {
+    if (do_db) {  // uniform over the workgroup
+      __syncthreads();
+      const float* red = db_part;
+      if (tid < 256 && m0 + tid < g.M) {
+        float t = red[tid];
+#pragma unroll
+        for (int w8 = 1; w8 < 8; ++w8) t += red[w8 * 256 + tid];
+        store_elem(g.db, g.db_dtype, m0 + tid, t);
+      }
+    }
+  }
 
   // ---------------------------------------------------------------- epilogue
   int64_t m0e = uniform64(m0), n0e = uniform64(n0);
@@ -1011,6 +1078,14 @@ template <int EL, int SA, int SB, int GRID, int SCM = SC_SHARED>
 void launch(const DqArgs& g, hipStream_t st) {
   const int64_t tiles = ((g.M + TM - 1) / TM) * ((g.N + TN - 1) / TN);
   const int64_t wgs = g.split_s > 1 ? (int64_t)g.split_base + (tiles - g.split_base) * g.split_s : tiles;
+  // the db variant is built for e4m3 codes only: with the int grid's decode
+  // it needs a few registers more than a wave of this kernel has
+  if constexpr (SA == SRC_TDIRECT && SB == SRC_TCODES && EL == EL_BF16 && GRID == GRID_E4M3) {
+    if (g.db) {
+      gemm_dq_kernel<EL, SA, SB, GRID, SCM, GRP_NONE, false, true><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
+      return;
+    }
+  }
   gemm_dq_kernel<EL, SA, SB, GRID, SCM><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
 }
 
@@ -1292,9 +1367,10 @@ extern "C" int ntlb_gemm_lowbit_dq_forward_ws(int fmt, int op_dtype, const void*
   return finish(fn, g, el, SRC_DIRECT, SRC_PCODES, y_dtype, ldy, stream, workspace, ws_bytes);
 }
 
-extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
-                                   const uint8_t* x, int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col,
-                                   int x_shift, int64_t K, void* dw, int dw_dtype, int64_t lddw, void* stream) {
+extern "C" int ntlb_gemm_ste_wgrad_db(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
+                                      const uint8_t* x, int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col,
+                                      int x_shift, int64_t K, void* dw, int dw_dtype, int64_t lddw, void* db,
+                                      int db_dtype, void* stream) {
   const char* fn = "ntlb_gemm_ste_wgrad";
   int el;
   if (int rc = elem_of(op_dtype, fn, el)) return rc;
@@ -1317,7 +1393,17 @@ extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, i
   if (int rc = tcodes_scales(fn, g.b)) return rc;
   g.M = N; g.N = K; g.Kc = Mc;
   g.bias = nullptr; g.bias_dtype = 0; g.y = dw;
+  if (db && !valid_dtype(db_dtype)) return fail(NTLB_EINVAL, "%s: bad db dtype", fn);
+  if (db && grid != NTLB_GRID_E4M3) return fail(NTLB_EUNSUPPORTED, "%s: db rides on the e4m3 kernel only", fn);
+  g.db = db; g.db_dtype = db_dtype;
   return finish(fn, g, el, SRC_TDIRECT, SRC_TCODES, dw_dtype, lddw, stream);
+}
+
+extern "C" int ntlb_gemm_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int64_t M, int64_t N, int grid,
+                                   const uint8_t* x, int64_t ldx, const float* sx, int64_t sx_row, int64_t sx_col,
+                                   int x_shift, int64_t K, void* dw, int dw_dtype, int64_t lddw, void* stream) {
+  return ntlb_gemm_ste_wgrad_db(op_dtype, dy, lddy, M, N, grid, x, ldx, sx, sx_row, sx_col, x_shift, K, dw, dw_dtype,
+                                lddw, nullptr, 0, stream);
 }
 
 // offset table of rows sorted by expert, as the grouped kernels read it

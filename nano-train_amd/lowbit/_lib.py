@@ -86,6 +86,8 @@ SIGNATURES = {
                                _P, _I64, _P],
     "ntlb_gemm_dq_workspace_bytes": [_I32, _I64, _I64, _I64],
     "ntlb_gemm_ste_wgrad": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_ste_wgrad_db": [_I32, _P, _I64, _I64, _I64, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64, _P, _I32, _I64,
+                               _P, _I32, _P],
     "ntlb_gemm_dense": [_I32, _P, _I64, _I32, _P, _I64, _I32, _I64, _I64, _I64, _P, _I32, _P, _I32, _I64, _P],
     "ntlb_gemm_dense_tn": [_I32, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "ntlb_colsum": [_P, _I32, _I64, _I64, _I64, _P, _I64, _P, _I32, _P],

@@ -251,7 +251,11 @@ class _HipLowBitLinear(torch.autograd.Function):
                 dx = dx.reshape(ctx.x_shape)
             if ctx.needs_input_grad[1]:
                 if qx is not None and dy2.dtype == torch.bfloat16:
-                    dw = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype)
+                    if ctx.has_bias and ctx.needs_input_grad[2] and qx.grid == _lib.GRID_E4M3:
+                        # db from the dY tiles the wgrad kernel stages (no pass of its own)
+                        dw, db = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype, db_dtype=ctx.bias_dtype)
+                    else:
+                        dw = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype)
                 else:
                     xdq = xq if xq is not None else ops.dequant(qx, out_dtype=ctx.x_dtype)
                     op = _gemm_op_dtype(dy2.dtype, xdq.dtype)
@@ -263,7 +267,7 @@ class _HipLowBitLinear(torch.autograd.Function):
                 dx = dx.to(ctx.x_dtype).reshape(ctx.x_shape)
             if dw is not None:
                 dw = dw.to(ctx.w_dtype)
-        if ctx.has_bias and ctx.needs_input_grad[2]:
+        if ctx.has_bias and ctx.needs_input_grad[2] and db is None:
             db = ops.colsum(dy2, out_dtype=ctx.bias_dtype)
         return dx, dw, db, None
 

@@ -624,9 +624,11 @@ def ste_dgrad(dy: torch.Tensor, w: QTensor, *, out_dtype: torch.dtype) -> torch.
     return out
 
 
-def ste_wgrad(dy: torch.Tensor, x: QTensor, *, out_dtype: torch.dtype) -> torch.Tensor:
+def ste_wgrad(dy: torch.Tensor, x: QTensor, *, out_dtype: torch.dtype, db_dtype: Optional[torch.dtype] = None):
     """dW[N, K] = dY[M, N]^T @ bf16(dq(x))[M, K] (the straight-through weight
-    gradient), decoded from the forward's activation codes."""
+    gradient), decoded from the forward's activation codes.  With db_dtype,
+    returns (dW, db): db[N] = dY summed over its rows in fp32 (the bias
+    gradient), formed by the same kernel from the dY tiles it stages."""
     _require_device(dy, x.codes)
     if dy.dtype != torch.bfloat16:
         raise TypeError("ste_wgrad takes a bfloat16 dY")
@@ -636,10 +638,11 @@ def ste_wgrad(dy: torch.Tensor, x: QTensor, *, out_dtype: torch.dtype) -> torch.
     if dy.stride(-1) != 1 or dy.stride(0) % 8 or dy.data_ptr() % 16:
         dy = _pad_cols(dy, 8)
     out = torch.empty((N, x.K), dtype=out_dtype, device=dy.device)
-    call("ntlb_gemm_ste_wgrad", _lib.BF16, dy.data_ptr(), dy.stride(0), M, N, x.grid, x.codes.data_ptr(),
+    db = torch.empty((N,), dtype=db_dtype, device=dy.device) if db_dtype is not None else None
+    call("ntlb_gemm_ste_wgrad_db", _lib.BF16, dy.data_ptr(), dy.stride(0), M, N, x.grid, x.codes.data_ptr(),
          x.codes.stride(0), x.scales.data_ptr(), x.s_row, x.s_col, x.shift, x.K, out.data_ptr(),
-         _dtype_code(out_dtype), out.stride(0), _stream())
-    return out
+         _dtype_code(out_dtype), out.stride(0), _ptr(db), _dtype_code(db_dtype) if db is not None else 0, _stream())
+    return out if db is None else (out, db)
 
 
 def grouped_ste_dgrad(dy: torch.Tensor, offsets: torch.Tensor, w_codes: torch.Tensor, w_scales: torch.Tensor, *,

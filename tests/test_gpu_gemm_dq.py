@@ -367,3 +367,33 @@ def test_ste_dgrad_split_tail_matches_unsplit(gpu_device, fmt, wscale, K):
     # the tail tiles lie in row tiles 28-31 (the last group of the grouped
     # raster); every tile above them runs whole in both calls, bit for bit
     assert torch.equal(dx[:7168].view(torch.int32), ref[:7168].view(torch.int32))
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 200, 384), (1000, 640, 1152), (77, 129, 257), (4096, 2304, 512)])
+def test_ste_wgrad_with_db_matches_colsum(gpu_device, M, N, K):
+    """The e4m3 straight-through wgrad that also forms db from its staged dY
+    tiles: dW bit-identical to the wgrad without db, db within fp32
+    reassociation of float64's column sums of dY (and of the separate
+    column-sum pass), repeats bit-identical; the int grid refuses db."""
+    ops = _ops()
+    from lowbit._lib import LowBitKernelError
+
+    x = seeded((M, K), seed=20262651, outliers=0.01).to(gpu_device)
+    dy = seeded((M, N), seed=20262652, std=1e-2).to(gpu_device)
+    qx = ops.quant_tile_1x128(x, fmt="e4m3")
+    dw0 = ops.ste_wgrad(dy, qx, out_dtype=torch.bfloat16)
+    dw1, db1 = ops.ste_wgrad(dy, qx, out_dtype=torch.bfloat16, db_dtype=torch.float32)
+    dw2, db2 = ops.ste_wgrad(dy, qx, out_dtype=torch.bfloat16, db_dtype=torch.float32)
+    _, db16 = ops.ste_wgrad(dy, qx, out_dtype=torch.bfloat16, db_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(dw0.view(torch.int16), dw1.view(torch.int16))
+    assert torch.equal(db1, db2) and torch.equal(dw1.view(torch.int16), dw2.view(torch.int16))
+    ref = to_np32(dy).astype(np.float64).sum(0)
+    err = np.abs(db1.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= 1e-6, err
+    sep = ops.colsum(dy, out_dtype=torch.float32).cpu().numpy()
+    assert np.abs(db1.cpu().numpy() - sep).max() <= 1e-6 * np.abs(ref).max()
+    assert np.array_equal(bf16_bits(db16), O.to_bf16_bits(db1.cpu().numpy()))
+    qi = ops.quant_tile_1x128(x, fmt="int_grid")
+    with pytest.raises((LowBitKernelError, ValueError, RuntimeError)):
+        ops.ste_wgrad(dy, qi, out_dtype=torch.bfloat16, db_dtype=torch.float32)
