@@ -379,6 +379,33 @@ int ntlb_gemm_grouped_ste_wgrad(int op_dtype, const void* dy, int64_t lddy, int6
                                 const float* sx, int64_t sx_row, int64_t sx_col, int x_shift, int64_t K, void* dw,
                                 int dw_dtype, int64_t lddw, int64_t dw_estride, void* stream);
 
+/*
+ * The three grouped backward GEMMs of the expert loop over dense bf16
+ * operands instead of codes: under stochastic rounding the reference's
+ * straight-through operands t + (t_dq - t) (te_backend.py:250-251, formed by
+ * ntlb_ste_value) differ from bf16(q * s), so the expert loop's backward
+ * multiplies them directly, as each expert Linear's autograd does
+ * (moe.py:1062-1093).
+ *   ntlb_gemm_grouped_dgrad_dense: dX rows of expert e = dY rows [R, N] (ld
+ *     >= N rounded up to 64, zero pad columns) . w_e, w [E][N][ldw] bf16 at
+ *     w + e * w_estride (elements), dX [R, K].
+ *   ntlb_gemm_grouped_dgrad_dense_gate_up: the interleaved gate / up form of
+ *     ntlb_gemm_grouped_ste_dgrad_gate_up over w [E][2I][ldw].
+ *   ntlb_gemm_grouped_wgrad_dense: dW_e [N, K] = dY rows^T . X rows over the
+ *     expert's rows, X bf16 [R, ldx]; dW at dw + e * dw_estride bytes (zero
+ *     for an expert without rows).
+ * ld % 4 == 0 and 16-byte alignment for the operands read transposed.
+ */
+int ntlb_gemm_grouped_dgrad_dense(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                  const int32_t* offsets, int n_experts, const void* w, int64_t ldw, int64_t w_estride,
+                                  int64_t K, void* dx, int dx_dtype, int64_t lddx, void* stream);
+int ntlb_gemm_grouped_dgrad_dense_gate_up(int op_dtype, const void* dgu, int64_t lddgu, int64_t R, int64_t I,
+                                          const int32_t* offsets, int n_experts, const void* w, int64_t ldw,
+                                          int64_t w_estride, int64_t K, void* dx, int64_t lddx, void* stream);
+int ntlb_gemm_grouped_wgrad_dense(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                  const int32_t* offsets, int n_experts, const void* x, int64_t ldx, int64_t K,
+                                  void* dw, int dw_dtype, int64_t lddw, int64_t dw_estride, void* stream);
+
 /* Y[M, N] = A[M, K] . op(B) + bias over bf16 or fp32 matrices (op_dtype), for
  * the dequantized tensors of granularities whose scales change along the
  * contraction element by element (the activation "channel" granularity of
@@ -770,7 +797,7 @@ int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* to
  * (w_dtype, n_assign = T*K entries).  Out: the kept rows, each expert's
  * highest weight first (equal weights keep row order), as pos_out
  * [n_assign] (assignment -> kept row, -1 dropped), inv_out [rows] (kept row
- * -> assignment; entries past the kept count are not written), offsets_out
+ * -> assignment; -1 past the kept count), offsets_out
  * [n_experts + 1] and counts_out int64 [n_experts].  capacity <= 0 keeps every
  * row in its order.
  */

@@ -668,7 +668,7 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     m0 += lo;
     g.M = hi;  // rows at or past the expert's end are not stored
     g.b.p += (int64_t)e * g.b_estride;
-    g.b.s += (int64_t)e * g.bs_estride;
+    if constexpr (SB == SRC_TCODES) g.b.s += (int64_t)e * g.bs_estride;
   } else if constexpr (GRP == GRP_K) {
     // every expert has the num_m x num_n tiles of its own Y; its contraction
     // is its rows, so both operands start at row offsets[e] and hold
@@ -703,9 +703,13 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     const int64_t lo = g.offsets[e], rows_e = g.offsets[e + 1] - lo;
     g.a.p += lo * g.a.ld * EB;
     g.a.kvalid = rows_e;
-    g.b.p += lo * g.b.ld;
-    g.b.s += lo;  // per-row scales, consecutive along the contraction
-    g.b.s_extent -= lo;
+    if constexpr (SB == SRC_TCODES) {
+      g.b.p += lo * g.b.ld;
+      g.b.s += lo;  // per-row scales, consecutive along the contraction
+      g.b.s_extent -= lo;
+    } else {
+      g.b.p += lo * g.b.ld * EB;  // a dense operand: ld in elements
+    }
     g.b.kvalid = rows_e;
     nk = max(1, (int)((rows_e + KSTEP - 1) / KSTEP));
     g.y = reinterpret_cast<uint8_t*>(g.y) + (int64_t)e * g.y_estride;
@@ -1148,6 +1152,13 @@ void launch_grouped(const DqArgs& g, int64_t wgs, hipStream_t st) {
     gemm_dq_kernel<EL_BF16, SA, SB, GRID_INT, SCM, GRP, IL><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
 }
 
+// the grouped GEMMs over dense bf16 operands (the straight-through operands
+// t + (t_dq - t) that stochastic rounding leaves apart from bf16(q * s))
+template <int SA, int SB, int GRP, bool IL = false>
+void launch_grouped_dense(const DqArgs& g, int64_t wgs, hipStream_t st) {
+  gemm_dq_kernel<EL_BF16, SA, SB, GRID_E4M3, SC_SHARED, GRP, IL><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
+}
+
 int elem_of(int op_dtype, const char* fn, int& el) {
   if (op_dtype == NTLB_BF16) el = EL_BF16;
   else if (op_dtype == NTLB_F32) el = EL_F32;
@@ -1535,6 +1546,117 @@ extern "C" int ntlb_gemm_grouped_ste_wgrad(int op_dtype, const void* dy, int64_t
   const int64_t wgs = ((N + TM - 1) / TM) * ((K + TN - 1) / TN) * n_experts;
   if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
   launch_grouped<SRC_TDIRECT, SRC_TCODES, SC_CONTIG, GRP_K>(g, wgs, as_stream(stream));
+  return check_launch(fn);
+}
+
+// a dense bf16 operand read transposed: 8-byte loads of four operand rows
+static int check_tdense(const char* fn, const char* what, const void* p, int64_t ld, int64_t rows, int64_t kvalid) {
+  if (!p) return fail(NTLB_EINVAL, "%s: NULL %s", fn, what);
+  if (ld < rows || ld % 4 || !aligned(p, 16))
+    return fail(NTLB_EINVAL, "%s: %s needs ld >= %lld, ld %% 4 == 0 and 16-byte alignment", fn, what, (long long)rows);
+  if ((kvalid + 64) * ld * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: %s exceeds 2 GiB", fn, what);
+  return NTLB_OK;
+}
+
+extern "C" int ntlb_gemm_grouped_dgrad_dense(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                             const int32_t* offsets, int n_experts, const void* w, int64_t ldw,
+                                             int64_t w_estride, int64_t K, void* dx, int dx_dtype, int64_t lddx,
+                                             void* stream) {
+  const char* fn = "ntlb_gemm_grouped_dgrad_dense";
+  if (op_dtype != NTLB_BF16) return fail(NTLB_EUNSUPPORTED, "%s: bf16 operands only", fn);
+  if (R < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (R == 0 || K == 0) return NTLB_OK;
+  if (N == 0) return fail(NTLB_EUNSUPPORTED, "%s: N == 0 (dX is zero)", fn);
+  if (!dy || !dx) return fail(NTLB_EINVAL, "%s: NULL dY or dX", fn);
+  if (int rc = check_offsets(fn, offsets, n_experts)) return rc;
+  const int64_t Nc = (N + 63) / 64 * 64;
+  if (lddy < Nc || !aligned(dy, 16) || (lddy * 2) % 16)
+    return fail(NTLB_EINVAL, "%s: dY needs ld >= N rounded up to 64 (zero pad columns), 16-byte rows and alignment",
+                fn);
+  if ((R + 256) * lddy * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: dY exceeds 2 GiB", fn);
+  if (int rc = check_tdense(fn, "W", w, ldw, K, N)) return rc;
+  if (w_estride < N * ldw || w_estride % 8) return fail(NTLB_EINVAL, "%s: bad W expert stride", fn);
+  if (!valid_dtype(dx_dtype) || lddx < K) return fail(NTLB_EINVAL, "%s: bad dX dtype or ld", fn);
+  DqArgs g{};
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, R, Nc, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  // W_e^T as the B operand: element (r = k, c = n) at w_e[n * ldw + k]
+  g.b = Operand{reinterpret_cast<const uint8_t*>(w), ldw, K, N, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.M = R; g.N = K; g.Kc = Nc;
+  g.y = dx; g.y_dtype = dx_dtype; g.ldy = lddx;
+  g.vec_out = aligned(dx, 16) && ((lddx * dtype_size(dx_dtype)) % 16 == 0);
+  g.offsets = offsets; g.n_experts = n_experts;
+  g.b_estride = w_estride * 2;
+  const int64_t num_n = (K + TN - 1) / TN;
+  const int64_t wgs = ((R + TM - 1) / TM + n_experts) * num_n;
+  if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS>(g, wgs, as_stream(stream));
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_grouped_dgrad_dense_gate_up(int op_dtype, const void* dgu, int64_t lddgu, int64_t R,
+                                                     int64_t I, const int32_t* offsets, int n_experts, const void* w,
+                                                     int64_t ldw, int64_t w_estride, int64_t K, void* dx,
+                                                     int64_t lddx, void* stream) {
+  const char* fn = "ntlb_gemm_grouped_dgrad_dense_gate_up";
+  if (op_dtype != NTLB_BF16) return fail(NTLB_EUNSUPPORTED, "%s: bf16 operands only", fn);
+  if (R < 0 || I < 0 || K < 0 || I % 128) return fail(NTLB_EINVAL, "%s: bad shape (I %% 128 == 0)", fn);
+  if (R == 0 || K == 0) return NTLB_OK;
+  if (I == 0) return fail(NTLB_EUNSUPPORTED, "%s: I == 0 (dX is zero)", fn);
+  if (!dgu || !dx) return fail(NTLB_EINVAL, "%s: NULL dY or dX", fn);
+  if (int rc = check_offsets(fn, offsets, n_experts)) return rc;
+  const int64_t N = 2 * I;
+  if (lddgu < N || !aligned(dgu, 16) || (lddgu * 2) % 16)
+    return fail(NTLB_EINVAL, "%s: d_gate_up needs ld >= 2I, 16-byte rows and alignment", fn);
+  if ((R + 256) * lddgu * 2 >= (int64_t)0x7FFFFFFF) return fail(NTLB_EUNSUPPORTED, "%s: dY exceeds 2 GiB", fn);
+  if (int rc = check_tdense(fn, "W", w, ldw, K, N)) return rc;
+  if (w_estride < N * ldw || w_estride % 8) return fail(NTLB_EINVAL, "%s: bad W expert stride", fn);
+  if (lddx < K) return fail(NTLB_EINVAL, "%s: bad dX ld", fn);
+  DqArgs g{};
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dgu), lddgu, R, N, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.b = Operand{reinterpret_cast<const uint8_t*>(w), ldw, K, N, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.M = R; g.N = K; g.Kc = I;  // one half of the interleaved contraction per launch
+  g.y = dx; g.y_dtype = DT_BF16; g.ldy = lddx;
+  g.vec_out = aligned(dx, 16) && ((lddx * 2) % 16 == 0);
+  g.offsets = offsets; g.n_experts = n_experts;
+  g.b_estride = w_estride * 2;
+  const int64_t num_n = (K + TN - 1) / TN;
+  const int64_t wgs = ((R + TM - 1) / TM + n_experts) * num_n;
+  if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  hipStream_t st = as_stream(stream);
+  g.il_half = 0; g.accum = 0;
+  launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS, true>(g, wgs, st);
+  g.il_half = 1; g.accum = 1;
+  launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS, true>(g, wgs, st);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_gemm_grouped_wgrad_dense(int op_dtype, const void* dy, int64_t lddy, int64_t R, int64_t N,
+                                             const int32_t* offsets, int n_experts, const void* x, int64_t ldx,
+                                             int64_t K, void* dw, int dw_dtype, int64_t lddw, int64_t dw_estride,
+                                             void* stream) {
+  const char* fn = "ntlb_gemm_grouped_wgrad_dense";
+  if (op_dtype != NTLB_BF16) return fail(NTLB_EUNSUPPORTED, "%s: bf16 operands only", fn);
+  if (R < 0 || N < 0 || K < 0) return fail(NTLB_EINVAL, "%s: negative shape", fn);
+  if (N == 0 || K == 0) return NTLB_OK;
+  if (!dy || !dw) return fail(NTLB_EINVAL, "%s: NULL dY or dW", fn);
+  if (int rc = check_offsets(fn, offsets, n_experts)) return rc;
+  if (int rc = check_tdense(fn, "dY", dy, lddy, N, R)) return rc;
+  if (int rc = check_tdense(fn, "X", x, ldx, K, R)) return rc;
+  if (!valid_dtype(dw_dtype) || lddw < K) return fail(NTLB_EINVAL, "%s: bad dW dtype or ld", fn);
+  if (dw_estride < N * lddw * dtype_size(dw_dtype)) return fail(NTLB_EINVAL, "%s: dW expert stride too small", fn);
+  DqArgs g{};
+  // dY^T and X^T as the operands: (r = n, c = m) at dy[m * lddy + n], (r = k, c = m) at x[m * ldx + k]; the
+  // kernel moves both to the expert's first row
+  g.a = Operand{reinterpret_cast<const uint8_t*>(dy), lddy, N, R, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.b = Operand{reinterpret_cast<const uint8_t*>(x), ldx, K, R, nullptr, 0, 0, 0, 0, 0, 0, 0};
+  g.M = N; g.N = K; g.Kc = (R + 63) / 64 * 64;
+  g.y = dw; g.y_dtype = dw_dtype; g.ldy = lddw;
+  g.vec_out = aligned(dw, 16) && ((lddw * dtype_size(dw_dtype)) % 16 == 0) && dw_estride % 16 == 0;
+  g.offsets = offsets; g.n_experts = n_experts;
+  g.y_estride = dw_estride;
+  const int64_t wgs = ((N + TM - 1) / TM) * ((K + TN - 1) / TN) * n_experts;
+  if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
+  launch_grouped_dense<SRC_TDIRECT, SRC_TDIRECT, GRP_K>(g, wgs, as_stream(stream));
   return check_launch(fn);
 }
 

@@ -321,6 +321,8 @@ extern "C" int ntlb_moe_capacity_keep(const int32_t* inv, const int32_t* offsets
   if (rows >= (int64_t)0x7FFFFFFF || n_experts > 65535) return fail(NTLB_EUNSUPPORTED, "%s: too large", fn);
   hipStream_t st = as_stream(stream);
   if (n_assign > 0) fill_i32_kernel<<<grid_for(n_assign, CAP_THREADS), CAP_THREADS, 0, st>>>(pos_out, n_assign, -1);
+  // rows past the kept count read -1 (a gather over inv_out must not meet stale indices)
+  if (rows > 0) fill_i32_kernel<<<grid_for(rows, CAP_THREADS), CAP_THREADS, 0, st>>>(inv_out, rows, -1);
   capacity_offsets_kernel<<<1, CAP_THREADS, 0, st>>>(offsets, n_experts, capacity, offsets_out, counts_out);
   if (rows > 0) {
     const int64_t chunks = (rows + CAP_THREADS - 1) / CAP_THREADS;  // bounds every expert's row count

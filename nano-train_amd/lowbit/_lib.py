@@ -113,6 +113,10 @@ SIGNATURES = {
                                             _I64, _I64, _I64, _P, _I64, _P],
     "ntlb_gemm_grouped_ste_wgrad": [_I32, _P, _I64, _I64, _I64, _P, _I32, _I32, _P, _I64, _P, _I64, _I64, _I32, _I64,
                                     _P, _I32, _I64, _I64, _P],
+    "ntlb_gemm_grouped_dgrad_dense": [_I32, _P, _I64, _I64, _I64, _P, _I32, _P, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "ntlb_gemm_grouped_dgrad_dense_gate_up": [_I32, _P, _I64, _I64, _I64, _P, _I32, _P, _I64, _I64, _I64, _P, _I64,
+                                              _P],
+    "ntlb_gemm_grouped_wgrad_dense": [_I32, _P, _I64, _I64, _I64, _P, _I32, _P, _I64, _I64, _P, _I32, _I64, _I64, _P],
     "ntlb_gemm_grouped_swiglu_quant_gu": [_I32, _P, _I64, _P, _I64, _I64, _I32, _P, _I64, _I64, _P, _I64, _I64, _I64,
                                           _P, _I32, _I64, _I64, _I64, _P, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _P,
                                           _I32, _I32, _I32, _U64, _U64, _P, _I64, _P],

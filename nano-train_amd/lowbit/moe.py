@@ -423,6 +423,15 @@ def split_gate_up(w_gate_up: torch.Tensor):
     return v[:, :, 0], v[:, :, 1]
 
 
+def _dequant_experts(codes: torch.Tensor, scales: torch.Tensor, grid: int, K: int) -> torch.Tensor:
+    """bf16(q * s) of quantize_expert_weights' codes [E, N, Kp] and 128x128
+    block scales [E, N/128, Kp/128], as [E, N, K]"""
+    E, N, Kp = codes.shape
+    q = QTensor(codes.reshape(E * N, Kp), scales.reshape(-1).contiguous(), scales.shape[2], 1, 7, grid, E * N, K,
+                None, None)
+    return ops.dequant(q, out_dtype=torch.bfloat16).reshape(E, N, K)
+
+
 class _LocalMoE(torch.autograd.Function):
     """The single-rank expert loop with its backward on HIP kernels.
 
@@ -459,24 +468,44 @@ class _LocalMoE(torch.autograd.Function):
         qx = ops.quant_tile_1x128_fanout(tokens.detach(), routing.pos, routing.top_k, routing.rows, fmt=fmt,
                                          bits=bits, rounding=rounding, seed=seed, offset=offset, want_nan_rows=True)
         train = any(ctx.needs_input_grad[:4])
+        # stochastic rounding: the backward multiplies the reference's operands
+        # t + (t_dq - t), which differ from bf16(q * s) (te_backend.py:250-251)
+        sr = train and rounding == "stochastic"
         gu = torch.empty((routing.rows, N2), dtype=torch.bfloat16, device=tokens.device) if train else None
-        _, qh = ops.gemm_swiglu_quant(qx, gu_codes, gu_scales, offsets=routing.offsets, fmt=fmt, bits=bits,
-                                      rounding=rounding, seed=seed, offset=offset + 1, want_h=False,
+        h, qh = ops.gemm_swiglu_quant(qx, gu_codes, gu_scales, offsets=routing.offsets, fmt=fmt, bits=bits,
+                                      rounding=rounding, seed=seed, offset=offset + 1, want_h=sr,
                                       want_nan_rows=True, b_nan_rows=gu_nan, gu_out=gu)
         y = ops.gemm_grouped_blockscaled(qh, d_codes, d_scales, routing.offsets, N=H, out_dtype=tokens.dtype,
                                          b_nan_rows=d_nan)
         out = combine_rows(y, routing, expert_ids, topk_w.detach(), T)
         ctx.meta = (T, H, E, I, routing.top_k, routing.rows, qx.grid, qx.s_col, qh.s_col, tokens.dtype,
                     w_gate_up.dtype, w_down.dtype)
-        ctx.save_for_backward(routing.pos, routing.inv, routing.counts, routing.offsets, expert_ids, topk_w.detach(),
-                              qx.codes, qx.scales, gu, qh.codes, qh.scales, y, gu_codes, gu_scales, d_codes, d_scales)
+        ctx.sr = sr
+        if sr:
+            bf = torch.bfloat16
+            # row -> token (the rows past the kept count hold -1: any in-range
+            # token serves them, the GEMMs never read those rows)
+            rows_tok = (routing.inv.clamp(0, T * routing.top_k - 1) // routing.top_k).long()
+            xq = ops.ste_value(tokens.detach().index_select(0, rows_tok), ops.dequant(qx, out_dtype=bf))
+            hq = ops.ste_value(h, ops.dequant(qh, out_dtype=bf))
+            wguq = ops.ste_value(w_gate_up.detach(), _dequant_experts(gu_codes, gu_scales, qx.grid, H))
+            wdq = ops.ste_value(w_down.detach(), _dequant_experts(d_codes, d_scales, qx.grid, I))
+            ctx.save_for_backward(routing.pos, routing.inv, routing.counts, routing.offsets, expert_ids,
+                                  topk_w.detach(), xq, gu, hq, y, wguq, wdq)
+        else:
+            ctx.save_for_backward(routing.pos, routing.inv, routing.counts, routing.offsets, expert_ids,
+                                  topk_w.detach(), qx.codes, qx.scales, gu, qh.codes, qh.scales, y, gu_codes,
+                                  gu_scales, d_codes, d_scales)
         return out
 
     @staticmethod
     def backward(ctx, d_out):
-        (pos, inv, counts, offsets, expert_ids, topk_w, xc, xs, gu, hc, hs, y, gu_codes, gu_scales, d_codes,
-         d_scales) = ctx.saved_tensors
         T, H, E, I, k, R, grid, x_rp, h_rp, tdt, gudt, ddt = ctx.meta
+        if ctx.sr:
+            pos, inv, counts, offsets, expert_ids, topk_w, xq, gu, hq, y, wguq, wdq = ctx.saved_tensors
+        else:
+            (pos, inv, counts, offsets, expert_ids, topk_w, xc, xs, gu, hc, hs, y, gu_codes, gu_scales, d_codes,
+             d_scales) = ctx.saved_tensors
         d_out = d_out.contiguous()
         dev = d_out.device
         routing = ExpertRouting(pos, inv, counts, offsets, k)
@@ -489,24 +518,36 @@ class _LocalMoE(torch.autograd.Function):
                   dyr.data_ptr(), ld, d_w.data_ptr(), ops._stream())
         dyr = dyr[:, :H]
         # down projection, then the SwiGLU
-        dh = ops.grouped_ste_dgrad(dyr, offsets, d_codes, d_scales, grid=grid, K=I, out_dtype=torch.bfloat16)
+        if ctx.sr:
+            dh = ops.grouped_dgrad_dense(dyr, offsets, wdq, out_dtype=torch.bfloat16)
+        else:
+            dh = ops.grouped_ste_dgrad(dyr, offsets, d_codes, d_scales, grid=grid, K=I, out_dtype=torch.bfloat16)
         d_gu = torch.empty((R, 2 * I), dtype=torch.bfloat16, device=dev)
         _lib.call("ntlb_swiglu_backward", dh.data_ptr(), dh.stride(0), gu.data_ptr(), gu.stride(0), R, I,
                   d_gu.data_ptr(), d_gu.stride(0), ops._stream())
         d_tok = dw_gu = dw_down = None
         if ctx.needs_input_grad[0]:
-            dxr = ops.grouped_ste_dgrad_gate_up(d_gu, offsets, gu_codes, gu_scales, grid=grid, K=H)
+            if ctx.sr:
+                dxr = ops.grouped_dgrad_dense_gate_up(d_gu, offsets, wguq)
+            else:
+                dxr = ops.grouped_ste_dgrad_gate_up(d_gu, offsets, gu_codes, gu_scales, grid=grid, K=H)
             d_tok = torch.empty((T, H), dtype=tdt, device=dev)
             ids = expert_ids.contiguous()
             _lib.call("ntlb_moe_token_grad", dxr.data_ptr(), dxr.stride(0), ops._dtype_code(dxr.dtype),
                       pos.data_ptr(), ids.data_ptr(), 1 if ids.dtype == torch.int64 else 0, T, k, H,
                       d_tok.data_ptr(), d_tok.stride(0), ops._stream())
         if ctx.needs_input_grad[3]:
-            qh = QTensor(hc, hs, 1, h_rp, 0, grid, R, I, None, None)
-            dw_down = ops.grouped_ste_wgrad(dyr, offsets, qh, E, out_dtype=ddt)
+            if ctx.sr:
+                dw_down = ops.grouped_wgrad_dense(dyr, offsets, hq, E, out_dtype=ddt)
+            else:
+                qh = QTensor(hc, hs, 1, h_rp, 0, grid, R, I, None, None)
+                dw_down = ops.grouped_ste_wgrad(dyr, offsets, qh, E, out_dtype=ddt)
         if ctx.needs_input_grad[2]:
-            qx = QTensor(xc, xs, 1, x_rp, 0, grid, R, H, None, None)
-            dw_gu = ops.grouped_ste_wgrad(d_gu, offsets, qx, E, out_dtype=gudt)
+            if ctx.sr:
+                dw_gu = ops.grouped_wgrad_dense(d_gu, offsets, xq, E, out_dtype=gudt)
+            else:
+                qx = QTensor(xc, xs, 1, x_rp, 0, grid, R, H, None, None)
+                dw_gu = ops.grouped_ste_wgrad(d_gu, offsets, qx, E, out_dtype=gudt)
         return d_tok, (d_w if ctx.needs_input_grad[1] else None), dw_gu, dw_down, None, None, None, None
 
 
@@ -536,9 +577,14 @@ def local_moe(
     routing weight (compute_capacity() gives the reference's value); the
     dropped assignments add nothing and get a zero routing-weight gradient.
     Forward arithmetic: the blockwise-scaled GEMMs (fp32 q * s operands);
-    backward: the straight-through gradients over the reference's bf16(q * s)
-    operands.  An expert that receives no rows gets a zero weight gradient
-    (the reference's separate Linears would get none)."""
+    backward: the straight-through gradients over the reference's operands,
+    t + (t_dq - t) in bf16 (te_backend.py:250-251): bf16(q * s), decoded from
+    the codes inside the GEMMs, under round to nearest; under stochastic
+    rounding, where the two differ, the operands themselves (ntlb_ste_value)
+    on the grouped bf16 GEMMs.  Stochastic rounding quantizes x once for the
+    gate and up projections (the reference's two Linears draw twice).  An
+    expert that receives no rows gets a zero weight gradient (the reference's
+    separate Linears would get none)."""
     if tokens.dim() != 2 or expert_ids.dim() != 2 or topk_w.shape != expert_ids.shape:
         raise ValueError("tokens must be [T, H], expert_ids and topk_w [T, k]")
     if tokens.dtype != torch.bfloat16 or w_gate_up.dtype != torch.bfloat16 or w_down.dtype != torch.bfloat16:

@@ -709,6 +709,63 @@ def grouped_ste_wgrad(dy: torch.Tensor, offsets: torch.Tensor, x: QTensor, n_exp
     return out
 
 
+def grouped_dgrad_dense(dy: torch.Tensor, offsets: torch.Tensor, w: torch.Tensor, *,
+                        out_dtype: torch.dtype) -> torch.Tensor:
+    """dX[rows of e] = dY[rows of e] @ w[e] for rows sorted by expert, w bf16
+    [E, N, K] (the straight-through operands of the experts' weights)."""
+    _require_device(dy, offsets, w)
+    if dy.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("grouped_dgrad_dense takes bf16 operands")
+    E, N, K = w.shape
+    if dy.shape[1] != N or offsets.numel() != E + 1 or offsets.dtype != torch.int32:
+        raise ValueError("dY columns must match the weights' rows and offsets must be int32 [E+1]")
+    w = w if (w.is_contiguous() and K % 4 == 0) else _pad_cols(w.reshape(E * N, K), 4).reshape(E, N, -1)
+    R = dy.shape[0]
+    dyp = _pad_cols(dy, 64)
+    out = torch.empty((R, K), dtype=out_dtype, device=dy.device)
+    call("ntlb_gemm_grouped_dgrad_dense", _lib.BF16, dyp.data_ptr(), dyp.stride(0), R, N, offsets.data_ptr(), E,
+         w.data_ptr(), w.stride(1), w.stride(0), K, out.data_ptr(), _dtype_code(out_dtype), out.stride(0), _stream())
+    return out
+
+
+def grouped_dgrad_dense_gate_up(d_gu: torch.Tensor, offsets: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """grouped_ste_dgrad_gate_up over dense bf16 gate/up operands w [E, 2I, H]
+    (128-row blocks alternating gate and up): bf16(dX_gate) + bf16(dX_up)."""
+    _require_device(d_gu, offsets, w)
+    if d_gu.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError("grouped_dgrad_dense_gate_up takes bf16 operands")
+    E, N2, H = w.shape
+    if d_gu.shape[1] != N2 or offsets.numel() != E + 1 or offsets.dtype != torch.int32:
+        raise ValueError("d_gate_up columns must match the weights' rows and offsets must be int32 [E+1]")
+    w = w if (w.is_contiguous() and H % 4 == 0) else _pad_cols(w.reshape(E * N2, H), 4).reshape(E, N2, -1)
+    R = d_gu.shape[0]
+    d_gu = _pad_cols(d_gu, 64)
+    out = torch.empty((R, H), dtype=torch.bfloat16, device=d_gu.device)
+    call("ntlb_gemm_grouped_dgrad_dense_gate_up", _lib.BF16, d_gu.data_ptr(), d_gu.stride(0), R, N2 // 2,
+         offsets.data_ptr(), E, w.data_ptr(), w.stride(1), w.stride(0), H, out.data_ptr(), out.stride(0), _stream())
+    return out
+
+
+def grouped_wgrad_dense(dy: torch.Tensor, offsets: torch.Tensor, x: torch.Tensor, n_experts: int, *,
+                        out_dtype: torch.dtype) -> torch.Tensor:
+    """dW[e] = dY[rows of e]^T @ x[rows of e] over dense bf16 rows (zero for an
+    expert without rows).  dW [E, N, K]."""
+    _require_device(dy, offsets, x)
+    if dy.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise TypeError("grouped_wgrad_dense takes bf16 operands")
+    R, N = dy.shape
+    K = x.shape[1]
+    if x.shape[0] != R or offsets.numel() != n_experts + 1 or offsets.dtype != torch.int32:
+        raise ValueError("dY and x must have the same rows and offsets must be int32 [E+1]")
+    dy = dy if (dy.stride(-1) == 1 and dy.stride(0) % 4 == 0 and dy.data_ptr() % 16 == 0) else _pad_cols(dy, 4)
+    x = x if (x.stride(-1) == 1 and x.stride(0) % 4 == 0 and x.data_ptr() % 16 == 0) else _pad_cols(x, 4)
+    out = torch.empty((n_experts, N, K), dtype=out_dtype, device=dy.device)
+    call("ntlb_gemm_grouped_wgrad_dense", _lib.BF16, dy.data_ptr(), dy.stride(0), R, N, offsets.data_ptr(),
+         n_experts, x.data_ptr(), x.stride(0), K, out.data_ptr(), _dtype_code(out_dtype), out.stride(1),
+         out.stride(0) * out.element_size(), _stream())
+    return out
+
+
 def gemm_dense(a: torch.Tensor, b: torch.Tensor, *, b_transposed: bool = False, bias: Optional[torch.Tensor] = None,
                out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
     """Y = a @ b^T (b [N, K]) or a @ b (b_transposed: b [K, N]) + bias over

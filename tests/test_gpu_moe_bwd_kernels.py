@@ -275,3 +275,42 @@ def test_grouped_ste_wgrad_equals_per_expert_wgrad(gpu_device, fmt):
         qe = ops.quant_tile_1x128(x[lo:hi], fmt=fmt)
         want = ops.ste_wgrad(dy[lo:hi], qe, out_dtype=torch.bfloat16)
         assert torch.equal(got[e], want), e
+
+
+def test_grouped_dense_gemms_equal_per_expert_dense(gpu_device):
+    """The grouped backward GEMMs over dense bf16 operands (the stochastic-
+    rounding form of the expert loop's backward) equal, on each expert's
+    rows, the dense kernels over that expert's operands bit for bit: dgrad
+    and the interleaved gate/up dgrad against ops.gemm_dense (W read
+    transposed), wgrad against ops.gemm_dense_tn; an expert without rows gets
+    a zero weight gradient."""
+    from lowbit import ops
+
+    E, N, K, I = len(COUNTS), 384, 700, 256
+    offs, offsets = _offsets(COUNTS, gpu_device)
+    R = offs[-1]
+    g = torch.Generator().manual_seed(20262561)
+    w = (torch.randn(E, N, K, generator=g) * 0.05).bfloat16().to(gpu_device)
+    wgu = (torch.randn(E, 2 * I, K, generator=g) * 0.05).bfloat16().to(gpu_device)
+    dy = torch.randn(R, N, generator=g).bfloat16().to(gpu_device)
+    dgu = torch.randn(R, 2 * I, generator=g).bfloat16().to(gpu_device)
+    x = torch.randn(R, K, generator=g).bfloat16().to(gpu_device)
+    dx = ops.grouped_dgrad_dense(dy, offsets, w, out_dtype=torch.bfloat16)
+    dxgu = ops.grouped_dgrad_dense_gate_up(dgu, offsets, wgu)
+    dw = ops.grouped_wgrad_dense(dy, offsets, x, E, out_dtype=torch.bfloat16)
+    j = torch.arange(I, device=gpu_device)
+    gate, up = 256 * (j // 128) + j % 128, 256 * (j // 128) + 128 + j % 128
+    for e in range(E):
+        lo, hi = offs[e], offs[e + 1]
+        if hi == lo:
+            assert bool((dw[e] == 0).all())
+            continue
+        want = ops.gemm_dense(dy[lo:hi], w[e], b_transposed=True, out_dtype=torch.bfloat16)
+        assert torch.equal(dx[lo:hi].view(torch.int16), want.view(torch.int16)), e
+        dg = ops.gemm_dense(dgu[lo:hi, gate].contiguous(), wgu[e, gate].contiguous(), b_transposed=True,
+                            out_dtype=torch.bfloat16)
+        du = ops.gemm_dense(dgu[lo:hi, up].contiguous(), wgu[e, up].contiguous(), b_transposed=True,
+                            out_dtype=torch.bfloat16)
+        assert torch.equal(dxgu[lo:hi].view(torch.int16), (dg + du).view(torch.int16)), e
+        want = ops.gemm_dense_tn(dy[lo:hi].contiguous(), x[lo:hi].contiguous(), out_dtype=torch.bfloat16)
+        assert torch.equal(dw[e].view(torch.int16), want.view(torch.int16)), e

@@ -150,6 +150,7 @@ def test_capacity_keeps_the_reference_rows_in_order(gpu_device):
     kept = set(inv[:offs[-1]].tolist())
     for a in range(T * k):
         assert (int(pos[a]) >= 0) == (a in kept)
+    assert bool((inv[offs[-1]:] == -1).all())  # no stale row -> assignment entries past the kept rows
     assert r.dropped() == T * k - offs[-1] > 0
 
 
@@ -262,3 +263,76 @@ def test_local_moe_config4_sampled(gpu_device):
         dx_ref[j] = acc
     assert rel_fro_bf16(d_tok[sample], dx_ref.double().cpu().numpy()) <= 1e-3
     assert O.rel_frobenius(to_np32(d_w[sample]), dwr_ref.cpu().numpy()) <= 1e-3
+
+
+def _sr_qdq_from_gpu(tokens, idx, w, w_gu, w_d, dev, *, capacity, fmt, seed, offset):
+    """The stochastic-rounding dq values local_moe draws (x at `offset`, h at
+    +1, gate/up weights at +2, down weights at +3), served to the oracle loop
+    in the order it quantizes: per expert with rows, x and the gate weight,
+    x and the up weight, h and the down weight.  Also the kernels' bf16
+    gate / up projections (rows in expert order) and the offsets."""
+    from lowbit import moe, ops
+
+    E, N2, H = w_gu.shape
+    I = N2 // 2
+    kw = dict(fmt=fmt, rounding="stochastic", seed=seed)
+    r = moe.route_by_expert(idx.to(dev), E, capacity=capacity, topk_w=w.to(dev))
+    gc, gs, gn = moe.quantize_expert_weights(w_gu.to(dev), offset=offset + 2, **kw)
+    dc, ds, _ = moe.quantize_expert_weights(w_d.to(dev), offset=offset + 3, **kw)
+    qx = ops.quant_tile_1x128_fanout(tokens.to(dev), r.pos, r.top_k, r.rows, offset=offset, want_nan_rows=True,
+                                     **kw)
+    gu = torch.empty((r.rows, N2), dtype=torch.bfloat16, device=dev)
+    _, qh = ops.gemm_swiglu_quant(qx, gc, gs, offsets=r.offsets, offset=offset + 1, want_h=False, b_nan_rows=gn,
+                                  gu_out=gu, **kw)
+
+    def deq_experts(c, s_, K):
+        En, Nn, Kp = c.shape
+        q = ops.QTensor(c.reshape(En * Nn, Kp), s_.reshape(-1).contiguous(), s_.shape[2], 1, 7, qx.grid, En * Nn, K)
+        return ops.dequant(q, out_dtype=torch.float32).reshape(En, Nn, K).cpu()
+
+    xd = ops.dequant(qx, out_dtype=torch.float32).cpu()
+    hd = ops.dequant(qh, out_dtype=torch.float32).cpu()
+    wgu_d = deq_experts(gc, gs, H).reshape(E, I // 128, 2, 128, H)
+    wd_d = deq_experts(dc, ds, I)
+    offs = r.offsets.cpu().tolist()
+    order = []
+    for e in range(E):
+        lo, hi = offs[e], offs[e + 1]
+        if hi > lo:
+            order += [xd[lo:hi], wgu_d[e, :, 0].reshape(I, H), xd[lo:hi], wgu_d[e, :, 1].reshape(I, H), hd[lo:hi],
+                      wd_d[e]]
+    it = iter(order)
+
+    def qdq(t, gr, gc_):
+        v = next(it)
+        assert v.shape == t.shape
+        return v
+
+    return qdq, gu.cpu(), offs
+
+
+@pytest.mark.parametrize("capacity", [0, 40])
+def test_local_moe_stochastic_rounding_gradients_match_reference_loop(gpu_device, capacity):
+    """Under stochastic rounding the expert loop's backward multiplies the
+    reference's straight-through operands t + (t_dq - t) (which differ from
+    bf16(q * s) there) on the grouped bf16 GEMMs: the gradients of tokens,
+    routing weights and both weight stacks against the reference loop's
+    autograd fed the same stochastic dq values (the ones the kernels draw)
+    and the kernels' bf16 projections, within 1e-3."""
+    T, H, I, E, k = 96, 256, 256, 6, 3
+    seed, offset = 4242, 16
+    tokens, idx, w, w_gu, w_d, d_out = _problem(T, H, I, E, k, seed=20262571)
+    out, grads = _run_gpu(tokens, idx, w, w_gu, w_d, d_out, gpu_device, capacity=capacity, fmt="e4m3",
+                          rounding="stochastic", seed=seed, offset=offset)
+    qdq, gu, offs = _sr_qdq_from_gpu(tokens, idx, w, w_gu, w_d, gpu_device, capacity=capacity, fmt="e4m3", seed=seed,
+                                     offset=offset)
+    leaves = [t.clone().requires_grad_(True) for t in (tokens, w, w_gu, w_d)]
+    values = lambda e: _split_rows(gu[offs[e]:offs[e + 1]])  # noqa: E731
+    ref = TE.local_moe_loop(leaves[0], idx, leaves[1], leaves[2], leaves[3], capacity=capacity, forward="fp32_dq",
+                            qdq=qdq, gate_up_values=values)
+    ref.backward(d_out)
+    assert rel_fro_bf16(out, ref.detach().double().numpy()) <= 1e-3
+    for name, g, r in zip(["tokens", "topk_w", "w_gate_up", "w_down"], grads, [t.grad for t in leaves]):
+        r = _grad_or_zero(r, g)
+        err = O.rel_frobenius(to_np32(g), to_np32(r)) if name == "topk_w" else rel_fro_bf16(g, r.double().numpy())
+        assert err <= 1e-3, (name, err)
