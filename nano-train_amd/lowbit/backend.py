@@ -111,6 +111,24 @@ def quantize_operand(
     return QTensor(codes, scales, 0, 0, 0, ops.grid_code(fmt), R, K, nan, dq), dq
 
 
+def _channel_folded_gemm(codes: torch.Tensor, col_scales: torch.Tensor, w_dq32: torch.Tensor, grid: int, bias,
+                         out_dtype: torch.dtype) -> torch.Tensor:
+    """Y = (q * s_x) @ W_dq^T for activation codes q [M, K] with one scale per
+    column (te_backend.py:175-185, channel_axis=-1) and fp32 weight values
+    W_dq [N, K], on bf16 MFMA: the codes are exact in bf16, s_x folds into the
+    weight (W' = s_x * W_dq, one fp32 rounding), and W' splits into bf16
+    W'_hi + W'_lo (16 significant bits), so one bf16 GEMM over [q | q] and
+    [W'_hi | W'_lo] with fp32 accumulation forms the fp32 product within about
+    2^-16 relative, where fp32 MFMA would run at 1/16 of the bf16 rate."""
+    K = w_dq32.shape[1]
+    wf = w_dq32 * col_scales.reshape(1, K).float()
+    w_hi = wf.to(torch.bfloat16)
+    w_lo = (wf - w_hi.float()).to(torch.bfloat16)
+    one = torch.ones(1, dtype=torch.float32, device=codes.device)
+    a = ops.dequant_raw(grid, codes, one, K=K, s_row=0, s_col=0, r_shift=0, c_shift=7, out_dtype=torch.bfloat16)
+    return ops.gemm_dense(torch.cat([a, a], dim=1), torch.cat([w_hi, w_lo], dim=1), bias=bias, out_dtype=out_dtype)
+
+
 def _gemm_op_dtype(*dts: torch.dtype) -> torch.dtype:
     """The MFMA operand type that carries the reference's values exactly:
     bf16 when every operand is bf16, else fp32 (bf16, fp16 and fp32 values
@@ -175,13 +193,23 @@ class _HipLowBitLinear(torch.autograd.Function):
         # dequantized tensors: for the forward, in the input dtypes (reference
         # mode, te_backend.py:173-202) or fp32 (blockscaled mode's q * s
         # operands); the backward rounds them to the input dtypes
-        x_dq_dt = xdt if (ref_fwd or not fwd_dq) else torch.float32
+        # blockscaled mode with per-column activation scales: the scales fold
+        # into the weight (_channel_folded_gemm), which multiplies X's codes;
+        # X's dequantized values serve only the backward, in x's dtype
+        fold = act_channel and not ref_fwd
+        x_dq_dt = xdt if (ref_fwd or not fwd_dq or fold) else torch.float32
         w_dq_dt = wdt if (ref_fwd or not fwd_dq) else torch.float32
-        want_xdq = fwd_dq or (ste and need_w_grad and not wgrad_codes)
+        want_xdq = (fwd_dq and not fold) or (ste and need_w_grad and not wgrad_codes)
         want_wdq = fwd_dq or (ste and need_x_grad and not dgrad_codes)
-        qx, xdq = quantize_operand(
-            x2, backend._activation_granularity, is_weight=False, original_dim=x.dim(), fmt=fmt, bits=bits,
-            rounding=rnd, seed=seed, offset=base + 0, want_dq=want_xdq, dq_dtype=x_dq_dt)
+        if fold:
+            R2 = x2.shape[0]
+            xcodes, xcol, xdq, _ = ops.quant_grouped(x2, R2, 1, fmt=fmt, bits=bits, rounding=rnd, seed=seed,
+                                                     offset=base + 0, want_dq=want_xdq, dq_dtype=x_dq_dt)
+            qx = None
+        else:
+            qx, xdq = quantize_operand(
+                x2, backend._activation_granularity, is_weight=False, original_dim=x.dim(), fmt=fmt, bits=bits,
+                rounding=rnd, seed=seed, offset=base + 0, want_dq=want_xdq, dq_dtype=x_dq_dt)
         qw, wdq = quantize_operand(
             weight, backend._weight_granularity, is_weight=True, original_dim=weight.dim(), fmt=fmt, bits=bits,
             rounding=rnd, seed=seed, offset=base + 1, want_dq=want_wdq, dq_dtype=w_dq_dt)
@@ -191,7 +219,9 @@ class _HipLowBitLinear(torch.autograd.Function):
             xq = _reference_operand(x2, xdq, xdt, sr)
         if ste and need_x_grad and not dgrad_codes:
             wq = _reference_operand(weight, wdq, wdt, sr)
-        if fwd_dq:
+        if fold:
+            y2 = _channel_folded_gemm(xcodes, xcol, wdq.float(), ops.grid_code(fmt), bias, out_dtype)
+        elif fwd_dq:
             if ref_fwd:
                 xf = xq if xq is not None else _reference_operand(x2, xdq, xdt, sr)
                 wf = wq if wq is not None else _reference_operand(weight, wdq, wdt, sr)

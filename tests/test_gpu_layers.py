@@ -540,3 +540,22 @@ def test_persistent_layer_fp32_and_ragged_k_decode_inside_the_gemms(gpu_device, 
         else:
             err = O.rel_frobenius(got.detach().cpu().numpy(), want64)
             assert err <= 1e-5, err
+
+
+@pytest.mark.parametrize("fmt", ["e4m3", "int_grid"])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 384), (77, 129, 264)])
+def test_activation_channel_fold_matches_the_fp32_product(gpu_device, fmt, M, N, K):
+    """Blockscaled mode with per-column activation scales multiplies X's codes
+    by the folded weight s_x * W_dq split into bf16 hi + lo on bf16 MFMA: in
+    fp32 output it stays within 1e-5 of the fp32 GEMM over (q * s_x) and W_dq
+    (the exact values the reference multiplies)."""
+    from lowbit import ops
+    from lowbit.backend import _channel_folded_gemm
+
+    x = seeded((M, K), seed=20262701, outliers=0.01, heavy_channels=True).to(gpu_device)
+    w = seeded((N, K), seed=20262702, std=0.02).to(gpu_device)
+    codes, cs, xdq, _ = ops.quant_grouped(x, M, 1, fmt=fmt, want_dq=True, dq_dtype=torch.float32)
+    qw, _ = ops.quant_block_128x128(w, fmt=fmt, want_dq=True, dq_dtype=torch.float32)
+    y = _channel_folded_gemm(codes, cs, qw.dq, ops.grid_code(fmt), None, torch.float32)
+    ref = O.gemm_ref(to_np32(xdq), to_np32(qw.dq))
+    assert O.rel_frobenius(y.cpu().numpy(), ref) <= 1e-5
