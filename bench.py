@@ -308,7 +308,34 @@ def other_config(args) -> dict:
                            st) * 1e3
         ret_bytes = n_rec * (H * 2 + rec_b)
         comb_bytes = n_rec * rec_b + tokens.shape[0] * H * 2
-        del rows, out_rows, ret
+        # the reference's channel comm-quant on the same layout: value records
+        # (the bf16 wire values and the metadata), both directions
+        chv = dict(granularity="channel")
+        send_v = ep.pack_dispatch(tokens, routing, topk_w, experts_per_rank=4, ep_size=8, **chv)
+        vpack_us = _time_ms(lambda i: ep.pack_dispatch(tokens, routing, topk_w, experts_per_rank=4, ep_size=8, **chv),
+                            args.steps, args.warmup, st) * 1e3
+        vunpack_us = _time_ms(lambda i: ep.unpack_dispatch(send_v.records, rcounts, H=H, local_experts=4,
+                                                           value_dtype=torch.bfloat16), args.steps, args.warmup,
+                              st) * 1e3
+        rows_v = ep.unpack_dispatch(send_v.records, rcounts, H=H, local_experts=4, value_dtype=torch.bfloat16)
+        ret_v = ep.pack_return(out_rows, rows_v, ep_size=8, **chv)
+        vret_us = _time_ms(lambda i: ep.pack_return(out_rows, rows_v, ep_size=8, **chv), args.steps, args.warmup,
+                           st) * 1e3
+        vcomb_us = _time_ms(lambda i: ep.combine(ret_v.records, routing, w_b, H=H, value_dtype=torch.bfloat16),
+                            args.steps, args.warmup, st) * 1e3
+        rec_v = send_v.records.shape[1]
+        T_t = tokens.shape[0]
+        # HBM bytes: the amax pass reads the rows once and the pack once more;
+        # the unpack writes each row's values and 4 metadata words
+        ep_values = {"record_bytes": rec_v, "pack_us": round(vpack_us, 2),
+                     "pack_GBs": round((2 * T_t * H * 2 + n_rec * rec_v) / vpack_us / 1e3, 1),
+                     "unpack_us": round(vunpack_us, 2),
+                     "unpack_GBs": round(n_rec * (rec_v + H * 2 + 16) / vunpack_us / 1e3, 1),
+                     "return_pack_us": round(vret_us, 2),
+                     "return_pack_GBs": round(n_rec * (2 * H * 2 + rec_v) / vret_us / 1e3, 1),
+                     "combine_us": round(vcomb_us, 2),
+                     "combine_GBs": round((n_rec * rec_v + T_t * H * 2) / vcomb_us / 1e3, 1)}
+        del rows, out_rows, ret, send_v, rows_v, ret_v
         # pack: every bf16 token row read once, one record written per assignment;
         # unpack: one record read, codes + tile scales + 5 words of metadata written per row
         pack_bytes = tokens.shape[0] * H * 2 + n_rec * rec_b
@@ -365,7 +392,8 @@ def other_config(args) -> dict:
                                 "pack_GBs": round(pack_bytes / pack_us / 1e3, 1), "unpack_us": round(unpack_us, 2),
                                 "unpack_GBs": round(unpack_bytes / unpack_us / 1e3, 1),
                                 "return_pack_us": round(ret_us, 2), "return_pack_GBs": round(ret_bytes / ret_us / 1e3, 1),
-                                "combine_us": round(comb_us, 2), "combine_GBs": round(comb_bytes / comb_us / 1e3, 1)})
+                                "combine_us": round(comb_us, 2), "combine_GBs": round(comb_bytes / comb_us / 1e3, 1),
+                                "channel_values": ep_values})
         return res
     # c5
     x, w = workloads.c5_inputs(device="cpu")

@@ -775,6 +775,76 @@ int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* to
  * counts, moe.py:851-854), read during the call; needed only with src_rank;
  * ep_size <= 256.  n < 2^31.
  */
+int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv, int64_t rows,
+                           const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc, float* scales,
+                           int64_t s_row, int64_t s_col, int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,
+                           int32_t* src_rank, float* weight, void* stream);
+
+/*
+ * Value records: the payload is the row's values themselves, in the input
+ * dtype, as the reference's comm-quant leaves them in its send buffers
+ * (_comm_quant_dequant, moe.py:79-143, of send_tokens at :805-814 and of
+ * send_back_features at :983-990): tensor + (dq - tensor) with dq = q * scale
+ * rounded to the dtype.  This carries any column grouping of the scales,
+ * including one per column (channel granularity, moe.py:112-121), which a
+ * code record's tile scales cannot, and moves 2 (bf16) or 4 bytes per value,
+ * as the reference's own exchange does.  Layout:
+ *   [0, P)          the H values, P = round_up(H * dtype size, 16)
+ *   [P, P + 32)     the metadata of a code record (token, slot, local expert,
+ *                   0, fp32 weight, 3 reserved)
+ * ntlb_ep_value_record_bytes(H, dtype) = P + 32 (0 for H <= 0 or a bad dtype).
+ */
+int64_t ntlb_ep_value_record_bytes(int64_t H, int dtype);
+
+/*
+ * ntlb_ep_pack_records_grouped with value records: assignment a -> record
+ * pos[a], the token row a / K of tokens [T, H] quantized with one scale per
+ * gc-column group over all rows (amax_bits from ntlb_amax_grouped on tokens
+ * with gr = T and the same gc; gc = 1 channel, 128 tile_1x128 /
+ * block_128x128, H tensor) and written as the straight-through value
+ * ntlb_comm_quant_dequant forms for send-buffer row p (SR element index p*H
+ * + column).  The values equal ntlb_comm_quant_dequant's on the send buffer
+ * tokens[inv / K] bit for bit.  tokens bf16 or fp32, H % 8 == 0, 16-byte
+ * aligned rows and records.
+ */
+int ntlb_ep_pack_values(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt, const int32_t* pos,
+                        const void* topk_idx, int idx_dtype, const void* topk_w, int w_dtype, int64_t K,
+                        int64_t experts_per_rank, const uint32_t* amax_bits, int64_t gc, int grid, int qmax,
+                        int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records, void* stream);
+
+/*
+ * ntlb_ep_pack_return with value records: row i of x [n, H] -> record pos[i]
+ * with token_idx[i], slot_idx[i], the optional local expert and weight, the
+ * values quantized with the group scales of ntlb_amax_grouped on x (gr = n)
+ * as in ntlb_ep_pack_values.
+ */
+int ntlb_ep_pack_return_values(const void* x, int x_dtype, int64_t n, int64_t H, int64_t ldx, const int32_t* pos,
+                               const int32_t* token_idx, const int32_t* slot_idx, const int32_t* local_expert,
+                               const float* weight, const uint32_t* amax_bits, int64_t gc, int grid, int qmax,
+                               int rounding, int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
+                               void* stream);
+
+/*
+ * ntlb_ep_unpack_records for value records of val_dtype: row i < rows of
+ * values [rows, ldv] (val_dtype) is the payload of record inv[i], with the
+ * optional token index, slot, routing weight and source rank as there
+ * (recv_offsets HOST memory, needed only with src_rank).  H % 8 == 0,
+ * 16-byte aligned records and value rows.
+ */
+int ntlb_ep_unpack_values(const uint8_t* records, int64_t n, int64_t H, int val_dtype, const int32_t* inv,
+                          int64_t rows, const int64_t* recv_offsets, int ep_size, void* values, int64_t ldv,
+                          int32_t* token_idx, int32_t* slot_idx, int32_t* src_rank, float* weight, void* stream);
+
+/*
+ * ntlb_ep_combine for value records of val_dtype: each returned value
+ * rounded to out_dtype (the reference's recv_back_features.to(tokens.dtype),
+ * moe.py:998-999), times its routing weight rounded to out_dtype, the
+ * products summed in fp32 in ascending expert id per token and the sum
+ * rounded once; capacity drops add nothing.  Shapes as ntlb_ep_combine.
+ */
+int ntlb_ep_combine_values(const uint8_t* records, int64_t n, int64_t H, int val_dtype, const void* topk_idx,
+                           int idx_dtype, const void* topk_w, int w_dtype, int64_t T, int64_t K, void* out,
+                           int out_dtype, int64_t ldo, int32_t* slot_map, void* stream);
 /*
  * Single-rank combine of the local experts' outputs (moe.py:1087-1088,
  * LocalRoutedMoE :489-490): out[t] starts at zero and, for token t's slots in
@@ -788,6 +858,9 @@ int ntlb_ep_combine(const uint8_t* records, int64_t n, int64_t H, const void* to
  * or int64 (1) and topk_w (w_dtype) [T, K] contiguous, 1 <= K <= 32, out
  * [T, ldo].
  */
+int ntlb_moe_combine_rows(const void* y, int64_t ldy, int64_t n, const int32_t* pos, const void* topk_idx,
+                          int idx_dtype, const void* topk_w, int w_dtype, int64_t T, int64_t K, int64_t H, void* out,
+                          int out_dtype, int64_t ldo, void* stream);
 /*
  * Capacity keep of the single-rank expert loop (moe.py:1077-1081,
  * LocalRoutedMoE :482-486: keep_rel = torch.topk(sort_weights, k=capacity,
@@ -828,6 +901,9 @@ int ntlb_moe_combine_backward(const void* d_out, int64_t ldo, const void* y, int
  * [R, 2I] in the interleaved column order of the fused gate/up GEMM (h column
  * j: gate column 256*(j/128) + j%128, up column that + 128); I % 128 == 0.
  */
+int ntlb_swiglu_backward(const uint16_t* dh, int64_t lddh, const uint16_t* gu, int64_t ldgu, int64_t R, int64_t I,
+                         uint16_t* dgu, int64_t lddgu, void* stream);
+
 /*
  * The token gradient of the single-rank loop's gather `tokens[token_indices]`
  * (moe.py:1086, :488) under autograd: out[t] = the rows dx[pos[t*K + s]] of
@@ -839,18 +915,6 @@ int ntlb_moe_combine_backward(const void* d_out, int64_t ldo, const void* y, int
  */
 int ntlb_moe_token_grad(const void* dx, int64_t lddx, int dtype, const int32_t* pos, const void* topk_idx,
                         int idx_dtype, int64_t T, int64_t K, int64_t H, void* out, int64_t ldo, void* stream);
-
-int ntlb_swiglu_backward(const uint16_t* dh, int64_t lddh, const uint16_t* gu, int64_t ldgu, int64_t R, int64_t I,
-                         uint16_t* dgu, int64_t lddgu, void* stream);
-
-int ntlb_moe_combine_rows(const void* y, int64_t ldy, int64_t n, const int32_t* pos, const void* topk_idx,
-                          int idx_dtype, const void* topk_w, int w_dtype, int64_t T, int64_t K, int64_t H, void* out,
-                          int out_dtype, int64_t ldo, void* stream);
-
-int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const int32_t* inv, int64_t rows,
-                           const int64_t* recv_offsets, int ep_size, uint8_t* codes, int64_t ldc, float* scales,
-                           int64_t s_row, int64_t s_col, int32_t* nan_rows, int32_t* token_idx, int32_t* slot_idx,
-                           int32_t* src_rank, float* weight, void* stream);
 
 #ifdef __cplusplus
 }

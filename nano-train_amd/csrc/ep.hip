@@ -160,7 +160,9 @@ struct RankOffsets {
 // scales[i*s_row + t*s_col]), NaN flag and metadata, and the source rank of
 // the record (the s with ro.v[s] <= inv[i] < ro.v[s+1]).  A wave per row; the
 // vector path issues up to eight 16-byte loads per lane before their stores.
-template <bool VEC>
+// TILES: a code record (Hp code bytes, then tile scales); otherwise a value
+// record (Hp payload bytes, no scales)
+template <bool VEC, bool TILES = true>
 __global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* __restrict__ rec, int64_t n, int64_t rows,
                                                         int64_t Hp,
                                                         int64_t R, int64_t s_off, int64_t m_off,
@@ -175,12 +177,12 @@ __global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* __restric
   const int64_t src = min<int64_t>(max<int32_t>(inv[i], 0), n - 1);  // a record index, clamped into the n records
   const uint8_t* r = rec + src * R;
   uint8_t* out = codes + i * ldc;
-  const int64_t nt = Hp >> 7;
+  const int64_t nt = TILES ? Hp >> 7 : 0;
   const float* sc = reinterpret_cast<const float*>(r + s_off);
   const int32_t* m = reinterpret_cast<const int32_t*>(r + m_off);
   // lane l < nt takes tile scale l, lanes 0-4 the metadata words (token, slot,
   // local expert, NaN flag, weight); both loads clamped into the record
-  float s_l = sc[min<int64_t>(lane, nt - 1)];
+  float s_l = TILES ? sc[min<int64_t>(lane, nt - 1)] : 0.f;
   int32_t m_l = m[min(lane, 7)];
   if constexpr (VEC) {
     constexpr int U = 8;
@@ -207,8 +209,10 @@ __global__ void __launch_bounds__(256) ep_gather_kernel(const uint8_t* __restric
   } else {
     for (int64_t c = lane; c < Hp; c += 64) out[c] = r[c];
   }
-  if (lane < nt) scales[i * s_row + lane * s_col] = s_l;
-  for (int64_t t = 64 + lane; t < nt; t += 64) scales[i * s_row + t * s_col] = sc[t];
+  if constexpr (TILES) {
+    if (lane < nt) scales[i * s_row + lane * s_col] = s_l;
+    for (int64_t t = 64 + lane; t < nt; t += 64) scales[i * s_row + t * s_col] = sc[t];
+  }
   if (lane == 0 && token_idx) token_idx[i] = m_l;
   if (lane == 1 && slot_idx) slot_idx[i] = m_l;
   if (lane == 3 && nan_rows) nan_rows[i] = m_l;
@@ -521,6 +525,85 @@ __global__ void __launch_bounds__(COMBINE_ROWS_THREADS) moe_combine_rows_kernel(
   }
 }
 
+// The combine over records that carry the reference's wire values instead of
+// codes (the channel comm-quant: moe.py:112-121 applied to the send-back
+// buffer, whose per-column scales a record's tile scales cannot hold): the
+// payload is a row of VAL_DT values at the record's start, the metadata at
+// R - 32.  The sum is ep_combine_kernel's: per token, the kept slots in
+// ascending expert id, each value in the output dtype times its weight
+// rounded to it, added in fp32, rounded once.
+template <int VAL_DT, int OUT_DT>
+__global__ void __launch_bounds__(256) ep_combine_values_kernel(const uint8_t* rec, int64_t n, int64_t R, int64_t H,
+                                                                const int32_t* slot_map, const void* topk_idx,
+                                                                int idx_dt, const void* topk_w, int w_dt, int K,
+                                                                void* out, int64_t ldo, int vec_out) {
+#pragma clang fp contract(off)
+  __shared__ int64_t s_e[EP_COMBINE_MAX_K];
+  __shared__ int32_t s_rec[EP_COMBINE_MAX_K];
+  __shared__ float s_w[EP_COMBINE_MAX_K];
+  const int64_t t = blockIdx.x;
+  const int k = threadIdx.x;
+  if (k < K) {
+    const int64_t a = t * K + k;
+    s_e[k] = idx_dt == 1 ? reinterpret_cast<const int64_t*>(topk_idx)[a]
+                         : (int64_t) reinterpret_cast<const int32_t*>(topk_idx)[a];
+  }
+  __syncthreads();
+  if (k < K) {
+    const int64_t ek = s_e[k];
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += (s_e[j] < ek || (s_e[j] == ek && j < k)) ? 1 : 0;
+    s_rec[rank] = slot_map[t * K + k];
+    s_w[rank] = load_elem(topk_w, w_dt, t * K + k);
+  }
+  __syncthreads();
+  constexpr int esz = VAL_DT == DT_F32 ? 4 : 2;
+  for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < H; c0 += 256 * 8) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; n > 0 && j < K; ++j) {
+      if (s_rec[j] < 0) continue;  // dropped by a capacity limit: never returned
+      const uint8_t* rp = rec + (int64_t)s_rec[j] * R + c0 * esz;
+      float v[8];
+      if constexpr (VAL_DT == DT_F32) {
+        const uint4 a = *reinterpret_cast<const uint4*>(rp), b = *reinterpret_cast<const uint4*>(rp + 16);
+        const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(u[i]);
+      } else {
+        const uint4 a = *reinterpret_cast<const uint4*>(rp);
+        const uint32_t u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t hb = (u[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+          v[i] = VAL_DT == DT_BF16 ? bf16_bits_to_f32(hb) : __half2float(__ushort_as_half((unsigned short)hb));
+        }
+      }
+      round8<OUT_DT>(v);  // the received row in the output dtype
+      const float w = s_w[j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = v[i] * w;
+      round8<OUT_DT>(v);  // the product, a tensor op of the output dtype
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] = acc[i] + v[i];
+    }
+    if constexpr (OUT_DT == DT_BF16) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pk[i] = bf16x2_bits(acc[2 * i], acc[2 * i + 1]);
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + t * ldo + c0;
+      if (vec_out) {
+        store16_nt(o, pk);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (uint16_t)(pk[i >> 1] >> (16 * (i & 1)));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) store_elem(out, OUT_DT, t * ldo + c0 + i, acc[i]);
+    }
+  }
+}
+
 }  // namespace ntlb
 
 using namespace ntlb;
@@ -593,6 +676,73 @@ extern "C" int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t
   else
     ep_gather_kernel<false><<<grd, blk, 0, st>>>(records, n, rows, Hp, R, s_off, m_off, inv, ro, ep_size, codes, ldc, scales,
                                                   s_row, s_col, nan_rows, token_idx, slot_idx, src_rank, weight);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_ep_unpack_values(const uint8_t* records, int64_t n, int64_t H, int val_dtype, const int32_t* inv,
+                                     int64_t rows, const int64_t* recv_offsets, int ep_size, void* values, int64_t ldv,
+                                     int32_t* token_idx, int32_t* slot_idx, int32_t* src_rank, float* weight,
+                                     void* stream) {
+  const char* fn = "ntlb_ep_unpack_values";
+  if (n < 0 || n > 0x7FFFFFFF || rows < 0 || (rows > 0 && n == 0) || H <= 0 || H % 8 != 0 || ldv < H ||
+      !valid_dtype(val_dtype))
+    return fail(NTLB_EINVAL, "%s: bad shape or dtype (0 <= n < 2^31, rows >= 0 with records to read, H %% 8 == 0, "
+                "ldv >= H)", fn);
+  RankOffsets ro{};
+  if (src_rank) {
+    if (!recv_offsets || ep_size < 1 || ep_size > EP_MAX_RANKS)
+      return fail(NTLB_EINVAL, "%s: src_rank needs recv_offsets and 1 <= ep_size <= %d", fn, EP_MAX_RANKS);
+    if (recv_offsets[0] != 0 || recv_offsets[ep_size] != n)
+      return fail(NTLB_EINVAL, "%s: recv_offsets must run from 0 to n", fn);
+    for (int s = 0; s <= ep_size; ++s) {
+      if (s > 0 && recv_offsets[s] < recv_offsets[s - 1])
+        return fail(NTLB_EINVAL, "%s: recv_offsets must not decrease", fn);
+      ro.v[s] = (int32_t)recv_offsets[s];
+    }
+  }
+  if (rows == 0) return NTLB_OK;
+  if (!records || !inv || !values) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  const int64_t esz = dtype_size(val_dtype);
+  if (!aligned(records, 16) || !aligned(values, 16) || (ldv * esz) % 16)
+    return fail(NTLB_EINVAL, "%s: records and value rows must be 16-byte aligned", fn);
+  const int64_t R = ntlb_ep_value_record_bytes(H, val_dtype);
+  dim3 grd((unsigned)cdiv(rows, 4)), blk(256);
+  ep_gather_kernel<true, false><<<grd, blk, 0, as_stream(stream)>>>(
+      records, n, rows, H * esz, R, 0, R - 32, inv, ro, ep_size, reinterpret_cast<uint8_t*>(values), ldv * esz,
+      nullptr, 0, 0, nullptr, token_idx, slot_idx, src_rank, weight);
+  return check_launch(fn);
+}
+
+extern "C" int ntlb_ep_combine_values(const uint8_t* records, int64_t n, int64_t H, int val_dtype,
+                                      const void* topk_idx, int idx_dtype, const void* topk_w, int w_dtype, int64_t T,
+                                      int64_t K, void* out, int out_dtype, int64_t ldo, int32_t* slot_map,
+                                      void* stream) {
+  const char* fn = "ntlb_ep_combine_values";
+  if (n < 0 || n > 0x7FFFFFFF || T < 0 || K < 1 || K > EP_COMBINE_MAX_K || H <= 0 || H % 8 != 0 || ldo < H)
+    return fail(NTLB_EINVAL, "%s: bad shape (H %% 8 == 0, 1 <= K <= %d, ldo >= H)", fn, EP_COMBINE_MAX_K);
+  if ((idx_dtype != 0 && idx_dtype != 1) || !valid_dtype(w_dtype) || !valid_dtype(out_dtype) || !valid_dtype(val_dtype))
+    return fail(NTLB_EINVAL, "%s: bad dtype", fn);
+  if (T == 0) return NTLB_OK;
+  if (!topk_idx || !topk_w || !out || !slot_map || (n > 0 && !records)) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  if (n > 0 && !aligned(records, 16)) return fail(NTLB_EINVAL, "%s: records must be 16-byte aligned", fn);
+  if (T * K > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
+  const int64_t R = ntlb_ep_value_record_bytes(H, val_dtype);
+  hipStream_t st = as_stream(stream);
+  ep_slot_fill_kernel<<<(unsigned)cdiv(T * K, 256), 256, 0, st>>>(slot_map, T * K);
+  if (n > 0)
+    ep_slot_scatter_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(records, n, R, R - 32, T, (int)K, slot_map);
+  const int vec = aligned(out, 16) && ldo % 8 == 0;
+  auto launch = [&](auto valc, auto outc) {
+    ep_combine_values_kernel<decltype(valc)::value, decltype(outc)::value><<<(unsigned)T, 256, 0, st>>>(
+        records, n, R, H, slot_map, topk_idx, idx_dtype, topk_w, w_dtype, (int)K, out, ldo, vec);
+  };
+  using B = std::integral_constant<int, DT_BF16>;
+  using F = std::integral_constant<int, DT_F32>;
+  using Hh = std::integral_constant<int, DT_F16>;
+  auto by_out = [&](auto valc) {
+    if (out_dtype == NTLB_BF16) launch(valc, B()); else if (out_dtype == NTLB_F32) launch(valc, F()); else launch(valc, Hh());
+  };
+  if (val_dtype == NTLB_BF16) by_out(B()); else if (val_dtype == NTLB_F32) by_out(F()); else by_out(Hh());
   return check_launch(fn);
 }
 

@@ -1944,6 +1944,68 @@ __global__ void __launch_bounds__(256) ep_pack_grouped_kernel(QuantArgs a, const
   }
 }
 
+// Value records: the reference's wire values themselves, as
+// _comm_quant_dequant (moe.py:79-143) leaves them in the send buffer of
+// _dispatch_tokens (moe.py:805-814) and _combine_remote_outputs
+// (moe.py:983-990).  Any column grouping, including one scale per column
+// (channel granularity, moe.py:112-121), whose scales a record's tile scales
+// cannot carry.  Thread (x, t) owns the 8-column chunk blockIdx.x*256 + t of
+// input rows blockIdx.y, blockIdx.y + gridDim.y, ...; its group scales are
+// read once (one row group spans every row).  Each element is quantized with
+// its group's scale (SR element index p*H + column of record p) and written
+// as tensor + (dq - tensor) in the input dtype, dq = q * scale rounded to it,
+// the expression comm_quant_ste_kernel evaluates; input row r goes to the
+// fan_k records fan_pos[r * fan_k + f] at byte p*R + 2 or 4 per column.
+template <int IN_DT, int GRID, bool SR>
+__global__ void __launch_bounds__(256) ep_pack_values_kernel(QuantArgs a, const uint32_t* amax_bits, int64_t gc,
+                                                             int64_t n_gc, uint8_t* rec, int64_t R) {
+#pragma clang fp contract(off)
+  const int64_t k0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (k0 >= a.K) return;  // K % 8 == 0: whole chunks
+  float sv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    sv[i] = scale_from_amax_bits(amax_bits[min<int64_t>((k0 + i) / gc, n_gc - 1)], a.qmaxf, a.scale_rule);
+  constexpr int64_t esz = IN_DT == DT_F32 ? 4 : 2;
+  for (int64_t r = blockIdx.y; r < a.R; r += gridDim.y) {
+    float v[8];
+    load8<IN_DT, true>(a.x, r * a.ldx, k0, a.K, v);
+    float o[8];
+    for (int64_t f = 0; f < a.fan_k; ++f) {
+      const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + f], 0), a.fan_rows - 1);
+      if (SR || f == 0) {  // round to nearest: one value for every copy
+        uint32_t rb[8];
+        sr_words<SR>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
+        float q[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) (void)quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = q[i] * sv[i];
+        round8_dtype<IN_DT>(o);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = o[i] - v[i];
+        round8_dtype<IN_DT>(o);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = v[i] + o[i];
+        round8_dtype<IN_DT>(o);
+      }
+      uint8_t* dst = rec + p * R + k0 * esz;  // 16-byte aligned: R % 16 == 0, k0 % 8 == 0
+      if constexpr (IN_DT == DT_BF16) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = (uint32_t)f32_to_bf16_bits(o[2 * i]) | ((uint32_t)f32_to_bf16_bits(o[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        *reinterpret_cast<uint4*>(dst) =
+            make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
+        *reinterpret_cast<uint4*>(dst + 16) =
+            make_uint4(__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]), __float_as_uint(o[7]));
+      }
+    }
+  }
+}
+
 // Shared by the dispatch and return packs: rows x [n_in, H] quantized into
 // records (codes, tile scales, NaN flag; the metadata kernels run first),
 // input row r going to the fan_k records fan_pos[r * fan_k + f].
@@ -2055,4 +2117,94 @@ extern "C" int ntlb_ep_pack_return(const void* x, int x_dtype, int64_t n, int64_
   if (rc) return rc;
   return ep_pack_payload(fn, x, x_dtype, n, H, ldx, pos, 1, n, amax_bits, gc, grid, qmax, rounding, scale_rule, seed,
                          offset, records, st);
+}
+
+extern "C" int64_t ntlb_ep_value_record_bytes(int64_t H, int dtype) {
+  if (H <= 0 || !valid_dtype(dtype)) return 0;
+  return (H * dtype_size(dtype) + 15) / 16 * 16 + 32;
+}
+
+// Value-record payload of rows x [n_in, H]: the metadata kernels run first.
+static int ep_pack_values_payload(const char* fn, const void* x, int x_dtype, int64_t n_in, int64_t H, int64_t ldx,
+                                  const int32_t* fan_pos, int64_t fan_k, int64_t n_rec, const uint32_t* amax_bits,
+                                  int64_t gc, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                  uint64_t offset, uint8_t* records, int64_t R, hipStream_t st) {
+  QuantArgs a = make_args(x, n_in, H, ldx, grid, qmax, scale_rule, seed, offset, nullptr, 0, nullptr, 0, 0, nullptr, 0,
+                          0, nullptr);
+  a.fan_pos = fan_pos;
+  a.fan_k = fan_k;
+  a.fan_rows = n_rec;
+  const int64_t n_gc = cdiv(H, gc);
+  const int64_t gx = cdiv(H / 8, 256);
+  dim3 grd((unsigned)gx, (unsigned)std::max<int64_t>(1, std::min<int64_t>(n_in, std::min<int64_t>(65535, 8192 / gx)))),
+      blk(256);
+  const bool sr = rounding == NTLB_ROUND_STOCHASTIC;
+  NTLB_DISPATCH_GRID_SR(grid, sr, {
+    if (x_dtype == NTLB_BF16)
+      ep_pack_values_kernel<DT_BF16, G_, S_><<<grd, blk, 0, st>>>(a, amax_bits, gc, n_gc, records, R);
+    else
+      ep_pack_values_kernel<DT_F32, G_, S_><<<grd, blk, 0, st>>>(a, amax_bits, gc, n_gc, records, R);
+  });
+  return check_launch(fn);
+}
+
+static int ep_check_values(const char* fn, const void* x, int x_dtype, int64_t H, int64_t ldx,
+                           const uint32_t* amax_bits, int64_t gc, const uint8_t* records) {
+  const bool vec = aligned(x, 16) && ((ldx * dtype_size(x_dtype)) % 16 == 0);
+  if (!(vec && H % 8 == 0 && (x_dtype == NTLB_BF16 || x_dtype == NTLB_F32) && aligned(records, 16) &&
+        cdiv(H / 8, 256) <= 65535))
+    return fail(NTLB_EUNSUPPORTED, "%s: needs bf16/fp32 rows, H %% 8 == 0, 16-byte aligned rows and records", fn);
+  if (!amax_bits || gc < 1) return fail(NTLB_EINVAL, "%s: needs the group amaxes and gc >= 1", fn);
+  if (cdiv(H, gc) >= ((int64_t)1 << 31)) return fail(NTLB_EUNSUPPORTED, "%s: 2^31 or more column groups", fn);
+  return NTLB_OK;
+}
+
+extern "C" int ntlb_ep_pack_values(const void* tokens, int x_dtype, int64_t T, int64_t H, int64_t ldt,
+                                   const int32_t* pos, const void* topk_idx, int idx_dtype, const void* topk_w,
+                                   int w_dtype, int64_t K, int64_t experts_per_rank, const uint32_t* amax_bits,
+                                   int64_t gc, int grid, int qmax, int rounding, int scale_rule, uint64_t seed,
+                                   uint64_t offset, uint8_t* records, void* stream) {
+  const char* fn = "ntlb_ep_pack_values";
+  if (K < 1 || experts_per_rank < 1 || T < 0 || (idx_dtype != 0 && idx_dtype != 1) || !valid_dtype(w_dtype))
+    return fail(NTLB_EINVAL, "%s: bad argument", fn);
+  const int64_t A = T * K;
+  if (A > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: more than 2^31 assignments", fn);
+  int rc = check_common(fn, tokens, x_dtype, T, H, ldt, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (A == 0 || H == 0) return NTLB_OK;
+  if (!pos || !topk_idx || !topk_w || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  rc = ep_check_values(fn, tokens, x_dtype, H, ldt, amax_bits, gc, records);
+  if (rc) return rc;
+  const int64_t R = ntlb_ep_value_record_bytes(H, x_dtype);
+  hipStream_t st = as_stream(stream);
+  ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, R - 32, A, pos, topk_idx, idx_dtype, topk_w,
+                                                          w_dtype, K, experts_per_rank);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  return ep_pack_values_payload(fn, tokens, x_dtype, T, H, ldt, pos, K, A, amax_bits, gc, grid, qmax, rounding,
+                                scale_rule, seed, offset, records, R, st);
+}
+
+extern "C" int ntlb_ep_pack_return_values(const void* x, int x_dtype, int64_t n, int64_t H, int64_t ldx,
+                                          const int32_t* pos, const int32_t* token_idx, const int32_t* slot_idx,
+                                          const int32_t* local_expert, const float* weight,
+                                          const uint32_t* amax_bits, int64_t gc, int grid, int qmax, int rounding,
+                                          int scale_rule, uint64_t seed, uint64_t offset, uint8_t* records,
+                                          void* stream) {
+  const char* fn = "ntlb_ep_pack_return_values";
+  if (n < 0 || n > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: need 0 <= n < 2^31", fn);
+  int rc = check_common(fn, x, x_dtype, n, H, ldx, grid, qmax, rounding, scale_rule, nullptr, 0, 0);
+  if (rc) return rc;
+  if (n == 0 || H == 0) return NTLB_OK;
+  if (!pos || !token_idx || !slot_idx || !records) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
+  rc = ep_check_values(fn, x, x_dtype, H, ldx, amax_bits, gc, records);
+  if (rc) return rc;
+  const int64_t R = ntlb_ep_value_record_bytes(H, x_dtype);
+  hipStream_t st = as_stream(stream);
+  ep_meta_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(records, R, R - 32, n, pos, token_idx, slot_idx,
+                                                               local_expert, weight);
+  rc = check_launch(fn);
+  if (rc) return rc;
+  return ep_pack_values_payload(fn, x, x_dtype, n, H, ldx, pos, 1, n, amax_bits, gc, grid, qmax, rounding, scale_rule,
+                                seed, offset, records, R, st);
 }

@@ -125,10 +125,18 @@ SIGNATURES = {
     "ntlb_moe_token_grad": [_P, _I64, _I32, _P, _P, _I32, _I64, _I64, _I64, _P, _I64, _P],
     "ntlb_swiglu_backward": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P],
     "ntlb_ep_unpack_records": [_P, _I64, _I64, _P, _I64, _P, _I32, _P, _I64, _P, _I64, _I64, _P, _P, _P, _P, _P, _P],
+    "ntlb_ep_value_record_bytes": [_I64, _I32],
+    "ntlb_ep_pack_values": [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P, _I32, _I64, _I64, _P, _I64, _I32, _I32,
+                            _I32, _I32, _U64, _U64, _P, _P],
+    "ntlb_ep_pack_return_values": [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _I32, _I32,
+                                   _U64, _U64, _P, _P],
+    "ntlb_ep_unpack_values": [_P, _I64, _I64, _I32, _P, _I64, _P, _I32, _P, _I64, _P, _P, _P, _P, _P],
+    "ntlb_ep_combine_values": [_P, _I64, _I64, _I32, _P, _I32, _P, _I32, _I64, _I64, _P, _I32, _I64, _P, _P],
 }
 
 # entry points that return a value instead of a status
 RESTYPES = {"ntlb_gemm_workspace_bytes": _I64, "ntlb_ep_record_bytes": _I64, "ntlb_colsum_workspace_bytes": _I64,
+            "ntlb_ep_value_record_bytes": _I64,
             "ntlb_gemm_lowbit_workspace_bytes": _I64, "ntlb_gemm_dq_workspace_bytes": _I64}
 
 _lib = None

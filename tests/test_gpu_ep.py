@@ -445,3 +445,231 @@ def test_combine_decodes_every_code(gpu_device, fmt, grid, out_dtype):
         want = O.round_bf16(want)
     want = np.float32(0.0) + want  # the sum starts from zero: -0 comes out as +0, as from index_add_ into zeros
     assert_bits_equal(out.float().cpu().numpy()[0], want, "decoded codes")
+
+
+def _value_payload(records: np.ndarray, H: int, dtype: torch.dtype):
+    """values (fp32), (token, slot, local expert, flag), weight, reserved of value records."""
+    from lowbit import ep
+
+    R, m_off = ep.value_record_layout(H, dtype)
+    rec = np.ascontiguousarray(records).reshape(-1, R)
+    esz = 2 if dtype == torch.bfloat16 else 4
+    raw = torch.from_numpy(rec[:, :H * esz].copy())
+    vals = raw.view(dtype).float().numpy() if len(rec) else np.zeros((0, H), np.float32)
+    meta = rec[:, m_off:m_off + 32].copy().view(np.int32)
+    return vals, meta[:, :4], meta[:, 4].copy().view(np.float32), meta[:, 5:]
+
+
+def _wire_values(rows: np.ndarray, gc: int, dtype: torch.dtype, rounding: str, seed: int, offset: int):
+    """The reference's wire value of a send buffer (moe.py:79-143): the
+    oracle's int-grid quantizer with one scale per gc columns over all rows
+    (amax checked before dividing), dq = q * scale in fp32, then tensor + (dq
+    - tensor) evaluated by torch on the CPU in the tensor's dtype."""
+    n, H = rows.shape
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    _, _, _, dq = O.quant_grouped(rows, max(n, 1), gc, grid=O.GRID_INT, rounding=rc,
+                                  scale_rule=O.SCALE_BEFORE_DIVIDE, seed=seed, offset=offset)
+    t = torch.from_numpy(rows).to(dtype)
+    d = torch.from_numpy(dq).to(dtype)
+    return (t + (d - t)).float().numpy()
+
+
+def _reference_channel_rn(rows: np.ndarray, dtype: torch.dtype):
+    """_comm_quant_dequant(granularity="channel", rounding "nearest") as the
+    reference's column loop forms it (moe.py:91-121), in torch on the CPU."""
+    tensor = torch.from_numpy(rows).to(dtype)
+    x = tensor.float()
+    cols = []
+    for c in range(x.shape[-1]):
+        block = x[..., c:c + 1]
+        scale = block.abs().amax()
+        scale = block.new_tensor(1.0) if (not torch.isfinite(scale) or scale <= 0) else scale / 127.0
+        cols.append(torch.clamp(torch.round(block / scale), min=-127, max=127) * scale)
+    dq = torch.cat(cols, dim=-1).to(dtype)
+    return (tensor + (dq - tensor)).float().numpy()
+
+
+@pytest.mark.parametrize("granularity", ["channel", "tile_1x128", "tensor"])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H", [1024, 200])
+def test_value_records_hold_the_reference_wire_values(gpu_device, granularity, rounding, dtype, H):
+    """Value records (the only wire of channel comm-quant): every record's
+    payload bit-exact against the reference's wire value of the send buffer
+    (oracle quantizer, the straight-through expression in torch on the CPU)
+    and against comm_quant_dequant of the send buffer on the GPU; metadata as
+    in code records.  Round to nearest with channel scales also against the
+    reference's own column loop restated in torch.  A NaN element makes its
+    column's (or strip's, or the tensor's) scale 1."""
+    from lowbit import ep, moe
+
+    T, K, epr, ep_size = 96, 4, 3, 4
+    x = seeded((T, H), seed=20261400, outliers=0.01, dtype=dtype).to(gpu_device)
+    x[11, 3] = float("nan")
+    x[20, 5] = 0.0
+    x[:, 7] = 0.0  # an all-zero column: scale 1
+    idx, w = _routing(T, K, epr * ep_size, 20261401)
+    send = ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=epr, ep_size=ep_size,
+                            granularity=granularity, wire="values", rounding=rounding, seed=77, offset=5)
+    order, counts = O.ep_send_order(idx.numpy(), epr, ep_size)
+    send_t = x[torch.from_numpy(order // K).to(gpu_device)]
+    gpu_wire = moe.comm_quant_dequant(send_t, granularity=granularity, rounding_mode=rounding, seed=77, offset=5)
+    torch.cuda.synchronize()
+    assert send.value_dtype == dtype and send.counts.cpu().numpy().tolist() == counts.tolist()
+    vals, meta, weight, reserved = _value_payload(send.records.cpu().numpy(), H, dtype)
+    send_rows = to_np32(x)[order // K]
+    gc = {"channel": 1, "tile_1x128": 128, "tensor": H}[granularity]
+    want = _wire_values(send_rows, gc, dtype, rounding, 77, 5)
+    assert_bits_equal(vals, want, "record values (oracle)")
+    assert_bits_equal(vals, to_np32(gpu_wire), "record values (comm_quant_dequant)")
+    if granularity == "channel" and rounding == "nearest" and H == 200:
+        assert_bits_equal(vals, _reference_channel_rn(send_rows, dtype), "record values (reference column loop)")
+    assert np.array_equal(meta[:, 0], order // K) and np.array_equal(meta[:, 1], order % K)
+    assert np.array_equal(meta[:, 2], idx.numpy().reshape(-1)[order] % epr) and not meta[:, 3].any()
+    assert_bits_equal(weight, w.numpy().reshape(-1)[order].astype(np.float32), "record weights")
+    assert not reserved.any()
+
+
+def test_value_records_reject_what_they_cannot_carry(gpu_device):
+    from lowbit import ep
+
+    x = seeded((8, 256), seed=20261402).to(gpu_device)
+    idx, w = _routing(8, 2, 4, 20261403)
+    with pytest.raises(ValueError, match="channel"):
+        ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=2, ep_size=2,
+                         granularity="channel", wire="codes")
+    with pytest.raises(ValueError, match="granularity"):
+        ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=2, ep_size=2, wire="values")
+
+
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+@pytest.mark.parametrize("capacity", [0, 7])
+def test_channel_value_records_dispatch_return_and_combine(gpu_device, rounding, capacity):
+    """The channel comm-quant end to end between 3 emulated ranks: dispatch
+    value records, the receiver's rows (expert order, metadata against the
+    oracle's ep_dispatch, each row the sender's wire value), a capacity drop,
+    synthetic expert outputs sent back as value records (against the
+    reference's wire value of the send-back buffer in its order), and the
+    combine bit-exact against index_add_ on the CPU of the returned rows in
+    the tokens' dtype times their weights, and against the oracle."""
+    from lowbit import ep
+
+    ep_size, epr, H, K = 3, 2, 384, 3
+    tokens = [50, 0, 37]
+    xs, idxs, ws, sends = [], [], [], []
+    for r, T in enumerate(tokens):
+        x = seeded((T, H), seed=20261410 + 10 * r, heavy_channels=True).to(gpu_device)
+        idx, w = _routing(T, K, epr * ep_size, 20261411 + 10 * r)
+        w = w.to(torch.bfloat16)
+        xs.append(x), idxs.append(idx), ws.append(w)
+        sends.append(ep.pack_dispatch(x, idx.to(gpu_device), w.to(gpu_device), experts_per_rank=epr,
+                                      ep_size=ep_size, granularity="channel", rounding=rounding, seed=31, offset=r))
+    torch.cuda.synchronize()
+    # each sender's wire values by assignment index
+    wire = []
+    for s in range(ep_size):
+        by_a = np.zeros((tokens[s] * K, H), np.float32)
+        if tokens[s]:
+            order, _ = O.ep_send_order(idxs[s].numpy(), epr, ep_size)
+            by_a[order] = _wire_values(to_np32(xs[s])[order // K], 1, torch.bfloat16, rounding, 31, s)
+        wire.append(by_a)
+    ref = O.ep_dispatch([i.numpy() for i in idxs], [w.float().numpy() for w in ws], epr, ep_size)
+    back = []
+    for r in range(ep_size):
+        parts, counts = [], []
+        for s in range(ep_size):
+            c = sends[s].counts.cpu().tolist()
+            start = sum(c[:r])
+            parts.append(sends[s].records[start:start + c[r]])
+            counts.append(c[r])
+        records = torch.cat(parts)
+        rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr, value_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        want = ref[r]
+        order = O.ep_expert_order(want["local_expert"], epr)
+        assert rows.q is None and rows.values.dtype == torch.bfloat16
+        assert np.array_equal(rows.order.cpu().numpy(), order), "expert order"
+        for key, got in (("src_rank", rows.src_rank), ("token_idx", rows.token_idx), ("slot_idx", rows.slot_idx)):
+            assert np.array_equal(got.cpu().numpy(), want[key][order]), key
+        exp_vals = np.stack([wire[s][a] for s, a in zip(want["src_rank"][order], want["src_row"][order])]) \
+            if len(order) else np.zeros((0, H), np.float32)
+        assert_bits_equal(to_np32(rows.values), exp_vals, "received rows")
+        if capacity:
+            korder, kept = ep.capacity_order(rows, capacity)
+            rows = ep.unpack_dispatch(records, counts, H=H, local_experts=epr, order=korder, order_counts=kept,
+                                      value_dtype=torch.bfloat16)
+            assert_bits_equal(to_np32(rows.values), _value_payload(records.cpu().numpy(), H, torch.bfloat16)[0][
+                korder.cpu().numpy()], "kept rows")
+        out_rows = seeded((rows.token_idx.numel(), H), seed=20261490 + r, std=2.0).to(gpu_device)
+        sb = ep.pack_return(out_rows, rows, ep_size=ep_size, granularity="channel", rounding=rounding, seed=9,
+                            offset=r)
+        torch.cuda.synchronize()
+        src = rows.src_rank.cpu().numpy()
+        ret_order = np.concatenate([np.nonzero(src == s)[0] for s in range(ep_size)]) if len(src) else \
+            np.zeros(0, np.int64)
+        vals, meta, _, _ = _value_payload(sb.records.cpu().numpy(), H, torch.bfloat16)
+        if len(ret_order):
+            assert_bits_equal(vals, _wire_values(to_np32(out_rows)[ret_order], 1, torch.bfloat16, rounding, 9, r),
+                              "return values")
+        assert np.array_equal(meta[:, 0], rows.token_idx.cpu().numpy()[ret_order]), "token index"
+        assert np.array_equal(meta[:, 1], rows.slot_idx.cpu().numpy()[ret_order]), "slot"
+        back.append((sb.records, sb.counts.cpu().tolist()))
+    for s in range(ep_size):
+        parts = []
+        for r in range(ep_size):
+            rec, cnt = back[r]
+            start = sum(cnt[:s])
+            parts.append(rec[start:start + cnt[s]])
+        got_rec = torch.cat(parts)
+        T = tokens[s]
+        out = ep.combine(got_rec, idxs[s].to(gpu_device), ws[s].to(gpu_device), H=H, value_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        assert out.shape == (T, H) and out.dtype == torch.bfloat16
+        feat, meta, _, _ = _value_payload(got_rec.cpu().numpy(), H, torch.bfloat16)
+        tok = torch.from_numpy(meta[:, 0].astype(np.int64))
+        slot = torch.from_numpy(meta[:, 1].astype(np.int64))
+        want = torch.zeros((T, H), dtype=torch.bfloat16)
+        if len(tok):
+            want.index_add_(0, tok, torch.from_numpy(feat).to(torch.bfloat16) * ws[s][tok, slot].unsqueeze(-1))
+        assert_bits_equal(out.float().cpu().numpy(), want.float().numpy(), "combined tokens")
+        if T:
+            assert_bits_equal(out.float().cpu().numpy(),
+                              O.ep_combine(feat, meta[:, 0], meta[:, 1], idxs[s].numpy(), ws[s].float().numpy(), T),
+                              "combined tokens (oracle)")
+
+
+@pytest.mark.parametrize("val_dtype,out_dtype", [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                                 (torch.float32, torch.float32)])
+def test_value_combine_rounds_each_value_to_the_output_dtype(gpu_device, val_dtype, out_dtype):
+    """fp32 values combined into bf16 round to bf16 first (the reference's
+    .to(tokens.dtype) after the exchange), then the product with the weight;
+    bf16 values into fp32 are exact.  Against index_add_ on the CPU."""
+    from lowbit import ep
+
+    T, K, H = 9, 3, 256
+    R, m_off = ep.value_record_layout(H, val_dtype)
+    g = torch.Generator().manual_seed(20261420)
+    idx = torch.stack([torch.randperm(8, generator=g)[:K] for _ in range(T)])
+    w = torch.rand((T, K), generator=g).to(out_dtype)
+    n = T * K - 2  # the last two assignments dropped
+    vals = (torch.randn((n, H), generator=g) * 3).to(val_dtype)
+    rec = np.zeros((n, R), dtype=np.uint8)
+    esz = 2 if val_dtype == torch.bfloat16 else 4
+    rec[:, :H * esz] = vals.view(torch.uint8).numpy().reshape(n, H * esz)
+    perm = torch.randperm(n, generator=g).numpy()  # arrival order other than the assignment order
+    a = np.arange(n)[perm]
+    meta = np.zeros((n, 8), np.int32)
+    meta[:, 0], meta[:, 1] = a // K, a % K
+    rec[:, m_off:] = meta.view(np.uint8).reshape(n, 32)
+    out = ep.combine(torch.from_numpy(rec).to(gpu_device), idx.to(gpu_device), w.to(gpu_device), H=H,
+                     out_dtype=out_dtype, value_dtype=val_dtype)
+    torch.cuda.synchronize()
+    feat = vals.to(out_dtype)
+    ref = torch.zeros((T, H), dtype=out_dtype)
+    # index_add_ over the rows in ascending expert id per token: the CPU order for one token
+    tok = torch.from_numpy(meta[:, 0].astype(np.int64))
+    slot = torch.from_numpy(meta[:, 1].astype(np.int64))
+    order = np.lexsort((idx.numpy()[meta[:, 0], meta[:, 1]], meta[:, 0]))
+    o = torch.from_numpy(order)
+    ref.index_add_(0, tok[o], feat[o] * w[tok[o], slot[o]].unsqueeze(-1))
+    assert_bits_equal(out.float().cpu().numpy(), ref.float().numpy(), "combined values")
