@@ -788,11 +788,14 @@ int ntlb_ep_unpack_records(const uint8_t* records, int64_t n, int64_t H, const i
  * rounded to the dtype.  This carries any column grouping of the scales,
  * including one per column (channel granularity, moe.py:112-121), which a
  * code record's tile scales cannot, and moves 2 (bf16) or 4 bytes per value,
- * as the reference's own exchange does.  Layout:
- *   [0, P)          the H values, P = round_up(H * dtype size, 16)
- *   [P, P + 32)     the metadata of a code record (token, slot, local expert,
+ * as the reference's own exchange does.  Layout, in whole 128-byte lines so
+ * that every payload starts on one:
+ *   [0, P)          the H values, P = H * dtype size
+ *   [P, R - 32)     zero padding
+ *   [R - 32, R)     the metadata of a code record (token, slot, local expert,
  *                   0, fp32 weight, 3 reserved)
- * ntlb_ep_value_record_bytes(H, dtype) = P + 32 (0 for H <= 0 or a bad dtype).
+ * ntlb_ep_value_record_bytes(H, dtype) = R = round_up(P + 32, 128) (0 for H <=
+ * 0 or a bad dtype).
  */
 int64_t ntlb_ep_value_record_bytes(int64_t H, int dtype);
 

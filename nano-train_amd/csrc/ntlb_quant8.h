@@ -84,6 +84,71 @@ __device__ __forceinline__ bool fast_div_ok(uint32_t m) {
   return m >= (SR ? 0x30000000u : 0x1A000000u) && m <= 0x7B800000u;
 }
 
+// The codes (and, with DQ, the values q as the reference holds them) of N
+// quotients x/s already clamped to [-qmax, qmax]: the int grid rounds them
+// (to nearest, or stochastically with the bits rb), e4m3 converts them in
+// hardware.
+template <int GRID, bool SR, bool DQ, int N>
+__device__ __forceinline__ void codes_from_quotients(const float (&vq)[N], const uint32_t (&rb)[N], float qmaxf,
+                                                     uint32_t& lo, uint32_t& hi, float (&q)[N]) {
+#pragma clang fp contract(off)
+  if constexpr (GRID == GRID_INT) {
+    uint32_t c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      float t;
+      if constexpr (SR) {
+        // floor(v + u) for v >= 0 and ceil(v - u) = -floor(|v| + u) below
+        // (round to nearest is symmetric), so one floor, negated for
+        // v < 0 (te_backend.py:61-65); v = -0 counts as v >= 0 there and
+        // gives +0, so the sign comes from the comparison, not from v.
+        // The reference clamps after rounding (:102-106): at the clamp,
+        // qmax + u rounds to qmax + 1 in fp32 when u >= 1 - 2^-18
+        const float uu = sr_uniform(rb[i]);
+        const float w = __builtin_floorf(__builtin_fabsf(vq[i]) + uu);
+        t = vq[i] >= 0.0f ? w : -w;
+        t = __builtin_amdgcn_fmed3f(t, -qmaxf, qmaxf);
+      } else {
+        t = __builtin_rintf(vq[i]);
+      }
+      q[i] = t;
+      c[i] = (uint32_t)(int32_t)t & 0xFFu;
+    }
+    lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
+    hi = N == 8 ? (c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)) : 0u;
+  } else {
+    uint32_t c[8];
+    hi = 0;
+    if constexpr (!SR) {
+      lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[0], vq[1], 0, false);
+      lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[2], vq[3], (int)lo, true);
+      if constexpr (N == 8) {
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4 % N], vq[5 % N], 0, false);
+        hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[6 % N], vq[7 % N], (int)hi, true);
+      }
+    } else {
+      // the hardware stochastic convert, whose rounding is e4m3_sr's (the
+      // clamped quotients are finite and at most 448)
+      lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[0], (int)rb[0], 0, 0);
+      lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[1], (int)rb[1], (int)lo, 1);
+      lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[2], (int)rb[2], (int)lo, 2);
+      lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[3], (int)rb[3], (int)lo, 3);
+      if constexpr (N == 8) {
+        hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[4 % N], (int)rb[4 % N], 0, 0);
+        hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[5 % N], (int)rb[5 % N], (int)hi, 1);
+        hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[6 % N], (int)rb[6 % N], (int)hi, 2);
+        hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[7 % N], (int)rb[7 % N], (int)hi, 3);
+      }
+    }
+    c[0] = lo & 0xFF; c[1] = (lo >> 8) & 0xFF; c[2] = (lo >> 16) & 0xFF; c[3] = lo >> 24;
+    c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
+    if constexpr (DQ) {
+#pragma unroll
+      for (int i = 0; i < N; ++i) q[i] = e4m3_to_f32(c[i]);
+    }
+  }
+}
+
 // rs is 1/s (IEEE, correctly rounded) wherever fast_div_ok(m) holds; it is
 // not read otherwise.
 template <int GRID, bool SR, bool DQ, int N>
@@ -117,63 +182,29 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[N], uint32_t m, 
         vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
       }
     }
-    if constexpr (GRID == GRID_INT) {
-      uint32_t c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-      for (int i = 0; i < N; ++i) {
-        float t;
-        if constexpr (SR) {
-          // floor(v + u) for v >= 0 and ceil(v - u) = -floor(|v| + u) below
-          // (round to nearest is symmetric), so one floor, negated for
-          // v < 0 (te_backend.py:61-65); v = -0 counts as v >= 0 there and
-          // gives +0, so the sign comes from the comparison, not from v.
-          // The reference clamps after rounding (:102-106): at the clamp,
-          // qmax + u rounds to qmax + 1 in fp32 when u >= 1 - 2^-18
-          const float uu = sr_uniform(rb[i]);
-          const float w = __builtin_floorf(__builtin_fabsf(vq[i]) + uu);
-          t = vq[i] >= 0.0f ? w : -w;
-          t = __builtin_amdgcn_fmed3f(t, -qmaxf, qmaxf);
-        } else {
-          t = __builtin_rintf(vq[i]);
-        }
-        q[i] = t;
-        c[i] = (uint32_t)(int32_t)t & 0xFFu;
-      }
-      lo = c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24);
-      hi = N == 8 ? (c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24)) : 0u;
-    } else {
-      uint32_t c[8];
-      hi = 0;
-      if constexpr (!SR) {
-        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[0], vq[1], 0, false);
-        lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[2], vq[3], (int)lo, true);
-        if constexpr (N == 8) {
-          hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[4 % N], vq[5 % N], 0, false);
-          hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(vq[6 % N], vq[7 % N], (int)hi, true);
-        }
-      } else {
-        // the hardware stochastic convert, whose rounding is e4m3_sr's (the
-        // clamped quotients are finite and at most 448)
-        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[0], (int)rb[0], 0, 0);
-        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[1], (int)rb[1], (int)lo, 1);
-        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[2], (int)rb[2], (int)lo, 2);
-        lo = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[3], (int)rb[3], (int)lo, 3);
-        if constexpr (N == 8) {
-          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[4 % N], (int)rb[4 % N], 0, 0);
-          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[5 % N], (int)rb[5 % N], (int)hi, 1);
-          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[6 % N], (int)rb[6 % N], (int)hi, 2);
-          hi = (uint32_t)__builtin_amdgcn_cvt_sr_fp8_f32(vq[7 % N], (int)rb[7 % N], (int)hi, 3);
-        }
-      }
-      c[0] = lo & 0xFF; c[1] = (lo >> 8) & 0xFF; c[2] = (lo >> 16) & 0xFF; c[3] = lo >> 24;
-      c[4] = hi & 0xFF; c[5] = (hi >> 8) & 0xFF; c[6] = (hi >> 16) & 0xFF; c[7] = hi >> 24;
-      if constexpr (DQ) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) q[i] = e4m3_to_f32(c[i]);
-      }
-    }
+    codes_from_quotients<GRID, SR, DQ, N>(vq, rb, qmaxf, lo, hi, q);
   }
   return false;
+}
+
+// Eight values with a scale each (s[i], from amax bits that all pass
+// fast_div_ok, rs[i] = 1/s[i] correctly rounded): the fast exact division of
+// quant8_tile_rs element by element.  The amax bits exclude NaN and
+// infinity, so no NaN reaches the clamp.
+template <int GRID, bool SR, bool DQ>
+__device__ __forceinline__ void quant8_cols_rs(const float (&v)[8], const float (&s)[8], const float (&rs)[8],
+                                               float qmaxf, const uint32_t (&rb)[8], uint32_t& lo, uint32_t& hi,
+                                               float (&q)[8]) {
+#pragma clang fp contract(off)
+  float vq[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = v[i] * rs[i];
+    const float e = __builtin_fmaf(-y, s[i], v[i]);
+    const float z = __builtin_copysignf(__builtin_fmaf(e, rs[i], y), v[i]);
+    vq[i] = __builtin_amdgcn_fmed3f(z, -qmaxf, qmaxf);
+  }
+  codes_from_quotients<GRID, SR, DQ, 8>(vq, rb, qmaxf, lo, hi, q);
 }
 
 template <int GRID, bool SR, bool DQ>

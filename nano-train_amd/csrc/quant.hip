@@ -633,6 +633,57 @@ __global__ void __launch_bounds__(256) amax_grouped_kernel(const void* x, int64_
   flush(cur_g);
 }
 
+// Group maxima for groups narrower than 8 columns (channel granularity: one
+// per column).  amax_grouped_kernel's threads own distinct columns, so each
+// of its workgroups issues one global atomic per column, and a 16-row
+// workgroup pays as many atomics as loads (the c4 dispatch rows, 4096 x
+// 7168: 1.8 million atomics on 7168 addresses, 72 us).  Here a workgroup
+// covers 512 columns and one row block of a single row group; its four waves
+// take every fourth row of the block with four rows' loads in flight, and the
+// four partial maxima of each column meet in LDS, so the workgroup issues one
+// atomic per column for four times the rows.  blockIdx.y = row group * bpg +
+// block within the group.
+template <int IN_DT, bool VEC>
+__global__ void __launch_bounds__(256) amax_narrow_kernel(const void* x, int64_t R, int64_t K, int64_t ldx,
+                                                          int64_t gr, int64_t gc, int64_t n_gc, int64_t rpb,
+                                                          int64_t bpg, uint32_t* amax_bits) {
+  __shared__ uint32_t sm[4][512];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * 512;
+  const int64_t kc = c0 + lane * 8;
+  const int64_t g = blockIdx.y / bpg;
+  const int64_t g_end = min(R, (g + 1) * gr);
+  const int64_t r_begin = g * gr + (blockIdx.y - g * bpg) * rpb;
+  const int64_t r_end = min(g_end, r_begin + rpb);
+  uint32_t m[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (kc < K) {
+    int64_t r = r_begin + wv;
+    for (; r + 12 < r_end; r += 16) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load8<IN_DT, VEC>(x, (r + 4 * u) * ldx, kc, K, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m[i] = max(m[i], abs_bits(v[u][i]));
+    }
+    for (; r < r_end; r += 4) {
+      float v[8];
+      load8<IN_DT, VEC>(x, r * ldx, kc, K, v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) m[i] = max(m[i], abs_bits(v[i]));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sm[wv][lane * 8 + i] = m[i];
+  __syncthreads();
+  for (int j = threadIdx.x; j < 512; j += 256) {
+    const int64_t k = c0 + j;
+    const uint32_t mm = max(max(sm[0][j], sm[1][j]), max(sm[2][j], sm[3][j]));
+    if (k < K && mm) atomicMax(amax_bits + g * n_gc + k / gc, mm);
+  }
+}
+
 typedef __bf16 v2bf_q __attribute__((ext_vector_type(2)));
 
 // eight values rounded to a float dtype in place; bf16 by the hardware
@@ -690,7 +741,8 @@ __global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const 
   // reciprocal), looked up again only when the row group changes: the
   // branch is uniform, as r is
   uint32_t gcur = 0xFFFFFFFFu, m = 0;
-  float rs = 1.0f, sv[8];
+  float rs = 1.0f, sv[8], rsv[8];
+  bool fast = false;  // every element's group allows the fast exact division
   for (int64_t r = blockIdx.y; r < a.R; r += gridDim.y) {
     float v[8];
     load8<IN_DT, VEC>(a.x, r * a.ldx, k0, a.K, v);
@@ -707,8 +759,14 @@ __global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const 
 #pragma unroll
         for (int i = 0; i < 8; ++i) sv[i] = s;
       } else {
+        fast = true;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sv[i] = scale_from_amax_bits(amax_bits[grow + kg[i]], a.qmaxf, a.scale_rule);
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t mi = amax_bits[grow + kg[i]];
+          sv[i] = scale_from_amax_bits(mi, a.qmaxf, a.scale_rule);
+          fast = fast && fast_div_ok<SR>(mi);
+          rsv[i] = 1.0f / sv[i];
+        }
       }
     }
     float q[8];
@@ -717,6 +775,11 @@ __global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const 
       // division where the group amax allows it, per element with a NaN)
       uint32_t lo, hi;
       (void)quant8_tile_rs<GRID, SR, true>(v, m, sv[0], rs, a.qmaxf, rb, lo, hi, q);
+    } else if (fast) {
+      // a group per element (channel): the same exact division element by
+      // element (c4 payload, channel groups with the amax pass: 329 us before)
+      uint32_t lo, hi;
+      quant8_cols_rs<GRID, SR, true>(v, sv, rsv, a.qmaxf, rb, lo, hi, q);
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) (void)quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]);
@@ -731,15 +794,18 @@ __global__ void __launch_bounds__(256) comm_quant_ste_kernel(QuantArgs a, const 
     round8_dtype<IN_DT>(o);
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = v[i] + o[i];
-    round8_dtype<IN_DT>(o);
     if (VEC && IN_DT == DT_BF16 && k0 + 8 <= a.K) {
+      // the last rounding gives the stored bits (the hardware pack-convert)
       uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)f32_to_bf16_bits(o[2 * i]) | ((uint32_t)f32_to_bf16_bits(o[2 * i + 1]) << 16);
+      for (int i = 0; i < 4; ++i) {
+        const v2bf_q pk = {(__bf16)o[2 * i], (__bf16)o[2 * i + 1]};
+        w[i] = __builtin_bit_cast(uint32_t, pk);
+      }
       // non-temporal: the straight-through value at c4 takes 335 us instead of 365
       store16_nt(reinterpret_cast<uint16_t*>(out) + r * ldo + k0, w);
     } else {
+      round8_dtype<IN_DT>(o);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (k0 + i < a.K) store_elem(out, IN_DT, r * ldo + k0 + i, o[i]);
@@ -1536,6 +1602,25 @@ extern "C" int ntlb_quant_block_128x128(const void* w, int w_dtype, int64_t N, i
 static int amax_grouped_launch(const char* fn, const void* x, int x_dtype, int64_t R, int64_t K, int64_t ldx,
                                int64_t gr, int64_t gc, uint32_t* amax_bits, hipStream_t st) {
   const int64_t n_gc = cdiv(K, gc);
+  // narrow groups: about 1024 workgroups of at least 64 rows, none
+  // straddling a row group (many short row groups take the kernel below)
+  const int64_t cb = cdiv(K, 512);
+  const int64_t ge = std::min(gr, R);
+  const int64_t nrpb = std::min(ge, std::max<int64_t>(64, cdiv(R, cdiv(1024, cb))));
+  const int64_t bpg = cdiv(ge, nrpb);
+  const int64_t nb = cdiv(R, ge) * bpg;
+  if (gc < 8 && nb <= 65535 && cb <= 0x7FFFFFFF) {
+    const int64_t rpb = nrpb;
+    dim3 grd((unsigned)cb, (unsigned)nb), blk(256);
+    const bool vec = K % 8 == 0 && ldx % 8 == 0 && aligned(x, 16);
+    NTLB_DISPATCH_DT(x_dtype, {
+      if (vec)
+        amax_narrow_kernel<D_, true><<<grd, blk, 0, st>>>(x, R, K, ldx, gr, gc, n_gc, rpb, bpg, amax_bits);
+      else
+        amax_narrow_kernel<D_, false><<<grd, blk, 0, st>>>(x, R, K, ldx, gr, gc, n_gc, rpb, bpg, amax_bits);
+    });
+    return check_launch(fn);
+  }
   const int64_t col_blocks = cdiv(cdiv(K, 8), 256);
   // rows per workgroup: enough to amortize the atomics, enough groups to fill
   // the GPU.  About 1024 workgroups (c4 payload with the straight-through
@@ -1876,12 +1961,20 @@ extern "C" int ntlb_dequant(int grid, const uint8_t* codes, int64_t ldc, const f
 // assignment a goes to record p = pos[a], whose metadata is token a / K, slot
 // a % K, local expert topk_idx[a] % experts_per_rank and routing weight
 // topk_w[a], with the NaN flag cleared for the quantizer to set.
+// Bytes [pad_off, m_off) of a record (the padding of a value record; none
+// in a code record) are zeroed, 16 at a time.
+__device__ __forceinline__ void ep_zero_pad(uint8_t* r, int64_t pad_off, int64_t m_off) {
+  for (int64_t b = pad_off; b < m_off; b += 16) *reinterpret_cast<uint4*>(r + b) = make_uint4(0, 0, 0, 0);
+}
+
 __global__ void __launch_bounds__(256) ep_meta_kernel(uint8_t* rec, int64_t R, int64_t m_off, int64_t A,
                                                       const int32_t* pos, const void* topk_idx, int idx_dt,
-                                                      const void* topk_w, int w_dt, int64_t K, int64_t epr) {
+                                                      const void* topk_w, int w_dt, int64_t K, int64_t epr,
+                                                      int64_t pad_off) {
   const int64_t a = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (a >= A) return;
   const int64_t p = min<int64_t>(max<int32_t>(pos[a], 0), A - 1);
+  ep_zero_pad(rec + p * R, pad_off, m_off);
   const int64_t e = idx_dt == 1 ? reinterpret_cast<const int64_t*>(topk_idx)[a]
                                 : (int64_t) reinterpret_cast<const int32_t*>(topk_idx)[a];
   const float w = load_elem(topk_w, w_dt, a);
@@ -1896,10 +1989,11 @@ __global__ void __launch_bounds__(256) ep_meta_kernel(uint8_t* rec, int64_t R, i
 __global__ void __launch_bounds__(256) ep_meta_rows_kernel(uint8_t* rec, int64_t R, int64_t m_off, int64_t n,
                                                            const int32_t* pos, const int32_t* token_idx,
                                                            const int32_t* slot_idx, const int32_t* local_expert,
-                                                           const float* weight) {
+                                                           const float* weight, int64_t pad_off) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   const int64_t p = min<int64_t>(max<int32_t>(pos[i], 0), n - 1);
+  ep_zero_pad(rec + p * R, pad_off, m_off);
   int32_t* m = reinterpret_cast<int32_t*>(rec + p * R + m_off);
   *reinterpret_cast<int4*>(m) = make_int4(token_idx[i], slot_idx[i], local_expert ? local_expert[i] : 0, 0);
   *reinterpret_cast<int4*>(m + 4) = make_int4(weight ? __float_as_int(weight[i]) : 0, 0, 0, 0);
@@ -1962,45 +2056,65 @@ __global__ void __launch_bounds__(256) ep_pack_values_kernel(QuantArgs a, const 
 #pragma clang fp contract(off)
   const int64_t k0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (k0 >= a.K) return;  // K % 8 == 0: whole chunks
-  float sv[8];
+  // the chunk's group scales, and their reciprocals where every one of the
+  // eight allows the fast exact division (quant8_tile_rs's condition)
+  float sv[8], rs[8];
+  bool fast = true;
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    sv[i] = scale_from_amax_bits(amax_bits[min<int64_t>((k0 + i) / gc, n_gc - 1)], a.qmaxf, a.scale_rule);
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t m = amax_bits[min<int64_t>((k0 + i) / gc, n_gc - 1)];
+    sv[i] = scale_from_amax_bits(m, a.qmaxf, a.scale_rule);
+    fast = fast && fast_div_ok<SR>(m);
+    rs[i] = 1.0f / sv[i];
+  }
   constexpr int64_t esz = IN_DT == DT_F32 ? 4 : 2;
+  // one row at a time: loading four rows ahead measured slower (c4 return
+  // pack 358 -> 368 us, the stochastic dispatch pack 243 -> 260)
   for (int64_t r = blockIdx.y; r < a.R; r += gridDim.y) {
     float v[8];
     load8<IN_DT, true>(a.x, r * a.ldx, k0, a.K, v);
-    float o[8];
-    for (int64_t f = 0; f < a.fan_k; ++f) {
-      const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + f], 0), a.fan_rows - 1);
-      if (SR || f == 0) {  // round to nearest: one value for every copy
-        uint32_t rb[8];
-        sr_words<SR>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
-        float q[8];
+    {
+      uint32_t w[8];  // the value's bits (bf16: 4 words)
+      for (int64_t f = 0; f < a.fan_k; ++f) {
+        const int64_t p = min<int64_t>(max<int32_t>(a.fan_pos[r * a.fan_k + f], 0), a.fan_rows - 1);
+        if (SR || f == 0) {  // round to nearest: one value for every copy
+          float o[8];
+          uint32_t rb[8];
+          sr_words<SR>((uint64_t)(p * a.K + k0), a.seed, a.offset, rb);
+          float q[8];
+          if (fast) {
+            uint32_t lo, hi;
+            quant8_cols_rs<GRID, SR, true>(v, sv, rs, a.qmaxf, rb, lo, hi, q);
+          } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) (void)quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]);
+            for (int i = 0; i < 8; ++i) (void)quant_one<GRID, SR>(v[i], sv[i], a.qmaxf, rb[i], q[i]);
+          }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = q[i] * sv[i];
-        round8_dtype<IN_DT>(o);
+          for (int i = 0; i < 8; ++i) o[i] = q[i] * sv[i];
+          round8_dtype<IN_DT>(o);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = o[i] - v[i];
-        round8_dtype<IN_DT>(o);
+          for (int i = 0; i < 8; ++i) o[i] = o[i] - v[i];
+          round8_dtype<IN_DT>(o);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = v[i] + o[i];
-        round8_dtype<IN_DT>(o);
-      }
-      uint8_t* dst = rec + p * R + k0 * esz;  // 16-byte aligned: R % 16 == 0, k0 % 8 == 0
-      if constexpr (IN_DT == DT_BF16) {
-        uint32_t w[4];
+          for (int i = 0; i < 8; ++i) o[i] = v[i] + o[i];
+          // the last rounding gives the stored bits: bf16 pairs by the
+          // hardware pack-convert (round to nearest even), fp32 as is
+          if constexpr (IN_DT == DT_BF16) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          w[i] = (uint32_t)f32_to_bf16_bits(o[2 * i]) | ((uint32_t)f32_to_bf16_bits(o[2 * i + 1]) << 16);
-        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-      } else {
-        *reinterpret_cast<uint4*>(dst) =
-            make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3]));
-        *reinterpret_cast<uint4*>(dst + 16) =
-            make_uint4(__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]), __float_as_uint(o[7]));
+            for (int i = 0; i < 4; ++i) {
+              const v2bf_q pk = {(__bf16)o[2 * i], (__bf16)o[2 * i + 1]};
+              w[i] = __builtin_bit_cast(uint32_t, pk);
+            }
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) w[i] = __float_as_uint(o[i]);
+          }
+        }
+        uint8_t* dst = rec + p * R + k0 * esz;  // 16-byte aligned: R % 16 == 0, k0 % 8 == 0
+        // non-temporal: the records go to the exchange, not to the next
+        // kernel (c4 return pack: 443 -> 419 us)
+        store16_nt(dst, w);
+        if constexpr (IN_DT == DT_F32) store16_nt(dst + 16, w + 4);
       }
     }
   }
@@ -2078,7 +2192,7 @@ extern "C" int ntlb_ep_pack_records_grouped(const void* tokens, int x_dtype, int
   const int64_t R = ntlb_ep_record_bytes(H);
   hipStream_t st = as_stream(stream);
   ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, R - 32, A, pos, topk_idx, idx_dtype, topk_w,
-                                                          w_dtype, K, experts_per_rank);
+                                                          w_dtype, K, experts_per_rank, R - 32);
   rc = check_launch(fn);
   if (rc) return rc;
   // each token row read once, quantized, and written to its K records
@@ -2112,7 +2226,7 @@ extern "C" int ntlb_ep_pack_return(const void* x, int x_dtype, int64_t n, int64_
   const int64_t R = ntlb_ep_record_bytes(H);
   hipStream_t st = as_stream(stream);
   ep_meta_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(records, R, R - 32, n, pos, token_idx, slot_idx,
-                                                               local_expert, weight);
+                                                               local_expert, weight, R - 32);
   rc = check_launch(fn);
   if (rc) return rc;
   return ep_pack_payload(fn, x, x_dtype, n, H, ldx, pos, 1, n, amax_bits, gc, grid, qmax, rounding, scale_rule, seed,
@@ -2121,7 +2235,8 @@ extern "C" int ntlb_ep_pack_return(const void* x, int x_dtype, int64_t n, int64_
 
 extern "C" int64_t ntlb_ep_value_record_bytes(int64_t H, int dtype) {
   if (H <= 0 || !valid_dtype(dtype)) return 0;
-  return (H * dtype_size(dtype) + 15) / 16 * 16 + 32;
+  // whole 128-byte lines: every record's payload starts on a line
+  return (H * dtype_size(dtype) + 32 + 127) / 128 * 128;
 }
 
 // Value-record payload of rows x [n_in, H]: the metadata kernels run first.
@@ -2178,7 +2293,7 @@ extern "C" int ntlb_ep_pack_values(const void* tokens, int x_dtype, int64_t T, i
   const int64_t R = ntlb_ep_value_record_bytes(H, x_dtype);
   hipStream_t st = as_stream(stream);
   ep_meta_kernel<<<(unsigned)cdiv(A, 256), 256, 0, st>>>(records, R, R - 32, A, pos, topk_idx, idx_dtype, topk_w,
-                                                          w_dtype, K, experts_per_rank);
+                                                          w_dtype, K, experts_per_rank, H * dtype_size(x_dtype));
   rc = check_launch(fn);
   if (rc) return rc;
   return ep_pack_values_payload(fn, tokens, x_dtype, T, H, ldt, pos, K, A, amax_bits, gc, grid, qmax, rounding,
@@ -2202,7 +2317,7 @@ extern "C" int ntlb_ep_pack_return_values(const void* x, int x_dtype, int64_t n,
   const int64_t R = ntlb_ep_value_record_bytes(H, x_dtype);
   hipStream_t st = as_stream(stream);
   ep_meta_rows_kernel<<<(unsigned)cdiv(n, 256), 256, 0, st>>>(records, R, R - 32, n, pos, token_idx, slot_idx,
-                                                               local_expert, weight);
+                                                               local_expert, weight, H * dtype_size(x_dtype));
   rc = check_launch(fn);
   if (rc) return rc;
   return ep_pack_values_payload(fn, x, x_dtype, n, H, ldx, pos, 1, n, amax_bits, gc, grid, qmax, rounding, scale_rule,

@@ -516,7 +516,11 @@ def test_value_records_hold_the_reference_wire_values(gpu_device, granularity, r
     gpu_wire = moe.comm_quant_dequant(send_t, granularity=granularity, rounding_mode=rounding, seed=77, offset=5)
     torch.cuda.synchronize()
     assert send.value_dtype == dtype and send.counts.cpu().numpy().tolist() == counts.tolist()
-    vals, meta, weight, reserved = _value_payload(send.records.cpu().numpy(), H, dtype)
+    rec = send.records.cpu().numpy()
+    R, m_off = ep.value_record_layout(H, dtype)
+    assert R % 128 == 0 and m_off == R - 32 and R - 32 >= H * x.element_size()
+    assert not rec[:, H * x.element_size():m_off].any(), "padding must be zero"
+    vals, meta, weight, reserved = _value_payload(rec, H, dtype)
     send_rows = to_np32(x)[order // K]
     gc = {"channel": 1, "tile_1x128": 128, "tensor": H}[granularity]
     want = _wire_values(send_rows, gc, dtype, rounding, 77, 5)
