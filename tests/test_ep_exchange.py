@@ -71,3 +71,35 @@ def test_exchange_over_gloo():
         want = [row for src in range(world) for row in _records(src) if int(row[1]) == dst]
         want = torch.stack(want) if want else torch.empty((0, R), dtype=torch.uint8)
         assert torch.equal(recv, want)
+
+
+def test_record_layouts_and_payload_modes():
+    """Value records are whole 128-byte lines with the 32 metadata bytes last
+    and room for the row; code records are unchanged.  The channel
+    granularity takes value records (the only wire that carries one scale
+    per column), and the other reference granularities take either wire."""
+    import pytest
+
+    from lowbit import _lib, ep
+
+    for H, dt, esz in [(7168, torch.bfloat16, 2), (200, torch.bfloat16, 2), (200, torch.float32, 4), (8, torch.float32, 4)]:
+        R, m_off = ep.value_record_layout(H, dt)
+        assert R % 128 == 0 and m_off == R - 32 and H * esz <= m_off < H * esz + 128
+    assert int(_lib.lib().ntlb_ep_value_record_bytes(0, 1)) == 0
+    assert int(_lib.lib().ntlb_ep_value_record_bytes(64, 7)) == 0
+    R, s_off, m_off = ep.record_layout(7168)
+    assert (R, s_off, m_off) == (7424, 7168, 7392)
+
+    assert ep._payload_mode("channel", None, None, 512)[2:] == (1, True)
+    assert ep._payload_mode("tile_1x128", None, None, 512)[2:] == (128, False)
+    assert ep._payload_mode("block_128x128", None, None, 512, "values")[2:] == (128, True)
+    assert ep._payload_mode("tensor", None, None, 512)[2:] == (512, False)
+    assert ep._payload_mode(None, None, None, 512)[2:] == (None, False)
+    with pytest.raises(ValueError, match="channel"):
+        ep._payload_mode("channel", None, None, 512, "codes")
+    with pytest.raises(ValueError, match="granularity"):
+        ep._payload_mode(None, None, None, 512, "values")
+    with pytest.raises(ValueError, match="granularity"):
+        ep._payload_mode("per_row", None, None, 512)
+    with pytest.raises(ValueError, match="wire"):
+        ep._payload_mode("tensor", None, None, 512, "bytes")
