@@ -360,6 +360,29 @@ def test_grouped_parity(gpu_device, kind, fmt, grid, rname, rcode):
     assert_bits_equal(to_np32(dq), torch.from_numpy(d2).to(x.dtype).float().numpy(), "dq")
 
 
+@pytest.mark.parametrize("R,K,gr,gc", [(300, 520, 128, 1), (300, 520, 7, 3), (70000, 8, 1, 1)])
+@pytest.mark.parametrize("rname,rcode", ROUNDS)
+def test_grouped_parity_narrow_column_groups(gpu_device, R, K, gr, gc, rname, rcode):
+    """Column groups narrower than 8 (one scale per column, or per 3) take
+    the workgroup-reduced amax pass, whose workgroups each cover one row
+    group: 128-row groups (the last ragged), 7-row groups, and 70000 one-row
+    groups, more than that pass launches, which fall back to the
+    wide-group pass.  Codes, scales and dq bit-exact against the oracle."""
+    from lowbit import ops
+
+    x = seeded((R, K), seed=20260107, outliers=0.01).to(gpu_device)
+    x[5, 2] = float("nan")
+    x[:, 1] = 0.0
+    codes, scales, dq, _ = ops.quant_grouped(x, gr, gc, fmt="int_grid", rounding=rname, seed=3, offset=1,
+                                             scale_rule=O.SCALE_BEFORE_DIVIDE, want_dq=True)
+    torch.cuda.synchronize()
+    c2, s2, q2, d2 = O.quant_grouped(to_np32(x), gr, gc, grid=O.GRID_INT, rounding=rcode, seed=3, offset=1,
+                                     scale_rule=O.SCALE_BEFORE_DIVIDE)
+    assert_bits_equal(codes.cpu().numpy(), c2, "codes")
+    assert_bits_equal(scales.cpu().numpy(), s2, "scales")
+    assert_bits_equal(to_np32(dq), torch.from_numpy(d2).to(x.dtype).float().numpy(), "dq")
+
+
 def test_strip_subnormal_amax_rule(gpu_device):
     from lowbit import ops
 
