@@ -463,8 +463,8 @@ __global__ void __launch_bounds__(COMBINE_ROWS_THREADS) moe_combine_rows_kernel(
           uint32_t pk[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) pk[i] = bf16x2_bits(acc[2 * i], acc[2 * i + 1]);
-          *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(out) + t * ldo + c0 + h * STEP) =
-              make_uint4(pk[0], pk[1], pk[2], pk[3]);
+          // non-temporal, as the EP combine's token rows (c4: 111 -> 106 us)
+          store16_nt(reinterpret_cast<uint16_t*>(out) + t * ldo + c0 + h * STEP, pk);
         }
       }
       return;
