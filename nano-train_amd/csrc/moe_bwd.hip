@@ -16,6 +16,8 @@
 //     bf16 op sequence (F.silu, mul), in B's interleaved gate / up columns.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "ntlb_device.h"
 #include "ntlb_host.h"
 
@@ -242,7 +244,7 @@ __global__ void __launch_bounds__(256) swiglu_backward_kernel(const uint16_t* dh
 // in the output dtype (rounded per add): the order and roundings in which
 // autograd accumulates the gradients of `tokens[token_indices]` over the
 // expert loop (its later experts' backward runs first)
-template <int DT>
+template <int DT, bool VEC>
 __global__ void __launch_bounds__(CB_THREADS) token_grad_kernel(const void* dx, int64_t lddx, const int32_t* pos,
                                                                 const void* topk_idx, int idx_dt, int K, int64_t H,
                                                                 void* out, int64_t ldo) {
@@ -271,6 +273,52 @@ __global__ void __launch_bounds__(CB_THREADS) token_grad_kernel(const void* dx, 
     }
   }
   __syncthreads();
+  if constexpr (VEC) {
+    // eight columns per thread: every kept slot's 16-byte chunk loaded before
+    // the sum (element-wise 2-byte loads ran the c4 token gradient at 2 TB/s)
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(dx);
+    uint16_t* dst = reinterpret_cast<uint16_t*>(out) + t * ldo;
+    for (int64_t c0 = (int64_t)threadIdx.x * 8; c0 < H; c0 += CB_THREADS * 8) {
+      uint4 raw[CB_MAX_K];
+#pragma unroll
+      for (int s = 0; s < CB_MAX_K; ++s) {
+        const int32_t row = s_row[s];
+        raw[s] = row >= 0 ? *reinterpret_cast<const uint4*>(src + (int64_t)row * lddx + c0) : make_uint4(0, 0, 0, 0);
+      }
+      bool any = false;
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < CB_MAX_K; ++s) {
+        if (s_row[s] < 0) continue;
+        const uint32_t w[4] = {raw[s].x, raw[s].y, raw[s].z, raw[s].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t hb = (w[i >> 1] >> (16 * (i & 1))) & 0xFFFFu;
+          const float v =
+              DT == DT_BF16 ? __uint_as_float(hb << 16) : __half2float(__ushort_as_half((unsigned short)hb));
+          acc[i] = any ? round_to_dtype(acc[i] + v, DT) : v;
+        }
+        any = true;
+      }
+      // the sums hold values of the dtype already (or a token without a kept
+      // slot: zero): their bits, exactly
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t lo, hi;
+        if constexpr (DT == DT_BF16) {
+          lo = __float_as_uint(acc[2 * i]) >> 16;
+          hi = __float_as_uint(acc[2 * i + 1]) >> 16;
+        } else {
+          lo = __half_as_ushort(f32_to_f16(acc[2 * i]));
+          hi = __half_as_ushort(f32_to_f16(acc[2 * i + 1]));
+        }
+        pk[i] = lo | (hi << 16);
+      }
+      *reinterpret_cast<uint4*>(dst + c0) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+    return;
+  }
   for (int64_t c = threadIdx.x; c < H; c += CB_THREADS) {
     bool any = false;
     float acc = 0.f;
@@ -300,12 +348,22 @@ extern "C" int ntlb_moe_token_grad(const void* dx, int64_t lddx, int dtype, cons
   if (T == 0 || H == 0) return NTLB_OK;
   if (!dx || !pos || !topk_idx || !out) return fail(NTLB_EINVAL, "%s: NULL pointer", fn);
   hipStream_t st = as_stream(stream);
-  if (dtype == NTLB_BF16)
-    token_grad_kernel<DT_BF16><<<(unsigned)T, CB_THREADS, 0, st>>>(dx, lddx, pos, topk_idx, idx_dtype, (int)K, H, out, ldo);
-  else if (dtype == NTLB_F16)
-    token_grad_kernel<DT_F16><<<(unsigned)T, CB_THREADS, 0, st>>>(dx, lddx, pos, topk_idx, idx_dtype, (int)K, H, out, ldo);
-  else
-    token_grad_kernel<DT_F32><<<(unsigned)T, CB_THREADS, 0, st>>>(dx, lddx, pos, topk_idx, idx_dtype, (int)K, H, out, ldo);
+  const bool vec = H % 8 == 0 && lddx % 8 == 0 && ldo % 8 == 0 && aligned(dx, 16) && aligned(out, 16);
+  auto launch = [&](auto dtc, auto vecc) {
+    token_grad_kernel<decltype(dtc)::value, decltype(vecc)::value><<<(unsigned)T, CB_THREADS, 0, st>>>(
+        dx, lddx, pos, topk_idx, idx_dtype, (int)K, H, out, ldo);
+  };
+  using B = std::integral_constant<int, DT_BF16>;
+  using Hh = std::integral_constant<int, DT_F16>;
+  using Y = std::true_type;
+  using N = std::false_type;
+  if (dtype == NTLB_BF16) {
+    if (vec) launch(B(), Y()); else launch(B(), N());
+  } else if (dtype == NTLB_F16) {
+    if (vec) launch(Hh(), Y()); else launch(Hh(), N());
+  } else {
+    launch(std::integral_constant<int, DT_F32>(), N());  // fp32: the element loop
+  }
   return check_launch(fn);
 }
 
