@@ -21,6 +21,7 @@
 
 #include "ntlb_device.h"
 #include "ntlb_host.h"
+#include "ntlb_quant8.h"
 #include "ntlb_splitk.h"
 
 #pragma clang fp contract(off)
@@ -421,11 +422,26 @@ __device__ __forceinline__ void refresh8(const float (&w)[8], uint32_t amax, int
   const float s = (amax < 0x7F800000u && amax != 0u) ? __uint_as_float(amax) : 1.0f;
   if ((tid & (gthreads - 1)) == 0) scales[e0 / block] = s;
   const bool full = e0 + 8 <= n;
+  // w / s by the exact reciprocal sequence of the fp8 quantizers wherever
+  // the block amax allows it (fast_div_ok: every quotient that can move a
+  // code, here |w/s| >= 2^-10 for e4m3 and >= 0.039 for NF4, has a normal
+  // residual), else by IEEE division: one division per 8 weights instead of 8
+  // (the NF4 pass was bound by its VALU work)
+  const bool fast = fast_div_ok<false>(amax);
+  const float rs = fast ? 1.0f / s : 1.0f;
+  auto quot = [&](float x) {
+    if (fast) {
+      const float y = x * rs;
+      const float e = __builtin_fmaf(-y, s, x);
+      return __builtin_copysignf(__builtin_fmaf(e, rs, y), x);
+    }
+    return x / s;
+  };
   if constexpr (RF == REFRESH_NF4) {
     uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float c = w[i] / s;
+      float c = quot(w[i]);
       c = (c < -1.0f) ? -1.0f : c;
       c = (c > 1.0f) ? 1.0f : c;
       word |= nf4_index(c) << (4 * i);
@@ -441,7 +457,7 @@ __device__ __forceinline__ void refresh8(const float (&w)[8], uint32_t amax, int
     uint32_t c8[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      float c = w[i] / s;
+      float c = quot(w[i]);
       c = (c < -448.0f) ? -448.0f : c;
       c = (c > 448.0f) ? 448.0f : c;
       c8[i] = e4m3_rne(c);
