@@ -17,6 +17,7 @@
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "ntlb_device.h"
@@ -396,41 +397,23 @@ struct AdamArgs {
 
 enum RefreshFmt : int { REFRESH_NONE = 0, REFRESH_NF4 = 1, REFRESH_FP8 = 2 };
 
-// Codes and scales of 8 consecutive values w[0..8) at e0 (thread tid of a
-// 256-thread workgroup covering 2048 consecutive elements), for power-of-two
-// scale blocks in [8, 2048]: the block amax is reduced over the block's
-// block/8 threads (shuffles, then LDS across waves), scale = amax with
-// _safe_scale (layers.py:86-101), then NF4 indices (layers.py:156-169) or
-// e4m3 of clamp(w/s, +-448) (layers.py:104-117).  Every thread of the
-// workgroup must call it (it may synchronize).
+// NF4 indices (layers.py:156-169) or e4m3 codes of clamp(w/s, +-448)
+// (layers.py:104-117) of 8 consecutive values w[0..8) at e0 with the scale s,
+// stored at their place in codes (4 packed bytes, or 8 code bytes)
 template <int RF>
-__device__ __forceinline__ void refresh8(const float (&w)[8], uint32_t amax, int64_t e0, int64_t n, int64_t block,
-                                         uint8_t* codes, float* scales, uint32_t* wave_amax, int tid) {
-  const int lane = tid & 63, wave = tid >> 6;
-  const int gthreads = (int)(block >> 3);
-  for (int off = 1; off < gthreads && off < 64; off <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
-  if (gthreads > 64) {
-    if (lane == 0) wave_amax[wave] = amax;
-    __syncthreads();
-    const int wpg = gthreads >> 6;  // waves per block: 2 or 4
-    const int w0 = (wave / wpg) * wpg;
-    uint32_t mm = 0;
-    for (int i = 0; i < wpg; ++i) mm = max(mm, wave_amax[w0 + i]);
-    amax = mm;
-  }
-  if (e0 >= n) return;
-  const float s = (amax < 0x7F800000u && amax != 0u) ? __uint_as_float(amax) : 1.0f;
-  if ((tid & (gthreads - 1)) == 0) scales[e0 / block] = s;
+__device__ __forceinline__ void quant8_store(const float (&w)[8], float s, int64_t e0, int64_t n, uint8_t* codes) {
   const bool full = e0 + 8 <= n;
   // w / s by the exact reciprocal sequence of the fp8 quantizers wherever
-  // the block amax allows it (fast_div_ok: every quotient that can move a
-  // code, here |w/s| >= 2^-10 for e4m3 and >= 0.039 for NF4, has a normal
-  // residual), else by IEEE division: one division per 8 weights instead of 8
-  // (the NF4 pass was bound by its VALU work)
-  const bool fast = fast_div_ok<false>(amax);
+  // the scale allows it (fast_div_ok on s, which is the block amax or 1:
+  // every quotient that can move a code, here |w/s| >= 2^-10 for e4m3 and
+  // >= 0.039 for NF4, has a normal residual) and w is finite (a block with
+  // an infinity or a NaN has scale 1, and inf * 1 - inf would give NaN where
+  // the division gives inf), else by IEEE division: one division per 8
+  // weights instead of 8 (the NF4 pass was bound by its VALU work)
+  const bool fast = fast_div_ok<false>(__float_as_uint(s));
   const float rs = fast ? 1.0f / s : 1.0f;
   auto quot = [&](float x) {
-    if (fast) {
+    if (fast && __builtin_isfinite(x)) {
       const float y = x * rs;
       const float e = __builtin_fmaf(-y, s, x);
       return __builtin_copysignf(__builtin_fmaf(e, rs, y), x);
@@ -470,6 +453,34 @@ __device__ __forceinline__ void refresh8(const float (&w)[8], uint32_t amax, int
         if (e0 + i < n) codes[e0 + i] = (uint8_t)c8[i];
     }
   }
+}
+
+// Codes and scales of 8 consecutive values w[0..8) at e0 (thread tid of a
+// 256-thread workgroup covering 2048 consecutive elements), for power-of-two
+// scale blocks in [8, 2048]: the block amax is reduced over the block's
+// block/8 threads (shuffles, then LDS across waves), scale = amax with
+// _safe_scale (layers.py:86-101), then NF4 indices (layers.py:156-169) or
+// e4m3 of clamp(w/s, +-448) (layers.py:104-117).  Every thread of the
+// workgroup must call it (it may synchronize).
+template <int RF>
+__device__ __forceinline__ void refresh8(const float (&w)[8], uint32_t amax, int64_t e0, int64_t n, int64_t block,
+                                         uint8_t* codes, float* scales, uint32_t* wave_amax, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  const int gthreads = (int)(block >> 3);
+  for (int off = 1; off < gthreads && off < 64; off <<= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
+  if (gthreads > 64) {
+    if (lane == 0) wave_amax[wave] = amax;
+    __syncthreads();
+    const int wpg = gthreads >> 6;  // waves per block: 2 or 4
+    const int w0 = (wave / wpg) * wpg;
+    uint32_t mm = 0;
+    for (int i = 0; i < wpg; ++i) mm = max(mm, wave_amax[w0 + i]);
+    amax = mm;
+  }
+  if (e0 >= n) return;
+  const float s = (amax < 0x7F800000u && amax != 0u) ? __uint_as_float(amax) : 1.0f;
+  if ((tid & (gthreads - 1)) == 0) scales[e0 / block] = s;
+  quant8_store<RF>(w, s, e0, n, codes);
 }
 
 // 8 consecutive values at e0 as fp32: one or two 16-byte loads when all 8 lie
@@ -559,6 +570,65 @@ __global__ void __launch_bounds__(256) adamw_refresh_kernel(AdamArgs a) {
 // One-pass block quantizer of a flat tensor for power-of-two blocks in
 // [8, 2048]: the persistent NF4 / FP8 quantization without the separate amax
 // pass and its atomics.
+// Two-pass persistent quantization for blocks the one-pass kernel does not
+// take (a row of more than 2048 values for per_channel, or the whole tensor
+// for per_tensor), over a 16-byte aligned flat tensor.  Pass 1: the block
+// maxima; each workgroup takes 2048-element chunks blockIdx.x, +gridDim.x,
+// and reduces a chunk over its four waves before one atomic (one block: the
+// workgroup keeps its maximum over all its chunks and issues one atomic in
+// all).  The wave-per-512-elements kernel above put every wave's atomic on
+// the one address of a per_tensor scale: 1.4 ms at the c5 weight.
+template <int IN_DT>
+__global__ void __launch_bounds__(256) flat_amax_chunks_kernel(const void* w, int64_t n, int64_t block,
+                                                               int64_t nchunks, uint32_t* amax_bits) {
+  __shared__ uint32_t red[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool one = n <= block;  // uniform
+  uint32_t run = 0;
+  for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+    const int64_t e0 = c * 2048 + (int64_t)threadIdx.x * 8;
+    float v[8];
+    load8f(w, IN_DT, e0, n, v);
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (e0 + i < n) m = max(m, abs_bits(v[i]));
+    if (one) {
+      run = max(run, m);
+      continue;
+    }
+    // block % 2048 == 0: the chunk lies inside block c*2048 / block
+    m = wave_max_u32(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t mm = max(max(red[0], red[1]), max(red[2], red[3]));
+      if (mm) atomicMax(amax_bits + (c * 2048) / block, mm);
+    }
+    __syncthreads();
+  }
+  if (one) {
+    run = wave_max_u32(run);
+    if (lane == 0) red[wave] = run;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t mm = max(max(red[0], red[1]), max(red[2], red[3]));
+      if (mm) atomicMax(amax_bits, mm);
+    }
+  }
+}
+
+// Pass 2: 8 consecutive values per thread (block % 8 == 0: one scale each)
+template <int RF>
+__global__ void __launch_bounds__(256) flat_quant8_kernel(const void* w, int w_dtype, int64_t n, int64_t block,
+                                                          const float* scales, uint8_t* codes) {
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (e0 >= n) return;
+  float v[8];
+  load8f(w, w_dtype, e0, n, v);
+  quant8_store<RF>(v, scales[e0 / block], e0, n, codes);
+}
+
 template <int RF>
 __global__ void __launch_bounds__(256) quant_blocks_onepass(const void* w_in, int w_dtype, int64_t n, int64_t block,
                                                             uint8_t* codes, float* scales) {
@@ -1059,6 +1129,25 @@ __global__ void __launch_bounds__(512, 1) gemm_lowbit_fused_kernel(FusedArgs g) 
 
 using namespace ntlb;
 
+// the two vectorized passes, when the tensor and its blocks allow them
+template <int RF>
+static bool flat_two_pass(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws, uint8_t* codes,
+                          float* scales, hipStream_t st) {
+  if (!aligned(w, 16) || block % 8 != 0 || !(n <= block || block % 2048 == 0)) return false;
+  const int64_t nb = cdiv(n, block);
+  const int64_t nchunks = cdiv(n, 2048);
+  const unsigned ga = (unsigned)std::min<int64_t>(nchunks, 2048);
+  if (w_dtype == NTLB_BF16)
+    flat_amax_chunks_kernel<DT_BF16><<<ga, 256, 0, st>>>(w, n, block, nchunks, amax_ws);
+  else if (w_dtype == NTLB_F32)
+    flat_amax_chunks_kernel<DT_F32><<<ga, 256, 0, st>>>(w, n, block, nchunks, amax_ws);
+  else
+    flat_amax_chunks_kernel<DT_F16><<<ga, 256, 0, st>>>(w, n, block, nchunks, amax_ws);
+  amax_to_scale_kernel<<<(unsigned)cdiv(nb, 256), 256, 0, st>>>(amax_ws, nb, scales);
+  flat_quant8_kernel<RF><<<(unsigned)cdiv(cdiv(n, 8), 256), 256, 0, st>>>(w, w_dtype, n, block, scales, codes);
+  return true;
+}
+
 extern "C" int ntlb_nf4_quant(const void* w, int w_dtype, int64_t n, int64_t block, uint32_t* amax_ws,
                               uint8_t* packed, float* scales, void* stream) {
   const char* fn = "ntlb_nf4_quant";
@@ -1076,6 +1165,7 @@ extern "C" int ntlb_nf4_quant(const void* w, int w_dtype, int64_t n, int64_t blo
   const int64_t threads = cdiv(n, 8);
   if (cdiv(threads, 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
   hipStream_t st = as_stream(stream);
+  if (flat_two_pass<REFRESH_NF4>(w, w_dtype, n, block, amax_ws, packed, scales, st)) return check_launch(fn);
   dim3 grd((unsigned)cdiv(threads, 256)), blk(256);
   if (w_dtype == NTLB_BF16)
     flat_block_amax_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
@@ -1233,8 +1323,10 @@ extern "C" int ntlb_fp8_persistent_quant(const void* w, int w_dtype, int64_t n, 
     return check_launch(fn);
   }
   const int64_t nb = cdiv(n, block);
+  if (cdiv(cdiv(n, 8), 256) > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too large", fn);
   dim3 grd((unsigned)cdiv(cdiv(n, 8), 256)), blk(256);
   hipStream_t st = as_stream(stream);
+  if (flat_two_pass<REFRESH_FP8>(w, w_dtype, n, block, amax_ws, codes, scales, st)) return check_launch(fn);
   if (w_dtype == NTLB_BF16)
     flat_block_amax_kernel<DT_BF16><<<grd, blk, 0, st>>>(w, n, block, amax_ws);
   else if (w_dtype == NTLB_F32)
