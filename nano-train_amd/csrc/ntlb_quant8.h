@@ -156,8 +156,10 @@ __device__ __forceinline__ bool quant8_tile_rs(const float (&v)[N], uint32_t m, 
                                                const uint32_t (&rb)[N], uint32_t& lo, uint32_t& hi, float (&q)[N]) {
 #pragma clang fp contract(off)
   static_assert(N == 8 || N == 4, "8 or 4 values");
-  if (m > 0x7F800000u) {
-    // NaN in the tile: reference semantics element by element
+  if (m > 0x7F800000u || !(s > 0.0f)) {
+    // NaN in the tile, or a scale that underflowed to zero (the rule that
+    // divides the amax after checking it: x / 0 is NaN or +-inf): reference
+    // semantics element by element
     quant8<GRID, SR>(v, s, qmaxf, rb, lo, hi, q);
     return true;
   } else {

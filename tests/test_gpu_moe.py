@@ -64,6 +64,28 @@ def test_comm_quant_dequant_special_values(gpu_device):
         assert_bits_equal(out.float().cpu().numpy(), ref.float().numpy(), f"comm dq {g}")
 
 
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_comm_quant_dequant_subnormal_group_amax(gpu_device, rounding):
+    """A group whose amax is subnormal: the reference divides it by qmax
+    after the check (moe.py:94-98), the scale underflows to zero and the
+    group's values become NaN (zeros) or +-qmax times zero (the rest); the
+    other groups are ordinary."""
+    from lowbit import moe
+
+    x = torch.zeros(4, 384)
+    x[0, :2] = torch.tensor([1e-45, -1e-45])
+    x[1, 300] = 1e-42
+    x[:, 128:256] = torch.randn(4, 128, generator=torch.Generator().manual_seed(20260403))
+    x = x.to(gpu_device)
+    rc = O.ROUND_STOCHASTIC if rounding == "stochastic" else O.ROUND_NEAREST
+    for g in ("tile_1x128", "tensor", "channel"):
+        out = moe.comm_quant_dequant(x, granularity=g, rounding_mode=rounding, seed=1, offset=1)
+        ref = _ref_comm(x, g, rc, 8, 1, 1)
+        assert_bits_equal(out.float().cpu().numpy(), ref.float().numpy(), f"comm dq {g}")
+    # the strips' scales: the first and last underflow
+    assert torch.isnan(moe.comm_quant_dequant(x, granularity="tile_1x128", rounding_mode=rounding)[2, 5]).item()
+
+
 @pytest.mark.parametrize("fmt,grid", [("e4m3", O.GRID_E4M3), ("int_grid", O.GRID_INT)])
 def test_comm_wire_format_round_trip(gpu_device, fmt, grid):
     from lowbit import moe
