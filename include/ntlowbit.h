@@ -550,7 +550,7 @@ int ntlb_fp8_persistent_dequant(const uint8_t* codes, const float* scales, int64
                                 int out_dtype, void* stream);
 
 /*
- * One AdamW step of DtypeConfiguredAdamW.step (optimizer_runtime.py:68-116)
+ * One AdamW step of PrecisionAdamW.step (optimizer_runtime.py:68-116)
  * on fp32 main_param, exp_avg, exp_avg_sq [n] in place, with the gradient in
  * grad_dtype, optionally writing the parameter copy in param_dtype
  * (param.data.copy_(main_param_f.to(param.dtype))).  The float scalars are the

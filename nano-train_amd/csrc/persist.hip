@@ -369,7 +369,7 @@ static void launch_dequant(const uint8_t* codes, const void* scales, int64_t n, 
 // ---------------------------------------------------------------------------
 // AdamW step fused with the persistent low-bit refresh.
 //
-// One pass over a parameter: the DtypeConfiguredAdamW update of
+// One pass over a parameter: the PrecisionAdamW update of
 // optimizer_runtime.py:68-116 on fp32 master, exp_avg and exp_avg_sq, the
 // parameter copy in its own dtype, and -- for scale blocks of at most 2048
 // elements -- the NF4 or persistent-FP8 codes and scales that

@@ -1,7 +1,7 @@
 """AdamW on the device with the persistent low-bit refresh fused in.
 
-nano-train steps its parameters with DtypeConfiguredAdamW
-(src/runtime/optimizer_runtime.py:18-116) and then re-quantizes every
+nano-train steps its parameters with PrecisionAdamW
+(src/runtime/optimizer_runtime.py:15-116) and then re-quantizes every
 persistent low-bit weight with refresh_persistent_lowbit_params
 (src/layers.py:353-407, called through mixed_precision.py:624-632).  Here one
 kernel does both for a parameter: the AdamW update of the fp32 master,
@@ -107,8 +107,8 @@ def _fused_block(module) -> Optional[int]:
     return None
 
 
-class DtypeConfiguredAdamW:
-    """Device mirror of DtypeConfiguredAdamW (optimizer_runtime.py:18-116).
+class PrecisionAdamW:
+    """Device mirror of PrecisionAdamW (optimizer_runtime.py:15-116).
 
     Same constructor and step(); the state dtypes must be fp32 (the reference
     defaults), which the fused kernel keeps.  attach_lowbit_refresh(model)

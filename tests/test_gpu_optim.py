@@ -138,20 +138,20 @@ def test_fused_refresh_matches_oracle(gpu_device, refresh, block):
 
 @pytest.mark.parametrize("mode", ["fp4", "fp8"])
 def test_optimizer_refreshes_layers(gpu_device, mode):
-    """DtypeConfiguredAdamW with attach_lowbit_refresh: after step() the module
+    """PrecisionAdamW with attach_lowbit_refresh: after step() the module
     buffers equal a fresh refresh_persistent_lowbit_params() of the stepped
     weight, for a weight the fused pass takes (rows of 256) and one it does
     not (rows of 384)."""
     from test_gpu_layers import _linear, _resolver
 
-    from lowbit.optim import DtypeConfiguredAdamW
+    from lowbit.optim import PrecisionAdamW
 
     flags = {"fp4": dict(fp4_param=True), "fp8": dict(fp8_param=True)}[mode]
     _, res = _resolver(bf16=True, persistent_scale_granularity="per_channel", persistent_lowbit_include=["fc"],
                        compute_lowbit_mode=None, **flags)
     model = torch.nn.Sequential(_linear(res, 256, 64, path="fc.a", bias=False),
                                 _linear(res, 384, 128, path="fc.b", bias=False))
-    opt = DtypeConfiguredAdamW(model.parameters(), **HP)
+    opt = PrecisionAdamW(model.parameters(), **HP)
     assert opt.attach_lowbit_refresh(model) == 2
     for layer in model:
         layer.refresh_persistent_lowbit_params()

@@ -285,6 +285,25 @@ def test_fp8p_fused_gemm_dequant_exact_all_codes(gpu_device, per_tensor):
     np.testing.assert_array_equal(got[keep], want[keep])
 
 
+@pytest.mark.parametrize("block", [64, 192])
+def test_fp8p_fused_gemm_block_scales_exact(gpu_device, block):
+    """ntlb_gemm_fp8p with a scale per block of 64 or 192 weights of a row:
+    X = I returns every code's bf16(value * its block's scale) bit for bit."""
+    K, N = 384, 64
+    rng = np.random.default_rng(20260611 + block)
+    codes = np.stack([rng.permutation(np.tile(np.arange(256), 2))[:K] for _ in range(N)]).astype(np.uint8)
+    codes[codes == 0x7F] = 0x00
+    codes[codes == 0xFF] = 0x80
+    scales = np.exp(rng.uniform(np.log(1e-20), np.log(1e20), N * (K // block))).astype(np.float32)
+    x = torch.eye(K, dtype=torch.bfloat16, device=gpu_device)
+    y = _fused_unsplit("fp8p", x, torch.from_numpy(codes).to(gpu_device), torch.from_numpy(scales).to(gpu_device),
+                       block, N, torch.float32)
+    torch.cuda.synchronize()
+    vals = O.decode_codes(codes, O.GRID_E4M3)
+    want = O.round_bf16(vals * np.repeat(scales.reshape(N, K // block), block, axis=1))
+    np.testing.assert_array_equal(y.cpu().numpy().T, want)
+
+
 @pytest.mark.parametrize("M,N,K", [(256, 256, 256), (130, 200, 320), (512, 384, 2048), (1, 64, 64)])
 @pytest.mark.parametrize("granularity", ["per_channel", "per_tensor"])
 def test_fp8p_fused_gemm(gpu_device, M, N, K, granularity):
@@ -328,14 +347,15 @@ def test_fp8p_fused_gemm_rejects_bad_scale_shape(gpu_device):
         P.linear_fp8p(x, w, torch.ones(3, device=gpu_device))
 
 
-@pytest.mark.parametrize("block", [64, 256, 0])
-def test_nf4_fused_gemm_dequant_exact_all_codes(gpu_device, block):
+# blocks of 32 * 2^p weights, of 32 * 6, one per row and one tensor-wide
+@pytest.mark.parametrize("block,K", [(64, 256), (256, 256), (0, 256), (32, 256), (192, 384), (384, 384)])
+def test_nf4_fused_gemm_dequant_exact_all_codes(gpu_device, block, K):
     """X = I returns deq(W)^T exactly: every NF4 code at every nibble position,
     under scales spanning many binades, against the oracle dequant (bit for
     bit, after the bf16 rounding of the weight dtype)."""
     from lowbit import persistent as P
 
-    K, N = 256, 80
+    N = 80
     rng = np.random.default_rng(20260604)
     idx = np.stack([rng.permutation(np.tile(np.arange(16), K // 16)) for _ in range(N)]).astype(np.uint8)
     flat = idx.reshape(-1)
