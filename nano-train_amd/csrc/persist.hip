@@ -33,7 +33,6 @@ namespace ntlb {
 __constant__ float kNF4[16] = NTLB_NF4_CODEBOOK;
 // the same values as compile-time constants (folded into immediates)
 constexpr float kNF4c[16] = NTLB_NF4_CODEBOOK;
-constexpr float kE2M1c[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
 __constant__ float kE2M1[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
 
 enum LowFmt : int { FMT_NF4 = 0, FMT_MXFP4 = 1, FMT_FP8P = 2 };
@@ -782,37 +781,21 @@ __device__ __forceinline__ void dequant8_fp8_to_lds(const Raw32& raw, float s, i
   *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = make_uint4(out[0], out[1], out[2], out[3]);
 }
 
-// The 16 bf16 weight values a thread can meet in one K step (all 32 of its
-// weights share one scale): value(code) * scale rounded to bf16, held as two
-// byte tables -- lo[q] / hi[q] carry the low / high bytes of entries
-// 4q..4q+3 -- so a code is looked up with byte permutes instead of a memory
-// read per weight.
+// The 16 bf16 weight values an NF4 thread can meet in one K step (all 32 of
+// its weights share one scale): codebook value times scale in fp32, then
+// bf16 (layers.py:172-184), held as two byte tables -- lo[q] / hi[q] carry
+// the low / high bytes of entries 4q..4q+3 -- so a code is looked up with
+// byte permutes instead of a memory read per weight.
 struct Lut16 {
   uint32_t lo[4], hi[4];
 };
 
-template <int FMT>
 __device__ __forceinline__ Lut16 lut16_build(float s) {
   uint32_t p[8];
-  if constexpr (FMT == FMT_NF4) {
-    // layers.py:172-184: codebook value times scale in fp32, then bf16
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const v2bf t = {(__bf16)(kNF4c[2 * k] * s), (__bf16)(kNF4c[2 * k + 1] * s)};
-      p[k] = __builtin_bit_cast(uint32_t, t);
-    }
-  } else {
-    // e2m1 value times 2^(e - 127) (s carries the e8m0 byte e); e = 0xFF
-    // marks a NaN block
-    const int e = (int)__float_as_uint(s) - 127;
-    const bool nan_block = __float_as_uint(s) == 0xFFu;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float v0 = ldexpf(k < 4 ? kE2M1c[2 * k] : -kE2M1c[2 * k - 8], e);
-      const float v1 = ldexpf(k < 4 ? kE2M1c[2 * k + 1] : -kE2M1c[2 * k - 7], e);
-      const v2bf t = {(__bf16)v0, (__bf16)v1};
-      p[k] = nan_block ? 0x7FC07FC0u : __builtin_bit_cast(uint32_t, t);
-    }
+  for (int k = 0; k < 8; ++k) {
+    const v2bf t = {(__bf16)(kNF4c[2 * k] * s), (__bf16)(kNF4c[2 * k + 1] * s)};
+    p[k] = __builtin_bit_cast(uint32_t, t);
   }
   Lut16 t;
 #pragma unroll
@@ -842,13 +825,25 @@ template <int FMT>
 struct StepDecode {
   Lut16 t;
   float s;
+  bool nan;
 };
 
+// MXFP4 takes no table: gfx950's v_cvt_scalef32_pk_bf16_fp4 turns two e2m1
+// codes times the block's power of two into a bf16 pair in one instruction
+// (exact: an e2m1 value times 2^(e-127) is a bf16 value, subnormal for the
+// smallest e, or overflows to inf as the fp32 product does), so d.s holds
+// 2^(e-127) as a float and d.nan marks the NaN scale byte 0xFF
 template <int FMT>
 __device__ __forceinline__ StepDecode<FMT> decode_begin(float s) {
   StepDecode<FMT> d;
-  d.s = s;
-  if constexpr (FMT != FMT_FP8P) d.t = lut16_build<FMT>(s);
+  if constexpr (FMT == FMT_MXFP4) {
+    const uint32_t e = __float_as_uint(s);
+    d.s = __uint_as_float(e ? e << 23 : 0x00400000u);
+    d.nan = e == 0xFFu;
+  } else {
+    d.s = s;
+    if constexpr (FMT == FMT_NF4) d.t = lut16_build(s);
+  }
   return d;
 }
 
@@ -859,6 +854,17 @@ __device__ __forceinline__ void decode_chunk(const StepDecode<FMT>& d, const Raw
                                              int h) {
   if constexpr (FMT == FMT_FP8P) {
     dequant8_fp8_to_lds(rw, d.s, j, tile, r, h);
+  } else if constexpr (FMT == FMT_MXFP4) {
+    // byte b of the word holds weights 2b (low nibble) and 2b+1: the pair
+    // the instruction returns in that order
+    const uint32_t words[4] = {rw.a.x, rw.a.y, rw.a.z, rw.a.w};
+    const uint32_t w = words[j];
+    uint4 out = make_uint4(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, d.s, 0)),
+                           __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, d.s, 1)),
+                           __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, d.s, 2)),
+                           __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, d.s, 3)));
+    if (d.nan) out = make_uint4(0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u);
+    *reinterpret_cast<uint4*>(tile + fswz(r, h * 4 + j)) = out;
   } else {
     const uint32_t words[4] = {rw.a.x, rw.a.y, rw.a.z, rw.a.w};
     const uint32_t w = words[j];

@@ -372,8 +372,9 @@ def test_nf4_fused_gemm_dequant_exact_all_codes(gpu_device, block, K):
 
 def test_mxfp4_fused_gemm_dequant_exact_all_codes(gpu_device):
     """X = I returns deq(W)^T exactly for every e2m1 code under a range of
-    e8m0 scales; a block with scale byte 0xFF (NaN) turns its row's output
-    column NaN."""
+    e8m0 scales, the smallest ones included (bf16 subnormal weights) and the
+    largest whose products stay finite; a block with scale byte 0xFF (NaN)
+    turns its row's output column NaN."""
     from lowbit import persistent as P
 
     K, N = 256, 64
@@ -382,6 +383,7 @@ def test_mxfp4_fused_gemm_dequant_exact_all_codes(gpu_device):
     flat = idx.reshape(-1)
     packed = (flat[0::2] | (flat[1::2] << 4)).astype(np.uint8)
     sbytes = rng.integers(127 - 100, 127 + 100, (N * K) // 32).astype(np.uint8)
+    sbytes[: 8 * (K // 32)] = np.repeat(np.array([0, 1, 2, 3, 4, 250, 251, 252], dtype=np.uint8), K // 32)
     nan_row = 9
     sbytes[nan_row * (K // 32) + 3] = 0xFF
     x = torch.eye(K, dtype=torch.bfloat16, device=gpu_device)
