@@ -476,13 +476,14 @@ def _c3_ste(args, res: dict, x, w, dy, st) -> dict:
     dg = _time_ms(lambda i: ops.ste_dgrad(dy, qw, out_dtype=bf), args.steps, args.warmup, st)
     wg = _time_ms(lambda i: ops.ste_wgrad(dy, qx, out_dtype=bf), args.steps, args.warmup, st)
     db = _time_ms(lambda i: ops.colsum(dy, out_dtype=bf), args.steps, args.warmup, st)
-    # e4m3: the wgrad kernel that also forms db from its staged dY tiles (what
-    # the layer step runs); its extra time against the plain wgrad
+    # e4m3: the wgrad variant that also forms db from its register-transposed
+    # dY tiles (one launch; the layer step runs the plain wgrad and the column
+    # sum, which is faster); its extra time against the plain wgrad
     wg_db = None
     if fmt == "e4m3":
         wg_db = _time_ms(lambda i: ops.ste_wgrad(dy, qx, out_dtype=bf, db_dtype=bf), args.steps, args.warmup, st)
     # the whole layer step through the backend's autograd function: both
-    # quantizers, the forward GEMM, dgrad, wgrad and db (e4m3: db inside the wgrad)
+    # quantizers, the forward GEMM, dgrad, wgrad and db
     spec = LowBitKernelSpec("linear", K, N, True, "tile_1x128", "block_128x128", "nearest")
     be = HipLowBitBackend(mode="fp8", kernel_spec=spec, code_format=fmt, seed=7)
     xg = x.detach().clone().requires_grad_(True)

@@ -39,6 +39,11 @@
 //                next row's codes follow in memory): the forward of a
 //                persistent layer over fp32 activations or a K that is not
 //                a multiple of 64
+//   SRC_TR     : bf16 stored transposed, as SRC_TDIRECT, copied global ->
+//                LDS as stored (buffer_load ... lds, no registers, no VALU)
+//                and read back transposed by gfx950's ds_read_b64_tr_b16;
+//                the host picks it for every bf16 SRC_TDIRECT operand
+//                except the wgrad that sums its dY rows into db
 // Scales of a coded operand: s(r, c) = s[(r >> r_shift)*s_r + (c >> c_shift)*s_c].
 //
 // Tiling: 256x256 output tile per workgroup, K step of 128 bytes per row (64
@@ -68,7 +73,8 @@ typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
 typedef float v2f __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-constexpr int SRC_DIRECT = 0, SRC_CODES = 1, SRC_TDIRECT = 2, SRC_TCODES = 3, SRC_TNF4 = 4, SRC_PCODES = 5;
+constexpr int SRC_DIRECT = 0, SRC_CODES = 1, SRC_TDIRECT = 2, SRC_TCODES = 3, SRC_TNF4 = 4, SRC_PCODES = 5,
+              SRC_TR = 6;
 // the code format of a SRC_PCODES operand (the GRID parameter): e4m3 codes,
 // or NF4 nibbles
 constexpr int GRID_NF4 = 2;
@@ -107,6 +113,42 @@ __device__ __forceinline__ v8i frag(const uint8_t* tile, int row0, int lane) {
   v8i f;
   f[0] = (int)lo.x; f[1] = (int)lo.y; f[2] = (int)lo.z; f[3] = (int)lo.w;
   f[4] = (int)hi.x; f[5] = (int)hi.y; f[6] = (int)hi.z; f[7] = (int)hi.w;
+  return f;
+}
+
+// SRC_TR stages: [64 contraction rows][256 operand rows] bf16, 512 bytes per
+// contraction row, the 16-byte chunk c (operand rows 8c..8c+7) of row k at
+// tr_off(k, c).  ds_read_b64_tr_b16 hands lane i of each 16-lane group the
+// four 16-bit values that lanes 4j + i/4 (j = 0..3) loaded at position i%4
+// (measured on gfx950).  So when lane 4j + q of the group loads operand rows
+// row0 + 4q .. 4q+3 of contraction row kk + j, lane i receives operand row
+// row0 + i at contraction kk .. kk+3.  A 16-lane group touches contraction
+// rows kk..kk+3 (k & 3 = j) and two adjacent chunks; the XOR with 2(k & 3)
+// spreads those eight 16-byte pieces over eight chunk slots, and bit 4 of
+// the row (the next group's rows, 16 further) flips bit 3 of the slot, so
+// 32 lanes read 256 distinct bytes.
+constexpr int TR_ROWB = 512;
+__device__ __forceinline__ int tr_perm(int k) { return (2 * (k & 3)) ^ (8 * ((k >> 4) & 1)); }
+__device__ __forceinline__ int tr_off(int k, int c) { return k * TR_ROWB + ((c ^ tr_perm(k)) << 4); }
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s* lds_v4s_ptr;
+
+// the fragment of frag() (lane group g: contraction 16g .. 16g+15 of the
+// step, operand row row0 + lane%16) from an SRC_TR stage: four transposing
+// loads of four contraction values each
+__device__ __forceinline__ v8i frag_tr(const uint8_t* tile, int row0, int lane) {
+  const int g = lane >> 4, j = (lane >> 2) & 3, q = lane & 3;
+  const int c = (row0 >> 3) + (q >> 1);
+  v8i f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int k = 16 * g + 4 * h + j;
+    const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4s_ptr)(tile + tr_off(k, c) + (q & 1) * 8));
+    f[2 * h] = (int)(((uint32_t)(uint16_t)v[1] << 16) | (uint16_t)v[0]);
+    f[2 * h + 1] = (int)(((uint32_t)(uint16_t)v[3] << 16) | (uint16_t)v[2]);
+  }
   return f;
 }
 
@@ -235,7 +277,7 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 template <int SRC, int EL, int GRID, int SCM>
 struct Stager;
 
-// DIRECT: no registers (global -> LDS copies issued by the step)
+// DIRECT and TR: no registers (global -> LDS copies issued by the step)
 template <int EL, int GRID, int SCM>
 struct Stager<SRC_DIRECT, EL, GRID, SCM> {
   __device__ void init(const Operand&, int64_t, int, int) {}
@@ -243,6 +285,8 @@ struct Stager<SRC_DIRECT, EL, GRID, SCM> {
   template <int H>
   __device__ void decode_half(const Operand&, uint8_t*) {}
 };
+template <int EL, int GRID, int SCM>
+struct Stager<SRC_TR, EL, GRID, SCM> : Stager<SRC_DIRECT, EL, GRID, SCM> {};
 
 // CODES: thread t decodes row t/2, half t%2 of the K block
 template <int EL, int GRID, int SCM>
@@ -608,6 +652,33 @@ struct Direct {
   }
 };
 
+// TR copies: copy j of wave w moves contraction rows R and R + 1 of the
+// stage, R = 2(w & 3) + 16(w >> 2) + 8(j & 1) + 32(j >> 1), one 1 KiB LDS
+// run: lane i lands at byte 16i of it (row R + i/32, chunk slot i%32) and
+// fetches the chunk (i%32) ^ tr_perm(row), which is the same for the four
+// copies (they differ in row bits 3 and 5, which tr_perm ignores).  Rows
+// past kvalid read zero through the resource; columns past the operand's
+// rows reach only outputs that are never stored.  The entry points check
+// (kvalid + 64) * ld * 2 < 2^31.
+struct TrCopy {
+  __amdgpu_buffer_rsrc_t rs;
+  uint32_t off, rowb;
+  __device__ static int row0(int wave, int j) {
+    return 2 * (wave & 3) + 16 * (wave >> 2) + 8 * (j & 1) + 32 * (j >> 1);
+  }
+  __device__ void init(const Operand& o, int64_t r0, int wave, int lane) {
+    const int R = row0(wave, 0) + (lane >> 5);
+    const int c = (lane & 31) ^ tr_perm(R);
+    rs = trows_rsrc(o, 2);
+    rowb = (uint32_t)(o.ld * 2);
+    off = (uint32_t)R * rowb + (uint32_t)((r0 + 8 * c) * 2);
+  }
+  __device__ void issue(uint8_t* stage, int kt, int wave, int j) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(stage + row0(wave, j) * TR_ROWB), 16, off,
+                                             (uint32_t)(kt * 64 + 8 * (j & 1) + 32 * (j >> 1)) * rowb, 0, 0);
+  }
+};
+
 template <int EL, int SA, int SB, int GRID, int SCM, int GRP = GRP_NONE, bool IL = false, bool DB = false>
 __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t la0[TILE];
@@ -720,9 +791,13 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     raster(pid, num_m, num_n, m0, n0);
   }
 
+  static_assert((SA != SRC_TR && SB != SRC_TR) || EL == EL_BF16, "transposing LDS loads take 16-bit values");
   Direct da, db;
+  TrCopy ta_c, tb_c;
   if constexpr (SA == SRC_DIRECT) da.init(g.a, m0, wave, lane, EB);
   if constexpr (SB == SRC_DIRECT) db.init(g.b, n0, wave, lane, EB);
+  if constexpr (SA == SRC_TR) ta_c.init(g.a, m0, wave, lane);
+  if constexpr (SB == SRC_TR) tb_c.init(g.b, n0, wave, lane);
   Stager<SA, EL, GRID, SCM> sa;
   Stager<SB, EL, GRID, SCM> sb;
   sa.init(g.a, m0, tid, lane);
@@ -786,6 +861,8 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   for (int j = 0; j < 4; ++j) {
     if constexpr (SA == SRC_DIRECT) da.issue(la0, kmap(kb0), wave, j);
     if constexpr (SB == SRC_DIRECT) db.issue(lb0, kmap(kb0), wave, j);
+    if constexpr (SA == SRC_TR) ta_c.issue(la0, kmap(kb0), wave, j);
+    if constexpr (SB == SRC_TR) tb_c.issue(lb0, kmap(kb0), wave, j);
   }
   sa.load(g.a, kmap(kb0));
   sb.load(g.b, kmap(kb0));
@@ -811,17 +888,21 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
     uint8_t* na = BUF ? la0 : la1;
     uint8_t* nb = BUF ? lb0 : lb1;
     const int kn = min(kt + 1, kb1 - 1);
+    auto frag_a = [&](int row0) { return SA == SRC_TR ? frag_tr(ta, row0, lane) : frag(ta, row0, lane); };
+    auto frag_b = [&](int row0) { return SB == SRC_TR ? frag_tr(tb, row0, lane) : frag(tb, row0, lane); };
     v8i bf[4];
 #pragma unroll
-    for (int tn = 0; tn < 4; ++tn) bf[tn] = frag(tb, wn * 64 + tn * 16, lane);
-    v8i af = frag(ta, wm * 128, lane);
+    for (int tn = 0; tn < 4; ++tn) bf[tn] = frag_b(wn * 64 + tn * 16);
+    v8i af = frag_a(wm * 128);
 #pragma unroll
     for (int tm = 0; tm < 8; ++tm) {
       v8i af_next;
-      if (tm + 1 < 8) af_next = frag(ta, wm * 128 + (tm + 1) * 16, lane);
+      if (tm + 1 < 8) af_next = frag_a(wm * 128 + (tm + 1) * 16);
       if (tm < 4) {
         if constexpr (SA == SRC_DIRECT) da.issue(na, kmap(kn), wave, tm);
         if constexpr (SB == SRC_DIRECT) db.issue(nb, kmap(kn), wave, tm);
+        if constexpr (SA == SRC_TR) ta_c.issue(na, kmap(kn), wave, tm);
+        if constexpr (SB == SRC_TR) tb_c.issue(nb, kmap(kn), wave, tm);
       }
       if (tm == 4) {
         sa.template decode_half<0>(g.a, na);
@@ -1093,10 +1174,20 @@ void launch(const DqArgs& g, hipStream_t st) {
   gemm_dq_kernel<EL, SA, SB, GRID, SCM><<<dim3((unsigned)wgs), dim3(NT), 0, st>>>(g);
 }
 
+// a bf16 operand stored transposed takes the transposing LDS loads when its
+// stored rows are whole 16-byte chunks (the copies move 16 bytes per lane);
+// otherwise the register transpose, which needs 8-byte rows
+static bool tr_ok(const Operand& o) { return aligned(o.p, 16) && (o.ld * 2) % 16 == 0; }
+
 // the source combinations this library instantiates
 int dispatch(int el, int sa, int sb, const DqArgs& g, hipStream_t st) {
   const int grid = (sa == SRC_CODES || sa == SRC_TCODES) ? g.a.grid : g.b.grid;  // PCODES: B's format
   const int scm = (sb == SRC_TCODES || sb == SRC_TNF4) ? g.b.smode : SC_SHARED;
+  // bf16 operands stored transposed go through the transposing LDS loads,
+  // except the wgrad that also sums its dY rows into db (that variant adds
+  // up the values its register transpose holds)
+  if (el == EL_BF16 && sa == SRC_TDIRECT && !g.db && tr_ok(g.a) && (sb != SRC_TDIRECT || tr_ok(g.b))) sa = SRC_TR;
+  if (el == EL_BF16 && sb == SRC_TDIRECT && tr_ok(g.b) && sa != SRC_TDIRECT) sb = SRC_TR;
 #define NTLB_DQ_CASE(E, A, B, G)                                \
   if (el == E && sa == A && sb == B && (grid == G || G < 0)) {  \
     launch<E, A, B, (G < 0 ? 0 : G)>(g, st);                    \
@@ -1113,6 +1204,10 @@ int dispatch(int el, int sa, int sb, const DqArgs& g, hipStream_t st) {
   NTLB_DQ_CASE_SC(EL_BF16, SRC_DIRECT, SRC_TCODES, GRID_E4M3, SC_SHARED)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_DIRECT, SRC_TCODES, GRID_INT, SC_CONTIG)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_DIRECT, SRC_TCODES, GRID_E4M3, SC_CONTIG)
+  NTLB_DQ_CASE_SC(EL_BF16, SRC_TR, SRC_TCODES, GRID_INT, SC_SHARED)
+  NTLB_DQ_CASE_SC(EL_BF16, SRC_TR, SRC_TCODES, GRID_E4M3, SC_SHARED)
+  NTLB_DQ_CASE_SC(EL_BF16, SRC_TR, SRC_TCODES, GRID_INT, SC_CONTIG)
+  NTLB_DQ_CASE_SC(EL_BF16, SRC_TR, SRC_TCODES, GRID_E4M3, SC_CONTIG)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_TDIRECT, SRC_TCODES, GRID_INT, SC_SHARED)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_TDIRECT, SRC_TCODES, GRID_E4M3, SC_SHARED)
   NTLB_DQ_CASE_SC(EL_BF16, SRC_TDIRECT, SRC_TCODES, GRID_INT, SC_CONTIG)
@@ -1128,6 +1223,8 @@ int dispatch(int el, int sa, int sb, const DqArgs& g, hipStream_t st) {
   NTLB_DQ_CASE(EL_F32, SRC_DIRECT, SRC_PCODES, GRID_NF4)
   NTLB_DQ_CASE(EL_F32, SRC_DIRECT, SRC_PCODES, GRID_E4M3)
   NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_DIRECT, -1)
+  NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_TR, -1)
+  NTLB_DQ_CASE(EL_BF16, SRC_TR, SRC_TR, -1)
   NTLB_DQ_CASE(EL_BF16, SRC_DIRECT, SRC_TDIRECT, -1)
   NTLB_DQ_CASE(EL_BF16, SRC_TDIRECT, SRC_TDIRECT, -1)
   NTLB_DQ_CASE(EL_F32, SRC_CODES, SRC_CODES, GRID_INT)
@@ -1545,7 +1642,10 @@ extern "C" int ntlb_gemm_grouped_ste_wgrad(int op_dtype, const void* dy, int64_t
   g.y_estride = dw_estride;
   const int64_t wgs = ((N + TM - 1) / TM) * ((K + TN - 1) / TN) * n_experts;
   if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
-  launch_grouped<SRC_TDIRECT, SRC_TCODES, SC_CONTIG, GRP_K>(g, wgs, as_stream(stream));
+  if (tr_ok(g.a))
+    launch_grouped<SRC_TR, SRC_TCODES, SC_CONTIG, GRP_K>(g, wgs, as_stream(stream));
+  else
+    launch_grouped<SRC_TDIRECT, SRC_TCODES, SC_CONTIG, GRP_K>(g, wgs, as_stream(stream));
   return check_launch(fn);
 }
 
@@ -1589,7 +1689,10 @@ extern "C" int ntlb_gemm_grouped_dgrad_dense(int op_dtype, const void* dy, int64
   const int64_t num_n = (K + TN - 1) / TN;
   const int64_t wgs = ((R + TM - 1) / TM + n_experts) * num_n;
   if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
-  launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS>(g, wgs, as_stream(stream));
+  if (tr_ok(g.b))
+    launch_grouped_dense<SRC_DIRECT, SRC_TR, GRP_ROWS>(g, wgs, as_stream(stream));
+  else
+    launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS>(g, wgs, as_stream(stream));
   return check_launch(fn);
 }
 
@@ -1623,10 +1726,14 @@ extern "C" int ntlb_gemm_grouped_dgrad_dense_gate_up(int op_dtype, const void* d
   const int64_t wgs = ((R + TM - 1) / TM + n_experts) * num_n;
   if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
   hipStream_t st = as_stream(stream);
-  g.il_half = 0; g.accum = 0;
-  launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS, true>(g, wgs, st);
-  g.il_half = 1; g.accum = 1;
-  launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS, true>(g, wgs, st);
+  const bool tr = tr_ok(g.b);
+  for (int half = 0; half < 2; ++half) {
+    g.il_half = half; g.accum = half;
+    if (tr)
+      launch_grouped_dense<SRC_DIRECT, SRC_TR, GRP_ROWS, true>(g, wgs, st);
+    else
+      launch_grouped_dense<SRC_DIRECT, SRC_TDIRECT, GRP_ROWS, true>(g, wgs, st);
+  }
   return check_launch(fn);
 }
 
@@ -1656,7 +1763,10 @@ extern "C" int ntlb_gemm_grouped_wgrad_dense(int op_dtype, const void* dy, int64
   g.y_estride = dw_estride;
   const int64_t wgs = ((N + TM - 1) / TM) * ((K + TN - 1) / TN) * n_experts;
   if (wgs > 0x7FFFFFFF) return fail(NTLB_EINVAL, "%s: too many tiles", fn);
-  launch_grouped_dense<SRC_TDIRECT, SRC_TDIRECT, GRP_K>(g, wgs, as_stream(stream));
+  if (tr_ok(g.a) && tr_ok(g.b))
+    launch_grouped_dense<SRC_TR, SRC_TR, GRP_K>(g, wgs, as_stream(stream));
+  else
+    launch_grouped_dense<SRC_TDIRECT, SRC_TDIRECT, GRP_K>(g, wgs, as_stream(stream));
   return check_launch(fn);
 }
 

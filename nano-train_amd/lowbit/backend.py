@@ -281,11 +281,10 @@ class _HipLowBitLinear(torch.autograd.Function):
                 dx = dx.reshape(ctx.x_shape)
             if ctx.needs_input_grad[1]:
                 if qx is not None and dy2.dtype == torch.bfloat16:
-                    if ctx.has_bias and ctx.needs_input_grad[2] and qx.grid == _lib.GRID_E4M3:
-                        # db from the dY tiles the wgrad kernel stages (no pass of its own)
-                        dw, db = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype, db_dtype=ctx.bias_dtype)
-                    else:
-                        dw = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype)
+                    # dY^T through the transposing LDS loads, db by the column-sum
+                    # pass below: together faster than the wgrad variant that sums
+                    # db from its register-transposed dY tiles (ste_wgrad's db_dtype)
+                    dw = ops.ste_wgrad(dy2, qx, out_dtype=ctx.w_dtype)
                 else:
                     xdq = xq if xq is not None else ops.dequant(qx, out_dtype=ctx.x_dtype)
                     op = _gemm_op_dtype(dy2.dtype, xdq.dtype)
