@@ -714,16 +714,15 @@ __global__ void __launch_bounds__(NT, 1) gemm_dq_kernel(DqArgs g) {
   int64_t m0, n0;
   int nk = (int)(g.Kc / KSTEP);
   if constexpr (GRP == GRP_ROWS) {
-    // experts in order, each one's row tiles in the raster of the dense case;
-    // the grid is an upper bound on the tile count (the offset table is read
-    // into LDS, free until the first copy, and the tiles counted there)
+    // experts in order, each one's row tiles in the raster of the dense case,
+    // consecutive tiles on consecutive XCDs (not a contiguous range per XCD:
+    // that gave the XCDs holding the small experts' ragged last row tiles
+    // less work than the others); the grid is an upper bound on the tile
+    // count (the offset table is read into LDS, free until the first copy)
     int32_t* tab = reinterpret_cast<int32_t*>(la0);
     for (int i = tid; i <= g.n_experts; i += NT) tab[i] = g.offsets[i];
     __syncthreads();
-    int total = 0;
-    for (int i = 0; i < g.n_experts; ++i) total += (int)((tab[i + 1] - tab[i] + TM - 1) / TM) * num_n;
-    int pid = (int)blockIdx.x;
-    if (pid < total) pid = xcd_local(pid, total);
+    const int pid = (int)blockIdx.x;
     int e = 0, before = 0, tiles_m = 0;
     int64_t lo = 0, hi = 0;
     for (; e < g.n_experts; ++e) {
