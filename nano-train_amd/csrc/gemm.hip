@@ -2,7 +2,8 @@
 //   Y[M,N] = sum_kb sa(m,kb) * sb(n,kb) * (A_kb[m,:] . B_kb[n,:])  (+ bias)
 // The F.linear of te_backend.py:253-259 with both operands kept as codes and
 // scales.  Each 128-wide K block is one MFMA chain on the matrix cores:
-//   e4m3 codes: v_mfma_scale_f32_16x16x128_f8f6f4 (unit e8m0 scales), fp32 out
+//   e4m3 codes: v_mfma_f32_16x16x128_f8f6f4 (the scaled builtin with zero
+//     scale operands, which selects the unscaled encoding), fp32 out
 //   int-grid codes: 2x v_mfma_i32_16x16x64_i8, exact int32 partials
 //     (|partial| <= 128*127^2 < 2^24, so the int32 -> fp32 conversion is exact)
 // and the partial tile is promoted into the fp32 accumulator with
