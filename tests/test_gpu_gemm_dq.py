@@ -369,10 +369,14 @@ def test_ste_dgrad_split_tail_matches_unsplit(gpu_device, fmt, wscale, K):
     assert torch.equal(dx[:7168].view(torch.int32), ref[:7168].view(torch.int32))
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 200, 384), (1000, 640, 1152), (77, 129, 257), (4096, 2304, 512)])
+# M = 1 and 65: a contraction of one row, and one row past a K step (the
+# transposing-load copies read zeros past the last row)
+@pytest.mark.parametrize("M,N,K", [(300, 200, 384), (1000, 640, 1152), (77, 129, 257), (4096, 2304, 512),
+                                   (1, 136, 128), (65, 264, 384)])
 def test_ste_wgrad_with_db_matches_colsum(gpu_device, M, N, K):
     """The e4m3 straight-through wgrad that also forms db from its staged dY
-    tiles: dW bit-identical to the wgrad without db, db within fp32
+    tiles (dY transposed in registers): dW bit-identical to the wgrad without
+    db (dY through the transposing LDS loads), db within fp32
     reassociation of float64's column sums of dY (and of the separate
     column-sum pass), repeats bit-identical; the int grid refuses db."""
     ops = _ops()
